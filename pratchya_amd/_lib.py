@@ -1,0 +1,80 @@
+"""ctypes binding of ``libpratchya_fp8.so`` (the C ABI in include/pratchya_fp8.h).
+
+The library is mandatory: every operator in this package runs on the gfx950
+kernels and there is no CPU or PyTorch fallback.  A missing or stale library is
+an ImportError-style failure at first use, never a silent slow path.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libpratchya_fp8.so"
+ABI_VERSION = 1
+
+OK, EINVAL, EHIP, EUNSUPPORTED = 0, 1, 2, 3
+DT_F32, DT_BF16 = 0, 1
+
+_c_i64 = ctypes.c_int64
+_c_p = ctypes.c_void_p
+_c_int = ctypes.c_int
+
+# (name, restype, argtypes) for every exported entry point.
+SIGNATURES = {
+    "pratchya_abi_version": (_c_int, []),
+    "pratchya_last_error": (ctypes.c_char_p, []),
+    "pratchya_quant_layout": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64,
+                                       ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64),
+                                       ctypes.POINTER(_c_i64)]),
+    "pratchya_quantize_workspace_bytes": (ctypes.c_size_t, [_c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
+    "pratchya_quantize": (_c_int, [_c_p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                   _c_p, _c_p, _c_p, _c_p, ctypes.c_size_t, _c_p]),
+    "pratchya_dequantize": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                     _c_p, _c_int, _c_p]),
+    "pratchya_dequantize_bwd": (_c_int, [_c_p, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
+                                         _c_i64, _c_p, _c_p]),
+    "pratchya_debug_bf16_to_e4m3": (_c_int, [_c_p, _c_p, _c_i64, _c_int, _c_p]),
+    "pratchya_debug_f32_to_bf16": (_c_int, [_c_p, _c_p, _c_i64, _c_int, _c_p]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class PratchyaError(RuntimeError):
+    """A HIP launch failure or an unsupported request reported by the library."""
+
+
+def load() -> ctypes.CDLL:
+    """Load the library once; raise if it is absent or has another ABI."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise ImportError(
+                f"{LIB_PATH} is not built; run `python -m pratchya_amd.build` "
+                "(the gfx950 kernels are required, there is no fallback)")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        ver = lib.pratchya_abi_version()
+        if ver != ABI_VERSION:
+            raise ImportError(f"{LIB_PATH} has ABI {ver}, expected {ABI_VERSION}; rebuild it")
+        _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    """Raise the Python error matching a library status code."""
+    if rc == OK:
+        return
+    msg = load().pratchya_last_error().decode(errors="replace")
+    if rc == EINVAL:
+        raise ValueError(f"{what}: {msg}")
+    raise PratchyaError(f"{what}: {msg} (status {rc})")

@@ -1,0 +1,743 @@
+// gfx950 kernels for pratchya's FP8 block quantizer and dequantizer, and the
+// C ABI declared in include/pratchya_fp8.h.
+//
+// Reference: pratchya/_qualia/_qarr.py quantize_impl (458-506), dequantize_impl
+// (541-569), dequantize_impl_bwd (575-601).  Results are bit-identical to the
+// reference's f32 arithmetic; the per-element arithmetic lives in fp8_math.h.
+//
+// Two quantize paths:
+//   * row-group (single pass): tgrid (1, b).  Blocks are b contiguous
+//     elements and a group is K*b contiguous elements, so one wavefront owns
+//     whole groups: 128-bit loads, block/group amax by lane shuffles, one
+//     division per block, a multiply per element.
+//   * general (four launches): any (a, b).  Block amax into a workspace with
+//     atomics, group max + e8m0 per group, then an elementwise cast.
+//
+// Per element the cast needs e4m3fn(bf16(x / S * 128)) with an IEEE division.
+// The row-group kernel computes t = x * RN(128/S) instead; t is within 2 ulp
+// of RN(128x/S).  For bf16 inputs with an unclamped S = 2^k * G (G a bf16
+// value) the exact quotient is never within 2^7 ulp of a bf16 rounding
+// midpoint (x and G have 8-bit significands), so bf16(t) == bf16(RN(x/S)*128).
+// For f32 inputs the wave checks the low 16 bits of t against the midpoint
+// and redoes the wave with exact division if any element is within 4 ulp.
+// Blocks whose S was clamped or is not finite always take the exact path.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "fp8_math.h"
+#include "pratchya_fp8.h"
+
+using namespace pfp8;
+
+// The single-pass kernel rounds with v_cvt_pk_bf16_f32 and converts with
+// v_cvt_scalef32_pk_fp8_bf16 (scale 1.0).  Both are exact (RNE, non-saturating)
+// on every finite input, which the test suite checks exhaustively through the
+// debug entry points; the kernel only feeds them finite values.
+#ifndef PRATCHYA_HW_CVT
+#define PRATCHYA_HW_CVT 1
+#endif
+
+// --------------------------------------------------------------------------
+// Error state
+// --------------------------------------------------------------------------
+static thread_local char g_err[512];
+
+int pratchya_set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+static int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return pratchya_set_error(PRATCHYA_EHIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+  g_err[0] = 0;
+  return PRATCHYA_OK;
+}
+
+extern "C" int pratchya_abi_version(void) { return 1; }
+extern "C" const char* pratchya_last_error(void) { return g_err; }
+
+// --------------------------------------------------------------------------
+// Element conversion helpers (4 values -> 4 packed e4m3fn bytes)
+// --------------------------------------------------------------------------
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef short short2_t __attribute__((ext_vector_type(2)));
+
+// t[i] finite.  Software path: bf16 RNE by integer rounding, then e4m3fn.
+__device__ __forceinline__ uint32_t cvt4_sw(float t0, float t1, float t2, float t3) {
+  uint32_t c0 = bf16_to_e4m3fn(f32_to_bf16_rne_nonan(t0));
+  uint32_t c1 = bf16_to_e4m3fn(f32_to_bf16_rne_nonan(t1));
+  uint32_t c2 = bf16_to_e4m3fn(f32_to_bf16_rne_nonan(t2));
+  uint32_t c3 = bf16_to_e4m3fn(f32_to_bf16_rne_nonan(t3));
+  return c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
+}
+
+// t[i] finite.  gfx950 path: v_cvt_pk_bf16_f32 (RNE) then
+// v_cvt_scalef32_pk_fp8_bf16 with scale 1.0.
+__device__ __forceinline__ uint32_t cvt4_hw(float t0, float t1, float t2, float t3) {
+  bf16x2_t lo = {(__bf16)t0, (__bf16)t1};
+  bf16x2_t hi = {(__bf16)t2, (__bf16)t3};
+  short2_t r = {0, 0};
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(r, lo, 1.0f, false);
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(r, hi, 1.0f, true);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+template <bool HW>
+__device__ __forceinline__ uint32_t cvt4(float t0, float t1, float t2, float t3) {
+  if constexpr (HW) return cvt4_hw(t0, t1, t2, t3);
+  else return cvt4_sw(t0, t1, t2, t3);
+}
+
+// Exact composition for 4 elements (any inputs, NaN/inf/overflow included).
+__device__ __forceinline__ uint32_t cvt4_exact(float x0, float x1, float x2, float x3, float S) {
+  return quant_elem_exact(x0, S) | (quant_elem_exact(x1, S) << 8) |
+         (quant_elem_exact(x2, S) << 16) | (quant_elem_exact(x3, S) << 24);
+}
+
+// Distance of the low 16 bits of t from the bf16 rounding midpoint is <= 4.
+__device__ __forceinline__ bool near_bf16_midpoint(float t) {
+  return ((f2u(t) + 4u - 0x8000u) & 0xFFFFu) <= 8u;
+}
+
+__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint32_t shfl_xor_u32(uint32_t v, int m) {
+  return (uint32_t)__shfl_xor((int)v, m, 64);
+}
+
+// Widen the i-th element of a 16-byte vector to f32.
+template <bool IS_BF16>
+__device__ __forceinline__ float elem_f32(const uint4& v, int i) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  if constexpr (IS_BF16) {
+    uint32_t word = w[i >> 1];
+    return u2f((i & 1) ? (word & 0xFFFF0000u) : (word << 16));
+  } else {
+    return u2f(w[i]);
+  }
+}
+
+// max |x| bits (as f32 bits) over the 16 bytes of v.
+template <bool IS_BF16>
+__device__ __forceinline__ uint32_t vec_absmax_bits(const uint4& v) {
+  if constexpr (IS_BF16) {
+    uint32_t m01 = umax(v.x & 0x7FFFu, (v.x >> 16) & 0x7FFFu);
+    uint32_t m23 = umax(v.y & 0x7FFFu, (v.y >> 16) & 0x7FFFu);
+    uint32_t m45 = umax(v.z & 0x7FFFu, (v.z >> 16) & 0x7FFFu);
+    uint32_t m67 = umax(v.w & 0x7FFFu, (v.w >> 16) & 0x7FFFu);
+    return umax(umax(m01, m23), umax(m45, m67)) << 16;
+  } else {
+    return umax(umax(v.x & 0x7FFFFFFFu, v.y & 0x7FFFFFFFu),
+                umax(v.z & 0x7FFFFFFFu, v.w & 0x7FFFFFFFu));
+  }
+}
+
+// --------------------------------------------------------------------------
+// Row-group quantize: tgrid (1, b), one wave per tile of R x 64 x VEC elements.
+//   BL = b / VEC lanes per block (power of two <= 64)
+//   GL = K * BL lanes per group; SPAN: GL == 64 * R (one group per wave),
+//   otherwise GL <= 64 and every row holds 64 / GL whole groups.
+// --------------------------------------------------------------------------
+template <bool IS_BF16, int R, bool SPAN, bool HW>
+__global__ __launch_bounds__(256) void k_quant_rowgroup(
+    const void* __restrict__ xv, uint8_t* __restrict__ q, uint8_t* __restrict__ sc8,
+    float* __restrict__ sc32, int64_t n_elems, int bl_log2, int gl_log2) {
+  constexpr int VEC = IS_BF16 ? 8 : 4;
+  constexpr int VLOG = IS_BF16 ? 3 : 2;
+  constexpr int TILE = R * 64 * VEC;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t base = wave * TILE;
+  if (base >= n_elems) return;
+  const int BL = 1 << bl_log2;
+  const int GL = 1 << gl_log2;
+
+  uint4 v[R];
+  bool live[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t off = base + (int64_t)(r * 64 + lane) * VEC;
+    live[r] = off < n_elems;
+    if (live[r]) {
+      v[r] = *reinterpret_cast<const uint4*>(static_cast<const char*>(xv) + off * (IS_BF16 ? 2 : 4));
+    } else {
+      v[r] = make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  // block and group maxima (f32 bit patterns of |x|; unsigned max propagates NaN)
+  uint32_t bmax[R], gmax[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    uint32_t m = vec_absmax_bits<IS_BF16>(v[r]);
+    for (int s = 1; s < BL; s <<= 1) m = umax(m, shfl_xor_u32(m, s));
+    bmax[r] = m;
+    if constexpr (!SPAN) {
+      for (int s = BL; s < GL; s <<= 1) m = umax(m, shfl_xor_u32(m, s));
+    }
+    gmax[r] = m;
+  }
+  if constexpr (SPAN) {
+    uint32_t g = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      uint32_t m = gmax[r];
+      for (int s = BL; s < 64; s <<= 1) m = umax(m, shfl_xor_u32(m, s));
+      g = umax(g, m);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) gmax[r] = g;
+  }
+
+  float S[R], y[R];
+  bool ok = true;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float m = u2f(bmax[r]);
+    const float G = u2f(gmax[r]);
+    const uint32_t e = e8m0_of(m, G);
+    const float sG = e8m0_decode(e) * G;
+    S[r] = quant_scale(e, G);
+    y[r] = 128.0f / S[r];
+    // unclamped and finite: S == sG exactly (false for NaN sG)
+    ok = ok && (!live[r] || (sG >= kClamp && sG <= 3.0e38f));
+    const int64_t off = base + (int64_t)(r * 64 + lane) * VEC;
+    if (live[r]) {
+      if ((lane & (BL - 1)) == 0) sc8[off >> (bl_log2 + VLOG)] = (uint8_t)e;
+      const bool glead = SPAN ? (r == 0 && lane == 0) : ((lane & (GL - 1)) == 0);
+      if (glead) sc32[off >> (gl_log2 + VLOG)] = G;
+    }
+  }
+
+  uint32_t out[R][VEC / 4];
+  bool exact = !__all(ok);
+  if (!exact) {
+    bool near = false;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+      for (int j = 0; j < VEC / 4; ++j) {
+        const float t0 = elem_f32<IS_BF16>(v[r], 4 * j + 0) * y[r];
+        const float t1 = elem_f32<IS_BF16>(v[r], 4 * j + 1) * y[r];
+        const float t2 = elem_f32<IS_BF16>(v[r], 4 * j + 2) * y[r];
+        const float t3 = elem_f32<IS_BF16>(v[r], 4 * j + 3) * y[r];
+        if constexpr (!IS_BF16) {
+          near = near || near_bf16_midpoint(t0) || near_bf16_midpoint(t1) ||
+                 near_bf16_midpoint(t2) || near_bf16_midpoint(t3);
+        }
+        out[r][j] = cvt4<HW>(t0, t1, t2, t3);
+      }
+    }
+    if constexpr (!IS_BF16) exact = __any(near);
+  }
+  if (exact) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+      for (int j = 0; j < VEC / 4; ++j) {
+        out[r][j] = cvt4_exact(elem_f32<IS_BF16>(v[r], 4 * j + 0), elem_f32<IS_BF16>(v[r], 4 * j + 1),
+                               elem_f32<IS_BF16>(v[r], 4 * j + 2), elem_f32<IS_BF16>(v[r], 4 * j + 3),
+                               S[r]);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (!live[r]) continue;
+    const int64_t off = base + (int64_t)(r * 64 + lane) * VEC;
+    if constexpr (IS_BF16) {
+      *reinterpret_cast<uint2*>(q + off) = make_uint2(out[r][0], out[r][1]);
+    } else {
+      *reinterpret_cast<uint32_t*>(q + off) = out[r][0];
+    }
+  }
+}
+
+// --------------------------------------------------------------------------
+// General path
+// --------------------------------------------------------------------------
+__global__ void k_fill_u32(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+template <bool IS_BF16>
+__device__ __forceinline__ float load_elem(const void* x, int64_t i) {
+  if constexpr (IS_BF16) return u2f((uint32_t)static_cast<const uint16_t*>(x)[i] << 16);
+  else return static_cast<const float*>(x)[i];
+}
+
+// Block amax: thread per chunk of CH consecutive elements of one row (CH | b).
+// Lanes of an aligned group of b/CH lanes cover one block row segment and are
+// combined by shuffles when b/CH is a power of two <= 64 (seg_log2 >= 0).
+template <bool IS_BF16, int CH>
+__global__ __launch_bounds__(256) void k_blockmax(const void* __restrict__ x,
+                                                  uint32_t* __restrict__ ws, int64_t n_chunks,
+                                                  int64_t W, int64_t a, int64_t b, int seg_log2) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool live = t < n_chunks;
+  uint32_t m = 0;
+  int64_t blk = 0;
+  if (live) {
+    const int64_t off = t * CH;
+    const int64_t i = off / W, c = off - i * W;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) m = umax(m, abs_bits(load_elem<IS_BF16>(x, off + k)));
+    blk = (i / a) * (W / b) + c / b;
+  }
+  if (seg_log2 >= 0) {
+    const int seg = 1 << seg_log2;
+    for (int s = 1; s < seg; s <<= 1) m = umax(m, shfl_xor_u32(m, s));
+    if (live && ((threadIdx.x & (seg - 1)) == 0)) atomicMax(&ws[blk], m);
+  } else if (live) {
+    atomicMax(&ws[blk], m);
+  }
+}
+
+// Group max and e8m0 bytes: one wave per group.
+__global__ __launch_bounds__(256) void k_group_scales(const uint32_t* __restrict__ ws,
+                                                      uint8_t* __restrict__ sc8,
+                                                      float* __restrict__ sc32, int64_t n_groups,
+                                                      int64_t K) {
+  const int lane = threadIdx.x & 63;
+  const int64_t g = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (g >= n_groups) return;
+  const uint32_t* m = ws + g * K;
+  uint32_t G = 0;
+  for (int64_t k = lane; k < K; k += 64) G = umax(G, m[k]);
+  for (int s = 1; s < 64; s <<= 1) G = umax(G, shfl_xor_u32(G, s));
+  const float Gf = u2f(G);
+  for (int64_t k = lane; k < K; k += 64) sc8[g * K + k] = (uint8_t)e8m0_of(u2f(m[k]), Gf);
+  if (lane == 0) sc32[g] = Gf;
+}
+
+// Group max and e8m0 bytes: one thread per group (small K).
+__global__ __launch_bounds__(256) void k_group_scales_small(const uint32_t* __restrict__ ws,
+                                                            uint8_t* __restrict__ sc8,
+                                                            float* __restrict__ sc32,
+                                                            int64_t n_groups, int64_t K) {
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= n_groups) return;
+  const uint32_t* m = ws + g * K;
+  uint32_t G = 0;
+  for (int64_t k = 0; k < K; ++k) G = umax(G, m[k]);
+  const float Gf = u2f(G);
+  for (int64_t k = 0; k < K; ++k) sc8[g * K + k] = (uint8_t)e8m0_of(u2f(m[k]), Gf);
+  sc32[g] = Gf;
+}
+
+// Elementwise cast, thread per chunk of CH elements of one block row segment.
+template <bool IS_BF16, int CH>
+__global__ __launch_bounds__(256) void k_cast_general(const void* __restrict__ x,
+                                                      uint8_t* __restrict__ q,
+                                                      const uint8_t* __restrict__ sc8,
+                                                      const float* __restrict__ sc32,
+                                                      int64_t n_chunks, int64_t W, int64_t a,
+                                                      int64_t b, int64_t K) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_chunks) return;
+  const int64_t off = t * CH;
+  const int64_t i = off / W, c = off - i * W;
+  const int64_t blk = (i / a) * (W / b) + c / b;
+  const uint32_t e = sc8[blk];
+  const float G = sc32[blk / K];
+  const float sG = e8m0_decode(e) * G;
+  const float S = quant_scale(e, G);
+  const bool ok = sG >= kClamp && sG <= 3.0e38f;
+  const float yv = 128.0f / S;
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const float xv = load_elem<IS_BF16>(x, off + k);
+    uint32_t code;
+    const float tv = xv * yv;
+    if (ok && (IS_BF16 || !near_bf16_midpoint(tv)))
+      code = bf16_to_e4m3fn(f32_to_bf16_rne_nonan(tv));
+    else
+      code = quant_elem_exact(xv, S);
+    q[off + k] = (uint8_t)code;
+  }
+}
+
+// --------------------------------------------------------------------------
+// Dequantize (and dequantize_bwd): thread per chunk of CH elements.
+//   IN: 0 = e4m3fn bytes, 1 = bf16, 2 = f32;  OUT_BF16: output dtype.
+// --------------------------------------------------------------------------
+template <int IN, bool OUT_BF16, int CH>
+__global__ __launch_bounds__(256) void k_dequant(const void* __restrict__ x,
+                                                 const uint8_t* __restrict__ sc8,
+                                                 const float* __restrict__ sc32,
+                                                 void* __restrict__ out, int64_t n_chunks,
+                                                 int64_t W, int64_t a, int64_t b, int64_t K) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_chunks) return;
+  const int64_t off = t * CH;
+  const int64_t i = off / W, c = off - i * W;
+  const int64_t blk = (i / a) * (W / b) + c / b;
+  const float sc = e8m0_decode(sc8[blk]) * sc32[blk / K];
+  float vals[CH];
+  if constexpr (IN == 0) {
+    if constexpr (CH == 8) {
+      const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(x) + off);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) vals[k] = e4m3fn_to_f32((w.x >> (8 * k)) & 0xFFu);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) vals[4 + k] = e4m3fn_to_f32((w.y >> (8 * k)) & 0xFFu);
+    } else {
+#pragma unroll
+      for (int k = 0; k < CH; ++k) vals[k] = e4m3fn_to_f32(static_cast<const uint8_t*>(x)[off + k]);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < CH; ++k) vals[k] = load_elem<IN == 1>(x, off + k);
+  }
+#pragma unroll
+  for (int k = 0; k < CH; ++k) vals[k] = (vals[k] * sc) * 0.0078125f;
+  if constexpr (OUT_BF16) {
+    uint16_t* o = static_cast<uint16_t*>(out) + off;
+    if constexpr (CH == 8) {
+      uint4 w;
+      w.x = f32_to_bf16_rne(vals[0]) | (f32_to_bf16_rne(vals[1]) << 16);
+      w.y = f32_to_bf16_rne(vals[2]) | (f32_to_bf16_rne(vals[3]) << 16);
+      w.z = f32_to_bf16_rne(vals[4]) | (f32_to_bf16_rne(vals[5]) << 16);
+      w.w = f32_to_bf16_rne(vals[6]) | (f32_to_bf16_rne(vals[7]) << 16);
+      *reinterpret_cast<uint4*>(o) = w;
+    } else {
+#pragma unroll
+      for (int k = 0; k < CH; ++k) o[k] = (uint16_t)f32_to_bf16_rne(vals[k]);
+    }
+  } else {
+    float* o = static_cast<float*>(out) + off;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) o[k] = vals[k];
+  }
+}
+
+// --------------------------------------------------------------------------
+// Debug conversion kernels (test hooks)
+// --------------------------------------------------------------------------
+template <bool HW>
+__global__ void k_dbg_bf16_e4m3(const uint16_t* __restrict__ in, uint8_t* __restrict__ out,
+                                int64_t n4) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n4) return;
+  const uint16_t* p = in + 4 * t;
+  const uint32_t r = cvt4<HW>(u2f((uint32_t)p[0] << 16), u2f((uint32_t)p[1] << 16),
+                              u2f((uint32_t)p[2] << 16), u2f((uint32_t)p[3] << 16));
+  *reinterpret_cast<uint32_t*>(out + 4 * t) = r;
+}
+
+template <bool HW>
+__global__ void k_dbg_f32_bf16(const float* __restrict__ in, uint16_t* __restrict__ out,
+                               int64_t n) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n) return;
+  if constexpr (HW) {
+    out[t] = __builtin_bit_cast(uint16_t, (__bf16)in[t]);
+  } else {
+    out[t] = (uint16_t)f32_to_bf16_rne(in[t]);
+  }
+}
+
+// --------------------------------------------------------------------------
+// Host side
+// --------------------------------------------------------------------------
+namespace {
+
+struct Layout {
+  int64_t S, H, W, a, b, n_blk, K, M;
+  int64_t rows() const { return S * H; }
+  int64_t n() const { return S * H * W; }
+};
+
+int64_t gcd64(int64_t x, int64_t y) {
+  while (y) {
+    int64_t t = x % y;
+    x = y;
+    y = t;
+  }
+  return x < 0 ? -x : x;
+}
+
+int make_layout(int64_t S, int64_t H, int64_t W, int64_t a, int64_t b, Layout* L) {
+  if (S < 0 || H < 0 || W < 0)
+    return pratchya_set_error(PRATCHYA_EINVAL, "negative shape (%lld, %lld, %lld)", (long long)S,
+                              (long long)H, (long long)W);
+  if (a < 1 || b < 1)
+    return pratchya_set_error(PRATCHYA_EINVAL, "tgrid (%lld, %lld) must be positive", (long long)a,
+                              (long long)b);
+  if (H % a || W % b)
+    return pratchya_set_error(PRATCHYA_EINVAL,
+                              "tgrid (%lld, %lld) does not divide the slice shape (%lld, %lld)",
+                              (long long)a, (long long)b, (long long)H, (long long)W);
+  L->S = S; L->H = H; L->W = W; L->a = a; L->b = b;
+  L->n_blk = (H / a) * (W / b);
+  const int64_t target = (a * b) / 16 > 1 ? (a * b) / 16 : 1;
+  L->K = gcd64(target, L->n_blk);
+  L->M = L->K ? L->n_blk / L->K : 0;
+  return PRATCHYA_OK;
+}
+
+bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+int ilog2(int64_t v) {
+  int r = 0;
+  while ((int64_t(1) << r) < v) ++r;
+  return r;
+}
+bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
+
+// Parameters of the row-group kernel, or false if it does not apply.
+struct RowGroupPlan {
+  int R, bl_log2, gl_log2;
+  bool span;
+};
+
+bool plan_rowgroup(const Layout& L, bool bf16, const void* x, const void* q, RowGroupPlan* p) {
+  const int VEC = bf16 ? 8 : 4;
+  if (L.a != 1 || L.b % VEC) return false;
+  const int64_t BL = L.b / VEC, GL = BL * L.K;
+  if (!is_pow2(BL) || BL > 64 || !is_pow2(GL) || GL > 256) return false;
+  if (!aligned(x, 16) || !aligned(q, bf16 ? 8 : 4)) return false;
+  p->bl_log2 = ilog2(BL);
+  p->gl_log2 = ilog2(GL);
+  if (GL > 64) {
+    p->span = true;
+    p->R = (int)(GL / 64);
+  } else {
+    p->span = false;
+    p->R = 2;
+  }
+  return true;
+}
+
+int chunk_elems(int64_t b, bool bf16) {
+  const int cap = bf16 ? 8 : 4;
+  int ch = 1;
+  while (ch < cap && b % (ch * 2) == 0) ch *= 2;
+  return ch;
+}
+
+template <bool IS_BF16, int R, bool SPAN>
+void launch_rowgroup_t(const void* x, uint8_t* q, uint8_t* sc8, float* sc32, int64_t n,
+                       const RowGroupPlan& p, hipStream_t st) {
+  constexpr int VEC = IS_BF16 ? 8 : 4;
+  const int64_t tile = (int64_t)R * 64 * VEC;
+  const int64_t waves = (n + tile - 1) / tile;
+  const int64_t blocks = (waves + 3) / 4;
+  hipLaunchKernelGGL((k_quant_rowgroup<IS_BF16, R, SPAN, PRATCHYA_HW_CVT != 0>), dim3((unsigned)blocks),
+                     dim3(256), 0, st, x, q, sc8, sc32, n, p.bl_log2, p.gl_log2);
+}
+
+template <bool IS_BF16>
+int launch_rowgroup(const void* x, uint8_t* q, uint8_t* sc8, float* sc32, int64_t n,
+                    const RowGroupPlan& p, hipStream_t st) {
+  if (p.span) {
+    switch (p.R) {
+      case 2: launch_rowgroup_t<IS_BF16, 2, true>(x, q, sc8, sc32, n, p, st); break;
+      case 4: launch_rowgroup_t<IS_BF16, 4, true>(x, q, sc8, sc32, n, p, st); break;
+      default: return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "row-group plan R=%d", p.R);
+    }
+  } else {
+    launch_rowgroup_t<IS_BF16, 2, false>(x, q, sc8, sc32, n, p, st);
+  }
+  return check_launch("quantize(row-group)");
+}
+
+unsigned grid_for(int64_t n, int per_block) {
+  int64_t g = (n + per_block - 1) / per_block;
+  return (unsigned)(g < 1 ? 1 : g);
+}
+
+template <bool IS_BF16>
+int launch_general(const void* x, uint8_t* q, uint8_t* sc8, float* sc32, uint32_t* ws,
+                   const Layout& L, hipStream_t st) {
+  const int64_t n_blocks_total = L.S * L.n_blk;
+  const int64_t n_groups = L.S * L.M;
+  hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(n_blocks_total, 256) > 4096 ? 4096 : grid_for(n_blocks_total, 256)),
+                     dim3(256), 0, st, ws, n_blocks_total, 0u);
+  const int ch = chunk_elems(L.b, IS_BF16);
+  const int64_t n_chunks = L.n() / ch;
+  const int64_t seg = L.b / ch;
+  const int seg_log2 = (is_pow2(seg) && seg <= 64) ? ilog2(seg) : -1;
+  const unsigned gr = grid_for(n_chunks, 256);
+#define PRATCHYA_BM(C)                                                                            \
+  hipLaunchKernelGGL((k_blockmax<IS_BF16, C>), dim3(gr), dim3(256), 0, st, x, ws, n_chunks, L.W, \
+                     L.a, L.b, seg_log2)
+  switch (ch) {
+    case 1: PRATCHYA_BM(1); break;
+    case 2: PRATCHYA_BM(2); break;
+    case 4: PRATCHYA_BM(4); break;
+    default: PRATCHYA_BM(8); break;
+  }
+#undef PRATCHYA_BM
+  if (L.K >= 32)
+    hipLaunchKernelGGL(k_group_scales, dim3(grid_for(n_groups, 4)), dim3(256), 0, st, ws, sc8,
+                       sc32, n_groups, L.K);
+  else
+    hipLaunchKernelGGL(k_group_scales_small, dim3(grid_for(n_groups, 256)), dim3(256), 0, st, ws,
+                       sc8, sc32, n_groups, L.K);
+#define PRATCHYA_CAST(C)                                                                     \
+  hipLaunchKernelGGL((k_cast_general<IS_BF16, C>), dim3(gr), dim3(256), 0, st, x, q, sc8, sc32, \
+                     n_chunks, L.W, L.a, L.b, L.K)
+  switch (ch) {
+    case 1: PRATCHYA_CAST(1); break;
+    case 2: PRATCHYA_CAST(2); break;
+    case 4: PRATCHYA_CAST(4); break;
+    default: PRATCHYA_CAST(8); break;
+  }
+#undef PRATCHYA_CAST
+  return check_launch("quantize(general)");
+}
+
+}  // namespace
+
+extern "C" int pratchya_quant_layout(int64_t H, int64_t W, int64_t a, int64_t b, int64_t* n_blk,
+                                     int64_t* K, int64_t* M) {
+  Layout L;
+  int rc = make_layout(1, H, W, a, b, &L);
+  if (rc) return rc;
+  if (n_blk) *n_blk = L.n_blk;
+  if (K) *K = L.K;
+  if (M) *M = L.M;
+  return PRATCHYA_OK;
+}
+
+extern "C" size_t pratchya_quantize_workspace_bytes(int x_dtype, int64_t slices, int64_t H,
+                                                    int64_t W, int64_t a, int64_t b) {
+  Layout L;
+  if (make_layout(slices, H, W, a, b, &L)) return 0;
+  // The single-pass row-group kernel needs no workspace.  It applies when the
+  // shape allows it and x is 16-byte / x_fp8 8-byte (f32: 4-byte) aligned.
+  static const char probe[16] __attribute__((aligned(16))) = {0};
+  RowGroupPlan p;
+  if (plan_rowgroup(L, x_dtype == PRATCHYA_DT_BF16, probe, probe, &p)) return 0;
+  return (size_t)(L.S * L.n_blk) * sizeof(uint32_t);
+}
+
+extern "C" int pratchya_quantize(const void* x, int x_dtype, int64_t slices, int64_t H, int64_t W,
+                                 int64_t a, int64_t b, uint8_t* x_fp8, uint8_t* sc_fp8,
+                                 float* sc_fp32, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream) {
+  Layout L;
+  int rc = make_layout(slices, H, W, a, b, &L);
+  if (rc) return rc;
+  if (x_dtype != PRATCHYA_DT_F32 && x_dtype != PRATCHYA_DT_BF16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize: unsupported input dtype %d", x_dtype);
+  const int64_t n = L.n();
+  if (n == 0) {
+    g_err[0] = 0;
+    return PRATCHYA_OK;
+  }
+  if (!x || !x_fp8 || !sc_fp8 || !sc_fp32)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize: null buffer");
+  const bool bf16 = x_dtype == PRATCHYA_DT_BF16;
+  RowGroupPlan p;
+  if (plan_rowgroup(L, bf16, x, x_fp8, &p))
+    return bf16 ? launch_rowgroup<true>(x, x_fp8, sc_fp8, sc_fp32, n, p, stream)
+                : launch_rowgroup<false>(x, x_fp8, sc_fp8, sc_fp32, n, p, stream);
+  const size_t need = (size_t)(L.S * L.n_blk) * sizeof(uint32_t);
+  if (!workspace || workspace_bytes < need)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize: workspace of %zu bytes needed, got %zu",
+                              need, workspace_bytes);
+  uint32_t* ws = static_cast<uint32_t*>(workspace);
+  return bf16 ? launch_general<true>(x, x_fp8, sc_fp8, sc_fp32, ws, L, stream)
+              : launch_general<false>(x, x_fp8, sc_fp8, sc_fp32, ws, L, stream);
+}
+
+namespace {
+template <int IN, bool OUT_BF16>
+int launch_dequant(const void* x, const uint8_t* sc8, const float* sc32, void* out,
+                   const Layout& L, hipStream_t st) {
+  const int ch = chunk_elems(L.b, true);
+  const int64_t n_chunks = L.n() / ch;
+  const unsigned gr = grid_for(n_chunks, 256);
+  // the 8-wide path loads 8 payload bytes at once and stores 8 bf16 at once
+  const bool vec_ok = ch == 8 && (IN != 0 || aligned(x, 8)) && (!OUT_BF16 || aligned(out, 16));
+#define PRATCHYA_DQ(C)                                                                    \
+  hipLaunchKernelGGL((k_dequant<IN, OUT_BF16, C>), dim3(gr), dim3(256), 0, st, x, sc8, sc32, \
+                     out, n_chunks, L.W, L.a, L.b, L.K)
+  if (ch == 8 && !vec_ok) {
+    const int64_t n4 = L.n() / 4;
+    hipLaunchKernelGGL((k_dequant<IN, OUT_BF16, 4>), dim3(grid_for(n4, 256)), dim3(256), 0, st, x,
+                       sc8, sc32, out, n4, L.W, L.a, L.b, L.K);
+  } else {
+    switch (ch) {
+      case 1: PRATCHYA_DQ(1); break;
+      case 2: PRATCHYA_DQ(2); break;
+      case 4: PRATCHYA_DQ(4); break;
+      default: PRATCHYA_DQ(8); break;
+    }
+  }
+#undef PRATCHYA_DQ
+  return check_launch("dequantize");
+}
+}  // namespace
+
+extern "C" int pratchya_dequantize(const uint8_t* x_fp8, const uint8_t* sc_fp8,
+                                   const float* sc_fp32, int64_t slices, int64_t H, int64_t W,
+                                   int64_t a, int64_t b, void* out, int out_dtype,
+                                   hipStream_t stream) {
+  Layout L;
+  int rc = make_layout(slices, H, W, a, b, &L);
+  if (rc) return rc;
+  if (out_dtype != PRATCHYA_DT_F32 && out_dtype != PRATCHYA_DT_BF16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "dequantize: unsupported output dtype %d", out_dtype);
+  if (L.n() == 0) {
+    g_err[0] = 0;
+    return PRATCHYA_OK;
+  }
+  if (!x_fp8 || !sc_fp8 || !sc_fp32 || !out)
+    return pratchya_set_error(PRATCHYA_EINVAL, "dequantize: null buffer");
+  return out_dtype == PRATCHYA_DT_BF16 ? launch_dequant<0, true>(x_fp8, sc_fp8, sc_fp32, out, L, stream)
+                                       : launch_dequant<0, false>(x_fp8, sc_fp8, sc_fp32, out, L, stream);
+}
+
+extern "C" int pratchya_dequantize_bwd(const void* g, int g_dtype, const uint8_t* sc_fp8,
+                                       const float* sc_fp32, int64_t slices, int64_t H, int64_t W,
+                                       int64_t a, int64_t b, void* out, hipStream_t stream) {
+  Layout L;
+  int rc = make_layout(slices, H, W, a, b, &L);
+  if (rc) return rc;
+  if (g_dtype != PRATCHYA_DT_F32 && g_dtype != PRATCHYA_DT_BF16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "dequantize_bwd: unsupported dtype %d", g_dtype);
+  if (L.n() == 0) {
+    g_err[0] = 0;
+    return PRATCHYA_OK;
+  }
+  if (!g || !sc_fp8 || !sc_fp32 || !out)
+    return pratchya_set_error(PRATCHYA_EINVAL, "dequantize_bwd: null buffer");
+  return g_dtype == PRATCHYA_DT_BF16 ? launch_dequant<1, true>(g, sc_fp8, sc_fp32, out, L, stream)
+                                     : launch_dequant<2, false>(g, sc_fp8, sc_fp32, out, L, stream);
+}
+
+extern "C" int pratchya_debug_bf16_to_e4m3(const uint16_t* in, uint8_t* out, int64_t n, int mode,
+                                           hipStream_t stream) {
+  if (n % 4 || n < 0) return pratchya_set_error(PRATCHYA_EINVAL, "debug: n must be a multiple of 4");
+  if (n == 0) return PRATCHYA_OK;
+  const int64_t n4 = n / 4;
+  if (mode == 1)
+    hipLaunchKernelGGL(k_dbg_bf16_e4m3<true>, dim3(grid_for(n4, 256)), dim3(256), 0, stream, in, out, n4);
+  else
+    hipLaunchKernelGGL(k_dbg_bf16_e4m3<false>, dim3(grid_for(n4, 256)), dim3(256), 0, stream, in, out, n4);
+  return check_launch("debug_bf16_to_e4m3");
+}
+
+extern "C" int pratchya_debug_f32_to_bf16(const float* in, uint16_t* out, int64_t n, int mode,
+                                          hipStream_t stream) {
+  if (n < 0) return pratchya_set_error(PRATCHYA_EINVAL, "debug: negative n");
+  if (n == 0) return PRATCHYA_OK;
+  if (mode == 1)
+    hipLaunchKernelGGL(k_dbg_f32_bf16<true>, dim3(grid_for(n, 256)), dim3(256), 0, stream, in, out, n);
+  else
+    hipLaunchKernelGGL(k_dbg_f32_bf16<false>, dim3(grid_for(n, 256)), dim3(256), 0, stream, in, out, n);
+  return check_launch("debug_f32_to_bf16");
+}

@@ -1,0 +1,71 @@
+"""The C-ABI library loads and exports every entry point the headers declare.
+
+CPU-only: no kernel is launched here (no GPU in the build container).
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+
+
+def declared_symbols():
+    names = set()
+    for h in HEADERS:
+        text = h.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"\b(pratchya_[a-z0-9_]+)\s*\(", text):
+            names.add(m.group(1))
+    return sorted(names)
+
+
+def test_headers_declare_entry_points():
+    names = declared_symbols()
+    assert "pratchya_quantize" in names and "pratchya_dequantize" in names
+    assert len(names) >= 8
+
+
+def test_library_exports_every_declared_symbol():
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    missing = [n for n in declared_symbols() if not hasattr(lib, n)]
+    assert not missing, f"missing exports: {missing}"
+
+
+def test_python_binding_covers_every_declared_symbol():
+    from pratchya_amd import _lib
+    assert set(declared_symbols()) <= set(_lib.SIGNATURES), \
+        set(declared_symbols()) - set(_lib.SIGNATURES)
+
+
+def test_layout_and_argument_errors_without_gpu():
+    from pratchya_amd import _kernels
+    assert _kernels.group_layout(1024, 1024, (128, 128)) == (64, 64, 1)
+    assert _kernels.group_layout(16384, 2048, (1, 128)) == (262144, 8, 32768)
+    assert _kernels.group_layout(0, 128, (1, 128)) == (0, 8, 0)
+    with pytest.raises(ValueError, match="does not divide"):
+        _kernels.group_layout(10, 10, (3, 5))
+
+
+def test_workspace_query():
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    # (1,128) bf16 takes the single-pass kernel: no workspace
+    assert lib.pratchya_quantize_workspace_bytes(_lib.DT_BF16, 1, 16384, 2048, 1, 128) == 0
+    # (128,128) needs one u32 per block
+    assert lib.pratchya_quantize_workspace_bytes(_lib.DT_BF16, 1, 2048, 8192, 128, 128) == 1024 * 4
+
+
+def test_invalid_tgrid_is_einval_without_launch():
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    rc = lib.pratchya_quantize(None, _lib.DT_F32, 1, 10, 10, 3, 5, None, None, None, None, 0, None)
+    assert rc == _lib.EINVAL
+    assert b"does not divide" in lib.pratchya_last_error()
+    rc = lib.pratchya_quantize(None, 7, 1, 8, 8, 1, 8, None, None, None, None, 0, None)
+    assert rc == _lib.EINVAL
+    # empty tensors are valid no-ops
+    assert lib.pratchya_quantize(None, _lib.DT_F32, 1, 0, 128, 1, 128, None, None, None, None, 0, None) == 0

@@ -55,6 +55,34 @@ def cpu_baseline_quantize(rows: int = 2048, min_seconds: float = 10.0):
                       f"config 2, tgrid (1,128), {reps} reps, {el:.1f} s (NumPy, single thread)"}
 
 
+def timed_graph(step, steps: int, warmup: int, per_graph: int):
+    """Capture ``per_graph`` consecutive steps in one HIP graph, replay it
+    (removes host launch gaps), and time the replays with events recorded on
+    the stream the kernels run on.  Returns (ms per step, wall seconds)."""
+    import torch
+    for i in range(max(warmup, 1)):
+        step(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(per_graph):
+            step(i)
+    reps = max(1, -(-steps // per_graph))
+    for _ in range(max(1, warmup // per_graph)):
+        g.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(st)
+    for _ in range(reps):
+        g.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return e0.elapsed_time(e1) / (reps * per_graph), wall
+
+
 def bench_quantize(steps: int, warmup: int):
     import torch
     from oracle import qarr_oracle as O
@@ -71,32 +99,18 @@ def bench_quantize(steps: int, warmup: int):
     from pratchya_amd import _lib
     import ctypes
     lib = _lib.load()
-    st = torch.cuda.current_stream()
-    stream = ctypes.c_void_p(st.cuda_stream)
 
     def step(i):
         x = xs[i % n_sets]
         q8, s8, s32 = outs[i % n_sets]
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         rc = lib.pratchya_quantize(ctypes.c_void_p(x.data_ptr()), _lib.DT_BF16, 1, CFG2_ROWS, CFG2_COLS,
                                    1, 128, ctypes.c_void_p(q8.data_ptr()), ctypes.c_void_p(s8.data_ptr()),
                                    ctypes.c_void_p(s32.data_ptr()), None, 0, stream)
         if rc:
             raise RuntimeError(lib.pratchya_last_error().decode())
 
-    for i in range(warmup):
-        step(i)
-    torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev[0].record(st)
-    for i in range(steps):
-        step(i)
-        ev[i + 1].record(st)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per_launch_ms = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
-    ms = sum(per_launch_ms) / steps
+    ms, wall = timed_graph(step, steps, warmup, per_graph=n_sets)
     # parity spot check of the last output against the oracle on a slice
     q8, s8, s32 = outs[(steps - 1) % n_sets]
     xb = O.activation_input(CFG2_ROWS, CFG2_COLS, seed=2)[:64]

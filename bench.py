@@ -119,12 +119,36 @@ def bench_quantize(steps: int, warmup: int):
     return ms, wall, ok
 
 
+def bench_gemm_fwd(steps: int, warmup: int):
+    """Config 3: A = quantize(cfg2 activation, (1,128)) [16384, 2048] x
+    W = quantize(N(0, 0.02) [2048, 8192], (128,128)) -> bf16 [16384, 8192].
+    The weight's K-contiguous payload copy is made once, outside the timed
+    region (a weight is quantized once per optimizer step).  Returns
+    (ms per GEMM, TFLOP/s)."""
+    import torch
+    from oracle import qarr_oracle as O
+    from pratchya_amd import _kernels as K
+    M, Kd, N = 16384, 2048, 8192
+    x = torch.from_numpy(O.activation_input(M, Kd, seed=2).view(np.int16)).view(torch.bfloat16).cuda()
+    w = torch.from_numpy(O.normal_input((Kd, N), 0.02, seed=3).view(np.int16)).view(torch.bfloat16).cuda()
+    a = K.operand_rows(*K.quantize(x, (1, 128)), (1, 128))
+    b = K.operand_transposed(*K.quantize(w, (128, 128)), (128, 128))
+    outs = [torch.empty((M, N), dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+
+    def step(i):
+        K.gemm_nt(a, b, out=outs[i % 2])
+
+    ms, _ = timed_graph(step, steps, warmup, per_graph=4)
+    return ms, 2.0 * M * N * Kd / (ms * 1e-3) / 1e12
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-gemm", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -140,6 +164,15 @@ def main():
     ms, wall, ok = bench_quantize(args.steps, args.warmup)
     _log(f"config 2 quantize: {ms * 1e3:.2f} us/step, parity spot check {'ok' if ok else 'FAILED'}")
     gbs = CFG2_BYTES / (ms * 1e-3) / 1e9
+    extra = {}
+    if not args.no_gemm:
+        _log("config 3 gemm fwd: start")
+        gms, tflops = bench_gemm_fwd(max(8, args.steps // 4), max(4, args.warmup // 4))
+        _log(f"config 3 gemm fwd: {gms * 1e3:.1f} us, {tflops:.1f} TFLOP/s")
+        extra["config3_gemm_fwd"] = {"value": round(tflops, 1), "unit": "TFLOP/s", "ms": round(gms, 4),
+                                     "frac_of_fp8_peak": round(tflops / FP8_PEAK_TFLOPS, 4),
+                                     "shape": "[16384,2048] x [2048,8192] -> bf16",
+                                     "flop": 2 * 16384 * 2048 * 8192}
     cpu = None
     if not args.no_cpu_baseline:
         _log("cpu baseline: start")
@@ -165,6 +198,7 @@ def main():
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": cpu,
         "parity_spot_check": ok,
+        "extra": extra,
     }
     print(json.dumps(line), flush=True)
 

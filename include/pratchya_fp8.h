@@ -85,6 +85,38 @@ int pratchya_dequantize_bwd(const void* g, int g_dtype, const uint8_t* sc_fp8,
                             const float* sc_fp32, int64_t slices, int64_t H, int64_t W,
                             int64_t a, int64_t b, void* out, hipStream_t stream);
 
+/* Block-scaled FP8 GEMM, "NT" form:                         replaces the f32 dot
+ *   C[m, n] = sum_k dequant(A)[m, k] * dequant(B)[n, k]      of matmul_impl
+ * (Q:605-608) and of its backward (Q:621-622), with FP8 operands.
+ * A: e4m3fn [M, K] (row stride lda bytes), B: e4m3fn [N, K] (ldb); both
+ * K-contiguous.  Each operand's scales are the (sc_fp8, sc_fp32) pair of the
+ * quantizer, addressed for (row, 128-wide K block kb) as
+ *   block = (row / rdiv) * sr + kb * sk,  e8m0 = sc8[block],  G = sc32[block / kg]
+ * so that an operand quantized as [rows, K] with tgrid (a, 128) is
+ * (rdiv, sr, sk, kg) = (a, K/128, 1, K_group), and one quantized as [K, rows]
+ * with tgrid (128, b) and transposed is (b, 1, rows/b, K_group).
+ * C: [M, N] with row stride ldc elements, c_dtype f32 or bf16.
+ * M and N must be multiples of 256 and K of 128 (PRATCHYA_EUNSUPPORTED
+ * otherwise); the group index must be affine in kb (every quantizer layout is). */
+int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, const float* a_sc32,
+                        int64_t a_rdiv, int64_t a_sr, int64_t a_sk, int64_t a_kg,
+                        const uint8_t* B, int64_t ldb, const uint8_t* b_sc8, const float* b_sc32,
+                        int64_t b_rdiv, int64_t b_sr, int64_t b_sk, int64_t b_kg,
+                        int64_t M, int64_t N, int64_t K, void* C, int64_t ldc, int c_dtype,
+                        hipStream_t stream);
+
+/* Number of consecutive 128-K blocks over which an operand's group maxima stay
+ * constant (the GEMM rescales its accumulator at those boundaries); 0 if the
+ * layout is not supported.  Host-only query, used by tests. */
+int64_t pratchya_gemm_span(int64_t rows, int64_t K, int64_t r_div, int64_t s_r, int64_t s_k,
+                           int64_t kg);
+
+/* Byte transpose of an fp8 payload: src [rows, cols] -> dst [cols, rows]
+ * (the K-contiguous operand layout the GEMM reads; QArrayImpl.T, Q:349-352,
+ * moves the data the same way).  rows and cols multiples of 64. */
+int pratchya_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* dst,
+                          hipStream_t stream);
+
 /* Test hooks for the element conversions the kernels use (no reference
  * counterpart; they let the tests check the device arithmetic exhaustively).
  *   mode 0: software bit arithmetic, mode 1: gfx950 conversion instructions.

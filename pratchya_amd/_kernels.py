@@ -153,3 +153,88 @@ def debug_f32_to_bf16(x: torch.Tensor, mode: int) -> torch.Tensor:
     _lib.check(_lib.load().pratchya_debug_f32_to_bf16(_ptr(x), _ptr(out), x.numel(), mode,
                                                       _stream(x)), "debug_f32_to_bf16")
     return out
+
+
+# --------------------------------------------------------------------------
+# Block-scaled FP8 GEMM operands
+# --------------------------------------------------------------------------
+class Operand:
+    """An FP8 GEMM operand in the K-contiguous layout the GEMM reads.
+
+    ``payload``: e4m3fn/uint8 [rows, K]; ``sc8``/``sc32``: the quantizer's
+    scale arrays; ``desc``: (rdiv, sr, sk, kg) addressing the block of
+    (row, 128-wide K block kb) as (row // rdiv) * sr + kb * sk, its group as
+    block // kg.
+    """
+
+    __slots__ = ("payload", "sc8", "sc32", "desc")
+
+    def __init__(self, payload, sc8, sc32, desc):
+        self.payload = payload
+        self.sc8 = sc8
+        self.sc32 = sc32
+        self.desc = tuple(int(v) for v in desc)
+
+    @property
+    def rows(self) -> int:
+        return int(self.payload.shape[0])
+
+    @property
+    def k(self) -> int:
+        return int(self.payload.shape[1])
+
+
+def operand_rows(x8: torch.Tensor, sc8: torch.Tensor, sc32: torch.Tensor, tgrid) -> Operand:
+    """Operand from a 2-D tensor quantized as [rows, K] with tgrid (a, 128)
+    (activations (1,128), dY, weights used as W[k_out, n] in dgrad)."""
+    a, b = int(tgrid[0]), int(tgrid[1])
+    if b != 128 or x8.dim() != 2:
+        raise ValueError(f"operand_rows needs a 2-D payload quantized with tgrid (a, 128), got {tgrid}")
+    R, K = x8.shape
+    _, kg, _ = group_layout(R, K, (a, b))
+    return Operand(x8, sc8, sc32, (a, K // 128, 1, kg))
+
+
+def operand_transposed(x8: torch.Tensor, sc8: torch.Tensor, sc32: torch.Tensor, tgrid,
+                       payload_t: torch.Tensor = None) -> Operand:
+    """Operand from a 2-D tensor quantized as [K, rows] with tgrid (128, b) and
+    contracted over its first axis (weights W[K, N] in the forward; (128,1)
+    token-axis quantized A and dY in wgrad).  The payload is transposed to
+    [rows, K] (or ``payload_t`` is used if the caller already holds it)."""
+    a, b = int(tgrid[0]), int(tgrid[1])
+    if a != 128 or x8.dim() != 2:
+        raise ValueError(f"operand_transposed needs a 2-D payload quantized with tgrid (128, b), got {tgrid}")
+    K, R = x8.shape
+    _, kg, _ = group_layout(K, R, (a, b))
+    pt = transpose_u8(x8) if payload_t is None else payload_t
+    return Operand(pt, sc8, sc32, (b, 1, R // b, kg))
+
+
+def transpose_u8(x8: torch.Tensor) -> torch.Tensor:
+    """[rows, cols] fp8 payload -> [cols, rows] (same dtype)."""
+    _require_gpu(x8)
+    src = _u8(x8).contiguous()
+    R, C = src.shape
+    out = torch.empty((C, R), dtype=torch.uint8, device=src.device)
+    _lib.check(_lib.load().pratchya_transpose_u8(_ptr(src), R, C, _ptr(out), _stream(src)), "transpose")
+    return out.view(x8.dtype) if x8.dtype != torch.uint8 else out
+
+
+def gemm_nt(a: Operand, b: Operand, out_dtype: torch.dtype = torch.bfloat16,
+            out: torch.Tensor = None) -> torch.Tensor:
+    """C[M, N] = dequant(a) @ dequant(b)^T on the FP8 MFMA kernel."""
+    _require_gpu(a.payload, b.payload)
+    if a.k != b.k:
+        raise ValueError(f"contraction mismatch: {a.k} vs {b.k}")
+    M, N, K = a.rows, b.rows, a.k
+    ap, bp = _u8(a.payload).contiguous(), _u8(b.payload).contiguous()
+    as8, bs8 = _u8(a.sc8).contiguous(), _u8(b.sc8).contiguous()
+    as32, bs32 = a.sc32.contiguous().float(), b.sc32.contiguous().float()
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=ap.device)
+    lib = _lib.load()
+    _lib.check(lib.pratchya_gemm_bs_nt(_ptr(ap), K, _ptr(as8), _ptr(as32), *a.desc,
+                                       _ptr(bp), K, _ptr(bs8), _ptr(bs32), *b.desc,
+                                       M, N, K, _ptr(out), out.stride(0), _dtype_code(out.dtype),
+                                       _stream(ap)), "gemm")
+    return out

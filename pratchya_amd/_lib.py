@@ -34,6 +34,11 @@ SIGNATURES = {
                                      _c_p, _c_int, _c_p]),
     "pratchya_dequantize_bwd": (_c_int, [_c_p, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
                                          _c_i64, _c_p, _c_p]),
+    "pratchya_gemm_bs_nt": (_c_int, [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
+                                     _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
+                                     _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_int, _c_p]),
+    "pratchya_gemm_span": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
+    "pratchya_transpose_u8": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "pratchya_debug_bf16_to_e4m3": (_c_int, [_c_p, _c_p, _c_i64, _c_int, _c_p]),
     "pratchya_debug_f32_to_bf16": (_c_int, [_c_p, _c_p, _c_i64, _c_int, _c_p]),
 }

@@ -316,6 +316,19 @@ __device__ __forceinline__ uint4 load_stream16(const char* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+#ifndef PRATCHYA_NT_STORE
+#define PRATCHYA_NT_STORE 1
+#endif
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void store_stream8(uint8_t* p, u32x2_t w) {
+  if (PRATCHYA_NT_STORE) __builtin_nontemporal_store(w, reinterpret_cast<u32x2_t*>(p));
+  else *reinterpret_cast<u32x2_t*>(p) = w;
+}
+__device__ __forceinline__ void store_stream4(uint8_t* p, uint32_t w) {
+  if (PRATCHYA_NT_STORE) __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(p));
+  else *reinterpret_cast<uint32_t*>(p) = w;
+}
+
 // max |x| (as f32 bits) of 8 packed bf16 values, on packed 16-bit lanes.
 typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t absmax8_bf16(const uint4& v) {
@@ -450,10 +463,12 @@ __global__ __launch_bounds__(256) void k_quant_g8(const void* __restrict__ xv,
     uint8_t* qg = q + g * 1024;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      if constexpr (IS_BF16)
-        *reinterpret_cast<uint2*>(qg + (r * 64 + lane) * 8) = make_uint2(out[r][0], out[r][1]);
-      else
-        *reinterpret_cast<uint32_t*>(qg + (r * 64 + lane) * 4) = out[r][0];
+      if constexpr (IS_BF16) {
+        const u32x2_t w = {out[r][0], out[r][1]};
+        store_stream8(qg + (r * 64 + lane) * 8, w);
+      } else {
+        store_stream4(qg + (r * 64 + lane) * 4, out[r][0]);
+      }
     }
     // the group's 8 e8m0 bytes (block k: row k / BPR, leader lane (k % BPR) * BL) and G
     uint32_t lo = 0, hi = 0;
@@ -825,10 +840,14 @@ bool use_g8(const Layout& L, bool bf16, const void* x, const void* q, const void
          aligned(sc8, 8);
 }
 
+#ifndef PRATCHYA_G8_BLOCKS_PER_CU
+#define PRATCHYA_G8_BLOCKS_PER_CU 8
+#endif
+
 int launch_g8(bool bf16, const void* x, uint8_t* q, uint8_t* sc8, float* sc32, int64_t n_groups,
               hipStream_t st) {
   int64_t blocks = (n_groups + 3) / 4;
-  const int64_t cap = (int64_t)num_cus() * 8;
+  const int64_t cap = (int64_t)num_cus() * PRATCHYA_G8_BLOCKS_PER_CU;
   if (blocks > cap) blocks = cap;
   if (bf16)
     hipLaunchKernelGGL((k_quant_g8<true, PRATCHYA_HW_CVT != 0>), dim3((unsigned)blocks), dim3(256), 0,

@@ -6,6 +6,7 @@ import ctypes
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -69,3 +70,36 @@ def test_invalid_tgrid_is_einval_without_launch():
     assert rc == _lib.EINVAL
     # empty tensors are valid no-ops
     assert lib.pratchya_quantize(None, _lib.DT_F32, 1, 0, 128, 1, 128, None, None, None, None, 0, None) == 0
+
+
+@pytest.mark.parametrize("rows,K,desc,expect", [
+    (16384, 2048, (1, 16, 1, 8), 8),          # (1,128) activation [16384, 2048]
+    (8192, 2048, (128, 1, 64, 1024), 16),     # W [2048, 8192] (128,128) used transposed
+    (2048, 8192, (128, 64, 1, 1024), 64),     # W [2048, 8192] (128,128) rows in dgrad
+    (2048, 16384, (1, 1, 2048, 8), 1),        # (128,1) token-axis A [16384, 2048] transposed
+    (4096, 16384, (128, 1, 32, 1024), 32),    # FFN down W [16384, 4096] used transposed
+])
+def test_gemm_group_span(rows, K, desc, expect):
+    from pratchya_amd import _lib
+    assert _lib.load().pratchya_gemm_span(rows, K, *desc) == expect
+
+
+def test_gemm_span_matches_brute_force():
+    """The span the GEMM uses keeps every row's group index constant."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    rng = np.random.default_rng(0)
+    for _ in range(200):
+        nk = int(rng.choice([1, 2, 4, 8, 16]))
+        rdiv = int(rng.choice([1, 2, 4, 128]))
+        rows = rdiv * int(rng.integers(1, 9))
+        sr = int(rng.choice([0, 1, 2, 4, nk, 2 * nk]))
+        sk = int(rng.choice([0, 1, 2, 8, rows // rdiv]))
+        kg = int(rng.choice([1, 2, 4, 8, 16, 64]))
+        P = lib.pratchya_gemm_span(rows, nk * 128, rdiv, sr, sk, kg)
+        if P == 0:
+            continue
+        for rb in range(rows // rdiv):
+            g = [(rb * sr + kb * sk) // kg for kb in range(nk)]
+            for s0 in range(0, nk, P):
+                assert len(set(g[s0:s0 + P])) == 1, (rows, nk, rdiv, sr, sk, kg, P)

@@ -1,0 +1,198 @@
+"""GPU parity of the block-scaled FP8 GEMM against the oracle's
+dequant-then-matmul (pratchya/_qualia/_qarr.py:605-608, 621-622).
+
+Tolerance: relative Frobenius error <= 1e-2 for bf16
+outputs.  f32 outputs are held to 1e-3: the FP8 MFMA's internal dot-product
+accumulation is not a sequence of IEEE f32 additions (deviations of 1e-5 to
+1e-4 relative on heavy-tailed data), while its arithmetic is exact whenever the
+sums are exactly representable -- ``test_exact_integer_products`` pins that
+case bit for bit, so the kernel's indexing and scale handling are checked
+exactly and only the hardware accumulation is inside the tolerance.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import qarr_oracle as O
+from tests.helpers import f32, to_dev_bf16, to_dev_f32, u8
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 1e-2
+F32_TOL = 1e-3
+
+
+def _K():
+    from pratchya_amd import _kernels
+    return _kernels
+
+
+def quant_dev(bits_or_f32, tgrid, bf16=True):
+    K = _K()
+    dev = to_dev_bf16(bits_or_f32) if bf16 else to_dev_f32(bits_or_f32)
+    return K.quantize(dev, tgrid)
+
+
+def deq_host(x8, s8, s32, tgrid):
+    return O.dequantize_impl(u8(x8), u8(s8), f32(s32), "float32", tgrid).astype(np.float64)
+
+
+def check(C, ref, tol, what):
+    err = O.rel_fro(f32(C), ref)
+    assert err <= tol, f"{what}: relative Frobenius error {err:.3e} > {tol}"
+    return err
+
+
+@pytest.mark.parametrize("out", ["bf16", "f32"])
+def test_forward_small(out):
+    """x (1,128) @ W (128,128): the quantized Linear forward (M:46-50)."""
+    K = _K()
+    M_, K_, N_ = 512, 2048, 1024
+    x = O.activation_input(M_, K_, seed=2)
+    w = O.normal_input((K_, N_), 0.02, seed=3)
+    xa = quant_dev(x, (1, 128))
+    wq = quant_dev(w, (128, 128))
+    a = K.operand_rows(*xa, (1, 128))
+    b = K.operand_transposed(*wq, (128, 128))
+    dt = torch.bfloat16 if out == "bf16" else torch.float32
+    C = K.gemm_nt(a, b, dt)
+    torch.cuda.synchronize()
+    ref = deq_host(*xa, (1, 128)) @ deq_host(*wq, (128, 128))
+    check(C, ref, BF16_TOL if out == "bf16" else F32_TOL, f"fwd {out}")
+
+
+def test_exact_integer_products():
+    """Small-integer data whose quantized payloads, products and K-sums are all
+    exact in f32: the GEMM must reproduce the exact product bit for bit
+    (forward layout with two K spans and a two-group weight, f32 out)."""
+    K = _K()
+    M_, K_, N_ = 256, 2048, 512
+    rng = np.random.default_rng(21)
+    x = rng.integers(-8, 9, size=(M_, K_)).astype(np.float32)
+    x[:, ::128] = 8.0                     # every block max 8 -> S = G = 8, q = 16 x
+    x[3, 1024:] *= 0.5                    # a span with G = 4 in one row
+    x[5, 1024:2048] = 0.0                 # an all-zero span
+    w = rng.integers(-4, 5, size=(K_, N_)).astype(np.float32)
+    w[::128, ::128] = 4.0
+    w[1024:] *= 2.0
+    xq = quant_dev(x, (1, 128), bf16=False)
+    wq = quant_dev(w, (128, 128), bf16=False)
+    xd, wd = deq_host(*xq, (1, 128)), deq_host(*wq, (128, 128))
+    assert np.array_equal(xd, x) and np.array_equal(wd, w)   # lossless quantization
+    C = K.gemm_nt(K.operand_rows(*xq, (1, 128)), K.operand_transposed(*wq, (128, 128)), torch.float32)
+    torch.cuda.synchronize()
+    # multiples of 1/2 with sums far below 2^24: float64 (and f32) exact
+    exact = (x.astype(np.float64) @ w.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(f32(C), exact)
+
+
+def test_transpose_u8():
+    K = _K()
+    rng = np.random.default_rng(0)
+    x = rng.integers(0, 256, size=(384, 640), dtype=np.uint8)
+    t = K.transpose_u8(torch.from_numpy(x).cuda())
+    assert np.array_equal(t.cpu().numpy(), x.T)
+
+
+def test_dgrad_shape():
+    """g (1,128) @ W^T: W [K_out, N] read as B rows without a transpose."""
+    K = _K()
+    M_, N_, Ko = 512, 1024, 768
+    g = O.normal_input((M_, N_), 1e-3, seed=4)
+    w = O.normal_input((Ko, N_), 0.02, seed=3)
+    gq = quant_dev(g, (1, 128))
+    wq = quant_dev(w, (128, 128))
+    a = K.operand_rows(*gq, (1, 128))
+    b = K.operand_rows(*wq, (128, 128))
+    C = K.gemm_nt(a, b, torch.float32)
+    torch.cuda.synchronize()
+    ref = deq_host(*gq, (1, 128)) @ deq_host(*wq, (128, 128)).T
+    check(C, ref, F32_TOL, "dgrad")
+
+
+def test_wgrad_token_axis_groups():
+    """A^T dY with both operands quantized (128,1) along tokens: group maxima
+    change every K block and every 8 rows/columns."""
+    K = _K()
+    T, Cin, N_ = 1024, 512, 768
+    a = O.activation_input(T, Cin, seed=5)
+    dy = O.normal_input((T, N_), 1e-3, seed=6)
+    aq = quant_dev(a, (128, 1))
+    dq = quant_dev(dy, (128, 1))
+    A_ = K.operand_transposed(*aq, (128, 1))
+    B_ = K.operand_transposed(*dq, (128, 1))
+    C = K.gemm_nt(A_, B_, torch.float32)
+    torch.cuda.synchronize()
+    ref = deq_host(*aq, (128, 1)).T @ deq_host(*dq, (128, 1))
+    check(C, ref, F32_TOL, "wgrad")
+
+
+def test_group_maxima_change_across_spans():
+    """Rows whose 1024-wide K spans differ by orders of magnitude, all-zero
+    spans, and a weight with two groups (the accumulator rescaling path)."""
+    K = _K()
+    M_, K_, N_ = 256, 4096, 512
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((M_, K_)).astype(np.float32)
+    scale = np.array([1.0, 1e4, 1e-4, 0.0], np.float32)
+    x *= np.repeat(scale, 1024)[None, :]
+    x[::7, 1024:2048] = 0.0
+    w = (rng.standard_normal((K_, N_)) * 0.02).astype(np.float32)
+    w[2048:] *= 300.0
+    xq = quant_dev(x, (1, 128), bf16=False)
+    wq = quant_dev(w, (128, 128), bf16=False)
+    assert wq[2].numel() == 1  # one group max for this weight ([4096,512]: 128 blocks)
+    a = K.operand_rows(*xq, (1, 128))
+    b = K.operand_transposed(*wq, (128, 128))
+    C = K.gemm_nt(a, b, torch.float32)
+    torch.cuda.synchronize()
+    ref = deq_host(*xq, (1, 128)) @ deq_host(*wq, (128, 128))
+    check(C, ref, F32_TOL, "spans")
+
+
+def test_weight_with_several_groups():
+    """W [2048, 16384] (128,128): 2048 blocks, groups of 1024 -> two group
+    maxima along K (config 5's FFN weights have four)."""
+    K = _K()
+    M_, K_, N_ = 256, 2048, 16384
+    x = O.activation_input(M_, K_, seed=12)
+    rng = np.random.default_rng(13)
+    w = (rng.standard_normal((K_, N_)) * 0.02).astype(np.float32)
+    w[1024:] *= 8.0
+    xq = quant_dev(x, (1, 128))
+    wq = quant_dev(w, (128, 128), bf16=False)
+    assert wq[2].numel() == 2
+    a = K.operand_rows(*xq, (1, 128))
+    b = K.operand_transposed(*wq, (128, 128))
+    C = K.gemm_nt(a, b, torch.float32)
+    torch.cuda.synchronize()
+    ref = deq_host(*xq, (1, 128)).astype(np.float32) @ deq_host(*wq, (128, 128)).astype(np.float32)
+    check(C, ref, F32_TOL, "w two groups")
+
+
+def test_config3_full_shape_sampled_rows():
+    """Config 3 at full size; the oracle is evaluated on 192 sampled rows."""
+    K = _K()
+    M_, K_, N_ = 16384, 2048, 8192
+    x = O.activation_input(M_, K_, seed=2)
+    w = O.normal_input((K_, N_), 0.02, seed=3)
+    xq = quant_dev(x, (1, 128))
+    wq = quant_dev(w, (128, 128))
+    a = K.operand_rows(*xq, (1, 128))
+    b = K.operand_transposed(*wq, (128, 128))
+    C = K.gemm_nt(a, b, torch.bfloat16)
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(1).choice(M_, 192, replace=False))
+    xs = O.dequantize_impl(u8(xq[0])[rows], u8(xq[1]).reshape(M_, 2, 8)[rows].reshape(-1, 8),
+                           f32(xq[2]).reshape(M_, 2)[rows].reshape(-1, 1, 1), "float32", (1, 128))
+    wd = deq_host(*wq, (128, 128)).astype(np.float32)
+    ref = xs.astype(np.float32) @ wd
+    check(C[torch.from_numpy(rows).cuda()], ref, BF16_TOL, "config 3 sampled")
+
+
+def test_unsupported_shape_is_reported():
+    K = _K()
+    xq = quant_dev(O.activation_input(128, 256, seed=1), (1, 128))
+    wq = quant_dev(O.normal_input((256, 256), 0.02, seed=1), (128, 128))
+    with pytest.raises(Exception, match="multiples of 256"):
+        K.gemm_nt(K.operand_rows(*xq, (1, 128)), K.operand_transposed(*wq, (128, 128)))

@@ -8,17 +8,27 @@
 // its backward (_qarr.py:621-622) with both operands in FP8 instead of
 // dequantized f32.
 //
-// Structure (one 256x256 output tile per workgroup, 8 waves of 64x128):
+// Structure (one 256x256 output tile per workgroup of 8 waves, each wave a
+// 64x128 sub-tile, two waves per SIMD):
 //   * 128-wide K tiles staged in LDS by global_load_lds_dwordx4 (DMA straight
-//     into LDS, 64 KB per stage, two stages), rows XOR-swizzled in 16-byte
-//     chunks so that the MFMA operand reads are bank-conflict free;
+//     into LDS, two stages), rows XOR-swizzled in 16-byte chunks so that the
+//     MFMA operand reads are bank-conflict free;
+//   * the e8m0 bytes and group maxima of the stage's 256 + 256 rows travel
+//     through LDS by the same DMA;
+//   * "ping-pong": the two waves sharing a SIMD belong to two groups whose
+//     phases are offset by one workgroup barrier, so while one group runs its
+//     MFMA cluster for a 64-wide K slice the other reads its next operands
+//     from LDS (and group 0 issues the next stage's DMA);
 //   * v_mfma_scale_f32_32x32x64_f8f6f4: the e8m0 byte of each operand row
 //     and 128-K block is applied by the MFMA itself;
 //   * the f32 group maxima G are constant over "spans" of K blocks (1024 K for
 //     (1,128) activations, the whole K for a single-group weight).  The
 //     accumulator holds C / (gA gB) of the current span and is rescaled by
 //     (gA_old/gA_new)(gB_old/gB_new) when a span starts, so one accumulator
-//     set suffices; the epilogue multiplies by gA gB / 2^14.
+//     set suffices; the epilogue multiplies by gA gB / 2^14;
+//   * tiles are numbered so that the workgroups resident on one XCD (the
+//     dispatcher deals workgroups round-robin to the 8 XCDs) cover a 4 x 8
+//     block of output tiles and share A and B panels in that XCD's L2.
 //
 // Differences from the reference's f32 dequant-then-matmul: summation order,
 // and blocks whose e8m0 byte is 0 (block max below 2^-126 of its group max):
@@ -40,6 +50,13 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int BM = 256, BN = 256, BK = 128;
 constexpr int TILE_BYTES = BM * BK;            // 32 KB per operand per stage
 constexpr int NTHREADS = 512;
+// LDS stage: A tile | B tile | A e8m0 words | B e8m0 words | A group max | B group max
+constexpr int OFF_B = TILE_BYTES;
+constexpr int OFF_EA = 2 * TILE_BYTES;
+constexpr int OFF_EB = OFF_EA + 4 * BM;
+constexpr int OFF_GA = OFF_EB + 4 * BN;
+constexpr int OFF_GB = OFF_GA + 4 * BM;
+constexpr int STAGE_BYTES = OFF_GB + 4 * BN;   // 69632
 
 struct Scales {
   const uint8_t* e8;   // e8m0 bytes
@@ -62,25 +79,19 @@ __device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Issue the DMA of one operand's 256 x 128-byte K tile into LDS (4 row groups
-// of 8 rows per wave; lane -> row (lane>>3), physical chunk (lane&7)).
-__device__ __forceinline__ void dma_tile(const uint8_t* __restrict__ src, int64_t ld, int row0,
-                                         int64_t k0, uint8_t* lds_tile, int wave, int lane) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int g = wave * 4 + i;
-    const int r = g * 8 + (lane >> 3);
-    const int c = (lane & 7) ^ swz(r);
-    const uint8_t* p = src + (int64_t)(row0 + r) * ld + k0 + c * 16;
-    __builtin_amdgcn_global_load_lds(p, (lds_void*)(lds_tile + g * 1024), 16, 0, 0);
-  }
+__device__ __forceinline__ void dma16(const void* g, uint8_t* lds) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* g, uint8_t* lds) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void*)lds, 4, 0, 0);
 }
 
-// 32-byte MFMA operand of LDS row r, logical chunks c0, c0+1.
-__device__ __forceinline__ v8i read_frag(const uint8_t* lds_tile, int r, int c0) {
-  const int s = swz(r);
-  const v4i lo = *reinterpret_cast<const v4i*>(lds_tile + r * BK + ((c0 ^ s) << 4));
-  const v4i hi = *reinterpret_cast<const v4i*>(lds_tile + r * BK + (((c0 + 1) ^ s) << 4));
+// 32-byte MFMA operand: two 16-byte LDS reads at a per-lane address plus a
+// compile-time offset (row block and operand), folded into ds_read's offset.
+template <int OFF>
+__device__ __forceinline__ v8i read_frag2(const uint8_t* base_lo, const uint8_t* base_hi) {
+  const v4i lo = *reinterpret_cast<const v4i*>(base_lo + OFF);
+  const v4i hi = *reinterpret_cast<const v4i*>(base_hi + OFF);
   return v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 }
 
@@ -93,186 +104,344 @@ __device__ __forceinline__ void mfma_tile(v16f (&acc)[2][4], const v8i (&fa)[2],
                                                                (int)eB, MI, (int)eA);
 }
 
+__device__ __forceinline__ void mfma_all(v16f (&acc)[2][4], const v8i (&fa)[2], const v8i (&fb)[4],
+                                         uint32_t eA, uint32_t eB) {
+  mfma_tile<0, 0>(acc, fa, fb, eA, eB);
+  mfma_tile<0, 1>(acc, fa, fb, eA, eB);
+  mfma_tile<0, 2>(acc, fa, fb, eA, eB);
+  mfma_tile<0, 3>(acc, fa, fb, eA, eB);
+  mfma_tile<1, 0>(acc, fa, fb, eA, eB);
+  mfma_tile<1, 1>(acc, fa, fb, eA, eB);
+  mfma_tile<1, 2>(acc, fa, fb, eA, eB);
+  mfma_tile<1, 3>(acc, fa, fb, eA, eB);
+}
+
+// Issue the DMA of stage data for K block kt: the two 256 x 128-byte K tiles
+// (8 row groups of 8 rows per operand per wave; lane -> row (lane>>3),
+// physical chunk (lane&7)), the e8m0 word of each of the 256 + 256 rows, and
+// at span starts their group maxima.
+struct DmaRows {
+  uint32_t ea_word, eb_word;   // e8m0 block index of this lane's DMA rows at kb = 0
+  uint32_t offa[2], offb[2];   // per-lane byte offset inside an 8-row group (even / odd group)
+};
+
+// Buffer resources of one operand: payload, e8m0 bytes, group maxima.  Raw
+// buffer loads are range-checked against num_records, so an offset outside an
+// array reads zeros instead of faulting.
+struct OperandRsrc {
+  __amdgpu_buffer_rsrc_t pay, e8, g32;
+};
+
+__device__ __forceinline__ OperandRsrc make_rsrc(const uint8_t* pay, uint32_t pay_bytes,
+                                                 const Scales& s, uint32_t e8_bytes,
+                                                 uint32_t g32_bytes) {
+  constexpr int kFlags = 0x00020000;   // gfx9 raw buffer: 32-bit data format
+  OperandRsrc r;
+  r.pay = __builtin_amdgcn_make_buffer_rsrc((void*)pay, 0, (int)pay_bytes, kFlags);
+  r.e8 = __builtin_amdgcn_make_buffer_rsrc((void*)s.e8, 0, (int)e8_bytes, kFlags);
+  r.g32 = __builtin_amdgcn_make_buffer_rsrc((void*)s.g32, 0, (int)g32_bytes, kFlags);
+  return r;
+}
+
+// Tile DMA: row group g (8 rows) of the 256-row tile goes to LDS bytes
+// [g*1024, g*1024+1024): lane -> row g*8 + (lane>>3), physical chunk lane&7,
+// logical chunk (lane&7) ^ swz(row) = (lane&7) ^ (lane>>3) ^ (g&1).  The
+// address is a wave-uniform soffset plus one of two per-lane offsets.
+__device__ __forceinline__ void dma_offsets(int64_t ld, int lane, uint32_t (&off)[2]) {
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int c = (lane & 7) ^ (lane >> 3) ^ par;
+    off[par] = (uint32_t)((lane >> 3) * ld + c * 16);
+  }
+}
+
+__device__ __forceinline__ void issue_stage(const OperandRsrc& ra, int64_t lda, const OperandRsrc& rb,
+                                            int64_t ldb, const Scales& sa, const Scales& sb,
+                                            const DmaRows& d, int m0, int n0, int kt,
+                                            bool span_start, uint8_t* st, int w4, int lane) {
+  const uint32_t k0 = (uint32_t)kt * BK;
+  const uint32_t abase = (uint32_t)(m0 + w4 * 64) * (uint32_t)lda + k0;
+  const uint32_t bbase = (uint32_t)(n0 + w4 * 64) * (uint32_t)ldb + k0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int g = w4 * 8 + i;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra.pay, (lds_void*)(st + g * 1024), 16, d.offa[i & 1],
+                                             abase + (uint32_t)(i * 8) * (uint32_t)lda, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb.pay, (lds_void*)(st + OFF_B + g * 1024), 16, d.offb[i & 1],
+                                             bbase + (uint32_t)(i * 8) * (uint32_t)ldb, 0, 0);
+  }
+  const uint32_t ia = d.ea_word + (uint32_t)kt * (uint32_t)sa.s_k;
+  const uint32_t ib = d.eb_word + (uint32_t)kt * (uint32_t)sb.s_k;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(ra.e8, (lds_void*)(st + OFF_EA + w4 * 256), 4, ia & ~3u, 0, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rb.e8, (lds_void*)(st + OFF_EB + w4 * 256), 4, ib & ~3u, 0, 0, 0);
+  if (span_start) {
+    // group of the row's block at kb = 0 (rare: recomputed instead of held)
+    const uint32_t ga0 = d.ea_word / (uint32_t)sa.kg, gb0 = d.eb_word / (uint32_t)sb.kg;
+    const uint32_t da = ((uint32_t)kt / (uint32_t)sa.bpg) * (uint32_t)sa.gstep;
+    const uint32_t db = ((uint32_t)kt / (uint32_t)sb.bpg) * (uint32_t)sb.gstep;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra.g32, (lds_void*)(st + OFF_GA + w4 * 256), 4,
+                                             (ga0 + da) * 4u, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb.g32, (lds_void*)(st + OFF_GB + w4 * 256), 4,
+                                             (gb0 + db) * 4u, 0, 0, 0);
+  }
+}
+
+// Workgroup barrier without the release/acquire fences of __syncthreads():
+// those make the compiler wait for every outstanding memory operation,
+// including the in-flight stage DMA.  Each use below states the waits it
+// needs explicitly; the memory clobber keeps the compiler from moving memory
+// accesses across the barrier.
+__device__ __forceinline__ void wg_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// s_waitcnt that the scheduler may not move other instructions across.
+#define PINNED_WAITCNT(imm)            \
+  do {                                 \
+    __builtin_amdgcn_sched_barrier(0); \
+    __builtin_amdgcn_s_waitcnt(imm);   \
+    __builtin_amdgcn_sched_barrier(0); \
+  } while (0)
+
+// Empty asm statements that "redefine" values: volatile asm keeps its order
+// relative to the barriers, so values passed through one cannot be computed
+// on the other side of a barrier (the MFMAs have no memory effects and would
+// otherwise be free to drift across phases).
+__device__ __forceinline__ void pin_frags(v8i (&fa)[2], v8i (&fb)[4]) {
+  asm volatile("" : "+v"(fa[0]), "+v"(fa[1]), "+v"(fb[0]), "+v"(fb[1]), "+v"(fb[2]), "+v"(fb[3]));
+}
+__device__ __forceinline__ void pin_acc(v16f (&acc)[2][4]) {
+  asm volatile("" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[0][2]), "+v"(acc[0][3]));
+  asm volatile("" : "+v"(acc[1][0]), "+v"(acc[1][1]), "+v"(acc[1][2]), "+v"(acc[1][3]));
+}
+
+__device__ __forceinline__ uint32_t lds_u32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+__device__ __forceinline__ float lds_f32(const uint8_t* p) { return *reinterpret_cast<const float*>(p); }
+
 // B-side group maxima held per lane: 4 (one per 32-column MFMA tile) or 16
 // (one per 4-column accumulator group, for scale groups narrower than 32 rows).
 template <bool FINE_B>
 struct BGroups {
   static constexpr int NJ = FINE_B ? 4 : 1;
   float g[4][NJ];
-  uint32_t idx0[4][NJ];
 };
+
+// Output tile of workgroup `bid`: XCD-aware numbering (see the file header).
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int* tm, int* tn) {
+  const int T = tiles_m * tiles_n;
+  int L = bid;
+  if (T % 8 == 0) L = (bid % 8) * (T / 8) + bid / 8;
+  const int GM = tiles_m < 4 ? tiles_m : 4;
+  const int band = L / (GM * tiles_n);
+  const int rows_in_band = (tiles_m - band * GM) < GM ? (tiles_m - band * GM) : GM;
+  const int w = L - band * GM * tiles_n;
+  *tm = band * GM + w % rows_in_band;
+  *tn = w / rows_in_band;
+}
 
 template <bool OUT_BF16, bool FINE_B>
 __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
-    Scales sa, Scales sb, void* __restrict__ C, int64_t ldc, int K, int span, int tiles_n) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_a0[TILE_BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_b0[TILE_BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_a1[TILE_BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_b1[TILE_BYTES];
+    Scales sa, Scales sb, void* __restrict__ C, int64_t ldc, int K, int span, int tiles_m,
+    int tiles_n, uint32_t a_bytes, uint32_t b_bytes, uint32_t ea_bytes, uint32_t eb_bytes,
+    uint32_t ga_bytes, uint32_t gb_bytes) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE_BYTES];
   constexpr int NJ = BGroups<FINE_B>::NJ;
+  const OperandRsrc ra = make_rsrc(A, a_bytes, sa, ea_bytes, ga_bytes);
+  const OperandRsrc rb = make_rsrc(B, b_bytes, sb, eb_bytes, gb_bytes);
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int wm = wave & 3, wn = wave >> 2;
-  const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
+  // wave index, made provably wave-uniform (LDS DMA targets go through M0)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // waves w, w+4 share SIMD w
+  const int grp = wave >> 2;              // ping-pong group
+  const int wm = wave & 3, wn = grp;      // 64-row band wm, 128-column half wn
+  int tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int nk = K / BK;
   const int l32 = lane & 31, lhi = lane >> 5;
 
-  // Block-index bases (kb = 0) of the rows this lane feeds to the MFMA: A rows
-  // (b-operand) and B rows (a-operand).
-  uint32_t baseA[2], baseB[4];
+  // Group 0 issues every stage DMA: its wave (wave & 3) covers 64 A rows and
+  // 64 B rows of the scale words.
+  DmaRows d;
+  {
+    const int64_t ra = m0 + (wave & 3) * 64 + lane, rb = n0 + (wave & 3) * 64 + lane;
+    const int64_t ia = blk_index(sa, ra, 0), ib = blk_index(sb, rb, 0);
+    d.ea_word = (uint32_t)ia;
+    d.eb_word = (uint32_t)ib;
+    dma_offsets(lda, lane, d.offa);
+    dma_offsets(ldb, lane, d.offb);
+  }
+  // e8m0 byte position inside the DMA'd word of each compute row at kb = 0,
+  // 2 bits per row: A rows i = 0, 1 in bits 2i, B rows i = 0..3 in bits 4 + 2i
+  uint32_t epos = 0;
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi) baseA[mi] = (uint32_t)blk_index(sa, m0 + wm * 64 + mi * 32 + l32, 0);
+  for (int i = 0; i < 2; ++i) epos |= ((uint32_t)blk_index(sa, m0 + wm * 64 + i * 32 + l32, 0) & 3u) << (2 * i);
 #pragma unroll
-  for (int ni = 0; ni < 4; ++ni) baseB[ni] = (uint32_t)blk_index(sb, n0 + wn * 128 + ni * 32 + l32, 0);
+  for (int i = 0; i < 4; ++i)
+    epos |= ((uint32_t)blk_index(sb, n0 + wn * 128 + i * 32 + l32, 0) & 3u) << (4 + 2 * i);
   const uint32_t skA = (uint32_t)sa.s_k, skB = (uint32_t)sb.s_k;
-
-  // group-max indices at kb = 0: A per lane row, B per output column group
-  uint32_t gidxA[2];
-  BGroups<FINE_B> bg;
+  // physical 16-byte chunk offsets of this lane's operand halves: K half ks,
+  // lo/hi chunk (logical 4*ks + 2*lhi + h, XOR-swizzled by the lane's row)
+  int ch[2][2];
+  {
+    const int sw = swz(l32);
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi) gidxA[mi] = baseA[mi] / (uint32_t)sa.kg;
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-  for (int ni = 0; ni < 4; ++ni)
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-      bg.idx0[ni][j] = (uint32_t)(blk_index(sb, n0 + wn * 128 + ni * 32 + 8 * j + 4 * lhi, 0) / sb.kg);
+      for (int h = 0; h < 2; ++h) ch[ks][h] = ((ks * 4 + lhi * 2 + h) ^ sw) << 4;
+  }
 
   v16f acc[2][4];
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = v16f{0};
-
-  // Group maxima of the current span.  A zero group max keeps the previous
-  // value: an all-zero group has an all-zero payload and adds nothing.
-  float gA[2];
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi) {
-    const float g = sa.g32[gidxA[mi]];
-    gA[mi] = g == 0.0f ? 1.0f : g;
-  }
+  float gA[2] = {1.0f, 1.0f};
+  BGroups<FINE_B> bg;
 #pragma unroll
   for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const float g = sb.g32[bg.idx0[ni][j]];
-      bg.g[ni][j] = g == 0.0f ? 1.0f : g;
-    }
-  float gAn[2], gBn[4][NJ];
+    for (int j = 0; j < NJ; ++j) bg.g[ni][j] = 1.0f;
 
-  // e8m0 bytes of the current K block, packed: byte mi of eA, byte ni of eB
-  uint32_t eA = 0, eB = 0;
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi) eA |= (uint32_t)sa.e8[baseA[mi]] << (8 * mi);
-#pragma unroll
-  for (int ni = 0; ni < 4; ++ni) eB |= (uint32_t)sb.e8[baseB[ni]] << (8 * ni);
-
-  dma_tile(A, lda, m0, 0, lds_a0, wave, lane);
-  dma_tile(B, ldb, n0, 0, lds_b0, wave, lane);
-
-  for (int kt = 0; kt < nk; ++kt) {
-    // the stage of kt has landed for every wave; every wave is done with kt-1
+  if (grp == 0) {
+    issue_stage(ra, lda, rb, ldb, sa, sb, d, m0, n0, 0, true, lds, wave & 3, lane);
     __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    const bool odd = kt & 1;
-    const uint8_t* la = odd ? lds_a1 : lds_a0;
-    const uint8_t* lb = odd ? lds_b1 : lds_b0;
+  }
+  __syncthreads();
+  if (grp == 1) wg_barrier();      // offset group 1 by one phase
 
-    if (kt > 0 && kt % span == 0) {
-      // a new span of group maxima starts: move the accumulator into its units
-      float rA[2], rB[4][NJ];
-#pragma unroll
-      for (int mi = 0; mi < 2; ++mi) {
-        const float g = gAn[mi] == 0.0f ? gA[mi] : gAn[mi];
-        rA[mi] = gA[mi] / g;
-        gA[mi] = g;
-      }
-#pragma unroll
-      for (int ni = 0; ni < 4; ++ni)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const float g = gBn[ni][j] == 0.0f ? bg.g[ni][j] : gBn[ni][j];
-          rB[ni][j] = bg.g[ni][j] / g;
-          bg.g[ni][j] = g;
-        }
-#pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < 4; ++ni)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) acc[mi][ni][v] *= rA[mi] * rB[ni][FINE_B ? (v >> 2) : 0];
-    }
-
-    uint32_t eAn = 0, eBn = 0;
-    if (kt + 1 < nk) {
-      dma_tile(A, lda, m0, (int64_t)(kt + 1) * BK, odd ? lds_a0 : lds_a1, wave, lane);
-      dma_tile(B, ldb, n0, (int64_t)(kt + 1) * BK, odd ? lds_b0 : lds_b1, wave, lane);
-      const uint32_t kn = (uint32_t)(kt + 1);
-#pragma unroll
-      for (int mi = 0; mi < 2; ++mi) eAn |= (uint32_t)sa.e8[baseA[mi] + kn * skA] << (8 * mi);
-#pragma unroll
-      for (int ni = 0; ni < 4; ++ni) eBn |= (uint32_t)sb.e8[baseB[ni] + kn * skB] << (8 * ni);
-      if (kn % (uint32_t)span == 0) {
-        const uint32_t dA = (kn / (uint32_t)sa.bpg) * (uint32_t)sa.gstep;
-        const uint32_t dB = (kn / (uint32_t)sb.bpg) * (uint32_t)sb.gstep;
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi) gAn[mi] = sa.g32[gidxA[mi] + dA];
-#pragma unroll
-        for (int ni = 0; ni < 4; ++ni)
-#pragma unroll
-          for (int j = 0; j < NJ; ++j) gBn[ni][j] = sb.g32[bg.idx0[ni][j] + dB];
-      }
-    }
-
+  uint32_t eA = 0, eB = 0;
+  for (int kt = 0; kt < nk; ++kt) {
+    const uint8_t* st = lds + (kt & 1) * STAGE_BYTES;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const int c0 = ks * 4 + lhi * 2;
+      // ---- memory phase ----
+      if (ks == 0) {
+        if (grp == 0 && kt + 1 < nk)
+          issue_stage(ra, lda, rb, ldb, sa, sb, d, m0, n0, kt + 1, (kt + 1) % span == 0,
+                      lds + ((kt + 1) & 1) * STAGE_BYTES, wave & 3, lane);
+        // e8m0 bytes of this K block for the lane's 2 A rows / 4 B rows
+        eA = 0;
+        eB = 0;
+        const uint8_t* ea = st + OFF_EA + (wm * 64 + l32) * 4;
+        const uint8_t* eb = st + OFF_EB + (wn * 128 + l32) * 4;
+        const uint32_t tA = (uint32_t)kt * skA, tB = (uint32_t)kt * skB;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const uint32_t w = lds_u32(ea + i * 128);
+          const uint32_t pos = (__builtin_amdgcn_ubfe(epos, 2 * i, 2) + tA) & 3u;
+          eA |= __builtin_amdgcn_ubfe(w, pos * 8u, 8) << (8 * i);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t w = lds_u32(eb + i * 128);
+          const uint32_t pos = (__builtin_amdgcn_ubfe(epos, 4 + 2 * i, 2) + tB) & 3u;
+          eB |= __builtin_amdgcn_ubfe(w, pos * 8u, 8) << (8 * i);
+        }
+        if (kt % span == 0) {
+          // a new span of group maxima: move the accumulator into its units.
+          // A zero group max keeps the previous units (an all-zero group has
+          // an all-zero payload and adds nothing).
+          float rA[2], rB[4][NJ];
+#pragma unroll
+          for (int mi = 0; mi < 2; ++mi) {
+            const float g0 = lds_f32(st + OFF_GA + (wm * 64 + mi * 32 + l32) * 4);
+            const float g = g0 == 0.0f ? gA[mi] : g0;
+            rA[mi] = gA[mi] * __builtin_amdgcn_rcpf(g);
+            gA[mi] = g;
+          }
+#pragma unroll
+          for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+              const int col = wn * 128 + ni * 32 + (FINE_B ? 8 * j + 4 * lhi : 0);
+              const float g0 = lds_f32(st + OFF_GB + col * 4);
+              const float g = g0 == 0.0f ? bg.g[ni][j] : g0;
+              rB[ni][j] = bg.g[ni][j] * __builtin_amdgcn_rcpf(g);
+              bg.g[ni][j] = g;
+            }
+          if (kt > 0) {
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+              for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[mi][ni][v] *= rA[mi] * rB[ni][FINE_B ? (v >> 2) : 0];
+          }
+        }
+      }
+      // rows of this lane: A wm*64 + i*32 + l32, B wn*128 + i*32 + l32; the
+      // swizzle of a row depends only on l32, so row blocks i are immediates
+      const uint8_t* alo = st + (wm * 64 + l32) * BK + ch[ks][0];
+      const uint8_t* ahi = st + (wm * 64 + l32) * BK + ch[ks][1];
+      const uint8_t* blo = st + (wn * 128 + l32) * BK + ch[ks][0];
+      const uint8_t* bhi = st + (wn * 128 + l32) * BK + ch[ks][1];
       v8i fa[2], fb[4];
-#pragma unroll
-      for (int mi = 0; mi < 2; ++mi) fa[mi] = read_frag(la, wm * 64 + mi * 32 + l32, c0);
-#pragma unroll
-      for (int ni = 0; ni < 4; ++ni) fb[ni] = read_frag(lb, wn * 128 + ni * 32 + l32, c0);
-      mfma_tile<0, 0>(acc, fa, fb, eA, eB);
-      mfma_tile<0, 1>(acc, fa, fb, eA, eB);
-      mfma_tile<0, 2>(acc, fa, fb, eA, eB);
-      mfma_tile<0, 3>(acc, fa, fb, eA, eB);
-      mfma_tile<1, 0>(acc, fa, fb, eA, eB);
-      mfma_tile<1, 1>(acc, fa, fb, eA, eB);
-      mfma_tile<1, 2>(acc, fa, fb, eA, eB);
-      mfma_tile<1, 3>(acc, fa, fb, eA, eB);
+      fa[0] = read_frag2<0>(alo, ahi);
+      fa[1] = read_frag2<32 * BK>(alo, ahi);
+      fb[0] = read_frag2<OFF_B>(blo, bhi);
+      fb[1] = read_frag2<OFF_B + 32 * BK>(blo, bhi);
+      fb[2] = read_frag2<OFF_B + 64 * BK>(blo, bhi);
+      fb[3] = read_frag2<OFF_B + 96 * BK>(blo, bhi);
+      PINNED_WAITCNT(0xC07F);   // lgkmcnt(0): operands in registers, stage reads done
+      wg_barrier();
+      // ---- compute phase ----
+      pin_frags(fa, fb);
+      mfma_all(acc, fa, fb, eA, eB);
+      pin_acc(acc);
+      if (grp == 0 && ks == 1) PINNED_WAITCNT(0);   // stage kt+1 landed
+      wg_barrier();
     }
-    eA = eAn;
-    eB = eBn;
   }
+  if (grp == 0) wg_barrier();      // match group 1's extra barrier
 
-  // epilogue: C[m][n] = acc * gA * gB / 2^14 (the two /128 of the dequant)
+  // Epilogue: C[m][n] = acc * gA * gB / 2^14 (the two /128 of the dequant).
+  // Each wave stages 32 rows x 128 columns at a time in LDS (the stage
+  // buffers are free now) and writes them back as full 16-byte lane chunks
+  // covering whole rows, instead of 8-byte scattered pieces.
+  constexpr int ESZ = OUT_BF16 ? 2 : 4;
+  constexpr int ROWB = 128 * ESZ;           // bytes of one staged row
+  constexpr int PITCH = ROWB + 16;          // padded LDS row pitch
+  constexpr int CHUNKS = ROWB / 16;         // 16-byte chunks per row
+  uint8_t* stg = lds + wave * (32 * PITCH);
+  __syncthreads();                          // every wave is done with the stage buffers
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi) {
-    const int64_t m = m0 + wm * 64 + mi * 32 + l32;
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int64_t n = n0 + wn * 128 + ni * 32 + 8 * j + 4 * lhi;
+        const int col = ni * 32 + 8 * j + 4 * lhi;
         const float f = gA[mi] * bg.g[ni][FINE_B ? j : 0] * 6.103515625e-05f;
         const float c0 = acc[mi][ni][4 * j + 0] * f, c1 = acc[mi][ni][4 * j + 1] * f;
         const float c2 = acc[mi][ni][4 * j + 2] * f, c3 = acc[mi][ni][4 * j + 3] * f;
+        uint8_t* dst = stg + l32 * PITCH + col * ESZ;
         if constexpr (OUT_BF16) {
           typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
           const bf16x2 p0 = {(__bf16)c0, (__bf16)c1};
           const bf16x2 p1 = {(__bf16)c2, (__bf16)c3};
-          uint2 w;
-          w.x = __builtin_bit_cast(uint32_t, p0);
-          w.y = __builtin_bit_cast(uint32_t, p1);
-          *reinterpret_cast<uint2*>(static_cast<uint16_t*>(C) + m * ldc + n) = w;
+          *reinterpret_cast<uint2*>(dst) =
+              make_uint2(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1));
         } else {
-          *reinterpret_cast<float4*>(static_cast<float*>(C) + m * ldc + n) = make_float4(c0, c1, c2, c3);
+          *reinterpret_cast<float4*>(dst) = make_float4(c0, c1, c2, c3);
         }
       }
     }
+    __builtin_amdgcn_s_waitcnt(0xC07F);     // lgkmcnt(0): this wave's staging writes are done
+    // rows wm*64 + mi*32 + [0, 32), columns wn*128 + [0, 128) of the tile
+    uint8_t* Cb = static_cast<uint8_t*>(C) +
+                  ((int64_t)(m0 + wm * 64 + mi * 32) * ldc + (n0 + wn * 128)) * ESZ;
+#pragma unroll
+    for (int it = 0; it < (32 * CHUNKS) / 64; ++it) {
+      const int q = it * 64 + lane;
+      const int r = q / CHUNKS, c = q % CHUNKS;
+      const uint4 v = *reinterpret_cast<const uint4*>(stg + r * PITCH + c * 16);
+      *reinterpret_cast<uint4*>(Cb + (int64_t)r * ldc * ESZ + c * 16) = v;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);     // staging reads done before the next half overwrites
   }
 }
 
@@ -359,6 +528,14 @@ extern "C" int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t*
   if ((M / a_rdiv) * a_sr + nk * a_sk > (int64_t)UINT32_MAX ||
       (N / b_rdiv) * b_sr + nk * b_sk > (int64_t)UINT32_MAX)
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: scale arrays beyond 2^32 blocks");
+  // The stage DMA reads each row's e8m0 byte as the aligned 4-byte word that
+  // holds it, so the byte count of each e8m0 array (last block + 1) must be a
+  // multiple of 4 (true for every quantizer layout with >= 4 blocks per slice
+  // row multiple of 4; anything else is reported).
+  const int64_t last_a = ((M - 1) / a_rdiv) * a_sr + (nk - 1) * a_sk;
+  const int64_t last_b = ((N - 1) / b_rdiv) * b_sr + (nk - 1) * b_sk;
+  if ((last_a + 1) % 4 || (last_b + 1) % 4)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: e8m0 arrays must hold a multiple of 4 blocks");
   // B's group max per lane: one per 32 output columns, or one per 4 columns.
   const bool fine_b = b_rdiv % 32 != 0;
   if (fine_b && !(b_rdiv % 4 == 0 || (b_rdiv == 1 && b_kg % (4 * b_sr) == 0 && b_sk % (4 * b_sr) == 0)))
@@ -370,11 +547,19 @@ extern "C" int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t*
     y = t;
   }
   const int64_t span = x < 1 ? 1 : x;
+  // buffer resources address bytes with 32-bit offsets
+  const int64_t a_bytes = (M - 1) * lda + K, b_bytes = (N - 1) * ldb + K;
+  const int64_t ga_bytes = (last_a / a_kg + 1) * 4, gb_bytes = (last_b / b_kg + 1) * 4;
+  if (a_bytes > (int64_t)INT32_MAX || b_bytes > (int64_t)INT32_MAX || last_a + 1 > INT32_MAX ||
+      last_b + 1 > INT32_MAX)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: operands beyond 2 GiB");
   const int64_t tiles_n = N / BN;
   const int64_t tiles = (M / BM) * tiles_n;
 #define PRATCHYA_GEMM(BF, FB)                                                                   \
   hipLaunchKernelGGL((k_gemm_bs_nt<BF, FB>), dim3((unsigned)tiles), dim3(NTHREADS), 0, stream, A, lda, \
-                     B, ldb, sa, sb, C, ldc, (int)K, (int)span, (int)tiles_n)
+                     B, ldb, sa, sb, C, ldc, (int)K, (int)span, (int)(M / BM), (int)tiles_n,   \
+                     (uint32_t)a_bytes, (uint32_t)b_bytes, (uint32_t)(last_a + 1),              \
+                     (uint32_t)(last_b + 1), (uint32_t)ga_bytes, (uint32_t)gb_bytes)
   const bool bf = c_dtype == PRATCHYA_DT_BF16;
   if (bf && !fine_b) PRATCHYA_GEMM(true, false);
   else if (bf) PRATCHYA_GEMM(true, true);

@@ -55,32 +55,44 @@ def cpu_baseline_quantize(rows: int = 2048, min_seconds: float = 10.0):
                       f"config 2, tgrid (1,128), {reps} reps, {el:.1f} s (NumPy, single thread)"}
 
 
-def timed_graph(step, steps: int, warmup: int, per_graph: int):
-    """Capture ``per_graph`` consecutive steps in one HIP graph, replay it
-    (removes host launch gaps), and time the replays with events recorded on
-    the stream the kernels run on.  Returns (ms per step, wall seconds)."""
+MAX_GRAPH_STEPS = 256
+
+
+def timed_graph(step, steps: int, warmup: int):
+    """Time exactly ``steps`` calls of ``step(i)``: the steps are captured in
+    HIP graphs of up to MAX_GRAPH_STEPS launches (no host launch gaps and
+    only one graph launch per MAX_GRAPH_STEPS steps), replayed between events
+    recorded on the stream the kernels run on.  ``warmup`` eager steps and
+    one untimed replay come first.  Returns (ms per step, wall seconds)."""
     import torch
     for i in range(max(warmup, 1)):
         step(i)
     torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for i in range(per_graph):
-            step(i)
-    reps = max(1, -(-steps // per_graph))
-    for _ in range(max(1, warmup // per_graph)):
+    n_main = min(steps, MAX_GRAPH_STEPS)
+    reps, rem = divmod(steps, n_main)
+    graphs = []
+    for count, times in ((n_main, reps), (rem, 1 if rem else 0)):
+        if times == 0:
+            continue
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(count):
+                step(i)
+        graphs.append((g, times))
+    for g, _ in graphs:
         g.replay()
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record(st)
-    for _ in range(reps):
-        g.replay()
+    for g, times in graphs:
+        for _ in range(times):
+            g.replay()
     e1.record(st)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    return e0.elapsed_time(e1) / (reps * per_graph), wall
+    return e0.elapsed_time(e1) / steps, wall
 
 
 def bench_quantize(steps: int, warmup: int):
@@ -110,7 +122,7 @@ def bench_quantize(steps: int, warmup: int):
         if rc:
             raise RuntimeError(lib.pratchya_last_error().decode())
 
-    ms, wall = timed_graph(step, steps, warmup, per_graph=n_sets)
+    ms, wall = timed_graph(step, steps, warmup)
     # parity spot check of the last output against the oracle on a slice
     q8, s8, s32 = outs[(steps - 1) % n_sets]
     xb = O.activation_input(CFG2_ROWS, CFG2_COLS, seed=2)[:64]
@@ -138,8 +150,59 @@ def bench_gemm_fwd(steps: int, warmup: int):
     def step(i):
         K.gemm_nt(a, b, out=outs[i % 2])
 
-    ms, _ = timed_graph(step, steps, warmup, per_graph=4)
+    ms, _ = timed_graph(step, steps, warmup)
     return ms, 2.0 * M * N * Kd / (ms * 1e-3) / 1e12
+
+
+COPY_BYTES = 256 << 20   # bytes read (and written) by the reference copy of the counter runs
+
+
+def counter_workload(reps: int = 10) -> None:
+    """Direct launches (no graph) for rocprofv3 counter runs: ``reps`` x the
+    config-2 quantize, ``reps`` x the config-3 GEMM, and ``reps`` x a plain
+    device-to-device copy of COPY_BYTES (``dst.copy_(src)``, which the HIP
+    runtime runs as its copyBuffer kernel), whose FETCH_SIZE / WRITE_SIZE
+    readings calibrate the counters against known byte counts."""
+    import torch
+    from oracle import qarr_oracle as O
+    from pratchya_amd import _kernels as K
+    x = torch.from_numpy(O.activation_input(CFG2_ROWS, CFG2_COLS, seed=2).view(np.int16)).view(
+        torch.bfloat16).cuda()
+    w = torch.from_numpy(O.normal_input((CFG2_COLS, 8192), 0.02, seed=3).view(np.int16)).view(
+        torch.bfloat16).cuda()
+    b = K.operand_transposed(*K.quantize(w, (128, 128)), (128, 128))
+    src = torch.ones(COPY_BYTES // 2, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        q = K.quantize(x, (1, 128))
+    torch.cuda.synchronize()
+    _log(f"counter workload: {reps} x quantize done")
+    a = K.operand_rows(*q, (1, 128))
+    out = torch.empty((CFG2_ROWS, 8192), dtype=torch.bfloat16, device="cuda")
+    for _ in range(reps):
+        K.gemm_nt(a, b, out=out)
+    torch.cuda.synchronize()
+    _log(f"counter workload: {reps} x gemm done")
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    _log(f"counter workload: {reps} x copy of {COPY_BYTES} B done")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the config-2 quantize kernel, from the committed
+    counter summary (FETCH_SIZE + WRITE_SIZE, calibrated by the copy kernel);
+    None if the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "k_quant_g8_cfg2_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        return None
+    return None
 
 
 def main():
@@ -149,6 +212,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--counter-workload", action="store_true",
+                    help="only run the direct-launch workload used for rocprofv3 --pmc runs")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -160,6 +225,9 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     _log(f"device {torch.cuda.get_device_name(0)}")
+    if args.counter_workload:
+        counter_workload()
+        return
     _log("config 2 quantize: start")
     ms, wall, ok = bench_quantize(args.steps, args.warmup)
     _log(f"config 2 quantize: {ms * 1e3:.2f} us/step, parity spot check {'ok' if ok else 'FAILED'}")
@@ -195,7 +263,7 @@ def main():
                                "Student-t(3) with 1% x50 outlier channels, seed 2",
                    "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,
         "parity_spot_check": ok,
         "extra": extra,

@@ -44,9 +44,10 @@ typedef struct ihipStream_t* hipStream_t;
 #define PRATCHYA_EHIP 2
 #define PRATCHYA_EUNSUPPORTED 3
 
-/* element types of unquantized buffers */
+/* element types of input buffers */
 #define PRATCHYA_DT_F32 0
 #define PRATCHYA_DT_BF16 1
+#define PRATCHYA_DT_E4M3 2   /* e4m3fn payload + its (1, 128) scales (pratchya_quantize_t128 only) */
 
 /* ABI version of this header (bumped on any signature change). */
 int pratchya_abi_version(void);
@@ -84,6 +85,22 @@ int pratchya_dequantize(const uint8_t* x_fp8, const uint8_t* sc_fp8, const float
 int pratchya_dequantize_bwd(const void* g, int g_dtype, const uint8_t* sc_fp8,
                             const float* sc_fp32, int64_t slices, int64_t H, int64_t W,
                             int64_t a, int64_t b, void* out, hipStream_t stream);
+
+/* Transposed requantize, tgrid (128, 1):     replaces quantize_impl(x, (128, 1)), Q:458-506,
+ * with the payload written transposed (the layout fp8_matmul's backward
+ * contracts, Q:784-789, and the wgrad GEMM reads).
+ * x: [slices, T, C] row-major, x_dtype PRATCHYA_DT_BF16 / PRATCHYA_DT_F32, or
+ * PRATCHYA_DT_E4M3: an e4m3fn payload quantized with tgrid (1, 128) whose
+ * scales are x_sc8 / x_sc32; it is dequantized to f32 exactly as
+ * dequantize_impl (Q:562-564) before requantization.
+ * Outputs: xt_fp8 uint8 [slices, C, T] (payload of quantize_impl transposed per
+ * slice), sc_fp8 [slices*M*8] and sc_fp32 [slices*M] exactly as
+ * quantize_impl(x, (128, 1)) (M = T*C/1024; a group is 8 adjacent channels of
+ * one 128-token block row).  T must be a multiple of 128 (PRATCHYA_EINVAL), C of
+ * 8 (PRATCHYA_EUNSUPPORTED) and, for an fp8 input, of 128 (PRATCHYA_EINVAL). */
+int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t* x_sc8, const float* x_sc32,
+                           int64_t slices, int64_t T, int64_t C, uint8_t* xt_fp8, uint8_t* sc_fp8,
+                           float* sc_fp32, hipStream_t stream);
 
 /* Block-scaled FP8 GEMM, "NT" form:                         replaces the f32 dot
  *   C[m, n] = sum_k dequant(A)[m, k] * dequant(B)[n, k]      of matmul_impl

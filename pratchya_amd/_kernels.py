@@ -98,6 +98,50 @@ def _u8(t: torch.Tensor) -> torch.Tensor:
     return t.view(torch.uint8) if t.dtype != torch.uint8 else t
 
 
+def quantize_t128(x: torch.Tensor, x_sc8: torch.Tensor = None, x_sc32: torch.Tensor = None):
+    """``quantize_impl(x, (128, 1))`` (pratchya/_qualia/_qarr.py:458-506) with
+    the payload transposed per slice.
+
+    ``x``: [..., T, C] bf16 or f32, or an e4m3fn payload quantized with tgrid
+    (1, 128) whose scales are ``x_sc8`` / ``x_sc32`` (dequantized to f32 first,
+    as ``dequantize_impl`` does).  Returns ``(xt_fp8 [..., C, T] e4m3fn,
+    sc_fp8 [..., M, 8] e8m0, sc_fp32 [..., M, 1, 1] f32)``: the scales are
+    exactly ``quantize_impl(x, (128, 1))``'s, the payload is its payload with
+    the last two axes swapped.
+    """
+    _require_gpu(x)
+    if x.dim() < 2:
+        raise ValueError("quantize_t128 needs a [..., T, C] tensor")
+    lead = tuple(x.shape[:-2])
+    T, C = int(x.shape[-2]), int(x.shape[-1])
+    S = 1
+    for d in lead:
+        S *= int(d)
+    if x.dtype in (E4M3, torch.uint8):
+        if x_sc8 is None or x_sc32 is None:
+            raise ValueError("an fp8 input needs its (1, 128) scales")
+        code = _lib.DT_E4M3
+        xs8, xs32 = _u8(x_sc8).contiguous(), x_sc32.contiguous().float()
+        xin = _u8(x)
+    else:
+        code = _dtype_code(x.dtype if x.dtype in (torch.float32, torch.bfloat16) else torch.float32)
+        xin = x if x.dtype in (torch.float32, torch.bfloat16) else x.float()
+        xs8 = xs32 = None
+    if not xin.is_contiguous() or not _aligned(xin, 16):
+        xin = xin.contiguous() if not xin.is_contiguous() else xin.clone()
+    _, K, M = group_layout(T, C, (128, 1))
+    xt = torch.empty(lead + (C, T), dtype=torch.uint8, device=x.device)
+    sc8 = torch.empty(lead + (M, K), dtype=torch.uint8, device=x.device)
+    sc32 = torch.empty(lead + (M, 1, 1), dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    _lib.check(lib.pratchya_quantize_t128(_ptr(xin), code,
+                                          _ptr(xs8) if xs8 is not None else None,
+                                          _ptr(xs32) if xs32 is not None else None,
+                                          S, T, C, _ptr(xt), _ptr(sc8), _ptr(sc32), _stream(xin)),
+               "quantize_t128")
+    return xt.view(E4M3), sc8.view(E8M0), sc32
+
+
 def dequantize(x_fp8: torch.Tensor, sc_fp8: torch.Tensor, sc_fp32: torch.Tensor,
                dtype: torch.dtype, tgrid) -> torch.Tensor:
     """``(f32(x8) * (f32(e<<23) * G)) / 128`` cast to ``dtype``
@@ -208,6 +252,15 @@ def operand_transposed(x8: torch.Tensor, sc8: torch.Tensor, sc32: torch.Tensor, 
     _, kg, _ = group_layout(K, R, (a, b))
     pt = transpose_u8(x8) if payload_t is None else payload_t
     return Operand(pt, sc8, sc32, (b, 1, R // b, kg))
+
+
+def operand_t128(xt8: torch.Tensor, sc8: torch.Tensor, sc32: torch.Tensor) -> Operand:
+    """Operand from ``quantize_t128`` of a 2-D [T, C] tensor: rows are the C
+    channels, the contraction runs over the T tokens (wgrad)."""
+    if xt8.dim() != 2:
+        raise ValueError("operand_t128 needs the payload of a 2-D tensor")
+    C, T = xt8.shape
+    return Operand(xt8, sc8, sc32, (1, 1, C, 8))
 
 
 def transpose_u8(x8: torch.Tensor) -> torch.Tensor:

@@ -14,7 +14,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libpratchya_fp8.so"
 ABI_VERSION = 1
 
 OK, EINVAL, EHIP, EUNSUPPORTED = 0, 1, 2, 3
-DT_F32, DT_BF16 = 0, 1
+DT_F32, DT_BF16, DT_E4M3 = 0, 1, 2
 
 _c_i64 = ctypes.c_int64
 _c_p = ctypes.c_void_p
@@ -34,6 +34,8 @@ SIGNATURES = {
                                      _c_p, _c_int, _c_p]),
     "pratchya_dequantize_bwd": (_c_int, [_c_p, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
                                          _c_i64, _c_p, _c_p]),
+    "pratchya_quantize_t128": (_c_int, [_c_p, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64,
+                                        _c_p, _c_p, _c_p, _c_p]),
     "pratchya_gemm_bs_nt": (_c_int, [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
                                      _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
                                      _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_int, _c_p]),

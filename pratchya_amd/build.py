@@ -17,7 +17,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 INCLUDE = ROOT / "include"
 LIB = PKG / "libpratchya_fp8.so"
-SOURCES = ["quantize.hip", "gemm.hip"]
+SOURCES = ["quantize.hip", "quantize_t.hip", "gemm.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -48,8 +48,6 @@ def build(verbose: bool = False) -> Path:
     build_dir.mkdir(exist_ok=True)
     for src in SOURCES:
         path = CSRC / src
-        if not path.exists():
-            continue
         obj = build_dir / (path.stem + ".o")
         out = _run([HIPCC, *DEVICE_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(path), "-o", str(obj)])
         if verbose and out.strip():

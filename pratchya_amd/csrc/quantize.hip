@@ -29,6 +29,7 @@
 
 #include "fp8_math.h"
 #include "pratchya_fp8.h"
+#include "quant_device.h"
 
 using namespace pfp8;
 
@@ -63,82 +64,6 @@ static int check_launch(const char* what) {
 
 extern "C" int pratchya_abi_version(void) { return 1; }
 extern "C" const char* pratchya_last_error(void) { return g_err; }
-
-// --------------------------------------------------------------------------
-// Element conversion helpers (4 values -> 4 packed e4m3fn bytes)
-// --------------------------------------------------------------------------
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef short short2_t __attribute__((ext_vector_type(2)));
-
-// t[i] finite.  Software path: bf16 RNE by integer rounding, then e4m3fn.
-__device__ __forceinline__ uint32_t cvt4_sw(float t0, float t1, float t2, float t3) {
-  uint32_t c0 = bf16_to_e4m3fn(f32_to_bf16_rne_nonan(t0));
-  uint32_t c1 = bf16_to_e4m3fn(f32_to_bf16_rne_nonan(t1));
-  uint32_t c2 = bf16_to_e4m3fn(f32_to_bf16_rne_nonan(t2));
-  uint32_t c3 = bf16_to_e4m3fn(f32_to_bf16_rne_nonan(t3));
-  return c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
-}
-
-// t[i] finite.  gfx950 path: v_cvt_pk_bf16_f32 (RNE) then
-// v_cvt_scalef32_pk_fp8_bf16 with scale 1.0.
-__device__ __forceinline__ uint32_t cvt4_hw(float t0, float t1, float t2, float t3) {
-  bf16x2_t lo = {(__bf16)t0, (__bf16)t1};
-  bf16x2_t hi = {(__bf16)t2, (__bf16)t3};
-  short2_t r = {0, 0};
-  r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(r, lo, 1.0f, false);
-  r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(r, hi, 1.0f, true);
-  return __builtin_bit_cast(uint32_t, r);
-}
-
-template <bool HW>
-__device__ __forceinline__ uint32_t cvt4(float t0, float t1, float t2, float t3) {
-  if constexpr (HW) return cvt4_hw(t0, t1, t2, t3);
-  else return cvt4_sw(t0, t1, t2, t3);
-}
-
-// Exact composition for 4 elements (any inputs, NaN/inf/overflow included).
-__device__ __forceinline__ uint32_t cvt4_exact(float x0, float x1, float x2, float x3, float S) {
-  return quant_elem_exact(x0, S) | (quant_elem_exact(x1, S) << 8) |
-         (quant_elem_exact(x2, S) << 16) | (quant_elem_exact(x3, S) << 24);
-}
-
-// Distance of the low 16 bits of t from the bf16 rounding midpoint is <= 4.
-__device__ __forceinline__ bool near_bf16_midpoint(float t) {
-  return ((f2u(t) + 4u - 0x8000u) & 0xFFFFu) <= 8u;
-}
-
-__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
-
-__device__ __forceinline__ uint32_t shfl_xor_u32(uint32_t v, int m) {
-  return (uint32_t)__shfl_xor((int)v, m, 64);
-}
-
-// Widen the i-th element of a 16-byte vector to f32.
-template <bool IS_BF16>
-__device__ __forceinline__ float elem_f32(const uint4& v, int i) {
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-  if constexpr (IS_BF16) {
-    uint32_t word = w[i >> 1];
-    return u2f((i & 1) ? (word & 0xFFFF0000u) : (word << 16));
-  } else {
-    return u2f(w[i]);
-  }
-}
-
-// max |x| bits (as f32 bits) over the 16 bytes of v.
-template <bool IS_BF16>
-__device__ __forceinline__ uint32_t vec_absmax_bits(const uint4& v) {
-  if constexpr (IS_BF16) {
-    uint32_t m01 = umax(v.x & 0x7FFFu, (v.x >> 16) & 0x7FFFu);
-    uint32_t m23 = umax(v.y & 0x7FFFu, (v.y >> 16) & 0x7FFFu);
-    uint32_t m45 = umax(v.z & 0x7FFFu, (v.z >> 16) & 0x7FFFu);
-    uint32_t m67 = umax(v.w & 0x7FFFu, (v.w >> 16) & 0x7FFFu);
-    return umax(umax(m01, m23), umax(m45, m67)) << 16;
-  } else {
-    return umax(umax(v.x & 0x7FFFFFFFu, v.y & 0x7FFFFFFFu),
-                umax(v.z & 0x7FFFFFFFu, v.w & 0x7FFFFFFFu));
-  }
-}
 
 // --------------------------------------------------------------------------
 // Row-group quantize: tgrid (1, b), one wave per tile of R x 64 x VEC elements.
@@ -285,70 +210,6 @@ __global__ __launch_bounds__(256) void k_quant_rowgroup(
 //    group with exact IEEE division;
 //  * a group whose G is not finite takes the exact per-element path.
 // --------------------------------------------------------------------------
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v) {
-  // bound_ctrl: lanes without a source read 0, the identity of unsigned max,
-  // which lets the compiler fuse the move into v_max_u32_dpp.
-  return umax(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true));
-}
-
-// Max over aligned groups of BL lanes; every lane of the group gets the result.
-template <int BL>
-__device__ __forceinline__ uint32_t lane_group_max(uint32_t v) {
-  if constexpr (BL >= 2) v = dpp_max_u32<0xB1>(v);   // quad_perm [1,0,3,2]
-  if constexpr (BL >= 4) v = dpp_max_u32<0x4E>(v);   // quad_perm [2,3,0,1]
-  if constexpr (BL >= 8) v = dpp_max_u32<0x141>(v);  // row_half_mirror
-  if constexpr (BL >= 16) v = dpp_max_u32<0x140>(v); // row_mirror
-  if constexpr (BL >= 32) v = umax(v, shfl_xor_u32(v, 16));
-  if constexpr (BL >= 64) v = umax(v, shfl_xor_u32(v, 32));
-  return v;
-}
-
-__device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int lane) {
-  return (uint32_t)__builtin_amdgcn_readlane((int)v, lane);
-}
-
-// 16-byte streaming load: the input is read exactly once, so it is loaded
-// non-temporally (measured ~12% more HBM throughput than a plain load here).
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 load_stream16(const char* p) {
-  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-
-#ifndef PRATCHYA_NT_STORE
-#define PRATCHYA_NT_STORE 1
-#endif
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ void store_stream8(uint8_t* p, u32x2_t w) {
-  if (PRATCHYA_NT_STORE) __builtin_nontemporal_store(w, reinterpret_cast<u32x2_t*>(p));
-  else *reinterpret_cast<u32x2_t*>(p) = w;
-}
-__device__ __forceinline__ void store_stream4(uint8_t* p, uint32_t w) {
-  if (PRATCHYA_NT_STORE) __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(p));
-  else *reinterpret_cast<uint32_t*>(p) = w;
-}
-
-// max |x| (as f32 bits) of 8 packed bf16 values, on packed 16-bit lanes.
-typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t absmax8_bf16(const uint4& v) {
-  const u16x2_t a = __builtin_bit_cast(u16x2_t, v.x & 0x7FFF7FFFu);
-  const u16x2_t b = __builtin_bit_cast(u16x2_t, v.y & 0x7FFF7FFFu);
-  const u16x2_t c = __builtin_bit_cast(u16x2_t, v.z & 0x7FFF7FFFu);
-  const u16x2_t d = __builtin_bit_cast(u16x2_t, v.w & 0x7FFF7FFFu);
-  const u16x2_t m = __builtin_elementwise_max(__builtin_elementwise_max(a, b),
-                                              __builtin_elementwise_max(c, d));
-  return (uint32_t)(m.x > m.y ? m.x : m.y) << 16;
-}
-
-// f32(128 / 1e-7f) rounded to nearest: the y of a clamped block.
-#define PRATCHYA_Y_CLAMP 1.28e9f
-
-// Near a bf16 rounding midpoint (low 16 bits within 8 of 0x8000).
-__device__ __forceinline__ uint32_t near_mid8(float t) {
-  return (((f2u(t) + 8u - 0x8000u) & 0xFFFFu) <= 16u) ? 1u : 0u;
-}
-
 template <bool IS_BF16, bool HW>
 __global__ __launch_bounds__(256) void k_quant_g8(const void* __restrict__ xv,
                                                   uint8_t* __restrict__ q,

@@ -1,0 +1,288 @@
+// Transposed requantize for tgrid (128, 1): the wgrad operands.
+//
+// quantize_impl(x, (128, 1)) (pratchya/_qualia/_qarr.py:458-506) on x [T, C]
+// (tokens x channels): blocks are 128 tokens of one channel, and with C a
+// multiple of 8 a group (K = gcd(8, n_blk) = 8 blocks) is 8 adjacent channels
+// of one 128-token block row.  The e8m0 bytes and group maxima are exactly
+// quantize_impl's; the payload is written transposed, [C, T] per slice (each
+// channel's tokens contiguous), which is the K-contiguous operand layout of
+// the GEMM that contracts over tokens (dW = x^T . dY).
+//
+// The input is bf16 or f32, or an e4m3fn payload quantized with tgrid (1, 128)
+// together with its scales; the latter is dequantized in registers exactly as
+// dequantize_impl does ((f32(q) * (2^(e-127) * G)) / 128, _qarr.py:562-564),
+// which is the requantization of a stored activation along the token axis
+// (fp8_matmul's backward, _qarr.py:784-789, quantizes x^T the same way).
+//
+// One wave per 128-token x 64-channel tile.  Lane (rs, cg) = (lane >> 3,
+// lane & 7) holds tokens [16 rs, 16 rs + 16) of the 8 channels of group cg:
+// channel maxima are an in-lane max over 16 tokens plus three xor shuffles
+// across rs, the group max an in-lane max over 8 channels, and each channel's
+// 16 payload bytes are one 16-byte store into the transposed layout.  The cast
+// uses the same division-free scheme as the row-group quantizer (exact for
+// bf16 inputs; f32 inputs and clamped blocks check the bf16 rounding midpoint
+// and redo the tile with IEEE division when any element is close).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fp8_math.h"
+#include "pratchya_fp8.h"
+#include "quant_device.h"
+
+int pratchya_set_error(int code, const char* fmt, ...);
+
+namespace {
+
+constexpr int TOK = 16;                     // consecutive tokens per lane
+enum { IN_F32 = 0, IN_BF16 = 1, IN_FP8 = 2 };
+
+template <int IN>
+struct InTraits {
+  static constexpr int ESZ = IN == IN_F32 ? 4 : (IN == IN_BF16 ? 2 : 1);
+  static constexpr int NW = 2 * ESZ;        // 32-bit words holding 8 channels
+};
+
+// 8 channels of one token row at p.
+template <int IN>
+__device__ __forceinline__ void load_row(const uint8_t* p, uint32_t (&w)[InTraits<IN>::NW]) {
+  if constexpr (IN == IN_F32) {
+    const uint4 a = load_stream16(reinterpret_cast<const char*>(p));
+    const uint4 b = load_stream16(reinterpret_cast<const char*>(p) + 16);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+  } else if constexpr (IN == IN_BF16) {
+    const uint4 a = load_stream16(reinterpret_cast<const char*>(p));
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  } else {
+    const u32x2_t a = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+    w[0] = a.x; w[1] = a.y;
+  }
+}
+
+// |channel j| of a row as f32 bits, from the raw bits (a different
+// expression from row_elem's, so the compiler does not keep 128 widened
+// values alive from the maxima to the cast).
+template <int IN>
+__device__ __forceinline__ uint32_t row_abs_bits(const uint32_t (&w)[InTraits<IN>::NW], int j, float dq) {
+  if constexpr (IN == IN_F32) {
+    return w[j] & 0x7FFFFFFFu;
+  } else if constexpr (IN == IN_BF16) {
+    const uint32_t word = w[j >> 1];
+    return ((j & 1) ? (word >> 16) : word) << 16 & 0x7FFF0000u;
+  } else {
+    const float q = e4m3fn_to_f32((w[j >> 2] >> (8 * (j & 3))) & 0x7Fu);
+    return f2u((q * dq) * 0.0078125f) & 0x7FFFFFFFu;
+  }
+}
+
+// Channel j of a row as f32 (fp8: dequantized with the row's scale dq).
+template <int IN>
+__device__ __forceinline__ float row_elem(const uint32_t (&w)[InTraits<IN>::NW], int j, float dq) {
+  if constexpr (IN == IN_F32) {
+    return u2f(w[j]);
+  } else if constexpr (IN == IN_BF16) {
+    const uint32_t word = w[j >> 1];
+    return u2f((j & 1) ? (word & 0xFFFF0000u) : (word << 16));
+  } else {
+    const float q = e4m3fn_to_f32((w[j >> 2] >> (8 * (j & 3))) & 0xFFu);
+    return (q * dq) * 0.0078125f;
+  }
+}
+
+// Element (t, c) of slice s read back from memory (the rare exact path,
+// which must not keep the tile's registers alive).
+template <int IN>
+__device__ __forceinline__ float elem_at(const uint8_t* x, const uint8_t* x_sc8, const float* x_sc32,
+                                         int64_t x_kg, int64_t T, int64_t C, int64_t s, int64_t t,
+                                         int64_t c) {
+  const int64_t i = (s * T + t) * C + c;
+  if constexpr (IN == IN_F32) {
+    return reinterpret_cast<const float*>(x)[i];
+  } else if constexpr (IN == IN_BF16) {
+    return u2f((uint32_t)reinterpret_cast<const uint16_t*>(x)[i] << 16);
+  } else {
+    const int64_t nbr = C / 128, nb_in = T * nbr, blk = t * nbr + c / 128;
+    const float dq = e8m0_decode(x_sc8[s * nb_in + blk]) * x_sc32[s * (nb_in / x_kg) + blk / x_kg];
+    return (e4m3fn_to_f32(x[i]) * dq) * 0.0078125f;
+  }
+}
+
+template <int IN, bool HW>
+__global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ x,
+                                                    const uint8_t* __restrict__ x_sc8,
+                                                    const float* __restrict__ x_sc32, int64_t x_kg,
+                                                    int64_t T, int64_t C, uint8_t* __restrict__ qt,
+                                                    uint8_t* __restrict__ sc8,
+                                                    float* __restrict__ sc32) {
+  constexpr int ESZ = InTraits<IN>::ESZ;
+  constexpr int NW = InTraits<IN>::NW;
+  const int lane = threadIdx.x & 63;
+  const int cg = lane & 7, rs = lane >> 3;
+  const int64_t c0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 64 + cg * 8;
+  // C is a multiple of 8, so a lane owns a whole group or nothing; the xor
+  // partners of a lane (same cg) share its fate.
+  if (c0 >= C) return;
+  const int64_t s = blockIdx.z, tb = blockIdx.y;
+  const int64_t t0 = tb * 128 + rs * TOK;
+
+  uint32_t w[TOK][NW];
+  const uint8_t* xr = x + ((s * T + t0) * C + c0) * ESZ;
+#pragma unroll
+  for (int r = 0; r < TOK; ++r) load_row<IN>(xr + (int64_t)r * C * ESZ, w[r]);
+
+  float dq[TOK];
+#pragma unroll
+  for (int r = 0; r < TOK; ++r) dq[r] = 1.0f;
+  if constexpr (IN == IN_FP8) {
+    // (1, 128) scales of the stored payload: block (t, c / 128) of the slice
+    const int64_t nbr = C / 128, nb_in = T * nbr;
+#pragma unroll
+    for (int r = 0; r < TOK; ++r) {
+      const int64_t blk = (t0 + r) * nbr + c0 / 128;
+      dq[r] = e8m0_decode(x_sc8[s * nb_in + blk]) * x_sc32[s * (nb_in / x_kg) + blk / x_kg];
+    }
+  }
+
+  // channel maxima (as |x| bits: unsigned order, NaN above inf) and group max
+  uint32_t mx[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int r = 0; r < TOK; ++r) m = umax(m, row_abs_bits<IN>(w[r], j, dq[r]));
+    m = umax(m, shfl_xor_u32(m, 8));
+    m = umax(m, shfl_xor_u32(m, 16));
+    m = umax(m, shfl_xor_u32(m, 32));
+    mx[j] = m;
+  }
+  uint32_t Gb = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) Gb = umax(Gb, mx[j]);
+  const float G = u2f(Gb);
+  const bool G_finite = (Gb >> 23) < 255u;
+
+  // e8m0 bytes, y ~ 128 / S per channel, and the division-free cast of the
+  // tile into registers.  If any group of the wave has a non-finite G, or
+  // (f32 / fp8 inputs, clamped blocks) any element lands within 8 ulp of a bf16
+  // rounding midpoint after the multiply, the wave redoes the cast with IEEE
+  // division instead (rare; it re-reads its elements from memory).
+  uint32_t e[8];
+  uint32_t out[8][TOK / 4];
+  uint32_t redo = G_finite ? 0u : 1u;
+  {
+    const float rcpG128 = __builtin_amdgcn_rcpf(G * 0.0078125f);
+    uint32_t clamped = 0;
+    float y[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      e[j] = e8m0_of(u2f(mx[j]), G);
+      const float sG = e8m0_decode(e[j]) * G;
+      const bool cl = !(sG >= kClamp);
+      y[j] = cl ? PRATCHYA_Y_CLAMP : u2f((254u - e[j]) << 23) * rcpG128;
+      clamped |= cl ? 1u : 0u;
+    }
+    const bool check = IN != IN_BF16 || __any(clamped);
+    uint32_t near = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int k = 0; k < TOK / 4; ++k) {
+        const float t0v = row_elem<IN>(w[4 * k + 0], j, dq[4 * k + 0]) * y[j];
+        const float t1v = row_elem<IN>(w[4 * k + 1], j, dq[4 * k + 1]) * y[j];
+        const float t2v = row_elem<IN>(w[4 * k + 2], j, dq[4 * k + 2]) * y[j];
+        const float t3v = row_elem<IN>(w[4 * k + 3], j, dq[4 * k + 3]) * y[j];
+        if (check) near |= near_mid8(t0v) | near_mid8(t1v) | near_mid8(t2v) | near_mid8(t3v);
+        out[j][k] = cvt4<HW>(t0v, t1v, t2v, t3v);
+      }
+    redo |= near;
+  }
+
+  uint8_t* qo = qt + (s * C + c0) * T + t0;
+  if (__any(redo)) {
+#pragma nounroll
+    for (int j = 0; j < 8; ++j) {
+      const float S = quant_scale(e[j], G);
+#pragma nounroll
+      for (int k = 0; k < TOK / 4; ++k) {
+        uint32_t word = 0;
+#pragma nounroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = elem_at<IN>(x, x_sc8, x_sc32, x_kg, T, C, s, t0 + 4 * k + i, c0 + j);
+          word |= quant_elem_exact(v, S) << (8 * i);
+        }
+        *reinterpret_cast<uint32_t*>(qo + (int64_t)j * T + 4 * k) = word;
+      }
+    }
+  } else {
+    // payload: channel c0 + j, tokens [t0, t0 + 16) of slice s in [C, T]
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const u32x4_t v = {out[j][0], out[j][1], out[j][2], out[j][3]};
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(qo + (int64_t)j * T));
+    }
+  }
+  if (rs == 0) {
+    // blocks (tb, c0 .. c0 + 7) are consecutive; they form group (tb*C + c0) / 8
+    const int64_t nb = (T / 128) * C;
+    const int64_t blk = tb * C + c0;
+    uint32_t* e8 = reinterpret_cast<uint32_t*>(sc8 + s * nb + blk);
+    e8[0] = e[0] | (e[1] << 8) | (e[2] << 16) | (e[3] << 24);
+    e8[1] = e[4] | (e[5] << 8) | (e[6] << 16) | (e[7] << 24);
+    sc32[s * (nb / 8) + blk / 8] = G;
+  }
+}
+
+int64_t gcd64(int64_t a, int64_t b) {
+  while (b) {
+    const int64_t t = a % b;
+    a = b;
+    b = t;
+  }
+  return a;
+}
+
+}  // namespace
+
+extern "C" int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t* x_sc8,
+                                      const float* x_sc32, int64_t slices, int64_t T, int64_t C,
+                                      uint8_t* xt_fp8, uint8_t* sc_fp8, float* sc_fp32,
+                                      hipStream_t stream) {
+  if (slices < 0 || T < 0 || C < 0) return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t128: negative size");
+  if (x_dtype != PRATCHYA_DT_F32 && x_dtype != PRATCHYA_DT_BF16 && x_dtype != PRATCHYA_DT_E4M3)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t128: unsupported input dtype %d", x_dtype);
+  if (T % 128)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t128: tgrid (128, 1) does not divide %lld tokens",
+                              (long long)T);
+  if (x_dtype == PRATCHYA_DT_E4M3 && C % 128)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t128: tgrid (1, 128) of the fp8 input does not divide "
+                              "%lld channels", (long long)C);
+  if (slices == 0 || T == 0 || C == 0) return PRATCHYA_OK;
+  if (C % 8)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t128: channels must be a multiple of 8 (got %lld)",
+                              (long long)C);
+  if (!x || !xt_fp8 || !sc_fp8 || !sc_fp32 || (x_dtype == PRATCHYA_DT_E4M3 && (!x_sc8 || !x_sc32)))
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t128: null buffer");
+  const uintptr_t xa = reinterpret_cast<uintptr_t>(x);
+  if (xa % (x_dtype == PRATCHYA_DT_E4M3 ? 8 : 16) || reinterpret_cast<uintptr_t>(xt_fp8) % 16 ||
+      reinterpret_cast<uintptr_t>(sc_fp8) % 4 || reinterpret_cast<uintptr_t>(sc_fp32) % 4)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t128: buffers are not aligned");
+  if (T / 128 > 65535 || slices > 65535)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t128: too many token blocks or slices");
+  const dim3 grid((unsigned)((C + 255) / 256), (unsigned)(T / 128), (unsigned)slices);
+  const uint8_t* xb = static_cast<const uint8_t*>(x);
+  if (x_dtype == PRATCHYA_DT_BF16) {
+    hipLaunchKernelGGL((k_quant_t128<IN_BF16, true>), grid, dim3(256), 0, stream, xb, nullptr, nullptr,
+                       (int64_t)1, T, C, xt_fp8, sc_fp8, sc_fp32);
+  } else if (x_dtype == PRATCHYA_DT_F32) {
+    hipLaunchKernelGGL((k_quant_t128<IN_F32, true>), grid, dim3(256), 0, stream, xb, nullptr, nullptr,
+                       (int64_t)1, T, C, xt_fp8, sc_fp8, sc_fp32);
+  } else {
+    const int64_t kg = gcd64(8, T * (C / 128));   // blocks per group of the (1, 128) input
+    hipLaunchKernelGGL((k_quant_t128<IN_FP8, true>), grid, dim3(256), 0, stream, xb, x_sc8, x_sc32, kg, T,
+                       C, xt_fp8, sc_fp8, sc_fp32);
+  }
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess)
+    return pratchya_set_error(PRATCHYA_EHIP, "quantize_t128: launch failed: %s", hipGetErrorString(err));
+  return PRATCHYA_OK;
+}

@@ -103,3 +103,19 @@ def test_gemm_span_matches_brute_force():
             g = [(rb * sr + kb * sk) // kg for kb in range(nk)]
             for s0 in range(0, nk, P):
                 assert len(set(g[s0:s0 + P])) == 1, (rows, nk, rdiv, sr, sk, kg, P)
+
+
+def test_quantize_t128_argument_codes_without_gpu():
+    """Shape errors are reported before anything touches a buffer."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    f = lib.pratchya_quantize_t128
+    # 100 tokens: tgrid (128, 1) does not divide -> the reference's reshape error
+    assert f(None, _lib.DT_BF16, None, None, 1, 100, 64, None, None, None, None) == _lib.EINVAL
+    # fp8 input whose (1, 128) grid does not divide the channels
+    assert f(None, _lib.DT_E4M3, None, None, 1, 128, 64, None, None, None, None) == _lib.EINVAL
+    # 12 channels: groups would straddle token blocks; not supported by this kernel
+    assert f(None, _lib.DT_BF16, None, None, 1, 128, 12, None, None, None, None) == _lib.EUNSUPPORTED
+    assert f(None, 7, None, None, 1, 128, 64, None, None, None, None) == _lib.EINVAL
+    # empty tensors are a no-op
+    assert f(None, _lib.DT_BF16, None, None, 0, 128, 64, None, None, None, None) == _lib.OK

@@ -127,6 +127,27 @@ def test_wgrad_token_axis_groups():
     check(C, ref, F32_TOL, "wgrad")
 
 
+def test_wgrad_from_transposed_requantize():
+    """The config-4 wgrad chain: the stored (1,128) activation requantized to
+    (128,1) from its fp8 payload, dY requantized (128,1) from bf16, both with
+    token-contiguous payloads from quantize_t128, then A^T dY in f32."""
+    K = _K()
+    T, Cin, N_ = 1024, 512, 768
+    a_bits = O.activation_input(T, Cin, seed=5)
+    dy_bits = O.normal_input((T, N_), 1e-3, seed=6)
+    a8 = K.quantize(to_dev_bf16(a_bits), (1, 128))                 # the forward's stored operand
+    at = K.quantize_t128(*a8)
+    dt = K.quantize_t128(to_dev_bf16(dy_bits))
+    C = K.gemm_nt(K.operand_t128(*at), K.operand_t128(*dt), torch.float32)
+    torch.cuda.synchronize()
+    a_deq = O.dequantize_impl(u8(a8[0]), u8(a8[1]), f32(a8[2]), "float32", (1, 128))
+    aq = O.quantize_impl(a_deq, (128, 1))
+    dq = O.quantize_impl(O.bf16_bits_to_f32(dy_bits), (128, 1))
+    ref = (O.dequantize_impl(*aq, "float32", (128, 1)).astype(np.float64).T
+           @ O.dequantize_impl(*dq, "float32", (128, 1)).astype(np.float64))
+    check(C, ref, F32_TOL, "wgrad via quantize_t128")
+
+
 def test_group_maxima_change_across_spans():
     """Rows whose 1024-wide K spans differ by orders of magnitude, all-zero
     spans, and a weight with two groups (the accumulator rescaling path)."""

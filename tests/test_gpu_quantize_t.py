@@ -1,0 +1,128 @@
+"""GPU parity of the transposed requantize (tgrid (128, 1), payload [C, T]).
+
+Expected values: the oracle's quantize_impl(x, (128, 1)) with the payload's
+last two axes swapped; for an fp8 input, quantize_impl(dequantize_impl(x8,
+sc8, sc32, f32, (1, 128)), (128, 1)).  Bit-exact payload, e8m0 and f32 bytes
+(a NaN payload byte's sign is compared as NaN-ness only).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import qarr_oracle as O
+from tests.helpers import (assert_bytes_equal, assert_f32_bits_equal, assert_payload_equal, f32,
+                           to_dev_bf16, to_dev_f32, u8)
+
+pytestmark = pytest.mark.gpu
+
+
+def _K():
+    from pratchya_amd import _kernels
+    return _kernels
+
+
+def oracle_t128(x_f32):
+    r8, rs8, rs32 = O.quantize_impl(x_f32, (128, 1))
+    return np.ascontiguousarray(np.swapaxes(r8, -1, -2)), rs8, rs32
+
+
+def check(dev, x_f32, what, x_sc8=None, x_sc32=None):
+    xt, s8, s32 = _K().quantize_t128(dev, x_sc8, x_sc32)
+    torch.cuda.synchronize()
+    r8, rs8, rs32 = oracle_t128(x_f32)
+    assert tuple(xt.shape) == r8.shape, (tuple(xt.shape), r8.shape)
+    assert tuple(s8.shape) == rs8.shape and tuple(s32.shape) == rs32.shape
+    assert_payload_equal(u8(xt), r8, f"{what} payload")
+    assert_bytes_equal(u8(s8), rs8, f"{what} e8m0")
+    assert_f32_bits_equal(f32(s32), rs32, f"{what} group max")
+    return xt, s8, s32
+
+
+@pytest.mark.parametrize("T,C", [(128, 64), (256, 128), (384, 72), (128, 8), (512, 320)])
+def test_bf16_activation(T, C):
+    bits = O.activation_input(T, C, seed=11)
+    check(to_dev_bf16(bits), O.bf16_bits_to_f32(bits), f"bf16 [{T},{C}]")
+
+
+def test_bf16_slices():
+    bits = O.activation_input(2 * 256, 128, seed=12).reshape(2, 256, 128)
+    check(to_dev_bf16(bits), O.bf16_bits_to_f32(bits), "bf16 [2,256,128]")
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_f32_normal(seed):
+    """Random f32 inputs hit the bf16-midpoint check and its exact redo."""
+    x = np.random.default_rng(seed).standard_normal((512, 256)).astype(np.float32)
+    check(to_dev_f32(x), x, f"f32 normal seed {seed}")
+
+
+def test_f32_exact_midpoints():
+    """Elements whose x/S*128 is exactly a bf16 rounding midpoint (ties to even)
+    and one f32 ulp either side of it."""
+    T, C = 128, 64
+    x = np.zeros((T, C), np.float32)
+    x[0, :] = 1.0                        # G = 1, S = 1 for channel maxima 1
+    mids = np.float32(1.0) + np.float32(2.0 ** -8) * np.arange(1, 64, 2, dtype=np.float32)
+    v = (mids / 128).astype(np.float32)          # x/S*128 = mid exactly (power-of-two scaling)
+    x[1:1 + v.size, 0] = v
+    x[1:1 + v.size, 1] = np.nextafter(v, np.float32(2))
+    x[1:1 + v.size, 2] = np.nextafter(v, np.float32(0))
+    check(to_dev_f32(x), x, "f32 midpoints")
+
+
+def test_edge_values():
+    """Zero groups (G = 0), zero blocks inside a group (e8m0 0), tiny groups
+    that hit the 1e-7 clamp, subnormals, NaN / inf."""
+    T, C = 256, 64
+    x = np.random.default_rng(3).standard_normal((T, C)).astype(np.float32)
+    x[:128, 0:8] = 0.0                              # group with G = 0
+    x[:128, 8] = 0.0                                # e8m0 0 block in a live group
+    x[:128, 16:24] *= np.float32(1e-12)             # clamped group
+    x[:128, 24:32] = np.float32(2.0 ** -140) * np.arange(1, 129, dtype=np.float32)[:, None]
+    x[5, 32] = np.inf
+    x[7, 40] = -np.inf
+    x[9, 48] = np.nan
+    x[130, 56] = 3.0e38                             # huge group next to normal ones
+    check(to_dev_f32(x), x, "f32 edges")
+    xb = O.f32_to_bf16_bits(x)
+    check(to_dev_bf16(xb), O.bf16_bits_to_f32(xb), "bf16 edges")
+
+
+@pytest.mark.parametrize("T,C", [(256, 256), (384, 1024)])
+def test_fp8_input_requantized_along_tokens(T, C):
+    """A stored (1, 128) activation requantized to (128, 1): the fp8 payload is
+    dequantized in registers exactly as dequantize_impl does."""
+    bits = O.activation_input(T, C, seed=21)
+    x8, s8, s32 = O.quantize_impl(O.bf16_bits_to_f32(bits), (1, 128))
+    deq = O.dequantize_impl(x8, s8, s32, "float32", (1, 128))
+    dev8 = torch.from_numpy(x8).cuda()
+    check(dev8, deq, f"fp8 [{T},{C}]", torch.from_numpy(s8).cuda(), torch.from_numpy(s32).cuda())
+
+
+def test_config4_dy_full_size_sampled_token_blocks():
+    """Config 4: dY bf16 [16384, 8192] ~ N(0, 1e-3), requantized (128, 1).  The
+    full tensor goes through the kernel; token blocks are independent under
+    (128, 1) groups, so sampled 128-token slabs are checked against the oracle."""
+    T, C = 16384, 8192
+    g = torch.Generator(device="cuda").manual_seed(4)
+    dy = (torch.randn((T, C), generator=g, device="cuda") * 1e-3).to(torch.bfloat16)
+    xt, s8, s32 = _K().quantize_t128(dy)
+    torch.cuda.synchronize()
+    xt_h = u8(xt)
+    s8_h = u8(s8).reshape(-1)
+    s32_h = f32(s32).reshape(-1)
+    for tb in (0, 1, 77, 127):
+        slab = dy[tb * 128:(tb + 1) * 128].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+        r8, rs8, rs32 = oracle_t128(O.bf16_bits_to_f32(slab))
+        assert_payload_equal(xt_h[:, tb * 128:(tb + 1) * 128], r8, f"slab {tb} payload")
+        assert_bytes_equal(s8_h[tb * C:(tb + 1) * C], rs8.reshape(-1), f"slab {tb} e8m0")
+        assert_f32_bits_equal(s32_h[tb * C // 8:(tb + 1) * C // 8], rs32.reshape(-1), f"slab {tb} G")
+
+
+def test_argument_errors():
+    K = _K()
+    with pytest.raises(ValueError, match="does not divide"):
+        K.quantize_t128(torch.zeros((100, 64), dtype=torch.bfloat16, device="cuda"))
+    from pratchya_amd._lib import PratchyaError
+    with pytest.raises(PratchyaError, match="multiple of 8"):
+        K.quantize_t128(torch.zeros((128, 12), dtype=torch.bfloat16, device="cuda"))

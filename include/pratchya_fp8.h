@@ -114,7 +114,8 @@ int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t* x_sc8, con
  * with tgrid (128, b) and transposed is (b, 1, rows/b, K_group).
  * C: [M, N] with row stride ldc elements, c_dtype f32 or bf16.
  * M and N must be multiples of 256 and K of 128 (PRATCHYA_EUNSUPPORTED
- * otherwise); the group index must be affine in kb (every quantizer layout is). */
+ * otherwise).  Any group layout is accepted: the kernel reloads group maxima
+ * wherever some row's group changes along K (see pratchya_gemm_span). */
 int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, const float* a_sc32,
                         int64_t a_rdiv, int64_t a_sr, int64_t a_sk, int64_t a_kg,
                         const uint8_t* B, int64_t ldb, const uint8_t* b_sc8, const float* b_sc32,
@@ -122,9 +123,10 @@ int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, con
                         int64_t M, int64_t N, int64_t K, void* C, int64_t ldc, int c_dtype,
                         hipStream_t stream);
 
-/* Number of consecutive 128-K blocks over which an operand's group maxima stay
- * constant (the GEMM rescales its accumulator at those boundaries); 0 if the
- * layout is not supported.  Host-only query, used by tests. */
+/* Span of an operand's scale layout: the largest P such that every row's group
+ * index is constant over each aligned run of P 128-wide K blocks (the GEMM
+ * reloads group maxima and rescales its accumulator at multiples of it);
+ * 0 for invalid arguments.  Host-only query, used by tests. */
 int64_t pratchya_gemm_span(int64_t rows, int64_t K, int64_t r_div, int64_t s_r, int64_t s_k,
                            int64_t kg);
 

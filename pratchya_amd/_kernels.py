@@ -11,6 +11,7 @@ from typing import Tuple
 import torch
 
 from . import _lib
+from ._lib import PratchyaError, PratchyaUnsupported  # noqa: F401  (re-exported)
 
 E4M3 = torch.float8_e4m3fn
 E8M0 = torch.float8_e8m0fnu

@@ -53,6 +53,11 @@ class PratchyaError(RuntimeError):
     """A HIP launch failure or an unsupported request reported by the library."""
 
 
+class PratchyaUnsupported(PratchyaError):
+    """A valid request outside what the kernels cover (PRATCHYA_EUNSUPPORTED),
+    e.g. a GEMM shape that is not a multiple of its tile."""
+
+
 def load() -> ctypes.CDLL:
     """Load the library once; raise if it is absent or has another ABI."""
     global _lib
@@ -84,4 +89,6 @@ def check(rc: int, what: str) -> None:
     msg = load().pratchya_last_error().decode(errors="replace")
     if rc == EINVAL:
         raise ValueError(f"{what}: {msg}")
+    if rc == EUNSUPPORTED:
+        raise PratchyaUnsupported(f"{what}: {msg} (status {rc})")
     raise PratchyaError(f"{what}: {msg} (status {rc})")

@@ -37,6 +37,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <numeric>
+
 #include "pratchya_fp8.h"
 
 int pratchya_set_error(int code, const char* fmt, ...);
@@ -64,9 +66,7 @@ struct Scales {
   int64_t r_div;       // rows per block along the non-contraction axis
   int64_t s_r;         // block index stride per row block
   int64_t s_k;         // block index stride per 128-K block
-  int64_t kg;          // blocks per group
-  int64_t bpg;         // group index of (row, kb) = (base(row) / kg) + (kb / bpg) * gstep
-  int64_t gstep;
+  int64_t kg;          // blocks per group: group of block i is i / kg
 };
 
 __host__ __device__ __forceinline__ int64_t blk_index(const Scales& s, int64_t row, int64_t kb) {
@@ -175,14 +175,12 @@ __device__ __forceinline__ void issue_stage(const OperandRsrc& ra, int64_t lda, 
   __builtin_amdgcn_raw_ptr_buffer_load_lds(ra.e8, (lds_void*)(st + OFF_EA + w4 * 256), 4, ia & ~3u, 0, 0, 0);
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rb.e8, (lds_void*)(st + OFF_EB + w4 * 256), 4, ib & ~3u, 0, 0, 0);
   if (span_start) {
-    // group of the row's block at kb = 0 (rare: recomputed instead of held)
-    const uint32_t ga0 = d.ea_word / (uint32_t)sa.kg, gb0 = d.eb_word / (uint32_t)sb.kg;
-    const uint32_t da = ((uint32_t)kt / (uint32_t)sa.bpg) * (uint32_t)sa.gstep;
-    const uint32_t db = ((uint32_t)kt / (uint32_t)sb.bpg) * (uint32_t)sb.gstep;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra.g32, (lds_void*)(st + OFF_GA + w4 * 256), 4,
-                                             (ga0 + da) * 4u, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb.g32, (lds_void*)(st + OFF_GB + w4 * 256), 4,
-                                             (gb0 + db) * 4u, 0, 0, 0);
+    // group maxima of the rows' blocks at this K block (exact group index)
+    const uint32_t ga = ia / (uint32_t)sa.kg, gb = ib / (uint32_t)sb.kg;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra.g32, (lds_void*)(st + OFF_GA + w4 * 256), 4, ga * 4u, 0,
+                                             0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb.g32, (lds_void*)(st + OFF_GB + w4 * 256), 4, gb * 4u, 0,
+                                             0, 0);
   }
 }
 
@@ -445,55 +443,37 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   }
 }
 
-// Affine group index of an operand's scale layout: returns false if the
-// group of block (rb, kb) = (rb*s_r + kb*s_k) / kg is not of the form
-// floor(rb*s_r / kg) + floor(kb / bpg) * gstep for every row block rb and
-// every kb < nk.  The closed forms below cover every layout pratchya's
-// quantizer produces for 128-wide contraction blocks; anything else is checked
-// exhaustively.
-bool affine_groups(Scales* s, int64_t rows, int64_t nk) {
-  const int64_t nrb = (rows + s->r_div - 1) / s->r_div;
-  auto verify = [&](int64_t bpg, int64_t gstep) {
-    if (nrb * nk > (int64_t)1 << 22) return false;
-    for (int64_t rb = 0; rb < nrb; ++rb)
-      for (int64_t kb = 0; kb < nk; ++kb)
-        if ((rb * s->s_r + kb * s->s_k) / s->kg != (rb * s->s_r) / s->kg + (kb / bpg) * gstep)
-          return false;
-    return true;
-  };
-  int64_t bpg = 0, gstep = 0;
-  if (s->s_k == 0) {
-    bpg = nk; gstep = 0;                                   // K does not move the index
-  } else if (s->s_k == 1 && s->s_r % s->kg == 0) {
-    bpg = s->kg; gstep = 1;                                // each row: aligned runs of kg blocks
-  } else if (s->s_k == 1 && s->s_r > 0 && s->kg % s->s_r == 0 && nk <= s->s_r) {
-    bpg = nk; gstep = 0;                                   // a row's blocks stay in one group
-  } else if (s->s_r * (nrb - 1) < s->s_k && s->kg % s->s_k == 0) {
-    bpg = s->kg / s->s_k; gstep = 1;                       // rows interleaved inside a K block
-  } else if (s->s_k % s->kg == 0 && s->s_r * (nrb - 1) < s->kg &&
-             (s->s_r == 0 || s->kg % s->s_r == 0)) {
-    bpg = 1; gstep = s->s_k / s->kg;                       // a new group every K block
-  } else {
-    for (int64_t b = nk; b >= 1 && !bpg; --b)
-      for (int64_t g = 0; g <= 1 && !bpg; ++g)
-        if (verify(b, g * ((s->s_k * b) / s->kg))) { bpg = b; gstep = g * ((s->s_k * b) / s->kg); }
-    if (!bpg) return false;
+// Span of an operand's scale layout: the largest P such that every row's
+// group index (block / kg) is constant over each aligned run [jP, jP + P) of
+// 128-wide K blocks, i.e. the gcd of all K-block positions at which some row's
+// group changes (nk if none does).  The kernel reloads group maxima and
+// rescales its accumulator at multiples of the span; P = 1 is always valid.
+// Row blocks whose base index has the same residue mod kg change groups at the
+// same positions, so only one period of residues is walked.
+int64_t group_span(const Scales& s, int64_t rows, int64_t nk) {
+  if (nk <= 1 || s.s_k == 0) return nk < 1 ? 1 : nk;
+  const int64_t nrb = (rows + s.r_div - 1) / s.r_div;
+  const int64_t period = s.kg / std::gcd(s.s_r, s.kg);
+  const int64_t n_res = nrb < period ? nrb : period;
+  int64_t P = 0;
+  for (int64_t rb = 0; rb < n_res && P != 1; ++rb) {
+    const int64_t r = (rb * s.s_r) % s.kg;
+    for (int64_t j = 1; P != 1; ++j) {
+      const int64_t kb = (j * s.kg - r + s.s_k - 1) / s.s_k;   // first kb reaching group boundary j
+      if (kb >= nk) break;
+      P = std::gcd(P, kb);
+    }
   }
-  if (bpg > nk) bpg = nk;
-  if (bpg < 1) bpg = 1;
-  s->bpg = bpg;
-  s->gstep = gstep;
-  return true;
+  return P == 0 ? nk : P;
 }
 
 }  // namespace
 
 extern "C" int64_t pratchya_gemm_span(int64_t rows, int64_t K, int64_t r_div, int64_t s_r,
                                       int64_t s_k, int64_t kg) {
-  if (K % BK || r_div < 1 || kg < 1) return 0;
-  Scales s{nullptr, nullptr, r_div, s_r, s_k, kg, 0, 0};
-  if (!affine_groups(&s, rows, K / BK)) return 0;
-  return s.bpg;
+  if (K % BK || r_div < 1 || kg < 1 || s_r < 0 || s_k < 0 || rows < 1) return 0;
+  Scales s{nullptr, nullptr, r_div, s_r, s_k, kg};
+  return group_span(s, rows, K / BK);
 }
 
 extern "C" int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t* a_sc8,
@@ -518,13 +498,11 @@ extern "C" int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t*
       (reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) % 16 ||
       reinterpret_cast<uintptr_t>(C) % 16)
     return pratchya_set_error(PRATCHYA_EINVAL, "gemm: leading dimensions / alignment not supported");
-  if (a_rdiv < 1 || b_rdiv < 1 || a_kg < 1 || b_kg < 1)
+  if (a_rdiv < 1 || b_rdiv < 1 || a_kg < 1 || b_kg < 1 || a_sr < 0 || a_sk < 0 || b_sr < 0 || b_sk < 0)
     return pratchya_set_error(PRATCHYA_EINVAL, "gemm: bad scale layout");
-  Scales sa{a_sc8, a_sc32, a_rdiv, a_sr, a_sk, a_kg, 0, 0};
-  Scales sb{b_sc8, b_sc32, b_rdiv, b_sr, b_sk, b_kg, 0, 0};
+  Scales sa{a_sc8, a_sc32, a_rdiv, a_sr, a_sk, a_kg};
+  Scales sb{b_sc8, b_sc32, b_rdiv, b_sr, b_sk, b_kg};
   const int64_t nk = K / BK;
-  if (!affine_groups(&sa, M, nk) || !affine_groups(&sb, N, nk))
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: scale groups are not affine in K");
   if ((M / a_rdiv) * a_sr + nk * a_sk > (int64_t)UINT32_MAX ||
       (N / b_rdiv) * b_sr + nk * b_sk > (int64_t)UINT32_MAX)
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: scale arrays beyond 2^32 blocks");
@@ -540,13 +518,8 @@ extern "C" int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t*
   const bool fine_b = b_rdiv % 32 != 0;
   if (fine_b && !(b_rdiv % 4 == 0 || (b_rdiv == 1 && b_kg % (4 * b_sr) == 0 && b_sk % (4 * b_sr) == 0)))
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: B scale groups narrower than 4 columns");
-  int64_t x = sa.bpg, y = sb.bpg;   // span: both group patterns are constant over it
-  while (y) {
-    const int64_t t = x % y;
-    x = y;
-    y = t;
-  }
-  const int64_t span = x < 1 ? 1 : x;
+  // span: both operands' group maxima are constant over it
+  const int64_t span = std::gcd(group_span(sa, M, nk), group_span(sb, N, nk));
   // buffer resources address bytes with 32-bit offsets
   const int64_t a_bytes = (M - 1) * lda + K, b_bytes = (N - 1) * ldb + K;
   const int64_t ga_bytes = (last_a / a_kg + 1) * 4, gb_bytes = (last_b / b_kg + 1) * 4;

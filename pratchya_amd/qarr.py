@@ -1,0 +1,702 @@
+"""Quantized arrays on the gfx950 kernels: the operator API of
+``pratchya/_qualia/_qarr.py`` (abbreviated ``Q``) over PyTorch tensors.
+
+Same class name, private attribute names (``_QArrayImpl__value``,
+``__sc_fp8``, ``__sc_fp32``, ``__tgrid``), methods, module functions,
+argument meaning, output shapes and custom-vjp semantics as the reference.
+Every quantize, dequantize, requantize and block-scaled GEMM runs on the
+gfx950 kernels of ``libpratchya_fp8.so``; PyTorch provides device memory,
+streams and autograd.
+
+Differentiation.  The reference differentiates through ``jax.custom_vjp``
+rules whose cotangents for an fp8 payload are bf16/f32 arrays (dequantize's
+backward, Q:575-601) or fp8 triples (matmul_impl's backward, Q:637-640), and
+quantize_impl's backward (Q:514-526) passes the former through and
+dequantizes the latter.  PyTorch's engine would round a gradient to its
+input's dtype (e4m3fn), so payloads here stay outside the autograd graph:
+``quantize_impl`` tags its payload with the tensor it was quantized from, and
+the autograd Functions below (dequantize, matmul, the mixed matmuls, the
+elementwise ops) return the composed cotangent -- what the reference's
+quantize backward would produce -- straight to that tensor.
+
+GEMM backward.  ``matmul_impl``'s reference backward contracts the f32
+cotangent with the dequantized operands in f32 (Q:621-622) and is the default
+here ("f32": dequantize kernels plus an f32 library GEMM).  The "fp8" mode
+(``set_matmul_backward("fp8")``) runs dgrad and wgrad on the FP8 MFMA kernel
+instead, with the cotangent quantized (1, 128) for dgrad and both wgrad
+operands requantized along the token axis (128, 1) -- the scheme of
+``fp8_matmul``'s backward (Q:784-789); its results differ from the f32
+backward by the quantization of the cotangent.
+"""
+from __future__ import annotations
+
+import math
+import operator
+from typing import Optional, Tuple, Union
+
+import torch
+import torch.utils._pytree as pytree
+
+from . import _kernels as K
+
+E4M3 = K.E4M3
+E8M0 = K.E8M0
+
+_SRC = "_pratchya_src"        # payload attribute: the tensor it was quantized from
+_PAYLOAD_T = "_pratchya_t"    # payload attribute: its byte transpose (weights)
+
+_BACKWARD_MODES = ("f32", "fp8")
+_backward_mode = "f32"
+
+
+def set_matmul_backward(mode: str) -> None:
+    """Select how matmul_impl's backward contracts: "f32" (the reference's
+    f32 dots of the dequantized operands, default) or "fp8" (FP8 MFMA GEMMs
+    on the requantized cotangent)."""
+    global _backward_mode
+    if mode not in _BACKWARD_MODES:
+        raise ValueError(f"matmul backward mode must be one of {_BACKWARD_MODES}, got {mode!r}")
+    _backward_mode = mode
+
+
+def get_matmul_backward() -> str:
+    return _backward_mode
+
+
+def _grid_hw(shape) -> Tuple[int, int]:
+    """(H, W) of the last two axes as the reference sees them (Q:461-464)."""
+    if len(shape) == 0:
+        return 1, 1
+    if len(shape) == 1:
+        return 1, int(shape[0])
+    return int(shape[-2]), int(shape[-1])
+
+
+def _src(x8) -> Optional[torch.Tensor]:
+    src = getattr(x8, _SRC, None)
+    return src if (src is not None and torch.is_grad_enabled()) else None
+
+
+def _reduce_broadcast(g: torch.Tensor, target_shape) -> torch.Tensor:
+    """Sum the broadcast axes of a cotangent (Q:624-632)."""
+    target_shape = tuple(target_shape)
+    if tuple(g.shape) == target_shape:
+        return g
+    axes = list(range(g.dim() - len(target_shape)))
+    for i, (gs, ts) in enumerate(zip(g.shape[len(axes):], target_shape)):
+        if ts == 1 and gs > 1:
+            axes.append(len(axes) + i)
+    g = g.sum(dim=tuple(axes))
+    return g.reshape(target_shape)
+
+
+# --------------------------------------------------------------------------
+# quantize_impl / dequantize_impl  (Q:458-506, Q:541-569, vjps Q:508-528, Q:571-603)
+# --------------------------------------------------------------------------
+def quantize_impl(x: torch.Tensor, tgrid: Tuple = (128, 128)):
+    """(x_fp8, sc_fp8, sc_fp32) of ``x`` with block grid ``tgrid`` (Q:458-506)."""
+    x8, s8, s32 = K.quantize(x.detach(), tuple(tgrid))
+    if x.requires_grad and torch.is_grad_enabled():
+        setattr(x8, _SRC, x)
+    return x8, s8, s32
+
+
+def _fix_nan_e8m0(sc8: torch.Tensor) -> torch.Tensor:
+    """quantize_impl_bwd's repair of NaN e8m0 cotangent scales to 1.0 (Q:522-523)."""
+    u = sc8.view(torch.uint8)
+    return torch.where(u == 0xFF, torch.full_like(u, 0x7F), u).view(E8M0)
+
+
+def _requant_cotangent(g32: torch.Tensor, tgrid) -> torch.Tensor:
+    """A matmul/elementwise f32 cotangent as it reaches the quantized input:
+    requantized with the input's grid (Q:637-638) and dequantized by
+    quantize_impl's backward (Q:521-526)."""
+    g8, gs8, gs32 = K.quantize(g32.contiguous(), tuple(tgrid))
+    return K.dequantize(g8, _fix_nan_e8m0(gs8), gs32, torch.float32, tuple(tgrid))
+
+
+class _Dequantize(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, src, x8, sc8, sc32, dtype, tgrid):
+        ctx.scales = (sc8, sc32)
+        ctx.tgrid = tgrid
+        return K.dequantize(x8, sc8, sc32, dtype, tgrid)
+
+    @staticmethod
+    def backward(ctx, g):
+        sc8, sc32 = ctx.scales
+        # dequantize_impl_bwd (Q:575-601), passed through quantize_impl_bwd (Q:518-519)
+        return K.dequantize_bwd(g.contiguous(), sc8, sc32, ctx.tgrid), None, None, None, None, None
+
+
+def dequantize_impl(x_fp8, sc_fp8, sc_fp32, dtype, tgrid):
+    """``(f32(q) * (2^(e-127) * G)) / 128`` cast to ``dtype`` (Q:541-569)."""
+    src = _src(x_fp8)
+    if src is not None:
+        return _Dequantize.apply(src, x_fp8, sc_fp8, sc_fp32, dtype, tuple(tgrid))
+    return K.dequantize(x_fp8, sc_fp8, sc_fp32, dtype, tuple(tgrid))
+
+
+def _deq32(x8, s8, s32, tgrid) -> torch.Tensor:
+    return K.dequantize(x8, s8, s32, torch.float32, tuple(tgrid))
+
+
+# --------------------------------------------------------------------------
+# Block-scaled GEMM planning
+# --------------------------------------------------------------------------
+_GEMM_TILE_MN, _GEMM_TILE_K = 256, 128
+
+
+def _lhs_operand(x8, s8, s32, grid):
+    """x [..., M, K] quantized (a, 128) as a K-contiguous GEMM operand, or None."""
+    if x8.dim() < 2 or tuple(grid)[1] != 128:
+        return None
+    M, Kd = int(x8.shape[-2]), int(x8.shape[-1])
+    lead = 1
+    for d in x8.shape[:-2]:
+        lead *= int(d)
+    rows = lead * M
+    a = int(grid[0])
+    # leading slices flatten into rows when the group size does not depend on them
+    if lead > 1 and K.group_layout(rows, Kd, grid)[1] != K.group_layout(M, Kd, grid)[1]:
+        return None
+    if rows % _GEMM_TILE_MN or Kd % _GEMM_TILE_K or a > M or M % a:
+        return None
+    return K.Operand(x8.reshape(rows, Kd), s8, s32, (a, Kd // 128, 1, K.group_layout(rows, Kd, grid)[1]))
+
+
+def _rhs_operand(y8, s8, s32, grid):
+    """y [K, N] quantized (128, b) as the transposed GEMM operand, or None."""
+    if y8.dim() != 2 or tuple(grid)[0] != 128:
+        return None
+    Kd, N = int(y8.shape[0]), int(y8.shape[1])
+    if N % _GEMM_TILE_MN or Kd % _GEMM_TILE_K:
+        return None
+    pt = getattr(y8, _PAYLOAD_T, None)
+    if pt is None:
+        pt = K.transpose_u8(y8)
+        setattr(y8, _PAYLOAD_T, pt)     # a weight is transposed once per quantization
+    return K.operand_transposed(y8, s8, s32, grid, payload_t=pt)
+
+
+def _try_gemm(op_a, op_b) -> Optional[torch.Tensor]:
+    """f32 C = dequant(op_a) . dequant(op_b)^T on the FP8 MFMA kernel, or None
+    if the kernel does not cover the operands' layouts (it reports that before
+    launching anything)."""
+    if op_a is None or op_b is None:
+        return None
+    try:
+        return K.gemm_nt(op_a, op_b, torch.float32)
+    except K.PratchyaUnsupported:
+        return None
+
+
+def _matmul_forward(x8, xs8, xs32, y8, ys8, ys32, gx, gy) -> torch.Tensor:
+    """f32 dequant(x) @ dequant(y) (Q:605-608): the FP8 MFMA GEMM when both
+    operands' block grids and shapes fit it ((a, 128) x (128, b) grids, M and N
+    multiples of 256, K of 128), else the reference's own f32 dot of the
+    operands dequantized by the kernels."""
+    op_a = _lhs_operand(x8, xs8, xs32, gx)
+    op_b = _rhs_operand(y8, ys8, ys32, gy) if op_a is not None else None
+    out = _try_gemm(op_a, op_b)
+    if out is not None:
+        return out.reshape(tuple(x8.shape[:-1]) + (int(y8.shape[1]),))
+    return torch.matmul(_deq32(x8, xs8, xs32, gx), _deq32(y8, ys8, ys32, gy))
+
+
+def _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y):
+    """dgrad / wgrad on the FP8 MFMA kernel (the "fp8" backward), or None
+    when the layouts do not fit it."""
+    if y8.dim() != 2 or tuple(gx) != (1, 128) or tuple(gy)[1] != 128:
+        return None
+    if _lhs_operand(x8, xs8, xs32, gx) is None:
+        return None
+    Kd, N = int(y8.shape[0]), int(y8.shape[1])
+    rows = g.numel() // N
+    if rows % _GEMM_TILE_MN or Kd % _GEMM_TILE_MN or N % _GEMM_TILE_MN:
+        return None
+    g2 = g.reshape(rows, N)
+    gxf = gyf = None
+    try:
+        if need_x:
+            gq = K.quantize(g2.contiguous(), (1, 128))
+            op_g = K.operand_rows(*gq, (1, 128))
+            op_w = K.operand_rows(y8, ys8, ys32, gy)          # W [K, N]: rows K, contraction N
+            gxf = K.gemm_nt(op_g, op_w, torch.float32).reshape(tuple(g.shape[:-1]) + (Kd,))
+        if need_y:
+            xt = K.quantize_t128(x8.reshape(rows, Kd), xs8, xs32)   # stored activation, requantized
+            gt = K.quantize_t128(g2.contiguous())
+            gyf = K.gemm_nt(K.operand_t128(*xt), K.operand_t128(*gt), torch.float32)
+    except K.PratchyaUnsupported:
+        return None
+    return gxf, gyf
+
+
+class _Matmul(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, src_x, src_y, x8, xs8, xs32, y8, ys8, ys32, gx, gy):
+        ctx.saved = (x8, xs8, xs32, y8, ys8, ys32)
+        ctx.grids = (gx, gy)
+        return _matmul_forward(x8, xs8, xs32, y8, ys8, ys32, gx, gy)
+
+    @staticmethod
+    def backward(ctx, g):
+        x8, xs8, xs32, y8, ys8, ys32 = ctx.saved
+        gx, gy = ctx.grids
+        need_x, need_y = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        g = g.float()
+        res = _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y) \
+            if _backward_mode == "fp8" else None
+        if res is not None:
+            gxf, gyf = res
+        else:
+            # Q:618-622: f32 dots of the dequantized operands
+            gxf = g @ _deq32(y8, ys8, ys32, gy).transpose(-1, -2) if need_x else None
+            gyf = _deq32(x8, xs8, xs32, gx).transpose(-1, -2) @ g if need_y else None
+        grad_x = grad_y = None
+        if need_x:
+            grad_x = _requant_cotangent(_reduce_broadcast(gxf, x8.shape), gx)
+        if need_y:
+            grad_y = _requant_cotangent(_reduce_broadcast(gyf, y8.shape), gy)
+        return grad_x, grad_y, None, None, None, None, None, None, None, None
+
+
+def matmul_impl(x_fp8, x_sc8, x_sc32, y_fp8, y_sc8, y_sc32, block_grid_x: Tuple, block_grid_y: Tuple):
+    """f32 ``dequant(x) @ dequant(y)`` with the reference's vjp (Q:605-640)."""
+    gx, gy = tuple(block_grid_x), tuple(block_grid_y)
+    sx, sy = _src(x_fp8), _src(y_fp8)
+    if sx is not None or sy is not None:
+        return _Matmul.apply(sx, sy, x_fp8, x_sc8, x_sc32, y_fp8, y_sc8, y_sc32, gx, gy)
+    return _matmul_forward(x_fp8, x_sc8, x_sc32, y_fp8, y_sc8, y_sc32, gx, gy)
+
+
+class _MatmulMixed(torch.autograd.Function):
+    """dequant(x) @ y with y a plain array (Q:645-676)."""
+
+    @staticmethod
+    def forward(ctx, src_x, y, x8, xs8, xs32, gx):
+        ctx.saved = (x8, xs8, xs32, y.detach())
+        ctx.gx = gx
+        return torch.matmul(_deq32(x8, xs8, xs32, gx), y.detach().float())
+
+    @staticmethod
+    def backward(ctx, g):
+        x8, xs8, xs32, y = ctx.saved
+        g = g.float()
+        grad_x = grad_y = None
+        if ctx.needs_input_grad[0]:
+            gxf = _reduce_broadcast(g @ y.float().transpose(-1, -2), x8.shape)
+            grad_x = _requant_cotangent(gxf, ctx.gx)
+        if ctx.needs_input_grad[1]:
+            grad_y = _deq32(x8, xs8, xs32, ctx.gx).transpose(-1, -2) @ g
+        return grad_x, grad_y, None, None, None, None
+
+
+def matmul_mixed_impl(x_fp8, x_sc8, x_sc32, y_f32, block_grid_x: Tuple):
+    gx = tuple(block_grid_x)
+    sx = _src(x_fp8)
+    if sx is not None or (torch.is_grad_enabled() and y_f32.requires_grad):
+        return _MatmulMixed.apply(sx, y_f32, x_fp8, x_sc8, x_sc32, gx)
+    return torch.matmul(_deq32(x_fp8, x_sc8, x_sc32, gx), y_f32.float())
+
+
+class _RMatmulMixed(torch.autograd.Function):
+    """x @ dequant(y) with x a plain array (Q:679-712)."""
+
+    @staticmethod
+    def forward(ctx, x, src_y, y8, ys8, ys32, gy):
+        ctx.saved = (x.detach(), y8, ys8, ys32)
+        ctx.gy = gy
+        return torch.matmul(x.detach().float(), _deq32(y8, ys8, ys32, gy))
+
+    @staticmethod
+    def backward(ctx, g):
+        x, y8, ys8, ys32 = ctx.saved
+        g = g.float()
+        grad_x = grad_y = None
+        if ctx.needs_input_grad[0]:
+            grad_x = g @ _deq32(y8, ys8, ys32, ctx.gy).transpose(-1, -2)
+        if ctx.needs_input_grad[1]:
+            gyf = _reduce_broadcast(x.float().transpose(-1, -2) @ g, y8.shape)
+            grad_y = _requant_cotangent(gyf, ctx.gy)
+        return grad_x, grad_y, None, None, None, None
+
+
+def rmatmul_mixed_impl(x_f32, y_fp8, y_sc8, y_sc32, block_grid_y: Tuple):
+    gy = tuple(block_grid_y)
+    sy = _src(y_fp8)
+    if sy is not None or (torch.is_grad_enabled() and x_f32.requires_grad):
+        return _RMatmulMixed.apply(x_f32, sy, y_fp8, y_sc8, y_sc32, gy)
+    return torch.matmul(x_f32.float(), _deq32(y_fp8, y_sc8, y_sc32, gy))
+
+
+# --------------------------------------------------------------------------
+# Elementwise ops on two quantized arrays (Q:715-763)
+# --------------------------------------------------------------------------
+class _Elementwise(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, src_x, src_y, x8, xs8, xs32, y8, ys8, ys32, op, tgrid):
+        ctx.saved = (x8, xs8, xs32, y8, ys8, ys32)
+        ctx.op, ctx.tgrid = op, tgrid
+        return op(_deq32(x8, xs8, xs32, tgrid), _deq32(y8, ys8, ys32, tgrid))
+
+    @staticmethod
+    def backward(ctx, g):
+        x8, xs8, xs32, y8, ys8, ys32 = ctx.saved
+        xf = _deq32(x8, xs8, xs32, ctx.tgrid)
+        yf = _deq32(y8, ys8, ys32, ctx.tgrid)
+        if ctx.op is operator.floordiv:
+            gxf = gyf = None                 # piecewise constant: zero cotangents
+        else:
+            with torch.enable_grad():
+                xf.requires_grad_(True)
+                yf.requires_grad_(True)
+                out = ctx.op(xf, yf)
+                gxf, gyf = torch.autograd.grad(out, (xf, yf), g, allow_unused=True)
+        gxf = torch.zeros_like(xf) if gxf is None else gxf
+        gyf = torch.zeros_like(yf) if gyf is None else gyf
+        grad_x = _requant_cotangent(_reduce_broadcast(gxf, x8.shape), ctx.tgrid) \
+            if ctx.needs_input_grad[0] else None
+        grad_y = _requant_cotangent(_reduce_broadcast(gyf, y8.shape), ctx.tgrid) \
+            if ctx.needs_input_grad[1] else None
+        return grad_x, grad_y, None, None, None, None, None, None, None, None
+
+
+def make_elementwise_impl(op):
+    def impl(x_fp8, x_sc8, x_sc32, y_fp8, y_sc8, y_sc32, tgrid):
+        tgrid = tuple(tgrid)
+        sx, sy = _src(x_fp8), _src(y_fp8)
+        if sx is not None or sy is not None:
+            return _Elementwise.apply(sx, sy, x_fp8, x_sc8, x_sc32, y_fp8, y_sc8, y_sc32, op, tgrid)
+        return op(_deq32(x_fp8, x_sc8, x_sc32, tgrid), _deq32(y_fp8, y_sc8, y_sc32, tgrid))
+    return impl
+
+
+# Python's operators on tensors are jnp's: // floors, % takes the divisor's sign.
+add_impl = make_elementwise_impl(operator.add)
+mul_impl = make_elementwise_impl(operator.mul)
+sub_impl = make_elementwise_impl(operator.sub)
+truediv_impl = make_elementwise_impl(operator.truediv)
+floordiv_impl = make_elementwise_impl(operator.floordiv)
+mod_impl = make_elementwise_impl(operator.mod)
+pow_impl = make_elementwise_impl(operator.pow)
+
+
+# --------------------------------------------------------------------------
+# QArrayImpl  (Q:15-425)
+# --------------------------------------------------------------------------
+_REFLECTED = {"__matmul__": "__rmatmul__", "__add__": "__radd__", "__sub__": "__rsub__",
+              "__mul__": "__rmul__", "__truediv__": "__rtruediv__", "__div__": "__rtruediv__",
+              "__floordiv__": "__rfloordiv__", "__mod__": "__rmod__", "__pow__": "__rpow__"}
+
+
+def _value_of(other):
+    return other.value if hasattr(other, "value") else other
+
+
+def _adapted_grid(grid, shape) -> Tuple[int, int]:
+    """Grid adapted to a new shape by gcd (Q:371-380)."""
+    H, W = _grid_hw(shape)
+    return math.gcd(int(grid[0]), H), math.gcd(int(grid[1]), W)
+
+
+class QArrayImpl:
+    """An FP8 block-quantized array: e4m3fn payload, per-block e8m0 scales and
+    per-group f32 maxima (Q:15-425).  ``quant=False`` wraps a plain tensor."""
+
+    def __init__(self, value: Union["QArrayImpl", torch.Tensor], tgrid: Optional[Tuple[int, int]] = None,
+                 quant: bool = True):
+        if not quant:
+            self.__value = value
+        elif isinstance(value, QArrayImpl):
+            self.__tgrid = value._QArrayImpl__tgrid
+            self.__value = value._QArrayImpl__value
+            self.__sc_fp8 = value._QArrayImpl__sc_fp8
+            self.__sc_fp32 = value._QArrayImpl__sc_fp32
+        else:
+            assert tgrid is not None
+            self.__tgrid = tuple(tgrid)
+            if not torch.is_tensor(value):
+                value = torch.as_tensor(value, dtype=torch.float32, device="cuda")
+            # the reference upcasts to f32 (Q:29); bf16 and f32 inputs quantize
+            # to identical bytes, so bf16 is passed through unconverted
+            if value.dtype not in (torch.float32, torch.bfloat16):
+                value = value.float()
+            self.__value, self.__sc_fp8, self.__sc_fp32 = self.__quantize(value)
+
+    def get_value(self):
+        return self.__value
+
+    def __quantize(self, value):
+        # Q:35-44: 3-D arrays are quantized slice by slice; the kernels treat
+        # leading axes as independent slices in one launch, with the same bytes.
+        return quantize_impl(value, self.__tgrid)
+
+    def dequantize(self, dtype):
+        if self.__value.dtype != E4M3:
+            return self.__value.to(dtype)
+        return dequantize_impl(self.__value, self.__sc_fp8, self.__sc_fp32, dtype, self.__tgrid)
+
+    def __jax_array__(self):
+        return self.dequantize(torch.float32)
+
+    @classmethod
+    def __torch_function__(cls, func, types, args=(), kwargs=None):
+        """Torch functions see a quantized array as its f32 dequantization
+        (the role of ``__jax_array__`` for jnp functions, Q:58-59).  A tensor
+        operator with the quantized array on its right (``t @ q``, ``t - q``)
+        goes to the array's reflected method, as Python's operator protocol
+        does for the reference's arrays."""
+        kwargs = kwargs or {}
+        name = getattr(func, "__name__", "")
+        if (name in _REFLECTED and len(args) == 2 and not kwargs and isinstance(args[1], QArrayImpl)
+                and not isinstance(args[0], QArrayImpl)):
+            return getattr(args[1], _REFLECTED[name])(args[0])
+        is_q = lambda v: isinstance(v, QArrayImpl)
+        unwrap = lambda v: v.astype(torch.float32) if is_q(v) else v
+        return func(*pytree.tree_map(unwrap, args, is_leaf=is_q), **pytree.tree_map(unwrap, kwargs, is_leaf=is_q))
+
+    @property
+    def shape(self):
+        return tuple(self.__value.shape)
+
+    @property
+    def size(self):
+        return self.__value.numel()
+
+    @property
+    def dtype(self):
+        return self.__value.dtype
+
+    @property
+    def tgrid(self):
+        return self.__tgrid
+
+    def _promote(self, other, grid_idx=0):
+        if isinstance(other, QArrayImpl):
+            return other
+        shape = tuple(other.shape) if hasattr(other, "shape") else tuple(torch.as_tensor(other).shape)
+        H, W = _grid_hw(shape)
+        target_a = self.__tgrid[0] if grid_idx == 0 else self.__tgrid[1]
+        target_b = self.__tgrid[1]
+        return QArrayImpl(other, tgrid=(math.gcd(target_a, H), math.gcd(target_b, W)))
+
+    def __matmul__(self, other):
+        other = _value_of(other)
+        if isinstance(other, QArrayImpl):
+            other = self._promote(other, 1)
+            x_out = matmul_impl(self.__value, self.__sc_fp8, self.__sc_fp32, other.__value, other.__sc_fp8,
+                                other.__sc_fp32, self.__tgrid, other.__tgrid)
+            return QArrayImpl(x_out, (self.__tgrid[0], other.__tgrid[1]))
+        return matmul_mixed_impl(self.__value, self.__sc_fp8, self.__sc_fp32, other, self.__tgrid)
+
+    def __rmatmul__(self, other):
+        other = _value_of(other)
+        if isinstance(other, QArrayImpl):
+            other = self._promote(other, 0)
+            x_out = matmul_impl(other.__value, other.__sc_fp8, other.__sc_fp32, self.__value, self.__sc_fp8,
+                                self.__sc_fp32, other.__tgrid, self.__tgrid)
+            return QArrayImpl(x_out, (other.__tgrid[0], self.__tgrid[1]))
+        return rmatmul_mixed_impl(other, self.__value, self.__sc_fp8, self.__sc_fp32, self.__tgrid)
+
+    # -- elementwise arithmetic (Q:121-261) --------------------------------
+    def _binary(self, other, impl, op, reverse=False):
+        other = _value_of(other)
+        if isinstance(other, QArrayImpl):
+            other = self._promote(other)
+            a, b = (other, self) if reverse else (self, other)
+            if self.__tgrid != other.tgrid:
+                return QArrayImpl(op(a.astype(torch.float32), b.astype(torch.float32)), self.__tgrid)
+            x_out = impl(a.__value, a.__sc_fp8, a.__sc_fp32, b.__value, b.__sc_fp8, b.__sc_fp32, self.__tgrid)
+            return QArrayImpl(x_out, self.__tgrid)
+        dt = getattr(other, "dtype", torch.float32)
+        mine = self.astype(dt if isinstance(dt, torch.dtype) else torch.float32)
+        return op(other, mine) if reverse else op(mine, other)
+
+    def __add__(self, other):
+        return self._binary(other, add_impl, operator.add)
+
+    def __radd__(self, other):
+        return self.__add__(_value_of(other))
+
+    def __sub__(self, other):
+        return self._binary(other, sub_impl, operator.sub)
+
+    def __rsub__(self, other):
+        return self._binary(other, sub_impl, operator.sub, reverse=True)
+
+    def __mul__(self, other):
+        return self._binary(other, mul_impl, operator.mul)
+
+    def __rmul__(self, other):
+        return self.__mul__(_value_of(other))
+
+    def __truediv__(self, other):
+        return self._binary(other, truediv_impl, operator.truediv)
+
+    def __rtruediv__(self, other):
+        return self._binary(other, truediv_impl, operator.truediv, reverse=True)
+
+    def __floordiv__(self, other):
+        return self._binary(other, floordiv_impl, operator.floordiv)
+
+    def __rfloordiv__(self, other):
+        return self._binary(other, floordiv_impl, operator.floordiv, reverse=True)
+
+    def __mod__(self, other):
+        return self._binary(other, mod_impl, operator.mod)
+
+    def __rmod__(self, other):
+        return self._binary(other, mod_impl, operator.mod, reverse=True)
+
+    def __pow__(self, other):
+        return self._binary(other, pow_impl, operator.pow)
+
+    def __rpow__(self, other):
+        return self._binary(other, pow_impl, operator.pow, reverse=True)
+
+    # -- views and restructuring (Q:263-402) --------------------------------
+    def __getitem__(self, idx):
+        if not hasattr(self, "_QArrayImpl__tgrid"):
+            return QArrayImpl(self.get_value()[idx], quant=False)
+        sliced = self.dequantize(torch.float32)[idx]
+        return QArrayImpl(sliced, _adapted_grid(self.__tgrid, sliced.shape))
+
+    def __neg__(self):
+        new_obj = QArrayImpl.__new__(QArrayImpl)
+        new_obj._QArrayImpl__tgrid = self.__tgrid
+        new_obj._QArrayImpl__value = self.__value
+        new_obj._QArrayImpl__sc_fp8 = self.__sc_fp8
+        new_obj._QArrayImpl__sc_fp32 = -self.__sc_fp32
+        return new_obj
+
+    def apply(self, func):
+        out_val = func(self.dequantize(torch.float32))
+        return QArrayImpl(out_val, _adapted_grid(self.__tgrid, out_val.shape))
+
+    def __abs__(self):
+        new_obj = QArrayImpl.__new__(QArrayImpl)
+        new_obj._QArrayImpl__tgrid = self.__tgrid
+        # |q| of an e4m3fn byte clears its sign bit (NaN stays NaN)
+        new_obj._QArrayImpl__value = (self.__value.view(torch.uint8) & 0x7F).view(E4M3)
+        new_obj._QArrayImpl__sc_fp8 = self.__sc_fp8
+        new_obj._QArrayImpl__sc_fp32 = self.__sc_fp32.abs()
+        return new_obj
+
+    def __repr__(self):
+        return f"{self.__value}"
+
+    @property
+    def at(self):
+        fp8_array = self
+
+        class _Setter:
+            def __init__(self, idx):
+                self.idx = idx
+
+            def set(self, val):
+                val_f32 = val.astype(torch.float32) if isinstance(val, QArrayImpl) else val
+                out = fp8_array.dequantize(torch.float32).clone()
+                out[self.idx] = val_f32
+                return QArrayImpl(out, fp8_array.tgrid)
+
+        class _Helper:
+            def __getitem__(self, idx):
+                return _Setter(idx)
+
+        return _Helper()
+
+    def astype(self, dtype):
+        if not hasattr(self, "_QArrayImpl__tgrid"):
+            return self.get_value().to(dtype)
+        return self.dequantize(dtype)
+
+    @property
+    def mT(self):
+        return QArrayImpl(self.astype(torch.float32).transpose(-1, -2), (self.__tgrid[1], self.__tgrid[0]))
+
+    @property
+    def T(self):
+        x = self.astype(torch.float32)
+        return QArrayImpl(x.permute(*reversed(range(x.dim()))), (self.__tgrid[1], self.__tgrid[0]))
+
+    def reshape(self, *args, **kwargs):
+        shape = args[0] if len(args) == 1 and isinstance(args[0], (tuple, list)) else args
+        return self._requantize(self.dequantize(torch.float32).reshape(*shape, **kwargs))
+
+    def transpose(self, *axes):
+        axes = axes[0] if len(axes) == 1 and isinstance(axes[0], (tuple, list)) else axes
+        x = self.dequantize(torch.float32)
+        return self._requantize(x.permute(*axes) if axes else x.permute(*reversed(range(x.dim()))))
+
+    def sum(self, *args, **kwargs):
+        if "axis" in kwargs:
+            kwargs["dim"] = kwargs.pop("axis")
+        if "keepdims" in kwargs:
+            kwargs["keepdim"] = kwargs.pop("keepdims")
+        return self._requantize(self.dequantize(torch.float32).sum(*args, **kwargs))
+
+    def _requantize(self, out_val):
+        return QArrayImpl(out_val, _adapted_grid(self.__tgrid, out_val.shape))
+
+    @classmethod
+    def concat(cls, arrays, axis=0):
+        fp32 = [a.astype(torch.float32) if isinstance(a, QArrayImpl) else a for a in arrays]
+        out = torch.cat(fp32, dim=axis)
+        first = next((a for a in arrays if isinstance(a, QArrayImpl)), None)
+        grid = first.tgrid if first else (1, 128)
+        return cls(out, _adapted_grid(grid, out.shape))
+
+    def _tree_flatten(self):
+        if hasattr(self, "_QArrayImpl__tgrid"):
+            return (self.__value, self.__sc_fp8, self.__sc_fp32), (True, self.__tgrid)
+        return (self.__value,), (False, None)
+
+    @classmethod
+    def _tree_unflatten(cls, aux_data, children):
+        is_quant, tgrid = aux_data
+        obj = cls.__new__(cls)
+        if is_quant:
+            obj._QArrayImpl__tgrid = tgrid
+            obj._QArrayImpl__value, obj._QArrayImpl__sc_fp8, obj._QArrayImpl__sc_fp32 = children
+        else:
+            obj._QArrayImpl__value = children[0]
+        return obj
+
+
+pytree.register_pytree_node(
+    QArrayImpl,
+    lambda q: q._tree_flatten(),
+    lambda children, aux: QArrayImpl._tree_unflatten(aux, tuple(children)),
+)
+
+
+# --------------------------------------------------------------------------
+# fp8_matmul (Q:766-793)
+# --------------------------------------------------------------------------
+def _fp8_matmul_value(x, y, tgrid):
+    with torch.no_grad():
+        out = QArrayImpl(x, tgrid) @ QArrayImpl(y, tgrid)
+        return out.dequantize(torch.float32)
+
+
+class _FP8Matmul(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, y, tgrid):
+        ctx.save_for_backward(x, y)
+        ctx.tgrid = tgrid
+        return _fp8_matmul_value(x.detach(), y.detach(), tgrid)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, y = ctx.saved_tensors
+        # Q:777-789: both gradients through the same quantized matmul, with the
+        # raw inputs transposed in f32 and quantized along the transposed axis
+        g_x = _fp8_matmul_value(g, y.transpose(-1, -2), ctx.tgrid) if ctx.needs_input_grad[0] else None
+        g_y = _fp8_matmul_value(x.transpose(-1, -2), g, ctx.tgrid) if ctx.needs_input_grad[1] else None
+        return g_x, g_y, None
+
+
+def fp8_matmul(x_f32, y_f32, tgrid=(1, 16)):
+    """End-to-end differentiable FP8 matrix multiplication (Q:766-793)."""
+    return _FP8Matmul.apply(x_f32, y_f32, tuple(tgrid))

@@ -17,15 +17,15 @@ def to_dev_f32(x: np.ndarray) -> torch.Tensor:
 
 
 def u8(t: torch.Tensor) -> np.ndarray:
-    return t.view(torch.uint8).cpu().numpy()
+    return t.detach().view(torch.uint8).cpu().numpy()
 
 
 def bf16_bits(t: torch.Tensor) -> np.ndarray:
-    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
 def f32(t: torch.Tensor) -> np.ndarray:
-    return t.float().cpu().numpy()
+    return t.detach().float().cpu().numpy()
 
 
 def assert_bytes_equal(got: np.ndarray, want: np.ndarray, what: str) -> None:

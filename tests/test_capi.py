@@ -3,6 +3,7 @@
 CPU-only: no kernel is launched here (no GPU in the build container).
 """
 import ctypes
+import math
 import re
 from pathlib import Path
 
@@ -78,6 +79,7 @@ def test_invalid_tgrid_is_einval_without_launch():
     (2048, 8192, (128, 64, 1, 1024), 64),     # W [2048, 8192] (128,128) rows in dgrad
     (2048, 16384, (1, 1, 2048, 8), 1),        # (128,1) token-axis A [16384, 2048] transposed
     (4096, 16384, (128, 1, 32, 1024), 32),    # FFN down W [16384, 4096] used transposed
+    (1024, 768, (128, 6, 1, 16), 2),          # W [1024, 768] (128,128): groups straddle block rows
 ])
 def test_gemm_group_span(rows, K, desc, expect):
     from pratchya_amd import _lib
@@ -97,12 +99,18 @@ def test_gemm_span_matches_brute_force():
         sk = int(rng.choice([0, 1, 2, 8, rows // rdiv]))
         kg = int(rng.choice([1, 2, 4, 8, 16, 64]))
         P = lib.pratchya_gemm_span(rows, nk * 128, rdiv, sr, sk, kg)
-        if P == 0:
-            continue
+        assert P >= 1
+        changes = set()
         for rb in range(rows // rdiv):
             g = [(rb * sr + kb * sk) // kg for kb in range(nk)]
             for s0 in range(0, nk, P):
                 assert len(set(g[s0:s0 + P])) == 1, (rows, nk, rdiv, sr, sk, kg, P)
+            changes |= {kb for kb in range(1, nk) if g[kb] != g[kb - 1]}
+        # maximal: the gcd of every position where some row's group changes
+        want = 0
+        for kb in changes:
+            want = math.gcd(want, kb)
+        assert P == (want or nk), (rows, nk, rdiv, sr, sk, kg, P, want)
 
 
 def test_quantize_t128_argument_codes_without_gpu():

@@ -110,6 +110,40 @@ def test_dgrad_shape():
     check(C, ref, F32_TOL, "dgrad")
 
 
+def test_dgrad_groups_straddling_block_rows():
+    """W [1024, 768] (128,128): 16-block groups start mid block-row, so rows'
+    group maxima change at different K blocks (span 2)."""
+    K = _K()
+    M_, N_, Ko = 512, 768, 1024
+    g = O.normal_input((M_, N_), 1e-3, seed=14)
+    w = O.normal_input((Ko, N_), 0.02, seed=15)
+    w_f = O.bf16_bits_to_f32(w)
+    w_f[256:384] *= np.float32(64.0)          # a group max that differs from its neighbours'
+    wq = quant_dev(w_f, (128, 128), bf16=False)
+    gq = quant_dev(g, (1, 128))
+    C = K.gemm_nt(K.operand_rows(*gq, (1, 128)), K.operand_rows(*wq, (128, 128)), torch.float32)
+    torch.cuda.synchronize()
+    ref = deq_host(*gq, (1, 128)) @ deq_host(*wq, (128, 128)).T
+    check(C, ref, F32_TOL, "dgrad straddling groups")
+
+
+def test_forward_weight_groups_straddling_block_rows():
+    """x (1,128) @ W [1024, 768] (128,128) used transposed: the weight's
+    16-block groups give its columns group changes at K blocks 3, 5, 6, ...
+    (span 1)."""
+    K = _K()
+    M_, K_, N_ = 512, 1024, 768
+    x = O.activation_input(M_, K_, seed=16)
+    w_f = O.bf16_bits_to_f32(O.normal_input((K_, N_), 0.02, seed=17))
+    w_f[384:512, 256:384] *= np.float32(64.0)
+    xq = quant_dev(x, (1, 128))
+    wq = quant_dev(w_f, (128, 128), bf16=False)
+    C = K.gemm_nt(K.operand_rows(*xq, (1, 128)), K.operand_transposed(*wq, (128, 128)), torch.float32)
+    torch.cuda.synchronize()
+    ref = deq_host(*xq, (1, 128)) @ deq_host(*wq, (128, 128))
+    check(C, ref, F32_TOL, "fwd straddling groups")
+
+
 def test_wgrad_token_axis_groups():
     """A^T dY with both operands quantized (128,1) along tokens: group maxima
     change every K block and every 8 rows/columns."""

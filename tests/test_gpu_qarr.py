@@ -1,0 +1,301 @@
+"""GPU parity of the quantized-array API (pratchya_amd.qarr) against the
+oracle's composition of the reference's steps (pratchya/_qualia/_qarr.py).
+
+Quantize / dequantize / requantize results are bit-exact.  Anything that goes
+through a GEMM is compared by relative Frobenius error (1e-2, the contract's
+bf16 bar): the reference's f32 dot and the MFMA kernel sum in different
+orders, which can move an element of a requantized result across a rounding
+boundary.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import qarr_oracle as O
+from tests.helpers import (assert_bytes_equal, assert_f32_bits_equal, assert_payload_equal, bf16_bits,
+                           f32, to_dev_bf16, to_dev_f32, u8)
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+@pytest.fixture
+def Q():
+    from pratchya_amd import qarr
+    prev = qarr.get_matmul_backward()
+    yield qarr
+    qarr.set_matmul_backward(prev)
+
+
+def oq(x, grid):
+    return O.quantize_impl(np.asarray(x, np.float32), grid)
+
+
+def odq(trip, grid, dtype="float32"):
+    return O.dequantize_impl(*trip, dtype, grid)
+
+
+def triple(q):
+    v, s8, s32 = q._tree_flatten()[0]
+    return u8(v), u8(s8), f32(s32)
+
+
+def assert_triple(q, want, what):
+    got = triple(q)
+    assert_payload_equal(got[0], want[0], f"{what} payload")
+    assert_bytes_equal(got[1], want[1], f"{what} e8m0")
+    assert_f32_bits_equal(got[2], want[2], f"{what} G")
+
+
+def rel(a, b):
+    return O.rel_fro(np.asarray(a, np.float64), np.asarray(b, np.float64))
+
+
+# --------------------------------------------------------------- construction
+def test_construct_and_dequantize_bit_exact(Q):
+    bits = O.activation_input(256, 512, seed=31)
+    x = to_dev_bf16(bits)
+    q = Q.QArrayImpl(x, (1, 128))
+    ref = oq(O.bf16_bits_to_f32(bits), (1, 128))
+    assert_triple(q, ref, "QArrayImpl(x, (1,128))")
+    assert q.shape == (256, 512) and q.size == 256 * 512 and q.tgrid == (1, 128)
+    assert q.dtype == torch.float8_e4m3fn
+    assert_bytes_equal(bf16_bits(q.astype(torch.bfloat16)), odq(ref, (1, 128), "bfloat16"), "astype bf16")
+    assert_f32_bits_equal(f32(q.dequantize(torch.float32)), odq(ref, (1, 128)), "dequantize f32")
+    # copy construction shares the buffers (Q:20-24)
+    q2 = Q.QArrayImpl(q)
+    assert q2.get_value() is q.get_value() and q2.tgrid == q.tgrid
+
+
+def test_three_d_slices(Q):
+    x = np.random.default_rng(1).standard_normal((3, 256, 256)).astype(np.float32)
+    q = Q.QArrayImpl(to_dev_f32(x), (128, 128))
+    assert_triple(q, oq(x, (128, 128)), "3-D")
+
+
+def test_module_functions(Q):
+    x = np.random.default_rng(2).standard_normal((128, 384)).astype(np.float32)
+    t = Q.quantize_impl(to_dev_f32(x), (1, 128))
+    ref = oq(x, (1, 128))
+    assert_payload_equal(u8(t[0]), ref[0], "quantize_impl")
+    y = Q.dequantize_impl(*t, torch.bfloat16, (1, 128))
+    assert_bytes_equal(bf16_bits(y), odq(ref, (1, 128), "bfloat16"), "dequantize_impl")
+
+
+# ------------------------------------------------------------------ Linear
+def _linear_case(seed=7, M=512, Kd=1024, N=768):
+    x = O.activation_input(M, Kd, seed=seed)
+    w = O.normal_input((Kd, N), 0.02, seed=seed + 1)
+    g = O.normal_input((M, N), 1.0, seed=seed + 2)
+    return x, w, g
+
+
+def _linear_reference(xb, wb, gb, out_scales, fp8_bwd=False):
+    """The reference's Linear (M:46-50) on the oracle: forward, and the
+    cotangents of x and W for the output cotangent g.
+
+    The output cotangent reaching the matmul is g * 2^(e-127) * G / 128 with
+    the *output's* block scales (Q:596-599 through Q:518-519), which jump by 2x
+    when an output block's m/G sits at a power of two -- where the f32 dot and
+    the MFMA can round to different sides.  The backward is therefore checked
+    from the output scales the forward under test produced (``out_scales``);
+    the forward is checked on its own."""
+    xq = oq(O.bf16_bits_to_f32(xb), (1, 128))
+    wq = oq(O.bf16_bits_to_f32(wb), (128, 128))
+    xd, wd = odq(xq, (1, 128)).astype(np.float64), odq(wq, (128, 128)).astype(np.float64)
+    out32 = (xd @ wd).astype(np.float32)
+    outq = oq(out32, (1, 128))
+    y = odq(outq, (1, 128), "bfloat16")
+    # dequantize_impl_bwd in g.dtype (bf16), passed through the output quantize
+    o8, o32 = out_scales
+    g1 = O.bf16_bits_to_f32(O.dequantize_bwd(O.bf16_bits_to_f32(gb), o8, o32, (1, 128), "bfloat16"))
+    if fp8_bwd:
+        gd = odq(oq(g1, (1, 128)), (1, 128)).astype(np.float64)
+        gx = gd @ wd.T
+        xt = odq(oq(xd.astype(np.float32), (128, 1)), (128, 1)).astype(np.float64)
+        gt = odq(oq(g1, (128, 1)), (128, 1)).astype(np.float64)
+        gw = xt.T @ gt
+    else:
+        gx = g1.astype(np.float64) @ wd.T
+        gw = xd.T @ g1.astype(np.float64)
+    gx = odq(oq(gx.astype(np.float32), (1, 128)), (1, 128))
+    gw = odq(oq(gw.astype(np.float32), (128, 128)), (128, 128))
+    return y, O.bf16_round(gx), O.bf16_round(gw)
+
+
+@pytest.mark.parametrize("mode", ["f32", "fp8"])
+def test_linear_forward_backward(Q, mode):
+    Q.set_matmul_backward(mode)
+    xb, wb, gb = _linear_case()
+    x = to_dev_bf16(xb).requires_grad_(True)
+    w = to_dev_bf16(wb).requires_grad_(True)
+    W = Q.QArrayImpl(w, (128, 128))
+    out = Q.QArrayImpl(x, (1, 128)) @ W
+    y = out.astype(torch.bfloat16)
+    y.backward(to_dev_bf16(gb))
+    _, o8, o32 = triple(out)
+    y_ref, gx_ref, gw_ref = _linear_reference(xb, wb, gb, (o8, o32), fp8_bwd=(mode == "fp8"))
+    assert y.dtype == torch.bfloat16 and x.grad.dtype == torch.bfloat16
+    assert rel(f32(y), O.bf16_bits_to_f32(y_ref)) <= TOL
+    assert rel(f32(x.grad), gx_ref) <= TOL, rel(f32(x.grad), gx_ref)
+    assert rel(f32(w.grad), gw_ref) <= TOL, rel(f32(w.grad), gw_ref)
+
+
+def test_linear_forward_uses_the_fp8_kernel(Q, monkeypatch):
+    """A (1,128) x (128,128) forward of tile-multiple shape must run the MFMA
+    GEMM, not the dequantize-and-matmul path."""
+    calls = []
+    real = Q.K.gemm_nt
+    monkeypatch.setattr(Q.K, "gemm_nt", lambda *a, **k: calls.append(1) or real(*a, **k))
+    xb, wb, _ = _linear_case(M=256, Kd=256, N=256)
+    Q.QArrayImpl(to_dev_bf16(xb), (1, 128)) @ Q.QArrayImpl(to_dev_bf16(wb), (128, 128))
+    assert calls
+
+
+def test_batched_activation(Q):
+    """[B, T, K] @ W: slices flatten into GEMM rows; W's cotangent sums the batch."""
+    Q.set_matmul_backward("f32")
+    xb = O.activation_input(2 * 256, 256, seed=9).reshape(2, 256, 256)
+    wb = O.normal_input((256, 256), 0.02, seed=10)
+    x = to_dev_bf16(xb).requires_grad_(True)
+    w = to_dev_bf16(wb).requires_grad_(True)
+    out = Q.QArrayImpl(x, (1, 128)) @ Q.QArrayImpl(w, (128, 128))
+    assert out.shape == (2, 256, 256)
+    out.astype(torch.float32).sum().backward()
+    xq = oq(O.bf16_bits_to_f32(xb), (1, 128))
+    wq = oq(O.bf16_bits_to_f32(wb), (128, 128))
+    ref = odq(xq, (1, 128)).astype(np.float64) @ odq(wq, (128, 128)).astype(np.float64)
+    ref = odq(oq(ref.astype(np.float32), (1, 128)), (1, 128))   # the output is requantized (Q:104-105)
+    assert rel(f32(out.astype(torch.float32)), ref) <= TOL
+    assert w.grad is not None and x.grad is not None
+
+
+# -------------------------------------------------------------- mixed / fp8
+def test_mixed_matmuls(Q):
+    x = np.random.default_rng(3).standard_normal((128, 256)).astype(np.float32)
+    y = np.random.default_rng(4).standard_normal((256, 64)).astype(np.float32)
+    q = Q.QArrayImpl(to_dev_f32(x), (1, 128))
+    yd = to_dev_f32(y).requires_grad_(True)
+    out = q @ yd
+    ref = odq(oq(x, (1, 128)), (1, 128)).astype(np.float64) @ y
+    assert rel(f32(out), ref) <= 1e-5
+    out.sum().backward()
+    assert rel(f32(yd.grad), odq(oq(x, (1, 128)), (1, 128)).T @ np.ones((128, 64))) <= 1e-5
+    z = torch.ones((32, 128), device="cuda") @ q          # rmatmul_mixed via __rmatmul__
+    assert tuple(z.shape) == (32, 256)
+
+
+def test_fp8_matmul(Q):
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((256, 256)).astype(np.float32)
+    y = rng.standard_normal((256, 256)).astype(np.float32)
+    g = rng.standard_normal((256, 256)).astype(np.float32)
+    xd = to_dev_f32(x).requires_grad_(True)
+    yd = to_dev_f32(y).requires_grad_(True)
+    out = Q.fp8_matmul(xd, yd, (1, 128))
+
+    def fwd(a, b):
+        p = odq(oq(a, (1, 128)), (1, 128)).astype(np.float64) @ odq(oq(b, (1, 128)), (1, 128)).astype(np.float64)
+        return odq(oq(p.astype(np.float32), (1, 128)), (1, 128))
+
+    assert rel(f32(out), fwd(x, y)) <= TOL
+    out.backward(to_dev_f32(g))
+    assert rel(f32(xd.grad), fwd(g, y.T.copy())) <= TOL
+    assert rel(f32(yd.grad), fwd(x.T.copy(), g)) <= TOL
+
+
+# ------------------------------------------------------------ elementwise
+@pytest.mark.parametrize("opname", ["add", "sub", "mul", "truediv"])
+def test_elementwise_bit_exact(Q, opname):
+    rng = np.random.default_rng(6)
+    a = rng.standard_normal((128, 256)).astype(np.float32)
+    b = rng.standard_normal((128, 256)).astype(np.float32) + np.float32(3.0)
+    qa, qb = Q.QArrayImpl(to_dev_f32(a), (1, 128)), Q.QArrayImpl(to_dev_f32(b), (1, 128))
+    out = {"add": qa + qb, "sub": qa - qb, "mul": qa * qb, "truediv": qa / qb}[opname]
+    da, db = odq(oq(a, (1, 128)), (1, 128)), odq(oq(b, (1, 128)), (1, 128))
+    r = {"add": da + db, "sub": da - db, "mul": da * db, "truediv": da / db}[opname].astype(np.float32)
+    assert_triple(out, oq(r, (1, 128)), opname)
+
+
+def test_elementwise_gradient(Q):
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal((128, 256)).astype(np.float32)
+    b = rng.standard_normal((128, 256)).astype(np.float32)
+    ad, bd = to_dev_f32(a).requires_grad_(True), to_dev_f32(b).requires_grad_(True)
+    (Q.QArrayImpl(ad, (1, 128)) * Q.QArrayImpl(bd, (1, 128))).astype(torch.float32).sum().backward()
+    # d/da = db (dequantized), requantized with the grid and dequantized (Q:750-763, Q:521-526);
+    # the cotangent reaching the product is dequantize_bwd(1) of the product's scales
+    da, db = odq(oq(a, (1, 128)), (1, 128)), odq(oq(b, (1, 128)), (1, 128))
+    prodq = oq((da * db).astype(np.float32), (1, 128))
+    g1 = O.dequantize_bwd(np.ones((128, 256), np.float32), prodq[1], prodq[2], (1, 128))
+    want = odq(oq((g1 * db).astype(np.float32), (1, 128)), (1, 128))
+    assert_f32_bits_equal(f32(ad.grad), want, "grad a")
+
+
+def test_scalar_and_mismatched_grid_ops(Q):
+    a = np.random.default_rng(8).standard_normal((128, 256)).astype(np.float32)
+    qa = Q.QArrayImpl(to_dev_f32(a), (1, 128))
+    da = odq(oq(a, (1, 128)), (1, 128))
+    assert_f32_bits_equal(f32(qa * 2.0), (da * np.float32(2.0)).astype(np.float32), "q * 2")
+    assert_f32_bits_equal(f32(1.0 - qa), (np.float32(1.0) - da).astype(np.float32), "1 - q")
+    qb = Q.QArrayImpl(to_dev_f32(a), (128, 128))
+    out = qa + qb           # different grids: f32 sum requantized with self's grid
+    db = odq(oq(a, (128, 128)), (128, 128))
+    assert_triple(out, oq((da + db).astype(np.float32), (1, 128)), "mismatched grids")
+
+
+# -------------------------------------------------------- views and layout
+def test_neg_abs(Q):
+    a = np.random.default_rng(9).standard_normal((128, 256)).astype(np.float32)
+    qa = Q.QArrayImpl(to_dev_f32(a), (1, 128))
+    da = odq(oq(a, (1, 128)), (1, 128))
+    assert_f32_bits_equal(f32((-qa).astype(torch.float32)), -da, "neg")
+    assert_f32_bits_equal(f32(abs(qa).astype(torch.float32)), np.abs(da), "abs")
+
+
+def test_transpose_reshape_sum_getitem_concat_apply(Q):
+    a = np.random.default_rng(10).standard_normal((256, 128)).astype(np.float32)
+    qa = Q.QArrayImpl(to_dev_f32(a), (1, 128))
+    da = odq(oq(a, (1, 128)), (1, 128))
+    assert qa.T.tgrid == (128, 1)
+    assert_triple(qa.T, oq(da.T.copy(), (128, 1)), ".T")
+    assert_triple(qa.mT, oq(da.T.copy(), (128, 1)), ".mT")
+    assert_triple(qa.reshape(128, 256), oq(da.reshape(128, 256), (1, 128)), "reshape")
+    assert_triple(qa.transpose(1, 0), oq(da.T.copy(), (1, 128)), "transpose")
+    s = qa.sum(axis=0)
+    assert s.tgrid == (1, 128)
+    # the f32 sum's order differs from NumPy's, so compare values, not bytes
+    want = odq(oq(da.sum(axis=0, dtype=np.float64).astype(np.float32), (1, 128)), (1, 128))
+    assert rel(f32(s.astype(torch.float32)), want) <= TOL
+    sl = qa[:64, :64]
+    assert sl.tgrid == (1, 64)
+    assert_triple(sl, oq(da[:64, :64].copy(), (1, 64)), "getitem")
+    cat = Q.QArrayImpl.concat([qa, qa], axis=0)
+    assert_triple(cat, oq(np.concatenate([da, da], 0), (1, 128)), "concat")
+    ap = qa.apply(lambda t: t * 3.0)
+    assert_triple(ap, oq(da * np.float32(3.0), (1, 128)), "apply")
+    upd = qa.at[0, 0].set(5.0)
+    d2 = da.copy()
+    d2[0, 0] = 5.0
+    assert_triple(upd, oq(d2, (1, 128)), "at.set")
+
+
+def test_pytree_round_trip(Q):
+    import torch.utils._pytree as pytree
+    a = np.random.default_rng(11).standard_normal((128, 128)).astype(np.float32)
+    qa = Q.QArrayImpl(to_dev_f32(a), (1, 128))
+    leaves, spec = pytree.tree_flatten({"w": qa})
+    assert len(leaves) == 3
+    back = pytree.tree_unflatten(leaves, spec)["w"]
+    assert back.tgrid == (1, 128) and back.get_value() is qa.get_value()
+    plain = Q.QArrayImpl(torch.ones(4, device="cuda"), quant=False)
+    assert plain._tree_flatten()[1] == (False, None)
+    assert plain[1:3].get_value().shape == (2,)
+
+
+def test_torch_functions_see_dequantized_values(Q):
+    a = np.random.default_rng(12).standard_normal((128, 128)).astype(np.float32)
+    qa = Q.QArrayImpl(to_dev_f32(a), (1, 128))
+    da = odq(oq(a, (1, 128)), (1, 128))
+    assert_f32_bits_equal(f32(torch.relu(qa)), np.maximum(da, 0), "relu(q)")

@@ -154,6 +154,121 @@ def bench_gemm_fwd(steps: int, warmup: int):
     return ms, 2.0 * M * N * Kd / (ms * 1e-3) / 1e12
 
 
+def bench_config4(steps: int, warmup: int):
+    """Config 4, the backward of config 3's Linear: dY bf16 [16384, 8192] ~
+    N(0, 1e-3) (seed 4) requantized (1, 128) for dgrad and (128, 1) along
+    tokens for wgrad; the stored activation A (config 2, (1, 128)) requantized
+    (128, 1) from its fp8 payload; dgrad = q(dY) . W^T -> f32 [16384, 2048],
+    wgrad = q(A)^T . q(dY) -> f32 [2048, 8192].  Each kernel is timed on its
+    own; requant bytes and GEMM FLOPs are the algorithmic counts."""
+    import torch
+    from oracle import qarr_oracle as O
+    from pratchya_amd import _kernels as K
+    T, Din, Dout = 16384, 2048, 8192
+    g = torch.Generator(device="cuda").manual_seed(4)
+    dy = (torch.randn((T, Dout), generator=g, device="cuda") * 1e-3).to(torch.bfloat16)
+    x = torch.from_numpy(O.activation_input(T, Din, seed=2).view(np.int16)).view(torch.bfloat16).cuda()
+    w = torch.from_numpy(O.normal_input((Din, Dout), 0.02, seed=3).view(np.int16)).view(torch.bfloat16).cuda()
+    a8 = K.quantize(x, (1, 128))
+    wq = K.quantize(w, (128, 128))
+    op_w = K.operand_rows(*wq, (128, 128))               # W [2048, 8192]: rows Din, contraction Dout
+    dyq = K.quantize(dy, (1, 128))
+    dyt = K.quantize_t128(dy)
+    at = K.quantize_t128(*a8)
+    op_dy, op_dyt, op_at = K.operand_rows(*dyq, (1, 128)), K.operand_t128(*dyt), K.operand_t128(*at)
+    gx = torch.empty((T, Din), dtype=torch.float32, device="cuda")
+    gw = torch.empty((Din, Dout), dtype=torch.float32, device="cuda")
+    # outputs written in place; the 33 MB activation rotates through 8 copies
+    # (> the 256 MB MALL together with their outputs)
+    n_a = 8
+    a_sets = [tuple(t.clone() for t in a8) for _ in range(n_a)]
+    at_outs = [tuple(torch.empty_like(t) for t in at) for _ in range(n_a)]
+    dyq_out = tuple(torch.empty_like(t) for t in dyq)
+    dyt_out = tuple(torch.empty_like(t) for t in dyt)
+    res = {}
+    e_dy, e_a = T * Dout, T * Din
+    cases = [
+        ("requant_dy_1x128", lambda i: K.quantize(dy, (1, 128), out=dyq_out),
+         e_dy * 3 + e_dy // 128 + e_dy // 1024 * 4),
+        ("requant_dy_128x1_t", lambda i: K.quantize_t128(dy, out=dyt_out),
+         e_dy * 3 + e_dy // 128 + e_dy // 1024 * 4),
+        ("requant_a_fp8_to_128x1_t", lambda i: K.quantize_t128(*a_sets[i % n_a], out=at_outs[i % n_a]),
+         e_a * 2 + 2 * (e_a // 128 + e_a // 1024 * 4)),
+    ]
+    for name, fn, nbytes in cases:
+        _log(f"config 4 {name}: start")
+        ms, _ = timed_graph(fn, steps, warmup)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                     "bytes": nbytes}
+    flop = 2 * T * Din * Dout
+    for name, fn in (("dgrad_gemm", lambda i: K.gemm_nt(op_dy, op_w, out=gx)),
+                     ("wgrad_gemm", lambda i: K.gemm_nt(op_at, op_dyt, out=gw))):
+        _log(f"config 4 {name}: start")
+        ms, _ = timed_graph(fn, max(8, steps // 4), max(2, warmup // 4))
+        tf = flop / (ms * 1e-3) / 1e12
+        res[name] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1), "frac_of_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4),
+                     "flop": flop}
+    return res
+
+
+CFG5_TOKENS, CFG5_D, CFG5_F = 32768, 4096, 16384
+CFG5_LINEARS = [(CFG5_D, CFG5_D)] * 4 + [(CFG5_D, CFG5_F), (CFG5_F, CFG5_D)]   # r, k, v, o, FFN up, down
+CFG5_FLOP = 3 * 2 * CFG5_TOKENS * sum(a * b for a, b in CFG5_LINEARS)
+
+
+def bench_config5(steps: int, warmup: int):
+    """Config 5: the six quantized linears of one RWKV-7 block at d_model 4096
+    (r/k/v/o [4096, 4096], FFN [4096, 16384] and [16384, 4096]) over 32768
+    tokens (batch 8 x seq 4096): forward, dgrad and wgrad of each through the
+    quantized-array API exactly as the reference's Linear composes them
+    (x quantized (1, 128), W (128, 128), output requantized and dequantized to
+    bf16, cotangents requantized), with the FP8 MFMA backward.  Synthetic bf16
+    activations N(0, 1), weights N(0, 0.02), output cotangents N(0, 1e-3),
+    seed 5.  A step is one layer's fwd + bwd; reported as tokens/s."""
+    import torch
+    from pratchya_amd import qarr as Q
+    prev = Q.get_matmul_backward()
+    Q.set_matmul_backward("fp8")
+    try:
+        gen = torch.Generator(device="cuda").manual_seed(5)
+        xs = {n: torch.randn((CFG5_TOKENS, n), generator=gen, device="cuda").to(torch.bfloat16)
+              for n in (CFG5_D, CFG5_F)}
+        ws, wqs, gs = [], [], []
+        for din, dout in CFG5_LINEARS:
+            w = (torch.randn((din, dout), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+            w.requires_grad_(True)
+            ws.append(w)
+            wqs.append(Q.QArrayImpl(w, (128, 128)))        # quantized once per optimizer step
+            gs.append((torch.randn((CFG5_TOKENS, dout), generator=gen, device="cuda") * 1e-3).to(torch.bfloat16))
+
+        def layer_step():
+            for (din, _), wq, w, g in zip(CFG5_LINEARS, wqs, ws, gs):
+                x = xs[din].detach().requires_grad_(True)
+                y = (Q.QArrayImpl(x, (1, 128)) @ wq).astype(torch.bfloat16)
+                y.backward(g)
+                w.grad = None
+
+        for _ in range(max(1, warmup)):
+            layer_step()
+        torch.cuda.synchronize()
+        st = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(steps):
+            layer_step()
+        e1.record(st)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+    finally:
+        Q.set_matmul_backward(prev)
+    tf = CFG5_FLOP / (ms * 1e-3) / 1e12
+    return {"tokens_per_s": round(CFG5_TOKENS / (ms * 1e-3), 1), "ms_per_layer_step": round(ms, 3),
+            "effective_TFLOP/s": round(tf, 1), "frac_of_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4),
+            "gemm_flop_per_step": CFG5_FLOP, "steps": steps,
+            "path": "pratchya_amd.qarr Linear composition, fp8 backward, eager (no graph)"}
+
+
 COPY_BYTES = 256 << 20   # bytes read (and written) by the reference copy of the counter runs
 
 
@@ -241,6 +356,11 @@ def main():
                                      "frac_of_fp8_peak": round(tflops / FP8_PEAK_TFLOPS, 4),
                                      "shape": "[16384,2048] x [2048,8192] -> bf16",
                                      "flop": 2 * 16384 * 2048 * 8192}
+        _log("config 4: start")
+        extra["config4_backward"] = bench_config4(max(20, args.steps // 4), max(4, args.warmup // 4))
+        _log("config 5: start")
+        extra["config5_layer"] = bench_config5(max(3, args.steps // 40), 2)
+        _log(f"config 5: {extra['config5_layer']['tokens_per_s']} tokens/s")
     cpu = None
     if not args.no_cpu_baseline:
         _log("cpu baseline: start")

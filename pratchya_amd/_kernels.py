@@ -68,11 +68,25 @@ def _aligned(t: torch.Tensor, n: int) -> bool:
     return t.data_ptr() % n == 0
 
 
-def quantize(x: torch.Tensor, tgrid) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+def _check_out(out, shapes, what):
+    """Caller-provided output buffers: contiguous, on the device, of the right
+    byte sizes (dtype views of uint8 / e4m3fn / e8m0 and f32 are accepted)."""
+    if len(out) != len(shapes):
+        raise ValueError(f"{what}: expected {len(shapes)} output buffers")
+    for t, (shape, esz) in zip(out, shapes):
+        n = 1
+        for d in shape:
+            n *= int(d)
+        if not t.is_cuda or not t.is_contiguous() or t.numel() * t.element_size() != n * esz:
+            raise ValueError(f"{what}: output buffer of {tuple(t.shape)} {t.dtype} does not fit {shape}")
+
+
+def quantize(x: torch.Tensor, tgrid, out=None) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Quantize ``x`` (bf16 or f32) with block grid ``tgrid``.
 
     Returns ``(x_fp8 [x.shape] e4m3fn, sc_fp8 [..., M, K] e8m0, sc_fp32
-    [..., M, 1, 1] f32)`` exactly as pratchya/_qualia/_qarr.py:506.
+    [..., M, 1, 1] f32)`` exactly as pratchya/_qualia/_qarr.py:506.  ``out``
+    may hold preallocated (payload, e8m0, f32) buffers to write instead.
     """
     _require_gpu(x)
     if x.dtype not in (torch.float32, torch.bfloat16):
@@ -83,15 +97,19 @@ def quantize(x: torch.Tensor, tgrid) -> Tuple[torch.Tensor, torch.Tensor, torch.
     lead = tuple(x.shape[:-2]) if x.dim() >= 2 else ()
     if not x.is_contiguous() or not _aligned(x, 16):
         x = x.contiguous() if not x.is_contiguous() else x.clone()
-    x8 = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
-    sc8 = torch.empty(lead + (M, K), dtype=torch.uint8, device=x.device)
-    sc32 = torch.empty(lead + (M, 1, 1), dtype=torch.float32, device=x.device)
+    if out is None:
+        x8 = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+        sc8 = torch.empty(lead + (M, K), dtype=torch.uint8, device=x.device)
+        sc32 = torch.empty(lead + (M, 1, 1), dtype=torch.float32, device=x.device)
+    else:
+        _check_out(out, [(x.shape, 1), (lead + (M, K), 1), (lead + (M, 1, 1), 4)], "quantize")
+        x8, sc8, sc32 = _u8(out[0]), _u8(out[1]), out[2]
     lib = _lib.load()
     code = _dtype_code(x.dtype)
     ws_bytes = lib.pratchya_quantize_workspace_bytes(code, S, H, W, a, b)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device) if ws_bytes else None
     _lib.check(lib.pratchya_quantize(_ptr(x), code, S, H, W, a, b, _ptr(x8), _ptr(sc8), _ptr(sc32),
-                                     _ptr(ws), ws_bytes, _stream(x)), "quantize")
+                                     _ptr(ws) if ws is not None else None, ws_bytes, _stream(x)), "quantize")
     return x8.view(E4M3), sc8.view(E8M0), sc32
 
 
@@ -99,7 +117,7 @@ def _u8(t: torch.Tensor) -> torch.Tensor:
     return t.view(torch.uint8) if t.dtype != torch.uint8 else t
 
 
-def quantize_t128(x: torch.Tensor, x_sc8: torch.Tensor = None, x_sc32: torch.Tensor = None):
+def quantize_t128(x: torch.Tensor, x_sc8: torch.Tensor = None, x_sc32: torch.Tensor = None, out=None):
     """``quantize_impl(x, (128, 1))`` (pratchya/_qualia/_qarr.py:458-506) with
     the payload transposed per slice.
 
@@ -108,7 +126,7 @@ def quantize_t128(x: torch.Tensor, x_sc8: torch.Tensor = None, x_sc32: torch.Ten
     as ``dequantize_impl`` does).  Returns ``(xt_fp8 [..., C, T] e4m3fn,
     sc_fp8 [..., M, 8] e8m0, sc_fp32 [..., M, 1, 1] f32)``: the scales are
     exactly ``quantize_impl(x, (128, 1))``'s, the payload is its payload with
-    the last two axes swapped.
+    the last two axes swapped.  ``out`` may hold preallocated buffers.
     """
     _require_gpu(x)
     if x.dim() < 2:
@@ -131,9 +149,13 @@ def quantize_t128(x: torch.Tensor, x_sc8: torch.Tensor = None, x_sc32: torch.Ten
     if not xin.is_contiguous() or not _aligned(xin, 16):
         xin = xin.contiguous() if not xin.is_contiguous() else xin.clone()
     _, K, M = group_layout(T, C, (128, 1))
-    xt = torch.empty(lead + (C, T), dtype=torch.uint8, device=x.device)
-    sc8 = torch.empty(lead + (M, K), dtype=torch.uint8, device=x.device)
-    sc32 = torch.empty(lead + (M, 1, 1), dtype=torch.float32, device=x.device)
+    if out is None:
+        xt = torch.empty(lead + (C, T), dtype=torch.uint8, device=x.device)
+        sc8 = torch.empty(lead + (M, K), dtype=torch.uint8, device=x.device)
+        sc32 = torch.empty(lead + (M, 1, 1), dtype=torch.float32, device=x.device)
+    else:
+        _check_out(out, [(lead + (C, T), 1), (lead + (M, K), 1), (lead + (M, 1, 1), 4)], "quantize_t128")
+        xt, sc8, sc32 = _u8(out[0]), _u8(out[1]), out[2]
     lib = _lib.load()
     _lib.check(lib.pratchya_quantize_t128(_ptr(xin), code,
                                           _ptr(xs8) if xs8 is not None else None,

@@ -292,20 +292,21 @@ __global__ __launch_bounds__(256) void k_quant_g8(const void* __restrict__ xv,
                                  elem_f32<IS_BF16>(v[r], 4 * j + 2) * y[r],
                                  elem_f32<IS_BF16>(v[r], 4 * j + 3) * y[r]);
       } else {
-        uint32_t near = 0;
+        // every element checked; a 4-element word with one close to a bf16
+        // rounding midpoint is recast with IEEE division (rare; the other
+        // lanes and words keep the fast result)
 #pragma unroll
         for (int r = 0; r < R; ++r) {
 #pragma unroll
           for (int j = 0; j < VEC / 4; ++j) {
-            const float t0 = elem_f32<IS_BF16>(v[r], 4 * j + 0) * y[r];
-            const float t1 = elem_f32<IS_BF16>(v[r], 4 * j + 1) * y[r];
-            const float t2 = elem_f32<IS_BF16>(v[r], 4 * j + 2) * y[r];
-            const float t3 = elem_f32<IS_BF16>(v[r], 4 * j + 3) * y[r];
-            near |= near_mid8(t0) | near_mid8(t1) | near_mid8(t2) | near_mid8(t3);
+            const float x0 = elem_f32<IS_BF16>(v[r], 4 * j + 0), x1 = elem_f32<IS_BF16>(v[r], 4 * j + 1);
+            const float x2 = elem_f32<IS_BF16>(v[r], 4 * j + 2), x3 = elem_f32<IS_BF16>(v[r], 4 * j + 3);
+            const float t0 = x0 * y[r], t1 = x1 * y[r], t2 = x2 * y[r], t3 = x3 * y[r];
             out[r][j] = cvt4<HW>(t0, t1, t2, t3);
+            if (near_mid8(t0) | near_mid8(t1) | near_mid8(t2) | near_mid8(t3))
+              out[r][j] = cvt4_exact(x0, x1, x2, x3, quant_scale(e[r], G));
           }
         }
-        exact = __any(near);
       }
     }
     if (exact) {

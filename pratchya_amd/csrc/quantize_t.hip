@@ -20,10 +20,13 @@
 // across rs, the group max an in-lane max over 8 channels, and each channel's
 // 16 payload bytes are one 16-byte store into the transposed layout.  The cast
 // uses the same division-free scheme as the row-group quantizer (exact for
-// bf16 inputs; f32 inputs and clamped blocks check the bf16 rounding midpoint
-// and redo the tile with IEEE division when any element is close).
+// bf16 inputs; for f32 / fp8 inputs and clamped blocks every element is
+// checked against the bf16 rounding midpoint, and a lane's 16-element chunk
+// holding a close one is recast with IEEE division).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "fp8_math.h"
 #include "pratchya_fp8.h"
@@ -35,6 +38,16 @@ namespace {
 
 constexpr int TOK = 16;                     // consecutive tokens per lane
 enum { IN_F32 = 0, IN_BF16 = 1, IN_FP8 = 2 };
+
+// Calls f(std::integral_constant<int, i>) for i = 0 .. N-1 (compile-time
+// channel indices, so per-channel helpers can take them as template arguments).
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
+  }
+}
 
 template <int IN>
 struct InTraits {
@@ -59,58 +72,55 @@ __device__ __forceinline__ void load_row(const uint8_t* p, uint32_t (&w)[InTrait
   }
 }
 
+// Two e4m3fn bytes of a word (bytes 0,1 or 2,3) -> f32, with gfx950's
+// v_cvt_scalef32_pk_f32_fp8 at scale 1.0 (OCP e4m3fn; exact for every byte,
+// which the tests check byte by byte through the requantize).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+template <int HALF>
+__device__ __forceinline__ f32x2_t fp8_pair(uint32_t word) {
+  return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, 1.0f, HALF != 0);
+}
+
+template <int J>
+__device__ __forceinline__ float fp8_elem(uint32_t word) {
+  const f32x2_t p = fp8_pair<(J >> 1) & 1>(word);
+  return (J & 1) ? p.y : p.x;
+}
+
 // |channel j| of a row as f32 bits, from the raw bits (a different
 // expression from row_elem's, so the compiler does not keep 128 widened
 // values alive from the maxima to the cast).
-template <int IN>
-__device__ __forceinline__ uint32_t row_abs_bits(const uint32_t (&w)[InTraits<IN>::NW], int j, float dq) {
+template <int IN, int J>
+__device__ __forceinline__ uint32_t row_abs_bits(const uint32_t (&w)[InTraits<IN>::NW], float dq) {
   if constexpr (IN == IN_F32) {
-    return w[j] & 0x7FFFFFFFu;
+    return w[J] & 0x7FFFFFFFu;
   } else if constexpr (IN == IN_BF16) {
-    const uint32_t word = w[j >> 1];
-    return ((j & 1) ? (word >> 16) : word) << 16 & 0x7FFF0000u;
+    const uint32_t word = w[J >> 1];
+    return ((J & 1) ? (word >> 16) : word) << 16 & 0x7FFF0000u;
   } else {
-    const float q = e4m3fn_to_f32((w[j >> 2] >> (8 * (j & 3))) & 0x7Fu);
+    const float q = fp8_elem<J>(w[J >> 2] & 0x7F7F7F7Fu);   // |q|: sign bits cleared
     return f2u((q * dq) * 0.0078125f) & 0x7FFFFFFFu;
   }
 }
 
-// Channel j of a row as f32 (fp8: dequantized with the row's scale dq).
-template <int IN>
-__device__ __forceinline__ float row_elem(const uint32_t (&w)[InTraits<IN>::NW], int j, float dq) {
+// Channel J of a row as f32 (fp8: dequantized with the row's scale dq, in
+// dequantize_impl's order: (q * (2^(e-127) * G)) / 128).
+template <int IN, int J>
+__device__ __forceinline__ float row_elem(const uint32_t (&w)[InTraits<IN>::NW], float dq) {
   if constexpr (IN == IN_F32) {
-    return u2f(w[j]);
+    return u2f(w[J]);
   } else if constexpr (IN == IN_BF16) {
-    const uint32_t word = w[j >> 1];
-    return u2f((j & 1) ? (word & 0xFFFF0000u) : (word << 16));
+    const uint32_t word = w[J >> 1];
+    return u2f((J & 1) ? (word & 0xFFFF0000u) : (word << 16));
   } else {
-    const float q = e4m3fn_to_f32((w[j >> 2] >> (8 * (j & 3))) & 0xFFu);
-    return (q * dq) * 0.0078125f;
-  }
-}
-
-// Element (t, c) of slice s read back from memory (the rare exact path,
-// which must not keep the tile's registers alive).
-template <int IN>
-__device__ __forceinline__ float elem_at(const uint8_t* x, const uint8_t* x_sc8, const float* x_sc32,
-                                         int64_t x_kg, int64_t T, int64_t C, int64_t s, int64_t t,
-                                         int64_t c) {
-  const int64_t i = (s * T + t) * C + c;
-  if constexpr (IN == IN_F32) {
-    return reinterpret_cast<const float*>(x)[i];
-  } else if constexpr (IN == IN_BF16) {
-    return u2f((uint32_t)reinterpret_cast<const uint16_t*>(x)[i] << 16);
-  } else {
-    const int64_t nbr = C / 128, nb_in = T * nbr, blk = t * nbr + c / 128;
-    const float dq = e8m0_decode(x_sc8[s * nb_in + blk]) * x_sc32[s * (nb_in / x_kg) + blk / x_kg];
-    return (e4m3fn_to_f32(x[i]) * dq) * 0.0078125f;
+    return (fp8_elem<J>(w[J >> 2]) * dq) * 0.0078125f;
   }
 }
 
 template <int IN, bool HW>
 __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ x,
                                                     const uint8_t* __restrict__ x_sc8,
-                                                    const float* __restrict__ x_sc32, int64_t x_kg,
+                                                    const float* __restrict__ x_sc32, int kg_shift,
                                                     int64_t T, int64_t C, uint8_t* __restrict__ qt,
                                                     uint8_t* __restrict__ sc8,
                                                     float* __restrict__ sc32) {
@@ -134,93 +144,82 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
 #pragma unroll
   for (int r = 0; r < TOK; ++r) dq[r] = 1.0f;
   if constexpr (IN == IN_FP8) {
-    // (1, 128) scales of the stored payload: block (t, c / 128) of the slice
-    const int64_t nbr = C / 128, nb_in = T * nbr;
+    // (1, 128) scales of the stored payload: block (t, c / 128) of the slice;
+    // a slice holds a whole number of groups (kg | T * C / 128), so the group
+    // of a block is its slice-global index >> kg_shift.  32-bit indices: the
+    // host checks slices * T * C / 128 < 2^32.
+    const uint32_t nbr = (uint32_t)(C >> 7);
+    const uint32_t b0 = (uint32_t)(s * T + t0) * nbr + (uint32_t)(c0 >> 7);
 #pragma unroll
     for (int r = 0; r < TOK; ++r) {
-      const int64_t blk = (t0 + r) * nbr + c0 / 128;
-      dq[r] = e8m0_decode(x_sc8[s * nb_in + blk]) * x_sc32[s * (nb_in / x_kg) + blk / x_kg];
+      const uint32_t blk = b0 + (uint32_t)r * nbr;
+      dq[r] = e8m0_decode(x_sc8[blk]) * x_sc32[blk >> kg_shift];
     }
   }
 
   // channel maxima (as |x| bits: unsigned order, NaN above inf) and group max
   uint32_t mx[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  static_for<8>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
     uint32_t m = 0;
 #pragma unroll
-    for (int r = 0; r < TOK; ++r) m = umax(m, row_abs_bits<IN>(w[r], j, dq[r]));
+    for (int r = 0; r < TOK; ++r) m = umax(m, row_abs_bits<IN, j>(w[r], dq[r]));
     m = umax(m, shfl_xor_u32(m, 8));
     m = umax(m, shfl_xor_u32(m, 16));
     m = umax(m, shfl_xor_u32(m, 32));
     mx[j] = m;
-  }
+  });
   uint32_t Gb = 0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) Gb = umax(Gb, mx[j]);
   const float G = u2f(Gb);
   const bool G_finite = (Gb >> 23) < 255u;
 
-  // e8m0 bytes, y ~ 128 / S per channel, and the division-free cast of the
-  // tile into registers.  If any group of the wave has a non-finite G, or
-  // (f32 / fp8 inputs, clamped blocks) any element lands within 8 ulp of a bf16
-  // rounding midpoint after the multiply, the wave redoes the cast with IEEE
-  // division instead (rare; it re-reads its elements from memory).
+  // e8m0 bytes and y ~ 128 / S per channel; then the division-free cast,
+  // chunk by chunk (channel j, this lane's 16 tokens).  A chunk is recast with
+  // IEEE division when its group's G is not finite, or (f32 / fp8 inputs,
+  // clamped blocks) one of its elements lands within 8 ulp of a bf16 rounding
+  // midpoint after the multiply -- rare, and only that chunk pays for it.
   uint32_t e[8];
-  uint32_t out[8][TOK / 4];
-  uint32_t redo = G_finite ? 0u : 1u;
-  {
-    const float rcpG128 = __builtin_amdgcn_rcpf(G * 0.0078125f);
-    uint32_t clamped = 0;
-    float y[8];
+  float y[8];
+  const float rcpG128 = __builtin_amdgcn_rcpf(G * 0.0078125f);
+  uint32_t clamped = 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      e[j] = e8m0_of(u2f(mx[j]), G);
-      const float sG = e8m0_decode(e[j]) * G;
-      const bool cl = !(sG >= kClamp);
-      y[j] = cl ? PRATCHYA_Y_CLAMP : u2f((254u - e[j]) << 23) * rcpG128;
-      clamped |= cl ? 1u : 0u;
-    }
-    const bool check = IN != IN_BF16 || __any(clamped);
-    uint32_t near = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int k = 0; k < TOK / 4; ++k) {
-        const float t0v = row_elem<IN>(w[4 * k + 0], j, dq[4 * k + 0]) * y[j];
-        const float t1v = row_elem<IN>(w[4 * k + 1], j, dq[4 * k + 1]) * y[j];
-        const float t2v = row_elem<IN>(w[4 * k + 2], j, dq[4 * k + 2]) * y[j];
-        const float t3v = row_elem<IN>(w[4 * k + 3], j, dq[4 * k + 3]) * y[j];
-        if (check) near |= near_mid8(t0v) | near_mid8(t1v) | near_mid8(t2v) | near_mid8(t3v);
-        out[j][k] = cvt4<HW>(t0v, t1v, t2v, t3v);
-      }
-    redo |= near;
+  for (int j = 0; j < 8; ++j) {
+    e[j] = e8m0_of(u2f(mx[j]), G);
+    const float sG = e8m0_decode(e[j]) * G;
+    const bool cl = !(sG >= kClamp);
+    y[j] = cl ? PRATCHYA_Y_CLAMP : u2f((254u - e[j]) << 23) * rcpG128;
+    clamped |= cl ? 1u : 0u;
   }
+  const bool check = IN != IN_BF16 || __any(clamped);
 
   uint8_t* qo = qt + (s * C + c0) * T + t0;
-  if (__any(redo)) {
-#pragma nounroll
-    for (int j = 0; j < 8; ++j) {
-      const float S = quant_scale(e[j], G);
-#pragma nounroll
-      for (int k = 0; k < TOK / 4; ++k) {
-        uint32_t word = 0;
-#pragma nounroll
-        for (int i = 0; i < 4; ++i) {
-          const float v = elem_at<IN>(x, x_sc8, x_sc32, x_kg, T, C, s, t0 + 4 * k + i, c0 + j);
-          word |= quant_elem_exact(v, S) << (8 * i);
-        }
-        *reinterpret_cast<uint32_t*>(qo + (int64_t)j * T + 4 * k) = word;
-      }
-    }
-  } else {
-    // payload: channel c0 + j, tokens [t0, t0 + 16) of slice s in [C, T]
+  static_for<8>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    uint32_t o[TOK / 4];
+    uint32_t near = 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const u32x4_t v = {out[j][0], out[j][1], out[j][2], out[j][3]};
-      __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(qo + (int64_t)j * T));
+    for (int k = 0; k < TOK / 4; ++k) {
+      const float t0v = row_elem<IN, j>(w[4 * k + 0], dq[4 * k + 0]) * y[j];
+      const float t1v = row_elem<IN, j>(w[4 * k + 1], dq[4 * k + 1]) * y[j];
+      const float t2v = row_elem<IN, j>(w[4 * k + 2], dq[4 * k + 2]) * y[j];
+      const float t3v = row_elem<IN, j>(w[4 * k + 3], dq[4 * k + 3]) * y[j];
+      if (check) near |= near_mid8(t0v) | near_mid8(t1v) | near_mid8(t2v) | near_mid8(t3v);
+      o[k] = cvt4<HW>(t0v, t1v, t2v, t3v);
     }
-  }
+    if (near || !G_finite) {
+      const float S = quant_scale(e[j], G);
+#pragma unroll
+      for (int k = 0; k < TOK / 4; ++k)
+        o[k] = cvt4_exact(row_elem<IN, j>(w[4 * k + 0], dq[4 * k + 0]),
+                          row_elem<IN, j>(w[4 * k + 1], dq[4 * k + 1]),
+                          row_elem<IN, j>(w[4 * k + 2], dq[4 * k + 2]),
+                          row_elem<IN, j>(w[4 * k + 3], dq[4 * k + 3]), S);
+    }
+    const u32x4_t v = {o[0], o[1], o[2], o[3]};
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(qo + (int64_t)j * T));
+  });
   if (rs == 0) {
     // blocks (tb, c0 .. c0 + 7) are consecutive; they form group (tb*C + c0) / 8
     const int64_t nb = (T / 128) * C;
@@ -268,18 +267,22 @@ extern "C" int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t*
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t128: buffers are not aligned");
   if (T / 128 > 65535 || slices > 65535)
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t128: too many token blocks or slices");
+  if (x_dtype == PRATCHYA_DT_E4M3 && (slices * T) * (C / 128) >= ((int64_t)1 << 32))
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t128: fp8 input scales beyond 2^32 blocks");
   const dim3 grid((unsigned)((C + 255) / 256), (unsigned)(T / 128), (unsigned)slices);
   const uint8_t* xb = static_cast<const uint8_t*>(x);
   if (x_dtype == PRATCHYA_DT_BF16) {
-    hipLaunchKernelGGL((k_quant_t128<IN_BF16, true>), grid, dim3(256), 0, stream, xb, nullptr, nullptr,
-                       (int64_t)1, T, C, xt_fp8, sc_fp8, sc_fp32);
+    hipLaunchKernelGGL((k_quant_t128<IN_BF16, true>), grid, dim3(256), 0, stream, xb, nullptr, nullptr, 0,
+                       T, C, xt_fp8, sc_fp8, sc_fp32);
   } else if (x_dtype == PRATCHYA_DT_F32) {
-    hipLaunchKernelGGL((k_quant_t128<IN_F32, true>), grid, dim3(256), 0, stream, xb, nullptr, nullptr,
-                       (int64_t)1, T, C, xt_fp8, sc_fp8, sc_fp32);
+    hipLaunchKernelGGL((k_quant_t128<IN_F32, true>), grid, dim3(256), 0, stream, xb, nullptr, nullptr, 0,
+                       T, C, xt_fp8, sc_fp8, sc_fp32);
   } else {
-    const int64_t kg = gcd64(8, T * (C / 128));   // blocks per group of the (1, 128) input
-    hipLaunchKernelGGL((k_quant_t128<IN_FP8, true>), grid, dim3(256), 0, stream, xb, x_sc8, x_sc32, kg, T,
-                       C, xt_fp8, sc_fp8, sc_fp32);
+    // blocks per group of the (1, 128) input: gcd(8, n_blk), a power of two
+    const int64_t kg = gcd64(8, T * (C / 128));
+    const int kg_shift = kg == 8 ? 3 : (kg == 4 ? 2 : (kg == 2 ? 1 : 0));
+    hipLaunchKernelGGL((k_quant_t128<IN_FP8, true>), grid, dim3(256), 0, stream, xb, x_sc8, x_sc32, kg_shift,
+                       T, C, xt_fp8, sc_fp8, sc_fp32);
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess)

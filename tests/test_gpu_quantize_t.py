@@ -99,6 +99,26 @@ def test_fp8_input_requantized_along_tokens(T, C):
     check(dev8, deq, f"fp8 [{T},{C}]", torch.from_numpy(s8).cuda(), torch.from_numpy(s32).cuda())
 
 
+def test_fp8_input_every_payload_byte():
+    """Every finite e4m3fn byte (normals, subnormals, zeros of both signs) as
+    the stored payload, under several block scales; then the NaN bytes."""
+    T, C = 256, 256
+    rng = np.random.default_rng(22)
+    finite = np.array([b for b in range(256) if (b & 0x7F) != 0x7F], dtype=np.uint8)
+    x8 = rng.choice(finite, size=(T, C)).astype(np.uint8)
+    x8[:2, :] = np.resize(finite, (2, C))            # each byte at least once
+    n_blk = T * C // 128
+    s8 = rng.integers(100, 140, size=(n_blk // 8, 8)).astype(np.uint8)
+    s32 = rng.uniform(0.5, 4.0, size=(n_blk // 8, 1, 1)).astype(np.float32)
+    deq = O.dequantize_impl(x8, s8, s32, "float32", (1, 128))
+    dev = [torch.from_numpy(a).cuda() for a in (x8, s8, s32)]
+    check(dev[0], deq, "fp8 every byte", dev[1], dev[2])
+    x8n = x8.copy()
+    x8n[5, 7], x8n[130, 200] = 0x7F, 0xFF
+    deqn = O.dequantize_impl(x8n, s8, s32, "float32", (1, 128))
+    check(torch.from_numpy(x8n).cuda(), deqn, "fp8 NaN bytes", dev[1], dev[2])
+
+
 def test_config4_dy_full_size_sampled_token_blocks():
     """Config 4: dY bf16 [16384, 8192] ~ N(0, 1e-3), requantized (128, 1).  The
     full tensor goes through the kernel; token blocks are independent under

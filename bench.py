@@ -329,6 +329,8 @@ def main():
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--counter-workload", action="store_true",
                     help="only run the direct-launch workload used for rocprofv3 --pmc runs")
+    ap.add_argument("--only", choices=["cfg3", "cfg4", "cfg5"], default=None,
+                    help="run one secondary configuration alone (for profiling) and print its result")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -342,6 +344,16 @@ def main():
     _log(f"device {torch.cuda.get_device_name(0)}")
     if args.counter_workload:
         counter_workload()
+        return
+    if args.only:
+        if args.only == "cfg3":
+            ms_, tf_ = bench_gemm_fwd(max(8, args.steps // 4), max(4, args.warmup // 4))
+            res = {"ms": ms_, "TFLOP/s": tf_}
+        elif args.only == "cfg4":
+            res = bench_config4(max(20, args.steps // 4), max(4, args.warmup // 4))
+        else:
+            res = bench_config5(max(3, args.steps // 40), 2)
+        print(json.dumps({args.only: res}), flush=True)
         return
     _log("config 2 quantize: start")
     ms, wall, ok = bench_quantize(args.steps, args.warmup)

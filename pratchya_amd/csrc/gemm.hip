@@ -104,6 +104,15 @@ __device__ __forceinline__ void mfma_tile(v16f (&acc)[2][4], const v8i (&fa)[2],
                                                                (int)eB, MI, (int)eA);
 }
 
+// One MFMA whose result is pinned right after it: the asm's memory clobber
+// keeps the stage DMA issued between MFMAs from being reordered around it.
+template <int MI, int NI>
+__device__ __forceinline__ void mfma_pinned(v16f (&acc)[2][4], const v8i (&fa)[2], const v8i (&fb)[4],
+                                            uint32_t eA, uint32_t eB) {
+  mfma_tile<MI, NI>(acc, fa, fb, eA, eB);
+  asm volatile("" : "+v"(acc[MI][NI]) : : "memory");
+}
+
 __device__ __forceinline__ void mfma_all(v16f (&acc)[2][4], const v8i (&fa)[2], const v8i (&fb)[4],
                                          uint32_t eA, uint32_t eB) {
   mfma_tile<0, 0>(acc, fa, fb, eA, eB);
@@ -115,15 +124,6 @@ __device__ __forceinline__ void mfma_all(v16f (&acc)[2][4], const v8i (&fa)[2], 
   mfma_tile<1, 2>(acc, fa, fb, eA, eB);
   mfma_tile<1, 3>(acc, fa, fb, eA, eB);
 }
-
-// Issue the DMA of stage data for K block kt: the two 256 x 128-byte K tiles
-// (8 row groups of 8 rows per operand per wave; lane -> row (lane>>3),
-// physical chunk (lane&7)), the e8m0 word of each of the 256 + 256 rows, and
-// at span starts their group maxima.
-struct DmaRows {
-  uint32_t ea_word, eb_word;   // e8m0 block index of this lane's DMA rows at kb = 0
-  uint32_t offa[2], offb[2];   // per-lane byte offset inside an 8-row group (even / odd group)
-};
 
 // Buffer resources of one operand: payload, e8m0 bytes, group maxima.  Raw
 // buffer loads are range-checked against num_records, so an offset outside an
@@ -155,33 +155,35 @@ __device__ __forceinline__ void dma_offsets(int64_t ld, int lane, uint32_t (&off
   }
 }
 
-__device__ __forceinline__ void issue_stage(const OperandRsrc& ra, int64_t lda, const OperandRsrc& rb,
-                                            int64_t ldb, const Scales& sa, const Scales& sb,
-                                            const DmaRows& d, int m0, int n0, int kt,
-                                            bool span_start, uint8_t* st, int w4, int lane) {
-  const uint32_t k0 = (uint32_t)kt * BK;
-  const uint32_t abase = (uint32_t)(m0 + w4 * 64) * (uint32_t)lda + k0;
-  const uint32_t bbase = (uint32_t)(n0 + w4 * 64) * (uint32_t)ldb + k0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int g = w4 * 8 + i;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra.pay, (lds_void*)(st + g * 1024), 16, d.offa[i & 1],
-                                             abase + (uint32_t)(i * 8) * (uint32_t)lda, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb.pay, (lds_void*)(st + OFF_B + g * 1024), 16, d.offb[i & 1],
-                                             bbase + (uint32_t)(i * 8) * (uint32_t)ldb, 0, 0);
-  }
-  const uint32_t ia = d.ea_word + (uint32_t)kt * (uint32_t)sa.s_k;
-  const uint32_t ib = d.eb_word + (uint32_t)kt * (uint32_t)sb.s_k;
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(ra.e8, (lds_void*)(st + OFF_EA + w4 * 256), 4, ia & ~3u, 0, 0, 0);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rb.e8, (lds_void*)(st + OFF_EB + w4 * 256), 4, ib & ~3u, 0, 0, 0);
-  if (span_start) {
-    // group maxima of the rows' blocks at this K block (exact group index)
-    const uint32_t ga = ia / (uint32_t)sa.kg, gb = ib / (uint32_t)sb.kg;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra.g32, (lds_void*)(st + OFF_GA + w4 * 256), 4, ga * 4u, 0,
-                                             0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb.g32, (lds_void*)(st + OFF_GB + w4 * 256), 4, gb * 4u, 0,
-                                             0, 0);
-  }
+// One wave's share of a stage's DMA.  The stage load is split between the
+// two ping-pong groups: wave w of group 0 loads A rows [64w, 64w + 64) of the
+// tile, their e8m0 words and (at span starts) group maxima; wave w of group 1
+// the same for B.  Each is issued inside a compute phase, between MFMAs, so
+// that the load issue (throttled by the vector memory address path) runs in
+// the MFMAs' shadow instead of lengthening a memory phase.
+struct DmaHalf {
+  __amdgpu_buffer_rsrc_t pay, e8, g32;
+  uint32_t ld;                 // operand row stride in bytes
+  uint32_t row0;               // first tile row of this wave's 64 rows (global row index)
+  uint32_t e_word;             // e8m0 block index of this lane's row at kb = 0
+  uint32_t s_k, kg;            // block index stride per K block, blocks per group
+  uint32_t off[2];             // per-lane byte offset inside an 8-row group (even / odd group)
+  int lds_pay, lds_e, lds_g;   // stage offsets of this wave's payload rows, e8m0 words, maxima
+};
+
+// Row group i (8 rows) of this wave's 64 rows for K block kt into stage st.
+__device__ __forceinline__ void dma_rows(const DmaHalf& h, uint8_t* st, int kt, int i) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(h.pay, (lds_void*)(st + h.lds_pay + i * 1024), 16, h.off[i & 1],
+                                           (h.row0 + (uint32_t)(i * 8)) * h.ld + (uint32_t)kt * BK, 0, 0);
+}
+
+// The e8m0 word of each of this wave's 64 rows for K block kt, and at span
+// starts their group maxima (exact group index block / kg).
+__device__ __forceinline__ void dma_scales(const DmaHalf& h, uint8_t* st, int kt, bool span_start) {
+  const uint32_t ia = h.e_word + (uint32_t)kt * h.s_k;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(h.e8, (lds_void*)(st + h.lds_e), 4, ia & ~3u, 0, 0, 0);
+  if (span_start)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(h.g32, (lds_void*)(st + h.lds_g), 4, (ia / h.kg) * 4u, 0, 0, 0);
 }
 
 // Workgroup barrier without the release/acquire fences of __syncthreads():
@@ -239,6 +241,57 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int* 
   *tn = w / rows_in_band;
 }
 
+// Epilogue: C[m][n] = acc * gA * gB / 2^14 (the two /128 of the dequant) for
+// this wave's 64 x 128 sub-tile at (row0, col0).  Each wave stages 32 rows x
+// 128 columns at a time in LDS (the stage buffers are free by then) and writes
+// them back as full 16-byte lane chunks covering whole rows.
+template <bool OUT_BF16, bool FINE_B>
+__device__ __forceinline__ void store_tile(const v16f (&acc)[2][4], const float (&gA)[2], const BGroups<FINE_B>& bg,
+                                           uint8_t* lds, int wave, int lane, void* C, int64_t ldc, int row0,
+                                           int col0) {
+  const int l32 = lane & 31, lhi = lane >> 5;
+  constexpr int ESZ = OUT_BF16 ? 2 : 4;
+  constexpr int ROWB = 128 * ESZ;           // bytes of one staged row
+  constexpr int PITCH = ROWB + 16;          // padded LDS row pitch
+  constexpr int CHUNKS = ROWB / 16;         // 16-byte chunks per row
+  uint8_t* stg = lds + wave * (32 * PITCH);
+  __syncthreads();                          // every wave is done with the stage buffers
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int col = ni * 32 + 8 * j + 4 * lhi;
+        const float f = gA[mi] * bg.g[ni][FINE_B ? j : 0] * 6.103515625e-05f;
+        const float c0 = acc[mi][ni][4 * j + 0] * f, c1 = acc[mi][ni][4 * j + 1] * f;
+        const float c2 = acc[mi][ni][4 * j + 2] * f, c3 = acc[mi][ni][4 * j + 3] * f;
+        uint8_t* dst = stg + l32 * PITCH + col * ESZ;
+        if constexpr (OUT_BF16) {
+          typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+          const bf16x2 p0 = {(__bf16)c0, (__bf16)c1};
+          const bf16x2 p1 = {(__bf16)c2, (__bf16)c3};
+          *reinterpret_cast<uint2*>(dst) =
+              make_uint2(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1));
+        } else {
+          *reinterpret_cast<float4*>(dst) = make_float4(c0, c1, c2, c3);
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);     // lgkmcnt(0): this wave's staging writes are done
+    // rows row0 + mi*32 + [0, 32), columns col0 + [0, 128)
+    uint8_t* Cb = static_cast<uint8_t*>(C) + ((int64_t)(row0 + mi * 32) * ldc + col0) * ESZ;
+#pragma unroll
+    for (int it = 0; it < (32 * CHUNKS) / 64; ++it) {
+      const int q = it * 64 + lane;
+      const int r = q / CHUNKS, c = q % CHUNKS;
+      const uint4 v = *reinterpret_cast<const uint4*>(stg + r * PITCH + c * 16);
+      *reinterpret_cast<uint4*>(Cb + (int64_t)r * ldc * ESZ + c * 16) = v;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);     // staging reads done before the next half overwrites
+  }
+}
+
 template <bool OUT_BF16, bool FINE_B>
 __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
@@ -261,16 +314,24 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   const int nk = K / BK;
   const int l32 = lane & 31, lhi = lane >> 5;
 
-  // Group 0 issues every stage DMA: its wave (wave & 3) covers 64 A rows and
-  // 64 B rows of the scale words.
-  DmaRows d;
+  // this wave's half of every stage load: A rows (group 0) or B rows (group 1)
+  DmaHalf h;
   {
-    const int64_t ra = m0 + (wave & 3) * 64 + lane, rb = n0 + (wave & 3) * 64 + lane;
-    const int64_t ia = blk_index(sa, ra, 0), ib = blk_index(sb, rb, 0);
-    d.ea_word = (uint32_t)ia;
-    d.eb_word = (uint32_t)ib;
-    dma_offsets(lda, lane, d.offa);
-    dma_offsets(ldb, lane, d.offb);
+    const int w4 = wave & 3;
+    const Scales& so = grp == 0 ? sa : sb;
+    const OperandRsrc& ro = grp == 0 ? ra : rb;
+    h.pay = ro.pay;
+    h.e8 = ro.e8;
+    h.g32 = ro.g32;
+    h.ld = (uint32_t)(grp == 0 ? lda : ldb);
+    h.row0 = (uint32_t)((grp == 0 ? m0 : n0) + w4 * 64);
+    h.e_word = (uint32_t)blk_index(so, (int64_t)h.row0 + lane, 0);
+    h.s_k = (uint32_t)so.s_k;
+    h.kg = (uint32_t)so.kg;
+    dma_offsets(grp == 0 ? lda : ldb, lane, h.off);
+    h.lds_pay = (grp == 0 ? 0 : OFF_B) + w4 * 8 * 1024;
+    h.lds_e = (grp == 0 ? OFF_EA : OFF_EB) + w4 * 256;
+    h.lds_g = (grp == 0 ? OFF_GA : OFF_GB) + w4 * 256;
   }
   // e8m0 byte position inside the DMA'd word of each compute row at kb = 0,
   // 2 bits per row: A rows i = 0, 1 in bits 2i, B rows i = 0..3 in bits 4 + 2i
@@ -304,12 +365,21 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
 #pragma unroll
     for (int j = 0; j < NJ; ++j) bg.g[ni][j] = 1.0f;
 
-  if (grp == 0) {
-    issue_stage(ra, lda, rb, ldb, sa, sb, d, m0, n0, 0, true, lds, wave & 3, lane);
-    __builtin_amdgcn_s_waitcnt(0);
-  }
+  // prologue: both halves of stage 0; group 1 then starts its half of stage 1
+  // (it is one stage ahead of group 0 throughout)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dma_rows(h, lds, 0, i);
+  dma_scales(h, lds, 0, true);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (grp == 1) wg_barrier();      // offset group 1 by one phase
+  if (grp == 1) {
+    if (1 < nk) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dma_rows(h, lds + STAGE_BYTES, 1, i);
+      dma_scales(h, lds + STAGE_BYTES, 1, 1 % span == 0);
+    }
+    wg_barrier();                  // offset group 1 by one phase
+  }
 
   uint32_t eA = 0, eB = 0;
   for (int kt = 0; kt < nk; ++kt) {
@@ -318,9 +388,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     for (int ks = 0; ks < 2; ++ks) {
       // ---- memory phase ----
       if (ks == 0) {
-        if (grp == 0 && kt + 1 < nk)
-          issue_stage(ra, lda, rb, ldb, sa, sb, d, m0, n0, kt + 1, (kt + 1) % span == 0,
-                      lds + ((kt + 1) & 1) * STAGE_BYTES, wave & 3, lane);
         // e8m0 bytes of this K block for the lane's 2 A rows / 4 B rows
         eA = 0;
         eB = 0;
@@ -384,63 +451,40 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
       fb[1] = read_frag2<OFF_B + 32 * BK>(blo, bhi);
       fb[2] = read_frag2<OFF_B + 64 * BK>(blo, bhi);
       fb[3] = read_frag2<OFF_B + 96 * BK>(blo, bhi);
-      PINNED_WAITCNT(0xC07F);   // lgkmcnt(0): operands in registers, stage reads done
+      if (grp == 1 && ks == 1 && kt + 1 < nk)
+        PINNED_WAITCNT(0);        // also group 1's half of stage kt+1 landed
+      else
+        PINNED_WAITCNT(0xC07F);   // lgkmcnt(0): operands in registers, stage reads done
       wg_barrier();
       // ---- compute phase ----
+      // Group 0 loads its half of stage kt+1 during its first K half, group 1
+      // its half of stage kt+2 during its second (both stages are free: every
+      // wave finished reading them before the preceding barrier).
+      const bool dma_now = grp == 0 ? (ks == 0 && kt + 1 < nk) : (ks == 1 && kt + 2 < nk);
+      const int dkt = grp == 0 ? kt + 1 : kt + 2;
+      uint8_t* dst = lds + (dkt & 1) * STAGE_BYTES;
       pin_frags(fa, fb);
-      mfma_all(acc, fa, fb, eA, eB);
+      mfma_pinned<0, 0>(acc, fa, fb, eA, eB);
+      if (dma_now) { dma_rows(h, dst, dkt, 0); dma_rows(h, dst, dkt, 1); }
+      mfma_pinned<0, 1>(acc, fa, fb, eA, eB);
+      if (dma_now) { dma_rows(h, dst, dkt, 2); dma_rows(h, dst, dkt, 3); }
+      mfma_pinned<0, 2>(acc, fa, fb, eA, eB);
+      if (dma_now) { dma_rows(h, dst, dkt, 4); dma_rows(h, dst, dkt, 5); }
+      mfma_pinned<0, 3>(acc, fa, fb, eA, eB);
+      if (dma_now) { dma_rows(h, dst, dkt, 6); dma_rows(h, dst, dkt, 7); }
+      mfma_pinned<1, 0>(acc, fa, fb, eA, eB);
+      if (dma_now) dma_scales(h, dst, dkt, dkt % span == 0);
+      mfma_pinned<1, 1>(acc, fa, fb, eA, eB);
+      mfma_pinned<1, 2>(acc, fa, fb, eA, eB);
+      mfma_pinned<1, 3>(acc, fa, fb, eA, eB);
       pin_acc(acc);
-      if (grp == 0 && ks == 1) PINNED_WAITCNT(0);   // stage kt+1 landed
+      if (grp == 0 && ks == 1 && kt + 1 < nk) PINNED_WAITCNT(0);   // group 0's half of stage kt+1 landed
       wg_barrier();
     }
   }
   if (grp == 0) wg_barrier();      // match group 1's extra barrier
 
-  // Epilogue: C[m][n] = acc * gA * gB / 2^14 (the two /128 of the dequant).
-  // Each wave stages 32 rows x 128 columns at a time in LDS (the stage
-  // buffers are free now) and writes them back as full 16-byte lane chunks
-  // covering whole rows, instead of 8-byte scattered pieces.
-  constexpr int ESZ = OUT_BF16 ? 2 : 4;
-  constexpr int ROWB = 128 * ESZ;           // bytes of one staged row
-  constexpr int PITCH = ROWB + 16;          // padded LDS row pitch
-  constexpr int CHUNKS = ROWB / 16;         // 16-byte chunks per row
-  uint8_t* stg = lds + wave * (32 * PITCH);
-  __syncthreads();                          // every wave is done with the stage buffers
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi) {
-#pragma unroll
-    for (int ni = 0; ni < 4; ++ni) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int col = ni * 32 + 8 * j + 4 * lhi;
-        const float f = gA[mi] * bg.g[ni][FINE_B ? j : 0] * 6.103515625e-05f;
-        const float c0 = acc[mi][ni][4 * j + 0] * f, c1 = acc[mi][ni][4 * j + 1] * f;
-        const float c2 = acc[mi][ni][4 * j + 2] * f, c3 = acc[mi][ni][4 * j + 3] * f;
-        uint8_t* dst = stg + l32 * PITCH + col * ESZ;
-        if constexpr (OUT_BF16) {
-          typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-          const bf16x2 p0 = {(__bf16)c0, (__bf16)c1};
-          const bf16x2 p1 = {(__bf16)c2, (__bf16)c3};
-          *reinterpret_cast<uint2*>(dst) =
-              make_uint2(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1));
-        } else {
-          *reinterpret_cast<float4*>(dst) = make_float4(c0, c1, c2, c3);
-        }
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);     // lgkmcnt(0): this wave's staging writes are done
-    // rows wm*64 + mi*32 + [0, 32), columns wn*128 + [0, 128) of the tile
-    uint8_t* Cb = static_cast<uint8_t*>(C) +
-                  ((int64_t)(m0 + wm * 64 + mi * 32) * ldc + (n0 + wn * 128)) * ESZ;
-#pragma unroll
-    for (int it = 0; it < (32 * CHUNKS) / 64; ++it) {
-      const int q = it * 64 + lane;
-      const int r = q / CHUNKS, c = q % CHUNKS;
-      const uint4 v = *reinterpret_cast<const uint4*>(stg + r * PITCH + c * 16);
-      *reinterpret_cast<uint4*>(Cb + (int64_t)r * ldc * ESZ + c * 16) = v;
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);     // staging reads done before the next half overwrites
-  }
+  store_tile<OUT_BF16, FINE_B>(acc, gA, bg, lds, wave, lane, C, ldc, m0 + wm * 64, n0 + wn * 128);
 }
 
 // Span of an operand's scale layout: the largest P such that every row's

@@ -74,6 +74,24 @@ int pratchya_quantize(const void* x, int x_dtype, int64_t slices, int64_t H, int
                       int64_t a, int64_t b, uint8_t* x_fp8, uint8_t* sc_fp8, float* sc_fp32,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Fake quantization in one pass (no payload is written):
+ *   out = dequantize_impl(*quantize_impl(x, tgrid), out_dtype, tgrid)
+ * the value of QArrayImpl(x, tgrid).astype(dtype) (Q:339-342 -> Q:458-506,
+ * Q:541-569), which is how a quantized Linear emits its output.  With
+ * fix_nan != 0 a NaN e8m0 (0xFF) is dequantized as 1.0, the composition
+ * quantize_impl -> quantize_impl_bwd (Q:512-526) that a requantized matmul
+ * cotangent (Q:637-638) takes back to its f32 input.  sc_fp8 / sc_fp32 receive
+ * quantize_impl's scales unrepaired.  out: `out_dtype` values [slices*H*W].
+ * `workspace`: pratchya_quantize_dequantize_workspace_bytes(...) bytes (0, and
+ * NULL allowed, for tgrid (1, 128) with K = 8 when x and out are 16-byte and
+ * sc_fp8 8-byte aligned). */
+size_t pratchya_quantize_dequantize_workspace_bytes(int x_dtype, int64_t slices, int64_t H,
+                                                    int64_t W, int64_t a, int64_t b);
+int pratchya_quantize_dequantize(const void* x, int x_dtype, int64_t slices, int64_t H, int64_t W,
+                                 int64_t a, int64_t b, void* out, int out_dtype, int fix_nan,
+                                 uint8_t* sc_fp8, float* sc_fp32, void* workspace,
+                                 size_t workspace_bytes, hipStream_t stream);
+
 /* dequantize_impl(x_fp8, sc_fp8, sc_fp32, dtype, tgrid)    replaces Q:541-569
  * out: `out_dtype` values [slices*H*W] = (f32(x8) * (f32(e<<23) * G)) / 128. */
 int pratchya_dequantize(const uint8_t* x_fp8, const uint8_t* sc_fp8, const float* sc_fp32,

@@ -113,6 +113,48 @@ def quantize(x: torch.Tensor, tgrid, out=None) -> Tuple[torch.Tensor, torch.Tens
     return x8.view(E4M3), sc8.view(E8M0), sc32
 
 
+def quantize_dequantize(x: torch.Tensor, tgrid, dtype: torch.dtype, fix_nan: bool = False, out=None):
+    """Fake quantization in one pass: ``dequantize_impl(*quantize_impl(x, tgrid),
+    dtype, tgrid)``, i.e. ``QArrayImpl(x, tgrid).astype(dtype)``
+    (pratchya/_qualia/_qarr.py:339-342, 458-506, 541-569), without writing
+    the payload.  ``fix_nan`` dequantizes NaN e8m0 scales as 1.0, as
+    quantize_impl's backward does for a requantized cotangent (Q:512-526).
+
+    Returns ``(y [x.shape] dtype, sc_fp8 [..., M, K] e8m0, sc_fp32 [..., M, 1, 1])``;
+    the scales are quantize_impl's, unrepaired.  ``out`` may hold preallocated
+    (y, e8m0, f32) buffers.
+    """
+    _require_gpu(x)
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        x = x.float()
+    if dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"quantize_dequantize: output dtype {dtype} is not float32 or bfloat16")
+    a, b = int(tgrid[0]), int(tgrid[1])
+    S, H, W = slices_hw(x.shape)
+    n_blk, K, M = group_layout(H, W, (a, b))
+    lead = tuple(x.shape[:-2]) if x.dim() >= 2 else ()
+    if not x.is_contiguous() or not _aligned(x, 16):
+        x = x.contiguous() if not x.is_contiguous() else x.clone()
+    if out is None:
+        y = torch.empty(x.shape, dtype=dtype, device=x.device)
+        sc8 = torch.empty(lead + (M, K), dtype=torch.uint8, device=x.device)
+        sc32 = torch.empty(lead + (M, 1, 1), dtype=torch.float32, device=x.device)
+    else:
+        esz = 2 if dtype == torch.bfloat16 else 4
+        _check_out(out, [(x.shape, esz), (lead + (M, K), 1), (lead + (M, 1, 1), 4)], "quantize_dequantize")
+        y, sc8, sc32 = out[0], _u8(out[1]), out[2]
+    lib = _lib.load()
+    code = _dtype_code(x.dtype)
+    ws_bytes = lib.pratchya_quantize_dequantize_workspace_bytes(code, S, H, W, a, b)
+    if ws_bytes == 0 and not (_aligned(y, 16) and _aligned(sc8, 8)):
+        ws_bytes = S * n_blk * 4      # misaligned caller buffers: the general path runs
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device) if ws_bytes else None
+    _lib.check(lib.pratchya_quantize_dequantize(
+        _ptr(x), code, S, H, W, a, b, _ptr(y), _dtype_code(dtype), 1 if fix_nan else 0, _ptr(sc8),
+        _ptr(sc32), _ptr(ws) if ws is not None else None, ws_bytes, _stream(x)), "quantize_dequantize")
+    return y, sc8.view(E8M0), sc32
+
+
 def _u8(t: torch.Tensor) -> torch.Tensor:
     return t.view(torch.uint8) if t.dtype != torch.uint8 else t
 

@@ -123,9 +123,40 @@ __device__ __forceinline__ void store_stream8(uint8_t* p, u32x2_t w) {
   if (PRATCHYA_NT_STORE) __builtin_nontemporal_store(w, reinterpret_cast<u32x2_t*>(p));
   else *reinterpret_cast<u32x2_t*>(p) = w;
 }
+__device__ __forceinline__ void store_stream16(void* p, u32x4_t w) {
+  if (PRATCHYA_NT_STORE) __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t*>(p));
+  else *reinterpret_cast<u32x4_t*>(p) = w;
+}
 __device__ __forceinline__ void store_stream4(uint8_t* p, uint32_t w) {
   if (PRATCHYA_NT_STORE) __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(p));
   else *reinterpret_cast<uint32_t*>(p) = w;
+}
+
+// Two e4m3fn bytes of a word (bytes 0,1 or 2,3) -> f32, with gfx950's
+// v_cvt_scalef32_pk_f32_fp8 at scale 1.0 (OCP e4m3fn; exact for every byte,
+// which the tests check byte by byte).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+template <int HALF>
+__device__ __forceinline__ f32x2_t fp8_pair(uint32_t word) {
+  return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, 1.0f, HALF != 0);
+}
+
+template <int J>
+__device__ __forceinline__ float fp8_elem(uint32_t word) {
+  const f32x2_t p = fp8_pair<(J >> 1) & 1>(word);
+  return (J & 1) ? p.y : p.x;
+}
+
+// Four e4m3fn bytes of a word -> f32, in byte order.
+__device__ __forceinline__ void fp8_word(uint32_t word, float& v0, float& v1, float& v2, float& v3) {
+  const f32x2_t lo = fp8_pair<0>(word), hi = fp8_pair<1>(word);
+  v0 = lo.x; v1 = lo.y; v2 = hi.x; v3 = hi.y;
+}
+
+// Two f32 -> packed bf16 bits (v_cvt_pk_bf16_f32, RNE; NaN stays NaN).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const bf16x2_t p = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, p);
 }
 
 // max |x| (as f32 bits) of 8 packed bf16 values, on packed 16-bit lanes.

@@ -209,10 +209,17 @@ __global__ __launch_bounds__(256) void k_quant_rowgroup(
 //    midpoint (+-8 ulp); if any element is that close the wave redoes the
 //    group with exact IEEE division;
 //  * a group whose G is not finite takes the exact per-element path.
+//
+// OUT selects what is written besides the scales: 0 the e4m3fn payload;
+// 1 / 2 the payload dequantized in registers, as bf16 / f32, exactly as
+// dequantize_impl computes it, (f32(q) * (2^(e-127) * G)) / 128 -- the fake
+// quantization QArrayImpl(x).astype(dtype).  FIXNAN dequantizes a NaN e8m0
+// (0xFF) as 1.0 (0x7F), quantize_impl's backward repair of a cotangent; the
+// stored e8m0 bytes are never repaired.
 // --------------------------------------------------------------------------
-template <bool IS_BF16, bool HW>
+template <bool IS_BF16, bool HW, int OUT, bool FIXNAN>
 __global__ __launch_bounds__(256) void k_quant_g8(const void* __restrict__ xv,
-                                                  uint8_t* __restrict__ q,
+                                                  void* __restrict__ outv,
                                                   uint8_t* __restrict__ sc8,
                                                   float* __restrict__ sc32, int64_t n_groups) {
   constexpr int VEC = IS_BF16 ? 8 : 4;        // elements per 16-byte load
@@ -322,14 +329,48 @@ __global__ __launch_bounds__(256) void k_quant_g8(const void* __restrict__ xv,
       }
     }
 
-    uint8_t* qg = q + g * 1024;
+    if constexpr (OUT == 0) {
+      uint8_t* qg = static_cast<uint8_t*>(outv) + g * 1024;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      if constexpr (IS_BF16) {
-        const u32x2_t w = {out[r][0], out[r][1]};
-        store_stream8(qg + (r * 64 + lane) * 8, w);
-      } else {
-        store_stream4(qg + (r * 64 + lane) * 4, out[r][0]);
+      for (int r = 0; r < R; ++r) {
+        if constexpr (IS_BF16) {
+          const u32x2_t w = {out[r][0], out[r][1]};
+          store_stream8(qg + (r * 64 + lane) * 8, w);
+        } else {
+          store_stream4(qg + (r * 64 + lane) * 4, out[r][0]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint32_t ed = (FIXNAN && e[r] == 0xFFu) ? 0x7Fu : e[r];
+        const float dq = e8m0_decode(ed) * G;
+        float d[VEC];
+#pragma unroll
+        for (int j = 0; j < VEC / 4; ++j) {
+          fp8_word(out[r][j], d[4 * j], d[4 * j + 1], d[4 * j + 2], d[4 * j + 3]);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) d[4 * j + k] = (d[4 * j + k] * dq) * 0.0078125f;
+        }
+        const int64_t eo = g * 1024 + (r * 64 + lane) * VEC;   // first element of this lane
+        if constexpr (OUT == 1) {
+          char* ob = static_cast<char*>(outv) + eo * 2;
+          if constexpr (VEC == 8) {
+            const u32x4_t w = {pack_bf16x2(d[0], d[1]), pack_bf16x2(d[2], d[3]),
+                               pack_bf16x2(d[4], d[5]), pack_bf16x2(d[6], d[7])};
+            store_stream16(ob, w);
+          } else {
+            const u32x2_t w = {pack_bf16x2(d[0], d[1]), pack_bf16x2(d[2], d[3])};
+            store_stream8(reinterpret_cast<uint8_t*>(ob), w);
+          }
+        } else {
+          char* ob = static_cast<char*>(outv) + eo * 4;
+#pragma unroll
+          for (int h = 0; h < VEC / 4; ++h) {
+            const u32x4_t w = {f2u(d[4 * h]), f2u(d[4 * h + 1]), f2u(d[4 * h + 2]), f2u(d[4 * h + 3])};
+            store_stream16(ob + 16 * h, w);
+          }
+        }
       }
     }
     // the group's 8 e8m0 bytes (block k: row k / BPR, leader lane (k % BPR) * BL) and G
@@ -422,13 +463,16 @@ __global__ __launch_bounds__(256) void k_group_scales_small(const uint32_t* __re
 }
 
 // Elementwise cast, thread per chunk of CH elements of one block row segment.
-template <bool IS_BF16, int CH>
+// OUT 0 writes the payload; OUT 1 / 2 write it dequantized as bf16 / f32
+// (fake quantization, with the NaN-e8m0 repair when fix_nan is set), as the
+// group-per-wave kernel's modes.
+template <bool IS_BF16, int CH, int OUT>
 __global__ __launch_bounds__(256) void k_cast_general(const void* __restrict__ x,
-                                                      uint8_t* __restrict__ q,
+                                                      void* __restrict__ outv,
                                                       const uint8_t* __restrict__ sc8,
                                                       const float* __restrict__ sc32,
                                                       int64_t n_chunks, int64_t W, int64_t a,
-                                                      int64_t b, int64_t K) {
+                                                      int64_t b, int64_t K, int fix_nan) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n_chunks) return;
   const int64_t off = t * CH;
@@ -440,6 +484,7 @@ __global__ __launch_bounds__(256) void k_cast_general(const void* __restrict__ x
   const float S = quant_scale(e, G);
   const bool ok = sG >= kClamp && sG <= 3.0e38f;
   const float yv = 128.0f / S;
+  const float dq = e8m0_decode((fix_nan && e == 0xFFu) ? 0x7Fu : e) * G;
 #pragma unroll
   for (int k = 0; k < CH; ++k) {
     const float xv = load_elem<IS_BF16>(x, off + k);
@@ -449,7 +494,13 @@ __global__ __launch_bounds__(256) void k_cast_general(const void* __restrict__ x
       code = bf16_to_e4m3fn(f32_to_bf16_rne_nonan(tv));
     else
       code = quant_elem_exact(xv, S);
-    q[off + k] = (uint8_t)code;
+    if constexpr (OUT == 0) {
+      static_cast<uint8_t*>(outv)[off + k] = (uint8_t)code;
+    } else {
+      const float d = (e4m3fn_to_f32(code) * dq) * 0.0078125f;
+      if constexpr (OUT == 1) static_cast<uint16_t*>(outv)[off + k] = (uint16_t)f32_to_bf16_rne(d);
+      else static_cast<float*>(outv)[off + k] = d;
+    }
   }
 }
 
@@ -642,9 +693,9 @@ unsigned grid_for(int64_t n, int per_block) {
   return (unsigned)(g < 1 ? 1 : g);
 }
 
-template <bool IS_BF16>
-int launch_general(const void* x, uint8_t* q, uint8_t* sc8, float* sc32, uint32_t* ws,
-                   const Layout& L, hipStream_t st) {
+template <bool IS_BF16, int OUT = 0>
+int launch_general(const void* x, void* q, uint8_t* sc8, float* sc32, uint32_t* ws,
+                   const Layout& L, hipStream_t st, int fix_nan = 0) {
   const int64_t n_blocks_total = L.S * L.n_blk;
   const int64_t n_groups = L.S * L.M;
   hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(n_blocks_total, 256) > 4096 ? 4096 : grid_for(n_blocks_total, 256)),
@@ -671,8 +722,8 @@ int launch_general(const void* x, uint8_t* q, uint8_t* sc8, float* sc32, uint32_
     hipLaunchKernelGGL(k_group_scales_small, dim3(grid_for(n_groups, 256)), dim3(256), 0, st, ws,
                        sc8, sc32, n_groups, L.K);
 #define PRATCHYA_CAST(C)                                                                     \
-  hipLaunchKernelGGL((k_cast_general<IS_BF16, C>), dim3(gr), dim3(256), 0, st, x, q, sc8, sc32, \
-                     n_chunks, L.W, L.a, L.b, L.K)
+  hipLaunchKernelGGL((k_cast_general<IS_BF16, C, OUT>), dim3(gr), dim3(256), 0, st, x, q, sc8, sc32, \
+                     n_chunks, L.W, L.a, L.b, L.K, fix_nan)
   switch (ch) {
     case 1: PRATCHYA_CAST(1); break;
     case 2: PRATCHYA_CAST(2); break;
@@ -706,18 +757,35 @@ bool use_g8(const Layout& L, bool bf16, const void* x, const void* q, const void
 #define PRATCHYA_G8_BLOCKS_PER_CU 8
 #endif
 
-int launch_g8(bool bf16, const void* x, uint8_t* q, uint8_t* sc8, float* sc32, int64_t n_groups,
-              hipStream_t st) {
+template <bool IS_BF16, int OUT, bool FIXNAN>
+void launch_g8_t(const void* x, void* out, uint8_t* sc8, float* sc32, int64_t n_groups,
+                 hipStream_t st) {
   int64_t blocks = (n_groups + 3) / 4;
   const int64_t cap = (int64_t)num_cus() * PRATCHYA_G8_BLOCKS_PER_CU;
   if (blocks > cap) blocks = cap;
-  if (bf16)
-    hipLaunchKernelGGL((k_quant_g8<true, PRATCHYA_HW_CVT != 0>), dim3((unsigned)blocks), dim3(256), 0,
-                       st, x, q, sc8, sc32, n_groups);
-  else
-    hipLaunchKernelGGL((k_quant_g8<false, PRATCHYA_HW_CVT != 0>), dim3((unsigned)blocks), dim3(256), 0,
-                       st, x, q, sc8, sc32, n_groups);
+  hipLaunchKernelGGL((k_quant_g8<IS_BF16, PRATCHYA_HW_CVT != 0, OUT, FIXNAN>), dim3((unsigned)blocks),
+                     dim3(256), 0, st, x, out, sc8, sc32, n_groups);
+}
+
+int launch_g8(bool bf16, const void* x, uint8_t* q, uint8_t* sc8, float* sc32, int64_t n_groups,
+              hipStream_t st) {
+  if (bf16) launch_g8_t<true, 0, false>(x, q, sc8, sc32, n_groups, st);
+  else launch_g8_t<false, 0, false>(x, q, sc8, sc32, n_groups, st);
   return check_launch("quantize(1x128)");
+}
+
+// Fake quantization through the group-per-wave kernel: OUT 1 (bf16) / 2 (f32).
+template <bool IS_BF16>
+int launch_g8_qdq(const void* x, void* out, bool out_bf16, bool fix_nan, uint8_t* sc8, float* sc32,
+                  int64_t n_groups, hipStream_t st) {
+  if (out_bf16) {
+    if (fix_nan) launch_g8_t<IS_BF16, 1, true>(x, out, sc8, sc32, n_groups, st);
+    else launch_g8_t<IS_BF16, 1, false>(x, out, sc8, sc32, n_groups, st);
+  } else {
+    if (fix_nan) launch_g8_t<IS_BF16, 2, true>(x, out, sc8, sc32, n_groups, st);
+    else launch_g8_t<IS_BF16, 2, false>(x, out, sc8, sc32, n_groups, st);
+  }
+  return check_launch("quantize_dequantize(1x128)");
 }
 
 }  // namespace
@@ -775,6 +843,62 @@ extern "C" int pratchya_quantize(const void* x, int x_dtype, int64_t slices, int
   uint32_t* ws = static_cast<uint32_t*>(workspace);
   return bf16 ? launch_general<true>(x, x_fp8, sc_fp8, sc_fp32, ws, L, stream)
               : launch_general<false>(x, x_fp8, sc_fp8, sc_fp32, ws, L, stream);
+}
+
+namespace {
+bool g8_layout(const Layout& L) { return L.a == 1 && L.b == 128 && L.K == 8; }
+}  // namespace
+
+extern "C" size_t pratchya_quantize_dequantize_workspace_bytes(int x_dtype, int64_t slices,
+                                                               int64_t H, int64_t W, int64_t a,
+                                                               int64_t b) {
+  (void)x_dtype;
+  Layout L;
+  if (make_layout(slices, H, W, a, b, &L)) return 0;
+  // the single-pass group-per-wave kernel (tgrid (1, 128), K = 8, 16-byte
+  // aligned x and out) needs none; every other layout runs the general path
+  if (g8_layout(L)) return 0;
+  return (size_t)(L.S * L.n_blk) * sizeof(uint32_t);
+}
+
+extern "C" int pratchya_quantize_dequantize(const void* x, int x_dtype, int64_t slices, int64_t H,
+                                            int64_t W, int64_t a, int64_t b, void* out,
+                                            int out_dtype, int fix_nan, uint8_t* sc_fp8,
+                                            float* sc_fp32, void* workspace,
+                                            size_t workspace_bytes, hipStream_t stream) {
+  Layout L;
+  int rc = make_layout(slices, H, W, a, b, &L);
+  if (rc) return rc;
+  if (x_dtype != PRATCHYA_DT_F32 && x_dtype != PRATCHYA_DT_BF16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_dequantize: unsupported input dtype %d", x_dtype);
+  if (out_dtype != PRATCHYA_DT_F32 && out_dtype != PRATCHYA_DT_BF16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_dequantize: unsupported output dtype %d",
+                              out_dtype);
+  const int64_t n = L.n();
+  if (n == 0) {
+    g_err[0] = 0;
+    return PRATCHYA_OK;
+  }
+  if (!x || !out || !sc_fp8 || !sc_fp32)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_dequantize: null buffer");
+  const bool bf16 = x_dtype == PRATCHYA_DT_BF16;
+  const bool obf16 = out_dtype == PRATCHYA_DT_BF16;
+  const bool fix = fix_nan != 0;
+  if (g8_layout(L) && aligned(x, 16) && aligned(out, 16) && aligned(sc_fp8, 8))
+    return bf16 ? launch_g8_qdq<true>(x, out, obf16, fix, sc_fp8, sc_fp32, n / 1024, stream)
+                : launch_g8_qdq<false>(x, out, obf16, fix, sc_fp8, sc_fp32, n / 1024, stream);
+  const size_t need = (size_t)(L.S * L.n_blk) * sizeof(uint32_t);
+  if (!workspace || workspace_bytes < need)
+    return pratchya_set_error(PRATCHYA_EINVAL,
+                              "quantize_dequantize: workspace of %zu bytes needed, got %zu", need,
+                              workspace_bytes);
+  uint32_t* ws = static_cast<uint32_t*>(workspace);
+  const int f = fix ? 1 : 0;
+  if (bf16)
+    return obf16 ? launch_general<true, 1>(x, out, sc_fp8, sc_fp32, ws, L, stream, f)
+                 : launch_general<true, 2>(x, out, sc_fp8, sc_fp32, ws, L, stream, f);
+  return obf16 ? launch_general<false, 1>(x, out, sc_fp8, sc_fp32, ws, L, stream, f)
+               : launch_general<false, 2>(x, out, sc_fp8, sc_fp32, ws, L, stream, f);
 }
 
 namespace {

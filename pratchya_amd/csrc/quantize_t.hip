@@ -72,21 +72,6 @@ __device__ __forceinline__ void load_row(const uint8_t* p, uint32_t (&w)[InTrait
   }
 }
 
-// Two e4m3fn bytes of a word (bytes 0,1 or 2,3) -> f32, with gfx950's
-// v_cvt_scalef32_pk_f32_fp8 at scale 1.0 (OCP e4m3fn; exact for every byte,
-// which the tests check byte by byte through the requantize).
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-template <int HALF>
-__device__ __forceinline__ f32x2_t fp8_pair(uint32_t word) {
-  return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, 1.0f, HALF != 0);
-}
-
-template <int J>
-__device__ __forceinline__ float fp8_elem(uint32_t word) {
-  const f32x2_t p = fp8_pair<(J >> 1) & 1>(word);
-  return (J & 1) ? p.y : p.x;
-}
-
 // |channel j| of a row as f32 bits, from the raw bits (a different
 // expression from row_elem's, so the compiler does not keep 128 widened
 // values alive from the maxima to the cast).

@@ -127,3 +127,21 @@ def test_quantize_t128_argument_codes_without_gpu():
     assert f(None, 7, None, None, 1, 128, 64, None, None, None, None) == _lib.EINVAL
     # empty tensors are a no-op
     assert f(None, _lib.DT_BF16, None, None, 0, 128, 64, None, None, None, None) == _lib.OK
+
+
+def test_quantize_dequantize_codes_without_gpu():
+    """Workspace query and argument errors of the one-pass fake quantization."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    ws = lib.pratchya_quantize_dequantize_workspace_bytes
+    assert ws(_lib.DT_F32, 1, 32768, 4096, 1, 128) == 0           # single-pass kernel
+    assert ws(_lib.DT_F32, 1, 4096, 16384, 128, 128) == 32 * 128 * 4
+    assert ws(_lib.DT_F32, 1, 64, 256, 1, 32) == 64 * 8 * 4        # (1, 32): general path
+    f = lib.pratchya_quantize_dequantize
+    args = lambda xdt, H, W, a, b, odt: (None, xdt, 1, H, W, a, b, None, odt, 0, None, None, None, 0, None)
+    assert f(*args(_lib.DT_F32, 10, 10, 3, 5, _lib.DT_BF16)) == _lib.EINVAL
+    assert b"does not divide" in lib.pratchya_last_error()
+    assert f(*args(7, 8, 128, 1, 128, _lib.DT_BF16)) == _lib.EINVAL
+    assert f(*args(_lib.DT_F32, 8, 128, 1, 128, _lib.DT_E4M3)) == _lib.EINVAL
+    assert f(*args(_lib.DT_F32, 0, 128, 1, 128, _lib.DT_F32)) == _lib.OK
+    assert f(*args(_lib.DT_F32, 8, 128, 1, 128, _lib.DT_F32)) == _lib.EINVAL      # null buffers

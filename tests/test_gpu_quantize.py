@@ -65,6 +65,7 @@ def test_debug_f32_to_bf16_ties_and_subnormals(mode):
     got = K.debug_f32_to_bf16(torch.from_numpy(x).cuda(), mode).cpu().numpy().view(np.uint16)
     nan = np.isnan(x)
     assert_bytes_equal(got[~nan], O.f32_to_bf16_bits(x)[~nan], f"f32->bf16 mode {mode}")
+    assert np.all((got[nan] & 0x7FFF) > 0x7F80), f"f32->bf16 mode {mode}: NaN not kept"
 
 
 def test_debug_f32_to_bf16_software():

@@ -101,18 +101,21 @@ def quantize_impl(x: torch.Tensor, tgrid: Tuple = (128, 128)):
     return x8, s8, s32
 
 
-def _fix_nan_e8m0(sc8: torch.Tensor) -> torch.Tensor:
-    """quantize_impl_bwd's repair of NaN e8m0 cotangent scales to 1.0 (Q:522-523)."""
-    u = sc8.view(torch.uint8)
-    return torch.where(u == 0xFF, torch.full_like(u, 0x7F), u).view(E8M0)
+def _grad_dtype(src: Optional[torch.Tensor]) -> torch.dtype:
+    """dtype a cotangent is delivered in: the source tensor's when a kernel can
+    write it (bf16 / f32), else f32 (autograd then casts, as it would anyway)."""
+    if src is not None and src.dtype in (torch.float32, torch.bfloat16):
+        return src.dtype
+    return torch.float32
 
 
-def _requant_cotangent(g32: torch.Tensor, tgrid) -> torch.Tensor:
+def _requant_cotangent(g32: torch.Tensor, tgrid, dtype: torch.dtype = torch.float32) -> torch.Tensor:
     """A matmul/elementwise f32 cotangent as it reaches the quantized input:
     requantized with the input's grid (Q:637-638) and dequantized by
-    quantize_impl's backward (Q:521-526)."""
-    g8, gs8, gs32 = K.quantize(g32.contiguous(), tuple(tgrid))
-    return K.dequantize(g8, _fix_nan_e8m0(gs8), gs32, torch.float32, tuple(tgrid))
+    quantize_impl's backward with NaN e8m0 scales read as 1.0 (Q:521-526), in
+    one pass.  ``dtype`` is the input's: the f32 result rounded to it is what
+    autograd would deliver."""
+    return K.quantize_dequantize(g32.contiguous(), tuple(tgrid), dtype, fix_nan=True)[0]
 
 
 class _Dequantize(torch.autograd.Function):
@@ -232,33 +235,83 @@ def _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y):
     return gxf, gyf
 
 
+def _matmul_cotangents(g, saved, grids, need_x, need_y):
+    """f32 cotangents of dequant(x) and dequant(y) from the product's cotangent
+    ``g`` (f32, or bf16 holding exact values): the FP8 MFMA dgrad / wgrad in
+    the "fp8" mode where the layouts fit, else the reference's f32 dots of the
+    dequantized operands (Q:618-622)."""
+    x8, xs8, xs32, y8, ys8, ys32 = saved
+    gx, gy = grids
+    res = _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y) \
+        if _backward_mode == "fp8" else None
+    if res is not None:
+        return res
+    g = g.float()
+    gxf = g @ _deq32(y8, ys8, ys32, gy).transpose(-1, -2) if need_x else None
+    gyf = _deq32(x8, xs8, xs32, gx).transpose(-1, -2) @ g if need_y else None
+    return gxf, gyf
+
+
 class _Matmul(torch.autograd.Function):
     @staticmethod
     def forward(ctx, src_x, src_y, x8, xs8, xs32, y8, ys8, ys32, gx, gy):
         ctx.saved = (x8, xs8, xs32, y8, ys8, ys32)
         ctx.grids = (gx, gy)
+        ctx.dtypes = (_grad_dtype(src_x), _grad_dtype(src_y))
         return _matmul_forward(x8, xs8, xs32, y8, ys8, ys32, gx, gy)
 
     @staticmethod
     def backward(ctx, g):
-        x8, xs8, xs32, y8, ys8, ys32 = ctx.saved
+        x8, y8 = ctx.saved[0], ctx.saved[3]
         gx, gy = ctx.grids
         need_x, need_y = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        g = g.float()
-        res = _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y) \
-            if _backward_mode == "fp8" else None
-        if res is not None:
-            gxf, gyf = res
-        else:
-            # Q:618-622: f32 dots of the dequantized operands
-            gxf = g @ _deq32(y8, ys8, ys32, gy).transpose(-1, -2) if need_x else None
-            gyf = _deq32(x8, xs8, xs32, gx).transpose(-1, -2) @ g if need_y else None
+        gxf, gyf = _matmul_cotangents(g, ctx.saved, ctx.grids, need_x, need_y)
         grad_x = grad_y = None
         if need_x:
-            grad_x = _requant_cotangent(_reduce_broadcast(gxf, x8.shape), gx)
+            grad_x = _requant_cotangent(_reduce_broadcast(gxf, x8.shape), gx, ctx.dtypes[0])
         if need_y:
-            grad_y = _requant_cotangent(_reduce_broadcast(gyf, y8.shape), gy)
+            grad_y = _requant_cotangent(_reduce_broadcast(gyf, y8.shape), gy, ctx.dtypes[1])
         return grad_x, grad_y, None, None, None, None, None, None, None, None
+
+
+class _QLinear(torch.autograd.Function):
+    """``QArrayImpl(matmul_impl(x, y), go).astype(dtype)`` as one node: the
+    composition a quantized Linear runs (pratchya/_nnx_impl/_module.py:46-50;
+    Q:100-105, Q:339-342).
+
+    Forward: the f32 product, then its requantization with grid ``go`` and
+    dequantization to ``dtype`` in one pass (no payload is stored).
+    Backward, the reference's chain: dequantize_impl_bwd of the cotangent
+    with the output's scales (Q:575-601), passed through the output
+    quantization's backward (Q:518-519), matmul_impl's backward (Q:615-640)
+    and each input quantization's backward (Q:521-526).  The cotangent stays
+    in its own dtype (its values are exact there) and each input cotangent is
+    written once, requantized and dequantized, in its source's dtype."""
+
+    @staticmethod
+    def forward(ctx, src_x, src_y, x8, xs8, xs32, y8, ys8, ys32, gx, gy, go, dtype):
+        out = _matmul_forward(x8, xs8, xs32, y8, ys8, ys32, gx, gy)
+        res, os8, os32 = K.quantize_dequantize(out, go, dtype)
+        ctx.saved = (x8, xs8, xs32, y8, ys8, ys32)
+        ctx.out_scales = (os8, os32)
+        ctx.grids = (gx, gy, go)
+        ctx.dtypes = (_grad_dtype(src_x), _grad_dtype(src_y))
+        return res
+
+    @staticmethod
+    def backward(ctx, g):
+        x8, y8 = ctx.saved[0], ctx.saved[3]
+        gx, gy, go = ctx.grids
+        os8, os32 = ctx.out_scales
+        need_x, need_y = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        g1 = K.dequantize_bwd(g.contiguous(), os8, os32, go)
+        gxf, gyf = _matmul_cotangents(g1, ctx.saved, (gx, gy), need_x, need_y)
+        grad_x = grad_y = None
+        if need_x:
+            grad_x = _requant_cotangent(_reduce_broadcast(gxf, x8.shape), gx, ctx.dtypes[0])
+        if need_y:
+            grad_y = _requant_cotangent(_reduce_broadcast(gyf, y8.shape), gy, ctx.dtypes[1])
+        return (grad_x, grad_y) + (None,) * 10
 
 
 def matmul_impl(x_fp8, x_sc8, x_sc32, y_fp8, y_sc8, y_sc32, block_grid_x: Tuple, block_grid_y: Tuple):
@@ -485,18 +538,17 @@ class QArrayImpl:
         other = _value_of(other)
         if isinstance(other, QArrayImpl):
             other = self._promote(other, 1)
-            x_out = matmul_impl(self.__value, self.__sc_fp8, self.__sc_fp32, other.__value, other.__sc_fp8,
-                                other.__sc_fp32, self.__tgrid, other.__tgrid)
-            return QArrayImpl(x_out, (self.__tgrid[0], other.__tgrid[1]))
+            # QArrayImpl(matmul_impl(self, other), (self.tgrid[0], other.tgrid[1])) (Q:100-105)
+            return _LazyProduct((self.__value, self.__sc_fp8, self.__sc_fp32, other.__value, other.__sc_fp8,
+                                 other.__sc_fp32), self.__tgrid, other.__tgrid)
         return matmul_mixed_impl(self.__value, self.__sc_fp8, self.__sc_fp32, other, self.__tgrid)
 
     def __rmatmul__(self, other):
         other = _value_of(other)
         if isinstance(other, QArrayImpl):
             other = self._promote(other, 0)
-            x_out = matmul_impl(other.__value, other.__sc_fp8, other.__sc_fp32, self.__value, self.__sc_fp8,
-                                self.__sc_fp32, other.__tgrid, self.__tgrid)
-            return QArrayImpl(x_out, (other.__tgrid[0], self.__tgrid[1]))
+            return _LazyProduct((other.__value, other.__sc_fp8, other.__sc_fp32, self.__value, self.__sc_fp8,
+                                 self.__sc_fp32), other.__tgrid, self.__tgrid)
         return rmatmul_mixed_impl(other, self.__value, self.__sc_fp8, self.__sc_fp32, self.__tgrid)
 
     # -- elementwise arithmetic (Q:121-261) --------------------------------
@@ -664,11 +716,91 @@ class QArrayImpl:
         return obj
 
 
-pytree.register_pytree_node(
-    QArrayImpl,
-    lambda q: q._tree_flatten(),
-    lambda children, aux: QArrayImpl._tree_unflatten(aux, tuple(children)),
-)
+class _LazyProduct(QArrayImpl):
+    """``QArrayImpl(matmul_impl(x, y), (x.tgrid[0], y.tgrid[1]))`` (Q:100-105,
+    Q:111-116) held as its operands until first use.
+
+    Dequantizing it to bf16 / f32 (``astype`` / ``dequantize``, how a Linear
+    emits its output, pratchya/_nnx_impl/_module.py:50) runs the product, the
+    requantization and the dequantization as one autograd node (_QLinear) and
+    never stores the requantized payload; values and gradients are those of
+    the step-by-step composition.  Any other use (payload, scales, slicing,
+    arithmetic, pytree flattening) first materialises the quantized array
+    exactly as the reference builds it, after which the object behaves as a
+    plain QArrayImpl.  Repeated dequantizations to one dtype before that return
+    the same tensor."""
+
+    _FIELDS = ("_QArrayImpl__value", "_QArrayImpl__sc_fp8", "_QArrayImpl__sc_fp32")
+
+    def __init__(self, operands, gx, gy):
+        self._QArrayImpl__tgrid = (int(gx[0]), int(gy[1]))
+        self._operands = operands
+        self._grids = (tuple(gx), tuple(gy))
+        self._grad_enabled = torch.is_grad_enabled()
+        self._srcs = (_src(operands[0]), _src(operands[3]))
+        self._dequantized = {}
+
+    def __getattr__(self, name):
+        # reached only for attributes not set yet: the quantized fields
+        if name in _LazyProduct._FIELDS and "_operands" in self.__dict__:
+            self._materialize()
+            return self.__dict__[name]
+        raise AttributeError(name)
+
+    def _materialize(self):
+        x8, xs8, xs32, y8, ys8, ys32 = self._operands
+        gx, gy = self._grids
+        sx, sy = self._srcs
+        with torch.set_grad_enabled(self._grad_enabled):
+            if sx is not None or sy is not None:
+                out = _Matmul.apply(sx, sy, x8, xs8, xs32, y8, ys8, ys32, gx, gy)
+            else:
+                out = _matmul_forward(x8, xs8, xs32, y8, ys8, ys32, gx, gy)
+            v, s8, s32 = quantize_impl(out, self._QArrayImpl__tgrid)
+        self._QArrayImpl__value, self._QArrayImpl__sc_fp8, self._QArrayImpl__sc_fp32 = v, s8, s32
+        del self._operands, self._srcs, self._dequantized
+
+    def dequantize(self, dtype):
+        if "_operands" not in self.__dict__ or dtype not in (torch.float32, torch.bfloat16):
+            return super().dequantize(dtype)
+        hit = self._dequantized.get(dtype)
+        if hit is not None:
+            return hit
+        x8, xs8, xs32, y8, ys8, ys32 = self._operands
+        gx, gy = self._grids
+        go = self._QArrayImpl__tgrid
+        sx, sy = self._srcs
+        with torch.set_grad_enabled(self._grad_enabled):
+            if sx is not None or sy is not None:
+                res = _QLinear.apply(sx, sy, x8, xs8, xs32, y8, ys8, ys32, gx, gy, go, dtype)
+            else:
+                out = _matmul_forward(x8, xs8, xs32, y8, ys8, ys32, gx, gy)
+                res = K.quantize_dequantize(out, go, dtype)[0]
+        self._dequantized[dtype] = res
+        return res
+
+    @property
+    def shape(self):
+        if "_operands" in self.__dict__:
+            x8, y8 = self._operands[0], self._operands[3]
+            return tuple(torch.empty(x8.shape, device="meta").matmul(torch.empty(y8.shape, device="meta")).shape)
+        return super().shape
+
+    @property
+    def size(self):
+        return math.prod(self.shape)
+
+    @property
+    def dtype(self):
+        return E4M3
+
+
+for _cls in (QArrayImpl, _LazyProduct):      # a lazy product flattens to its materialised fields
+    pytree.register_pytree_node(
+        _cls,
+        lambda q: q._tree_flatten(),
+        lambda children, aux: QArrayImpl._tree_unflatten(aux, tuple(children)),
+    )
 
 
 # --------------------------------------------------------------------------

@@ -149,8 +149,48 @@ def test_linear_forward_uses_the_fp8_kernel(Q, monkeypatch):
     real = Q.K.gemm_nt
     monkeypatch.setattr(Q.K, "gemm_nt", lambda *a, **k: calls.append(1) or real(*a, **k))
     xb, wb, _ = _linear_case(M=256, Kd=256, N=256)
-    Q.QArrayImpl(to_dev_bf16(xb), (1, 128)) @ Q.QArrayImpl(to_dev_bf16(wb), (128, 128))
-    assert calls
+    prod = Q.QArrayImpl(to_dev_bf16(xb), (1, 128)) @ Q.QArrayImpl(to_dev_bf16(wb), (128, 128))
+    prod.astype(torch.bfloat16)              # the fused Linear output
+    assert len(calls) == 1
+    prod.get_value()                         # the materialised quantized product
+    assert len(calls) == 2
+
+
+@pytest.mark.parametrize("mode", ["f32", "fp8"])
+@pytest.mark.parametrize("xdtype", ["bf16", "f32"])
+def test_fused_linear_matches_materialised_composition(Q, mode, xdtype):
+    """``(QArrayImpl(x) @ W).astype(x.dtype)`` runs as one node; forcing the
+    quantized product first (payload access) runs the step-by-step graph.
+    Output and both input cotangents agree bit for bit."""
+    Q.set_matmul_backward(mode)
+    xb, wb, gb = _linear_case(seed=13)
+    dt = torch.bfloat16 if xdtype == "bf16" else torch.float32
+    results = []
+    for materialise in (False, True):
+        x = to_dev_bf16(xb).to(dt).requires_grad_(True)
+        w = to_dev_bf16(wb).requires_grad_(True)
+        prod = Q.QArrayImpl(x, (1, 128)) @ Q.QArrayImpl(w, (128, 128))
+        assert prod.shape == (512, 768) and prod.dtype == torch.float8_e4m3fn
+        assert ("_operands" in prod.__dict__) is True      # shape / dtype do not materialise
+        if materialise:
+            prod.get_value()
+        y = prod.astype(dt)
+        if not materialise:
+            assert y is prod.astype(dt)          # one node per dtype
+        y.backward(to_dev_bf16(gb).to(dt))
+        assert x.grad.dtype == dt and w.grad.dtype == torch.bfloat16
+        results.append([t.detach().float().cpu().numpy() for t in (y, x.grad, w.grad)])
+    for a, b, what in zip(results[0], results[1], ("y", "x.grad", "w.grad")):
+        assert_f32_bits_equal(a, b, f"fused vs materialised {what} ({mode}, {xdtype})")
+
+
+def test_fused_linear_without_grad(Q):
+    xb, wb, _ = _linear_case(seed=14, M=256, Kd=256, N=512)
+    with torch.no_grad():
+        prod = Q.QArrayImpl(to_dev_bf16(xb), (1, 128)) @ Q.QArrayImpl(to_dev_bf16(wb), (128, 128))
+        y = prod.astype(torch.bfloat16)
+        trip = triple(prod)
+    assert_bytes_equal(bf16_bits(y), odq(trip, (1, 128), "bfloat16"), "no-grad fused output")
 
 
 def test_batched_activation(Q):

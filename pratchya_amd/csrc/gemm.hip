@@ -164,23 +164,28 @@ __device__ __forceinline__ void dma_offsets(int64_t ld, int lane, uint32_t (&off
 struct DmaHalf {
   __amdgpu_buffer_rsrc_t pay, e8, g32;
   uint32_t ld;                 // operand row stride in bytes
-  uint32_t row0;               // first tile row of this wave's 64 rows (global row index)
-  uint32_t e_word;             // e8m0 block index of this lane's row at kb = 0
   uint32_t s_k, kg;            // block index stride per K block, blocks per group
   uint32_t off[2];             // per-lane byte offset inside an 8-row group (even / odd group)
   int lds_pay, lds_e, lds_g;   // stage offsets of this wave's payload rows, e8m0 words, maxima
 };
 
+// The rows a wave loads for one output tile: the first of its 64 rows (global
+// row index) and the e8m0 block index of the lane's row at kb = 0.
+struct DmaRows {
+  uint32_t row0, e_word;
+};
+
 // Row group i (8 rows) of this wave's 64 rows for K block kt into stage st.
-__device__ __forceinline__ void dma_rows(const DmaHalf& h, uint8_t* st, int kt, int i) {
+__device__ __forceinline__ void dma_rows(const DmaHalf& h, const DmaRows& r, uint8_t* st, int kt, int i) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(h.pay, (lds_void*)(st + h.lds_pay + i * 1024), 16, h.off[i & 1],
-                                           (h.row0 + (uint32_t)(i * 8)) * h.ld + (uint32_t)kt * BK, 0, 0);
+                                           (r.row0 + (uint32_t)(i * 8)) * h.ld + (uint32_t)kt * BK, 0, 0);
 }
 
 // The e8m0 word of each of this wave's 64 rows for K block kt, and at span
 // starts their group maxima (exact group index block / kg).
-__device__ __forceinline__ void dma_scales(const DmaHalf& h, uint8_t* st, int kt, bool span_start) {
-  const uint32_t ia = h.e_word + (uint32_t)kt * h.s_k;
+__device__ __forceinline__ void dma_scales(const DmaHalf& h, const DmaRows& r, uint8_t* st, int kt,
+                                           bool span_start) {
+  const uint32_t ia = r.e_word + (uint32_t)kt * h.s_k;
   __builtin_amdgcn_raw_ptr_buffer_load_lds(h.e8, (lds_void*)(st + h.lds_e), 4, ia & ~3u, 0, 0, 0);
   if (span_start)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(h.g32, (lds_void*)(st + h.lds_g), 4, (ia / h.kg) * 4u, 0, 0, 0);
@@ -242,53 +247,62 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int* 
 }
 
 // Epilogue: C[m][n] = acc * gA * gB / 2^14 (the two /128 of the dequant) for
-// this wave's 64 x 128 sub-tile at (row0, col0).  Each wave stages 32 rows x
-// 128 columns at a time in LDS (the stage buffers are free by then) and writes
-// them back as full 16-byte lane chunks covering whole rows.
+// this wave's 64 x 128 sub-tile at (row0, col0).  The waves stage RP rows x
+// 128 columns each at a time in one LDS stage buffer (free once every wave has
+// passed the barrier below) and write them back as full 16-byte lane chunks
+// covering whole rows, with non-temporal stores (the output is not read again
+// by this kernel; streaming it keeps the operand panels in L2).
 template <bool OUT_BF16, bool FINE_B>
 __device__ __forceinline__ void store_tile(const v16f (&acc)[2][4], const float (&gA)[2], const BGroups<FINE_B>& bg,
-                                           uint8_t* lds, int wave, int lane, void* C, int64_t ldc, int row0,
+                                           uint8_t* stage, int wave, int lane, void* C, int64_t ldc, int row0,
                                            int col0) {
   const int l32 = lane & 31, lhi = lane >> 5;
   constexpr int ESZ = OUT_BF16 ? 2 : 4;
   constexpr int ROWB = 128 * ESZ;           // bytes of one staged row
   constexpr int PITCH = ROWB + 16;          // padded LDS row pitch
   constexpr int CHUNKS = ROWB / 16;         // 16-byte chunks per row
-  uint8_t* stg = lds + wave * (32 * PITCH);
-  __syncthreads();                          // every wave is done with the stage buffers
+  constexpr int RP = OUT_BF16 ? 32 : 16;    // rows staged per pass
+  static_assert(8 * RP * PITCH <= STAGE_BYTES, "staging must fit one stage buffer");
+  uint8_t* stg = stage + wave * (RP * PITCH);
+  __syncthreads();                          // every wave is done with the stage buffer
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi) {
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni) {
+    for (int p = 0; p < 32 / RP; ++p) {
+      if (RP == 32 || (l32 / RP) == p) {    // lanes whose row is staged in this pass
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int col = ni * 32 + 8 * j + 4 * lhi;
-        const float f = gA[mi] * bg.g[ni][FINE_B ? j : 0] * 6.103515625e-05f;
-        const float c0 = acc[mi][ni][4 * j + 0] * f, c1 = acc[mi][ni][4 * j + 1] * f;
-        const float c2 = acc[mi][ni][4 * j + 2] * f, c3 = acc[mi][ni][4 * j + 3] * f;
-        uint8_t* dst = stg + l32 * PITCH + col * ESZ;
-        if constexpr (OUT_BF16) {
-          typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-          const bf16x2 p0 = {(__bf16)c0, (__bf16)c1};
-          const bf16x2 p1 = {(__bf16)c2, (__bf16)c3};
-          *reinterpret_cast<uint2*>(dst) =
-              make_uint2(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1));
-        } else {
-          *reinterpret_cast<float4*>(dst) = make_float4(c0, c1, c2, c3);
+        for (int ni = 0; ni < 4; ++ni) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int col = ni * 32 + 8 * j + 4 * lhi;
+            const float f = gA[mi] * bg.g[ni][FINE_B ? j : 0] * 6.103515625e-05f;
+            const float c0 = acc[mi][ni][4 * j + 0] * f, c1 = acc[mi][ni][4 * j + 1] * f;
+            const float c2 = acc[mi][ni][4 * j + 2] * f, c3 = acc[mi][ni][4 * j + 3] * f;
+            uint8_t* dst = stg + (l32 % RP) * PITCH + col * ESZ;
+            if constexpr (OUT_BF16) {
+              typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+              const bf16x2 p0 = {(__bf16)c0, (__bf16)c1};
+              const bf16x2 p1 = {(__bf16)c2, (__bf16)c3};
+              *reinterpret_cast<uint2*>(dst) =
+                  make_uint2(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1));
+            } else {
+              *reinterpret_cast<float4*>(dst) = make_float4(c0, c1, c2, c3);
+            }
+          }
         }
       }
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);     // lgkmcnt(0): this wave's staging writes are done
-    // rows row0 + mi*32 + [0, 32), columns col0 + [0, 128)
-    uint8_t* Cb = static_cast<uint8_t*>(C) + ((int64_t)(row0 + mi * 32) * ldc + col0) * ESZ;
+      __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's staging writes are done
+      // rows row0 + mi*32 + p*RP + [0, RP), columns col0 + [0, 128)
+      uint8_t* Cb = static_cast<uint8_t*>(C) + ((int64_t)(row0 + mi * 32 + p * RP) * ldc + col0) * ESZ;
 #pragma unroll
-    for (int it = 0; it < (32 * CHUNKS) / 64; ++it) {
-      const int q = it * 64 + lane;
-      const int r = q / CHUNKS, c = q % CHUNKS;
-      const uint4 v = *reinterpret_cast<const uint4*>(stg + r * PITCH + c * 16);
-      *reinterpret_cast<uint4*>(Cb + (int64_t)r * ldc * ESZ + c * 16) = v;
+      for (int it = 0; it < (RP * CHUNKS) / 64; ++it) {
+        const int q = it * 64 + lane;
+        const int r = q / CHUNKS, c = q % CHUNKS;
+        const v4i v = *reinterpret_cast<const v4i*>(stg + r * PITCH + c * 16);
+        __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(Cb + (int64_t)r * ldc * ESZ + c * 16));
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);   // staging reads done before the next pass overwrites
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);     // staging reads done before the next half overwrites
   }
 }
 
@@ -308,24 +322,20 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // waves w, w+4 share SIMD w
   const int grp = wave >> 2;              // ping-pong group
   const int wm = wave & 3, wn = grp;      // 64-row band wm, 128-column half wn
-  int tm, tn;
-  tile_of(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
-  const int m0 = tm * BM, n0 = tn * BN;
   const int nk = K / BK;
+  const int T = tiles_m * tiles_n;
   const int l32 = lane & 31, lhi = lane >> 5;
 
   // this wave's half of every stage load: A rows (group 0) or B rows (group 1)
+  const int w4 = wave & 3;
+  const Scales& so = grp == 0 ? sa : sb;
   DmaHalf h;
   {
-    const int w4 = wave & 3;
-    const Scales& so = grp == 0 ? sa : sb;
     const OperandRsrc& ro = grp == 0 ? ra : rb;
     h.pay = ro.pay;
     h.e8 = ro.e8;
     h.g32 = ro.g32;
     h.ld = (uint32_t)(grp == 0 ? lda : ldb);
-    h.row0 = (uint32_t)((grp == 0 ? m0 : n0) + w4 * 64);
-    h.e_word = (uint32_t)blk_index(so, (int64_t)h.row0 + lane, 0);
     h.s_k = (uint32_t)so.s_k;
     h.kg = (uint32_t)so.kg;
     dma_offsets(grp == 0 ? lda : ldb, lane, h.off);
@@ -333,14 +343,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     h.lds_e = (grp == 0 ? OFF_EA : OFF_EB) + w4 * 256;
     h.lds_g = (grp == 0 ? OFF_GA : OFF_GB) + w4 * 256;
   }
-  // e8m0 byte position inside the DMA'd word of each compute row at kb = 0,
-  // 2 bits per row: A rows i = 0, 1 in bits 2i, B rows i = 0..3 in bits 4 + 2i
-  uint32_t epos = 0;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) epos |= ((uint32_t)blk_index(sa, m0 + wm * 64 + i * 32 + l32, 0) & 3u) << (2 * i);
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    epos |= ((uint32_t)blk_index(sb, n0 + wn * 128 + i * 32 + l32, 0) & 3u) << (4 + 2 * i);
+  auto rows_of = [&](int tm_, int tn_) {
+    DmaRows r;
+    r.row0 = (uint32_t)((grp == 0 ? tm_ * BM : tn_ * BN) + w4 * 64);
+    r.e_word = (uint32_t)blk_index(so, (int64_t)r.row0 + lane, 0);
+    return r;
+  };
   const uint32_t skA = (uint32_t)sa.s_k, skB = (uint32_t)sb.s_k;
   // physical 16-byte chunk offsets of this lane's operand halves: K half ks,
   // lo/hi chunk (logical 4*ks + 2*lhi + h, XOR-swizzled by the lane's row)
@@ -350,141 +358,212 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) ch[ks][h] = ((ks * 4 + lhi * 2 + h) ^ sw) << 4;
+      for (int hh = 0; hh < 2; ++hh) ch[ks][hh] = ((ks * 4 + lhi * 2 + hh) ^ sw) << 4;
   }
 
-  v16f acc[2][4];
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = v16f{0};
-  float gA[2] = {1.0f, 1.0f};
-  BGroups<FINE_B> bg;
-#pragma unroll
-  for (int ni = 0; ni < 4; ++ni)
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) bg.g[ni][j] = 1.0f;
+  // Persistent: workgroup b computes tiles b, b + G, b + 2G, ... (G = grid
+  // size, a multiple of the 8 XCDs, so every tile of a workgroup falls in the
+  // L2 band of its XCD).  The stage pipeline runs on across tile boundaries:
+  // the next tile's first stage is loaded during the current tile's last K
+  // steps into the stage buffer they no longer read, and its latency is
+  // covered by the epilogue, which stages the output in the other buffer.
+  int t = blockIdx.x;
+  int tm, tn;
+  tile_of(t, tiles_m, tiles_n, &tm, &tn);
+  DmaRows cur = rows_of(tm, tn);
+  int par = 0;                            // stage buffer of the tile's K block 0
 
   // prologue: both halves of stage 0; group 1 then starts its half of stage 1
   // (it is one stage ahead of group 0 throughout)
 #pragma unroll
-  for (int i = 0; i < 8; ++i) dma_rows(h, lds, 0, i);
-  dma_scales(h, lds, 0, true);
+  for (int i = 0; i < 8; ++i) dma_rows(h, cur, lds, 0, i);
+  dma_scales(h, cur, lds, 0, true);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (grp == 1) {
-    if (1 < nk) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) dma_rows(h, lds + STAGE_BYTES, 1, i);
-      dma_scales(h, lds + STAGE_BYTES, 1, 1 % span == 0);
-    }
-    wg_barrier();                  // offset group 1 by one phase
-  }
 
-  uint32_t eA = 0, eB = 0;
-  for (int kt = 0; kt < nk; ++kt) {
-    const uint8_t* st = lds + (kt & 1) * STAGE_BYTES;
+  for (;;) {
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int t_next = t + (int)gridDim.x;
+    const bool has_next = t_next < T;
+    int tm2 = 0, tn2 = 0;
+    DmaRows nxt = cur;
+    if (has_next) {
+      tile_of(t_next, tiles_m, tiles_n, &tm2, &tn2);
+      nxt = rows_of(tm2, tn2);
+    }
+    if (grp == 1) {
+      if (1 < nk) {
+        uint8_t* s1 = lds + ((1 + par) & 1) * STAGE_BYTES;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      // ---- memory phase ----
-      if (ks == 0) {
-        // e8m0 bytes of this K block for the lane's 2 A rows / 4 B rows
-        eA = 0;
-        eB = 0;
-        const uint8_t* ea = st + OFF_EA + (wm * 64 + l32) * 4;
-        const uint8_t* eb = st + OFF_EB + (wn * 128 + l32) * 4;
-        const uint32_t tA = (uint32_t)kt * skA, tB = (uint32_t)kt * skB;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const uint32_t w = lds_u32(ea + i * 128);
-          const uint32_t pos = (__builtin_amdgcn_ubfe(epos, 2 * i, 2) + tA) & 3u;
-          eA |= __builtin_amdgcn_ubfe(w, pos * 8u, 8) << (8 * i);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t w = lds_u32(eb + i * 128);
-          const uint32_t pos = (__builtin_amdgcn_ubfe(epos, 4 + 2 * i, 2) + tB) & 3u;
-          eB |= __builtin_amdgcn_ubfe(w, pos * 8u, 8) << (8 * i);
-        }
-        if (kt % span == 0) {
-          // a new span of group maxima: move the accumulator into its units.
-          // A zero group max keeps the previous units (an all-zero group has
-          // an all-zero payload and adds nothing).
-          float rA[2], rB[4][NJ];
-#pragma unroll
-          for (int mi = 0; mi < 2; ++mi) {
-            const float g0 = lds_f32(st + OFF_GA + (wm * 64 + mi * 32 + l32) * 4);
-            const float g = g0 == 0.0f ? gA[mi] : g0;
-            rA[mi] = gA[mi] * __builtin_amdgcn_rcpf(g);
-            gA[mi] = g;
-          }
-#pragma unroll
-          for (int ni = 0; ni < 4; ++ni)
-#pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-              const int col = wn * 128 + ni * 32 + (FINE_B ? 8 * j + 4 * lhi : 0);
-              const float g0 = lds_f32(st + OFF_GB + col * 4);
-              const float g = g0 == 0.0f ? bg.g[ni][j] : g0;
-              rB[ni][j] = bg.g[ni][j] * __builtin_amdgcn_rcpf(g);
-              bg.g[ni][j] = g;
-            }
-          if (kt > 0) {
-#pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-              for (int ni = 0; ni < 4; ++ni)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) acc[mi][ni][v] *= rA[mi] * rB[ni][FINE_B ? (v >> 2) : 0];
-          }
-        }
+        for (int i = 0; i < 8; ++i) dma_rows(h, cur, s1, 1, i);
+        dma_scales(h, cur, s1, 1, 1 % span == 0);
       }
-      // rows of this lane: A wm*64 + i*32 + l32, B wn*128 + i*32 + l32; the
-      // swizzle of a row depends only on l32, so row blocks i are immediates
-      const uint8_t* alo = st + (wm * 64 + l32) * BK + ch[ks][0];
-      const uint8_t* ahi = st + (wm * 64 + l32) * BK + ch[ks][1];
-      const uint8_t* blo = st + (wn * 128 + l32) * BK + ch[ks][0];
-      const uint8_t* bhi = st + (wn * 128 + l32) * BK + ch[ks][1];
-      v8i fa[2], fb[4];
-      fa[0] = read_frag2<0>(alo, ahi);
-      fa[1] = read_frag2<32 * BK>(alo, ahi);
-      fb[0] = read_frag2<OFF_B>(blo, bhi);
-      fb[1] = read_frag2<OFF_B + 32 * BK>(blo, bhi);
-      fb[2] = read_frag2<OFF_B + 64 * BK>(blo, bhi);
-      fb[3] = read_frag2<OFF_B + 96 * BK>(blo, bhi);
-      if (grp == 1 && ks == 1 && kt + 1 < nk)
-        PINNED_WAITCNT(0);        // also group 1's half of stage kt+1 landed
-      else
-        PINNED_WAITCNT(0xC07F);   // lgkmcnt(0): operands in registers, stage reads done
-      wg_barrier();
-      // ---- compute phase ----
-      // Group 0 loads its half of stage kt+1 during its first K half, group 1
-      // its half of stage kt+2 during its second (both stages are free: every
-      // wave finished reading them before the preceding barrier).
-      const bool dma_now = grp == 0 ? (ks == 0 && kt + 1 < nk) : (ks == 1 && kt + 2 < nk);
-      const int dkt = grp == 0 ? kt + 1 : kt + 2;
-      uint8_t* dst = lds + (dkt & 1) * STAGE_BYTES;
-      pin_frags(fa, fb);
-      mfma_pinned<0, 0>(acc, fa, fb, eA, eB);
-      if (dma_now) { dma_rows(h, dst, dkt, 0); dma_rows(h, dst, dkt, 1); }
-      mfma_pinned<0, 1>(acc, fa, fb, eA, eB);
-      if (dma_now) { dma_rows(h, dst, dkt, 2); dma_rows(h, dst, dkt, 3); }
-      mfma_pinned<0, 2>(acc, fa, fb, eA, eB);
-      if (dma_now) { dma_rows(h, dst, dkt, 4); dma_rows(h, dst, dkt, 5); }
-      mfma_pinned<0, 3>(acc, fa, fb, eA, eB);
-      if (dma_now) { dma_rows(h, dst, dkt, 6); dma_rows(h, dst, dkt, 7); }
-      mfma_pinned<1, 0>(acc, fa, fb, eA, eB);
-      if (dma_now) dma_scales(h, dst, dkt, dkt % span == 0);
-      mfma_pinned<1, 1>(acc, fa, fb, eA, eB);
-      mfma_pinned<1, 2>(acc, fa, fb, eA, eB);
-      mfma_pinned<1, 3>(acc, fa, fb, eA, eB);
-      pin_acc(acc);
-      if (grp == 0 && ks == 1 && kt + 1 < nk) PINNED_WAITCNT(0);   // group 0's half of stage kt+1 landed
-      wg_barrier();
+      wg_barrier();                  // offset group 1 by one phase
     }
-  }
-  if (grp == 0) wg_barrier();      // match group 1's extra barrier
+    // e8m0 byte position inside the DMA'd word of each compute row at kb = 0,
+    // 2 bits per row: A rows i = 0, 1 in bits 2i, B rows i = 0..3 in bits 4 + 2i
+    uint32_t epos = 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) epos |= ((uint32_t)blk_index(sa, m0 + wm * 64 + i * 32 + l32, 0) & 3u) << (2 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      epos |= ((uint32_t)blk_index(sb, n0 + wn * 128 + i * 32 + l32, 0) & 3u) << (4 + 2 * i);
 
-  store_tile<OUT_BF16, FINE_B>(acc, gA, bg, lds, wave, lane, C, ldc, m0 + wm * 64, n0 + wn * 128);
+    v16f acc[2][4];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = v16f{0};
+    float gA[2] = {1.0f, 1.0f};
+    BGroups<FINE_B> bg;
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) bg.g[ni][j] = 1.0f;
+
+    uint32_t eA = 0, eB = 0;
+    for (int kt = 0; kt < nk; ++kt) {
+      const uint8_t* st = lds + ((kt + par) & 1) * STAGE_BYTES;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        // ---- memory phase ----
+        if (ks == 0) {
+          // e8m0 bytes of this K block for the lane's 2 A rows / 4 B rows
+          eA = 0;
+          eB = 0;
+          const uint8_t* ea = st + OFF_EA + (wm * 64 + l32) * 4;
+          const uint8_t* eb = st + OFF_EB + (wn * 128 + l32) * 4;
+          const uint32_t tA = (uint32_t)kt * skA, tB = (uint32_t)kt * skB;
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const uint32_t w = lds_u32(ea + i * 128);
+            const uint32_t pos = (__builtin_amdgcn_ubfe(epos, 2 * i, 2) + tA) & 3u;
+            eA |= __builtin_amdgcn_ubfe(w, pos * 8u, 8) << (8 * i);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t w = lds_u32(eb + i * 128);
+            const uint32_t pos = (__builtin_amdgcn_ubfe(epos, 4 + 2 * i, 2) + tB) & 3u;
+            eB |= __builtin_amdgcn_ubfe(w, pos * 8u, 8) << (8 * i);
+          }
+          if (kt % span == 0) {
+            // a new span of group maxima: move the accumulator into its units.
+            // A zero group max keeps the previous units (an all-zero group has
+            // an all-zero payload and adds nothing).
+            float rA[2], rB[4][NJ];
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) {
+              const float g0 = lds_f32(st + OFF_GA + (wm * 64 + mi * 32 + l32) * 4);
+              const float g = g0 == 0.0f ? gA[mi] : g0;
+              rA[mi] = gA[mi] * __builtin_amdgcn_rcpf(g);
+              gA[mi] = g;
+            }
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+              for (int j = 0; j < NJ; ++j) {
+                const int col = wn * 128 + ni * 32 + (FINE_B ? 8 * j + 4 * lhi : 0);
+                const float g0 = lds_f32(st + OFF_GB + col * 4);
+                const float g = g0 == 0.0f ? bg.g[ni][j] : g0;
+                rB[ni][j] = bg.g[ni][j] * __builtin_amdgcn_rcpf(g);
+                bg.g[ni][j] = g;
+              }
+            if (kt > 0) {
+#pragma unroll
+              for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+                  for (int v = 0; v < 16; ++v) acc[mi][ni][v] *= rA[mi] * rB[ni][FINE_B ? (v >> 2) : 0];
+            }
+          }
+        }
+        // rows of this lane: A wm*64 + i*32 + l32, B wn*128 + i*32 + l32; the
+        // swizzle of a row depends only on l32, so row blocks i are immediates
+        const uint8_t* alo = st + (wm * 64 + l32) * BK + ch[ks][0];
+        const uint8_t* ahi = st + (wm * 64 + l32) * BK + ch[ks][1];
+        const uint8_t* blo = st + (wn * 128 + l32) * BK + ch[ks][0];
+        const uint8_t* bhi = st + (wn * 128 + l32) * BK + ch[ks][1];
+        v8i fa[2], fb[4];
+        fa[0] = read_frag2<0>(alo, ahi);
+        fa[1] = read_frag2<32 * BK>(alo, ahi);
+        fb[0] = read_frag2<OFF_B>(blo, bhi);
+        fb[1] = read_frag2<OFF_B + 32 * BK>(blo, bhi);
+        fb[2] = read_frag2<OFF_B + 64 * BK>(blo, bhi);
+        fb[3] = read_frag2<OFF_B + 96 * BK>(blo, bhi);
+        if (grp == 1 && ks == 1 && kt + 1 < nk)
+          PINNED_WAITCNT(0);        // also group 1's half of stage kt+1 landed
+        else
+          PINNED_WAITCNT(0xC07F);   // lgkmcnt(0): operands in registers, stage reads done
+        wg_barrier();
+        // ---- compute phase ----
+        // Group 0 loads its half of stage kt+1 during its first K half, group 1
+        // its half of stage kt+2 during its second (both stages are free: every
+        // wave finished reading them before the preceding barrier).  Past the
+        // tile's last stage the load is the next tile's stage 0; group 1 skips
+        // the next tile's stage 1, whose buffer the epilogue stages in.
+        bool dma_now;
+        int dkt;                       // stage index counted from this tile's K block 0
+        if (grp == 0) {
+          dma_now = ks == 0 && (kt + 1 < nk || has_next);
+          dkt = kt + 1;
+        } else {
+          dma_now = ks == 1 && (kt + 2 < nk || (has_next && (kt + 2 == nk || nk == 1)));
+          dkt = nk == 1 ? kt + 1 : kt + 2;
+        }
+        const bool to_next = dkt >= nk;
+        const DmaRows& dr = to_next ? nxt : cur;
+        const int lkt = to_next ? 0 : dkt;            // K block inside the tile loaded
+        uint8_t* dst = lds + ((dkt + par) & 1) * STAGE_BYTES;
+        pin_frags(fa, fb);
+        mfma_pinned<0, 0>(acc, fa, fb, eA, eB);
+        if (dma_now) { dma_rows(h, dr, dst, lkt, 0); dma_rows(h, dr, dst, lkt, 1); }
+        mfma_pinned<0, 1>(acc, fa, fb, eA, eB);
+        if (dma_now) { dma_rows(h, dr, dst, lkt, 2); dma_rows(h, dr, dst, lkt, 3); }
+        mfma_pinned<0, 2>(acc, fa, fb, eA, eB);
+        if (dma_now) { dma_rows(h, dr, dst, lkt, 4); dma_rows(h, dr, dst, lkt, 5); }
+        mfma_pinned<0, 3>(acc, fa, fb, eA, eB);
+        if (dma_now) { dma_rows(h, dr, dst, lkt, 6); dma_rows(h, dr, dst, lkt, 7); }
+        mfma_pinned<1, 0>(acc, fa, fb, eA, eB);
+        if (dma_now) dma_scales(h, dr, dst, lkt, lkt % span == 0);
+        mfma_pinned<1, 1>(acc, fa, fb, eA, eB);
+        mfma_pinned<1, 2>(acc, fa, fb, eA, eB);
+        mfma_pinned<1, 3>(acc, fa, fb, eA, eB);
+        pin_acc(acc);
+        if (grp == 0 && ks == 1 && kt + 1 < nk) PINNED_WAITCNT(0);   // group 0's half of stage kt+1 landed
+        wg_barrier();
+      }
+    }
+    if (grp == 0) wg_barrier();      // match group 1's extra barrier
+
+    // the last stage's buffer holds no pending load: stage the output there
+    store_tile<OUT_BF16, FINE_B>(acc, gA, bg, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc,
+                                 m0 + wm * 64, n0 + wn * 128);
+    if (!has_next) break;
+    t = t_next;
+    tm = tm2;
+    tn = tn2;
+    cur = nxt;
+    par = (par + nk) & 1;
+    // the next tile's stage 0 (and this tile's output stores) complete, and
+    // every wave is done with the staging buffer
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+}
+
+// Compute units of the current device (cached per device), rounded down to a
+// multiple of 8 so that a persistent workgroup's tiles stay on one XCD's band.
+int64_t gemm_num_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 8) v = 256;
+    cached[dev] = v - v % 8;
+  }
+  return cached[dev];
 }
 
 // Span of an operand's scale layout: the largest P such that every row's
@@ -572,8 +651,13 @@ extern "C" int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t*
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: operands beyond 2 GiB");
   const int64_t tiles_n = N / BN;
   const int64_t tiles = (M / BM) * tiles_n;
+  if (tiles > INT32_MAX) return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: too many output tiles");
+  // persistent grid: one workgroup per CU (the kernel's LDS allows no more), a
+  // multiple of the 8 XCDs
+  const int64_t cus = gemm_num_cus();
+  const int64_t grid = tiles < cus ? tiles : cus;
 #define PRATCHYA_GEMM(BF, FB)                                                                   \
-  hipLaunchKernelGGL((k_gemm_bs_nt<BF, FB>), dim3((unsigned)tiles), dim3(NTHREADS), 0, stream, A, lda, \
+  hipLaunchKernelGGL((k_gemm_bs_nt<BF, FB>), dim3((unsigned)grid), dim3(NTHREADS), 0, stream, A, lda, \
                      B, ldb, sa, sb, C, ldc, (int)K, (int)span, (int)(M / BM), (int)tiles_n,   \
                      (uint32_t)a_bytes, (uint32_t)b_bytes, (uint32_t)(last_a + 1),              \
                      (uint32_t)(last_b + 1), (uint32_t)ga_bytes, (uint32_t)gb_bytes)

@@ -217,6 +217,9 @@ __global__ __launch_bounds__(256) void k_quant_rowgroup(
 // (0xFF) as 1.0 (0x7F), quantize_impl's backward repair of a cotangent; the
 // stored e8m0 bytes are never repaired.
 // --------------------------------------------------------------------------
+constexpr int kRawBuffer = 0x00020000;            // raw buffer resource, 32-bit data format
+constexpr int kOutOfRange = (int)0xFFFFFFF0u;     // buffer offset past any scale array
+
 template <bool IS_BF16, bool HW, int OUT, bool FIXNAN>
 __global__ __launch_bounds__(256) void k_quant_g8(const void* __restrict__ xv,
                                                   void* __restrict__ outv,
@@ -232,6 +235,9 @@ __global__ __launch_bounds__(256) void k_quant_g8(const void* __restrict__ xv,
   int64_t g = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (g >= n_groups) return;
   const char* xb = static_cast<const char*>(xv);
+  // scale arrays as raw buffers (byte counts below 2^32 - 16, checked on the host)
+  const __amdgpu_buffer_rsrc_t r8 = __builtin_amdgcn_make_buffer_rsrc(sc8, 0, (int)(uint32_t)(n_groups * 8), kRawBuffer);
+  const __amdgpu_buffer_rsrc_t r32 = __builtin_amdgcn_make_buffer_rsrc(sc32, 0, (int)(uint32_t)(n_groups * 4), kRawBuffer);
 
   uint4 nxt[R];
 #pragma unroll
@@ -381,10 +387,13 @@ __global__ __launch_bounds__(256) void k_quant_g8(const void* __restrict__ xv,
       if (k < 4) lo |= ek << (8 * k);
       else hi |= ek << (8 * (k - 4));
     }
-    if (lane == 0) {
-      *reinterpret_cast<uint2*>(sc8 + g * 8) = make_uint2(lo, hi);
-      sc32[g] = G;
-    }
+    // Every lane issues both scale stores; lanes other than 0 address past the
+    // end of the buffer, where the range check drops them.  A store count that
+    // does not depend on a branch lets the wait for the next group's loads at
+    // the loop head leave this group's stores in flight.
+    const bool lead = lane == 0;
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{lo, hi}, r8, lead ? (int)(g * 8) : kOutOfRange, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(f2u(G), r32, lead ? (int)(g * 4) : kOutOfRange, 0, 0);
   }
 }
 
@@ -748,8 +757,11 @@ int num_cus() {
 }
 
 // The group-per-wave kernel: tgrid (1,128), K = 8, aligned buffers.
+// (the kernel addresses its scale arrays through 32-bit buffer offsets)
+bool g8_fits(const Layout& L) { return (L.n() / 1024) * 8 < (int64_t)0xFFFFFFF0u; }
+
 bool use_g8(const Layout& L, bool bf16, const void* x, const void* q, const void* sc8) {
-  return L.a == 1 && L.b == 128 && L.K == 8 && aligned(x, 16) && aligned(q, bf16 ? 8 : 4) &&
+  return L.a == 1 && L.b == 128 && L.K == 8 && g8_fits(L) && aligned(x, 16) && aligned(q, bf16 ? 8 : 4) &&
          aligned(sc8, 8);
 }
 
@@ -846,7 +858,7 @@ extern "C" int pratchya_quantize(const void* x, int x_dtype, int64_t slices, int
 }
 
 namespace {
-bool g8_layout(const Layout& L) { return L.a == 1 && L.b == 128 && L.K == 8; }
+bool g8_layout(const Layout& L) { return L.a == 1 && L.b == 128 && L.K == 8 && g8_fits(L); }
 }  // namespace
 
 extern "C" size_t pratchya_quantize_dequantize_workspace_bytes(int x_dtype, int64_t slices,

@@ -92,6 +92,21 @@ int pratchya_quantize_dequantize(const void* x, int x_dtype, int64_t slices, int
                                  uint8_t* sc_fp8, float* sc_fp32, void* workspace,
                                  size_t workspace_bytes, hipStream_t stream);
 
+/* Requantization of a Linear output's cotangent for the FP8 dgrad, tgrid (1, 128):
+ *   quantize_impl(dequantize_impl_bwd(g, g_sc8, g_sc32, (1, 128)), (1, 128))
+ * i.e. the output quantization's backward (Q:575-601: (g * 2^(e-127) * G) / 128
+ * in g's dtype, passed through Q:518-519) followed by the quantization of the
+ * cotangent that fp8_matmul's backward contracts (Q:784-789), in one pass (the
+ * dequantized cotangent never reaches memory).  g: bf16 / f32 [slices*H*W];
+ * g_sc8 / g_sc32: the (1, 128) scales of the tensor g is the cotangent of.
+ * Outputs as pratchya_quantize with tgrid (1, 128).  Needs 8 blocks per group
+ * (H*W/128 a multiple of 8), 16-byte aligned g, 8-byte aligned e8m0 arrays
+ * (PRATCHYA_EUNSUPPORTED otherwise). */
+int pratchya_requantize_cotangent(const void* g, int g_dtype, const uint8_t* g_sc8,
+                                  const float* g_sc32, int64_t slices, int64_t H, int64_t W,
+                                  uint8_t* x_fp8, uint8_t* sc_fp8, float* sc_fp32,
+                                  hipStream_t stream);
+
 /* dequantize_impl(x_fp8, sc_fp8, sc_fp32, dtype, tgrid)    replaces Q:541-569
  * out: `out_dtype` values [slices*H*W] = (f32(x8) * (f32(e<<23) * G)) / 128. */
 int pratchya_dequantize(const uint8_t* x_fp8, const uint8_t* sc_fp8, const float* sc_fp32,
@@ -110,12 +125,15 @@ int pratchya_dequantize_bwd(const void* g, int g_dtype, const uint8_t* sc_fp8,
  * x: [slices, T, C] row-major, x_dtype PRATCHYA_DT_BF16 / PRATCHYA_DT_F32, or
  * PRATCHYA_DT_E4M3: an e4m3fn payload quantized with tgrid (1, 128) whose
  * scales are x_sc8 / x_sc32; it is dequantized to f32 exactly as
- * dequantize_impl (Q:562-564) before requantization.
+ * dequantize_impl (Q:562-564) before requantization.  A bf16 x given with
+ * x_sc8 / x_sc32 is the cotangent of a tensor quantized (1, 128) with those
+ * scales: dequantize_impl_bwd (Q:575-601, bf16((x * 2^(e-127) * G) / 128)) is
+ * applied first, in registers (the wgrad cotangent of the FP8 backward).
  * Outputs: xt_fp8 uint8 [slices, C, T] (payload of quantize_impl transposed per
  * slice), sc_fp8 [slices*M*8] and sc_fp32 [slices*M] exactly as
  * quantize_impl(x, (128, 1)) (M = T*C/1024; a group is 8 adjacent channels of
  * one 128-token block row).  T must be a multiple of 128 (PRATCHYA_EINVAL), C of
- * 8 (PRATCHYA_EUNSUPPORTED) and, for an fp8 input, of 128 (PRATCHYA_EINVAL). */
+ * 8 (PRATCHYA_EUNSUPPORTED) and, with input scales, of 128 (PRATCHYA_EINVAL). */
 int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t* x_sc8, const float* x_sc32,
                            int64_t slices, int64_t T, int64_t C, uint8_t* xt_fp8, uint8_t* sc_fp8,
                            float* sc_fp32, hipStream_t stream);

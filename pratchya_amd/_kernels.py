@@ -155,6 +155,38 @@ def quantize_dequantize(x: torch.Tensor, tgrid, dtype: torch.dtype, fix_nan: boo
     return y, sc8.view(E8M0), sc32
 
 
+def requantize_cotangent(g: torch.Tensor, g_sc8: torch.Tensor, g_sc32: torch.Tensor, out=None):
+    """``quantize_impl(dequantize_impl_bwd(g, g_sc8, g_sc32, (1, 128)), (1, 128))``
+    in one pass (pratchya/_qualia/_qarr.py:575-601 then 458-506): the cotangent
+    of a Linear output requantized for the FP8 dgrad.  ``g`` bf16 / f32 with the
+    (1, 128) scales of the tensor it is the cotangent of.  Returns
+    ``(g_fp8, sc_fp8, sc_fp32)`` as ``quantize(g1, (1, 128))``; raises
+    ``PratchyaUnsupported`` unless the layout has 8 blocks per group."""
+    _require_gpu(g, g_sc8, g_sc32)
+    if g.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"requantize_cotangent: dtype {g.dtype} is not float32 or bfloat16")
+    S, H, W = slices_hw(g.shape)
+    n_blk, K, M = group_layout(H, W, (1, 128))
+    lead = tuple(g.shape[:-2]) if g.dim() >= 2 else ()
+    if not g.is_contiguous() or not _aligned(g, 16):
+        g = g.contiguous() if not g.is_contiguous() else g.clone()
+    gs8, gs32 = _u8(g_sc8).contiguous(), g_sc32.contiguous().float()
+    if gs8.numel() != S * n_blk or gs32.numel() != S * M:
+        raise ValueError("requantize_cotangent: scales do not match a (1, 128) quantization of g's shape")
+    if out is None:
+        x8 = torch.empty(g.shape, dtype=torch.uint8, device=g.device)
+        sc8 = torch.empty(lead + (M, K), dtype=torch.uint8, device=g.device)
+        sc32 = torch.empty(lead + (M, 1, 1), dtype=torch.float32, device=g.device)
+    else:
+        _check_out(out, [(g.shape, 1), (lead + (M, K), 1), (lead + (M, 1, 1), 4)], "requantize_cotangent")
+        x8, sc8, sc32 = _u8(out[0]), _u8(out[1]), out[2]
+    lib = _lib.load()
+    _lib.check(lib.pratchya_requantize_cotangent(_ptr(g), _dtype_code(g.dtype), _ptr(gs8), _ptr(gs32), S, H, W,
+                                                 _ptr(x8), _ptr(sc8), _ptr(sc32), _stream(g)),
+               "requantize_cotangent")
+    return x8.view(E4M3), sc8.view(E8M0), sc32
+
+
 def _u8(t: torch.Tensor) -> torch.Tensor:
     return t.view(torch.uint8) if t.dtype != torch.uint8 else t
 
@@ -165,7 +197,9 @@ def quantize_t128(x: torch.Tensor, x_sc8: torch.Tensor = None, x_sc32: torch.Ten
 
     ``x``: [..., T, C] bf16 or f32, or an e4m3fn payload quantized with tgrid
     (1, 128) whose scales are ``x_sc8`` / ``x_sc32`` (dequantized to f32 first,
-    as ``dequantize_impl`` does).  Returns ``(xt_fp8 [..., C, T] e4m3fn,
+    as ``dequantize_impl`` does).  A bf16 ``x`` given with scales is the
+    cotangent of a tensor quantized (1, 128) with them: it goes through
+    ``dequantize_impl_bwd`` (Q:575-601) first, in registers.  Returns ``(xt_fp8 [..., C, T] e4m3fn,
     sc_fp8 [..., M, 8] e8m0, sc_fp32 [..., M, 1, 1] f32)``: the scales are
     exactly ``quantize_impl(x, (128, 1))``'s, the payload is its payload with
     the last two axes swapped.  ``out`` may hold preallocated buffers.
@@ -184,7 +218,13 @@ def quantize_t128(x: torch.Tensor, x_sc8: torch.Tensor = None, x_sc32: torch.Ten
         code = _lib.DT_E4M3
         xs8, xs32 = _u8(x_sc8).contiguous(), x_sc32.contiguous().float()
         xin = _u8(x)
+    elif x.dtype == torch.bfloat16 and x_sc8 is not None and x_sc32 is not None:
+        code = _lib.DT_BF16
+        xs8, xs32 = _u8(x_sc8).contiguous(), x_sc32.contiguous().float()
+        xin = x
     else:
+        if x_sc8 is not None or x_sc32 is not None:
+            raise ValueError("input scales apply to an fp8 payload or a bf16 cotangent only")
         code = _dtype_code(x.dtype if x.dtype in (torch.float32, torch.bfloat16) else torch.float32)
         xin = x if x.dtype in (torch.float32, torch.bfloat16) else x.float()
         xs8 = xs32 = None

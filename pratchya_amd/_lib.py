@@ -35,6 +35,8 @@ SIGNATURES = {
     "pratchya_quantize_dequantize": (_c_int, [_c_p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                               _c_p, _c_int, _c_int, _c_p, _c_p, _c_p, ctypes.c_size_t,
                                               _c_p]),
+    "pratchya_requantize_cotangent": (_c_int, [_c_p, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64,
+                                               _c_p, _c_p, _c_p, _c_p]),
     "pratchya_dequantize": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                      _c_p, _c_int, _c_p]),
     "pratchya_dequantize_bwd": (_c_int, [_c_p, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,

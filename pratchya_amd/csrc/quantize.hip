@@ -216,16 +216,21 @@ __global__ __launch_bounds__(256) void k_quant_rowgroup(
 // dequantize_impl computes it, (f32(q) * (2^(e-127) * G)) / 128 -- the fake
 // quantization QArrayImpl(x).astype(dtype).  FIXNAN dequantizes a NaN e8m0
 // (0xFF) as 1.0 (0x7F), quantize_impl's backward repair of a cotangent; the
-// stored e8m0 bytes are never repaired.
+// stored e8m0 bytes are never repaired.  PRE: x is a cotangent of a tensor
+// quantized with the same (1, 128) grid, whose scales psc8 / psc32 apply
+// dequantize_impl_bwd first ((x * 2^(e-127) * G) / 128 in x's dtype,
+// _qarr.py:575-601), in registers.
 // --------------------------------------------------------------------------
 constexpr int kRawBuffer = 0x00020000;            // raw buffer resource, 32-bit data format
 constexpr int kOutOfRange = (int)0xFFFFFFF0u;     // buffer offset past any scale array
 
-template <bool IS_BF16, bool HW, int OUT, bool FIXNAN>
+template <bool IS_BF16, bool HW, int OUT, bool FIXNAN, bool PRE>
 __global__ __launch_bounds__(256) void k_quant_g8(const void* __restrict__ xv,
                                                   void* __restrict__ outv,
                                                   uint8_t* __restrict__ sc8,
-                                                  float* __restrict__ sc32, int64_t n_groups) {
+                                                  float* __restrict__ sc32, int64_t n_groups,
+                                                  const uint8_t* __restrict__ psc8,
+                                                  const float* __restrict__ psc32) {
   constexpr int VEC = IS_BF16 ? 8 : 4;        // elements per 16-byte load
   constexpr int R = IS_BF16 ? 2 : 4;          // 64-lane rows per 1024-element group
   constexpr int BL = 128 / VEC;               // lanes per block
@@ -252,6 +257,29 @@ __global__ __launch_bounds__(256) void k_quant_g8(const void* __restrict__ xv,
 #pragma unroll
       for (int r = 0; r < R; ++r)
         nxt[r] = load_stream16(xb + (g + wstride) * GROUP_BYTES + (r * 64 + lane) * 16);
+    }
+    if constexpr (PRE) {
+      // the group's 8 e8m0 bytes and G (wave-uniform); block of this lane's
+      // row r: r * BPR + lane / BL
+      const uint64_t e8w = *reinterpret_cast<const uint64_t*>(psc8 + g * 8);
+      const float Gp = psc32[g];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int k = r * BPR + lane / BL;
+        const float dq = e8m0_decode((uint32_t)(e8w >> (8 * k)) & 0xFFu) * Gp;
+        uint32_t wv[4] = {v[r].x, v[r].y, v[r].z, v[r].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (IS_BF16) {
+            const float lo = (u2f(wv[i] << 16) * dq) * 0.0078125f;
+            const float hi = (u2f(wv[i] & 0xFFFF0000u) * dq) * 0.0078125f;
+            wv[i] = pack_bf16x2(lo, hi);
+          } else {
+            wv[i] = f2u((u2f(wv[i]) * dq) * 0.0078125f);
+          }
+        }
+        v[r] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+      }
     }
 
     // block maxima (every lane of a block holds its block's max) and group max
@@ -761,13 +789,13 @@ bool use_g8(const Layout& L, bool bf16, const void* x, const void* q, const void
 #define PRATCHYA_G8_MAX_BLOCKS (1 << 30)
 #endif
 
-template <bool IS_BF16, int OUT, bool FIXNAN>
+template <bool IS_BF16, int OUT, bool FIXNAN, bool PRE = false>
 void launch_g8_t(const void* x, void* out, uint8_t* sc8, float* sc32, int64_t n_groups,
-                 hipStream_t st) {
+                 hipStream_t st, const uint8_t* psc8 = nullptr, const float* psc32 = nullptr) {
   int64_t blocks = (n_groups + 3) / 4;
   if (blocks > PRATCHYA_G8_MAX_BLOCKS) blocks = PRATCHYA_G8_MAX_BLOCKS;
-  hipLaunchKernelGGL((k_quant_g8<IS_BF16, PRATCHYA_HW_CVT != 0, OUT, FIXNAN>), dim3((unsigned)blocks),
-                     dim3(256), 0, st, x, out, sc8, sc32, n_groups);
+  hipLaunchKernelGGL((k_quant_g8<IS_BF16, PRATCHYA_HW_CVT != 0, OUT, FIXNAN, PRE>), dim3((unsigned)blocks),
+                     dim3(256), 0, st, x, out, sc8, sc32, n_groups, psc8, psc32);
 }
 
 int launch_g8(bool bf16, const void* x, uint8_t* q, uint8_t* sc8, float* sc32, int64_t n_groups,
@@ -902,6 +930,31 @@ extern "C" int pratchya_quantize_dequantize(const void* x, int x_dtype, int64_t 
                  : launch_general<true, 2>(x, out, sc_fp8, sc_fp32, ws, L, stream, f);
   return obf16 ? launch_general<false, 1>(x, out, sc_fp8, sc_fp32, ws, L, stream, f)
                : launch_general<false, 2>(x, out, sc_fp8, sc_fp32, ws, L, stream, f);
+}
+
+extern "C" int pratchya_requantize_cotangent(const void* g, int g_dtype, const uint8_t* g_sc8,
+                                            const float* g_sc32, int64_t slices, int64_t H, int64_t W,
+                                            uint8_t* x_fp8, uint8_t* sc_fp8, float* sc_fp32,
+                                            hipStream_t stream) {
+  Layout L;
+  int rc = make_layout(slices, H, W, 1, 128, &L);
+  if (rc) return rc;
+  if (g_dtype != PRATCHYA_DT_F32 && g_dtype != PRATCHYA_DT_BF16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "requantize_cotangent: unsupported dtype %d", g_dtype);
+  const int64_t n = L.n();
+  if (n == 0) {
+    g_err[0] = 0;
+    return PRATCHYA_OK;
+  }
+  if (!g || !g_sc8 || !g_sc32 || !x_fp8 || !sc_fp8 || !sc_fp32)
+    return pratchya_set_error(PRATCHYA_EINVAL, "requantize_cotangent: null buffer");
+  const bool bf16 = g_dtype == PRATCHYA_DT_BF16;
+  if (!use_g8(L, bf16, g, x_fp8, sc_fp8) || !aligned(g_sc8, 8) || !aligned(g_sc32, 4))
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED,
+                              "requantize_cotangent: needs 8 blocks per group and aligned buffers");
+  if (bf16) launch_g8_t<true, 0, false, true>(g, x_fp8, sc_fp8, sc_fp32, n / 1024, stream, g_sc8, g_sc32);
+  else launch_g8_t<false, 0, false, true>(g, x_fp8, sc_fp8, sc_fp32, n / 1024, stream, g_sc8, g_sc32);
+  return check_launch("requantize_cotangent");
 }
 
 namespace {

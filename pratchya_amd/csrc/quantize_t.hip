@@ -37,7 +37,10 @@ int pratchya_set_error(int code, const char* fmt, ...);
 namespace {
 
 constexpr int TOK = 16;                     // consecutive tokens per lane
-enum { IN_F32 = 0, IN_BF16 = 1, IN_FP8 = 2 };
+// IN_BF16S: a bf16 cotangent g of a (1, 128)-quantized tensor, taken through
+// dequantize_impl_bwd with that tensor's scales (bf16((g * 2^(e-127) * G) / 128),
+// _qarr.py:575-601) in registers before it is requantized.
+enum { IN_F32 = 0, IN_BF16 = 1, IN_FP8 = 2, IN_BF16S = 3 };
 
 // Calls f(std::integral_constant<int, i>) for i = 0 .. N-1 (compile-time
 // channel indices, so per-channel helpers can take them as template arguments).
@@ -51,7 +54,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 template <int IN>
 struct InTraits {
-  static constexpr int ESZ = IN == IN_F32 ? 4 : (IN == IN_BF16 ? 2 : 1);
+  static constexpr int ESZ = IN == IN_F32 ? 4 : ((IN == IN_BF16 || IN == IN_BF16S) ? 2 : 1);
   static constexpr int NW = 2 * ESZ;        // 32-bit words holding 8 channels
 };
 
@@ -63,7 +66,7 @@ __device__ __forceinline__ void load_row(const uint8_t* p, uint32_t (&w)[InTrait
     const uint4 b = load_stream16(reinterpret_cast<const char*>(p) + 16);
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
     w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
-  } else if constexpr (IN == IN_BF16) {
+  } else if constexpr (IN == IN_BF16 || IN == IN_BF16S) {
     const uint4 a = load_stream16(reinterpret_cast<const char*>(p));
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
   } else {
@@ -128,7 +131,7 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
   float dq[TOK];
 #pragma unroll
   for (int r = 0; r < TOK; ++r) dq[r] = 1.0f;
-  if constexpr (IN == IN_FP8) {
+  if constexpr (IN == IN_FP8 || IN == IN_BF16S) {
     // (1, 128) scales of the stored payload: block (t, c / 128) of the slice;
     // a slice holds a whole number of groups (kg | T * C / 128), so the group
     // of a block is its slice-global index >> kg_shift.  32-bit indices: the
@@ -141,6 +144,19 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
       dq[r] = e8m0_decode(x_sc8[blk]) * x_sc32[blk >> kg_shift];
     }
   }
+  if constexpr (IN == IN_BF16S) {
+    // the cotangent's dequantize_impl_bwd, in place: from here on the rows are
+    // plain bf16 values
+#pragma unroll
+    for (int r = 0; r < TOK; ++r)
+#pragma unroll
+      for (int k = 0; k < NW; ++k) {
+        const float lo = (u2f(w[r][k] << 16) * dq[r]) * 0.0078125f;
+        const float hi = (u2f(w[r][k] & 0xFFFF0000u) * dq[r]) * 0.0078125f;
+        w[r][k] = pack_bf16x2(lo, hi);
+      }
+  }
+  constexpr int INC = IN == IN_BF16S ? IN_BF16 : IN;   // element kind after the prologue
 
   // channel maxima (as |x| bits: unsigned order, NaN above inf) and group max
   uint32_t mx[8];
@@ -148,7 +164,7 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
     constexpr int j = decltype(jc)::value;
     uint32_t m = 0;
 #pragma unroll
-    for (int r = 0; r < TOK; ++r) m = umax(m, row_abs_bits<IN, j>(w[r], dq[r]));
+    for (int r = 0; r < TOK; ++r) m = umax(m, row_abs_bits<INC, j>(w[r], dq[r]));
     m = umax(m, shfl_xor_u32(m, 8));
     m = umax(m, shfl_xor_u32(m, 16));
     m = umax(m, shfl_xor_u32(m, 32));
@@ -177,7 +193,7 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
     y[j] = cl ? PRATCHYA_Y_CLAMP : u2f((254u - e[j]) << 23) * rcpG128;
     clamped |= cl ? 1u : 0u;
   }
-  const bool check = IN != IN_BF16 || __any(clamped);
+  const bool check = INC != IN_BF16 || __any(clamped);
 
   uint8_t* qo = qt + (s * C + c0) * T + t0;
   static_for<8>([&](auto jc) {
@@ -186,10 +202,10 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
     uint32_t near = 0;
 #pragma unroll
     for (int k = 0; k < TOK / 4; ++k) {
-      const float t0v = row_elem<IN, j>(w[4 * k + 0], dq[4 * k + 0]) * y[j];
-      const float t1v = row_elem<IN, j>(w[4 * k + 1], dq[4 * k + 1]) * y[j];
-      const float t2v = row_elem<IN, j>(w[4 * k + 2], dq[4 * k + 2]) * y[j];
-      const float t3v = row_elem<IN, j>(w[4 * k + 3], dq[4 * k + 3]) * y[j];
+      const float t0v = row_elem<INC, j>(w[4 * k + 0], dq[4 * k + 0]) * y[j];
+      const float t1v = row_elem<INC, j>(w[4 * k + 1], dq[4 * k + 1]) * y[j];
+      const float t2v = row_elem<INC, j>(w[4 * k + 2], dq[4 * k + 2]) * y[j];
+      const float t3v = row_elem<INC, j>(w[4 * k + 3], dq[4 * k + 3]) * y[j];
       if (check) near |= near_mid8(t0v) | near_mid8(t1v) | near_mid8(t2v) | near_mid8(t3v);
       o[k] = cvt4<HW>(t0v, t1v, t2v, t3v);
     }
@@ -197,10 +213,10 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
       const float S = quant_scale(e[j], G);
 #pragma unroll
       for (int k = 0; k < TOK / 4; ++k)
-        o[k] = cvt4_exact(row_elem<IN, j>(w[4 * k + 0], dq[4 * k + 0]),
-                          row_elem<IN, j>(w[4 * k + 1], dq[4 * k + 1]),
-                          row_elem<IN, j>(w[4 * k + 2], dq[4 * k + 2]),
-                          row_elem<IN, j>(w[4 * k + 3], dq[4 * k + 3]), S);
+        o[k] = cvt4_exact(row_elem<INC, j>(w[4 * k + 0], dq[4 * k + 0]),
+                          row_elem<INC, j>(w[4 * k + 1], dq[4 * k + 1]),
+                          row_elem<INC, j>(w[4 * k + 2], dq[4 * k + 2]),
+                          row_elem<INC, j>(w[4 * k + 3], dq[4 * k + 3]), S);
     }
     const u32x4_t v = {o[0], o[1], o[2], o[3]};
     __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(qo + (int64_t)j * T));
@@ -237,8 +253,10 @@ extern "C" int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t*
   if (T % 128)
     return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t128: tgrid (128, 1) does not divide %lld tokens",
                               (long long)T);
-  if (x_dtype == PRATCHYA_DT_E4M3 && C % 128)
-    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t128: tgrid (1, 128) of the fp8 input does not divide "
+  // an fp8 payload, or a bf16 cotangent given with scales: (1, 128) input scales
+  const bool scaled = x_dtype == PRATCHYA_DT_E4M3 || (x_dtype == PRATCHYA_DT_BF16 && x_sc8 && x_sc32);
+  if (scaled && C % 128)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t128: tgrid (1, 128) of the input scales does not divide "
                               "%lld channels", (long long)C);
   if (slices == 0 || T == 0 || C == 0) return PRATCHYA_OK;
   if (C % 8)
@@ -252,20 +270,23 @@ extern "C" int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t*
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t128: buffers are not aligned");
   if (T / 128 > 65535 || slices > 65535)
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t128: too many token blocks or slices");
-  if (x_dtype == PRATCHYA_DT_E4M3 && (slices * T) * (C / 128) >= ((int64_t)1 << 32))
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t128: fp8 input scales beyond 2^32 blocks");
+  if (scaled && (slices * T) * (C / 128) >= ((int64_t)1 << 32))
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t128: input scales beyond 2^32 blocks");
   const dim3 grid((unsigned)((C + 255) / 256), (unsigned)(T / 128), (unsigned)slices);
   const uint8_t* xb = static_cast<const uint8_t*>(x);
-  if (x_dtype == PRATCHYA_DT_BF16) {
+  // blocks per group of a (1, 128) input: gcd(8, n_blk), a power of two
+  const int64_t kg = scaled ? gcd64(8, T * (C / 128)) : 1;
+  const int kg_shift = kg == 8 ? 3 : (kg == 4 ? 2 : (kg == 2 ? 1 : 0));
+  if (x_dtype == PRATCHYA_DT_BF16 && scaled) {
+    hipLaunchKernelGGL((k_quant_t128<IN_BF16S, true>), grid, dim3(256), 0, stream, xb, x_sc8, x_sc32, kg_shift,
+                       T, C, xt_fp8, sc_fp8, sc_fp32);
+  } else if (x_dtype == PRATCHYA_DT_BF16) {
     hipLaunchKernelGGL((k_quant_t128<IN_BF16, true>), grid, dim3(256), 0, stream, xb, nullptr, nullptr, 0,
                        T, C, xt_fp8, sc_fp8, sc_fp32);
   } else if (x_dtype == PRATCHYA_DT_F32) {
     hipLaunchKernelGGL((k_quant_t128<IN_F32, true>), grid, dim3(256), 0, stream, xb, nullptr, nullptr, 0,
                        T, C, xt_fp8, sc_fp8, sc_fp32);
   } else {
-    // blocks per group of the (1, 128) input: gcd(8, n_blk), a power of two
-    const int64_t kg = gcd64(8, T * (C / 128));
-    const int kg_shift = kg == 8 ? 3 : (kg == 4 ? 2 : (kg == 2 ? 1 : 0));
     hipLaunchKernelGGL((k_quant_t128<IN_FP8, true>), grid, dim3(256), 0, stream, xb, x_sc8, x_sc32, kg_shift,
                        T, C, xt_fp8, sc_fp8, sc_fp32);
   }

@@ -207,9 +207,11 @@ def _matmul_forward(x8, xs8, xs32, y8, ys8, ys32, gx, gy) -> torch.Tensor:
     return torch.matmul(_deq32(x8, xs8, xs32, gx), _deq32(y8, ys8, ys32, gy))
 
 
-def _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y):
+def _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y, pre=None):
     """dgrad / wgrad on the FP8 MFMA kernel (the "fp8" backward), or None
-    when the layouts do not fit it."""
+    when the layouts do not fit it.  ``pre``: the (1, 128) scales of the
+    product's output quantization when ``g`` is the cotangent of that output
+    before dequantize_impl_bwd (the quantizers apply it in registers)."""
     if y8.dim() != 2 or tuple(gx) != (1, 128) or tuple(gy)[1] != 128:
         return None
     if _lhs_operand(x8, xs8, xs32, gx) is None:
@@ -222,13 +224,13 @@ def _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y):
     gxf = gyf = None
     try:
         if need_x:
-            gq = K.quantize(g2.contiguous(), (1, 128))
+            gq = K.requantize_cotangent(g2, *pre) if pre is not None else K.quantize(g2.contiguous(), (1, 128))
             op_g = K.operand_rows(*gq, (1, 128))
             op_w = K.operand_rows(y8, ys8, ys32, gy)          # W [K, N]: rows K, contraction N
             gxf = K.gemm_nt(op_g, op_w, torch.float32).reshape(tuple(g.shape[:-1]) + (Kd,))
         if need_y:
             xt = K.quantize_t128(x8.reshape(rows, Kd), xs8, xs32)   # stored activation, requantized
-            gt = K.quantize_t128(g2.contiguous())
+            gt = K.quantize_t128(g2.contiguous(), *(pre if pre is not None else ()))
             gyf = K.gemm_nt(K.operand_t128(*xt), K.operand_t128(*gt), torch.float32)
     except K.PratchyaUnsupported:
         return None
@@ -304,8 +306,19 @@ class _QLinear(torch.autograd.Function):
         gx, gy, go = ctx.grids
         os8, os32 = ctx.out_scales
         need_x, need_y = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        g1 = K.dequantize_bwd(g.contiguous(), os8, os32, go)
-        gxf, gyf = _matmul_cotangents(g1, ctx.saved, (gx, gy), need_x, need_y)
+        g = g.contiguous()
+        res = None
+        if (_backward_mode == "fp8" and tuple(go) == (1, 128) and g.dtype == torch.bfloat16
+                and int(os8.shape[-1]) == 8):
+            # the FP8 dgrad / wgrad quantizers take the cotangent through the
+            # output's dequantize_impl_bwd themselves (8-block groups: the
+            # output's scales index the same way for the flattened rows)
+            res = _fp8_backward(g, *ctx.saved, gx, gy, need_x, need_y, pre=(os8, os32))
+        if res is not None:
+            gxf, gyf = res
+        else:
+            g1 = K.dequantize_bwd(g, os8, os32, go)
+            gxf, gyf = _matmul_cotangents(g1, ctx.saved, (gx, gy), need_x, need_y)
         grad_x = grad_y = None
         if need_x:
             grad_x = _requant_cotangent(_reduce_broadcast(gxf, x8.shape), gx, ctx.dtypes[0])

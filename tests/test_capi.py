@@ -145,3 +145,13 @@ def test_quantize_dequantize_codes_without_gpu():
     assert f(*args(_lib.DT_F32, 8, 128, 1, 128, _lib.DT_E4M3)) == _lib.EINVAL
     assert f(*args(_lib.DT_F32, 0, 128, 1, 128, _lib.DT_F32)) == _lib.OK
     assert f(*args(_lib.DT_F32, 8, 128, 1, 128, _lib.DT_F32)) == _lib.EINVAL      # null buffers
+
+
+def test_requantize_cotangent_codes_without_gpu():
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    f = lib.pratchya_requantize_cotangent
+    assert f(None, _lib.DT_BF16, None, None, 1, 10, 100, None, None, None, None) == _lib.EINVAL   # 128 does not divide 100
+    assert f(None, 7, None, None, 1, 8, 1024, None, None, None, None) == _lib.EINVAL
+    assert f(None, _lib.DT_BF16, None, None, 1, 0, 1024, None, None, None, None) == _lib.OK
+    assert f(None, _lib.DT_BF16, None, None, 1, 8, 1024, None, None, None, None) == _lib.EINVAL  # null buffers

@@ -4,7 +4,9 @@ Expected values: the oracle's dequantize_impl(*quantize_impl(x, tgrid), dtype,
 tgrid) -- QArrayImpl(x, tgrid).astype(dtype) -- and, with fix_nan, the same
 with NaN e8m0 bytes replaced by 0x7F first (quantize_impl's backward,
 pratchya/_qualia/_qarr.py:512-526).  Bit-exact outputs (NaN compared as
-NaN-ness) and bit-exact scales.
+NaN-ness) and bit-exact scales.  Also the one-pass requantization of a
+Linear output's cotangent, pratchya_requantize_cotangent, against
+quantize_impl(dequantize_bwd(g)).
 """
 import ctypes
 
@@ -13,8 +15,8 @@ import pytest
 import torch
 
 from oracle import qarr_oracle as O
-from tests.helpers import (assert_bytes_equal, assert_f32_bits_equal, f32, to_dev_bf16,
-                           to_dev_f32, u8)
+from tests.helpers import (assert_bytes_equal, assert_f32_bits_equal, assert_payload_equal, f32,
+                           to_dev_bf16, to_dev_f32, u8)
 from tests.test_gpu_quantize import edge_tensor
 
 pytestmark = pytest.mark.gpu
@@ -150,3 +152,42 @@ def test_argument_errors():
         K.quantize_dequantize(x, (1, 128), torch.float16)
     with pytest.raises(ValueError, match="does not divide"):
         K.quantize_dequantize(x, (1, 96), torch.float32)
+
+
+@pytest.mark.parametrize("gdt", ["bfloat16", "float32"])
+@pytest.mark.parametrize("shape", [(256, 1024), (2, 128, 512)])
+def test_requantize_cotangent(gdt, shape):
+    """quantize_impl(dequantize_impl_bwd(g, s8, s32, (1, 128)), (1, 128)) in one
+    pass, bit-exact, including zero and NaN e8m0 scales and NaN / inf
+    cotangent elements."""
+    rng = np.random.default_rng(41)
+    y = (rng.standard_normal(shape) * 5).astype(np.float32)
+    _, s8, s32 = O.quantize_impl(y, (1, 128))
+    s8 = s8.copy()
+    s8.reshape(-1)[3] = 0
+    s8.reshape(-1)[11] = 0xFF
+    g = (rng.standard_normal(shape) * 1e-3).astype(np.float32)
+    g.reshape(-1)[100] = np.nan
+    g.reshape(-1)[2000] = np.inf
+    if gdt == "bfloat16":
+        gb = O.f32_to_bf16_bits(g)
+        g = O.bf16_bits_to_f32(gb)
+        dev = to_dev_bf16(gb)
+        g1 = O.bf16_bits_to_f32(O.dequantize_bwd(g, s8, s32, (1, 128), "bfloat16"))
+    else:
+        dev = to_dev_f32(g)
+        g1 = O.dequantize_bwd(g, s8, s32, (1, 128), "float32")
+    q8, q_s8, q_s32 = _K().requantize_cotangent(dev, torch.from_numpy(s8).cuda(), torch.from_numpy(s32).cuda())
+    torch.cuda.synchronize()
+    r8, rs8, rs32 = O.quantize_impl(g1, (1, 128))
+    assert_payload_equal(u8(q8), r8, f"{gdt}{shape} payload")
+    assert_bytes_equal(u8(q_s8), rs8, f"{gdt}{shape} e8m0")
+    assert_f32_bits_equal(f32(q_s32), rs32, f"{gdt}{shape} G")
+
+
+def test_requantize_cotangent_unsupported_layout():
+    from pratchya_amd._lib import PratchyaUnsupported
+    g = torch.zeros((4, 128), dtype=torch.bfloat16, device="cuda")   # 4 blocks: K = 4
+    with pytest.raises(PratchyaUnsupported):
+        _K().requantize_cotangent(g, torch.zeros((1, 4), dtype=torch.uint8, device="cuda"),
+                                  torch.ones((1, 1, 1), device="cuda"))

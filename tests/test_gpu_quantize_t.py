@@ -146,3 +146,27 @@ def test_argument_errors():
     from pratchya_amd._lib import PratchyaError
     with pytest.raises(PratchyaError, match="multiple of 8"):
         K.quantize_t128(torch.zeros((128, 12), dtype=torch.bfloat16, device="cuda"))
+
+
+@pytest.mark.parametrize("T,C", [(256, 256), (384, 1024)])
+def test_bf16_cotangent_with_output_scales(T, C):
+    """A bf16 cotangent g of a (1, 128)-quantized tensor, given with that
+    tensor's scales: dequantize_impl_bwd (bf16((g * 2^(e-127) * G) / 128))
+    is applied before the token-axis requantization."""
+    rng = np.random.default_rng(31)
+    y = (rng.standard_normal((T, C)) * 3).astype(np.float32)
+    _, s8, s32 = O.quantize_impl(y, (1, 128))
+    s8 = s8.copy()
+    s8.reshape(-1)[5] = 0                      # a zero e8m0 (dq = 0) and a NaN one
+    s8.reshape(-1)[9] = 0xFF
+    gb = O.f32_to_bf16_bits((rng.standard_normal((T, C)) * 1e-3).astype(np.float32))
+    gb[3, 17] = 0x7FC0                          # NaN cotangent element
+    g1 = O.bf16_bits_to_f32(O.dequantize_bwd(O.bf16_bits_to_f32(gb), s8, s32, (1, 128), "bfloat16"))
+    check(to_dev_bf16(gb), g1, f"bf16 cotangent [{T},{C}]", torch.from_numpy(s8).cuda(),
+          torch.from_numpy(s32).cuda())
+
+
+def test_scales_rejected_for_f32_input():
+    x = torch.zeros((128, 128), device="cuda")
+    with pytest.raises(ValueError, match="input scales"):
+        _K().quantize_t128(x, torch.zeros(16, dtype=torch.uint8, device="cuda"), torch.ones(2, device="cuda"))

@@ -441,23 +441,46 @@ __device__ __forceinline__ float load_elem(const void* x, int64_t i) {
   else return static_cast<const float*>(x)[i];
 }
 
-// Block amax: thread per chunk of CH consecutive elements of one row (CH | b).
-// Lanes of an aligned group of b/CH lanes cover one block row segment and are
-// combined by shuffles when b/CH is a power of two <= 64 (seg_log2 >= 0).
-template <bool IS_BF16, int CH>
+// CH consecutive elements at element offset off, as f32; VEC: one 16-byte
+// load (the host checks the alignment).
+template <bool IS_BF16, int CH, bool VEC>
+__device__ __forceinline__ void load_chunk(const void* x, int64_t off, float (&v)[CH]) {
+  if constexpr (VEC) {
+    static_assert(CH * (IS_BF16 ? 2 : 4) == 16, "a vector chunk is 16 bytes");
+    const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const char*>(x) + off * (IS_BF16 ? 2 : 4));
+#pragma unroll
+    for (int k = 0; k < CH; ++k) v[k] = elem_f32<IS_BF16>(w, k);
+  } else {
+#pragma unroll
+    for (int k = 0; k < CH; ++k) v[k] = load_elem<IS_BF16>(x, off + k);
+  }
+}
+
+// Block amax: thread per chunk of CH consecutive elements (CH | b) in each of
+// `rows` consecutive rows of one block row (rows | a), so a thread folds
+// rows x CH elements before any atomic.  Lanes of an aligned group of b/CH
+// lanes cover one block's columns and are combined by shuffles when b/CH is a
+// power of two <= 64 (seg_log2 >= 0): one atomic per block and row chunk.
+template <bool IS_BF16, int CH, bool VEC>
 __global__ __launch_bounds__(256) void k_blockmax(const void* __restrict__ x,
-                                                  uint32_t* __restrict__ ws, int64_t n_chunks,
-                                                  int64_t W, int64_t a, int64_t b, int seg_log2) {
+                                                  uint32_t* __restrict__ ws, int64_t n_threads,
+                                                  int64_t W, int64_t a, int64_t b, int seg_log2,
+                                                  int rows) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const bool live = t < n_chunks;
+  const bool live = t < n_threads;
   uint32_t m = 0;
   int64_t blk = 0;
   if (live) {
-    const int64_t off = t * CH;
-    const int64_t i = off / W, c = off - i * W;
+    const int64_t cpr = W / CH;                   // chunks per row
+    const int64_t rg = t / cpr, c = (t - rg * cpr) * CH;
+    const int64_t i0 = rg * rows;                 // first row (slices stacked: a | H)
+    for (int r = 0; r < rows; ++r) {
+      float v[CH];
+      load_chunk<IS_BF16, CH, VEC>(x, (i0 + r) * W + c, v);
 #pragma unroll
-    for (int k = 0; k < CH; ++k) m = umax(m, abs_bits(load_elem<IS_BF16>(x, off + k)));
-    blk = (i / a) * (W / b) + c / b;
+      for (int k = 0; k < CH; ++k) m = umax(m, abs_bits(v[k]));
+    }
+    blk = (i0 / a) * (W / b) + c / b;
   }
   if (seg_log2 >= 0) {
     const int seg = 1 << seg_log2;
@@ -504,7 +527,8 @@ __global__ __launch_bounds__(256) void k_group_scales_small(const uint32_t* __re
 // OUT 0 writes the payload; OUT 1 / 2 write it dequantized as bf16 / f32
 // (fake quantization, with the NaN-e8m0 repair when fix_nan is set), as the
 // group-per-wave kernel's modes.
-template <bool IS_BF16, int CH, int OUT>
+// VEC: 16-byte input loads and one vector store per chunk (host-checked alignment).
+template <bool IS_BF16, int CH, int OUT, bool VEC>
 __global__ __launch_bounds__(256) void k_cast_general(const void* __restrict__ x,
                                                       void* __restrict__ outv,
                                                       const uint8_t* __restrict__ sc8,
@@ -523,21 +547,49 @@ __global__ __launch_bounds__(256) void k_cast_general(const void* __restrict__ x
   const bool ok = sG >= kClamp && sG <= 3.0e38f;
   const float yv = 128.0f / S;
   const float dq = e8m0_decode((fix_nan && e == 0xFFu) ? 0x7Fu : e) * G;
+  float xv[CH];
+  load_chunk<IS_BF16, CH, VEC>(x, off, xv);
+  uint32_t ov[CH];                              // output element bits
 #pragma unroll
   for (int k = 0; k < CH; ++k) {
-    const float xv = load_elem<IS_BF16>(x, off + k);
     uint32_t code;
-    const float tv = xv * yv;
+    const float tv = xv[k] * yv;
     if (ok && (IS_BF16 || !near_bf16_midpoint(tv)))
       code = bf16_to_e4m3fn(f32_to_bf16_rne_nonan(tv));
     else
-      code = quant_elem_exact(xv, S);
+      code = quant_elem_exact(xv[k], S);
     if constexpr (OUT == 0) {
-      static_cast<uint8_t*>(outv)[off + k] = (uint8_t)code;
+      ov[k] = code;
     } else {
       const float d = (e4m3fn_to_f32(code) * dq) * 0.0078125f;
-      if constexpr (OUT == 1) static_cast<uint16_t*>(outv)[off + k] = (uint16_t)f32_to_bf16_rne(d);
-      else static_cast<float*>(outv)[off + k] = d;
+      ov[k] = OUT == 1 ? f32_to_bf16_rne(d) : f2u(d);
+    }
+  }
+  if constexpr (VEC && OUT == 0) {
+    uint32_t w[CH / 4];
+#pragma unroll
+    for (int i = 0; i < CH / 4; ++i)
+      w[i] = ov[4 * i] | (ov[4 * i + 1] << 8) | (ov[4 * i + 2] << 16) | (ov[4 * i + 3] << 24);
+    if constexpr (CH == 8) *reinterpret_cast<uint2*>(static_cast<uint8_t*>(outv) + off) = make_uint2(w[0], w[1]);
+    else *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(outv) + off) = w[0];
+  } else if constexpr (VEC && OUT == 1) {
+    uint32_t w[CH / 2];
+#pragma unroll
+    for (int i = 0; i < CH / 2; ++i) w[i] = ov[2 * i] | (ov[2 * i + 1] << 16);
+    uint16_t* o = static_cast<uint16_t*>(outv) + off;
+    if constexpr (CH == 8) *reinterpret_cast<uint4*>(o) = make_uint4(w[0], w[1], w[2], w[3]);
+    else *reinterpret_cast<uint2*>(o) = make_uint2(w[0], w[1]);
+  } else if constexpr (VEC && OUT == 2) {
+    float* o = static_cast<float*>(outv) + off;
+#pragma unroll
+    for (int i = 0; i < CH / 4; ++i)
+      *reinterpret_cast<uint4*>(o + 4 * i) = make_uint4(ov[4 * i], ov[4 * i + 1], ov[4 * i + 2], ov[4 * i + 3]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      if constexpr (OUT == 0) static_cast<uint8_t*>(outv)[off + k] = (uint8_t)ov[k];
+      else if constexpr (OUT == 1) static_cast<uint16_t*>(outv)[off + k] = (uint16_t)ov[k];
+      else static_cast<float*>(outv)[off + k] = u2f(ov[k]);
     }
   }
 }
@@ -743,14 +795,24 @@ int launch_general(const void* x, void* q, uint8_t* sc8, float* sc32, uint32_t* 
   const int64_t seg = L.b / ch;
   const int seg_log2 = (is_pow2(seg) && seg <= 64) ? ilog2(seg) : -1;
   const unsigned gr = grid_for(n_chunks, 256);
-#define PRATCHYA_BM(C)                                                                            \
-  hipLaunchKernelGGL((k_blockmax<IS_BF16, C>), dim3(gr), dim3(256), 0, st, x, ws, n_chunks, L.W, \
-                     L.a, L.b, seg_log2)
-  switch (ch) {
-    case 1: PRATCHYA_BM(1); break;
-    case 2: PRATCHYA_BM(2); break;
-    case 4: PRATCHYA_BM(4); break;
-    default: PRATCHYA_BM(8); break;
+  // rows folded per block-max thread: the largest power of two <= 16 dividing a
+  int rows = 1;
+  while (rows < 16 && L.a % (rows * 2) == 0) rows *= 2;
+  const int64_t n_bm = n_chunks / rows;
+  // 16-byte input chunks when the input is aligned (f32 x4, bf16 x8)
+  const bool vin = ch == (IS_BF16 ? 8 : 4) && aligned(x, 16);
+#define PRATCHYA_BM(C, V)                                                                        \
+  hipLaunchKernelGGL((k_blockmax<IS_BF16, C, V>), dim3(grid_for(n_bm, 256)), dim3(256), 0, st, x, ws, \
+                     n_bm, L.W, L.a, L.b, seg_log2, rows)
+  if (vin) {
+    PRATCHYA_BM((IS_BF16 ? 8 : 4), true);
+  } else {
+    switch (ch) {
+      case 1: PRATCHYA_BM(1, false); break;
+      case 2: PRATCHYA_BM(2, false); break;
+      case 4: PRATCHYA_BM(4, false); break;
+      default: PRATCHYA_BM(8, false); break;
+    }
   }
 #undef PRATCHYA_BM
   if (L.K >= 32)
@@ -759,14 +821,19 @@ int launch_general(const void* x, void* q, uint8_t* sc8, float* sc32, uint32_t* 
   else
     hipLaunchKernelGGL(k_group_scales_small, dim3(grid_for(n_groups, 256)), dim3(256), 0, st, ws,
                        sc8, sc32, n_groups, L.K);
-#define PRATCHYA_CAST(C)                                                                     \
-  hipLaunchKernelGGL((k_cast_general<IS_BF16, C, OUT>), dim3(gr), dim3(256), 0, st, x, q, sc8, sc32, \
+#define PRATCHYA_CAST(C, V)                                                                    \
+  hipLaunchKernelGGL((k_cast_general<IS_BF16, C, OUT, V>), dim3(gr), dim3(256), 0, st, x, q, sc8, sc32, \
                      n_chunks, L.W, L.a, L.b, L.K, fix_nan)
-  switch (ch) {
-    case 1: PRATCHYA_CAST(1); break;
-    case 2: PRATCHYA_CAST(2); break;
-    case 4: PRATCHYA_CAST(4); break;
-    default: PRATCHYA_CAST(8); break;
+  const int out_esz = OUT == 0 ? 1 : (OUT == 1 ? 2 : 4);
+  if (vin && aligned(q, (size_t)ch * out_esz)) {
+    PRATCHYA_CAST((IS_BF16 ? 8 : 4), true);
+  } else {
+    switch (ch) {
+      case 1: PRATCHYA_CAST(1, false); break;
+      case 2: PRATCHYA_CAST(2, false); break;
+      case 4: PRATCHYA_CAST(4, false); break;
+      default: PRATCHYA_CAST(8, false); break;
+    }
   }
 #undef PRATCHYA_CAST
   return check_launch("quantize(general)");

@@ -14,11 +14,11 @@
 // which is the requantization of a stored activation along the token axis
 // (fp8_matmul's backward, _qarr.py:784-789, quantizes x^T the same way).
 //
-// One wave per 128-token x 64-channel tile.  Lane (rs, cg) = (lane >> 3,
-// lane & 7) holds tokens [16 rs, 16 rs + 16) of the 8 channels of group cg:
-// channel maxima are an in-lane max over 16 tokens plus three xor shuffles
-// across rs, the group max an in-lane max over 8 channels, and each channel's
-// 16 payload bytes are one 16-byte store into the transposed layout.  The cast
+// One wave per 128-token x (8 * CGW)-channel tile.  Lane (rs, cg) holds TOK
+// consecutive tokens (16 or 8) of the 8 channels of group cg: channel maxima
+// are an in-lane max over TOK tokens plus xor shuffles across rs, the group
+// max an in-lane max over 8 channels, and each channel's TOK payload bytes are
+// one 16- or 8-byte store into the transposed layout.  The cast
 // uses the same division-free scheme as the row-group quantizer (exact for
 // bf16 inputs; for f32 / fp8 inputs and clamped blocks every element is
 // checked against the bf16 rounding midpoint, and a lane's 16-element chunk
@@ -36,7 +36,6 @@ int pratchya_set_error(int code, const char* fmt, ...);
 
 namespace {
 
-constexpr int TOK = 16;                     // consecutive tokens per lane
 // IN_BF16S: a bf16 cotangent g of a (1, 128)-quantized tensor, taken through
 // dequantize_impl_bwd with that tensor's scales (bf16((g * 2^(e-127) * G) / 128),
 // _qarr.py:575-601) in registers before it is requantized.
@@ -105,7 +104,9 @@ __device__ __forceinline__ float row_elem(const uint32_t (&w)[InTraits<IN>::NW],
   }
 }
 
-template <int IN, bool HW>
+// TOK consecutive tokens per lane; RS = 128 / TOK lanes cover a 128-token
+// block, CGW = 64 / RS groups of 8 channels per wave.
+template <int IN, bool HW, int TOK>
 __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ x,
                                                     const uint8_t* __restrict__ x_sc8,
                                                     const float* __restrict__ x_sc32, int kg_shift,
@@ -115,8 +116,9 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
   constexpr int ESZ = InTraits<IN>::ESZ;
   constexpr int NW = InTraits<IN>::NW;
   const int lane = threadIdx.x & 63;
-  const int cg = lane & 7, rs = lane >> 3;
-  const int64_t c0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 64 + cg * 8;
+  constexpr int RS = 128 / TOK, CGW = 64 / RS;
+  const int cg = lane % CGW, rs = lane / CGW;
+  const int64_t c0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * (8 * CGW) + cg * 8;
   // C is a multiple of 8, so a lane owns a whole group or nothing; the xor
   // partners of a lane (same cg) share its fate.
   if (c0 >= C) return;
@@ -165,9 +167,8 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
     uint32_t m = 0;
 #pragma unroll
     for (int r = 0; r < TOK; ++r) m = umax(m, row_abs_bits<INC, j>(w[r], dq[r]));
-    m = umax(m, shfl_xor_u32(m, 8));
-    m = umax(m, shfl_xor_u32(m, 16));
-    m = umax(m, shfl_xor_u32(m, 32));
+#pragma unroll
+    for (int sh = CGW; sh < 64; sh <<= 1) m = umax(m, shfl_xor_u32(m, sh));
     mx[j] = m;
   });
   uint32_t Gb = 0;
@@ -218,8 +219,14 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
                           row_elem<INC, j>(w[4 * k + 2], dq[4 * k + 2]),
                           row_elem<INC, j>(w[4 * k + 3], dq[4 * k + 3]), S);
     }
-    const u32x4_t v = {o[0], o[1], o[2], o[3]};
-    __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(qo + (int64_t)j * T));
+    if constexpr (TOK == 16) {
+      const u32x4_t v = {o[0], o[1], o[2], o[3]};
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(qo + (int64_t)j * T));
+    } else {
+      static_assert(TOK == 8, "8 or 16 tokens per lane");
+      const u32x2_t v = {o[0], o[1]};
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x2_t*>(qo + (int64_t)j * T));
+    }
   });
   if (rs == 0) {
     // blocks (tb, c0 .. c0 + 7) are consecutive; they form group (tb*C + c0) / 8
@@ -272,22 +279,30 @@ extern "C" int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t*
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t128: too many token blocks or slices");
   if (scaled && (slices * T) * (C / 128) >= ((int64_t)1 << 32))
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t128: input scales beyond 2^32 blocks");
-  const dim3 grid((unsigned)((C + 255) / 256), (unsigned)(T / 128), (unsigned)slices);
+  // 16 tokens per lane (64 channels per wave, 128-byte row segments) for bf16
+  // inputs; 8 (32 channels per wave, half the registers) for the VALU-heavier
+  // f32 and fp8 inputs, where occupancy matters more than segment length
+  // (measured on [16384, 2048] and [16384, 8192]: bf16 85 vs 106 us, fp8 44 vs
+  // 36 us, f32 57 vs 48 us for 16 vs 8 tokens)
+  auto grid_for_tok = [&](int tok) {
+    const int cpw = 8 * (64 / (128 / tok));             // channels per wave
+    return dim3((unsigned)((C + 4 * cpw - 1) / (4 * cpw)), (unsigned)(T / 128), (unsigned)slices);
+  };
   const uint8_t* xb = static_cast<const uint8_t*>(x);
   // blocks per group of a (1, 128) input: gcd(8, n_blk), a power of two
   const int64_t kg = scaled ? gcd64(8, T * (C / 128)) : 1;
   const int kg_shift = kg == 8 ? 3 : (kg == 4 ? 2 : (kg == 2 ? 1 : 0));
   if (x_dtype == PRATCHYA_DT_BF16 && scaled) {
-    hipLaunchKernelGGL((k_quant_t128<IN_BF16S, true>), grid, dim3(256), 0, stream, xb, x_sc8, x_sc32, kg_shift,
+    hipLaunchKernelGGL((k_quant_t128<IN_BF16S, true, 16>), grid_for_tok(16), dim3(256), 0, stream, xb, x_sc8, x_sc32, kg_shift,
                        T, C, xt_fp8, sc_fp8, sc_fp32);
   } else if (x_dtype == PRATCHYA_DT_BF16) {
-    hipLaunchKernelGGL((k_quant_t128<IN_BF16, true>), grid, dim3(256), 0, stream, xb, nullptr, nullptr, 0,
+    hipLaunchKernelGGL((k_quant_t128<IN_BF16, true, 16>), grid_for_tok(16), dim3(256), 0, stream, xb, nullptr, nullptr, 0,
                        T, C, xt_fp8, sc_fp8, sc_fp32);
   } else if (x_dtype == PRATCHYA_DT_F32) {
-    hipLaunchKernelGGL((k_quant_t128<IN_F32, true>), grid, dim3(256), 0, stream, xb, nullptr, nullptr, 0,
+    hipLaunchKernelGGL((k_quant_t128<IN_F32, true, 8>), grid_for_tok(8), dim3(256), 0, stream, xb, nullptr, nullptr, 0,
                        T, C, xt_fp8, sc_fp8, sc_fp32);
   } else {
-    hipLaunchKernelGGL((k_quant_t128<IN_FP8, true>), grid, dim3(256), 0, stream, xb, x_sc8, x_sc32, kg_shift,
+    hipLaunchKernelGGL((k_quant_t128<IN_FP8, true, 8>), grid_for_tok(8), dim3(256), 0, stream, xb, x_sc8, x_sc32, kg_shift,
                        T, C, xt_fp8, sc_fp8, sc_fp32);
   }
   hipError_t err = hipGetLastError();

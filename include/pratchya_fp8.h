@@ -119,6 +119,17 @@ int pratchya_dequantize_bwd(const void* g, int g_dtype, const uint8_t* sc_fp8,
                             const float* sc_fp32, int64_t slices, int64_t H, int64_t W,
                             int64_t a, int64_t b, void* out, hipStream_t stream);
 
+/* Row gather of a dequantized table: out[i, :] = dequantize_impl(x)[idx[i], :]
+ * for a [H, W] table quantized with tgrid (a, b) -- the value of
+ * QArrayImpl.__getitem__ with an integer index array (Q:263-284, an embedding
+ * lookup, M:32-37) before it is requantized, reading only the rows returned.
+ * idx: int64 [n_idx] device array; a negative index counts from the end, and
+ * indices are clamped to [0, H - 1] (jnp's out-of-range gather).
+ * out: `out_dtype` [n_idx, W]. */
+int pratchya_gather_dequantize(const uint8_t* x_fp8, const uint8_t* sc_fp8, const float* sc_fp32,
+                               int64_t H, int64_t W, int64_t a, int64_t b, const int64_t* idx,
+                               int64_t n_idx, void* out, int out_dtype, hipStream_t stream);
+
 /* Transposed requantize, tgrid (128, 1):     replaces quantize_impl(x, (128, 1)), Q:458-506,
  * with the payload written transposed (the layout fp8_matmul's backward
  * contracts, Q:784-789, and the wgrad GEMM reads).

@@ -265,6 +265,31 @@ def dequantize(x_fp8: torch.Tensor, sc_fp8: torch.Tensor, sc_fp32: torch.Tensor,
     return out if out_dtype == dtype else out.to(dtype)
 
 
+def gather_dequantize(x_fp8: torch.Tensor, sc_fp8: torch.Tensor, sc_fp32: torch.Tensor, tgrid,
+                      idx: torch.Tensor, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """``dequantize_impl(x)[idx]`` for a 2-D quantized table and an integer index
+    array of any shape (pratchya/_qualia/_qarr.py:263-284 without the full
+    dequantization): returns ``idx.shape + (W,)`` in ``dtype``.  Negative
+    indices count from the end; indices are clamped to the table."""
+    _require_gpu(x_fp8, sc_fp8, sc_fp32, idx)
+    if x_fp8.dim() != 2:
+        raise ValueError("gather_dequantize needs a 2-D table")
+    if dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"gather_dequantize: output dtype {dtype} is not float32 or bfloat16")
+    H, W = int(x_fp8.shape[0]), int(x_fp8.shape[1])
+    a, b = int(tgrid[0]), int(tgrid[1])
+    ids = idx.reshape(-1).to(torch.int64).contiguous()
+    out = torch.empty(tuple(idx.shape) + (W,), dtype=dtype, device=x_fp8.device)
+    x8 = _u8(x_fp8).contiguous()
+    sc8 = _u8(sc_fp8).contiguous()
+    sc32 = sc_fp32.contiguous().float()
+    lib = _lib.load()
+    _lib.check(lib.pratchya_gather_dequantize(_ptr(x8), _ptr(sc8), _ptr(sc32), H, W, a, b, _ptr(ids),
+                                              ids.numel(), _ptr(out), _dtype_code(dtype), _stream(x8)),
+               "gather_dequantize")
+    return out
+
+
 def dequantize_bwd(g: torch.Tensor, sc_fp8: torch.Tensor, sc_fp32: torch.Tensor, tgrid) -> torch.Tensor:
     """Cotangent of the payload: ``(g * (f32(e<<23) * G) / 128).astype(g.dtype)``
     (pratchya/_qualia/_qarr.py:575-601)."""

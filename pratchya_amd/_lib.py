@@ -37,6 +37,8 @@ SIGNATURES = {
                                               _c_p]),
     "pratchya_requantize_cotangent": (_c_int, [_c_p, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64,
                                                _c_p, _c_p, _c_p, _c_p]),
+    "pratchya_gather_dequantize": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p,
+                                            _c_i64, _c_p, _c_int, _c_p]),
     "pratchya_dequantize": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                      _c_p, _c_int, _c_p]),
     "pratchya_dequantize_bwd": (_c_int, [_c_p, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,

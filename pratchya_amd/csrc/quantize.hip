@@ -649,6 +649,43 @@ __global__ __launch_bounds__(256) void k_dequant(const void* __restrict__ x,
 }
 
 // --------------------------------------------------------------------------
+// Gather-dequantize: out[i, c] = dequantize_impl(x)[row(i), c] for rows
+// idx[i] of a [H, W] table quantized with tgrid (a, b) -- an embedding lookup
+// that reads only the rows it returns.  row(i) = idx[i] (+ H when negative),
+// clamped to [0, H - 1] (jnp's indexing of a dequantized array).  Thread per
+// CH consecutive columns (CH | b) of one output row.
+// --------------------------------------------------------------------------
+template <bool OUT_BF16, int CH>
+__global__ __launch_bounds__(256) void k_gather_dequant(const uint8_t* __restrict__ x,
+                                                        const uint8_t* __restrict__ sc8,
+                                                        const float* __restrict__ sc32,
+                                                        const int64_t* __restrict__ idx, int64_t n_idx,
+                                                        int64_t H, int64_t W, int64_t a, int64_t b,
+                                                        int64_t K, void* __restrict__ out) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t cpr = W / CH;
+  if (t >= n_idx * cpr) return;
+  const int64_t i = t / cpr, c = (t - i * cpr) * CH;
+  int64_t r = idx[i];
+  if (r < 0) r += H;
+  r = r < 0 ? 0 : (r >= H ? H - 1 : r);
+  const int64_t blk = (r / a) * (W / b) + c / b;
+  const float sc = e8m0_decode(sc8[blk]) * sc32[blk / K];
+  const uint8_t* q = x + r * W + c;
+  float v[CH];
+#pragma unroll
+  for (int k = 0; k < CH; ++k) v[k] = (e4m3fn_to_f32(q[k]) * sc) * 0.0078125f;
+  const int64_t o = i * W + c;
+  if constexpr (OUT_BF16) {
+#pragma unroll
+    for (int k = 0; k < CH; ++k) static_cast<uint16_t*>(out)[o + k] = (uint16_t)f32_to_bf16_rne(v[k]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < CH; ++k) static_cast<float*>(out)[o + k] = v[k];
+  }
+}
+
+// --------------------------------------------------------------------------
 // Debug conversion kernels (test hooks)
 // --------------------------------------------------------------------------
 template <bool HW>
@@ -1088,6 +1125,42 @@ extern "C" int pratchya_dequantize_bwd(const void* g, int g_dtype, const uint8_t
     return pratchya_set_error(PRATCHYA_EINVAL, "dequantize_bwd: null buffer");
   return g_dtype == PRATCHYA_DT_BF16 ? launch_dequant<1, true>(g, sc_fp8, sc_fp32, out, L, stream)
                                      : launch_dequant<2, false>(g, sc_fp8, sc_fp32, out, L, stream);
+}
+
+extern "C" int pratchya_gather_dequantize(const uint8_t* x_fp8, const uint8_t* sc_fp8,
+                                          const float* sc_fp32, int64_t H, int64_t W, int64_t a,
+                                          int64_t b, const int64_t* idx, int64_t n_idx, void* out,
+                                          int out_dtype, hipStream_t stream) {
+  Layout L;
+  int rc = make_layout(1, H, W, a, b, &L);
+  if (rc) return rc;
+  if (out_dtype != PRATCHYA_DT_F32 && out_dtype != PRATCHYA_DT_BF16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "gather_dequantize: unsupported output dtype %d", out_dtype);
+  if (n_idx < 0) return pratchya_set_error(PRATCHYA_EINVAL, "gather_dequantize: negative index count");
+  if (n_idx == 0 || W == 0) {
+    g_err[0] = 0;
+    return PRATCHYA_OK;
+  }
+  if (H == 0) return pratchya_set_error(PRATCHYA_EINVAL, "gather_dequantize: index into an empty table");
+  if (!x_fp8 || !sc_fp8 || !sc_fp32 || !idx || !out)
+    return pratchya_set_error(PRATCHYA_EINVAL, "gather_dequantize: null buffer");
+  const int ch = chunk_elems(L.b, true);
+  const int64_t n_thr = n_idx * (W / ch);
+  const unsigned gr = grid_for(n_thr, 256);
+  const bool bf = out_dtype == PRATCHYA_DT_BF16;
+#define PRATCHYA_GD(C)                                                                              \
+  if (bf) hipLaunchKernelGGL((k_gather_dequant<true, C>), dim3(gr), dim3(256), 0, stream, x_fp8, sc_fp8, \
+                             sc_fp32, idx, n_idx, H, W, L.a, L.b, L.K, out);                        \
+  else hipLaunchKernelGGL((k_gather_dequant<false, C>), dim3(gr), dim3(256), 0, stream, x_fp8, sc_fp8, \
+                          sc_fp32, idx, n_idx, H, W, L.a, L.b, L.K, out)
+  switch (ch) {
+    case 1: PRATCHYA_GD(1); break;
+    case 2: PRATCHYA_GD(2); break;
+    case 4: PRATCHYA_GD(4); break;
+    default: PRATCHYA_GD(8); break;
+  }
+#undef PRATCHYA_GD
+  return check_launch("gather_dequantize");
 }
 
 extern "C" int pratchya_debug_bf16_to_e4m3(const uint16_t* in, uint8_t* out, int64_t n, int mode,

@@ -140,6 +140,37 @@ def dequantize_impl(x_fp8, sc_fp8, sc_fp32, dtype, tgrid):
     return K.dequantize(x_fp8, sc_fp8, sc_fp32, dtype, tuple(tgrid))
 
 
+class _GatherDequantize(torch.autograd.Function):
+    """``dequantize_impl(x)[idx]`` (Q:263-284 for an integer index array) with
+    the same vjp as that composition: the cotangent is scattered into the
+    table's shape (summing repeated rows, as indexing's backward does) and
+    taken through dequantize_impl_bwd (Q:575-601) to the table's source."""
+
+    @staticmethod
+    def forward(ctx, src, x8, sc8, sc32, tgrid, idx):
+        ctx.saved = (sc8, sc32, idx)
+        ctx.tgrid = tgrid
+        ctx.H = int(x8.shape[0])
+        return K.gather_dequantize(x8, sc8, sc32, tgrid, idx, torch.float32)
+
+    @staticmethod
+    def backward(ctx, g):
+        sc8, sc32, idx = ctx.saved
+        H, W = ctx.H, int(g.shape[-1])
+        rows = idx.reshape(-1).to(torch.int64)
+        rows = torch.where(rows < 0, rows + H, rows).clamp(0, H - 1)
+        full = torch.zeros((H, W), dtype=torch.float32, device=g.device)
+        full.index_put_((rows,), g.reshape(-1, W).float(), accumulate=True)
+        return K.dequantize_bwd(full, sc8, sc32, ctx.tgrid), None, None, None, None, None
+
+
+def _gather_dequantize(x8, sc8, sc32, tgrid, idx):
+    src = _src(x8)
+    if src is not None:
+        return _GatherDequantize.apply(src, x8, sc8, sc32, tuple(tgrid), idx)
+    return K.gather_dequantize(x8, sc8, sc32, tuple(tgrid), idx, torch.float32)
+
+
 def _deq32(x8, s8, s32, tgrid) -> torch.Tensor:
     return K.dequantize(x8, s8, s32, torch.float32, tuple(tgrid))
 
@@ -624,7 +655,13 @@ class QArrayImpl:
     def __getitem__(self, idx):
         if not hasattr(self, "_QArrayImpl__tgrid"):
             return QArrayImpl(self.get_value()[idx], quant=False)
-        sliced = self.dequantize(torch.float32)[idx]
+        if (torch.is_tensor(idx) and not idx.is_floating_point() and idx.dtype != torch.bool
+                and self.__value.dim() == 2 and self.__value.dtype == E4M3):
+            # an embedding lookup: only the indexed rows are dequantized
+            sliced = _gather_dequantize(self.__value, self.__sc_fp8, self.__sc_fp32, self.__tgrid,
+                                        idx.to(self.__value.device))
+        else:
+            sliced = self.dequantize(torch.float32)[idx]
         return QArrayImpl(sliced, _adapted_grid(self.__tgrid, sliced.shape))
 
     def __neg__(self):

@@ -339,3 +339,44 @@ def test_torch_functions_see_dequantized_values(Q):
     qa = Q.QArrayImpl(to_dev_f32(a), (1, 128))
     da = odq(oq(a, (1, 128)), (1, 128))
     assert_f32_bits_equal(f32(torch.relu(qa)), np.maximum(da, 0), "relu(q)")
+
+
+# ------------------------------------------------------------- embedding lookup
+def test_embedding_lookup_matches_full_dequantize(Q):
+    """table[ids] reads only the indexed rows; the value and the requantized
+    result equal the reference's dequantize-then-index path bit for bit,
+    including negative and out-of-range ids (jnp clamps)."""
+    from pratchya_amd import _kernels as K
+    V, D = 1024, 512
+    tb = O.normal_input((V, D), 1.0, seed=51)
+    table = Q.QArrayImpl(to_dev_bf16(tb), (16, 128))
+    ids = torch.tensor([[0, 5, 1023, -1], [17, 17, 1200, -2000]], device="cuda")
+    got = table[ids]
+    full = K.dequantize(*table._tree_flatten()[0], torch.float32, (16, 128))
+    idx = torch.where(ids < 0, ids + V, ids).clamp(0, V - 1)
+    want = full[idx]
+    assert got.shape == (2, 4, D) and got.tgrid == (4, 128)
+    # the gathered values, then the reference's requantization of them
+    g8 = K.gather_dequantize(*table._tree_flatten()[0], (16, 128), ids, torch.float32)
+    assert torch.equal(g8.view(torch.int32), want.view(torch.int32))
+    ref = oq(want.cpu().numpy(), (4, 128))
+    assert_triple(got, ref, "table[ids]")
+    bf = K.gather_dequantize(*table._tree_flatten()[0], (16, 128), ids, torch.bfloat16)
+    assert torch.equal(bf.view(torch.int16), want.to(torch.bfloat16).view(torch.int16))
+
+
+def test_embedding_lookup_gradient(Q):
+    """The table's gradient through the fast path equals the dequantize-then-
+    index path (distinct ids: no summation-order freedom)."""
+    V, D = 512, 256
+    tb = O.normal_input((V, D), 1.0, seed=52)
+    ids = torch.tensor([3, 100, 511, 0, 64], device="cuda")
+    gy = torch.randn((5, D), device="cuda")
+    grads = []
+    for fast in (True, False):
+        w = to_dev_bf16(tb).float().requires_grad_(True)
+        table = Q.QArrayImpl(w, (1, 128))
+        out = table[ids] if fast else Q.QArrayImpl(table.dequantize(torch.float32)[ids], (1, 128))
+        out.astype(torch.float32).backward(gy)
+        grads.append(w.grad.detach().clone())
+    assert torch.equal(grads[0].view(torch.int32), grads[1].view(torch.int32))

@@ -131,6 +131,53 @@ def bench_quantize(steps: int, warmup: int):
     return ms, wall, ok
 
 
+CFG1_N = 1024
+# quantize: 2 B in + 1 B payload; dequantize: 1 B payload + 2 B out; the 68 scale bytes
+# (64 e8m0 + 1 group max) written once and read once
+CFG1_BYTES = 3 * CFG1_N * CFG1_N + 3 * CFG1_N * CFG1_N + 2 * 68
+
+
+def bench_config1(steps: int, warmup: int):
+    """Config 1: bf16 [1024, 1024] ~ N(0, 1) (seed 1) quantized with 128 x 128
+    blocks and dequantized back to bf16 -- the reference's CPU-runnable round
+    trip.  2 MB of data: launch- and latency-bound on the GPU; reported for
+    completeness.  A step is quantize (the multi-kernel general path: one
+    group over the matrix) + dequantize."""
+    import ctypes
+    import torch
+    from oracle import qarr_oracle as O
+    from pratchya_amd import _lib
+    n = CFG1_N
+    x = torch.from_numpy(O.normal_input((n, n), 1.0, seed=1).view(np.int16)).view(torch.bfloat16).cuda()
+    lib = _lib.load()
+    ws_bytes = lib.pratchya_quantize_workspace_bytes(_lib.DT_BF16, 1, n, n, 128, 128)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+    q8 = torch.empty((n, n), dtype=torch.uint8, device="cuda")
+    s8 = torch.empty(64, dtype=torch.uint8, device="cuda")
+    s32 = torch.empty(1, dtype=torch.float32, device="cuda")
+    y = torch.empty((n, n), dtype=torch.bfloat16, device="cuda")
+    P = ctypes.c_void_p
+
+    def step(i):
+        st = P(torch.cuda.current_stream().cuda_stream)
+        rc = lib.pratchya_quantize(P(x.data_ptr()), _lib.DT_BF16, 1, n, n, 128, 128, P(q8.data_ptr()),
+                                   P(s8.data_ptr()), P(s32.data_ptr()), P(ws.data_ptr()), ws_bytes, st)
+        rc = rc or lib.pratchya_dequantize(P(q8.data_ptr()), P(s8.data_ptr()), P(s32.data_ptr()), 1, n, n,
+                                           128, 128, P(y.data_ptr()), _lib.DT_BF16, st)
+        if rc:
+            raise RuntimeError(lib.pratchya_last_error().decode())
+
+    ms, _ = timed_graph(step, steps, warmup)
+    # parity of the round trip against the oracle
+    xb = O.normal_input((n, n), 1.0, seed=1)
+    r8, rs8, rs32 = O.quantize_impl(O.bf16_bits_to_f32(xb), (128, 128))
+    want = O.dequantize_impl(r8, rs8, rs32, "bfloat16", (128, 128))
+    ok = bool(np.array_equal(y.view(torch.int16).cpu().numpy().view(np.uint16), want))
+    return {"us_per_round_trip": round(ms * 1e3, 2), "GB/s": round(CFG1_BYTES / (ms * 1e-3) / 1e9, 1),
+            "bytes": CFG1_BYTES, "bit_exact_vs_oracle": ok,
+            "shape": "bf16 [1024,1024] -> (128,128) e4m3fn -> bf16"}
+
+
 def bench_gemm_fwd(steps: int, warmup: int):
     """Config 3: A = quantize(cfg2 activation, (1,128)) [16384, 2048] x
     W = quantize(N(0, 0.02) [2048, 8192], (128,128)) -> bf16 [16384, 8192].
@@ -360,6 +407,9 @@ def main():
     _log(f"config 2 quantize: {ms * 1e3:.2f} us/step, parity spot check {'ok' if ok else 'FAILED'}")
     gbs = CFG2_BYTES / (ms * 1e-3) / 1e9
     extra = {}
+    _log("config 1 round trip: start")
+    extra["config1_round_trip"] = bench_config1(max(20, args.steps // 4), max(4, args.warmup // 4))
+    _log(f"config 1 round trip: {extra['config1_round_trip']['us_per_round_trip']} us")
     if not args.no_gemm:
         _log("config 3 gemm fwd: start")
         gms, tflops = bench_gemm_fwd(max(8, args.steps // 4), max(4, args.warmup // 4))

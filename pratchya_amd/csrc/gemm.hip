@@ -13,8 +13,10 @@
 //   * 128-wide K tiles staged in LDS by global_load_lds_dwordx4 (DMA straight
 //     into LDS, two stages), rows XOR-swizzled in 16-byte chunks so that the
 //     MFMA operand reads are bank-conflict free;
-//   * the e8m0 bytes and group maxima of the stage's 256 + 256 rows travel
-//     through LDS by the same DMA;
+//   * the e8m0 bytes of the stage's 256 + 256 rows travel through LDS by the
+//     same DMA; their f32 group maxima are loaded into registers by the wave
+//     that loads the rows, which writes the accumulator units and unit
+//     ratios derived from them into the stage (see publish_g);
 //   * "ping-pong": the two waves sharing a SIMD belong to two groups whose
 //     phases are offset by one workgroup barrier, so while one group runs its
 //     MFMA cluster for a 64-wide K slice the other reads its next operands
@@ -47,18 +49,28 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 256, BN = 256, BK = 128;
 constexpr int TILE_BYTES = BM * BK;            // 32 KB per operand per stage
 constexpr int NTHREADS = 512;
-// LDS stage: A tile | B tile | A e8m0 words | B e8m0 words | A group max | B group max
+// LDS stage: A tile | B tile | A e8m0 words | B e8m0 words | A unit ratios |
+// B unit ratios.  After the two stages: A units | B units (of the latest span
+// start).  The ratio and unit arrays are in the order the MFMA lanes read
+// them: A per row as [band wm][l32][mi] (one 8-byte read per lane), B per 4
+// rows as [wn][ni][lhi][j] (one 16-byte read per 32-column tile).
 constexpr int OFF_B = TILE_BYTES;
 constexpr int OFF_EA = 2 * TILE_BYTES;
 constexpr int OFF_EB = OFF_EA + 4 * BM;
-constexpr int OFF_GA = OFF_EB + 4 * BN;
-constexpr int OFF_GB = OFF_GA + 4 * BM;
-constexpr int STAGE_BYTES = OFF_GB + 4 * BN;   // 69632
+constexpr int OFF_RA = OFF_EB + 4 * BN;
+constexpr int OFF_RB = OFF_RA + 4 * BM;
+constexpr int STAGE_BYTES = 69632;             // OFF_RB + BN, rounded up to 1 KB
+constexpr int OFF_UA = 2 * STAGE_BYTES;
+constexpr int OFF_UB = OFF_UA + 4 * BM;
+constexpr int LDS_BYTES = OFF_UB + BN;
+static_assert(OFF_RB + BN <= STAGE_BYTES && LDS_BYTES <= 160 * 1024, "LDS layout");
 
 struct Scales {
   const uint8_t* e8;   // e8m0 bytes
@@ -157,16 +169,18 @@ __device__ __forceinline__ void dma_offsets(int64_t ld, int lane, uint32_t (&off
 
 // One wave's share of a stage's DMA.  The stage load is split between the
 // two ping-pong groups: wave w of group 0 loads A rows [64w, 64w + 64) of the
-// tile, their e8m0 words and (at span starts) group maxima; wave w of group 1
-// the same for B.  Each is issued inside a compute phase, between MFMAs, so
-// that the load issue (throttled by the vector memory address path) runs in
-// the MFMAs' shadow instead of lengthening a memory phase.
+// tile, their e8m0 words and group maxima; wave w of group 1 the same for B.
+// Each is issued inside a compute phase, between MFMAs, so that the load
+// issue (throttled by the vector memory address path) runs in the MFMAs'
+// shadow instead of lengthening a memory phase.
 struct DmaHalf {
   __amdgpu_buffer_rsrc_t pay, e8, g32;
   uint32_t ld;                 // operand row stride in bytes
   uint32_t s_k, kg;            // block index stride per K block, blocks per group
   uint32_t off[2];             // per-lane byte offset inside an 8-row group (even / odd group)
-  int lds_pay, lds_e, lds_g;   // stage offsets of this wave's payload rows, e8m0 words, maxima
+  int lds_pay, lds_e;          // stage offsets of this wave's payload rows, e8m0 words
+  int lds_r, lds_u;            // offsets of the operand's unit ratio (in a stage) and unit arrays
+  int pub;                     // byte offset of the lane's row in those arrays
 };
 
 // The rows a wave loads for one output tile: the first of its 64 rows (global
@@ -181,14 +195,35 @@ __device__ __forceinline__ void dma_rows(const DmaHalf& h, const DmaRows& r, uin
                                            (r.row0 + (uint32_t)(i * 8)) * h.ld + (uint32_t)kt * BK, 0, 0);
 }
 
-// The e8m0 word of each of this wave's 64 rows for K block kt, and at span
-// starts their group maxima (exact group index block / kg).
-__device__ __forceinline__ void dma_scales(const DmaHalf& h, const DmaRows& r, uint8_t* st, int kt,
-                                           bool span_start) {
+// The e8m0 word of each of this wave's 64 rows for K block kt.
+__device__ __forceinline__ void dma_scales(const DmaHalf& h, const DmaRows& r, uint8_t* st, int kt) {
   const uint32_t ia = r.e_word + (uint32_t)kt * h.s_k;
   __builtin_amdgcn_raw_ptr_buffer_load_lds(h.e8, (lds_void*)(st + h.lds_e), 4, ia & ~3u, 0, 0, 0);
-  if (span_start)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(h.g32, (lds_void*)(st + h.lds_g), 4, (ia / h.kg) * 4u, 0, 0, 0);
+}
+
+// The group max of the lane's row for K block kt (exact group index block /
+// kg), into a register: it is turned into units by publish_g once the stage
+// has landed.
+__device__ __forceinline__ float load_g(const DmaHalf& h, const DmaRows& r, int kt) {
+  const uint32_t ia = r.e_word + (uint32_t)kt * h.s_k;
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(h.g32, (int)((ia / h.kg) * 4u), 0, 0));
+}
+
+// The accumulator holds C / (uA uB) in the units u of its operands' rows,
+// set at each span start: the group max, or the previous units where the
+// group max is 0 (an all-zero group has an all-zero payload and adds
+// nothing); a tile's first K block starts from units 1.  The wave that
+// loaded a span start's rows writes the factor old / new units into the
+// stage and the new units into the unit arrays, once per row instead of once
+// per MFMA lane (for the (128,1) operands of a weight gradient the span is
+// one K block).
+__device__ __forceinline__ void publish_g(const DmaHalf& h, uint8_t* lds, uint8_t* st, float g_ld, bool first,
+                                          float& u_prev) {
+  const float prev = first ? 1.0f : u_prev;
+  const float u = g_ld == 0.0f ? prev : g_ld;
+  *reinterpret_cast<float*>(st + h.lds_r + h.pub) = prev * __builtin_amdgcn_rcpf(u);
+  *reinterpret_cast<float*>(lds + h.lds_u + h.pub) = u;
+  u_prev = u;
 }
 
 // Workgroup barrier without the release/acquire fences of __syncthreads():
@@ -225,13 +260,29 @@ __device__ __forceinline__ void pin_acc(v16f (&acc)[2][4]) {
 __device__ __forceinline__ uint32_t lds_u32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
 __device__ __forceinline__ float lds_f32(const uint8_t* p) { return *reinterpret_cast<const float*>(p); }
 
-// B-side group maxima held per lane: 4 (one per 32-column MFMA tile) or 16
-// (one per 4-column accumulator group, for scale groups narrower than 32 rows).
+// The lane's entries of a stage's unit (or unit ratio) arrays: its A rows
+// wm*64 + mi*32 + l32 (mi = 0, 1), and its B rows wn*128 + ni*32 + 8j + 4*lhi
+// (FINE_B: j = 0..3, for scale groups narrower than 32 rows) or wn*128 + ni*32.
 template <bool FINE_B>
-struct BGroups {
-  static constexpr int NJ = FINE_B ? 4 : 1;
-  float g[4][NJ];
-};
+__device__ __forceinline__ void load_units(const uint8_t* a, const uint8_t* b, int wm, int wn, int lane,
+                                           float (&uA)[2], float (&uB)[4][FINE_B ? 4 : 1]) {
+  const int l32 = lane & 31, lhi = lane >> 5;
+  const v2f va = *reinterpret_cast<const v2f*>(a + (wm * 64 + l32 * 2) * 4);
+  uA[0] = va.x;
+  uA[1] = va.y;
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni) {
+    if constexpr (FINE_B) {
+      const v4f vb = *reinterpret_cast<const v4f*>(b + (wn * 32 + (ni * 2 + lhi) * 4) * 4);
+      uB[ni][0] = vb.x;
+      uB[ni][1] = vb.y;
+      uB[ni][2] = vb.z;
+      uB[ni][3] = vb.w;
+    } else {
+      uB[ni][0] = lds_f32(b + (wn * 32 + ni * 8) * 4);
+    }
+  }
+}
 
 // Output tile of workgroup `bid`: XCD-aware numbering (see the file header).
 __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int* tm, int* tn) {
@@ -253,7 +304,8 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int* 
 // covering whole rows, with non-temporal stores (the output is not read again
 // by this kernel; streaming it keeps the operand panels in L2).
 template <bool OUT_BF16, bool FINE_B>
-__device__ __forceinline__ void store_tile(const v16f (&acc)[2][4], const float (&gA)[2], const BGroups<FINE_B>& bg,
+__device__ __forceinline__ void store_tile(const v16f (&acc)[2][4], const float (&gA)[2],
+                                           const float (&gB)[4][FINE_B ? 4 : 1],
                                            uint8_t* stage, int wave, int lane, void* C, int64_t ldc, int row0,
                                            int col0) {
   const int l32 = lane & 31, lhi = lane >> 5;
@@ -275,7 +327,7 @@ __device__ __forceinline__ void store_tile(const v16f (&acc)[2][4], const float 
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int col = ni * 32 + 8 * j + 4 * lhi;
-            const float f = gA[mi] * bg.g[ni][FINE_B ? j : 0] * 6.103515625e-05f;
+            const float f = gA[mi] * gB[ni][FINE_B ? j : 0] * 6.103515625e-05f;
             const float c0 = acc[mi][ni][4 * j + 0] * f, c1 = acc[mi][ni][4 * j + 1] * f;
             const float c2 = acc[mi][ni][4 * j + 2] * f, c3 = acc[mi][ni][4 * j + 3] * f;
             uint8_t* dst = stg + (l32 % RP) * PITCH + col * ESZ;
@@ -312,8 +364,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     Scales sa, Scales sb, void* __restrict__ C, int64_t ldc, int K, int span, int tiles_m,
     int tiles_n, uint32_t a_bytes, uint32_t b_bytes, uint32_t ea_bytes, uint32_t eb_bytes,
     uint32_t ga_bytes, uint32_t gb_bytes) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * STAGE_BYTES];
-  constexpr int NJ = BGroups<FINE_B>::NJ;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+  constexpr int NJ = FINE_B ? 4 : 1;
   const OperandRsrc ra = make_rsrc(A, a_bytes, sa, ea_bytes, ga_bytes);
   const OperandRsrc rb = make_rsrc(B, b_bytes, sb, eb_bytes, gb_bytes);
 
@@ -341,7 +393,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     dma_offsets(grp == 0 ? lda : ldb, lane, h.off);
     h.lds_pay = (grp == 0 ? 0 : OFF_B) + w4 * 8 * 1024;
     h.lds_e = (grp == 0 ? OFF_EA : OFF_EB) + w4 * 256;
-    h.lds_g = (grp == 0 ? OFF_GA : OFF_GB) + w4 * 256;
+    h.lds_r = grp == 0 ? OFF_RA : OFF_RB;
+    h.lds_u = grp == 0 ? OFF_UA : OFF_UB;
+    if (grp == 0) {
+      h.pub = (w4 * 64 + l32 * 2 + lhi) * 4;              // A row w4*64 + lane: band w4, mi = lhi
+    } else {
+      const int r = w4 * 64 + lane, c = r & 127, q = c & 31;   // B row: wn = r / 128, ni = c / 32
+      h.pub = ((r >> 7) * 32 + ((c >> 5) * 2 + ((q >> 2) & 1)) * 4 + (q >> 3)) * 4;
+    }
   }
   auto rows_of = [&](int tm_, int tn_) {
     DmaRows r;
@@ -374,11 +433,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   int par = 0;                            // stage buffer of the tile's K block 0
 
   // prologue: both halves of stage 0; group 1 then starts its half of stage 1
-  // (it is one stage ahead of group 0 throughout)
+  // (it is one stage ahead of group 0 throughout).  The wave's last stage
+  // DMA, not yet published: g_pub (a span start), its group max g_ld, its
+  // buffer g_st, g_first (a tile's K block 0).
 #pragma unroll
   for (int i = 0; i < 8; ++i) dma_rows(h, cur, lds, 0, i);
-  dma_scales(h, cur, lds, 0, true);
+  dma_scales(h, cur, lds, 0);
+  float g_ld = load_g(h, cur, 0), u_prev = 1.0f;
+  uint8_t* g_st = lds;
+  bool g_first = true, g_pub = true;
   __builtin_amdgcn_s_waitcnt(0);
+  publish_g(h, lds, g_st, g_ld, g_first, u_prev);
   __syncthreads();
 
   for (;;) {
@@ -396,7 +461,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
         uint8_t* s1 = lds + ((1 + par) & 1) * STAGE_BYTES;
 #pragma unroll
         for (int i = 0; i < 8; ++i) dma_rows(h, cur, s1, 1, i);
-        dma_scales(h, cur, s1, 1, 1 % span == 0);
+        dma_scales(h, cur, s1, 1);
+        g_pub = span == 1;
+        if (g_pub) g_ld = load_g(h, cur, 1);
+        g_st = s1;
+        g_first = false;
       }
       wg_barrier();                  // offset group 1 by one phase
     }
@@ -414,12 +483,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
       for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = v16f{0};
-    float gA[2] = {1.0f, 1.0f};
-    BGroups<FINE_B> bg;
-#pragma unroll
-    for (int ni = 0; ni < 4; ++ni)
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) bg.g[ni][j] = 1.0f;
 
     uint32_t eA = 0, eB = 0;
     for (int kt = 0; kt < nk; ++kt) {
@@ -428,6 +491,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
       for (int ks = 0; ks < 2; ++ks) {
         // ---- memory phase ----
         if (ks == 0) {
+          // group 0 publishes its half of stage kt here (it landed at the end
+          // of the previous phase); its own waves read only their own rows'
+          // ratios, group 1 reads them one phase later
+          if (grp == 0 && kt > 0 && g_pub) publish_g(h, lds, g_st, g_ld, g_first, u_prev);
           // e8m0 bytes of this K block for the lane's 2 A rows / 4 B rows
           eA = 0;
           eB = 0;
@@ -446,36 +513,16 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
             const uint32_t pos = (__builtin_amdgcn_ubfe(epos, 4 + 2 * i, 2) + tB) & 3u;
             eB |= __builtin_amdgcn_ubfe(w, pos * 8u, 8) << (8 * i);
           }
-          if (kt % span == 0) {
-            // a new span of group maxima: move the accumulator into its units.
-            // A zero group max keeps the previous units (an all-zero group has
-            // an all-zero payload and adds nothing).
+          if (kt > 0 && kt % span == 0) {
+            // a new span of group maxima: move the accumulator into its units
             float rA[2], rB[4][NJ];
+            load_units<FINE_B>(st + OFF_RA, st + OFF_RB, wm, wn, lane, rA, rB);
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi) {
-              const float g0 = lds_f32(st + OFF_GA + (wm * 64 + mi * 32 + l32) * 4);
-              const float g = g0 == 0.0f ? gA[mi] : g0;
-              rA[mi] = gA[mi] * __builtin_amdgcn_rcpf(g);
-              gA[mi] = g;
-            }
+            for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-            for (int ni = 0; ni < 4; ++ni)
+              for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
-              for (int j = 0; j < NJ; ++j) {
-                const int col = wn * 128 + ni * 32 + (FINE_B ? 8 * j + 4 * lhi : 0);
-                const float g0 = lds_f32(st + OFF_GB + col * 4);
-                const float g = g0 == 0.0f ? bg.g[ni][j] : g0;
-                rB[ni][j] = bg.g[ni][j] * __builtin_amdgcn_rcpf(g);
-                bg.g[ni][j] = g;
-              }
-            if (kt > 0) {
-#pragma unroll
-              for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-                for (int ni = 0; ni < 4; ++ni)
-#pragma unroll
-                  for (int v = 0; v < 16; ++v) acc[mi][ni][v] *= rA[mi] * rB[ni][FINE_B ? (v >> 2) : 0];
-            }
+                for (int v = 0; v < 16; ++v) acc[mi][ni][v] *= rA[mi] * rB[ni][FINE_B ? (v >> 2) : 0];
           }
         }
         // rows of this lane: A wm*64 + i*32 + l32, B wn*128 + i*32 + l32; the
@@ -491,10 +538,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
         fb[1] = read_frag2<OFF_B + 32 * BK>(blo, bhi);
         fb[2] = read_frag2<OFF_B + 64 * BK>(blo, bhi);
         fb[3] = read_frag2<OFF_B + 96 * BK>(blo, bhi);
-        if (grp == 1 && ks == 1 && kt + 1 < nk)
+        if (grp == 1 && ks == 1 && kt + 1 < nk) {
           PINNED_WAITCNT(0);        // also group 1's half of stage kt+1 landed
-        else
-          PINNED_WAITCNT(0xC07F);   // lgkmcnt(0): operands in registers, stage reads done
+          if (g_pub) publish_g(h, lds, g_st, g_ld, g_first, u_prev);
+        }
+        PINNED_WAITCNT(0xC07F);     // lgkmcnt(0): operands in registers, stage reads (and writes) done
         wg_barrier();
         // ---- compute phase ----
         // Group 0 loads its half of stage kt+1 during its first K half, group 1
@@ -525,7 +573,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
         mfma_pinned<0, 3>(acc, fa, fb, eA, eB);
         if (dma_now) { dma_rows(h, dr, dst, lkt, 6); dma_rows(h, dr, dst, lkt, 7); }
         mfma_pinned<1, 0>(acc, fa, fb, eA, eB);
-        if (dma_now) dma_scales(h, dr, dst, lkt, lkt % span == 0);
+        if (dma_now) {
+          dma_scales(h, dr, dst, lkt);
+          g_pub = lkt % span == 0;
+          if (g_pub) g_ld = load_g(h, dr, lkt);
+          g_st = dst;
+          g_first = lkt == 0;
+        }
         mfma_pinned<1, 1>(acc, fa, fb, eA, eB);
         mfma_pinned<1, 2>(acc, fa, fb, eA, eB);
         mfma_pinned<1, 3>(acc, fa, fb, eA, eB);
@@ -536,8 +590,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     }
     if (grp == 0) wg_barrier();      // match group 1's extra barrier
 
-    // the last stage's buffer holds no pending load: stage the output there
-    store_tile<OUT_BF16, FINE_B>(acc, gA, bg, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc,
+    // units of the last span; the last stage's buffer holds no pending load:
+    // stage the output there
+    float gA[2], gB[4][NJ];
+    load_units<FINE_B>(lds + OFF_UA, lds + OFF_UB, wm, wn, lane, gA, gB);
+    store_tile<OUT_BF16, FINE_B>(acc, gA, gB, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc,
                                  m0 + wm * 64, n0 + wn * 128);
     if (!has_next) break;
     t = t_next;
@@ -548,6 +605,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     // the next tile's stage 0 (and this tile's output stores) complete, and
     // every wave is done with the staging buffer
     __builtin_amdgcn_s_waitcnt(0);
+    publish_g(h, lds, g_st, g_ld, g_first, u_prev);
     __syncthreads();
   }
 }

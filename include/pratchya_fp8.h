@@ -130,6 +130,38 @@ int pratchya_gather_dequantize(const uint8_t* x_fp8, const uint8_t* sc_fp8, cons
                                int64_t H, int64_t W, int64_t a, int64_t b, const int64_t* idx,
                                int64_t n_idx, void* out, int out_dtype, hipStream_t stream);
 
+/* Momentum of the quantized Miulion optimizer step, one pass      replaces
+ * pratchya/_nnx_impl/_optimizer.py:124-135 (a layer of a 3-D stacked leaf,
+ * bf16 arithmetic) and :157-176 (a 2-D leaf, f32 arithmetic):
+ *   m = dequantize(momentum) in the arithmetic dtype, g = the gradient in it,
+ *   c_out = beta1 * m + beta1c * g,   m_new = beta2 * m + beta2c * g
+ * with beta1c = 1 - beta1 and beta2c = 1 - beta2 as the host rounds them.
+ * Every product and sum is rounded separately in arith_dtype (PRATCHYA_DT_F32
+ * or PRATCHYA_DT_BF16; the constants must already be values of that dtype).
+ * momentum: an e4m3fn payload [slices, H, W] with its scales (tgrid (a, b));
+ * g: e4m3fn with g_sc8 / g_sc32 in the same layout (a quantized gradient), or
+ * bf16 / f32 [slices, H, W].  c_out and m_new: arith_dtype [slices, H, W];
+ * m_new is quantized with pratchya_quantize to give the new momentum. */
+int pratchya_momentum(const uint8_t* m_fp8, const uint8_t* m_sc8, const float* m_sc32, const void* g,
+                      int g_dtype, const uint8_t* g_sc8, const float* g_sc32, int64_t slices, int64_t H,
+                      int64_t W, int64_t a, int64_t b, int arith_dtype, float beta1, float beta1c,
+                      float beta2, float beta2c, void* c_out, void* m_new, hipStream_t stream);
+
+/* Update of the Miulion step                                  replaces
+ * pratchya/_nnx_impl/_optimizer.py:147-153 and :189-197:
+ *   out = -(lr * u' + lr_wd * p),  u' = sign(u) (use_sign, Lion) or u * scale (Muon:
+ *   u = Newton-Schulz(c), scale = sqrt(max(N, M)))
+ * The parameter p and u * scale are rounded to the leaf dtype arith_dtype
+ * (scale already a value of it); the products and the sum are f32 (lr and
+ * lr_wd = lr * wd are f32), rounded once to out_dtype.  u: f32 or bf16
+ * [slices, H, W] (an f32 u with bf16 arith_dtype only with use_sign); p: the
+ * parameter, e4m3fn with p_sc8 / p_sc32 (tgrid (a, b)), or bf16 / f32; out:
+ * out_dtype (f32 or bf16). */
+int pratchya_apply_update(const void* u, int u_dtype, int use_sign, float scale, const void* p,
+                          int p_dtype, const uint8_t* p_sc8, const float* p_sc32, int64_t slices,
+                          int64_t H, int64_t W, int64_t a, int64_t b, int arith_dtype, float lr,
+                          float lr_wd, void* out, int out_dtype, hipStream_t stream);
+
 /* Transposed requantize, tgrid (128, 1):     replaces quantize_impl(x, (128, 1)), Q:458-506,
  * with the payload written transposed (the layout fp8_matmul's backward
  * contracts, Q:784-789, and the wgrad GEMM reads).

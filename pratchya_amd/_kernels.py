@@ -421,3 +421,64 @@ def gemm_nt(a: Operand, b: Operand, out_dtype: torch.dtype = torch.bfloat16,
                                        M, N, K, _ptr(out), out.stride(0), _dtype_code(out.dtype),
                                        _stream(ap)), "gemm")
     return out
+
+
+def _as_operand(x, tgrid, what):
+    """(tensor, dtype code, sc8, sc32) of an optimizer operand: an fp8 payload
+    given as a (payload, sc8, sc32) triple, or a bf16 / f32 tensor."""
+    if isinstance(x, (tuple, list)):
+        x8, s8, s32 = x
+        _require_gpu(x8, s8, s32)
+        return _u8(x8).contiguous(), _lib.DT_E4M3, _u8(s8).contiguous(), s32.contiguous().float()
+    _require_gpu(x)
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"{what}: unsupported dtype {x.dtype}")
+    return x.contiguous(), _dtype_code(x.dtype), None, None
+
+
+def momentum(m, g, tgrid, arith: torch.dtype, beta1: float, beta1c: float, beta2: float, beta2c: float):
+    """``c = beta1*m + beta1c*g`` and ``m_new = beta2*m + beta2c*g`` of the
+    Miulion step (pratchya/_nnx_impl/_optimizer.py:124-135, :157-176), one
+    rounding per operation in ``arith`` (float32 or bfloat16), in one pass.
+    ``m``: the quantized momentum as a (payload, sc8, sc32) triple with tgrid
+    ``tgrid``; ``g``: a triple in the same layout or a bf16 / f32 tensor.  The
+    constants must be values of ``arith``.  Returns ``(c, m_new)`` in ``arith``."""
+    m8, _, ms8, ms32 = _as_operand(m, tgrid, "momentum")
+    gt, gcode, gs8, gs32 = _as_operand(g, tgrid, "momentum gradient")
+    if tuple(gt.shape) != tuple(m8.shape):
+        raise ValueError(f"momentum: gradient shape {tuple(gt.shape)} != momentum shape {tuple(m8.shape)}")
+    S, H, W = slices_hw(m8.shape)
+    c = torch.empty(m8.shape, dtype=arith, device=m8.device)
+    nm = torch.empty(m8.shape, dtype=arith, device=m8.device)
+    lib = _lib.load()
+    _lib.check(lib.pratchya_momentum(_ptr(m8), _ptr(ms8), _ptr(ms32), _ptr(gt), gcode,
+                                     _ptr(gs8) if gs8 is not None else None,
+                                     _ptr(gs32) if gs32 is not None else None,
+                                     S, H, W, int(tgrid[0]), int(tgrid[1]), _dtype_code(arith),
+                                     beta1, beta1c, beta2, beta2c, _ptr(c), _ptr(nm), _stream(m8)), "momentum")
+    return c, nm
+
+
+def apply_update(u: torch.Tensor, use_sign: bool, scale: float, p, tgrid, arith: torch.dtype,
+                 lr: float, lr_wd: float, out_dtype: torch.dtype) -> torch.Tensor:
+    """``-(lr * u' + lr_wd * p)`` with ``u' = sign(u)`` (Lion) or ``u * scale``
+    (Muon) (pratchya/_nnx_impl/_optimizer.py:147-153, :189-197): ``p`` and
+    ``u * scale`` rounded to the leaf dtype ``arith``, the products and the sum
+    in f32 (``lr``, ``lr_wd`` f32 values), one rounding to ``out_dtype``.
+    ``p``: a (payload, sc8, sc32) triple with tgrid ``tgrid`` or a bf16 / f32
+    tensor of ``u``'s shape."""
+    _require_gpu(u)
+    uu = u.contiguous()
+    pt, pcode, ps8, ps32 = _as_operand(p, tgrid, "update parameter")
+    if tuple(pt.shape) != tuple(uu.shape):
+        raise ValueError(f"apply_update: parameter shape {tuple(pt.shape)} != direction shape {tuple(uu.shape)}")
+    S, H, W = slices_hw(uu.shape)
+    a, b = (int(tgrid[0]), int(tgrid[1])) if pcode == _lib.DT_E4M3 else (1, 1)
+    out = torch.empty(uu.shape, dtype=out_dtype, device=uu.device)
+    lib = _lib.load()
+    _lib.check(lib.pratchya_apply_update(_ptr(uu), _dtype_code(uu.dtype), 1 if use_sign else 0, scale,
+                                         _ptr(pt), pcode, _ptr(ps8) if ps8 is not None else None,
+                                         _ptr(ps32) if ps32 is not None else None, S, H, W, a, b,
+                                         _dtype_code(arith), lr, lr_wd, _ptr(out), _dtype_code(out_dtype),
+                                         _stream(uu)), "apply_update")
+    return out

@@ -1,0 +1,262 @@
+// Elementwise kernels of pratchya's quantized-momentum optimizer step
+// (Miulion, pratchya/_nnx_impl/_optimizer.py:62-217) for gfx950.
+//
+// Per parameter leaf the reference computes, in the leaf's arithmetic dtype
+// (f32 for a 2-D quantized parameter, :153-199; bf16 per layer of a 3-D
+// stacked one, :117-142):
+//   m, g     = dequantize(momentum), dequantize(gradient)     (:124-125, :160-161)
+//   c        = beta1 * m + (1 - beta1) * g                    (:134, :175)
+//   m_new    = beta2 * m + (1 - beta2) * g                    (:135, :176)
+//   momentum = QArrayImpl(m_new, tgrid)                       (:145, :187)
+//   update   = -(lr * u + lr * wd * p),  u = NS(c) * sqrt(max(N, M))  (Muon, :147-150, :189-193)
+//                                        u = sign(c)                   (Lion, :151-153, :194-197)
+// k_momentum produces c and m_new in one pass over the quantized momentum
+// and gradient (m_new is then quantized by the block quantizer);
+// k_update produces the update from u (or c) and the quantized parameter.
+// NS (Newton-Schulz) is plain GEMMs and runs on the BLAS library.
+//
+// Arithmetic follows the reference's operation order with one rounding per
+// operation: products and sums are separately rounded (no fused
+// multiply-add).  The momentum runs in the leaf's dtype (bf16: every
+// intermediate rounded to bf16), with the Python-scalar constants rounded to
+// it by the host.  The update runs in f32: the learning rates come from
+// schedules of the int32 step count, f32 arrays that promote the bf16
+// operands (only u * sqrt(max(N, M)) stays in the leaf's dtype).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fp8_math.h"
+#include "pratchya_fp8.h"
+
+int pratchya_set_error(int code, const char* fmt, ...);
+
+#pragma clang fp contract(off)
+
+namespace {
+
+using namespace pfp8;
+
+// Round to the arithmetic dtype (identity for f32).
+template <bool BF16>
+__device__ __forceinline__ float rnd(float x) {
+  if constexpr (BF16) return u2f(f32_to_bf16_rne(x) << 16);
+  return x;
+}
+
+// Block index of element `off` of a [rows, W] array with tgrid (a, b).
+__device__ __forceinline__ int64_t block_of(int64_t off, int64_t W, int64_t a, int64_t b) {
+  const int64_t i = off / W, c = off - i * W;
+  return (i / a) * (W / b) + c / b;
+}
+
+// Dequantization scale s * G of a block (K blocks per group, _qarr.py:562-564).
+__device__ __forceinline__ float block_scale(const uint8_t* __restrict__ sc8, const float* __restrict__ sc32,
+                                             int64_t blk, int64_t K) {
+  return e8m0_decode(sc8[blk]) * sc32[blk / K];
+}
+
+// Element `off` of an operand given as an fp8 payload (mode 0, block scale
+// sc), bf16 (1) or f32 (2), in the arithmetic dtype.
+template <int MODE, bool BF16>
+__device__ __forceinline__ float operand(const void* __restrict__ x, float sc, int64_t off) {
+  if constexpr (MODE == 0)
+    return rnd<BF16>((e4m3fn_to_f32(static_cast<const uint8_t*>(x)[off]) * sc) * 0.0078125f);
+  else if constexpr (MODE == 1)
+    return u2f((uint32_t) static_cast<const uint16_t*>(x)[off] << 16);
+  else
+    return rnd<BF16>(static_cast<const float*>(x)[off]);
+}
+
+template <bool BF16>
+__device__ __forceinline__ void store(void* out, int64_t off, float v) {
+  if constexpr (BF16)
+    static_cast<uint16_t*>(out)[off] = (uint16_t)f32_to_bf16_rne(v);
+  else
+    static_cast<float*>(out)[off] = v;
+}
+
+// c = b1*m + b1c*g and m_new = b2*m + b2c*g for CH consecutive elements per
+// thread, CH dividing b (one block per chunk; the momentum shares the
+// gradient's layout).
+template <int G_MODE, bool BF16, int CH>
+__global__ __launch_bounds__(256) void k_momentum(const uint8_t* __restrict__ m8, const uint8_t* __restrict__ m_sc8,
+                                                  const float* __restrict__ m_sc32, const void* __restrict__ g,
+                                                  const uint8_t* __restrict__ g_sc8, const float* __restrict__ g_sc32,
+                                                  int64_t n_chunks, int64_t W, int64_t a, int64_t b, int64_t K,
+                                                  float b1, float b1c, float b2, float b2c, void* __restrict__ c_out,
+                                                  void* __restrict__ m_new) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_chunks) return;
+  const int64_t base = t * CH;
+  const int64_t blk = block_of(base, W, a, b);
+  const float msc = block_scale(m_sc8, m_sc32, blk, K);
+  const float gsc = G_MODE == 0 ? block_scale(g_sc8, g_sc32, blk, K) : 0.0f;
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int64_t off = base + k;
+    const float mv = operand<0, BF16>(m8, msc, off);
+    const float gv = operand<G_MODE, BF16>(g, gsc, off);
+    const float c = rnd<BF16>(rnd<BF16>(b1 * mv) + rnd<BF16>(b1c * gv));
+    const float nm = rnd<BF16>(rnd<BF16>(b2 * mv) + rnd<BF16>(b2c * gv));
+    store<BF16>(c_out, off, c);
+    store<BF16>(m_new, off, nm);
+  }
+}
+
+// jnp.sign: +-1 for nonzero, the argument itself for +-0 and NaN.
+__device__ __forceinline__ float sign_of(float x) { return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : x); }
+
+// update = -(lr * u' + lr_wd * p) in f32, u' = sign(u) (Lion) or u * scale
+// in the leaf's dtype (Muon), p in the leaf's dtype; CH consecutive elements
+// per thread as in k_momentum.
+template <bool SIGN, int U_MODE, int P_MODE, bool BF16, bool OUT_BF16, int CH>
+__global__ __launch_bounds__(256) void k_update(const void* __restrict__ u, const void* __restrict__ p,
+                                                const uint8_t* __restrict__ p_sc8, const float* __restrict__ p_sc32,
+                                                int64_t n_chunks, int64_t W, int64_t a, int64_t b, int64_t K,
+                                                float scale, float lr, float lr_wd, void* __restrict__ out) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_chunks) return;
+  const int64_t base = t * CH;
+  const float psc = P_MODE == 0 ? block_scale(p_sc8, p_sc32, block_of(base, W, a, b), K) : 0.0f;
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int64_t off = base + k;
+    const float uv = operand<U_MODE, BF16>(u, 0.0f, off);
+    const float ut = SIGN ? sign_of(uv) : rnd<BF16>(uv * scale);
+    const float pv = operand<P_MODE, BF16>(p, psc, off);
+    const float v = -((lr * ut) + (lr_wd * pv));
+    store<OUT_BF16>(out, off, v);
+  }
+}
+
+int64_t gcd64(int64_t x, int64_t y) {
+  while (y) {
+    const int64_t t = x % y;
+    x = y;
+    y = t;
+  }
+  return x;
+}
+
+struct Grid {
+  int64_t n, W, a, b, K;
+  int ch() const { return b % 4 == 0 ? 4 : 1; }   // elements per thread: a divisor of b
+};
+
+int make_grid(const char* what, int64_t S, int64_t H, int64_t W, int64_t a, int64_t b, Grid* g) {
+  if (S < 0 || H < 0 || W < 0 || a < 1 || b < 1 || H % a || W % b)
+    return pratchya_set_error(PRATCHYA_EINVAL, "%s: tgrid (%lld, %lld) does not fit the slice (%lld, %lld)", what,
+                              (long long)a, (long long)b, (long long)H, (long long)W);
+  const int64_t n_blk = (H / a) * (W / b);
+  const int64_t target = (a * b) / 16 > 1 ? (a * b) / 16 : 1;
+  g->n = S * H * W;
+  g->W = W;
+  g->a = a;
+  g->b = b;
+  g->K = n_blk ? gcd64(target, n_blk) : 1;
+  return PRATCHYA_OK;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return pratchya_set_error(PRATCHYA_EHIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return PRATCHYA_OK;
+}
+
+bool is_float_dtype(int d) { return d == PRATCHYA_DT_F32 || d == PRATCHYA_DT_BF16; }
+
+}  // namespace
+
+extern "C" int pratchya_momentum(const uint8_t* m_fp8, const uint8_t* m_sc8, const float* m_sc32, const void* g,
+                                 int g_dtype, const uint8_t* g_sc8, const float* g_sc32, int64_t slices, int64_t H,
+                                 int64_t W, int64_t a, int64_t b, int arith_dtype, float beta1, float beta1c,
+                                 float beta2, float beta2c, void* c_out, void* m_new, hipStream_t stream) {
+  Grid L;
+  int rc = make_grid("momentum", slices, H, W, a, b, &L);
+  if (rc) return rc;
+  if (!is_float_dtype(arith_dtype))
+    return pratchya_set_error(PRATCHYA_EINVAL, "momentum: arithmetic dtype must be f32 or bf16 (got %d)", arith_dtype);
+  if (g_dtype != PRATCHYA_DT_E4M3 && !is_float_dtype(g_dtype))
+    return pratchya_set_error(PRATCHYA_EINVAL, "momentum: unsupported gradient dtype %d", g_dtype);
+  if (L.n == 0) return PRATCHYA_OK;
+  if (!m_fp8 || !m_sc8 || !m_sc32 || !g || !c_out || !m_new || (g_dtype == PRATCHYA_DT_E4M3 && (!g_sc8 || !g_sc32)))
+    return pratchya_set_error(PRATCHYA_EINVAL, "momentum: null buffer");
+  const int ch = L.ch();
+  const int64_t chunks = L.n / ch;
+  if (chunks / 256 + 1 > 0x7FFFFFFF) return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "momentum: too many elements");
+  const dim3 grid((unsigned)((chunks + 255) / 256));
+#define PRATCHYA_MOM(GM, BF, C)                                                                               \
+  hipLaunchKernelGGL((k_momentum<GM, BF, C>), grid, dim3(256), 0, stream, m_fp8, m_sc8, m_sc32, g, g_sc8, g_sc32, \
+                     chunks, L.W, L.a, L.b, L.K, beta1, beta1c, beta2, beta2c, c_out, m_new)
+#define PRATCHYA_MOM_G(BF, C)                                 \
+  if (g_dtype == PRATCHYA_DT_E4M3) PRATCHYA_MOM(0, BF, C);    \
+  else if (g_dtype == PRATCHYA_DT_BF16) PRATCHYA_MOM(1, BF, C); \
+  else PRATCHYA_MOM(2, BF, C);
+  const bool bf = arith_dtype == PRATCHYA_DT_BF16;
+  if (ch == 4) {
+    if (bf) { PRATCHYA_MOM_G(true, 4) } else { PRATCHYA_MOM_G(false, 4) }
+  } else {
+    if (bf) { PRATCHYA_MOM_G(true, 1) } else { PRATCHYA_MOM_G(false, 1) }
+  }
+#undef PRATCHYA_MOM_G
+#undef PRATCHYA_MOM
+  return check_launch("momentum");
+}
+
+extern "C" int pratchya_apply_update(const void* u, int u_dtype, int use_sign, float scale, const void* p,
+                                     int p_dtype, const uint8_t* p_sc8, const float* p_sc32, int64_t slices,
+                                     int64_t H, int64_t W, int64_t a, int64_t b, int arith_dtype, float lr,
+                                     float lr_wd, void* out, int out_dtype, hipStream_t stream) {
+  Grid L;
+  int rc = make_grid("apply_update", slices, H, W, a, b, &L);
+  if (rc) return rc;
+  if (!is_float_dtype(arith_dtype) || !is_float_dtype(u_dtype) || !is_float_dtype(out_dtype) ||
+      (p_dtype != PRATCHYA_DT_E4M3 && !is_float_dtype(p_dtype)))
+    return pratchya_set_error(PRATCHYA_EINVAL, "apply_update: unsupported dtypes (u %d, p %d, arith %d, out %d)",
+                              u_dtype, p_dtype, arith_dtype, out_dtype);
+  if (u_dtype == PRATCHYA_DT_F32 && arith_dtype == PRATCHYA_DT_BF16 && !use_sign)
+    return pratchya_set_error(PRATCHYA_EINVAL, "apply_update: an f32 direction needs f32 arithmetic");
+  if (L.n == 0) return PRATCHYA_OK;
+  if (!u || !p || !out || (p_dtype == PRATCHYA_DT_E4M3 && (!p_sc8 || !p_sc32)))
+    return pratchya_set_error(PRATCHYA_EINVAL, "apply_update: null buffer");
+  const int ch = L.ch();
+  const int64_t chunks = L.n / ch;
+  if (chunks / 256 + 1 > 0x7FFFFFFF) return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "apply_update: too many elements");
+  const dim3 grid((unsigned)((chunks + 255) / 256));
+  const bool bf = arith_dtype == PRATCHYA_DT_BF16, ob = out_dtype == PRATCHYA_DT_BF16;
+  use_sign = use_sign ? 1 : 0;
+  const int um = u_dtype == PRATCHYA_DT_BF16 ? 1 : 2;
+  const int pm = p_dtype == PRATCHYA_DT_E4M3 ? 0 : (p_dtype == PRATCHYA_DT_BF16 ? 1 : 2);
+  // one instantiation per (sign, u, p, arithmetic, output) combination in use
+#define PRATCHYA_UPD(SG, UM, PM, BF, OB)                                                                     \
+  if (use_sign == SG && um == UM && pm == PM && bf == BF && ob == OB) {                                       \
+    if (ch == 4)                                                                                              \
+      hipLaunchKernelGGL((k_update<SG, UM, PM, BF, OB, 4>), grid, dim3(256), 0, stream, u, p, p_sc8, p_sc32,   \
+                         chunks, L.W, L.a, L.b, L.K, scale, lr, lr_wd, out);                                   \
+    else                                                                                                      \
+      hipLaunchKernelGGL((k_update<SG, UM, PM, BF, OB, 1>), grid, dim3(256), 0, stream, u, p, p_sc8, p_sc32,   \
+                         chunks, L.W, L.a, L.b, L.K, scale, lr, lr_wd, out);                                   \
+    return check_launch("apply_update");                                                                      \
+  }
+#define PRATCHYA_UPD_P(SG, UM, BF, OB) \
+  PRATCHYA_UPD(SG, UM, 0, BF, OB)      \
+  PRATCHYA_UPD(SG, UM, 1, BF, OB)      \
+  PRATCHYA_UPD(SG, UM, 2, BF, OB)
+  PRATCHYA_UPD_P(1, 1, true, true)
+  PRATCHYA_UPD_P(1, 1, true, false)
+  PRATCHYA_UPD_P(1, 1, false, true)
+  PRATCHYA_UPD_P(1, 1, false, false)
+  PRATCHYA_UPD_P(1, 2, true, true)
+  PRATCHYA_UPD_P(1, 2, true, false)
+  PRATCHYA_UPD_P(1, 2, false, true)
+  PRATCHYA_UPD_P(1, 2, false, false)
+  PRATCHYA_UPD_P(0, 1, true, true)
+  PRATCHYA_UPD_P(0, 1, true, false)
+  PRATCHYA_UPD_P(0, 1, false, true)
+  PRATCHYA_UPD_P(0, 1, false, false)
+  PRATCHYA_UPD_P(0, 2, false, true)
+  PRATCHYA_UPD_P(0, 2, false, false)
+#undef PRATCHYA_UPD_P
+#undef PRATCHYA_UPD
+  return pratchya_set_error(PRATCHYA_EINVAL, "apply_update: unsupported combination");
+}

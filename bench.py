@@ -24,6 +24,7 @@ sys.path.insert(0, ROOT)
 METRIC = "block-scaled FP8 GEMM TFLOP/s + quantize GB/s, as % of MI355X peak (1 GPU)"
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
 
 # Algorithmic bytes of config 2 (bf16 in, e4m3fn out, e8m0 per block, f32 per group)
 CFG2_ROWS, CFG2_COLS = 16384, 2048
@@ -316,6 +317,85 @@ def bench_config5(steps: int, warmup: int):
             "path": "pratchya_amd.qarr Linear composition, fp8 backward, eager (no graph)"}
 
 
+def _event_ms(fn, reps: int) -> float:
+    """Mean ms of ``fn()`` over ``reps`` eager calls, timed with HIP events on
+    the current stream after one untimed call."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        fn()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def bench_optimizer(steps: int):
+    """The quantized Miulion optimizer step (pratchya/_nnx_impl/_optimizer.py:
+    62-217) over the six weights of config 5's layer, each a layer-stacked
+    quantized leaf [1, N, M] with tgrid (128, 128) (the model's stacked layout:
+    bf16 momentum arithmetic, Muon with 5 Newton-Schulz iterations in bf16),
+    gradients quantized (128, 128).  Synthetic: weights N(0, 0.02), gradients
+    N(0, 1e-3), seed 6.  Reports the whole step and, on the [16384, 4096]
+    weight, the momentum and update kernels against the HBM roofline and the
+    Newton-Schulz GEMMs against the bf16 MFMA peak."""
+    import torch
+    from pratchya_amd import _kernels as K
+    from pratchya_amd.optim import MiulionHyperParams, MiulionScheduler, miulion_optimizer, newton_schulz
+    from pratchya_amd.qarr import QArrayImpl
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    names = ["w_r", "w_k", "w_v", "w_o", "ffn_up", "ffn_down"]
+    tg = (128, 128)
+    params = {"blocks": {n: QArrayImpl((torch.randn((1, din, dout), generator=gen, device="cuda") * 0.02), tg)
+                         for n, (din, dout) in zip(names, CFG5_LINEARS)}}
+    grads = {"blocks": {n: QArrayImpl((torch.randn((1, din, dout), generator=gen, device="cuda") * 1e-3), tg)
+                        for n, (din, dout) in zip(names, CFG5_LINEARS)}}
+    hp = MiulionHyperParams(lion_lr=4e-3, muon_lr=5e-2)
+    tx = miulion_optimizer(hp, MiulionScheduler(lambda s: 5e-2, lambda s: 4e-3, hp.weight_decay))
+    state = tx.init(params)
+    state = tx.update(grads, state, params)[1]          # a nonzero momentum
+    torch.cuda.synchronize()
+    step_ms = _event_ms(lambda: tx.update(grads, state, params), steps)
+    n_elem = sum(din * dout for din, dout in CFG5_LINEARS)
+    ns_flop = sum(5 * 4 * min(din, dout) ** 2 * max(din, dout) for din, dout in CFG5_LINEARS)
+
+    # kernels of one leaf, the [16384, 4096] FFN down-projection
+    din, dout = CFG5_LINEARS[-1]
+    n = din * dout
+    m_t = state.momentum["blocks"]["ffn_down"]._tree_flatten()[0]
+    g_t = grads["blocks"]["ffn_down"]._tree_flatten()[0]
+    p_t = params["blocks"]["ffn_down"]._tree_flatten()[0]
+    sl = lambda t: tuple(a[0] for a in t)
+    bf = torch.bfloat16
+    c, _ = K.momentum(sl(m_t), sl(g_t), tg, bf, 0.8984375, 0.10009765625, 0.98828125, 0.010009765625)
+    mom_ms = _event_ms(lambda: K.momentum(sl(m_t), sl(g_t), tg, bf, 0.8984375, 0.10009765625, 0.98828125,
+                                          0.010009765625), 10)
+    u = newton_schulz(c, 5)
+    ns_ms = _event_ms(lambda: newton_schulz(c, 5), 3)
+    upd_ms = _event_ms(lambda: K.apply_update(u, False, 128.0, sl(p_t), tg, bf, 0.05, 0.005, bf), 10)
+    mom_bytes = n * (1 + 1 + 2 + 2)          # fp8 momentum + fp8 gradient in, bf16 c + bf16 new momentum out
+    upd_bytes = n * (2 + 1 + 2)              # bf16 u + fp8 parameter in, bf16 update out
+    leaf_ns_flop = 5 * 4 * min(din, dout) ** 2 * max(din, dout)
+    mom_gbs = mom_bytes / (mom_ms * 1e-3) / 1e9
+    upd_gbs = upd_bytes / (upd_ms * 1e-3) / 1e9
+    ns_tf = leaf_ns_flop / (ns_ms * 1e-3) / 1e12
+    return {"ms_per_step": round(step_ms, 3), "weights": "config 5 layer: 4 x [4096,4096], [4096,16384], "
+                                                         "[16384,4096] as [1, N, M] quantized (128,128)",
+            "elements": n_elem, "newton_schulz_flop": ns_flop,
+            "step_effective_bf16_TFLOP/s": round(ns_flop / (step_ms * 1e-3) / 1e12, 1),
+            "ffn_down_momentum": {"us": round(mom_ms * 1e3, 1), "GB/s": round(mom_gbs, 1),
+                                  "frac_of_hbm_peak": round(mom_gbs / HBM_PEAK_GBS, 4), "bytes": mom_bytes},
+            "ffn_down_update": {"us": round(upd_ms * 1e3, 1), "GB/s": round(upd_gbs, 1),
+                                "frac_of_hbm_peak": round(upd_gbs / HBM_PEAK_GBS, 4), "bytes": upd_bytes},
+            "ffn_down_newton_schulz": {"ms": round(ns_ms, 3), "TFLOP/s": round(ns_tf, 1),
+                                       "frac_of_bf16_peak": round(ns_tf / BF16_PEAK_TFLOPS, 4),
+                                       "flop": leaf_ns_flop, "library": "torch.matmul (hipBLASLt)"},
+            "steps": steps}
+
+
 COPY_BYTES = 256 << 20   # bytes read (and written) by the reference copy of the counter runs
 
 
@@ -376,7 +456,7 @@ def main():
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--counter-workload", action="store_true",
                     help="only run the direct-launch workload used for rocprofv3 --pmc runs")
-    ap.add_argument("--only", choices=["cfg3", "cfg4", "cfg5"], default=None,
+    ap.add_argument("--only", choices=["cfg3", "cfg4", "cfg5", "optim"], default=None,
                     help="run one secondary configuration alone (for profiling) and print its result")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -398,6 +478,8 @@ def main():
             res = {"ms": ms_, "TFLOP/s": tf_}
         elif args.only == "cfg4":
             res = bench_config4(max(20, args.steps // 4), max(4, args.warmup // 4))
+        elif args.only == "optim":
+            res = bench_optimizer(3)
         else:
             res = bench_config5(max(3, args.steps // 40), 2)
         print(json.dumps({args.only: res}), flush=True)
@@ -423,6 +505,9 @@ def main():
         _log("config 5: start")
         extra["config5_layer"] = bench_config5(max(3, args.steps // 40), 2)
         _log(f"config 5: {extra['config5_layer']['tokens_per_s']} tokens/s")
+        _log("optimizer step: start")
+        extra["optimizer_step"] = bench_optimizer(3)
+        _log(f"optimizer step: {extra['optimizer_step']['ms_per_step']} ms")
     cpu = None
     if not args.no_cpu_baseline:
         _log("cpu baseline: start")

@@ -25,6 +25,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <initializer_list>
+#include <utility>
+
 #include "fp8_math.h"
 #include "pratchya_fp8.h"
 
@@ -55,24 +58,45 @@ __device__ __forceinline__ float block_scale(const uint8_t* __restrict__ sc8, co
   return e8m0_decode(sc8[blk]) * sc32[blk / K];
 }
 
-// Element `off` of an operand given as an fp8 payload (mode 0, block scale
-// sc), bf16 (1) or f32 (2), in the arithmetic dtype.
-template <int MODE, bool BF16>
-__device__ __forceinline__ float operand(const void* __restrict__ x, float sc, int64_t off) {
-  if constexpr (MODE == 0)
-    return rnd<BF16>((e4m3fn_to_f32(static_cast<const uint8_t*>(x)[off]) * sc) * 0.0078125f);
-  else if constexpr (MODE == 1)
-    return u2f((uint32_t) static_cast<const uint16_t*>(x)[off] << 16);
-  else
-    return rnd<BF16>(static_cast<const float*>(x)[off]);
+// CH elements of type T loaded or stored as one unit (16-byte vector
+// accesses for 16 or more bytes; the host checks the alignment).
+template <typename T, int CH>
+struct alignas((sizeof(T) * CH) >= 16 ? 16 : sizeof(T) * CH) Vec {
+  T v[CH];
+};
+
+// CH consecutive elements from `off` of an operand given as an fp8 payload
+// (mode 0, block scale sc), bf16 (1) or f32 (2), in the arithmetic dtype.
+template <int MODE, bool BF16, int CH>
+__device__ __forceinline__ void load_operand(const void* __restrict__ x, float sc, int64_t off, float (&out)[CH]) {
+  if constexpr (MODE == 0) {
+    const Vec<uint8_t, CH> w = *reinterpret_cast<const Vec<uint8_t, CH>*>(static_cast<const uint8_t*>(x) + off);
+#pragma unroll
+    for (int k = 0; k < CH; ++k) out[k] = rnd<BF16>((e4m3fn_to_f32(w.v[k]) * sc) * 0.0078125f);
+  } else if constexpr (MODE == 1) {
+    const Vec<uint16_t, CH> w = *reinterpret_cast<const Vec<uint16_t, CH>*>(static_cast<const uint16_t*>(x) + off);
+#pragma unroll
+    for (int k = 0; k < CH; ++k) out[k] = u2f((uint32_t)w.v[k] << 16);
+  } else {
+    const Vec<float, CH> w = *reinterpret_cast<const Vec<float, CH>*>(static_cast<const float*>(x) + off);
+#pragma unroll
+    for (int k = 0; k < CH; ++k) out[k] = rnd<BF16>(w.v[k]);
+  }
 }
 
-template <bool BF16>
-__device__ __forceinline__ void store(void* out, int64_t off, float v) {
-  if constexpr (BF16)
-    static_cast<uint16_t*>(out)[off] = (uint16_t)f32_to_bf16_rne(v);
-  else
-    static_cast<float*>(out)[off] = v;
+template <bool BF16, int CH>
+__device__ __forceinline__ void store_chunk(void* out, int64_t off, const float (&v)[CH]) {
+  if constexpr (BF16) {
+    Vec<uint16_t, CH> w;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) w.v[k] = (uint16_t)f32_to_bf16_rne(v[k]);
+    *reinterpret_cast<Vec<uint16_t, CH>*>(static_cast<uint16_t*>(out) + off) = w;
+  } else {
+    Vec<float, CH> w;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) w.v[k] = v[k];
+    *reinterpret_cast<Vec<float, CH>*>(static_cast<float*>(out) + off) = w;
+  }
 }
 
 // c = b1*m + b1c*g and m_new = b2*m + b2c*g for CH consecutive elements per
@@ -91,16 +115,16 @@ __global__ __launch_bounds__(256) void k_momentum(const uint8_t* __restrict__ m8
   const int64_t blk = block_of(base, W, a, b);
   const float msc = block_scale(m_sc8, m_sc32, blk, K);
   const float gsc = G_MODE == 0 ? block_scale(g_sc8, g_sc32, blk, K) : 0.0f;
+  float mv[CH], gv[CH], c[CH], nm[CH];
+  load_operand<0, BF16, CH>(m8, msc, base, mv);
+  load_operand<G_MODE, BF16, CH>(g, gsc, base, gv);
 #pragma unroll
   for (int k = 0; k < CH; ++k) {
-    const int64_t off = base + k;
-    const float mv = operand<0, BF16>(m8, msc, off);
-    const float gv = operand<G_MODE, BF16>(g, gsc, off);
-    const float c = rnd<BF16>(rnd<BF16>(b1 * mv) + rnd<BF16>(b1c * gv));
-    const float nm = rnd<BF16>(rnd<BF16>(b2 * mv) + rnd<BF16>(b2c * gv));
-    store<BF16>(c_out, off, c);
-    store<BF16>(m_new, off, nm);
+    c[k] = rnd<BF16>(rnd<BF16>(b1 * mv[k]) + rnd<BF16>(b1c * gv[k]));
+    nm[k] = rnd<BF16>(rnd<BF16>(b2 * mv[k]) + rnd<BF16>(b2c * gv[k]));
   }
+  store_chunk<BF16, CH>(c_out, base, c);
+  store_chunk<BF16, CH>(m_new, base, nm);
 }
 
 // jnp.sign: +-1 for nonzero, the argument itself for +-0 and NaN.
@@ -118,15 +142,15 @@ __global__ __launch_bounds__(256) void k_update(const void* __restrict__ u, cons
   if (t >= n_chunks) return;
   const int64_t base = t * CH;
   const float psc = P_MODE == 0 ? block_scale(p_sc8, p_sc32, block_of(base, W, a, b), K) : 0.0f;
+  float uv[CH], pv[CH], v[CH];
+  load_operand<U_MODE, BF16, CH>(u, 0.0f, base, uv);
+  load_operand<P_MODE, BF16, CH>(p, psc, base, pv);
 #pragma unroll
   for (int k = 0; k < CH; ++k) {
-    const int64_t off = base + k;
-    const float uv = operand<U_MODE, BF16>(u, 0.0f, off);
-    const float ut = SIGN ? sign_of(uv) : rnd<BF16>(uv * scale);
-    const float pv = operand<P_MODE, BF16>(p, psc, off);
-    const float v = -((lr * ut) + (lr_wd * pv));
-    store<OUT_BF16>(out, off, v);
+    const float ut = SIGN ? sign_of(uv[k]) : rnd<BF16>(uv[k] * scale);
+    v[k] = -((lr * ut) + (lr_wd * pv[k]));
   }
+  store_chunk<OUT_BF16, CH>(out, base, v);
 }
 
 int64_t gcd64(int64_t x, int64_t y) {
@@ -140,8 +164,24 @@ int64_t gcd64(int64_t x, int64_t y) {
 
 struct Grid {
   int64_t n, W, a, b, K;
-  int ch() const { return b % 4 == 0 ? 4 : 1; }   // elements per thread: a divisor of b
 };
+
+// Elements per thread: 16 or 4 when they divide b (a chunk then lies in one
+// block) and every pointer is aligned for the vector accesses, else 1.
+int chunk_of(int64_t b, std::initializer_list<std::pair<const void*, int>> ptrs) {
+  for (int ch : {16, 4}) {
+    if (b % ch) continue;
+    bool ok = true;
+    for (auto [p, esz] : ptrs) {
+      const int64_t need = (int64_t)ch * esz >= 16 ? 16 : (int64_t)ch * esz;
+      if (p && reinterpret_cast<uintptr_t>(p) % need) ok = false;
+    }
+    if (ok) return ch;
+  }
+  return 1;
+}
+
+int dtype_size(int d) { return d == PRATCHYA_DT_F32 ? 4 : (d == PRATCHYA_DT_BF16 ? 2 : 1); }
 
 int make_grid(const char* what, int64_t S, int64_t H, int64_t W, int64_t a, int64_t b, Grid* g) {
   if (S < 0 || H < 0 || W < 0 || a < 1 || b < 1 || H % a || W % b)
@@ -181,7 +221,8 @@ extern "C" int pratchya_momentum(const uint8_t* m_fp8, const uint8_t* m_sc8, con
   if (L.n == 0) return PRATCHYA_OK;
   if (!m_fp8 || !m_sc8 || !m_sc32 || !g || !c_out || !m_new || (g_dtype == PRATCHYA_DT_E4M3 && (!g_sc8 || !g_sc32)))
     return pratchya_set_error(PRATCHYA_EINVAL, "momentum: null buffer");
-  const int ch = L.ch();
+  const int ch = chunk_of(L.b, {{m_fp8, 1}, {g, dtype_size(g_dtype)}, {c_out, dtype_size(arith_dtype)},
+                                {m_new, dtype_size(arith_dtype)}});
   const int64_t chunks = L.n / ch;
   if (chunks / 256 + 1 > 0x7FFFFFFF) return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "momentum: too many elements");
   const dim3 grid((unsigned)((chunks + 255) / 256));
@@ -193,7 +234,9 @@ extern "C" int pratchya_momentum(const uint8_t* m_fp8, const uint8_t* m_sc8, con
   else if (g_dtype == PRATCHYA_DT_BF16) PRATCHYA_MOM(1, BF, C); \
   else PRATCHYA_MOM(2, BF, C);
   const bool bf = arith_dtype == PRATCHYA_DT_BF16;
-  if (ch == 4) {
+  if (ch == 16) {
+    if (bf) { PRATCHYA_MOM_G(true, 16) } else { PRATCHYA_MOM_G(false, 16) }
+  } else if (ch == 4) {
     if (bf) { PRATCHYA_MOM_G(true, 4) } else { PRATCHYA_MOM_G(false, 4) }
   } else {
     if (bf) { PRATCHYA_MOM_G(true, 1) } else { PRATCHYA_MOM_G(false, 1) }
@@ -219,7 +262,7 @@ extern "C" int pratchya_apply_update(const void* u, int u_dtype, int use_sign, f
   if (L.n == 0) return PRATCHYA_OK;
   if (!u || !p || !out || (p_dtype == PRATCHYA_DT_E4M3 && (!p_sc8 || !p_sc32)))
     return pratchya_set_error(PRATCHYA_EINVAL, "apply_update: null buffer");
-  const int ch = L.ch();
+  const int ch = chunk_of(L.b, {{u, dtype_size(u_dtype)}, {p, dtype_size(p_dtype)}, {out, dtype_size(out_dtype)}});
   const int64_t chunks = L.n / ch;
   if (chunks / 256 + 1 > 0x7FFFFFFF) return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "apply_update: too many elements");
   const dim3 grid((unsigned)((chunks + 255) / 256));
@@ -230,7 +273,10 @@ extern "C" int pratchya_apply_update(const void* u, int u_dtype, int use_sign, f
   // one instantiation per (sign, u, p, arithmetic, output) combination in use
 #define PRATCHYA_UPD(SG, UM, PM, BF, OB)                                                                     \
   if (use_sign == SG && um == UM && pm == PM && bf == BF && ob == OB) {                                       \
-    if (ch == 4)                                                                                              \
+    if (ch == 16)                                                                                             \
+      hipLaunchKernelGGL((k_update<SG, UM, PM, BF, OB, 16>), grid, dim3(256), 0, stream, u, p, p_sc8, p_sc32,  \
+                         chunks, L.W, L.a, L.b, L.K, scale, lr, lr_wd, out);                                   \
+    else if (ch == 4)                                                                                         \
       hipLaunchKernelGGL((k_update<SG, UM, PM, BF, OB, 4>), grid, dim3(256), 0, stream, u, p, p_sc8, p_sc32,   \
                          chunks, L.W, L.a, L.b, L.K, scale, lr, lr_wd, out);                                   \
     else                                                                                                      \

@@ -53,7 +53,8 @@ def _host(t: torch.Tensor) -> np.ndarray:
     return t.float().cpu().numpy()
 
 
-@pytest.mark.parametrize("shape,tgrid", [((256, 384), (128, 128)), ((64, 256), (1, 128)), ((2, 6, 12), (3, 6))])
+@pytest.mark.parametrize("shape,tgrid", [((256, 384), (128, 128)), ((64, 256), (1, 128)), ((2, 6, 12), (3, 6)),
+                                         ((4, 8, 16), (2, 4))])
 @pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
 @pytest.mark.parametrize("gmode", ["fp8", "bf16", "f32"])
 def test_momentum_kernel(shape, tgrid, dtype, gmode):
@@ -218,6 +219,27 @@ def test_miulion_two_steps():
         assert_f32_bits_equal(_host(state.momentum["norm"]),
                               (np.float32(0.99) * m + np.float32(1.0 - 0.99) * g).astype(np.float32),
                               f"norm step {step} momentum")
+
+
+def test_misaligned_operands():
+    """Operands at offsets that rule out vector accesses take the scalar path
+    with the same results."""
+    rng = np.random.default_rng(8)
+    shape, tgrid = (128, 256), (128, 128)
+    m = _quantized(rng, shape, tgrid)
+    gv = (rng.standard_normal(shape) * 1e-3).astype(np.float32)
+    big = torch.zeros(shape[0] * shape[1] + 1, device="cuda")
+    big[1:] = torch.from_numpy(gv.reshape(-1)).cuda()
+    g_dev = big[1:].view(shape)                      # 4-byte aligned only
+    c, nm = _K().momentum(_dev_triple(m), g_dev, tgrid, torch.float32, 0.9, 0.1, 0.99, 0.01)
+    torch.cuda.synchronize()
+    wc, wnm = OO.momentum(_deq(m, tgrid, "float32"), gv, 0.9, 0.99, "float32")
+    assert_f32_bits_equal(_host(c), wc, "misaligned c")
+    assert_f32_bits_equal(_host(nm), wnm, "misaligned m_new")
+    upd = _K().apply_update(g_dev, True, 0.0, _dev_triple(m), tgrid, torch.float32, 0.02, 0.002, torch.float32)
+    torch.cuda.synchronize()
+    want = OO.apply_update(gv, True, 0.0, _deq(m, tgrid, "float32"), 0.02, 0.1, "float32")
+    assert_f32_bits_equal(_host(upd), want, "misaligned update")
 
 
 def test_argument_errors():

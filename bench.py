@@ -202,6 +202,27 @@ def bench_gemm_fwd(steps: int, warmup: int):
     return ms, 2.0 * M * N * Kd / (ms * 1e-3) / 1e12
 
 
+def bench_library_fp8(steps: int):
+    """Reference point for the GEMM: hipBLASLt's plain FP8 GEMM
+    (``torch._scaled_mm``, e4m3fn operands, one scale per tensor, bf16 out) at
+    config 3's shape, timed like the other legs.  It has no block scales, so
+    it is context for the MFMA efficiency of the block-scaled kernel, not the
+    same computation."""
+    import torch
+    M, Kd, N = 16384, 2048, 8192
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    a = torch.randn((M, Kd), generator=gen, device="cuda").to(torch.float8_e4m3fn)
+    b = (torch.randn((N, Kd), generator=gen, device="cuda") * 0.1).to(torch.float8_e4m3fn).t()
+    one = torch.tensor(1.0, device="cuda")
+    try:
+        ms = _event_ms(lambda: torch._scaled_mm(a, b, scale_a=one, scale_b=one, out_dtype=torch.bfloat16), steps)
+    except Exception as ex:                       # the library call is context only
+        return {"error": repr(ex)[:200]}
+    tf = 2 * M * N * Kd / (ms * 1e-3) / 1e12
+    return {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1), "frac_of_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4),
+            "call": "torch._scaled_mm, tensor-wise scales (hipBLASLt)"}
+
+
 def bench_config4(steps: int, warmup: int):
     """Config 4, the backward of config 3's Linear: dY bf16 [16384, 8192] ~
     N(0, 1e-3) (seed 4) requantized (1, 128) for dgrad and (128, 1) along
@@ -499,7 +520,8 @@ def main():
         extra["config3_gemm_fwd"] = {"value": round(tflops, 1), "unit": "TFLOP/s", "ms": round(gms, 4),
                                      "frac_of_fp8_peak": round(tflops / FP8_PEAK_TFLOPS, 4),
                                      "shape": "[16384,2048] x [2048,8192] -> bf16",
-                                     "flop": 2 * 16384 * 2048 * 8192}
+                                     "flop": 2 * 16384 * 2048 * 8192,
+                                     "hipblaslt_fp8_no_block_scales": bench_library_fp8(20)}
         _log("config 4: start")
         extra["config4_backward"] = bench_config4(max(20, args.steps // 4), max(4, args.warmup // 4))
         _log("config 5: start")

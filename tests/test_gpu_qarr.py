@@ -142,6 +142,40 @@ def test_linear_forward_backward(Q, mode):
     assert rel(f32(w.grad), gw_ref) <= TOL, rel(f32(w.grad), gw_ref)
 
 
+# lm_head: Linear(hidden, vocab, (blksize, 1)) (_model.py:77); LoRA:
+# Linear(hidden, rank, (a, 1)) then Linear(rank, hidden, (b, 1)) (M:75-88).
+# The product's grid is (1, 1): every element is its own group.
+ODD_LINEARS = {"lm_head": (256, 512), "lora_down": (1024, 128), "lora_up": (128, 1024)}
+
+
+@pytest.mark.parametrize("mode", ["f32", "fp8"])
+@pytest.mark.parametrize("case", sorted(ODD_LINEARS))
+def test_odd_grid_linears(Q, mode, case):
+    Q.set_matmul_backward(mode)
+    Kd, N = ODD_LINEARS[case]
+    xb, wb, gb = _linear_case(seed=31, M=256, Kd=Kd, N=N)
+    x = to_dev_bf16(xb).requires_grad_(True)
+    w = to_dev_bf16(wb).requires_grad_(True)
+    out = Q.QArrayImpl(x, (1, 128)) @ Q.QArrayImpl(w, (128, 1))
+    assert out.tgrid == (1, 1)
+    y = out.astype(torch.bfloat16)
+    y.backward(to_dev_bf16(gb))
+    _, o8, o32 = triple(out)
+    xq, wq = oq(O.bf16_bits_to_f32(xb), (1, 128)), oq(O.bf16_bits_to_f32(wb), (128, 1))
+    xd, wd = odq(xq, (1, 128)).astype(np.float64), odq(wq, (128, 1)).astype(np.float64)
+    out32 = (xd @ wd).astype(np.float32)
+    y_ref = O.bf16_bits_to_f32(odq(oq(out32, (1, 1)), (1, 1), "bfloat16"))
+    assert rel(f32(y), y_ref) <= TOL
+    # the product's (1,1) scales: e8m0 127 and G = |element| (r = 1) wherever |out| >= 1e-7
+    big = np.abs(out32) > 1e-3
+    assert np.all(o8.reshape(out32.shape)[big] == 127)
+    g1 = O.bf16_bits_to_f32(O.dequantize_bwd(O.bf16_bits_to_f32(gb), o8, o32, (1, 1), "bfloat16")).astype(np.float64)
+    gx = O.bf16_round(odq(oq((g1 @ wd.T).astype(np.float32), (1, 128)), (1, 128)))
+    gw = O.bf16_round(odq(oq((xd.T @ g1).astype(np.float32), (128, 1)), (128, 1)))
+    assert rel(f32(x.grad), gx) <= TOL, rel(f32(x.grad), gx)
+    assert rel(f32(w.grad), gw) <= TOL, rel(f32(w.grad), gw)
+
+
 def test_linear_forward_uses_the_fp8_kernel(Q, monkeypatch):
     """A (1,128) x (128,128) forward of tile-multiple shape must run the MFMA
     GEMM, not the dequantize-and-matmul path."""

@@ -423,7 +423,7 @@ def gemm_nt(a: Operand, b: Operand, out_dtype: torch.dtype = torch.bfloat16,
     return out
 
 
-def _as_operand(x, tgrid, what):
+def _as_operand(x, what):
     """(tensor, dtype code, sc8, sc32) of an optimizer operand: an fp8 payload
     given as a (payload, sc8, sc32) triple, or a bf16 / f32 tensor."""
     if isinstance(x, (tuple, list)):
@@ -443,8 +443,8 @@ def momentum(m, g, tgrid, arith: torch.dtype, beta1: float, beta1c: float, beta2
     ``m``: the quantized momentum as a (payload, sc8, sc32) triple with tgrid
     ``tgrid``; ``g``: a triple in the same layout or a bf16 / f32 tensor.  The
     constants must be values of ``arith``.  Returns ``(c, m_new)`` in ``arith``."""
-    m8, _, ms8, ms32 = _as_operand(m, tgrid, "momentum")
-    gt, gcode, gs8, gs32 = _as_operand(g, tgrid, "momentum gradient")
+    m8, _, ms8, ms32 = _as_operand(m, "momentum")
+    gt, gcode, gs8, gs32 = _as_operand(g, "momentum gradient")
     if tuple(gt.shape) != tuple(m8.shape):
         raise ValueError(f"momentum: gradient shape {tuple(gt.shape)} != momentum shape {tuple(m8.shape)}")
     S, H, W = slices_hw(m8.shape)
@@ -469,7 +469,7 @@ def apply_update(u: torch.Tensor, use_sign: bool, scale: float, p, tgrid, arith:
     tensor of ``u``'s shape."""
     _require_gpu(u)
     uu = u.contiguous()
-    pt, pcode, ps8, ps32 = _as_operand(p, tgrid, "update parameter")
+    pt, pcode, ps8, ps32 = _as_operand(p, "update parameter")
     if tuple(pt.shape) != tuple(uu.shape):
         raise ValueError(f"apply_update: parameter shape {tuple(pt.shape)} != direction shape {tuple(uu.shape)}")
     S, H, W = slices_hw(uu.shape)

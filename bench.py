@@ -56,6 +56,51 @@ def cpu_baseline_quantize(rows: int = 2048, min_seconds: float = 10.0):
                       f"config 2, tgrid (1,128), {reps} reps, {el:.1f} s (NumPy, single thread)"}
 
 
+def _blas_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+        return max((d.get("num_threads", 1) for d in threadpool_info() if d.get("user_api") == "blas"), default=1)
+    except Exception:                     # threadpoolctl is optional
+        return 1
+
+
+def cpu_baseline_config1(reps: int = 5):
+    """The oracle's config-1 round trip (quantize (128,128) + dequantize to
+    bf16 of the seeded [1024,1024] tensor), the reference's own CPU-runnable
+    case, on this host."""
+    from oracle import qarr_oracle as O
+    x = O.bf16_bits_to_f32(O.normal_input((CFG1_N, CFG1_N), 1.0, seed=1))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        q = O.quantize_impl(x, (128, 128))
+        O.dequantize_impl(*q, "bfloat16", (128, 128))
+    per = (time.perf_counter() - t0) / reps
+    return {"value": round(CFG1_BYTES / per / 1e9, 4), "unit": "GB/s", "us_per_round_trip": round(per * 1e6, 1),
+            "cores": 1, "kind": "port", "sample": f"full config 1, {reps} reps (NumPy, single thread)"}
+
+
+def cpu_baseline_config3(rows: int = 512):
+    """The oracle's config-3 forward -- dequantize both operands to f32 and
+    multiply (matmul_impl, Q:605-608) -- on a row sample of the activation,
+    on this host's BLAS threads."""
+    from oracle import qarr_oracle as O
+    Kd, N = 2048, 8192
+    xq = O.quantize_impl(O.bf16_bits_to_f32(O.activation_input(rows, Kd, seed=2)), (1, 128))
+    wq = O.quantize_impl(O.bf16_bits_to_f32(O.normal_input((Kd, N), 0.02, seed=3)), (128, 128))
+    xd = O.dequantize_impl(*xq, "float32", (1, 128))
+    wd = O.dequantize_impl(*wq, "float32", (128, 128))
+    xd @ wd                                            # warm
+    t0 = time.perf_counter()
+    reps = 3
+    for _ in range(reps):
+        xd @ wd
+    per = (time.perf_counter() - t0) / reps
+    tf = 2 * rows * Kd * N / per / 1e12
+    return {"value": round(tf, 4), "unit": "TFLOP/s", "cores": _blas_threads(), "kind": "port",
+            "sample": f"f32 matmul of the dequantized operands, {rows} of 16384 rows, {reps} reps "
+                      f"(NumPy / OpenBLAS)"}
+
+
 MAX_GRAPH_STEPS = 256
 
 
@@ -535,6 +580,10 @@ def main():
         _log("cpu baseline: start")
         cpu = cpu_baseline_quantize()
         _log(f"cpu baseline: {cpu['value']} GB/s")
+        extra["config1_round_trip"]["cpu_baseline"] = cpu_baseline_config1()
+        if "config3_gemm_fwd" in extra:
+            extra["config3_gemm_fwd"]["cpu_baseline"] = cpu_baseline_config3()
+        _log("cpu baselines of configs 1 and 3: done")
     line = {
         "metric": METRIC,
         "value": round(gbs, 2),

@@ -14,7 +14,9 @@
 // which is the requantization of a stored activation along the token axis
 // (fp8_matmul's backward, _qarr.py:784-789, quantizes x^T the same way).
 //
-// One wave per 128-token x (8 * CGW)-channel tile.  Lane (rs, cg) holds TOK
+// One wave per 128-token x (8 * CGW)-channel tile (an fp8 input is staged
+// through LDS per 128 x 128 workgroup tile, so that its global loads cover
+// whole 128-byte rows).  Lane (rs, cg) holds TOK
 // consecutive tokens (16 or 8) of the 8 channels of group cg: channel maxima
 // are an in-lane max over TOK tokens plus xor shuffles across rs, the group
 // max an in-lane max over 8 channels, and each channel's TOK payload bytes are
@@ -120,15 +122,46 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
   const int cg = lane % CGW, rs = lane / CGW;
   const int64_t c0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * (8 * CGW) + cg * 8;
   // C is a multiple of 8, so a lane owns a whole group or nothing; the xor
-  // partners of a lane (same cg) share its fate.
-  if (c0 >= C) return;
+  // partners of a lane (same cg) share its fate.  (fp8 inputs: C is a multiple
+  // of 128, so every lane of the grid has a group.)
+  if constexpr (IN != IN_FP8) {
+    if (c0 >= C) return;
+  }
   const int64_t s = blockIdx.z, tb = blockIdx.y;
   const int64_t t0 = tb * 128 + rs * TOK;
 
   uint32_t w[TOK][NW];
-  const uint8_t* xr = x + ((s * T + t0) * C + c0) * ESZ;
+  if constexpr (IN == IN_FP8) {
+    // A lane's rows are 8-byte pieces; read from global memory directly, a
+    // wave's row segments would be 32 bytes.  The workgroup's 128 tokens x
+    // 128 channels are staged through LDS instead, with 16-byte loads that
+    // cover whole 128-byte rows (8 lanes per row).
+    static_assert(TOK == 8 && CGW == 4, "the fp8 tile is 128 tokens x 4 waves x 32 channels");
+    constexpr int kPitch = 136;              // bytes per staged row (8-byte aligned, fewer bank conflicts)
+    __shared__ __attribute__((aligned(16))) uint8_t tile[128 * kPitch];
+    const int64_t cw = (int64_t)blockIdx.x * 128;
+    const uint8_t* xt = x + (s * T + tb * 128) * C + cw;
 #pragma unroll
-  for (int r = 0; r < TOK; ++r) load_row<IN>(xr + (int64_t)r * C * ESZ, w[r]);
+    for (int i = 0; i < 4; ++i) {
+      const int q = i * 256 + (int)threadIdx.x, row = q >> 3, cc = (q & 7) * 16;
+      const uint4 v = load_stream16(reinterpret_cast<const char*>(xt + (int64_t)row * C + cc));
+      uint2* d = reinterpret_cast<uint2*>(tile + row * kPitch + cc);
+      d[0] = make_uint2(v.x, v.y);
+      d[1] = make_uint2(v.z, v.w);
+    }
+    __syncthreads();
+    const int lc = (int)(threadIdx.x >> 6) * 32 + cg * 8;   // the lane's first channel in the tile
+#pragma unroll
+    for (int r = 0; r < TOK; ++r) {
+      const uint2 v = *reinterpret_cast<const uint2*>(tile + (rs * TOK + r) * kPitch + lc);
+      w[r][0] = v.x;
+      w[r][1] = v.y;
+    }
+  } else {
+    const uint8_t* xr = x + ((s * T + t0) * C + c0) * ESZ;
+#pragma unroll
+    for (int r = 0; r < TOK; ++r) load_row<IN>(xr + (int64_t)r * C * ESZ, w[r]);
+  }
 
   float dq[TOK];
 #pragma unroll
@@ -272,7 +305,7 @@ extern "C" int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t*
   if (!x || !xt_fp8 || !sc_fp8 || !sc_fp32 || (x_dtype == PRATCHYA_DT_E4M3 && (!x_sc8 || !x_sc32)))
     return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t128: null buffer");
   const uintptr_t xa = reinterpret_cast<uintptr_t>(x);
-  if (xa % (x_dtype == PRATCHYA_DT_E4M3 ? 8 : 16) || reinterpret_cast<uintptr_t>(xt_fp8) % 16 ||
+  if (xa % 16 || reinterpret_cast<uintptr_t>(xt_fp8) % 16 ||
       reinterpret_cast<uintptr_t>(sc_fp8) % 4 || reinterpret_cast<uintptr_t>(sc_fp32) % 4)
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t128: buffers are not aligned");
   if (T / 128 > 65535 || slices > 65535)

@@ -46,8 +46,14 @@ __device__ __forceinline__ float rnd(float x) {
   return x;
 }
 
-// Block index of element `off` of a [rows, W] array with tgrid (a, b).
-__device__ __forceinline__ int64_t block_of(int64_t off, int64_t W, int64_t a, int64_t b) {
+// Block index of element `off` of a [rows, W] array with tgrid (a, b)
+// (32-bit divisions when the array is small enough).
+__device__ __forceinline__ int64_t block_of(int64_t off, int64_t W, int64_t a, int64_t b, bool narrow) {
+  if (narrow) {
+    const uint32_t o = (uint32_t)off, w = (uint32_t)W;
+    const uint32_t i = o / w, c = o - i * w;
+    return (int64_t)((i / (uint32_t)a) * (w / (uint32_t)b) + c / (uint32_t)b);
+  }
   const int64_t i = off / W, c = off - i * W;
   return (i / a) * (W / b) + c / b;
 }
@@ -112,7 +118,7 @@ __global__ __launch_bounds__(256) void k_momentum(const uint8_t* __restrict__ m8
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n_chunks) return;
   const int64_t base = t * CH;
-  const int64_t blk = block_of(base, W, a, b);
+  const int64_t blk = block_of(base, W, a, b, n_chunks * CH <= 0x7FFFFFFF);
   const float msc = block_scale(m_sc8, m_sc32, blk, K);
   const float gsc = G_MODE == 0 ? block_scale(g_sc8, g_sc32, blk, K) : 0.0f;
   float mv[CH], gv[CH], c[CH], nm[CH];
@@ -141,7 +147,8 @@ __global__ __launch_bounds__(256) void k_update(const void* __restrict__ u, cons
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n_chunks) return;
   const int64_t base = t * CH;
-  const float psc = P_MODE == 0 ? block_scale(p_sc8, p_sc32, block_of(base, W, a, b), K) : 0.0f;
+  const float psc = P_MODE == 0 ? block_scale(p_sc8, p_sc32, block_of(base, W, a, b, n_chunks * CH <= 0x7FFFFFFF), K)
+                                : 0.0f;
   float uv[CH], pv[CH], v[CH];
   load_operand<U_MODE, BF16, CH>(u, 0.0f, base, uv);
   load_operand<P_MODE, BF16, CH>(p, psc, base, pv);

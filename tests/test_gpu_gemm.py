@@ -245,6 +245,50 @@ def test_config3_full_shape_sampled_rows():
     check(C[torch.from_numpy(rows).cuda()], ref, BF16_TOL, "config 3 sampled")
 
 
+def _deq_t128_rows(xt8, s8, s32, T, C, rows):
+    """Host dequantization of rows ``rows`` of a transposed (128,1) payload
+    [C, T] (quantize_impl(x, (128,1)) of x [T, C], payload transposed)."""
+    lut = O.e4m3fn_to_f32(np.arange(256, dtype=np.uint8))
+    q = lut[u8(xt8)[rows]]                                            # [n, T]
+    e = u8(s8).reshape(T // 128, C)[:, rows]                          # [T/128, n]
+    G = f32(s32).reshape(-1)[(np.arange(T // 128)[:, None] * C + np.asarray(rows)[None, :]) // 8]
+    sc = (O.e8m0_to_f32(e) * G).astype(np.float32)                   # [T/128, n]
+    return ((q * np.repeat(sc.T, 128, axis=1)).astype(np.float32) / np.float32(128.0)).astype(np.float64)
+
+
+def test_config4_full_shape_sampled_rows():
+    """Config 4 at full size: dgrad dY [16384,8192] (1,128) x W [2048,8192]
+    (128,128), and wgrad A^T . dY with both operands requantized along tokens
+    by quantize_t128 (A from its stored fp8 payload), f32 outputs.  The
+    oracle product is evaluated on sampled output rows from the GPU operands
+    dequantized on the host (the quantizers' bytes are pinned separately)."""
+    K = _K()
+    T, Cin, N_ = 16384, 2048, 8192
+    dy_bits = O.normal_input((T, N_), 1e-3, seed=4)
+    w_bits = O.normal_input((Cin, N_), 0.02, seed=3)
+    a_bits = O.activation_input(T, Cin, seed=2)
+    dyq = quant_dev(dy_bits, (1, 128))
+    wq = quant_dev(w_bits, (128, 128))
+    dx = K.gemm_nt(K.operand_rows(*dyq, (1, 128)), K.operand_rows(*wq, (128, 128)), torch.float32)
+    a8 = K.quantize(to_dev_bf16(a_bits), (1, 128))
+    at = K.quantize_t128(*a8)
+    dt = K.quantize_t128(to_dev_bf16(dy_bits))
+    dw = K.gemm_nt(K.operand_t128(*at), K.operand_t128(*dt), torch.float32)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(4)
+    # dgrad: 128 sampled rows of dY
+    rows = np.sort(rng.choice(T, 128, replace=False))
+    dys = O.dequantize_impl(u8(dyq[0])[rows], u8(dyq[1]).reshape(T, 8, 8)[rows].reshape(-1, 8),
+                            f32(dyq[2]).reshape(T, 8)[rows].reshape(-1, 1, 1), "float32", (1, 128))
+    ref = dys.astype(np.float64) @ deq_host(*wq, (128, 128)).T
+    check(dx[torch.from_numpy(rows).cuda()], ref, F32_TOL, "config 4 dgrad sampled")
+    # wgrad: 16 sampled channels of A against every channel of dY
+    ch = np.sort(rng.choice(Cin, 16, replace=False))
+    a_rows = _deq_t128_rows(*at, T, Cin, ch)
+    g_all = _deq_t128_rows(*dt, T, N_, np.arange(N_))
+    check(dw[torch.from_numpy(ch).cuda()], a_rows @ g_all.T, F32_TOL, "config 4 wgrad sampled")
+
+
 def test_unsupported_shape_is_reported():
     K = _K()
     xq = quant_dev(O.activation_input(128, 256, seed=1), (1, 128))

@@ -1,7 +1,7 @@
 """Benchmark of the MI355X FP8 block-quantization path.
 
 Contract: ``python bench.py --gpus N --steps K --warmup W`` prints ONE JSON line.
-The headline workload is BASELINE.json configs[1] (activation quantize,
+The headline workload is benchmark configuration 2 (activation quantize,
 bf16 [16384, 2048], per-token 1x128 groups): a step is one quantize pass over
 one synthetic activation tensor already resident in HBM.  Rotating input and
 output buffers (> 256 MB in total) keep the 256 MB MALL from serving repeated

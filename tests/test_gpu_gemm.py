@@ -1,7 +1,7 @@
 """GPU parity of the block-scaled FP8 GEMM against the oracle's
 dequant-then-matmul (pratchya/_qualia/_qarr.py:605-608, 621-622).
 
-Tolerance: relative Frobenius error <= 1e-2 for bf16
+Tolerance (the GEMM contract): relative Frobenius error <= 1e-2 for bf16
 outputs.  f32 outputs are held to 1e-3: the FP8 MFMA's internal dot-product
 accumulation is not a sequence of IEEE f32 additions (deviations of 1e-5 to
 1e-4 relative on heavy-tailed data), while its arithmetic is exact whenever the

@@ -101,6 +101,82 @@ def cpu_baseline_config3(rows: int = 512):
                       f"(NumPy / OpenBLAS)"}
 
 
+def cpu_baseline_config4(rows: int = 256):
+    """The oracle's config-4 backward on a token sample: dY (rows tokens)
+    requantized (1,128) and contracted with W^T (dgrad), and A^T dY with both
+    operands requantized (128,1) along the sampled tokens (wgrad), f32 dots on
+    the host's BLAS threads.  Reported per token, scaled to the full 16384."""
+    from oracle import qarr_oracle as O
+    T, Cin, N = rows, 2048, 8192
+    dy = O.bf16_bits_to_f32(O.normal_input((T, N), 1e-3, seed=4))
+    a = O.bf16_bits_to_f32(O.activation_input(T, Cin, seed=2))
+    wd = O.dequantize_impl(*O.quantize_impl(O.bf16_bits_to_f32(O.normal_input((Cin, N), 0.02, seed=3)),
+                                            (128, 128)), "float32", (128, 128))
+    t0 = time.perf_counter()
+    dyd = O.dequantize_impl(*O.quantize_impl(dy, (1, 128)), "float32", (1, 128))
+    dyd @ wd.T                                                       # dgrad
+    ad = O.dequantize_impl(*O.quantize_impl(a, (1, 128)), "float32", (1, 128))
+    at = O.dequantize_impl(*O.quantize_impl(ad, (128, 1)), "float32", (128, 1))
+    gt = O.dequantize_impl(*O.quantize_impl(dy, (128, 1)), "float32", (128, 1))
+    at.T @ gt                                                        # wgrad
+    el = time.perf_counter() - t0
+    full_s = el * 16384 / rows
+    return {"value": round(2 * 549755813888 / full_s / 1e12, 4), "unit": "TFLOP/s (dgrad + wgrad)",
+            "cores": _blas_threads(), "kind": "port",
+            "sample": f"{rows} of 16384 tokens: requantizes + f32 dots of dgrad and wgrad, {el:.1f} s, "
+                      f"scaled to the full token count (NumPy / OpenBLAS)"}
+
+
+def cpu_baseline_config5(tokens: int = 256):
+    """The oracle's config-5 layer, estimated from one [4096, 4096] linear:
+    the per-token part (x quantized (1,128), the f32 forward dot, the output
+    requantized, the f32 dgrad and wgrad dots of the reference's matmul
+    backward, Q:616-640, the dgrad requantize) timed on ``tokens`` tokens, and
+    the per-step part (the weight gradient's (128,128) requantize) timed once;
+    both scale with din x dout, so the six linears cost 12x the [4096, 4096]
+    one.  Reported as tokens/s of the full 32768-token step."""
+    from oracle import qarr_oracle as O
+    rng = np.random.default_rng(5)
+    d = CFG5_D
+    x = O.bf16_round(rng.standard_normal((tokens, d)).astype(np.float32))
+    w = O.bf16_round((rng.standard_normal((d, d)) * 0.02).astype(np.float32))
+    g = O.bf16_round((rng.standard_normal((tokens, d)) * 1e-3).astype(np.float32))
+    wd = O.dequantize_impl(*O.quantize_impl(w, (128, 128)), "float32", (128, 128))
+    t0 = time.perf_counter()
+    xd = O.dequantize_impl(*O.quantize_impl(x, (1, 128)), "float32", (1, 128))
+    y = xd @ wd
+    O.dequantize_impl(*O.quantize_impl(y, (1, 128)), "bfloat16", (1, 128))
+    gx = g @ wd.T
+    O.quantize_impl(gx, (1, 128))
+    gw = xd.T @ g
+    per_token = (time.perf_counter() - t0) / tokens
+    t0 = time.perf_counter()
+    O.quantize_impl(gw, (128, 128))
+    per_step = time.perf_counter() - t0
+    scale = sum(a * b for a, b in CFG5_LINEARS) / (d * d)
+    step_s = scale * (per_token * CFG5_TOKENS + per_step)
+    return {"value": round(CFG5_TOKENS / step_s, 2), "unit": "tokens/s", "cores": _blas_threads(), "kind": "port",
+            "sample": f"one [4096,4096] linear on {tokens} tokens ({per_token * 1e3:.2f} ms/token) + its weight-"
+                      f"gradient requantize ({per_step:.2f} s), scaled x{scale:.0f} to the six linears and to "
+                      f"{CFG5_TOKENS} tokens: {step_s:.0f} s per layer step (NumPy / OpenBLAS)"}
+
+
+def cpu_baseline_optimizer():
+    """The oracle's optimizer step on one [4096, 4096] quantized leaf in f32
+    (momentum, requantize, Newton-Schulz, update), on this host."""
+    from oracle import optim_oracle as OO
+    from oracle import qarr_oracle as O
+    rng = np.random.default_rng(6)
+    n = 4096
+    t = lambda sc: O.quantize_impl((rng.standard_normal((n, n)) * sc).astype(np.float32), (128, 128))
+    m, g, p = t(1e-3), t(1e-3), t(0.02)
+    t0 = time.perf_counter()
+    OO.quantized_leaf_step("['w_r']", g, m, p, (128, 128), 0.9, 0.99, 5, 4e-3, 5e-2, 0.1, "float32")
+    el = time.perf_counter() - t0
+    return {"value": round(el * 1e3, 1), "unit": "ms per [4096,4096] leaf (f32)", "cores": _blas_threads(),
+            "kind": "port", "sample": "one 2-D quantized leaf, Muon branch (NumPy / OpenBLAS)"}
+
+
 MAX_GRAPH_STEPS = 256
 
 
@@ -583,7 +659,10 @@ def main():
         extra["config1_round_trip"]["cpu_baseline"] = cpu_baseline_config1()
         if "config3_gemm_fwd" in extra:
             extra["config3_gemm_fwd"]["cpu_baseline"] = cpu_baseline_config3()
-        _log("cpu baselines of configs 1 and 3: done")
+            extra["config4_backward"]["cpu_baseline"] = cpu_baseline_config4()
+            extra["config5_layer"]["cpu_baseline"] = cpu_baseline_config5()
+            extra["optimizer_step"]["cpu_baseline"] = cpu_baseline_optimizer()
+        _log("cpu baselines of configs 1, 3, 4, 5 and the optimizer: done")
     line = {
         "metric": METRIC,
         "value": round(gbs, 2),

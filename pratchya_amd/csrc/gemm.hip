@@ -189,6 +189,14 @@ struct DmaRows {
   uint32_t row0, e_word;
 };
 
+// Row group i (8 rows) of a stage load whose row group 0 starts at byte
+// offset soff0 of the operand (row0 * ld + kt * BK) and LDS address lds0:
+// one add per row group, so that little scalar work sits between the MFMAs.
+__device__ __forceinline__ void dma_rows_at(const DmaHalf& h, uint32_t soff0, uint8_t* lds0, int i) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(h.pay, (lds_void*)(lds0 + i * 1024), 16, h.off[i & 1],
+                                           soff0 + (uint32_t)i * (8u * h.ld), 0, 0);
+}
+
 // Row group i (8 rows) of this wave's 64 rows for K block kt into stage st.
 __device__ __forceinline__ void dma_rows(const DmaHalf& h, const DmaRows& r, uint8_t* st, int kt, int i) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(h.pay, (lds_void*)(st + h.lds_pay + i * 1024), 16, h.off[i & 1],
@@ -563,15 +571,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
         const DmaRows& dr = to_next ? nxt : cur;
         const int lkt = to_next ? 0 : dkt;            // K block inside the tile loaded
         uint8_t* dst = lds + ((dkt + par) & 1) * STAGE_BYTES;
+        const uint32_t soff0 = dr.row0 * h.ld + (uint32_t)lkt * BK;
+        uint8_t* const lds0 = dst + h.lds_pay;
         pin_frags(fa, fb);
         mfma_pinned<0, 0>(acc, fa, fb, eA, eB);
-        if (dma_now) { dma_rows(h, dr, dst, lkt, 0); dma_rows(h, dr, dst, lkt, 1); }
+        if (dma_now) { dma_rows_at(h, soff0, lds0, 0); dma_rows_at(h, soff0, lds0, 1); }
         mfma_pinned<0, 1>(acc, fa, fb, eA, eB);
-        if (dma_now) { dma_rows(h, dr, dst, lkt, 2); dma_rows(h, dr, dst, lkt, 3); }
+        if (dma_now) { dma_rows_at(h, soff0, lds0, 2); dma_rows_at(h, soff0, lds0, 3); }
         mfma_pinned<0, 2>(acc, fa, fb, eA, eB);
-        if (dma_now) { dma_rows(h, dr, dst, lkt, 4); dma_rows(h, dr, dst, lkt, 5); }
+        if (dma_now) { dma_rows_at(h, soff0, lds0, 4); dma_rows_at(h, soff0, lds0, 5); }
         mfma_pinned<0, 3>(acc, fa, fb, eA, eB);
-        if (dma_now) { dma_rows(h, dr, dst, lkt, 6); dma_rows(h, dr, dst, lkt, 7); }
+        if (dma_now) { dma_rows_at(h, soff0, lds0, 6); dma_rows_at(h, soff0, lds0, 7); }
         mfma_pinned<1, 0>(acc, fa, fb, eA, eB);
         if (dma_now) {
           dma_scales(h, dr, dst, lkt);

@@ -155,3 +155,37 @@ def test_requantize_cotangent_codes_without_gpu():
     assert f(None, 7, None, None, 1, 8, 1024, None, None, None, None) == _lib.EINVAL
     assert f(None, _lib.DT_BF16, None, None, 1, 0, 1024, None, None, None, None) == _lib.OK
     assert f(None, _lib.DT_BF16, None, None, 1, 8, 1024, None, None, None, None) == _lib.EINVAL  # null buffers
+
+
+def test_optimizer_entry_point_codes_without_gpu():
+    """pratchya_momentum / pratchya_apply_update validate layouts, dtypes and
+    buffers before any launch (empty tensors are a no-op)."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    m = lib.pratchya_momentum
+    F32, BF16, E4M3 = _lib.DT_F32, _lib.DT_BF16, _lib.DT_E4M3
+    # tgrid (96, 128) does not divide 256 x 256
+    assert m(None, None, None, None, E4M3, None, None, 1, 256, 256, 96, 128, F32, 0.9, 0.1, 0.99, 0.01,
+             None, None, None) == _lib.EINVAL
+    assert b"does not fit" in lib.pratchya_last_error()
+    # unsupported arithmetic and gradient dtypes
+    assert m(None, None, None, None, E4M3, None, None, 1, 256, 256, 128, 128, E4M3, 0.9, 0.1, 0.99, 0.01,
+             None, None, None) == _lib.EINVAL
+    assert m(None, None, None, None, 7, None, None, 1, 256, 256, 128, 128, F32, 0.9, 0.1, 0.99, 0.01,
+             None, None, None) == _lib.EINVAL
+    # empty: nothing to do; non-empty with null buffers: an error
+    assert m(None, None, None, None, BF16, None, None, 1, 0, 256, 128, 128, BF16, 0.9, 0.1, 0.99, 0.01,
+             None, None, None) == _lib.OK
+    assert m(None, None, None, None, BF16, None, None, 1, 256, 256, 128, 128, BF16, 0.9, 0.1, 0.99, 0.01,
+             None, None, None) == _lib.EINVAL
+    u = lib.pratchya_apply_update
+    # an f32 direction with bf16 arithmetic is only valid for the sign (Lion) form
+    assert u(None, F32, 0, 64.0, None, E4M3, None, None, 1, 256, 256, 128, 128, BF16, 0.05, 0.005,
+             None, BF16, None) == _lib.EINVAL
+    assert b"f32 direction" in lib.pratchya_last_error()
+    assert u(None, E4M3, 1, 0.0, None, E4M3, None, None, 1, 256, 256, 128, 128, F32, 0.05, 0.005,
+             None, F32, None) == _lib.EINVAL
+    assert u(None, F32, 1, 0.0, None, F32, None, None, 1, 0, 256, 1, 1, F32, 0.05, 0.005,
+             None, F32, None) == _lib.OK
+    assert u(None, F32, 1, 0.0, None, F32, None, None, 1, 256, 256, 1, 1, F32, 0.05, 0.005,
+             None, F32, None) == _lib.EINVAL

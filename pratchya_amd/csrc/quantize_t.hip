@@ -122,13 +122,37 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
   const int cg = lane % CGW, rs = lane / CGW;
   const int64_t c0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * (8 * CGW) + cg * 8;
   // C is a multiple of 8, so a lane owns a whole group or nothing; the xor
-  // partners of a lane (same cg) share its fate.  (fp8 inputs: C is a multiple
-  // of 128, so every lane of the grid has a group.)
-  if constexpr (IN != IN_FP8) {
+  // partners of a lane (same cg) share its fate.  (Inputs with scales: C is a
+  // multiple of 128, so a wave is wholly inside or outside; fp8 inputs: every
+  // wave of the grid is inside.  Their waves outside return after the
+  // workgroup barrier below.)
+  constexpr bool SCALED = IN == IN_FP8 || IN == IN_BF16S;
+  if constexpr (!SCALED) {
     if (c0 >= C) return;
   }
   const int64_t s = blockIdx.z, tb = blockIdx.y;
   const int64_t t0 = tb * 128 + rs * TOK;
+
+  // (1, 128) input scales of the workgroup's 128 token rows and NB channel
+  // blocks, loaded once per workgroup into LDS: block (t, c / 128) of the
+  // slice; a slice holds a whole number of groups (kg | T * C / 128), so the
+  // group of a block is its slice-global index >> kg_shift.  32-bit indices:
+  // the host checks slices * T * C / 128 < 2^32.
+  constexpr int NB = SCALED ? (4 * 8 * CGW) / 128 : 1;
+  __shared__ float sdq[NB][128];
+  if constexpr (SCALED) {
+    const uint32_t nbr = (uint32_t)(C >> 7);
+    const uint32_t cb0 = (uint32_t)blockIdx.x * NB;
+    for (int i = (int)threadIdx.x; i < NB * 128; i += 256) {
+      const uint32_t b = (uint32_t)i >> 7, row = (uint32_t)i & 127u;
+      float v = 0.0f;
+      if (cb0 + b < nbr) {
+        const uint32_t blk = (uint32_t)(s * T + tb * 128 + row) * nbr + cb0 + b;
+        v = e8m0_decode(x_sc8[blk]) * x_sc32[blk >> kg_shift];
+      }
+      sdq[b][row] = v;
+    }
+  }
 
   uint32_t w[TOK][NW];
   if constexpr (IN == IN_FP8) {
@@ -158,26 +182,24 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
       w[r][1] = v.y;
     }
   } else {
-    const uint8_t* xr = x + ((s * T + t0) * C + c0) * ESZ;
+    if (!SCALED || c0 < C) {
+      const uint8_t* xr = x + ((s * T + t0) * C + c0) * ESZ;
 #pragma unroll
-    for (int r = 0; r < TOK; ++r) load_row<IN>(xr + (int64_t)r * C * ESZ, w[r]);
+      for (int r = 0; r < TOK; ++r) load_row<IN>(xr + (int64_t)r * C * ESZ, w[r]);
+    }
+    if constexpr (SCALED) {
+      __syncthreads();                       // the staged scales are visible
+      if (c0 >= C) return;
+    }
   }
 
   float dq[TOK];
 #pragma unroll
   for (int r = 0; r < TOK; ++r) dq[r] = 1.0f;
-  if constexpr (IN == IN_FP8 || IN == IN_BF16S) {
-    // (1, 128) scales of the stored payload: block (t, c / 128) of the slice;
-    // a slice holds a whole number of groups (kg | T * C / 128), so the group
-    // of a block is its slice-global index >> kg_shift.  32-bit indices: the
-    // host checks slices * T * C / 128 < 2^32.
-    const uint32_t nbr = (uint32_t)(C >> 7);
-    const uint32_t b0 = (uint32_t)(s * T + t0) * nbr + (uint32_t)(c0 >> 7);
+  if constexpr (SCALED) {
+    const int b = (int)((c0 >> 7) - (int64_t)blockIdx.x * NB);
 #pragma unroll
-    for (int r = 0; r < TOK; ++r) {
-      const uint32_t blk = b0 + (uint32_t)r * nbr;
-      dq[r] = e8m0_decode(x_sc8[blk]) * x_sc32[blk >> kg_shift];
-    }
+    for (int r = 0; r < TOK; ++r) dq[r] = sdq[b][rs * TOK + r];
   }
   if constexpr (IN == IN_BF16S) {
     // the cotangent's dequantize_impl_bwd, in place: from here on the rows are

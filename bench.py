@@ -538,6 +538,87 @@ def bench_optimizer(steps: int):
             "steps": steps}
 
 
+# quantized triple of a config 2 tensor: payload + e8m0 per 128 + f32 group max per 1024
+CFG2_TRIPLE_BYTES = CFG2_ROWS * CFG2_COLS * (1 + 1 / 128 + 4 / 1024)
+
+
+def bench_elementwise(steps: int, warmup: int):
+    """QArrayImpl addition of two config 2 activations quantized (1, 128) (the
+    residual add of quantized streams, pratchya/_qualia/_qarr.py:121-130):
+    the fused kernel (pratchya_elementwise) against the HBM roofline, beside
+    the unfused composition it replaces (two f32 dequantizations, a torch add,
+    a quantization).  Both timed in HIP graphs over 4 input sets (> the MALL)."""
+    import ctypes
+    import torch
+    from oracle import qarr_oracle as O
+    from pratchya_amd import _kernels as K
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    g = (1, 128)
+    n_sets = 4
+    xs = []
+    for i in range(n_sets):
+        a = torch.from_numpy(O.activation_input(CFG2_ROWS, CFG2_COLS, seed=20 + i).view(np.int16)).view(
+            torch.bfloat16).cuda()
+        xs.append((K.quantize(a, g), K.quantize(a * 0.5 + 1.0, g)))
+    outs = [(torch.empty(CFG2_ROWS, CFG2_COLS, dtype=torch.uint8, device="cuda"),
+             torch.empty(CFG2_ROWS * CFG2_COLS // 1024, 8, dtype=torch.uint8, device="cuda"),
+             torch.empty(CFG2_ROWS * CFG2_COLS // 1024, 1, 1, dtype=torch.float32, device="cuda"))
+            for _ in range(n_sets)]
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+
+    def fused(i):
+        (x8, xs8, xs32), (y8, ys8, ys32) = xs[i % n_sets]
+        q, s8, s32 = outs[i % n_sets]
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        rc = lib.pratchya_elementwise(0, p(x8), p(xs8), p(xs32), 1, 128, p(y8), p(ys8), p(ys32), 1, 128, 1,
+                                      CFG2_ROWS, CFG2_COLS, 1, 128, p(q), p(s8), p(s32), None, 0, st)
+        if rc:
+            raise RuntimeError(lib.pratchya_last_error().decode())
+
+    def unfused(i):
+        x, y = xs[i % n_sets]
+        K.quantize(K.dequantize(*x, torch.float32, g) + K.dequantize(*y, torch.float32, g), g,
+                   out=outs[i % n_sets])
+
+    ms, _ = timed_graph(fused, steps, warmup)
+    ms_u, _ = timed_graph(unfused, max(8, steps // 8), 2)
+    nbytes = int(3 * CFG2_TRIPLE_BYTES)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    # parity spot check: the last output of set 0 against the oracle on 64 rows
+    fused(0)
+    torch.cuda.synchronize()
+    from oracle import elementwise_oracle as E
+    (x8, xs8, xs32), (y8, ys8, ys32) = xs[0]
+    tr = lambda v, s8, s32: (v[:64].view(torch.uint8).cpu().numpy(), s8[:128].view(torch.uint8).cpu().numpy(),
+                             s32[:128].cpu().numpy())
+    want = E.elementwise("add", tr(x8, xs8, xs32), g, tr(y8, ys8, ys32), g, g)
+    q, s8, _ = outs[0]
+    ok = bool(np.array_equal(q[:64].cpu().numpy(), want[0]) and np.array_equal(s8[:128].cpu().numpy(),
+                                                                                 want[1].reshape(128, 8)))
+    return {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes": nbytes, "shape": f"[{CFG2_ROWS},{CFG2_COLS}] + [{CFG2_ROWS},{CFG2_COLS}], tgrid (1,128)",
+            "unfused_us": round(ms_u * 1e3, 2),
+            "unfused": "dequantize x, y to f32 + torch add + quantize (27 B per element)",
+            "bit_exact_vs_oracle": ok}
+
+
+def cpu_baseline_elementwise(rows: int = 2048):
+    """The oracle's quantized add on ``rows`` rows of the config 2 shape,
+    scaled to the full tensor."""
+    from oracle import elementwise_oracle as E
+    from oracle import qarr_oracle as O
+    g = (1, 128)
+    a = O.bf16_bits_to_f32(O.activation_input(rows, CFG2_COLS, seed=20))
+    x, y = O.quantize_impl(a, g), O.quantize_impl((a * np.float32(0.5) + np.float32(1.0)).astype(np.float32), g)
+    t0 = time.perf_counter()
+    E.elementwise("add", x, g, y, g, g)
+    el = time.perf_counter() - t0
+    gbs = 3 * CFG2_TRIPLE_BYTES * (rows / CFG2_ROWS) / el / 1e9
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle elementwise add on {rows} of {CFG2_ROWS} rows, {el:.1f} s (NumPy, single thread)"}
+
+
 COPY_BYTES = 256 << 20   # bytes read (and written) by the reference copy of the counter runs
 
 
@@ -598,7 +679,7 @@ def main():
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--counter-workload", action="store_true",
                     help="only run the direct-launch workload used for rocprofv3 --pmc runs")
-    ap.add_argument("--only", choices=["cfg3", "cfg4", "cfg5", "optim"], default=None,
+    ap.add_argument("--only", choices=["cfg3", "cfg4", "cfg5", "optim", "elementwise"], default=None,
                     help="run one secondary configuration alone (for profiling) and print its result")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -622,6 +703,8 @@ def main():
             res = bench_config4(max(20, args.steps // 4), max(4, args.warmup // 4))
         elif args.only == "optim":
             res = bench_optimizer(3)
+        elif args.only == "elementwise":
+            res = bench_elementwise(max(20, args.steps // 2), max(4, args.warmup // 4))
         else:
             res = bench_config5(max(3, args.steps // 40), 2)
         print(json.dumps({args.only: res}), flush=True)
@@ -634,6 +717,9 @@ def main():
     _log("config 1 round trip: start")
     extra["config1_round_trip"] = bench_config1(max(20, args.steps // 4), max(4, args.warmup // 4))
     _log(f"config 1 round trip: {extra['config1_round_trip']['us_per_round_trip']} us")
+    _log("elementwise add: start")
+    extra["elementwise_add"] = bench_elementwise(max(20, args.steps // 2), max(4, args.warmup // 4))
+    _log(f"elementwise add: {extra['elementwise_add']['us']} us")
     if not args.no_gemm:
         _log("config 3 gemm fwd: start")
         gms, tflops = bench_gemm_fwd(max(8, args.steps // 4), max(4, args.warmup // 4))
@@ -657,12 +743,13 @@ def main():
         cpu = cpu_baseline_quantize()
         _log(f"cpu baseline: {cpu['value']} GB/s")
         extra["config1_round_trip"]["cpu_baseline"] = cpu_baseline_config1()
+        extra["elementwise_add"]["cpu_baseline"] = cpu_baseline_elementwise()
         if "config3_gemm_fwd" in extra:
             extra["config3_gemm_fwd"]["cpu_baseline"] = cpu_baseline_config3()
             extra["config4_backward"]["cpu_baseline"] = cpu_baseline_config4()
             extra["config5_layer"]["cpu_baseline"] = cpu_baseline_config5()
             extra["optimizer_step"]["cpu_baseline"] = cpu_baseline_optimizer()
-        _log("cpu baselines of configs 1, 3, 4, 5 and the optimizer: done")
+        _log("cpu baselines of configs 1, 3, 4, 5, the elementwise add and the optimizer: done")
     line = {
         "metric": METRIC,
         "value": round(gbs, 2),

@@ -130,6 +130,37 @@ int pratchya_gather_dequantize(const uint8_t* x_fp8, const uint8_t* sc_fp8, cons
                                int64_t H, int64_t W, int64_t a, int64_t b, const int64_t* idx,
                                int64_t n_idx, void* out, int out_dtype, hipStream_t stream);
 
+/* operators of pratchya_elementwise (jnp's float32 semantics) */
+#define PRATCHYA_OP_ADD 0        /* x + y                                                   */
+#define PRATCHYA_OP_SUB 1        /* x - y                                                   */
+#define PRATCHYA_OP_MUL 2        /* x * y                                                   */
+#define PRATCHYA_OP_DIV 3        /* x / y (IEEE)                                            */
+#define PRATCHYA_OP_FLOORDIV 4   /* jnp.floor_divide: round(div) of float divmod            */
+#define PRATCHYA_OP_MOD 5        /* jnp.remainder: fmod(x, y), + y where the signs differ   */
+
+/* Workspace of pratchya_elementwise for 16-byte aligned payloads (0 when the
+ * one-pass kernel applies: result tgrid (1, b), b a multiple of 16 and W of 16,
+ * groups of at most 1024 elements, operand grids with b multiples of 16);
+ * otherwise slices * n_blk * 4 bytes.  0 for an invalid shape too. */
+size_t pratchya_elementwise_workspace_bytes(int64_t slices, int64_t H, int64_t W, int64_t xa, int64_t xb,
+                                            int64_t ya, int64_t yb, int64_t a, int64_t b);
+
+/* Quantized arithmetic, one fused pass:                        replaces
+ *   QArrayImpl(op(dequantize_impl(x, f32), dequantize_impl(y, f32)), (a, b))
+ * -- QArrayImpl's binary operators (Q:121-261; make_elementwise_impl,
+ * Q:715-720, then the result's quantize_impl, Q:458-506).  x and y: e4m3fn
+ * payloads [slices, H, W] with their scales, quantized with grids (xa, xb) and
+ * (ya, yb); op: PRATCHYA_OP_*; out_fp8 / out_sc8 / out_sc32: the result
+ * quantized with tgrid (a, b), exactly the bytes quantize_impl gives for the
+ * f32 result.  `workspace`: pratchya_elementwise_workspace_bytes(...) bytes
+ * (may be NULL when that is 0; unaligned payloads need the general path's
+ * workspace, else PRATCHYA_EINVAL). */
+int pratchya_elementwise(int op, const uint8_t* x_fp8, const uint8_t* x_sc8, const float* x_sc32, int64_t xa,
+                         int64_t xb, const uint8_t* y_fp8, const uint8_t* y_sc8, const float* y_sc32, int64_t ya,
+                         int64_t yb, int64_t slices, int64_t H, int64_t W, int64_t a, int64_t b,
+                         uint8_t* out_fp8, uint8_t* out_sc8, float* out_sc32, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream);
+
 /* Momentum of the quantized Miulion optimizer step, one pass      replaces
  * pratchya/_nnx_impl/_optimizer.py:124-135 (a layer of a 3-D stacked leaf,
  * bf16 arithmetic) and :157-176 (a 2-D leaf, f32 arithmetic):

@@ -290,6 +290,51 @@ def gather_dequantize(x_fp8: torch.Tensor, sc_fp8: torch.Tensor, sc_fp32: torch.
     return out
 
 
+ELEMENTWISE_OPS = ("add", "sub", "mul", "div", "floordiv", "mod")
+
+
+def elementwise(op: str, x, grid_x, y, grid_y, tgrid, out=None):
+    """``QArrayImpl(op(dequantize_impl(x, f32), dequantize_impl(y, f32)), tgrid)``
+    in one fused pass (pratchya/_qualia/_qarr.py:121-261, 715-720): ``x`` and
+    ``y`` are quantized (payload, e8m0, f32) triples of one shape with block
+    grids ``grid_x`` / ``grid_y``; ``op`` one of ELEMENTWISE_OPS (jnp's add,
+    subtract, multiply, divide, floor_divide, remainder).  Returns the result's
+    ``(payload, sc_fp8, sc_fp32)`` as ``quantize`` lays them out; ``out`` may
+    hold preallocated buffers."""
+    if op not in ELEMENTWISE_OPS:
+        raise ValueError(f"elementwise: operator {op!r} is not one of {ELEMENTWISE_OPS}")
+    x8, xs8, xs32 = x
+    y8, ys8, ys32 = y
+    _require_gpu(x8, xs8, xs32, y8, ys8, ys32)
+    if tuple(x8.shape) != tuple(y8.shape):
+        raise ValueError(f"elementwise: operand shapes {tuple(x8.shape)} and {tuple(y8.shape)} differ")
+    a, b = int(tgrid[0]), int(tgrid[1])
+    S, H, W = slices_hw(x8.shape)
+    n_blk, K, M = group_layout(H, W, (a, b))
+    lead = tuple(x8.shape[:-2]) if x8.dim() >= 2 else ()
+    xq, yq = _u8(x8).contiguous(), _u8(y8).contiguous()
+    xs8c, ys8c = _u8(xs8).contiguous(), _u8(ys8).contiguous()
+    xs32c, ys32c = xs32.contiguous().float(), ys32.contiguous().float()
+    if out is None:
+        q = torch.empty(x8.shape, dtype=torch.uint8, device=x8.device)
+        sc8 = torch.empty(lead + (M, K), dtype=torch.uint8, device=x8.device)
+        sc32 = torch.empty(lead + (M, 1, 1), dtype=torch.float32, device=x8.device)
+    else:
+        _check_out(out, [(x8.shape, 1), (lead + (M, K), 1), (lead + (M, 1, 1), 4)], "elementwise")
+        q, sc8, sc32 = _u8(out[0]), _u8(out[1]), out[2]
+    (xa, xb), (ya, yb) = (int(v) for v in grid_x), (int(v) for v in grid_y)
+    lib = _lib.load()
+    ws_bytes = lib.pratchya_elementwise_workspace_bytes(S, H, W, xa, xb, ya, yb, a, b)
+    if ws_bytes == 0 and not (_aligned(xq, 16) and _aligned(yq, 16) and _aligned(q, 16)):
+        ws_bytes = S * n_blk * 4          # unaligned payloads take the general path
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x8.device) if ws_bytes else None
+    _lib.check(lib.pratchya_elementwise(ELEMENTWISE_OPS.index(op), _ptr(xq), _ptr(xs8c), _ptr(xs32c), xa, xb,
+                                        _ptr(yq), _ptr(ys8c), _ptr(ys32c), ya, yb, S, H, W, a, b, _ptr(q),
+                                        _ptr(sc8), _ptr(sc32), _ptr(ws) if ws is not None else None, ws_bytes,
+                                        _stream(xq)), "elementwise")
+    return q.view(E4M3), sc8.view(E8M0), sc32
+
+
 def dequantize_bwd(g: torch.Tensor, sc_fp8: torch.Tensor, sc_fp32: torch.Tensor, tgrid) -> torch.Tensor:
     """Cotangent of the payload: ``(g * (f32(e<<23) * G) / 128).astype(g.dtype)``
     (pratchya/_qualia/_qarr.py:575-601)."""

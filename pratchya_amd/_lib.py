@@ -45,6 +45,10 @@ SIGNATURES = {
                                          _c_i64, _c_p, _c_p]),
     "pratchya_quantize_t128": (_c_int, [_c_p, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64,
                                         _c_p, _c_p, _c_p, _c_p]),
+    "pratchya_elementwise_workspace_bytes": (ctypes.c_size_t, [_c_i64] * 9),
+    "pratchya_elementwise": (_c_int, [_c_int, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i64,
+                                      _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p,
+                                      ctypes.c_size_t, _c_p]),
     "pratchya_momentum": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64,
                                    _c_i64, _c_i64, _c_int, ctypes.c_float, ctypes.c_float, ctypes.c_float,
                                    ctypes.c_float, _c_p, _c_p, _c_p]),

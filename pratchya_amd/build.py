@@ -17,7 +17,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 INCLUDE = ROOT / "include"
 LIB = PKG / "libpratchya_fp8.so"
-SOURCES = ["quantize.hip", "quantize_t.hip", "gemm.hip", "optim.hip"]
+SOURCES = ["quantize.hip", "quantize_t.hip", "gemm.hip", "optim.hip", "elementwise.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

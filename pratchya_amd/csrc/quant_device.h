@@ -178,3 +178,47 @@ __device__ __forceinline__ uint32_t absmax8_bf16(const uint4& v) {
 __device__ __forceinline__ uint32_t near_mid8(float t) {
   return (((f2u(t) + 8u - 0x8000u) & 0xFFFFu) <= 16u) ? 1u : 0u;
 }
+
+// --------------------------------------------------------------------------
+// Kernels shared by the general (multi-launch) quantize paths: workspace
+// fill, and the per-group scales from the block maxima in the workspace
+// (f32 bit patterns of max |x|, one per block).  Internal linkage: each
+// translation unit that launches them has its own copy.
+// --------------------------------------------------------------------------
+static __global__ void k_fill_u32(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+// Group max and e8m0 bytes: one wave per group.
+static __global__ __launch_bounds__(256) void k_group_scales(const uint32_t* __restrict__ ws,
+                                                             uint8_t* __restrict__ sc8,
+                                                             float* __restrict__ sc32, int64_t n_groups,
+                                                             int64_t K) {
+  const int lane = threadIdx.x & 63;
+  const int64_t g = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (g >= n_groups) return;
+  const uint32_t* m = ws + g * K;
+  uint32_t G = 0;
+  for (int64_t k = lane; k < K; k += 64) G = umax(G, m[k]);
+  for (int s = 1; s < 64; s <<= 1) G = umax(G, shfl_xor_u32(G, s));
+  const float Gf = u2f(G);
+  for (int64_t k = lane; k < K; k += 64) sc8[g * K + k] = (uint8_t)e8m0_of(u2f(m[k]), Gf);
+  if (lane == 0) sc32[g] = Gf;
+}
+
+// Group max and e8m0 bytes: one thread per group (small K).
+static __global__ __launch_bounds__(256) void k_group_scales_small(const uint32_t* __restrict__ ws,
+                                                                   uint8_t* __restrict__ sc8,
+                                                                   float* __restrict__ sc32,
+                                                                   int64_t n_groups, int64_t K) {
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= n_groups) return;
+  const uint32_t* m = ws + g * K;
+  uint32_t G = 0;
+  for (int64_t k = 0; k < K; ++k) G = umax(G, m[k]);
+  const float Gf = u2f(G);
+  for (int64_t k = 0; k < K; ++k) sc8[g * K + k] = (uint8_t)e8m0_of(u2f(m[k]), Gf);
+  sc32[g] = Gf;
+}

@@ -429,12 +429,6 @@ __global__ __launch_bounds__(256) void k_quant_g8(const void* __restrict__ xv,
 // --------------------------------------------------------------------------
 // General path
 // --------------------------------------------------------------------------
-__global__ void k_fill_u32(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x)
-    p[i] = v;
-}
-
 template <bool IS_BF16>
 __device__ __forceinline__ float load_elem(const void* x, int64_t i) {
   if constexpr (IS_BF16) return u2f((uint32_t)static_cast<const uint16_t*>(x)[i] << 16);
@@ -489,38 +483,6 @@ __global__ __launch_bounds__(256) void k_blockmax(const void* __restrict__ x,
   } else if (live) {
     atomicMax(&ws[blk], m);
   }
-}
-
-// Group max and e8m0 bytes: one wave per group.
-__global__ __launch_bounds__(256) void k_group_scales(const uint32_t* __restrict__ ws,
-                                                      uint8_t* __restrict__ sc8,
-                                                      float* __restrict__ sc32, int64_t n_groups,
-                                                      int64_t K) {
-  const int lane = threadIdx.x & 63;
-  const int64_t g = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (g >= n_groups) return;
-  const uint32_t* m = ws + g * K;
-  uint32_t G = 0;
-  for (int64_t k = lane; k < K; k += 64) G = umax(G, m[k]);
-  for (int s = 1; s < 64; s <<= 1) G = umax(G, shfl_xor_u32(G, s));
-  const float Gf = u2f(G);
-  for (int64_t k = lane; k < K; k += 64) sc8[g * K + k] = (uint8_t)e8m0_of(u2f(m[k]), Gf);
-  if (lane == 0) sc32[g] = Gf;
-}
-
-// Group max and e8m0 bytes: one thread per group (small K).
-__global__ __launch_bounds__(256) void k_group_scales_small(const uint32_t* __restrict__ ws,
-                                                            uint8_t* __restrict__ sc8,
-                                                            float* __restrict__ sc32,
-                                                            int64_t n_groups, int64_t K) {
-  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (g >= n_groups) return;
-  const uint32_t* m = ws + g * K;
-  uint32_t G = 0;
-  for (int64_t k = 0; k < K; ++k) G = umax(G, m[k]);
-  const float Gf = u2f(G);
-  for (int64_t k = 0; k < K; ++k) sc8[g * K + k] = (uint8_t)e8m0_of(u2f(m[k]), Gf);
-  sc32[g] = Gf;
 }
 
 // Elementwise cast, thread per chunk of CH elements of one block row segment.

@@ -430,6 +430,25 @@ def rmatmul_mixed_impl(x_f32, y_fp8, y_sc8, y_sc32, block_grid_y: Tuple):
 # --------------------------------------------------------------------------
 # Elementwise ops on two quantized arrays (Q:715-763)
 # --------------------------------------------------------------------------
+def _floor_divide(x, y):
+    """jnp.floor_divide on float tensors: the quotient of jnp's float divmod
+    (CPython's float_divmod): mod = fmod(x, y), div = (x - mod) / y, minus one
+    where mod != 0 and sign(y) != sign(mod), rounded half away from zero
+    (lax.round).  Differs from torch.floor_divide for a zero divisor (NaN, not
+    +-inf) and in the sign of some zero quotients."""
+    if not torch.is_tensor(x):
+        x = torch.as_tensor(x, dtype=y.dtype, device=y.device)
+    if not torch.is_tensor(y):
+        y = torch.as_tensor(y, dtype=x.dtype, device=x.device)
+    mod = torch.fmod(x, y)
+    div = (x - mod) / y
+    # sign(y) != sign(mod) for a nonzero mod: a NaN mod (zero or NaN divisor), or opposite signs
+    ind = (mod != 0) & (torch.isnan(mod) | ((y < 0) != (mod < 0)))
+    div = torch.where(ind, div - 1, div)
+    t = torch.trunc(div)
+    return torch.where((div - t).abs() >= 0.5, t + torch.sign(div), t)
+
+
 class _Elementwise(torch.autograd.Function):
     @staticmethod
     def forward(ctx, src_x, src_y, x8, xs8, xs32, y8, ys8, ys32, op, tgrid):
@@ -442,7 +461,7 @@ class _Elementwise(torch.autograd.Function):
         x8, xs8, xs32, y8, ys8, ys32 = ctx.saved
         xf = _deq32(x8, xs8, xs32, ctx.tgrid)
         yf = _deq32(y8, ys8, ys32, ctx.tgrid)
-        if ctx.op is operator.floordiv:
+        if ctx.op is _floor_divide:
             gxf = gyf = None                 # piecewise constant: zero cotangents
         else:
             with torch.enable_grad():
@@ -469,14 +488,58 @@ def make_elementwise_impl(op):
     return impl
 
 
-# Python's operators on tensors are jnp's: // floors, % takes the divisor's sign.
+# Python's operators on float tensors are jnp's except floor division: % is
+# torch.remainder (fmod, plus the divisor where the signs differ), as jnp.mod.
 add_impl = make_elementwise_impl(operator.add)
 mul_impl = make_elementwise_impl(operator.mul)
 sub_impl = make_elementwise_impl(operator.sub)
 truediv_impl = make_elementwise_impl(operator.truediv)
-floordiv_impl = make_elementwise_impl(operator.floordiv)
+floordiv_impl = make_elementwise_impl(_floor_divide)
 mod_impl = make_elementwise_impl(operator.mod)
 pow_impl = make_elementwise_impl(operator.pow)
+
+
+class _ElementwiseResult(_Elementwise):
+    """Autograd node of an elementwise result computed by the fused kernel
+    (pratchya_elementwise), which never stores the f32 result op(x, y).  The
+    node's output stands in for that result as the source of the quantized
+    payload: consumers of a quantized array compute from its payload and
+    scales and use the source only to route the cotangent, so the output is a
+    zero placeholder of the result's shape.  Backward is make_elementwise_impl's
+    vjp (Q:722-750), as for _Elementwise."""
+
+    @staticmethod
+    def forward(ctx, src_x, src_y, x8, xs8, xs32, y8, ys8, ys32, op, tgrid):
+        ctx.saved = (x8, xs8, xs32, y8, ys8, ys32)
+        ctx.op, ctx.tgrid = op, tgrid
+        return torch.zeros((), dtype=torch.float32, device=x8.device).expand(x8.shape)
+
+
+# Operators the fused kernel computes (jnp.power is not among them: its f32
+# results depend on the pow implementation).
+_FUSED = {operator.add: "add", operator.sub: "sub", operator.mul: "mul", operator.truediv: "div",
+          _floor_divide: "floordiv", operator.mod: "mod"}
+
+
+def _fused_elementwise(op, x, grid_x, y, grid_y, tgrid):
+    """QArrayImpl(op(dequant(x), dequant(y)), tgrid) for quantized triples of
+    one shape, by the fused kernel, or None where it does not apply: another
+    operator, broadcast shapes, or a gradient through operands quantized with
+    different grids (that value is an f32 sum of two astype()s, Q:127-128, whose
+    vjp is dequantize_impl's rather than the elementwise one)."""
+    name = _FUSED.get(op)
+    if name is None or tuple(x[0].shape) != tuple(y[0].shape) or not x[0].is_cuda:
+        return None
+    if x[0].dtype != E4M3 or y[0].dtype != E4M3:
+        return None
+    sx, sy = _src(x[0]), _src(y[0])
+    grad = sx is not None or sy is not None
+    if grad and (tuple(grid_x) != tuple(tgrid) or tuple(grid_y) != tuple(tgrid)):
+        return None
+    out8, s8, s32 = K.elementwise(name, x, grid_x, y, grid_y, tgrid)
+    if grad:
+        setattr(out8, _SRC, _ElementwiseResult.apply(sx, sy, *x, *y, op, tuple(tgrid)))
+    return QArrayImpl._tree_unflatten((True, tuple(tgrid)), (out8, s8, s32))
 
 
 # --------------------------------------------------------------------------
@@ -601,6 +664,10 @@ class QArrayImpl:
         if isinstance(other, QArrayImpl):
             other = self._promote(other)
             a, b = (other, self) if reverse else (self, other)
+            fused = _fused_elementwise(op, (a.__value, a.__sc_fp8, a.__sc_fp32), a.__tgrid,
+                                       (b.__value, b.__sc_fp8, b.__sc_fp32), b.__tgrid, self.__tgrid)
+            if fused is not None:
+                return fused
             if self.__tgrid != other.tgrid:
                 return QArrayImpl(op(a.astype(torch.float32), b.astype(torch.float32)), self.__tgrid)
             x_out = impl(a.__value, a.__sc_fp8, a.__sc_fp32, b.__value, b.__sc_fp8, b.__sc_fp32, self.__tgrid)
@@ -634,10 +701,10 @@ class QArrayImpl:
         return self._binary(other, truediv_impl, operator.truediv, reverse=True)
 
     def __floordiv__(self, other):
-        return self._binary(other, floordiv_impl, operator.floordiv)
+        return self._binary(other, floordiv_impl, _floor_divide)
 
     def __rfloordiv__(self, other):
-        return self._binary(other, floordiv_impl, operator.floordiv, reverse=True)
+        return self._binary(other, floordiv_impl, _floor_divide, reverse=True)
 
     def __mod__(self, other):
         return self._binary(other, mod_impl, operator.mod)

@@ -30,6 +30,7 @@
 
 #include "fp8_math.h"
 #include "pratchya_fp8.h"
+#include "quant_device.h"
 
 int pratchya_set_error(int code, const char* fmt, ...);
 
@@ -44,6 +45,26 @@ template <bool BF16>
 __device__ __forceinline__ float rnd(float x) {
   if constexpr (BF16) return u2f(f32_to_bf16_rne(x) << 16);
   return x;
+}
+
+// Round element pairs of v to the arithmetic dtype: bf16 with
+// v_cvt_pk_bf16_f32 (RNE, two values per instruction; checked against the
+// software rounding on ties and every subnormal pattern by the test suite).
+template <bool BF16, int CH>
+__device__ __forceinline__ void rnd_all(float (&v)[CH]) {
+  if constexpr (BF16) {
+    if constexpr (CH % 2 == 0) {
+#pragma unroll
+      for (int k = 0; k < CH; k += 2) {
+        const uint32_t w = pack_bf16x2(v[k], v[k + 1]);
+        v[k] = u2f(w << 16);
+        v[k + 1] = u2f(w & 0xFFFF0000u);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < CH; ++k) v[k] = rnd<true>(v[k]);
+    }
+  }
 }
 
 // Block index of element `off` of a [rows, W] array with tgrid (a, b)
@@ -77,8 +98,21 @@ template <int MODE, bool BF16, int CH>
 __device__ __forceinline__ void load_operand(const void* __restrict__ x, float sc, int64_t off, float (&out)[CH]) {
   if constexpr (MODE == 0) {
     const Vec<uint8_t, CH> w = *reinterpret_cast<const Vec<uint8_t, CH>*>(static_cast<const uint8_t*>(x) + off);
+    if constexpr (CH % 4 == 0) {
+      // four bytes per word through v_cvt_scalef32_pk_f32_fp8 (exact)
 #pragma unroll
-    for (int k = 0; k < CH; ++k) out[k] = rnd<BF16>((e4m3fn_to_f32(w.v[k]) * sc) * 0.0078125f);
+      for (int j = 0; j < CH / 4; ++j) {
+        const uint32_t word = (uint32_t)w.v[4 * j] | ((uint32_t)w.v[4 * j + 1] << 8) |
+                              ((uint32_t)w.v[4 * j + 2] << 16) | ((uint32_t)w.v[4 * j + 3] << 24);
+        fp8_word(word, out[4 * j], out[4 * j + 1], out[4 * j + 2], out[4 * j + 3]);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < CH; ++k) out[k] = e4m3fn_to_f32(w.v[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < CH; ++k) out[k] = (out[k] * sc) * 0.0078125f;
+    rnd_all<BF16, CH>(out);
   } else if constexpr (MODE == 1) {
     const Vec<uint16_t, CH> w = *reinterpret_cast<const Vec<uint16_t, CH>*>(static_cast<const uint16_t*>(x) + off);
 #pragma unroll
@@ -86,13 +120,22 @@ __device__ __forceinline__ void load_operand(const void* __restrict__ x, float s
   } else {
     const Vec<float, CH> w = *reinterpret_cast<const Vec<float, CH>*>(static_cast<const float*>(x) + off);
 #pragma unroll
-    for (int k = 0; k < CH; ++k) out[k] = rnd<BF16>(w.v[k]);
+    for (int k = 0; k < CH; ++k) out[k] = w.v[k];
+    rnd_all<BF16, CH>(out);
   }
 }
 
-template <bool BF16, int CH>
+// HW: round pairs with v_cvt_pk_bf16_f32 (k_update keeps the integer
+// rounding: the compiler's selection of the packed conversion fails on its
+// negated sums with packed f32 operations disabled).
+template <bool BF16, int CH, bool HW = false>
 __device__ __forceinline__ void store_chunk(void* out, int64_t off, const float (&v)[CH]) {
-  if constexpr (BF16) {
+  if constexpr (BF16 && HW && CH % 2 == 0) {
+    Vec<uint32_t, CH / 2> w;
+#pragma unroll
+    for (int k = 0; k < CH; k += 2) w.v[k / 2] = pack_bf16x2(v[k], v[k + 1]);
+    *reinterpret_cast<Vec<uint32_t, CH / 2>*>(static_cast<uint16_t*>(out) + off) = w;
+  } else if constexpr (BF16) {
     Vec<uint16_t, CH> w;
 #pragma unroll
     for (int k = 0; k < CH; ++k) w.v[k] = (uint16_t)f32_to_bf16_rne(v[k]);
@@ -121,16 +164,28 @@ __global__ __launch_bounds__(256) void k_momentum(const uint8_t* __restrict__ m8
   const int64_t blk = block_of(base, W, a, b, n_chunks * CH <= 0x7FFFFFFF);
   const float msc = block_scale(m_sc8, m_sc32, blk, K);
   const float gsc = G_MODE == 0 ? block_scale(g_sc8, g_sc32, blk, K) : 0.0f;
-  float mv[CH], gv[CH], c[CH], nm[CH];
+  float mv[CH], gv[CH], c[CH], nm[CH], t1[CH], t2[CH], t3[CH], t4[CH];
   load_operand<0, BF16, CH>(m8, msc, base, mv);
   load_operand<G_MODE, BF16, CH>(g, gsc, base, gv);
 #pragma unroll
   for (int k = 0; k < CH; ++k) {
-    c[k] = rnd<BF16>(rnd<BF16>(b1 * mv[k]) + rnd<BF16>(b1c * gv[k]));
-    nm[k] = rnd<BF16>(rnd<BF16>(b2 * mv[k]) + rnd<BF16>(b2c * gv[k]));
+    t1[k] = b1 * mv[k];
+    t2[k] = b1c * gv[k];
+    t3[k] = b2 * mv[k];
+    t4[k] = b2c * gv[k];
   }
-  store_chunk<BF16, CH>(c_out, base, c);
-  store_chunk<BF16, CH>(m_new, base, nm);
+  rnd_all<BF16, CH>(t1);
+  rnd_all<BF16, CH>(t2);
+  rnd_all<BF16, CH>(t3);
+  rnd_all<BF16, CH>(t4);
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    c[k] = t1[k] + t2[k];
+    nm[k] = t3[k] + t4[k];
+  }
+  // the sums are rounded once more by the bf16 store (RNE), as rnd() would
+  store_chunk<BF16, CH, true>(c_out, base, c);
+  store_chunk<BF16, CH, true>(m_new, base, nm);
 }
 
 // jnp.sign: +-1 for nonzero, the argument itself for +-0 and NaN.
@@ -149,14 +204,14 @@ __global__ __launch_bounds__(256) void k_update(const void* __restrict__ u, cons
   const int64_t base = t * CH;
   const float psc = P_MODE == 0 ? block_scale(p_sc8, p_sc32, block_of(base, W, a, b, n_chunks * CH <= 0x7FFFFFFF), K)
                                 : 0.0f;
-  float uv[CH], pv[CH], v[CH];
+  float uv[CH], pv[CH], ut[CH], v[CH];
   load_operand<U_MODE, BF16, CH>(u, 0.0f, base, uv);
   load_operand<P_MODE, BF16, CH>(p, psc, base, pv);
 #pragma unroll
-  for (int k = 0; k < CH; ++k) {
-    const float ut = SIGN ? sign_of(uv[k]) : rnd<BF16>(uv[k] * scale);
-    v[k] = -((lr * ut) + (lr_wd * pv[k]));
-  }
+  for (int k = 0; k < CH; ++k) ut[k] = SIGN ? sign_of(uv[k]) : uv[k] * scale;
+  if constexpr (!SIGN) rnd_all<BF16, CH>(ut);
+#pragma unroll
+  for (int k = 0; k < CH; ++k) v[k] = -((lr * ut[k]) + (lr_wd * pv[k]));
   store_chunk<OUT_BF16, CH>(out, base, v);
 }
 
@@ -173,10 +228,11 @@ struct Grid {
   int64_t n, W, a, b, K;
 };
 
-// Elements per thread: 16 or 4 when they divide b (a chunk then lies in one
-// block) and every pointer is aligned for the vector accesses, else 1.
-int chunk_of(int64_t b, std::initializer_list<std::pair<const void*, int>> ptrs) {
-  for (int ch : {16, 4}) {
+// Elements per thread: the first of `sizes` that divides b (a chunk then lies
+// in one block) with every pointer aligned for the vector accesses, else 1.
+int chunk_of(int64_t b, std::initializer_list<std::pair<const void*, int>> ptrs,
+             std::initializer_list<int> sizes = {16, 4}) {
+  for (int ch : sizes) {
     if (b % ch) continue;
     bool ok = true;
     for (auto [p, esz] : ptrs) {
@@ -228,8 +284,10 @@ extern "C" int pratchya_momentum(const uint8_t* m_fp8, const uint8_t* m_sc8, con
   if (L.n == 0) return PRATCHYA_OK;
   if (!m_fp8 || !m_sc8 || !m_sc32 || !g || !c_out || !m_new || (g_dtype == PRATCHYA_DT_E4M3 && (!g_sc8 || !g_sc32)))
     return pratchya_set_error(PRATCHYA_EINVAL, "momentum: null buffer");
+  // chunks of 16 output bytes: one full-width store per lane and output,
+  // contiguous across the wave
   const int ch = chunk_of(L.b, {{m_fp8, 1}, {g, dtype_size(g_dtype)}, {c_out, dtype_size(arith_dtype)},
-                                {m_new, dtype_size(arith_dtype)}});
+                                {m_new, dtype_size(arith_dtype)}}, {16 / dtype_size(arith_dtype), 4});
   const int64_t chunks = L.n / ch;
   if (chunks / 256 + 1 > 0x7FFFFFFF) return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "momentum: too many elements");
   const dim3 grid((unsigned)((chunks + 255) / 256));
@@ -241,8 +299,8 @@ extern "C" int pratchya_momentum(const uint8_t* m_fp8, const uint8_t* m_sc8, con
   else if (g_dtype == PRATCHYA_DT_BF16) PRATCHYA_MOM(1, BF, C); \
   else PRATCHYA_MOM(2, BF, C);
   const bool bf = arith_dtype == PRATCHYA_DT_BF16;
-  if (ch == 16) {
-    if (bf) { PRATCHYA_MOM_G(true, 16) } else { PRATCHYA_MOM_G(false, 16) }
+  if (ch == 8) {
+    PRATCHYA_MOM_G(true, 8)
   } else if (ch == 4) {
     if (bf) { PRATCHYA_MOM_G(true, 4) } else { PRATCHYA_MOM_G(false, 4) }
   } else {
@@ -269,7 +327,10 @@ extern "C" int pratchya_apply_update(const void* u, int u_dtype, int use_sign, f
   if (L.n == 0) return PRATCHYA_OK;
   if (!u || !p || !out || (p_dtype == PRATCHYA_DT_E4M3 && (!p_sc8 || !p_sc32)))
     return pratchya_set_error(PRATCHYA_EINVAL, "apply_update: null buffer");
-  const int ch = chunk_of(L.b, {{u, dtype_size(u_dtype)}, {p, dtype_size(p_dtype)}, {out, dtype_size(out_dtype)}});
+  // chunks of 16 bytes of the widest stream (u or out)
+  const int wide = dtype_size(u_dtype) > dtype_size(out_dtype) ? dtype_size(u_dtype) : dtype_size(out_dtype);
+  const int ch = chunk_of(L.b, {{u, dtype_size(u_dtype)}, {p, dtype_size(p_dtype)}, {out, dtype_size(out_dtype)}},
+                          {16 / wide, 4});
   const int64_t chunks = L.n / ch;
   if (chunks / 256 + 1 > 0x7FFFFFFF) return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "apply_update: too many elements");
   const dim3 grid((unsigned)((chunks + 255) / 256));
@@ -280,8 +341,8 @@ extern "C" int pratchya_apply_update(const void* u, int u_dtype, int use_sign, f
   // one instantiation per (sign, u, p, arithmetic, output) combination in use
 #define PRATCHYA_UPD(SG, UM, PM, BF, OB)                                                                     \
   if (use_sign == SG && um == UM && pm == PM && bf == BF && ob == OB) {                                       \
-    if (ch == 16)                                                                                             \
-      hipLaunchKernelGGL((k_update<SG, UM, PM, BF, OB, 16>), grid, dim3(256), 0, stream, u, p, p_sc8, p_sc32,  \
+    if (ch == 8)                                                                                              \
+      hipLaunchKernelGGL((k_update<SG, UM, PM, BF, OB, 8>), grid, dim3(256), 0, stream, u, p, p_sc8, p_sc32,   \
                          chunks, L.W, L.a, L.b, L.K, scale, lr, lr_wd, out);                                   \
     else if (ch == 4)                                                                                         \
       hipLaunchKernelGGL((k_update<SG, UM, PM, BF, OB, 4>), grid, dim3(256), 0, stream, u, p, p_sc8, p_sc32,   \

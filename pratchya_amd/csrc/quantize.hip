@@ -559,54 +559,89 @@ __global__ __launch_bounds__(256) void k_cast_general(const void* __restrict__ x
 // --------------------------------------------------------------------------
 // Dequantize (and dequantize_bwd): thread per chunk of CH elements.
 //   IN: 0 = e4m3fn bytes, 1 = bf16, 2 = f32;  OUT_BF16: output dtype.
+//   VEC: input and output pointers aligned for one access of the chunk each
+//   (CH is 16 output bytes: 8 for a bf16 output, 4 for f32, so every lane
+//   stores 16 contiguous bytes and a wave's stores are contiguous).
+//   I: index type (32-bit when the tensor has fewer than 2^31 elements);
+//   FLAT: a == 1 and b, K powers of two (block and group by shifts lb, lk).
 // --------------------------------------------------------------------------
-template <int IN, bool OUT_BF16, int CH>
+template <int IN, int CH, bool VEC>
+__device__ __forceinline__ void dq_load(const void* __restrict__ x, int64_t off, float (&v)[CH]) {
+  if constexpr (IN == 0) {
+    const uint8_t* p = static_cast<const uint8_t*>(x) + off;
+    if constexpr (VEC && CH % 4 == 0) {
+#pragma unroll
+      for (int j = 0; j < CH / 4; ++j)
+        fp8_word(reinterpret_cast<const uint32_t*>(p)[j], v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < CH; ++k) v[k] = e4m3fn_to_f32(p[k]);
+    }
+  } else if constexpr (VEC && CH * (IN == 1 ? 2 : 4) % 16 == 0) {
+    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + off * (IN == 1 ? 2 : 4));
+#pragma unroll
+    for (int j = 0; j < CH * (IN == 1 ? 2 : 4) / 16; ++j) {
+      const uint4 w = p[j];
+      constexpr int E = IN == 1 ? 8 : 4;
+#pragma unroll
+      for (int k = 0; k < E; ++k) v[j * E + k] = elem_f32<IN == 1>(w, k);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < CH; ++k) v[k] = load_elem<IN == 1>(x, off + k);
+  }
+}
+
+template <int IN, bool OUT_BF16, int CH, bool VEC, typename I = int64_t, bool FLAT = false>
 __global__ __launch_bounds__(256) void k_dequant(const void* __restrict__ x,
                                                  const uint8_t* __restrict__ sc8,
                                                  const float* __restrict__ sc32,
                                                  void* __restrict__ out, int64_t n_chunks,
-                                                 int64_t W, int64_t a, int64_t b, int64_t K) {
+                                                 int64_t W, int64_t a, int64_t b, int64_t K, int lb, int lk) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n_chunks) return;
   const int64_t off = t * CH;
-  const int64_t i = off / W, c = off - i * W;
-  const int64_t blk = (i / a) * (W / b) + c / b;
-  const float sc = e8m0_decode(sc8[blk]) * sc32[blk / K];
-  float vals[CH];
-  if constexpr (IN == 0) {
-    if constexpr (CH == 8) {
-      const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(x) + off);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) vals[k] = e4m3fn_to_f32((w.x >> (8 * k)) & 0xFFu);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) vals[4 + k] = e4m3fn_to_f32((w.y >> (8 * k)) & 0xFFu);
-    } else {
-#pragma unroll
-      for (int k = 0; k < CH; ++k) vals[k] = e4m3fn_to_f32(static_cast<const uint8_t*>(x)[off + k]);
-    }
+  I blk, grp;
+  if constexpr (FLAT) {
+    blk = (I)off >> lb;
+    grp = blk >> lk;
   } else {
-#pragma unroll
-    for (int k = 0; k < CH; ++k) vals[k] = load_elem<IN == 1>(x, off + k);
+    const I i = (I)off / (I)W, c = (I)off - i * (I)W;
+    blk = (i / (I)a) * ((I)W / (I)b) + c / (I)b;
+    grp = blk / (I)K;
   }
+  const float sc = e8m0_decode(sc8[blk]) * sc32[grp];
+  float vals[CH];
+  dq_load<IN, CH, VEC>(x, off, vals);
 #pragma unroll
   for (int k = 0; k < CH; ++k) vals[k] = (vals[k] * sc) * 0.0078125f;
   if constexpr (OUT_BF16) {
     uint16_t* o = static_cast<uint16_t*>(out) + off;
-    if constexpr (CH == 8) {
-      uint4 w;
-      w.x = f32_to_bf16_rne(vals[0]) | (f32_to_bf16_rne(vals[1]) << 16);
-      w.y = f32_to_bf16_rne(vals[2]) | (f32_to_bf16_rne(vals[3]) << 16);
-      w.z = f32_to_bf16_rne(vals[4]) | (f32_to_bf16_rne(vals[5]) << 16);
-      w.w = f32_to_bf16_rne(vals[6]) | (f32_to_bf16_rne(vals[7]) << 16);
-      *reinterpret_cast<uint4*>(o) = w;
+    if constexpr (VEC && CH % 8 == 0) {
+#pragma unroll
+      for (int j = 0; j < CH / 8; ++j) {
+        uint4 w;
+        w.x = f32_to_bf16_rne(vals[8 * j + 0]) | (f32_to_bf16_rne(vals[8 * j + 1]) << 16);
+        w.y = f32_to_bf16_rne(vals[8 * j + 2]) | (f32_to_bf16_rne(vals[8 * j + 3]) << 16);
+        w.z = f32_to_bf16_rne(vals[8 * j + 4]) | (f32_to_bf16_rne(vals[8 * j + 5]) << 16);
+        w.w = f32_to_bf16_rne(vals[8 * j + 6]) | (f32_to_bf16_rne(vals[8 * j + 7]) << 16);
+        reinterpret_cast<uint4*>(o)[j] = w;
+      }
     } else {
 #pragma unroll
       for (int k = 0; k < CH; ++k) o[k] = (uint16_t)f32_to_bf16_rne(vals[k]);
     }
   } else {
     float* o = static_cast<float*>(out) + off;
+    if constexpr (VEC && CH % 4 == 0) {
 #pragma unroll
-    for (int k = 0; k < CH; ++k) o[k] = vals[k];
+      for (int j = 0; j < CH / 4; ++j)
+        reinterpret_cast<uint4*>(o)[j] =
+            make_uint4(f2u(vals[4 * j]), f2u(vals[4 * j + 1]), f2u(vals[4 * j + 2]), f2u(vals[4 * j + 3]));
+    } else {
+#pragma unroll
+      for (int k = 0; k < CH; ++k) o[k] = vals[k];
+    }
   }
 }
 
@@ -1027,24 +1062,32 @@ namespace {
 template <int IN, bool OUT_BF16>
 int launch_dequant(const void* x, const uint8_t* sc8, const float* sc32, void* out,
                    const Layout& L, hipStream_t st) {
-  const int ch = chunk_elems(L.b, true);
+  // 16 output bytes per thread when b allows it and the buffers are aligned
+  const int want = OUT_BF16 ? 8 : 4;
+  int ch = 1;
+  while (ch < want && L.b % (ch * 2) == 0) ch *= 2;
+  const int in_esz = IN == 0 ? 1 : (IN == 1 ? 2 : 4);
+  const bool vec = ch == want && aligned(x, (size_t)(ch * in_esz < 16 ? ch * in_esz : 16)) && aligned(out, 16);
   const int64_t n_chunks = L.n() / ch;
   const unsigned gr = grid_for(n_chunks, 256);
-  // the 8-wide path loads 8 payload bytes at once and stores 8 bf16 at once
-  const bool vec_ok = ch == 8 && (IN != 0 || aligned(x, 8)) && (!OUT_BF16 || aligned(out, 16));
-#define PRATCHYA_DQ(C)                                                                    \
-  hipLaunchKernelGGL((k_dequant<IN, OUT_BF16, C>), dim3(gr), dim3(256), 0, st, x, sc8, sc32, \
-                     out, n_chunks, L.W, L.a, L.b, L.K)
-  if (ch == 8 && !vec_ok) {
-    const int64_t n4 = L.n() / 4;
-    hipLaunchKernelGGL((k_dequant<IN, OUT_BF16, 4>), dim3(grid_for(n4, 256)), dim3(256), 0, st, x,
-                       sc8, sc32, out, n4, L.W, L.a, L.b, L.K);
+  const bool narrow = L.n() <= 0x7FFFFFFF;
+  const bool flat = L.a == 1 && is_pow2(L.b) && is_pow2(L.K);
+  const int lb = flat ? ilog2(L.b) : 0, lk = flat ? ilog2(L.K) : 0;
+#define PRATCHYA_DQ(C, V, ...)                                                                              \
+  hipLaunchKernelGGL((k_dequant<IN, OUT_BF16, C, V, ##__VA_ARGS__>), dim3(gr), dim3(256), 0, st, x, sc8, sc32, \
+                     out, n_chunks, L.W, L.a, L.b, L.K, lb, lk)
+  if (vec && narrow && flat) {
+    PRATCHYA_DQ((OUT_BF16 ? 8 : 4), true, uint32_t, true);
+  } else if (vec && narrow) {
+    PRATCHYA_DQ((OUT_BF16 ? 8 : 4), true, uint32_t, false);
+  } else if (vec) {
+    PRATCHYA_DQ((OUT_BF16 ? 8 : 4), true);
   } else {
     switch (ch) {
-      case 1: PRATCHYA_DQ(1); break;
-      case 2: PRATCHYA_DQ(2); break;
-      case 4: PRATCHYA_DQ(4); break;
-      default: PRATCHYA_DQ(8); break;
+      case 1: PRATCHYA_DQ(1, false); break;
+      case 2: PRATCHYA_DQ(2, false); break;
+      case 4: PRATCHYA_DQ(4, false); break;
+      default: PRATCHYA_DQ(8, false); break;
     }
   }
 #undef PRATCHYA_DQ

@@ -178,6 +178,14 @@ int pratchya_momentum(const uint8_t* m_fp8, const uint8_t* m_sc8, const float* m
                       int64_t W, int64_t a, int64_t b, int arith_dtype, float beta1, float beta1c,
                       float beta2, float beta2c, void* c_out, void* m_new, hipStream_t stream);
 
+/* One Newton-Schulz combination                                 replaces
+ * pratchya/_nnx_impl/_optimizer.py:26-27 (X = 1.5 * X - 0.5 * B, B = (X X^T) X):
+ *   out = rnd(rnd(1.5 * x) - rnd(0.5 * b))
+ * elementwise over n elements of `dtype` (PRATCHYA_DT_BF16 or PRATCHYA_DT_F32),
+ * every operation rounded to dtype as the reference's jnp arithmetic does.
+ * out may be x. */
+int pratchya_ns_combine(const void* x, const void* b, void* out, int64_t n, int dtype, hipStream_t stream);
+
 /* Update of the Miulion step                                  replaces
  * pratchya/_nnx_impl/_optimizer.py:147-153 and :189-197:
  *   out = -(lr * u' + lr_wd * p),  u' = sign(u) (use_sign, Lion) or u * scale (Muon:

@@ -82,14 +82,20 @@ def newton_schulz(G: np.ndarray, steps: int = 5, dtype: str = "float32") -> np.n
     norm = _rnd(np.array([np.sqrt(np.float64(total))]), dtype)[0]
     den = _rnd(np.array([norm + const(1e-7, dtype)]), dtype)[0]
     X = _rnd(G / den, dtype)
-    c15, c05 = const(1.5, dtype), const(0.5, dtype)
     for _ in range(steps):
         A = _rnd(X.astype(np.float64) @ X.T.astype(np.float64), dtype)
         B = _rnd(A.astype(np.float64) @ X.astype(np.float64), dtype)
-        X = _rnd(_rnd(c15 * X, dtype) - _rnd(c05 * B, dtype), dtype)
+        X = ns_combine(X, B, dtype)
     if transpose:
         X = X.T
     return np.ascontiguousarray(X)
+
+
+def ns_combine(X: np.ndarray, B: np.ndarray, dtype: str) -> np.ndarray:
+    """O:26-27's ``1.5 * X - 0.5 * B`` with every operation rounded to ``dtype``."""
+    c15, c05 = const(1.5, dtype), const(0.5, dtype)
+    with np.errstate(all="ignore"):
+        return _rnd(_rnd(c15 * np.asarray(X, F32), dtype) - _rnd(c05 * np.asarray(B, F32), dtype), dtype)
 
 
 def momentum(m: np.ndarray, g: np.ndarray, beta1: float, beta2: float, dtype: str):

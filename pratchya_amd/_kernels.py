@@ -504,6 +504,24 @@ def momentum(m, g, tgrid, arith: torch.dtype, beta1: float, beta1c: float, beta2
     return c, nm
 
 
+def ns_combine(x: torch.Tensor, b: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
+    """``1.5 * x - 0.5 * b`` with each operation rounded to ``x.dtype`` (bf16 or
+    f32), one Newton-Schulz step's combination (pratchya/_nnx_impl/_optimizer.py:
+    26-27), in one pass.  ``out`` may be ``x``."""
+    _require_gpu(x, b)
+    if x.dtype != b.dtype or tuple(x.shape) != tuple(b.shape):
+        raise ValueError("ns_combine: x and b must share dtype and shape")
+    xx, bb = x.contiguous(), b.contiguous()
+    if out is None:
+        out = torch.empty_like(xx)
+    elif not out.is_contiguous() or tuple(out.shape) != tuple(xx.shape) or out.dtype != xx.dtype:
+        raise ValueError("ns_combine: out must be a contiguous tensor like x")
+    lib = _lib.load()
+    _lib.check(lib.pratchya_ns_combine(_ptr(xx), _ptr(bb), _ptr(out), xx.numel(), _dtype_code(xx.dtype),
+                                       _stream(xx)), "ns_combine")
+    return out
+
+
 def apply_update(u: torch.Tensor, use_sign: bool, scale: float, p, tgrid, arith: torch.dtype,
                  lr: float, lr_wd: float, out_dtype: torch.dtype) -> torch.Tensor:
     """``-(lr * u' + lr_wd * p)`` with ``u' = sign(u)`` (Lion) or ``u * scale``

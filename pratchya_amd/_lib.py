@@ -52,6 +52,7 @@ SIGNATURES = {
     "pratchya_momentum": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64,
                                    _c_i64, _c_i64, _c_int, ctypes.c_float, ctypes.c_float, ctypes.c_float,
                                    ctypes.c_float, _c_p, _c_p, _c_p]),
+    "pratchya_ns_combine": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_int, _c_p]),
     "pratchya_apply_update": (_c_int, [_c_p, _c_int, _c_int, ctypes.c_float, _c_p, _c_int, _c_p, _c_p,
                                        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, ctypes.c_float,
                                        ctypes.c_float, _c_p, _c_int, _c_p]),

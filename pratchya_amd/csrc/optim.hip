@@ -188,6 +188,33 @@ __global__ __launch_bounds__(256) void k_momentum(const uint8_t* __restrict__ m8
   store_chunk<BF16, CH, true>(m_new, base, nm);
 }
 
+// One Newton-Schulz combination X <- 1.5 X - 0.5 B (_optimizer.py:26-27,
+// B = (X X^T) X from the library GEMMs) in the dtype of X: both products and
+// the difference rounded separately (1.5 and 0.5 are exact in bf16).  CH
+// elements per thread (16 bytes of X; CH = 1 for any size and alignment).
+// `out` may be `x` (no restrict on them).
+template <bool BF16, int CH>
+__global__ __launch_bounds__(256) void k_ns_combine(const void* x, const void* __restrict__ bm, void* out,
+                                                    int64_t n_chunks) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_chunks) return;
+  const int64_t base = t * CH;
+  constexpr int MODE = BF16 ? 1 : 2;
+  float xv[CH], bv[CH], v[CH];
+  load_operand<MODE, BF16, CH>(x, 0.0f, base, xv);
+  load_operand<MODE, BF16, CH>(bm, 0.0f, base, bv);
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    xv[k] = 1.5f * xv[k];
+    bv[k] = 0.5f * bv[k];
+  }
+  rnd_all<BF16, CH>(xv);
+  rnd_all<BF16, CH>(bv);
+#pragma unroll
+  for (int k = 0; k < CH; ++k) v[k] = xv[k] - bv[k];
+  store_chunk<BF16, CH, true>(out, base, v);        // the difference's rounding (RNE)
+}
+
 // jnp.sign: +-1 for nonzero, the argument itself for +-0 and NaN.
 __device__ __forceinline__ float sign_of(float x) { return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : x); }
 
@@ -309,6 +336,29 @@ extern "C" int pratchya_momentum(const uint8_t* m_fp8, const uint8_t* m_sc8, con
 #undef PRATCHYA_MOM_G
 #undef PRATCHYA_MOM
   return check_launch("momentum");
+}
+
+extern "C" int pratchya_ns_combine(const void* x, const void* b, void* out, int64_t n, int dtype,
+                                   hipStream_t stream) {
+  if (!is_float_dtype(dtype))
+    return pratchya_set_error(PRATCHYA_EINVAL, "ns_combine: dtype must be f32 or bf16 (got %d)", dtype);
+  if (n < 0) return pratchya_set_error(PRATCHYA_EINVAL, "ns_combine: negative size");
+  if (n == 0) return PRATCHYA_OK;
+  if (!x || !b || !out) return pratchya_set_error(PRATCHYA_EINVAL, "ns_combine: null buffer");
+  const int esz = dtype_size(dtype), ch = 16 / esz;
+  const bool vec = n % ch == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(b) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0;
+  const int64_t chunks = vec ? n / ch : n;
+  if (chunks / 256 + 1 > 0x7FFFFFFF) return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "ns_combine: too many elements");
+  const dim3 grid((unsigned)((chunks + 255) / 256));
+  if (dtype == PRATCHYA_DT_BF16) {
+    if (vec) hipLaunchKernelGGL((k_ns_combine<true, 8>), grid, dim3(256), 0, stream, x, b, out, chunks);
+    else hipLaunchKernelGGL((k_ns_combine<true, 1>), grid, dim3(256), 0, stream, x, b, out, chunks);
+  } else {
+    if (vec) hipLaunchKernelGGL((k_ns_combine<false, 4>), grid, dim3(256), 0, stream, x, b, out, chunks);
+    else hipLaunchKernelGGL((k_ns_combine<false, 1>), grid, dim3(256), 0, stream, x, b, out, chunks);
+  }
+  return check_launch("ns_combine");
 }
 
 extern "C" int pratchya_apply_update(const void* u, int u_dtype, int use_sign, float scale, const void* p,

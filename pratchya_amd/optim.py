@@ -54,13 +54,14 @@ def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
     dtype.  The products run on the BLAS library (f32 accumulation)."""
     m, n = G.shape
     transpose = m > n
-    if transpose:
-        G = G.T
+    # X row-major throughout: elementwise ops on a transposed view would keep
+    # its column-major strides and run torch's strided kernels
+    G = G.T.contiguous() if transpose else G.contiguous()
     X = G / (torch.sqrt(torch.sum(G * G)) + 1e-7)
     for _ in range(steps):
-        A = X @ X.T.contiguous()
+        A = X @ X.T                      # a 2-D NT GEMM: the library reads X.T in place
         B = A @ X
-        X = 1.5 * X - 0.5 * B
+        X = K.ns_combine(X, B, out=X) if X.dtype in (torch.bfloat16, torch.float32) else 1.5 * X - 0.5 * B
     if transpose:
         X = X.T
     return X.contiguous()

@@ -120,6 +120,27 @@ def test_apply_update_kernel(dtype, use_sign, pmode):
     assert_f32_bits_equal(_host(got), want, f"update {dtype} sign={use_sign} p={pmode}")
 
 
+@pytest.mark.parametrize("n", [64 * 1024, 1001])        # vector and scalar paths
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_ns_combine_kernel(n, dtype):
+    """1.5 X - 0.5 B of a Newton-Schulz step, each operation rounded to the
+    dtype, bit for bit; in place as newton_schulz calls it."""
+    K = _K()
+    rng = np.random.default_rng(31)
+    X = (rng.standard_normal(n) * np.exp2(rng.integers(-30, 30, n))).astype(np.float32)
+    B = (rng.standard_normal(n) * np.exp2(rng.integers(-30, 30, n))).astype(np.float32)
+    X[:6] = [0.0, -0.0, 3e38, 1e-40, np.inf, 1.0]
+    B[:6] = [-0.0, 0.0, -3e38, 1e-40, 1.0, 2.0]
+    if dtype == "bfloat16":
+        X, B = O.bf16_round(X), O.bf16_round(B)
+    xd = torch.from_numpy(X).cuda().to(TDT[dtype])
+    bd = torch.from_numpy(B).cuda().to(TDT[dtype])
+    got = K.ns_combine(xd, bd, out=xd)
+    torch.cuda.synchronize()
+    assert got.data_ptr() == xd.data_ptr()
+    assert_f32_bits_equal(_host(got), OO.ns_combine(X, B, dtype), f"ns_combine {dtype} n={n}")
+
+
 @pytest.mark.parametrize("shape", [(256, 384), (384, 256)])
 @pytest.mark.parametrize("dtype,tol", [("float32", 1e-4), ("bfloat16", 3e-2)])
 def test_newton_schulz(shape, dtype, tol):

@@ -54,17 +54,23 @@ def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
     dtype.  The products run on the BLAS library (f32 accumulation)."""
     m, n = G.shape
     transpose = m > n
-    # X row-major throughout: elementwise ops on a transposed view would keep
-    # its column-major strides and run torch's strided kernels
-    G = G.T.contiguous() if transpose else G.contiguous()
-    X = G / (torch.sqrt(torch.sum(G * G)) + 1e-7)
+    # A tall G is iterated untransposed: with Y = X^T = G / (||G|| + eps),
+    # X X^T = Y^T Y and ((X X^T) X)^T = Y (Y^T Y) (X X^T is symmetric), so
+    # Y <- 1.5 Y - 0.5 Y (Y^T Y) is the transposed iteration without the two
+    # transposing copies.  Y stays row-major, and the library reads the
+    # transposed operand in place (2-D TN / NT GEMMs).
+    X = G.contiguous()
+    X = X / (torch.sqrt(torch.sum(X * X)) + 1e-7)
+    fused = X.dtype in (torch.bfloat16, torch.float32)
     for _ in range(steps):
-        A = X @ X.T                      # a 2-D NT GEMM: the library reads X.T in place
-        B = A @ X
-        X = K.ns_combine(X, B, out=X) if X.dtype in (torch.bfloat16, torch.float32) else 1.5 * X - 0.5 * B
-    if transpose:
-        X = X.T
-    return X.contiguous()
+        if transpose:
+            A = X.T @ X
+            B = X @ A
+        else:
+            A = X @ X.T
+            B = A @ X
+        X = K.ns_combine(X, B, out=X) if fused else 1.5 * X - 0.5 * B
+    return X
 
 
 class MiulionState(NamedTuple):

@@ -323,14 +323,38 @@ def bench_gemm_fwd(steps: int, warmup: int):
     return ms, 2.0 * M * N * Kd / (ms * 1e-3) / 1e12
 
 
-def bench_library_fp8(steps: int):
+def bench_gemm_ffn(steps: int, warmup: int):
+    """The GEMM target's shape: config 5's d=4096 FFN up-projection forward,
+    A = quantize(x, (1,128)) [32768, 4096] x W = quantize(N(0, 0.02)
+    [4096, 16384], (128,128)) -> bf16 [32768, 16384] (synthetic x ~ N(0,1),
+    seed 5).  Returns a dict with TFLOP/s and the fraction of dense FP8 peak,
+    beside hipBLASLt's unscaled FP8 GEMM at the same shape."""
+    import torch
+    from pratchya_amd import _kernels as K
+    M, Kd, N = CFG5_TOKENS, CFG5_D, CFG5_F
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn((M, Kd), generator=gen, device="cuda").to(torch.bfloat16)
+    w = (torch.randn((Kd, N), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+    a = K.operand_rows(*K.quantize(x, (1, 128)), (1, 128))
+    b = K.operand_transposed(*K.quantize(w, (128, 128)), (128, 128))
+    del x, w
+    out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    ms, _ = timed_graph(lambda i: K.gemm_nt(a, b, out=out), steps, warmup)
+    flop = 2 * M * N * Kd
+    tf = flop / (ms * 1e-3) / 1e12
+    return {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1), "frac_of_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4),
+            "flop": flop, "shape": f"[{M},{Kd}] x [{Kd},{N}] -> bf16",
+            "hipblaslt_fp8_no_block_scales": bench_library_fp8(10, (M, Kd, N))}
+
+
+def bench_library_fp8(steps: int, shape=(16384, 2048, 8192)):
     """Reference point for the GEMM: hipBLASLt's plain FP8 GEMM
     (``torch._scaled_mm``, e4m3fn operands, one scale per tensor, bf16 out) at
-    config 3's shape, timed like the other legs.  It has no block scales, so
-    it is context for the MFMA efficiency of the block-scaled kernel, not the
-    same computation."""
+    the given (M, K, N), config 3's by default, timed like the other legs.  It
+    has no block scales, so it is context for the MFMA efficiency of the
+    block-scaled kernel, not the same computation."""
     import torch
-    M, Kd, N = 16384, 2048, 8192
+    M, Kd, N = shape
     gen = torch.Generator(device="cuda").manual_seed(3)
     a = torch.randn((M, Kd), generator=gen, device="cuda").to(torch.float8_e4m3fn)
     b = (torch.randn((N, Kd), generator=gen, device="cuda") * 0.1).to(torch.float8_e4m3fn).t()
@@ -679,7 +703,7 @@ def main():
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--counter-workload", action="store_true",
                     help="only run the direct-launch workload used for rocprofv3 --pmc runs")
-    ap.add_argument("--only", choices=["cfg3", "cfg4", "cfg5", "optim", "elementwise"], default=None,
+    ap.add_argument("--only", choices=["cfg3", "ffn", "cfg4", "cfg5", "optim", "elementwise"], default=None,
                     help="run one secondary configuration alone (for profiling) and print its result")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -701,6 +725,8 @@ def main():
             res = {"ms": ms_, "TFLOP/s": tf_}
         elif args.only == "cfg4":
             res = bench_config4(max(20, args.steps // 4), max(4, args.warmup // 4))
+        elif args.only == "ffn":
+            res = bench_gemm_ffn(max(8, args.steps // 10), 2)
         elif args.only == "optim":
             res = bench_optimizer(3)
         elif args.only == "elementwise":
@@ -729,6 +755,9 @@ def main():
                                      "shape": "[16384,2048] x [2048,8192] -> bf16",
                                      "flop": 2 * 16384 * 2048 * 8192,
                                      "hipblaslt_fp8_no_block_scales": bench_library_fp8(20)}
+        _log("d=4096 FFN gemm fwd: start")
+        extra["ffn_d4096_gemm_fwd"] = bench_gemm_ffn(max(8, args.steps // 10), 2)
+        _log(f"d=4096 FFN gemm fwd: {extra['ffn_d4096_gemm_fwd']['TFLOP/s']} TFLOP/s")
         _log("config 4: start")
         extra["config4_backward"] = bench_config4(max(20, args.steps // 4), max(4, args.warmup // 4))
         _log("config 5: start")

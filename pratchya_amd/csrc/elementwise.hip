@@ -376,15 +376,15 @@ EwPlan plan(const QOperand& X, const QOperand& Y, const uint8_t* q, int64_t W, i
 template <int OP, typename I>
 void launch_one_pass(const QOperand& X, const QOperand& Y, uint8_t* q, uint8_t* sc8, float* sc32, int64_t n,
                      int64_t W, const EwPlan& p, hipStream_t st) {
-  const dim3 grid(blocks_for(n, 4096));
+  const dim3 grid(blocks_for(n, 1024));           // one wave per workgroup
   if (X.lb >= 0 && Y.lb >= 0 && p.bl_log2 == 3 && p.gl_log2 == 6)     // (1, 128), K = 8 everywhere
-    hipLaunchKernelGGL((k_ew_rowgroup<OP, true, I, 8, 64>), grid, dim3(256), 0, st, X, Y, q, sc8, sc32, n, W,
+    hipLaunchKernelGGL((k_ew_rowgroup<OP, true, I, 8, 64>), grid, dim3(64), 0, st, X, Y, q, sc8, sc32, n, W,
                        p.bl_log2, p.gl_log2);
   else if (X.lb >= 0 && Y.lb >= 0)
-    hipLaunchKernelGGL((k_ew_rowgroup<OP, true, I, 0, 0>), grid, dim3(256), 0, st, X, Y, q, sc8, sc32, n, W,
+    hipLaunchKernelGGL((k_ew_rowgroup<OP, true, I, 0, 0>), grid, dim3(64), 0, st, X, Y, q, sc8, sc32, n, W,
                        p.bl_log2, p.gl_log2);
   else
-    hipLaunchKernelGGL((k_ew_rowgroup<OP, false, I, 0, 0>), grid, dim3(256), 0, st, X, Y, q, sc8, sc32, n, W,
+    hipLaunchKernelGGL((k_ew_rowgroup<OP, false, I, 0, 0>), grid, dim3(64), 0, st, X, Y, q, sc8, sc32, n, W,
                        p.bl_log2, p.gl_log2);
 }
 

@@ -101,6 +101,29 @@ def cpu_baseline_config3(rows: int = 512):
                       f"(NumPy / OpenBLAS)"}
 
 
+def cpu_baseline_ffn(rows: int = 256):
+    """The oracle's d=4096 FFN forward, matmul_impl's f32 product of the
+    dequantized operands (Q:605-608), timed on a row sample of the
+    [32768, 4096] activation against a [4096, 16384] weight on this host's
+    BLAS threads.  The operands are f32 stand-ins of the dequantized arrays
+    (the product's cost does not depend on the values, and the NumPy quantizer
+    would take a minute on the 67M-element weight)."""
+    Kd, N = CFG5_D, CFG5_F
+    rng = np.random.default_rng(5)
+    xd = rng.standard_normal((rows, Kd), dtype=np.float32)
+    wd = rng.standard_normal((Kd, N), dtype=np.float32) * np.float32(0.02)
+    xd @ wd                                            # warm
+    t0 = time.perf_counter()
+    reps = 3
+    for _ in range(reps):
+        xd @ wd
+    per = (time.perf_counter() - t0) / reps
+    tf = 2 * rows * Kd * N / per / 1e12
+    return {"value": round(tf, 4), "unit": "TFLOP/s", "cores": _blas_threads(), "kind": "port",
+            "sample": f"f32 matmul of operands of the dequantized shapes, {rows} of {CFG5_TOKENS} "
+                      f"rows, {reps} reps (NumPy / OpenBLAS)"}
+
+
 def cpu_baseline_config4(rows: int = 256):
     """The oracle's config-4 backward on a token sample: dY (rows tokens)
     requantized (1,128) and contracted with W^T (dgrad), and A^T dY with both
@@ -775,10 +798,11 @@ def main():
         extra["elementwise_add"]["cpu_baseline"] = cpu_baseline_elementwise()
         if "config3_gemm_fwd" in extra:
             extra["config3_gemm_fwd"]["cpu_baseline"] = cpu_baseline_config3()
+            extra["ffn_d4096_gemm_fwd"]["cpu_baseline"] = cpu_baseline_ffn()
             extra["config4_backward"]["cpu_baseline"] = cpu_baseline_config4()
             extra["config5_layer"]["cpu_baseline"] = cpu_baseline_config5()
             extra["optimizer_step"]["cpu_baseline"] = cpu_baseline_optimizer()
-        _log("cpu baselines of configs 1, 3, 4, 5, the elementwise add and the optimizer: done")
+        _log("cpu baselines of configs 1, 3, 4, 5, the FFN GEMM, the elementwise add and the optimizer: done")
     line = {
         "metric": METRIC,
         "value": round(gbs, 2),

@@ -671,7 +671,8 @@ COPY_BYTES = 256 << 20   # bytes read (and written) by the reference copy of the
 
 def counter_workload(reps: int = 10) -> None:
     """Direct launches (no graph) for rocprofv3 counter runs: ``reps`` x the
-    config-2 quantize, ``reps`` x the config-3 GEMM, and ``reps`` x a plain
+    config-2 quantize, ``reps`` x the config-3 GEMM, ``reps`` x the d=4096 FFN
+    GEMM (after its operands are quantized), and ``reps`` x a plain
     device-to-device copy of COPY_BYTES (``dst.copy_(src)``, which the HIP
     runtime runs as its copyBuffer kernel), whose FETCH_SIZE / WRITE_SIZE
     readings calibrate the counters against known byte counts."""
@@ -696,6 +697,18 @@ def counter_workload(reps: int = 10) -> None:
         K.gemm_nt(a, b, out=out)
     torch.cuda.synchronize()
     _log(f"counter workload: {reps} x gemm done")
+    # the GEMM target's shape: d=4096 FFN up-projection forward
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    xf = torch.randn((CFG5_TOKENS, CFG5_D), generator=gen, device="cuda").to(torch.bfloat16)
+    wf = (torch.randn((CFG5_D, CFG5_F), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+    af = K.operand_rows(*K.quantize(xf, (1, 128)), (1, 128))
+    bf = K.operand_transposed(*K.quantize(wf, (128, 128)), (128, 128))
+    outf = torch.empty((CFG5_TOKENS, CFG5_F), dtype=torch.bfloat16, device="cuda")
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        K.gemm_nt(af, bf, out=outf)
+    torch.cuda.synchronize()
+    _log(f"counter workload: {reps} x d=4096 FFN gemm done")
     for _ in range(reps):
         dst.copy_(src)
     torch.cuda.synchronize()

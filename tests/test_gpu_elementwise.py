@@ -81,6 +81,9 @@ def test_elementwise_special_values(K, op):
     b[0, :5] = [0.0, 0.0, 0.0, 1e-3, 3e38]
     a[1] = 1e-30
     b[1] = 1e-30
+    a[2, :64] = 3e-36            # block scales below 2^-110: the unfolded dequantization
+    b[2, 64:] = -2e-37
+    a[3] = 1e36                  # block scales at or above 2^119
     xa, xb = O.quantize_impl(a, (1, 128)), O.quantize_impl(b, (1, 128))
     for go in ((1, 128), (4, 32)):
         want = E.elementwise(op, xa, (1, 128), xb, (1, 128), go)

@@ -439,11 +439,17 @@ __device__ __forceinline__ float load_elem(const void* x, int64_t i) {
 // load (the host checks the alignment).
 template <bool IS_BF16, int CH, bool VEC>
 __device__ __forceinline__ void load_chunk(const void* x, int64_t off, float (&v)[CH]) {
-  if constexpr (VEC) {
-    static_assert(CH * (IS_BF16 ? 2 : 4) == 16, "a vector chunk is 16 bytes");
-    const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const char*>(x) + off * (IS_BF16 ? 2 : 4));
+  constexpr int ESZ = IS_BF16 ? 2 : 4;
+  if constexpr (VEC && CH * ESZ >= 16) {
+    // 16-byte loads (the host checks the alignment)
+    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + off * ESZ);
+    constexpr int E = 16 / ESZ;
 #pragma unroll
-    for (int k = 0; k < CH; ++k) v[k] = elem_f32<IS_BF16>(w, k);
+    for (int j = 0; j < CH / E; ++j) {
+      const uint4 w = p[j];
+#pragma unroll
+      for (int k = 0; k < E; ++k) v[j * E + k] = elem_f32<IS_BF16>(w, k);
+    }
   } else {
 #pragma unroll
     for (int k = 0; k < CH; ++k) v[k] = load_elem<IS_BF16>(x, off + k);
@@ -489,8 +495,10 @@ __global__ __launch_bounds__(256) void k_blockmax(const void* __restrict__ x,
 // OUT 0 writes the payload; OUT 1 / 2 write it dequantized as bf16 / f32
 // (fake quantization, with the NaN-e8m0 repair when fix_nan is set), as the
 // group-per-wave kernel's modes.
-// VEC: 16-byte input loads and one vector store per chunk (host-checked alignment).
-template <bool IS_BF16, int CH, int OUT, bool VEC>
+// VEC: CH is 16 output bytes (16 payload bytes, 8 bf16 or 4 f32 values), the
+// input read with 16-byte loads and the output with one 16-byte store
+// (host-checked alignment).  I: index type (32-bit below 2^31 elements).
+template <bool IS_BF16, int CH, int OUT, bool VEC, typename I = int64_t>
 __global__ __launch_bounds__(256) void k_cast_general(const void* __restrict__ x,
                                                       void* __restrict__ outv,
                                                       const uint8_t* __restrict__ sc8,
@@ -499,18 +507,18 @@ __global__ __launch_bounds__(256) void k_cast_general(const void* __restrict__ x
                                                       int64_t b, int64_t K, int fix_nan) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n_chunks) return;
-  const int64_t off = t * CH;
-  const int64_t i = off / W, c = off - i * W;
-  const int64_t blk = (i / a) * (W / b) + c / b;
+  const I off = (I)t * CH;
+  const I i = off / (I)W, c = off - i * (I)W;
+  const I blk = (i / (I)a) * ((I)W / (I)b) + c / (I)b;
   const uint32_t e = sc8[blk];
-  const float G = sc32[blk / K];
+  const float G = sc32[blk / (I)K];
   const float sG = e8m0_decode(e) * G;
   const float S = quant_scale(e, G);
   const bool ok = sG >= kClamp && sG <= 3.0e38f;
   const float yv = 128.0f / S;
   const float dq = e8m0_decode((fix_nan && e == 0xFFu) ? 0x7Fu : e) * G;
   float xv[CH];
-  load_chunk<IS_BF16, CH, VEC>(x, off, xv);
+  load_chunk<IS_BF16, CH, VEC && (CH * (IS_BF16 ? 2 : 4) >= 16)>(x, (int64_t)off, xv);
   uint32_t ov[CH];                              // output element bits
 #pragma unroll
   for (int k = 0; k < CH; ++k) {
@@ -527,25 +535,22 @@ __global__ __launch_bounds__(256) void k_cast_general(const void* __restrict__ x
       ov[k] = OUT == 1 ? f32_to_bf16_rne(d) : f2u(d);
     }
   }
-  if constexpr (VEC && OUT == 0) {
-    uint32_t w[CH / 4];
+  if constexpr (VEC) {
+    // pack into 32-bit words and store them as one 16-byte vector
+    constexpr int PER = OUT == 0 ? 4 : (OUT == 1 ? 2 : 1);      // elements per word
+    static_assert(CH / PER == 4, "a vector chunk is 16 output bytes");
+    uint32_t w[4];
 #pragma unroll
-    for (int i = 0; i < CH / 4; ++i)
-      w[i] = ov[4 * i] | (ov[4 * i + 1] << 8) | (ov[4 * i + 2] << 16) | (ov[4 * i + 3] << 24);
-    if constexpr (CH == 8) *reinterpret_cast<uint2*>(static_cast<uint8_t*>(outv) + off) = make_uint2(w[0], w[1]);
-    else *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(outv) + off) = w[0];
-  } else if constexpr (VEC && OUT == 1) {
-    uint32_t w[CH / 2];
-#pragma unroll
-    for (int i = 0; i < CH / 2; ++i) w[i] = ov[2 * i] | (ov[2 * i + 1] << 16);
-    uint16_t* o = static_cast<uint16_t*>(outv) + off;
-    if constexpr (CH == 8) *reinterpret_cast<uint4*>(o) = make_uint4(w[0], w[1], w[2], w[3]);
-    else *reinterpret_cast<uint2*>(o) = make_uint2(w[0], w[1]);
-  } else if constexpr (VEC && OUT == 2) {
-    float* o = static_cast<float*>(outv) + off;
-#pragma unroll
-    for (int i = 0; i < CH / 4; ++i)
-      *reinterpret_cast<uint4*>(o + 4 * i) = make_uint4(ov[4 * i], ov[4 * i + 1], ov[4 * i + 2], ov[4 * i + 3]);
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (PER == 4)
+        w[j] = ov[4 * j] | (ov[4 * j + 1] << 8) | (ov[4 * j + 2] << 16) | (ov[4 * j + 3] << 24);
+      else if constexpr (PER == 2)
+        w[j] = ov[2 * j] | (ov[2 * j + 1] << 16);
+      else
+        w[j] = ov[j];
+    }
+    char* o = static_cast<char*>(outv) + (int64_t)off * (OUT == 0 ? 1 : (OUT == 1 ? 2 : 4));
+    *reinterpret_cast<uint4*>(o) = make_uint4(w[0], w[1], w[2], w[3]);
   } else {
 #pragma unroll
     for (int k = 0; k < CH; ++k) {
@@ -828,7 +833,6 @@ int launch_general(const void* x, void* q, uint8_t* sc8, float* sc32, uint32_t* 
   const int64_t n_chunks = L.n() / ch;
   const int64_t seg = L.b / ch;
   const int seg_log2 = (is_pow2(seg) && seg <= 64) ? ilog2(seg) : -1;
-  const unsigned gr = grid_for(n_chunks, 256);
   // rows folded per block-max thread: the largest power of two <= 16 dividing a
   int rows = 1;
   while (rows < 16 && L.a % (rows * 2) == 0) rows *= 2;
@@ -855,18 +859,30 @@ int launch_general(const void* x, void* q, uint8_t* sc8, float* sc32, uint32_t* 
   else
     hipLaunchKernelGGL(k_group_scales_small, dim3(grid_for(n_groups, 256)), dim3(256), 0, st, ws,
                        sc8, sc32, n_groups, L.K);
-#define PRATCHYA_CAST(C, V)                                                                    \
-  hipLaunchKernelGGL((k_cast_general<IS_BF16, C, OUT, V>), dim3(gr), dim3(256), 0, st, x, q, sc8, sc32, \
-                     n_chunks, L.W, L.a, L.b, L.K, fix_nan)
+  // the cast: 16 output bytes per thread when b allows it and the buffers are
+  // aligned (payload 16, bf16 8, f32 4 elements), 32-bit indices below 2^31
   const int out_esz = OUT == 0 ? 1 : (OUT == 1 ? 2 : 4);
-  if (vin && aligned(q, (size_t)ch * out_esz)) {
-    PRATCHYA_CAST((IS_BF16 ? 8 : 4), true);
+  const int want = 16 / out_esz;
+  int cch = 1;
+  while (cch < want && L.b % (cch * 2) == 0) cch *= 2;
+  const int in_esz = IS_BF16 ? 2 : 4;
+  const bool cvec = cch == want && aligned(x, (size_t)(cch * in_esz < 16 ? cch * in_esz : 16)) && aligned(q, 16);
+  const int64_t n_cast = L.n() / cch;
+  const unsigned gc = grid_for(n_cast, 256);
+#define PRATCHYA_CAST(C, V, ...)                                                                  \
+  hipLaunchKernelGGL((k_cast_general<IS_BF16, C, OUT, V, ##__VA_ARGS__>), dim3(gc), dim3(256), 0, st, x, q, sc8, \
+                     sc32, n_cast, L.W, L.a, L.b, L.K, fix_nan)
+  if (cvec && L.n() <= 0x7FFFFFFF) {
+    PRATCHYA_CAST((16 / (OUT == 0 ? 1 : (OUT == 1 ? 2 : 4))), true, uint32_t);
+  } else if (cvec) {
+    PRATCHYA_CAST((16 / (OUT == 0 ? 1 : (OUT == 1 ? 2 : 4))), true);
   } else {
-    switch (ch) {
+    switch (cch) {
       case 1: PRATCHYA_CAST(1, false); break;
       case 2: PRATCHYA_CAST(2, false); break;
       case 4: PRATCHYA_CAST(4, false); break;
-      default: PRATCHYA_CAST(8, false); break;
+      case 8: PRATCHYA_CAST(8, false); break;
+      default: PRATCHYA_CAST(16, false); break;
     }
   }
 #undef PRATCHYA_CAST

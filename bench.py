@@ -650,6 +650,73 @@ def bench_elementwise(steps: int, warmup: int):
             "bit_exact_vs_oracle": ok}
 
 
+EMB_VOCAB = 65536          # RWKV-7's vocabulary; the table is [vocab, d_model] quantized (128, 128)
+
+
+def bench_embedding(steps: int, warmup: int):
+    """Embedding lookup of config 5's 32768 tokens in a [65536, 4096] table
+    quantized (128, 128) (QArrayImpl.__getitem__ with an index array,
+    pratchya/_qualia/_qarr.py:263-284; M:32-37): pratchya_gather_dequantize
+    (only the indexed rows, bf16 out) against the HBM roofline, beside the
+    reference's order of work (dequantize the whole table to f32, then
+    index).  Synthetic table N(0, 0.02) and uniform token ids, seed 7."""
+    import ctypes
+    import torch
+    from pratchya_amd import _kernels as K
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    g = (128, 128)
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    table = (torch.randn((EMB_VOCAB, CFG5_D), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+    t8, ts8, ts32 = K.quantize(table, g)
+    del table
+    idx = torch.randint(0, EMB_VOCAB, (CFG5_TOKENS,), generator=gen, device="cuda", dtype=torch.int64)
+    out = torch.empty((CFG5_TOKENS, CFG5_D), dtype=torch.bfloat16, device="cuda")
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+
+    def fused(i):
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        rc = lib.pratchya_gather_dequantize(p(t8), p(ts8), p(ts32), EMB_VOCAB, CFG5_D, 128, 128, p(idx),
+                                            CFG5_TOKENS, p(out), _lib.DT_BF16, st)
+        if rc:
+            raise RuntimeError(lib.pratchya_last_error().decode())
+
+    def whole(i):
+        out.copy_(K.dequantize(t8, ts8, ts32, torch.float32, g)[idx])
+
+    ms, _ = timed_graph(fused, steps, warmup)
+    ms_w, _ = timed_graph(whole, max(4, steps // 10), 2)
+    fused(0)
+    ok = bool(torch.equal(out, K.dequantize(t8, ts8, ts32, torch.float32, g)[idx].to(torch.bfloat16)))
+    nbytes = CFG5_TOKENS * CFG5_D * (1 + 2) + CFG5_TOKENS * 8
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes": nbytes, "shape": f"{CFG5_TOKENS} ids into [{EMB_VOCAB},{CFG5_D}] (128,128) -> bf16",
+            "dequantize_whole_table_then_index_us": round(ms_w * 1e3, 1),
+            "same_as_whole_table_path": ok}
+
+
+def cpu_baseline_embedding(rows: int = 1024):
+    """The reference's order of work on this host: the oracle's dequantize_impl
+    of the whole table (timed on ``rows`` of its rows and scaled to all of
+    them) followed by the row gather; reported in the gather's algorithmic
+    GB/s."""
+    from oracle import qarr_oracle as O
+    rng = np.random.default_rng(7)
+    part = O.quantize_impl((rng.standard_normal((rows, CFG5_D)) * 0.02).astype(np.float32), (128, 128))
+    t0 = time.perf_counter()
+    deq = O.dequantize_impl(*part, "float32", (128, 128))
+    el = (time.perf_counter() - t0) * (EMB_VOCAB / rows)
+    ids = rng.integers(0, rows, CFG5_TOKENS)
+    t0 = time.perf_counter()
+    deq[ids]                                           # the reference indexes the f32 dequantization
+    el += time.perf_counter() - t0
+    nbytes = CFG5_TOKENS * CFG5_D * 3 + CFG5_TOKENS * 8
+    return {"value": round(nbytes / el / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle dequantize_impl of {rows} of {EMB_VOCAB} table rows scaled to the whole table "
+                      f"({el:.1f} s) + the gather of {CFG5_TOKENS} rows (NumPy)"}
+
+
 def cpu_baseline_elementwise(rows: int = 2048):
     """The oracle's quantized add on ``rows`` rows of the config 2 shape,
     scaled to the full tensor."""
@@ -739,7 +806,8 @@ def main():
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--counter-workload", action="store_true",
                     help="only run the direct-launch workload used for rocprofv3 --pmc runs")
-    ap.add_argument("--only", choices=["cfg3", "ffn", "cfg4", "cfg5", "optim", "elementwise"], default=None,
+    ap.add_argument("--only", choices=["cfg3", "ffn", "cfg4", "cfg5", "optim", "elementwise", "embedding"],
+                    default=None,
                     help="run one secondary configuration alone (for profiling) and print its result")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -767,6 +835,8 @@ def main():
             res = bench_optimizer(3)
         elif args.only == "elementwise":
             res = bench_elementwise(max(20, args.steps // 2), max(4, args.warmup // 4))
+        elif args.only == "embedding":
+            res = bench_embedding(max(20, args.steps // 4), max(4, args.warmup // 4))
         else:
             res = bench_config5(max(3, args.steps // 40), 2)
         print(json.dumps({args.only: res}), flush=True)
@@ -779,6 +849,9 @@ def main():
     _log("config 1 round trip: start")
     extra["config1_round_trip"] = bench_config1(max(20, args.steps // 4), max(4, args.warmup // 4))
     _log(f"config 1 round trip: {extra['config1_round_trip']['us_per_round_trip']} us")
+    _log("embedding lookup: start")
+    extra["embedding_lookup"] = bench_embedding(max(20, args.steps // 4), max(4, args.warmup // 4))
+    _log(f"embedding lookup: {extra['embedding_lookup']['us']} us")
     _log("elementwise add: start")
     extra["elementwise_add"] = bench_elementwise(max(20, args.steps // 2), max(4, args.warmup // 4))
     _log(f"elementwise add: {extra['elementwise_add']['us']} us")
@@ -809,13 +882,15 @@ def main():
         _log(f"cpu baseline: {cpu['value']} GB/s")
         extra["config1_round_trip"]["cpu_baseline"] = cpu_baseline_config1()
         extra["elementwise_add"]["cpu_baseline"] = cpu_baseline_elementwise()
+        extra["embedding_lookup"]["cpu_baseline"] = cpu_baseline_embedding()
         if "config3_gemm_fwd" in extra:
             extra["config3_gemm_fwd"]["cpu_baseline"] = cpu_baseline_config3()
             extra["ffn_d4096_gemm_fwd"]["cpu_baseline"] = cpu_baseline_ffn()
             extra["config4_backward"]["cpu_baseline"] = cpu_baseline_config4()
             extra["config5_layer"]["cpu_baseline"] = cpu_baseline_config5()
             extra["optimizer_step"]["cpu_baseline"] = cpu_baseline_optimizer()
-        _log("cpu baselines of configs 1, 3, 4, 5, the FFN GEMM, the elementwise add and the optimizer: done")
+        _log("cpu baselines of configs 1, 3, 4, 5, the FFN GEMM, the embedding lookup, the elementwise add and "
+             "the optimizer: done")
     line = {
         "metric": METRIC,
         "value": round(gbs, 2),

@@ -574,7 +574,16 @@ template <int IN, int CH, bool VEC>
 __device__ __forceinline__ void dq_load(const void* __restrict__ x, int64_t off, float (&v)[CH]) {
   if constexpr (IN == 0) {
     const uint8_t* p = static_cast<const uint8_t*>(x) + off;
-    if constexpr (VEC && CH % 4 == 0) {
+    if constexpr (VEC && CH % 16 == 0) {
+#pragma unroll
+      for (int j = 0; j < CH / 16; ++j) {
+        const uint4 w = reinterpret_cast<const uint4*>(p)[j];
+        fp8_word(w.x, v[16 * j + 0], v[16 * j + 1], v[16 * j + 2], v[16 * j + 3]);
+        fp8_word(w.y, v[16 * j + 4], v[16 * j + 5], v[16 * j + 6], v[16 * j + 7]);
+        fp8_word(w.z, v[16 * j + 8], v[16 * j + 9], v[16 * j + 10], v[16 * j + 11]);
+        fp8_word(w.w, v[16 * j + 12], v[16 * j + 13], v[16 * j + 14], v[16 * j + 15]);
+      }
+    } else if constexpr (VEC && CH % 4 == 0) {
 #pragma unroll
       for (int j = 0; j < CH / 4; ++j)
         fp8_word(reinterpret_cast<const uint32_t*>(p)[j], v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
@@ -657,7 +666,7 @@ __global__ __launch_bounds__(256) void k_dequant(const void* __restrict__ x,
 // clamped to [0, H - 1] (jnp's indexing of a dequantized array).  Thread per
 // CH consecutive columns (CH | b) of one output row.
 // --------------------------------------------------------------------------
-template <bool OUT_BF16, int CH>
+template <bool OUT_BF16, int CH, bool VEC = false, typename I = int64_t>
 __global__ __launch_bounds__(256) void k_gather_dequant(const uint8_t* __restrict__ x,
                                                         const uint8_t* __restrict__ sc8,
                                                         const float* __restrict__ sc32,
@@ -665,25 +674,46 @@ __global__ __launch_bounds__(256) void k_gather_dequant(const uint8_t* __restric
                                                         int64_t H, int64_t W, int64_t a, int64_t b,
                                                         int64_t K, void* __restrict__ out) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t cpr = W / CH;
-  if (t >= n_idx * cpr) return;
-  const int64_t i = t / cpr, c = (t - i * cpr) * CH;
+  const I cpr = (I)(W / CH);
+  if (t >= n_idx * (int64_t)cpr) return;
+  const I i = (I)t / cpr, c = ((I)t - i * cpr) * CH;
   int64_t r = idx[i];
   if (r < 0) r += H;
   r = r < 0 ? 0 : (r >= H ? H - 1 : r);
-  const int64_t blk = (r / a) * (W / b) + c / b;
+  const int64_t blk = (r / a) * (W / b) + (int64_t)c / b;
   const float sc = e8m0_decode(sc8[blk]) * sc32[blk / K];
-  const uint8_t* q = x + r * W + c;
   float v[CH];
+  dq_load<0, CH, VEC>(x, r * W + c, v);
 #pragma unroll
-  for (int k = 0; k < CH; ++k) v[k] = (e4m3fn_to_f32(q[k]) * sc) * 0.0078125f;
-  const int64_t o = i * W + c;
+  for (int k = 0; k < CH; ++k) v[k] = (v[k] * sc) * 0.0078125f;
+  const int64_t o = (int64_t)i * W + c;
   if constexpr (OUT_BF16) {
+    uint16_t* po = static_cast<uint16_t*>(out) + o;
+    if constexpr (VEC && CH % 8 == 0) {
 #pragma unroll
-    for (int k = 0; k < CH; ++k) static_cast<uint16_t*>(out)[o + k] = (uint16_t)f32_to_bf16_rne(v[k]);
+      for (int j = 0; j < CH / 8; ++j) {
+        uint4 w;
+        w.x = f32_to_bf16_rne(v[8 * j + 0]) | (f32_to_bf16_rne(v[8 * j + 1]) << 16);
+        w.y = f32_to_bf16_rne(v[8 * j + 2]) | (f32_to_bf16_rne(v[8 * j + 3]) << 16);
+        w.z = f32_to_bf16_rne(v[8 * j + 4]) | (f32_to_bf16_rne(v[8 * j + 5]) << 16);
+        w.w = f32_to_bf16_rne(v[8 * j + 6]) | (f32_to_bf16_rne(v[8 * j + 7]) << 16);
+        reinterpret_cast<uint4*>(po)[j] = w;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < CH; ++k) po[k] = (uint16_t)f32_to_bf16_rne(v[k]);
+    }
   } else {
+    float* po = static_cast<float*>(out) + o;
+    if constexpr (VEC && CH % 4 == 0) {
 #pragma unroll
-    for (int k = 0; k < CH; ++k) static_cast<float*>(out)[o + k] = v[k];
+      for (int j = 0; j < CH / 4; ++j)
+        reinterpret_cast<uint4*>(po)[j] =
+            make_uint4(f2u(v[4 * j]), f2u(v[4 * j + 1]), f2u(v[4 * j + 2]), f2u(v[4 * j + 3]));
+    } else {
+#pragma unroll
+      for (int k = 0; k < CH; ++k) po[k] = v[k];
+    }
   }
 }
 
@@ -1167,20 +1197,32 @@ extern "C" int pratchya_gather_dequantize(const uint8_t* x_fp8, const uint8_t* s
   if (H == 0) return pratchya_set_error(PRATCHYA_EINVAL, "gather_dequantize: index into an empty table");
   if (!x_fp8 || !sc_fp8 || !sc_fp32 || !idx || !out)
     return pratchya_set_error(PRATCHYA_EINVAL, "gather_dequantize: null buffer");
-  const int ch = chunk_elems(L.b, true);
+  // 16 payload bytes per thread (one 16-byte load; two bf16 or four f32
+  // 16-byte stores) when b allows it and the buffers are aligned
+  const bool bf = out_dtype == PRATCHYA_DT_BF16;
+  const int want = 16;
+  int ch = 1;
+  while (ch < want && L.b % (ch * 2) == 0) ch *= 2;
+  const bool vec = ch == want && aligned(x_fp8, (size_t)ch) && aligned(out, 16);
+  const bool narrow = n_idx * W <= 0x7FFFFFFF;
   const int64_t n_thr = n_idx * (W / ch);
   const unsigned gr = grid_for(n_thr, 256);
-  const bool bf = out_dtype == PRATCHYA_DT_BF16;
-#define PRATCHYA_GD(C)                                                                              \
-  if (bf) hipLaunchKernelGGL((k_gather_dequant<true, C>), dim3(gr), dim3(256), 0, stream, x_fp8, sc_fp8, \
-                             sc_fp32, idx, n_idx, H, W, L.a, L.b, L.K, out);                        \
-  else hipLaunchKernelGGL((k_gather_dequant<false, C>), dim3(gr), dim3(256), 0, stream, x_fp8, sc_fp8, \
-                          sc_fp32, idx, n_idx, H, W, L.a, L.b, L.K, out)
-  switch (ch) {
-    case 1: PRATCHYA_GD(1); break;
-    case 2: PRATCHYA_GD(2); break;
-    case 4: PRATCHYA_GD(4); break;
-    default: PRATCHYA_GD(8); break;
+#define PRATCHYA_GD(C, ...)                                                                              \
+  if (bf) hipLaunchKernelGGL((k_gather_dequant<true, C, ##__VA_ARGS__>), dim3(gr), dim3(256), 0, stream, x_fp8, \
+                             sc_fp8, sc_fp32, idx, n_idx, H, W, L.a, L.b, L.K, out);                    \
+  else hipLaunchKernelGGL((k_gather_dequant<false, C, ##__VA_ARGS__>), dim3(gr), dim3(256), 0, stream, x_fp8, \
+                          sc_fp8, sc_fp32, idx, n_idx, H, W, L.a, L.b, L.K, out)
+  if (vec) {
+    if (narrow) PRATCHYA_GD(16, true, uint32_t);
+    else PRATCHYA_GD(16, true);
+  } else {
+    switch (ch) {
+      case 1: PRATCHYA_GD(1); break;
+      case 2: PRATCHYA_GD(2); break;
+      case 4: PRATCHYA_GD(4); break;
+      case 8: PRATCHYA_GD(8); break;
+      default: PRATCHYA_GD(16); break;
+    }
   }
 #undef PRATCHYA_GD
   return check_launch("gather_dequantize");

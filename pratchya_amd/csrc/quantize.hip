@@ -1110,11 +1110,12 @@ namespace {
 template <int IN, bool OUT_BF16>
 int launch_dequant(const void* x, const uint8_t* sc8, const float* sc32, void* out,
                    const Layout& L, hipStream_t st) {
-  // 16 output bytes per thread when b allows it and the buffers are aligned
-  // (16 payload bytes, two stores, for an fp8 input to bf16; an f32 output
-  // keeps one contiguous 16-byte store per lane: 4 values per lane measured
-  // 35.6 us against 47.9 us for 16 on a (1, 128) [16384, 2048] payload)
-  const int want = IN == 0 && OUT_BF16 ? 16 : (OUT_BF16 ? 8 : 4);
+  // Chunk per thread when b allows it and the buffers are aligned: an fp8
+  // input takes 16 payload bytes to bf16 (two 16-byte stores) and 8 to f32
+  // (two; on a (1, 128) [16384, 2048] payload 8 f32 values per lane took
+  // 36.0-36.9 us, 4 39.0-39.4 us, 16 47.9 us); bf16 / f32 cotangents 16
+  // output bytes.
+  const int want = IN == 0 && OUT_BF16 ? 16 : (OUT_BF16 ? 8 : (IN == 0 ? 8 : 4));
   int ch = 1;
   while (ch < want && L.b % (ch * 2) == 0) ch *= 2;
   const int in_esz = IN == 0 ? 1 : (IN == 1 ? 2 : 4);
@@ -1127,7 +1128,7 @@ int launch_dequant(const void* x, const uint8_t* sc8, const float* sc32, void* o
 #define PRATCHYA_DQ(C, V, ...)                                                                              \
   hipLaunchKernelGGL((k_dequant<IN, OUT_BF16, C, V, ##__VA_ARGS__>), dim3(gr), dim3(256), 0, st, x, sc8, sc32, \
                      out, n_chunks, L.W, L.a, L.b, L.K, lb, lk)
-  constexpr int VCH = IN == 0 && OUT_BF16 ? 16 : (OUT_BF16 ? 8 : 4);
+  constexpr int VCH = IN == 0 && OUT_BF16 ? 16 : (OUT_BF16 ? 8 : (IN == 0 ? 8 : 4));
   constexpr int OCH = OUT_BF16 ? 8 : 4;          // 16 output bytes, for b not a multiple of 16
   const bool vec_o = VCH != OCH && !vec && ch == OCH && aligned(x, (size_t)OCH) && aligned(out, 16);
   if (vec && narrow && flat) {

@@ -189,3 +189,36 @@ def test_optimizer_entry_point_codes_without_gpu():
              None, F32, None) == _lib.OK
     assert u(None, F32, 1, 0.0, None, F32, None, None, 1, 256, 256, 1, 1, F32, 0.05, 0.005,
              None, F32, None) == _lib.EINVAL
+
+
+def test_elementwise_and_ns_combine_codes_without_gpu():
+    """pratchya_elementwise / pratchya_ns_combine and the workspace query
+    validate operators, grids, dtypes and buffers before any launch."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    e = lib.pratchya_elementwise
+    # unknown operator, non-dividing result grid, non-dividing operand grid
+    assert e(6, None, None, None, 1, 128, None, None, None, 1, 128, 1, 64, 256, 1, 128,
+             None, None, None, None, 0, None) == _lib.EINVAL
+    assert b"unknown operator" in lib.pratchya_last_error()
+    assert e(0, None, None, None, 1, 128, None, None, None, 1, 128, 1, 64, 256, 3, 128,
+             None, None, None, None, 0, None) == _lib.EINVAL
+    assert b"result grid" in lib.pratchya_last_error()
+    assert e(0, None, None, None, 1, 128, None, None, None, 1, 96, 1, 64, 256, 1, 128,
+             None, None, None, None, 0, None) == _lib.EINVAL
+    assert b"y grid" in lib.pratchya_last_error()
+    # empty: nothing to do; non-empty with null buffers: an error
+    assert e(0, None, None, None, 1, 128, None, None, None, 1, 128, 1, 0, 256, 1, 128,
+             None, None, None, None, 0, None) == _lib.OK
+    assert e(0, None, None, None, 1, 128, None, None, None, 1, 128, 1, 64, 256, 1, 128,
+             None, None, None, None, 0, None) == _lib.EINVAL
+    assert b"null buffer" in lib.pratchya_last_error()
+    ws = lib.pratchya_elementwise_workspace_bytes
+    assert ws(1, 64, 256, 1, 128, 1, 128, 1, 128) == 0                 # one-pass layout
+    assert ws(1, 256, 256, 128, 128, 128, 128, 128, 128) == 4 * 4      # 2 x 2 blocks of (128, 128)
+    assert ws(1, 64, 256, 1, 128, 1, 128, 3, 128) == 0                 # invalid: 0
+    c = lib.pratchya_ns_combine
+    assert c(None, None, None, 16, _lib.DT_E4M3, None) == _lib.EINVAL
+    assert c(None, None, None, -1, _lib.DT_F32, None) == _lib.EINVAL
+    assert c(None, None, None, 0, _lib.DT_BF16, None) == _lib.OK
+    assert c(None, None, None, 16, _lib.DT_BF16, None) == _lib.EINVAL

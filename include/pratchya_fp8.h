@@ -130,6 +130,20 @@ int pratchya_gather_dequantize(const uint8_t* x_fp8, const uint8_t* sc_fp8, cons
                                int64_t H, int64_t W, int64_t a, int64_t b, const int64_t* idx,
                                int64_t n_idx, void* out, int out_dtype, hipStream_t stream);
 
+/* Embedding lookup, requantized, in one pass over the indexed rows:   replaces
+ *   QArrayImpl(dequantize_impl(x)[idx], (a, b))   (Q:263-284 with an integer
+ * index array, then Q:458-506) without the f32 gather in between.
+ * x: e4m3fn table [H, W] with its scales, tgrid (xa, xb); idx: int64
+ * [slices * T] (negative ids count from the end; clamped to [0, H - 1]); the
+ * result [slices, T, W] quantized with tgrid (a, b) into out_fp8 / out_sc8 /
+ * out_sc32, exactly the bytes quantize_impl gives for the f32 rows.
+ * `workspace`: slices * n_blk * 4 bytes (n_blk of a [T, W] slice under (a, b),
+ * pratchya_quant_layout). */
+int pratchya_gather_quantize(const uint8_t* x_fp8, const uint8_t* x_sc8, const float* x_sc32, int64_t H, int64_t W,
+                             int64_t xa, int64_t xb, const int64_t* idx, int64_t slices, int64_t T, int64_t a,
+                             int64_t b, uint8_t* out_fp8, uint8_t* out_sc8, float* out_sc32, void* workspace,
+                             size_t workspace_bytes, hipStream_t stream);
+
 /* operators of pratchya_elementwise (jnp's float32 semantics) */
 #define PRATCHYA_OP_ADD 0        /* x + y                                                   */
 #define PRATCHYA_OP_SUB 1        /* x - y                                                   */

@@ -335,6 +335,37 @@ def elementwise(op: str, x, grid_x, y, grid_y, tgrid, out=None):
     return q.view(E4M3), sc8.view(E8M0), sc32
 
 
+def gather_quantize(x_fp8: torch.Tensor, sc_fp8: torch.Tensor, sc_fp32: torch.Tensor, tgrid, idx: torch.Tensor,
+                    out_grid):
+    """``quantize_impl(dequantize_impl(x)[idx], out_grid)`` for a 2-D quantized
+    table and an integer index array of any shape, in one fused pass
+    (pratchya/_qualia/_qarr.py:263-284 then 458-506): returns the
+    ``(payload, sc_fp8, sc_fp32)`` of ``idx.shape + (W,)`` as ``quantize``
+    lays them out."""
+    _require_gpu(x_fp8, sc_fp8, sc_fp32, idx)
+    if x_fp8.dim() != 2:
+        raise ValueError("gather_quantize needs a 2-D table")
+    H, W = int(x_fp8.shape[0]), int(x_fp8.shape[1])
+    shape = tuple(idx.shape) + (W,)
+    S, T, Wd = slices_hw(shape)
+    a, b = int(out_grid[0]), int(out_grid[1])
+    n_blk, K, M = group_layout(T, Wd, (a, b))
+    lead = shape[:-2] if len(shape) >= 2 else ()
+    ids = idx.reshape(-1).to(torch.int64).contiguous()
+    q = torch.empty(shape, dtype=torch.uint8, device=x_fp8.device)
+    sc8 = torch.empty(lead + (M, K), dtype=torch.uint8, device=x_fp8.device)
+    sc32 = torch.empty(lead + (M, 1, 1), dtype=torch.float32, device=x_fp8.device)
+    ws_bytes = S * n_blk * 4
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x_fp8.device)
+    x8 = _u8(x_fp8).contiguous()
+    lib = _lib.load()
+    _lib.check(lib.pratchya_gather_quantize(_ptr(x8), _ptr(_u8(sc_fp8).contiguous()), _ptr(sc_fp32.contiguous().float()),
+                                            H, W, int(tgrid[0]), int(tgrid[1]), _ptr(ids), S, T, a, b, _ptr(q),
+                                            _ptr(sc8), _ptr(sc32), _ptr(ws), ws_bytes, _stream(x8)),
+               "gather_quantize")
+    return q.view(E4M3), sc8.view(E8M0), sc32
+
+
 def dequantize_bwd(g: torch.Tensor, sc_fp8: torch.Tensor, sc_fp32: torch.Tensor, tgrid) -> torch.Tensor:
     """Cotangent of the payload: ``(g * (f32(e<<23) * G) / 128).astype(g.dtype)``
     (pratchya/_qualia/_qarr.py:575-601)."""

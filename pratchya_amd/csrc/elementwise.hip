@@ -48,7 +48,13 @@ struct QOperand {
   const float* s32;
   int64_t a, b, K;
   int lb, lk;            // log2 b and log2 K when a == 1 and both are powers of two, else -1
+  const int64_t* rows;   // OP_GATHER: operand row of each result row (a [rows_h, W] table)
+  int64_t rows_h;
 };
+
+// Internal operator: the result is the dequantized operand X read through its
+// row map (an embedding lookup), Y unused.
+constexpr int OP_GATHER = 100;
 
 // Dequantization factor 2^(e-127) * G of the operand's block holding
 // element (i, c) of the [rows, W] array (row-major blocks, _qarr.py:562-564).
@@ -64,7 +70,9 @@ __device__ __forceinline__ float lax_sign(float v) {
 
 template <int OP>
 __device__ __forceinline__ float ew_apply(float x, float y) {
-  if constexpr (OP == PRATCHYA_OP_ADD) {
+  if constexpr (OP == OP_GATHER) {
+    return x;
+  } else if constexpr (OP == PRATCHYA_OP_ADD) {
     return x + y;
   } else if constexpr (OP == PRATCHYA_OP_SUB) {
     return x - y;
@@ -136,7 +144,19 @@ __device__ __forceinline__ void ew_values(const QOperand& X, const QOperand& Y, 
 // operands' block widths, so each operand has one block scale for them.
 template <int OP, int CH, bool VEC, typename I>
 __device__ __forceinline__ void ew_chunk(const QOperand& X, const QOperand& Y, I i, I c, I W, float (&z)[CH]) {
-  ew_values<OP, CH, VEC>(X, Y, operand_scale<I>(X, i, c, W), operand_scale<I>(Y, i, c, W), (size_t)(i * W + c), z);
+  if constexpr (OP == OP_GATHER) {
+    // table row idx[i] (negative counts from the end, clamped: jnp's gather)
+    int64_t r = X.rows[i];
+    if (r < 0) r += X.rows_h;
+    r = r < 0 ? 0 : (r >= X.rows_h ? X.rows_h - 1 : r);
+    const float sx = operand_scale<int64_t>(X, r, (int64_t)c, (int64_t)W);
+    float xv[CH];
+    load_fp8<CH, VEC>(X.q + r * (int64_t)W + c, xv);
+#pragma unroll
+    for (int k = 0; k < CH; ++k) z[k] = (xv[k] * sx) * 0.0078125f;
+  } else {
+    ew_values<OP, CH, VEC>(X, Y, operand_scale<I>(X, i, c, W), operand_scale<I>(Y, i, c, W), (size_t)(i * W + c), z);
+  }
 }
 
 // --------------------------------------------------------------------------
@@ -342,7 +362,7 @@ int grid_layout(const char* what, int64_t H, int64_t W, int64_t a, int64_t b, in
 
 QOperand operand(const uint8_t* q, const uint8_t* s8, const float* s32, int64_t a, int64_t b, int64_t K) {
   const bool flat = a == 1 && pow2(b) && pow2(K);
-  return QOperand{q, s8, s32, a, b, K, flat ? log2_of(b) : -1, flat ? log2_of(K) : -1};
+  return QOperand{q, s8, s32, a, b, K, flat ? log2_of(b) : -1, flat ? log2_of(K) : -1, nullptr, 0};
 }
 
 struct EwPlan {
@@ -514,5 +534,55 @@ extern "C" int pratchya_elementwise(int op, const uint8_t* x_fp8, const uint8_t*
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return pratchya_set_error(PRATCHYA_EHIP, "elementwise: launch failed: %s", hipGetErrorString(e));
+  return pratchya_set_error(PRATCHYA_OK, "");
+}
+
+extern "C" int pratchya_gather_quantize(const uint8_t* x_fp8, const uint8_t* x_sc8, const float* x_sc32, int64_t H,
+                                        int64_t W, int64_t xa, int64_t xb, const int64_t* idx, int64_t slices,
+                                        int64_t T, int64_t a, int64_t b, uint8_t* out_fp8, uint8_t* out_sc8,
+                                        float* out_sc32, void* workspace, size_t workspace_bytes,
+                                        hipStream_t stream) {
+  if (H < 0 || W < 0 || slices < 0 || T < 0)
+    return pratchya_set_error(PRATCHYA_EINVAL, "gather_quantize: negative shape");
+  int64_t tblk, tK, n_blk, K;
+  int rc = grid_layout("table", H, W, xa, xb, &tblk, &tK);
+  if (!rc) rc = grid_layout("result", T, W, a, b, &n_blk, &K);
+  if (rc) return rc;
+  const int64_t n = slices * T * W;
+  if (n == 0) return pratchya_set_error(PRATCHYA_OK, "");
+  if (H == 0) return pratchya_set_error(PRATCHYA_EINVAL, "gather_quantize: index into an empty table");
+  if (!x_fp8 || !x_sc8 || !x_sc32 || !idx || !out_fp8 || !out_sc8 || !out_sc32)
+    return pratchya_set_error(PRATCHYA_EINVAL, "gather_quantize: null buffer");
+  const int64_t n_blk_total = slices * n_blk, n_groups = n_blk_total / K;
+  const size_t need = (size_t)n_blk_total * sizeof(uint32_t);
+  if (!workspace || workspace_bytes < need)
+    return pratchya_set_error(PRATCHYA_EINVAL, "gather_quantize: workspace of %zu bytes needed, got %zu", need,
+                              workspace_bytes);
+  QOperand X = operand(x_fp8, x_sc8, x_sc32, xa, xb, tK);
+  X.rows = idx;
+  X.rows_h = H;
+  X.lb = X.lk = -1;
+  EwPlan p = plan(X, X, out_fp8, W, a, b, K);
+  if (p.one_pass) {                      // the row map needs the general path
+    p.one_pass = false;
+    const int64_t bb = gcd_i64(b, xb);
+    p.ch = 1;
+    while (p.ch < 16 && bb % (p.ch * 2) == 0) p.ch *= 2;
+    p.vec = p.ch >= 4 && is_aligned(x_fp8, p.ch) && is_aligned(out_fp8, p.ch);
+    p.rows = 1;
+    while (p.rows < 16 && a % (p.rows * 2) == 0) p.rows *= 2;
+    const int64_t seg = b / p.ch;
+    p.seg_log2 = (pow2(seg) && seg <= 64) ? log2_of(seg) : -1;
+  }
+  uint32_t* ws = static_cast<uint32_t*>(workspace);
+  if (n <= 0x7FFFFFFF)
+    launch_general<OP_GATHER, uint32_t>(X, X, out_fp8, out_sc8, out_sc32, ws, n, W, a, b, K, n_blk_total, n_groups,
+                                        p, stream);
+  else
+    launch_general<OP_GATHER, int64_t>(X, X, out_fp8, out_sc8, out_sc32, ws, n, W, a, b, K, n_blk_total, n_groups,
+                                       p, stream);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return pratchya_set_error(PRATCHYA_EHIP, "gather_quantize: launch failed: %s", hipGetErrorString(e));
   return pratchya_set_error(PRATCHYA_OK, "");
 }

@@ -724,9 +724,15 @@ class QArrayImpl:
             return QArrayImpl(self.get_value()[idx], quant=False)
         if (torch.is_tensor(idx) and not idx.is_floating_point() and idx.dtype != torch.bool
                 and self.__value.dim() == 2 and self.__value.dtype == E4M3):
-            # an embedding lookup: only the indexed rows are dequantized
-            sliced = _gather_dequantize(self.__value, self.__sc_fp8, self.__sc_fp32, self.__tgrid,
-                                        idx.to(self.__value.device))
+            # an embedding lookup: only the indexed rows are dequantized; without
+            # a gradient to route, the rows are requantized in the same pass
+            idx = idx.to(self.__value.device)
+            if _src(self.__value) is None:
+                grid = _adapted_grid(self.__tgrid, tuple(idx.shape) + (int(self.__value.shape[1]),))
+                return QArrayImpl._tree_unflatten(
+                    (True, grid), K.gather_quantize(self.__value, self.__sc_fp8, self.__sc_fp32, self.__tgrid,
+                                                    idx, grid))
+            sliced = _gather_dequantize(self.__value, self.__sc_fp8, self.__sc_fp32, self.__tgrid, idx)
         else:
             sliced = self.dequantize(torch.float32)[idx]
         return QArrayImpl(sliced, _adapted_grid(self.__tgrid, sliced.shape))

@@ -174,3 +174,36 @@ def test_floor_divide_follows_jnp_in_the_unfused_path(Q):
     b = np.array([[2.0, 2.0, 0.0, -2.0]], np.float32).repeat(32, 1)
     got = Q._floor_divide(to_dev_f32(a), to_dev_f32(b))
     assert_f32_bits_equal(f32(got), E.jnp_floor_divide(a, np.broadcast_to(b, a.shape)), "floor_divide")
+
+
+# ------------------------------------------------------------ embedding lookup
+@pytest.mark.parametrize("ids_shape,out_grid", [((2, 256), (128, 128)), ((384,), (128, 128)), ((3, 40), (8, 128)),
+                                                ((2, 256), (1, 128))])
+def test_gather_quantize_matches_oracle(K, ids_shape, out_grid):
+    """quantize_impl(dequantize_impl(table)[ids], grid) in one pass, ids with
+    negative and out-of-range entries (clamped as jnp's gather)."""
+    rng = np.random.default_rng(60)
+    table = (rng.standard_normal((512, 256)) * np.exp2(rng.integers(-3, 3, (512, 1)))).astype(np.float32)
+    tq = O.quantize_impl(table, (128, 128))
+    ids = rng.integers(-600, 700, ids_shape).astype(np.int64)
+    got = K.gather_quantize(*_dev(tq), (128, 128), torch.from_numpy(ids).cuda(), out_grid)
+    rows = np.clip(np.where(ids < 0, ids + 512, ids), 0, 511)
+    deq = O.dequantize_impl(*tq, "float32", (128, 128))[rows]
+    _check(got, O.quantize_impl(deq, out_grid), f"gather {ids_shape} -> {out_grid}")
+
+
+def test_getitem_fuses_the_requantization(Q, K, monkeypatch):
+    """QArrayImpl.__getitem__ with an index array (no gradient) gives the bytes
+    of the gather-then-quantize composition through the fused kernel."""
+    rng = np.random.default_rng(61)
+    table = torch.from_numpy(rng.standard_normal((512, 256)).astype(np.float32)).cuda()
+    qt = Q.QArrayImpl(table, (128, 128))
+    ids = torch.from_numpy(rng.integers(0, 512, (2, 128))).cuda()
+    calls = []
+    real = K.gather_quantize
+    monkeypatch.setattr(K, "gather_quantize", lambda *a, **k: calls.append(1) or real(*a, **k))
+    got = qt[ids]
+    assert len(calls) == 1 and got.tgrid == (128, 128)
+    v, s8, s32 = qt._tree_flatten()[0]
+    want = K.quantize(K.gather_dequantize(v, s8, s32, (128, 128), ids, torch.float32), (128, 128))
+    _check(_triple(got), (u8(want[0]), u8(want[1]), f32(want[2])), "getitem")

@@ -222,3 +222,19 @@ def test_elementwise_and_ns_combine_codes_without_gpu():
     assert c(None, None, None, -1, _lib.DT_F32, None) == _lib.EINVAL
     assert c(None, None, None, 0, _lib.DT_BF16, None) == _lib.OK
     assert c(None, None, None, 16, _lib.DT_BF16, None) == _lib.EINVAL
+
+
+def test_gather_quantize_codes_without_gpu():
+    """pratchya_gather_quantize validates grids, the table and buffers before
+    any launch."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    f = lib.pratchya_gather_quantize
+    # table grid (96, 128) does not divide [512, 256]; result grid (3, 128) does not divide [40, 256]
+    assert f(None, None, None, 512, 256, 96, 128, None, 1, 40, 8, 128, None, None, None, None, 0, None) == _lib.EINVAL
+    assert f(None, None, None, 512, 256, 128, 128, None, 1, 40, 3, 128, None, None, None, None, 0, None) == _lib.EINVAL
+    # nothing to look up; an empty table; null buffers; a missing workspace
+    assert f(None, None, None, 512, 256, 128, 128, None, 1, 0, 1, 128, None, None, None, None, 0, None) == _lib.OK
+    assert f(None, None, None, 0, 256, 1, 128, None, 1, 40, 8, 128, None, None, None, None, 0, None) == _lib.EINVAL
+    assert f(None, None, None, 512, 256, 128, 128, None, 1, 40, 8, 128, None, None, None, None, 0, None) == _lib.EINVAL
+    assert b"null buffer" in lib.pratchya_last_error()

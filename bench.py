@@ -79,49 +79,45 @@ def cpu_baseline_config1(reps: int = 5):
             "cores": 1, "kind": "port", "sample": f"full config 1, {reps} reps (NumPy, single thread)"}
 
 
-def cpu_baseline_config3(rows: int = 512):
-    """The oracle's config-3 forward -- dequantize both operands to f32 and
-    multiply (matmul_impl, Q:605-608) -- on a row sample of the activation,
-    on this host's BLAS threads."""
+def _gemm_host_sample(xq, wq, out, rows, n_blk_row):
+    """Host copies for a GEMM's CPU baseline and parity check: the quantized
+    activation's payload and scales on the sampled ``rows`` ((1,128) grid:
+    ``n_blk_row`` e8m0 bytes and n_blk_row/8 group maxima per row), the whole
+    quantized weight (payload [K, N], e8m0, group maxima), and the GPU
+    output's sampled rows as f32."""
+    import torch
+    ridx = torch.from_numpy(rows).cuda()
+    x8 = xq[0].view(torch.uint8)[ridx].cpu().numpy()
+    s8 = xq[1].view(torch.uint8).reshape(-1, n_blk_row)[ridx].cpu().numpy().reshape(-1, 8)
+    s32 = xq[2].reshape(-1, n_blk_row // 8)[ridx].cpu().numpy().reshape(-1, 1, 1)
+    w = tuple(t.view(torch.uint8).cpu().numpy() if t.dtype != torch.float32 else t.cpu().numpy() for t in wq)
+    c = out[ridx].float().cpu().numpy()
+    return {"rows": rows, "x": (x8, s8, s32), "w": w, "c": c}
+
+
+def cpu_baseline_gemm(sample, total_rows: int):
+    """The oracle's matmul_impl forward (Q:605-608) -- both operands
+    dequantized to f32 and multiplied -- on the GPU run's own quantized bytes
+    for a row sample of the activation, timed on this host's BLAS threads;
+    the GPU output's rows are checked against it (relative Frobenius error,
+    bf16 output tolerance 1e-2)."""
     from oracle import qarr_oracle as O
-    Kd, N = 2048, 8192
-    xq = O.quantize_impl(O.bf16_bits_to_f32(O.activation_input(rows, Kd, seed=2)), (1, 128))
-    wq = O.quantize_impl(O.bf16_bits_to_f32(O.normal_input((Kd, N), 0.02, seed=3)), (128, 128))
-    xd = O.dequantize_impl(*xq, "float32", (1, 128))
-    wd = O.dequantize_impl(*wq, "float32", (128, 128))
-    xd @ wd                                            # warm
+    rows = sample["rows"]
+    xd = O.dequantize_impl(*sample["x"], "float32", (1, 128))
+    wd = O.dequantize_impl(*sample["w"], "float32", (128, 128))
+    ref = xd @ wd                                      # warm
     t0 = time.perf_counter()
     reps = 3
     for _ in range(reps):
-        xd @ wd
+        ref = xd @ wd
     per = (time.perf_counter() - t0) / reps
-    tf = 2 * rows * Kd * N / per / 1e12
+    Kd, N = wd.shape
+    tf = 2 * len(rows) * Kd * N / per / 1e12
+    err = O.rel_fro(sample["c"], ref.astype(np.float64))
     return {"value": round(tf, 4), "unit": "TFLOP/s", "cores": _blas_threads(), "kind": "port",
-            "sample": f"f32 matmul of the dequantized operands, {rows} of 16384 rows, {reps} reps "
-                      f"(NumPy / OpenBLAS)"}
-
-
-def cpu_baseline_ffn(rows: int = 256):
-    """The oracle's d=4096 FFN forward, matmul_impl's f32 product of the
-    dequantized operands (Q:605-608), timed on a row sample of the
-    [32768, 4096] activation against a [4096, 16384] weight on this host's
-    BLAS threads.  The operands are f32 stand-ins of the dequantized arrays
-    (the product's cost does not depend on the values, and the NumPy quantizer
-    would take a minute on the 67M-element weight)."""
-    Kd, N = CFG5_D, CFG5_F
-    rng = np.random.default_rng(5)
-    xd = rng.standard_normal((rows, Kd), dtype=np.float32)
-    wd = rng.standard_normal((Kd, N), dtype=np.float32) * np.float32(0.02)
-    xd @ wd                                            # warm
-    t0 = time.perf_counter()
-    reps = 3
-    for _ in range(reps):
-        xd @ wd
-    per = (time.perf_counter() - t0) / reps
-    tf = 2 * rows * Kd * N / per / 1e12
-    return {"value": round(tf, 4), "unit": "TFLOP/s", "cores": _blas_threads(), "kind": "port",
-            "sample": f"f32 matmul of operands of the dequantized shapes, {rows} of {CFG5_TOKENS} "
-                      f"rows, {reps} reps (NumPy / OpenBLAS)"}
+            "sample": f"f32 matmul of the oracle-dequantized operands of this run, {len(rows)} of {total_rows} "
+                      f"rows, {reps} reps (NumPy / OpenBLAS)",
+            "parity_rel_fro_vs_oracle": float(f"{err:.3e}"), "parity_ok": bool(err <= 1e-2)}
 
 
 def cpu_baseline_config4(rows: int = 256):
@@ -203,12 +199,14 @@ def cpu_baseline_optimizer():
 MAX_GRAPH_STEPS = 256
 
 
-def timed_graph(step, steps: int, warmup: int):
+def timed_graph(step, steps: int, warmup: int, replays: int = 1):
     """Time exactly ``steps`` calls of ``step(i)``: the steps are captured in
     HIP graphs of up to MAX_GRAPH_STEPS launches (no host launch gaps and
     only one graph launch per MAX_GRAPH_STEPS steps), replayed between events
     recorded on the stream the kernels run on.  ``warmup`` eager steps and
-    one untimed replay come first.  Returns (ms per step, wall seconds)."""
+    one untimed replay come first.  With ``replays`` > 1 the timed region is
+    repeated that many times and the median is reported.  Returns (ms per
+    step, wall seconds of all timed regions)."""
     import torch
     for i in range(max(warmup, 1)):
         step(i)
@@ -228,16 +226,19 @@ def timed_graph(step, steps: int, warmup: int):
         g.replay()
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    per_step = []
     t0 = time.perf_counter()
-    e0.record(st)
-    for g, times in graphs:
-        for _ in range(times):
-            g.replay()
-    e1.record(st)
-    torch.cuda.synchronize()
+    for _ in range(max(1, replays)):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for g, times in graphs:
+            for _ in range(times):
+                g.replay()
+        e1.record(st)
+        torch.cuda.synchronize()
+        per_step.append(e0.elapsed_time(e1) / steps)
     wall = time.perf_counter() - t0
-    return e0.elapsed_time(e1) / steps, wall
+    return float(np.median(per_step)), wall
 
 
 def bench_quantize(steps: int, warmup: int):
@@ -323,51 +324,66 @@ def bench_config1(steps: int, warmup: int):
             "shape": "bf16 [1024,1024] -> (128,128) e4m3fn -> bf16"}
 
 
-def bench_gemm_fwd(steps: int, warmup: int):
+GEMM_LAUNCHES, GEMM_REPLAYS = 50, 5     # every GEMM leg: median of 5 timed replays of 50 launches
+
+
+def bench_gemm_fwd():
     """Config 3: A = quantize(cfg2 activation, (1,128)) [16384, 2048] x
     W = quantize(N(0, 0.02) [2048, 8192], (128,128)) -> bf16 [16384, 8192].
     The weight's K-contiguous payload copy is made once, outside the timed
-    region (a weight is quantized once per optimizer step).  Returns
-    (ms per GEMM, TFLOP/s)."""
+    region (a weight is quantized once per optimizer step).  Timed as the
+    median of GEMM_REPLAYS replays of GEMM_LAUNCHES launches (fixed counts,
+    independent of --steps).  Returns (ms per GEMM, TFLOP/s, host sample for
+    the CPU baseline and parity check)."""
     import torch
     from oracle import qarr_oracle as O
     from pratchya_amd import _kernels as K
     M, Kd, N = 16384, 2048, 8192
     x = torch.from_numpy(O.activation_input(M, Kd, seed=2).view(np.int16)).view(torch.bfloat16).cuda()
     w = torch.from_numpy(O.normal_input((Kd, N), 0.02, seed=3).view(np.int16)).view(torch.bfloat16).cuda()
-    a = K.operand_rows(*K.quantize(x, (1, 128)), (1, 128))
-    b = K.operand_transposed(*K.quantize(w, (128, 128)), (128, 128))
+    xq = K.quantize(x, (1, 128))
+    wq = K.quantize(w, (128, 128))
+    a = K.operand_rows(*xq, (1, 128))
+    b = K.operand_transposed(*wq, (128, 128))
     outs = [torch.empty((M, N), dtype=torch.bfloat16, device="cuda") for _ in range(2)]
 
     def step(i):
         K.gemm_nt(a, b, out=outs[i % 2])
 
-    ms, _ = timed_graph(step, steps, warmup)
-    return ms, 2.0 * M * N * Kd / (ms * 1e-3) / 1e12
+    ms, _ = timed_graph(step, GEMM_LAUNCHES, 4, GEMM_REPLAYS)
+    rows = np.sort(np.random.default_rng(3).choice(M, 256, replace=False))
+    sample = _gemm_host_sample(xq, wq, outs[(GEMM_LAUNCHES - 1) % 2], rows, Kd // 128)
+    return ms, 2.0 * M * N * Kd / (ms * 1e-3) / 1e12, sample
 
 
-def bench_gemm_ffn(steps: int, warmup: int):
+def bench_gemm_ffn():
     """The GEMM target's shape: config 5's d=4096 FFN up-projection forward,
     A = quantize(x, (1,128)) [32768, 4096] x W = quantize(N(0, 0.02)
     [4096, 16384], (128,128)) -> bf16 [32768, 16384] (synthetic x ~ N(0,1),
-    seed 5).  Returns a dict with TFLOP/s and the fraction of dense FP8 peak,
-    beside hipBLASLt's unscaled FP8 GEMM at the same shape."""
+    seed 5; the weight has four group maxima).  Median of GEMM_REPLAYS
+    replays of 20 launches.  Returns (a dict with TFLOP/s and the fraction of
+    dense FP8 peak, beside hipBLASLt's unscaled FP8 GEMM at the same shape;
+    host sample for the CPU baseline and parity check)."""
     import torch
     from pratchya_amd import _kernels as K
     M, Kd, N = CFG5_TOKENS, CFG5_D, CFG5_F
     gen = torch.Generator(device="cuda").manual_seed(5)
     x = torch.randn((M, Kd), generator=gen, device="cuda").to(torch.bfloat16)
     w = (torch.randn((Kd, N), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
-    a = K.operand_rows(*K.quantize(x, (1, 128)), (1, 128))
-    b = K.operand_transposed(*K.quantize(w, (128, 128)), (128, 128))
+    xq = K.quantize(x, (1, 128))
+    wq = K.quantize(w, (128, 128))
+    a = K.operand_rows(*xq, (1, 128))
+    b = K.operand_transposed(*wq, (128, 128))
     del x, w
     out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-    ms, _ = timed_graph(lambda i: K.gemm_nt(a, b, out=out), steps, warmup)
+    ms, _ = timed_graph(lambda i: K.gemm_nt(a, b, out=out), 20, 2, GEMM_REPLAYS)
+    rows = np.sort(np.random.default_rng(5).choice(M, 128, replace=False))
+    sample = _gemm_host_sample(xq, wq, out, rows, Kd // 128)
     flop = 2 * M * N * Kd
     tf = flop / (ms * 1e-3) / 1e12
     return {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1), "frac_of_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4),
-            "flop": flop, "shape": f"[{M},{Kd}] x [{Kd},{N}] -> bf16",
-            "hipblaslt_fp8_no_block_scales": bench_library_fp8(10, (M, Kd, N))}
+            "flop": flop, "shape": f"[{M},{Kd}] x [{Kd},{N}] -> bf16", "launches": f"median of {GEMM_REPLAYS} x 20",
+            "hipblaslt_fp8_no_block_scales": bench_library_fp8(10, (M, Kd, N))}, sample
 
 
 def bench_library_fp8(steps: int, shape=(16384, 2048, 8192)):
@@ -391,13 +407,14 @@ def bench_library_fp8(steps: int, shape=(16384, 2048, 8192)):
             "call": "torch._scaled_mm, tensor-wise scales (hipBLASLt)"}
 
 
-def bench_config4(steps: int, warmup: int):
+def bench_config4():
     """Config 4, the backward of config 3's Linear: dY bf16 [16384, 8192] ~
     N(0, 1e-3) (seed 4) requantized (1, 128) for dgrad and (128, 1) along
     tokens for wgrad; the stored activation A (config 2, (1, 128)) requantized
     (128, 1) from its fp8 payload; dgrad = q(dY) . W^T -> f32 [16384, 2048],
     wgrad = q(A)^T . q(dY) -> f32 [2048, 8192].  Each kernel is timed on its
-    own; requant bytes and GEMM FLOPs are the algorithmic counts."""
+    own (median of 5 timed replays of 50 launches; dY rotates through two
+    copies); requant bytes and GEMM FLOPs are the algorithmic counts."""
     import torch
     from oracle import qarr_oracle as O
     from pratchya_amd import _kernels as K
@@ -411,6 +428,8 @@ def bench_config4(steps: int, warmup: int):
     op_w = K.operand_rows(*wq, (128, 128))               # W [2048, 8192]: rows Din, contraction Dout
     dyq = K.quantize(dy, (1, 128))
     dyt = K.quantize_t128(dy)
+    # the 268 MB dY rotates through two copies (537 MB > the 256 MB MALL)
+    dys = [dy, dy.clone()]
     at = K.quantize_t128(*a8)
     op_dy, op_dyt, op_at = K.operand_rows(*dyq, (1, 128)), K.operand_t128(*dyt), K.operand_t128(*at)
     gx = torch.empty((T, Din), dtype=torch.float32, device="cuda")
@@ -425,16 +444,16 @@ def bench_config4(steps: int, warmup: int):
     res = {}
     e_dy, e_a = T * Dout, T * Din
     cases = [
-        ("requant_dy_1x128", lambda i: K.quantize(dy, (1, 128), out=dyq_out),
+        ("requant_dy_1x128", lambda i: K.quantize(dys[i % 2], (1, 128), out=dyq_out),
          e_dy * 3 + e_dy // 128 + e_dy // 1024 * 4),
-        ("requant_dy_128x1_t", lambda i: K.quantize_t128(dy, out=dyt_out),
+        ("requant_dy_128x1_t", lambda i: K.quantize_t128(dys[i % 2], out=dyt_out),
          e_dy * 3 + e_dy // 128 + e_dy // 1024 * 4),
         ("requant_a_fp8_to_128x1_t", lambda i: K.quantize_t128(*a_sets[i % n_a], out=at_outs[i % n_a]),
          e_a * 2 + 2 * (e_a // 128 + e_a // 1024 * 4)),
     ]
     for name, fn, nbytes in cases:
         _log(f"config 4 {name}: start")
-        ms, _ = timed_graph(fn, steps, warmup)
+        ms, _ = timed_graph(fn, 50, 4, 5)
         gbs = nbytes / (ms * 1e-3) / 1e9
         res[name] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                      "bytes": nbytes}
@@ -442,7 +461,7 @@ def bench_config4(steps: int, warmup: int):
     for name, fn in (("dgrad_gemm", lambda i: K.gemm_nt(op_dy, op_w, out=gx)),
                      ("wgrad_gemm", lambda i: K.gemm_nt(op_at, op_dyt, out=gw))):
         _log(f"config 4 {name}: start")
-        ms, _ = timed_graph(fn, max(8, steps // 4), max(2, warmup // 4))
+        ms, _ = timed_graph(fn, GEMM_LAUNCHES, 4, GEMM_REPLAYS)
         tf = flop / (ms * 1e-3) / 1e12
         res[name] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1), "frac_of_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4),
                      "flop": flop}
@@ -454,7 +473,7 @@ CFG5_LINEARS = [(CFG5_D, CFG5_D)] * 4 + [(CFG5_D, CFG5_F), (CFG5_F, CFG5_D)]   #
 CFG5_FLOP = 3 * 2 * CFG5_TOKENS * sum(a * b for a, b in CFG5_LINEARS)
 
 
-def bench_config5(steps: int, warmup: int):
+def bench_config5(steps: int = 10, warmup: int = 2):
     """Config 5: the six quantized linears of one RWKV-7 block at d_model 4096
     (r/k/v/o [4096, 4096], FFN [4096, 16384] and [16384, 4096]) over 32768
     tokens (batch 8 x seq 4096): forward, dgrad and wgrad of each through the
@@ -462,7 +481,8 @@ def bench_config5(steps: int, warmup: int):
     (x quantized (1, 128), W (128, 128), output requantized and dequantized to
     bf16, cotangents requantized), with the FP8 MFMA backward.  Synthetic bf16
     activations N(0, 1), weights N(0, 0.02), output cotangents N(0, 1e-3),
-    seed 5.  A step is one layer's fwd + bwd; reported as tokens/s."""
+    seed 5.  A step is one layer's fwd + bwd; the median of ``steps`` (10)
+    event-timed steps is reported as tokens/s."""
     import torch
     from pratchya_amd import qarr as Q
     prev = Q.get_matmul_backward()
@@ -490,19 +510,19 @@ def bench_config5(steps: int, warmup: int):
             layer_step()
         torch.cuda.synchronize()
         st = torch.cuda.current_stream()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(st)
-        for _ in range(steps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        ev[0].record(st)
+        for i in range(steps):
             layer_step()
-        e1.record(st)
+            ev[i + 1].record(st)
         torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / steps
+        ms = float(np.median([ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]))
     finally:
         Q.set_matmul_backward(prev)
     tf = CFG5_FLOP / (ms * 1e-3) / 1e12
     return {"tokens_per_s": round(CFG5_TOKENS / (ms * 1e-3), 1), "ms_per_layer_step": round(ms, 3),
             "effective_TFLOP/s": round(tf, 1), "frac_of_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4),
-            "gemm_flop_per_step": CFG5_FLOP, "steps": steps,
+            "gemm_flop_per_step": CFG5_FLOP, "steps": f"median of {steps}",
             "path": "pratchya_amd.qarr Linear composition, fp8 backward, eager (no graph)"}
 
 
@@ -853,12 +873,12 @@ def main():
         return
     if args.only:
         if args.only == "cfg3":
-            ms_, tf_ = bench_gemm_fwd(max(8, args.steps // 4), max(4, args.warmup // 4))
+            ms_, tf_, _ = bench_gemm_fwd()
             res = {"ms": ms_, "TFLOP/s": tf_}
         elif args.only == "cfg4":
-            res = bench_config4(max(20, args.steps // 4), max(4, args.warmup // 4))
+            res = bench_config4()
         elif args.only == "ffn":
-            res = bench_gemm_ffn(max(8, args.steps // 10), 2)
+            res = bench_gemm_ffn()[0]
         elif args.only == "optim":
             res = bench_optimizer(3)
         elif args.only == "elementwise":
@@ -866,7 +886,7 @@ def main():
         elif args.only == "embedding":
             res = bench_embedding(max(20, args.steps // 4), max(4, args.warmup // 4))
         else:
-            res = bench_config5(max(3, args.steps // 40), 2)
+            res = bench_config5()
         print(json.dumps({args.only: res}), flush=True)
         return
     _log("config 2 quantize: start")
@@ -885,20 +905,21 @@ def main():
     _log(f"elementwise add: {extra['elementwise_add']['us']} us")
     if not args.no_gemm:
         _log("config 3 gemm fwd: start")
-        gms, tflops = bench_gemm_fwd(max(8, args.steps // 4), max(4, args.warmup // 4))
+        gms, tflops, cfg3_sample = bench_gemm_fwd()
         _log(f"config 3 gemm fwd: {gms * 1e3:.1f} us, {tflops:.1f} TFLOP/s")
         extra["config3_gemm_fwd"] = {"value": round(tflops, 1), "unit": "TFLOP/s", "ms": round(gms, 4),
                                      "frac_of_fp8_peak": round(tflops / FP8_PEAK_TFLOPS, 4),
                                      "shape": "[16384,2048] x [2048,8192] -> bf16",
                                      "flop": 2 * 16384 * 2048 * 8192,
+                                     "launches": f"median of {GEMM_REPLAYS} x {GEMM_LAUNCHES}",
                                      "hipblaslt_fp8_no_block_scales": bench_library_fp8(20)}
         _log("d=4096 FFN gemm fwd: start")
-        extra["ffn_d4096_gemm_fwd"] = bench_gemm_ffn(max(8, args.steps // 10), 2)
+        extra["ffn_d4096_gemm_fwd"], ffn_sample = bench_gemm_ffn()
         _log(f"d=4096 FFN gemm fwd: {extra['ffn_d4096_gemm_fwd']['TFLOP/s']} TFLOP/s")
         _log("config 4: start")
-        extra["config4_backward"] = bench_config4(max(20, args.steps // 4), max(4, args.warmup // 4))
+        extra["config4_backward"] = bench_config4()
         _log("config 5: start")
-        extra["config5_layer"] = bench_config5(max(3, args.steps // 40), 2)
+        extra["config5_layer"] = bench_config5()
         _log(f"config 5: {extra['config5_layer']['tokens_per_s']} tokens/s")
         _log("optimizer step: start")
         extra["optimizer_step"] = bench_optimizer(3)
@@ -912,8 +933,8 @@ def main():
         extra["elementwise_add"]["cpu_baseline"] = cpu_baseline_elementwise()
         extra["embedding_lookup"]["cpu_baseline"] = cpu_baseline_embedding()
         if "config3_gemm_fwd" in extra:
-            extra["config3_gemm_fwd"]["cpu_baseline"] = cpu_baseline_config3()
-            extra["ffn_d4096_gemm_fwd"]["cpu_baseline"] = cpu_baseline_ffn()
+            extra["config3_gemm_fwd"]["cpu_baseline"] = cpu_baseline_gemm(cfg3_sample, 16384)
+            extra["ffn_d4096_gemm_fwd"]["cpu_baseline"] = cpu_baseline_gemm(ffn_sample, CFG5_TOKENS)
             extra["config4_backward"]["cpu_baseline"] = cpu_baseline_config4()
             extra["config5_layer"]["cpu_baseline"] = cpu_baseline_config5()
             extra["optimizer_step"]["cpu_baseline"] = cpu_baseline_optimizer()

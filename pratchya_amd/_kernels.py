@@ -107,6 +107,8 @@ def quantize(x: torch.Tensor, tgrid, out=None) -> Tuple[torch.Tensor, torch.Tens
     lib = _lib.load()
     code = _dtype_code(x.dtype)
     ws_bytes = lib.pratchya_quantize_workspace_bytes(code, S, H, W, a, b)
+    if ws_bytes == 0 and not _aligned(x8, 8 if x.dtype == torch.bfloat16 else 4):
+        ws_bytes = S * n_blk * 4      # a misaligned caller payload buffer: the general path runs
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device) if ws_bytes else None
     _lib.check(lib.pratchya_quantize(_ptr(x), code, S, H, W, a, b, _ptr(x8), _ptr(sc8), _ptr(sc32),
                                      _ptr(ws) if ws is not None else None, ws_bytes, _stream(x)), "quantize")

@@ -80,11 +80,7 @@ PFN uint32_t bf16_to_e4m3fn(uint32_t h) {
     code = code > 0x7Fu ? 0x7Fu : code;
   } else {                              // e4m3 subnormal: multiples of 2^-9
     float v = u2f(mag << 16) * 512.0f;  // exact: < 8 with <= 8 significant bits
-#if defined(__HIP_DEVICE_COMPILE__)
     code = (uint32_t)__builtin_rintf(v);
-#else
-    code = (uint32_t)__builtin_rintf(v);
-#endif
   }
   return code | sign;
 }

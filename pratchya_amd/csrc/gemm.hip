@@ -750,7 +750,9 @@ namespace {
 __global__ __launch_bounds__(256) void k_transpose_u8(const uint8_t* __restrict__ src, int64_t rows,
                                                       int64_t cols, uint8_t* __restrict__ dst) {
   __shared__ uint32_t tile[64][17];   // 64 rows x 64 bytes (+1 word pad)
-  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  // one-dimensional grid over the 64x64 tiles (no 65535 limit on either axis)
+  const int64_t tiles_c = cols / 64;
+  const int64_t r0 = ((int64_t)blockIdx.x / tiles_c) * 64, c0 = ((int64_t)blockIdx.x % tiles_c) * 64;
   const int t = threadIdx.x;
   {
     const int r = t >> 2, q = t & 3;   // row r, 16-byte quarter q
@@ -791,8 +793,9 @@ extern "C" int pratchya_transpose_u8(const uint8_t* src, int64_t rows, int64_t c
   if (rows % 64 || cols % 64 || reinterpret_cast<uintptr_t>(src) % 16 || reinterpret_cast<uintptr_t>(dst) % 16)
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "transpose: sizes must be multiples of 64, buffers 16-byte aligned");
   if (!src || !dst) return pratchya_set_error(PRATCHYA_EINVAL, "transpose: null buffer");
-  hipLaunchKernelGGL(k_transpose_u8, dim3((unsigned)(cols / 64), (unsigned)(rows / 64)), dim3(256), 0,
-                     stream, src, rows, cols, dst);
+  const int64_t tiles = (rows / 64) * (cols / 64);
+  if (tiles > INT32_MAX) return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "transpose: more than 2^31 64x64 tiles");
+  hipLaunchKernelGGL(k_transpose_u8, dim3((unsigned)tiles), dim3(256), 0, stream, src, rows, cols, dst);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return pratchya_set_error(PRATCHYA_EHIP, "transpose: %s", hipGetErrorString(e));
   return PRATCHYA_OK;

@@ -850,8 +850,10 @@ class _LazyProduct(QArrayImpl):
     the step-by-step composition.  Any other use (payload, scales, slicing,
     arithmetic, pytree flattening) first materialises the quantized array
     exactly as the reference builds it, after which the object behaves as a
-    plain QArrayImpl.  Repeated dequantizations to one dtype before that return
-    the same tensor."""
+    plain QArrayImpl.  Repeated dequantizations to one dtype before that run
+    the product once and return copies of its result; if the first result was
+    changed in place (impossible on the reference's immutable arrays), the
+    product is run again, so no returned tensor sees another's changes."""
 
     _FIELDS = ("_QArrayImpl__value", "_QArrayImpl__sc_fp8", "_QArrayImpl__sc_fp32")
 
@@ -887,8 +889,8 @@ class _LazyProduct(QArrayImpl):
         if "_operands" not in self.__dict__ or dtype not in (torch.float32, torch.bfloat16):
             return super().dequantize(dtype)
         hit = self._dequantized.get(dtype)
-        if hit is not None:
-            return hit
+        if hit is not None and hit[0]._version == hit[1]:
+            return hit[0].clone()
         x8, xs8, xs32, y8, ys8, ys32 = self._operands
         gx, gy = self._grids
         go = self._QArrayImpl__tgrid
@@ -899,7 +901,7 @@ class _LazyProduct(QArrayImpl):
             else:
                 out = _matmul_forward(x8, xs8, xs32, y8, ys8, ys32, gx, gy)
                 res = K.quantize_dequantize(out, go, dtype)[0]
-        self._dequantized[dtype] = res
+        self._dequantized[dtype] = (res, res._version)   # recomputed if changed in place
         return res
 
     @property

@@ -61,6 +61,18 @@ def test_workspace_query():
     assert lib.pratchya_quantize_workspace_bytes(_lib.DT_BF16, 1, 2048, 8192, 128, 128) == 1024 * 4
 
 
+def test_transpose_arguments_without_gpu():
+    """Argument checks of pratchya_transpose_u8 return before any launch."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)          # aligned, never dereferenced
+    assert lib.pratchya_transpose_u8(fake, 0, 64, fake, None) == 0
+    assert lib.pratchya_transpose_u8(fake, 96, 64, fake, None) == _lib.EUNSUPPORTED
+    assert lib.pratchya_transpose_u8(None, 64, 64, None, None) == _lib.EINVAL
+    assert lib.pratchya_transpose_u8(fake, 64 << 31, 128, fake, None) == _lib.EUNSUPPORTED
+    assert b"2^31" in lib.pratchya_last_error()
+
+
 def test_invalid_tgrid_is_einval_without_launch():
     from pratchya_amd import _lib
     lib = _lib.load()

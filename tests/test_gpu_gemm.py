@@ -94,6 +94,16 @@ def test_transpose_u8():
     assert np.array_equal(t.cpu().numpy(), x.T)
 
 
+def test_transpose_u8_tall():
+    """More than 65535 row tiles: the tile index runs on one grid axis."""
+    K = _K()
+    rows = 65600 * 64
+    x = torch.randint(0, 256, (rows, 64), dtype=torch.uint8, device="cuda")
+    t = K.transpose_u8(x)
+    torch.cuda.synchronize()
+    assert torch.equal(t, x.t().contiguous())
+
+
 def test_dgrad_shape():
     """g (1,128) @ W^T: W [K_out, N] read as B rows without a transpose."""
     K = _K()

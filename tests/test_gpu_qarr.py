@@ -210,12 +210,28 @@ def test_fused_linear_matches_materialised_composition(Q, mode, xdtype):
             prod.get_value()
         y = prod.astype(dt)
         if not materialise:
-            assert y is prod.astype(dt)          # one node per dtype
+            y2 = prod.astype(dt)                 # one product per dtype, returned as a copy
+            assert y2 is not y and torch.equal(y2, y)
         y.backward(to_dev_bf16(gb).to(dt))
         assert x.grad.dtype == dt and w.grad.dtype == torch.bfloat16
         results.append([t.detach().float().cpu().numpy() for t in (y, x.grad, w.grad)])
     for a, b, what in zip(results[0], results[1], ("y", "x.grad", "w.grad")):
         assert_f32_bits_equal(a, b, f"fused vs materialised {what} ({mode}, {xdtype})")
+
+
+def test_lazy_product_results_are_independent(Q):
+    """A second dequantization of a lazy product is not changed by an in-place
+    change of the first (jnp arrays are immutable; torch tensors are not)."""
+    xb, wb, _ = _linear_case(seed=15, M=256, Kd=256, N=256)
+    with torch.no_grad():
+        prod = Q.QArrayImpl(to_dev_bf16(xb), (1, 128)) @ Q.QArrayImpl(to_dev_bf16(wb), (128, 128))
+        y1 = prod.astype(torch.bfloat16)
+        want = y1.clone()
+        y1.add_(1.0)
+        y2 = prod.astype(torch.bfloat16)
+        assert torch.equal(y2, want)
+        y2.mul_(2.0)
+        assert torch.equal(prod.astype(torch.bfloat16), want)
 
 
 def test_fused_linear_without_grad(Q):

@@ -74,6 +74,21 @@ int pratchya_quantize(const void* x, int x_dtype, int64_t slices, int64_t H, int
                       int64_t a, int64_t b, uint8_t* x_fp8, uint8_t* sc_fp8, float* sc_fp32,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Allocation-free pratchya_quantize.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, results and errors as pratchya_quantize without the workspace:
+ * layouts that need one use a file-scope device array of
+ * pratchya_quantize_noalloc_max_bytes() bytes (16 MiB: 4 Mi blocks; larger
+ * layouts fail with PRATCHYA_EUNSUPPORTED), one per device, kept until the
+ * process ends.  It allocates nothing and calls no allocating routine.  All
+ * calls on one device share that array: calls that overlap on one device
+ * (different streams or threads) race. */
+int pratchya_quantize_noalloc(const void* x, int x_dtype, int64_t slices, int64_t H, int64_t W,
+                              int64_t a, int64_t b, uint8_t* x_fp8, uint8_t* sc_fp8, float* sc_fp32,
+                              hipStream_t stream);
+size_t pratchya_quantize_noalloc_max_bytes(void);
+
 /* Fake quantization in one pass (no payload is written):
  *   out = dequantize_impl(*quantize_impl(x, tgrid), out_dtype, tgrid)
  * the value of QArrayImpl(x, tgrid).astype(dtype) (Q:339-342 -> Q:458-506,

@@ -30,6 +30,9 @@ SIGNATURES = {
     "pratchya_quantize_workspace_bytes": (ctypes.c_size_t, [_c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
     "pratchya_quantize": (_c_int, [_c_p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                    _c_p, _c_p, _c_p, _c_p, ctypes.c_size_t, _c_p]),
+    "pratchya_quantize_noalloc": (_c_int, [_c_p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                           _c_p, _c_p, _c_p, _c_p]),
+    "pratchya_quantize_noalloc_max_bytes": (ctypes.c_size_t, []),
     "pratchya_quantize_dequantize_workspace_bytes": (ctypes.c_size_t, [_c_int, _c_i64, _c_i64, _c_i64,
                                                                        _c_i64, _c_i64]),
     "pratchya_quantize_dequantize": (_c_int, [_c_p, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,

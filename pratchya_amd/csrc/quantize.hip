@@ -22,6 +22,7 @@
 // and redoes the wave with exact division if any element is within 4 ulp.
 // Blocks whose S was clamped or is not finite always take the exact path.
 #include <hip/hip_runtime.h>
+#include <pthread.h>
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -1264,4 +1265,77 @@ extern "C" int pratchya_debug_f32_to_bf16(const float* in, uint16_t* out, int64_
   else
     hipLaunchKernelGGL(k_dbg_f32_bf16<false>, dim3(grid_for(n, 256)), dim3(256), 0, stream, in, out, n);
   return check_launch("debug_f32_to_bf16");
+}
+
+// --------------------------------------------------------------------------
+// Allocation-free quantize: pratchya_quantize with the general path's block
+// maxima in a file-scope device array instead of a caller workspace, for
+// callers that cannot allocate device memory (HIP graph capture, serving
+// loops).  Each device holds its own copy of the array for the life of the
+// process; every call on one device shares it (the general path clears the
+// words it uses with a fill kernel first), so calls that overlap on one
+// device race.
+// --------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;   // 4 Mi block maxima
+static __device__ __align__(256) uint32_t scratch[kNoAllocScratchBytes / sizeof(uint32_t)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
+pthread_mutex_t g_scratch_mu = PTHREAD_MUTEX_INITIALIZER;
+
+// Device address of the current device's scratch array, resolved once per
+// device with that device current (the array's name is a host-side stand-in
+// and must never be passed to a kernel).
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return pratchya_set_error(PRATCHYA_EHIP, "quantize_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_noalloc: device %d beyond %d", dev, kMaxDevices);
+  pthread_mutex_lock(&g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      pthread_mutex_unlock(&g_scratch_mu);
+      return pratchya_set_error(PRATCHYA_EHIP, "quantize_noalloc: hipGetSymbolAddress: %s",
+                                hipGetErrorString(e));
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  pthread_mutex_unlock(&g_scratch_mu);
+  return PRATCHYA_OK;
+}
+}  // namespace
+
+extern "C" size_t pratchya_quantize_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int pratchya_quantize_noalloc(const void* x, int x_dtype, int64_t slices, int64_t H, int64_t W,
+                                         int64_t a, int64_t b, uint8_t* x_fp8, uint8_t* sc_fp8,
+                                         float* sc_fp32, hipStream_t stream) {
+  Layout L;
+  int rc = make_layout(slices, H, W, a, b, &L);
+  if (rc) return rc;
+  if (x_dtype != PRATCHYA_DT_F32 && x_dtype != PRATCHYA_DT_BF16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_noalloc: unsupported input dtype %d", x_dtype);
+  if (L.n() == 0 || !x || !x_fp8 || !sc_fp8 || !sc_fp32)   // no-ops and argument errors as pratchya_quantize
+    return pratchya_quantize(x, x_dtype, slices, H, W, a, b, x_fp8, sc_fp8, sc_fp32, nullptr, 0, stream);
+  const bool bf16 = x_dtype == PRATCHYA_DT_BF16;
+  RowGroupPlan p;
+  if (use_g8(L, bf16, x, x_fp8, sc_fp8) || plan_rowgroup(L, bf16, x, x_fp8, &p))   // single pass, no scratch
+    return pratchya_quantize(x, x_dtype, slices, H, W, a, b, x_fp8, sc_fp8, sc_fp32, nullptr, 0, stream);
+  const size_t need = (size_t)(L.S * L.n_blk) * sizeof(uint32_t);
+  if (need > kNoAllocScratchBytes)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED,
+                              "quantize_noalloc: %lld blocks need %zu bytes of scratch, the maximum is %zu "
+                              "(use pratchya_quantize with a workspace)",
+                              (long long)(L.S * L.n_blk), need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  rc = scratch_address(&ws);
+  if (rc) return rc;
+  return pratchya_quantize(x, x_dtype, slices, H, W, a, b, x_fp8, sc_fp8, sc_fp32, ws, kNoAllocScratchBytes,
+                           stream);
 }

@@ -73,6 +73,23 @@ def test_transpose_arguments_without_gpu():
     assert b"2^31" in lib.pratchya_last_error()
 
 
+def test_noalloc_quantize_arguments_without_gpu():
+    """pratchya_quantize_noalloc rejects layouts beyond its scratch array and
+    bad arguments before any HIP call."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)          # aligned, never dereferenced
+    n = 2049 * 128                           # (128,128): 2049^2 blocks > 4 Mi
+    assert lib.pratchya_quantize_noalloc(fake, _lib.DT_BF16, 1, n, n, 128, 128, fake, fake, fake,
+                                         None) == _lib.EUNSUPPORTED
+    assert b"maximum" in lib.pratchya_last_error()
+    assert lib.pratchya_quantize_noalloc(None, _lib.DT_F32, 1, 10, 10, 3, 5, None, None, None, None) == _lib.EINVAL
+    assert lib.pratchya_quantize_noalloc(None, 9, 1, 8, 8, 1, 8, None, None, None, None) == _lib.EINVAL
+    assert lib.pratchya_quantize_noalloc(None, _lib.DT_F32, 1, 0, 128, 1, 128, None, None, None, None) == 0
+    assert lib.pratchya_quantize_noalloc(None, _lib.DT_F32, 1, 128, 128, 128, 128, None, None, None,
+                                         None) == _lib.EINVAL
+
+
 def test_invalid_tgrid_is_einval_without_launch():
     from pratchya_amd import _lib
     lib = _lib.load()

@@ -259,10 +259,16 @@ int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t* x_sc8, con
  * so that an operand quantized as [rows, K] with tgrid (a, 128) is
  * (rdiv, sr, sk, kg) = (a, K/128, 1, K_group), and one quantized as [K, rows]
  * with tgrid (128, b) and transposed is (b, 1, rows/b, K_group).
- * C: [M, N] with row stride ldc elements, c_dtype f32 or bf16.
- * M and N must be multiples of 256 and K of 128 (PRATCHYA_EUNSUPPORTED
- * otherwise).  Any group layout is accepted: the kernel reloads group maxima
- * wherever some row's group changes along K (see pratchya_gemm_span). */
+ * C: [M, N] with row stride ldc elements (a multiple of 4 for f32, 8 for
+ * bf16), c_dtype f32 or bf16; only the M x N outputs are written.
+ * K must be a multiple of 128 (PRATCHYA_EUNSUPPORTED otherwise); M and N are
+ * any sizes, except that an N below 256 must be a multiple of 4 (f32) or 8
+ * (bf16).  An operand of fewer than 256 rows is read as 256 rows: its buffer
+ * must be readable that far (the extra rows' contents only reach outputs that
+ * are not stored).  The e8m0 arrays are read in aligned 4-byte words: each
+ * must be readable up to the next multiple of 4 bytes.  Any group layout is
+ * accepted: the kernel reloads group maxima wherever some row's group changes
+ * along K (see pratchya_gemm_span). */
 int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, const float* a_sc32,
                         int64_t a_rdiv, int64_t a_sr, int64_t a_sk, int64_t a_kg,
                         const uint8_t* B, int64_t ldb, const uint8_t* b_sc8, const float* b_sc32,
@@ -279,7 +285,7 @@ int64_t pratchya_gemm_span(int64_t rows, int64_t K, int64_t r_div, int64_t s_r, 
 
 /* Byte transpose of an fp8 payload: src [rows, cols] -> dst [cols, rows]
  * (the K-contiguous operand layout the GEMM reads; QArrayImpl.T, Q:349-352,
- * moves the data the same way).  rows and cols multiples of 64. */
+ * moves the data the same way).  rows and cols multiples of 16. */
 int pratchya_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* dst,
                           hipStream_t stream);
 

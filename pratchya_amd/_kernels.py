@@ -481,15 +481,50 @@ def transpose_u8(x8: torch.Tensor) -> torch.Tensor:
     return out.view(x8.dtype) if x8.dtype != torch.uint8 else out
 
 
+GEMM_TILE_ROWS = 256
+
+
+def _tile_readable(p: torch.Tensor) -> torch.Tensor:
+    """A [rows, K] payload whose buffer is readable for at least
+    GEMM_TILE_ROWS rows: the kernel reads an operand of fewer rows as one full
+    tile (rows beyond ``rows`` feed only outputs that are not stored).  A
+    payload whose storage already extends that far is used in place; a
+    shorter one is copied into a zero-padded buffer."""
+    rows, K = int(p.shape[0]), int(p.shape[1])
+    if rows >= GEMM_TILE_ROWS:
+        return p
+    avail = p.untyped_storage().nbytes() - p.storage_offset() * p.element_size()
+    if avail >= GEMM_TILE_ROWS * K:
+        return p
+    padded = torch.zeros((GEMM_TILE_ROWS, K), dtype=p.dtype, device=p.device)
+    padded[:rows].copy_(p)
+    return padded[:rows]
+
+
+def _word_readable(e8: torch.Tensor) -> torch.Tensor:
+    """An e8m0 array readable up to the next multiple of 4 bytes (the GEMM
+    reads each byte as the aligned word that holds it): used in place when its
+    storage extends that far, else copied into a padded buffer."""
+    n = e8.numel()
+    need = (n + 3) & ~3
+    avail = e8.untyped_storage().nbytes() - e8.storage_offset()
+    if avail >= need:
+        return e8
+    padded = torch.zeros(need, dtype=torch.uint8, device=e8.device)
+    padded[:n].copy_(e8.reshape(-1))
+    return padded[:n]
+
+
 def gemm_nt(a: Operand, b: Operand, out_dtype: torch.dtype = torch.bfloat16,
             out: torch.Tensor = None) -> torch.Tensor:
-    """C[M, N] = dequant(a) @ dequant(b)^T on the FP8 MFMA kernel."""
+    """C[M, N] = dequant(a) @ dequant(b)^T on the FP8 MFMA kernel (any M, N;
+    K a multiple of 128)."""
     _require_gpu(a.payload, b.payload)
     if a.k != b.k:
         raise ValueError(f"contraction mismatch: {a.k} vs {b.k}")
     M, N, K = a.rows, b.rows, a.k
-    ap, bp = _u8(a.payload).contiguous(), _u8(b.payload).contiguous()
-    as8, bs8 = _u8(a.sc8).contiguous(), _u8(b.sc8).contiguous()
+    ap, bp = _tile_readable(_u8(a.payload).contiguous()), _tile_readable(_u8(b.payload).contiguous())
+    as8, bs8 = _word_readable(_u8(a.sc8).contiguous()), _word_readable(_u8(b.sc8).contiguous())
     as32, bs32 = a.sc32.contiguous().float(), b.sc32.contiguous().float()
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=ap.device)

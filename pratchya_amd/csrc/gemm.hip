@@ -305,6 +305,19 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int* 
   *tn = w / rows_in_band;
 }
 
+// First row of tile t along a dimension of n rows: t * 256, except that the
+// last tile of a dimension of at least 256 rows that is not a multiple of 256
+// is moved back to end at row n: it overlaps the previous tile, whose outputs
+// it recomputes with the same values, and every row it reads exists.  (B's
+// scale groups stay aligned: an N quantized in blocks of 32 or more rows is a
+// multiple of them, and the host requires N % 4 == 0 for finer groups.)  A
+// dimension below 256 rows has one tile at 0: its operand buffer holds 256
+// readable rows, and outputs beyond n are not stored.
+__device__ __forceinline__ int tile_base(int t, int n) {
+  const int b = t * 256;
+  return (n >= 256 && b > n - 256) ? n - 256 : b;
+}
+
 // Epilogue: C[m][n] = acc * gA * gB / 2^14 (the two /128 of the dequant) for
 // this wave's 64 x 128 sub-tile at (row0, col0).  The waves stage RP rows x
 // 128 columns each at a time in one LDS stage buffer (free once every wave has
@@ -315,7 +328,7 @@ template <bool OUT_BF16, bool FINE_B>
 __device__ __forceinline__ void store_tile(const v16f (&acc)[2][4], const float (&gA)[2],
                                            const float (&gB)[4][FINE_B ? 4 : 1],
                                            uint8_t* stage, int wave, int lane, void* C, int64_t ldc, int row0,
-                                           int col0) {
+                                           int col0, int M, int N) {
   const int l32 = lane & 31, lhi = lane >> 5;
   constexpr int ESZ = OUT_BF16 ? 2 : 4;
   constexpr int ROWB = 128 * ESZ;           // bytes of one staged row
@@ -359,7 +372,9 @@ __device__ __forceinline__ void store_tile(const v16f (&acc)[2][4], const float 
         const int q = it * 64 + lane;
         const int r = q / CHUNKS, c = q % CHUNKS;
         const v4i v = *reinterpret_cast<const v4i*>(stg + r * PITCH + c * 16);
-        __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(Cb + (int64_t)r * ldc * ESZ + c * 16));
+        // rows / columns beyond [M, N] (a dimension below one tile) are not stored
+        if (row0 + mi * 32 + p * RP + r < M && col0 + c * (16 / ESZ) < N)
+          __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(Cb + (int64_t)r * ldc * ESZ + c * 16));
       }
       __builtin_amdgcn_s_waitcnt(0xC07F);   // staging reads done before the next pass overwrites
     }
@@ -371,7 +386,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     Scales sa, Scales sb, void* __restrict__ C, int64_t ldc, int K, int span, int tiles_m,
     int tiles_n, uint32_t a_bytes, uint32_t b_bytes, uint32_t ea_bytes, uint32_t eb_bytes,
-    uint32_t ga_bytes, uint32_t gb_bytes) {
+    uint32_t ga_bytes, uint32_t gb_bytes, int M, int N) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
   constexpr int NJ = FINE_B ? 4 : 1;
   const OperandRsrc ra = make_rsrc(A, a_bytes, sa, ea_bytes, ga_bytes);
@@ -412,7 +427,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   }
   auto rows_of = [&](int tm_, int tn_) {
     DmaRows r;
-    r.row0 = (uint32_t)((grp == 0 ? tm_ * BM : tn_ * BN) + w4 * 64);
+    r.row0 = (uint32_t)((grp == 0 ? tile_base(tm_, M) : tile_base(tn_, N)) + w4 * 64);
     r.e_word = (uint32_t)blk_index(so, (int64_t)r.row0 + lane, 0);
     return r;
   };
@@ -455,7 +470,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   __syncthreads();
 
   for (;;) {
-    const int m0 = tm * BM, n0 = tn * BN;
+    const int m0 = tile_base(tm, M), n0 = tile_base(tn, N);
     const int t_next = t + (int)gridDim.x;
     const bool has_next = t_next < T;
     int tm2 = 0, tn2 = 0;
@@ -605,7 +620,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     float gA[2], gB[4][NJ];
     load_units<FINE_B>(lds + OFF_UA, lds + OFF_UB, wm, wn, lane, gA, gB);
     store_tile<OUT_BF16, FINE_B>(acc, gA, gB, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc,
-                                 m0 + wm * 64, n0 + wn * 128);
+                                 m0 + wm * 64, n0 + wn * 128, M, N);
     if (!has_next) break;
     t = t_next;
     tm = tm2;
@@ -677,15 +692,17 @@ extern "C" int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t*
     if (M < 0 || N < 0 || K < 0) return pratchya_set_error(PRATCHYA_EINVAL, "gemm: negative size");
     return PRATCHYA_OK;
   }
-  if (M % BM || N % BN || K % BK)
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED,
-                              "gemm: M, N must be multiples of 256 and K of 128 (got %lld, %lld, %lld)",
-                              (long long)M, (long long)N, (long long)K);
+  if (K % BK)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: K must be a multiple of 128 (got %lld)", (long long)K);
+  // outputs are stored in 16-byte chunks: a dimension below one tile must end on a chunk
+  if (N < BN && N % (c_dtype == PRATCHYA_DT_BF16 ? 8 : 4))
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: N below 256 must be a multiple of %d (got %lld)",
+                              c_dtype == PRATCHYA_DT_BF16 ? 8 : 4, (long long)N);
   if (!A || !B || !a_sc8 || !a_sc32 || !b_sc8 || !b_sc32 || !C)
     return pratchya_set_error(PRATCHYA_EINVAL, "gemm: null buffer");
   if (c_dtype != PRATCHYA_DT_F32 && c_dtype != PRATCHYA_DT_BF16)
     return pratchya_set_error(PRATCHYA_EINVAL, "gemm: unsupported output dtype %d", c_dtype);
-  if (lda < K || ldb < K || ldc < N || lda % 16 || ldb % 16 || ldc % 4 ||
+  if (lda < K || ldb < K || ldc < N || lda % 16 || ldb % 16 || ldc % (c_dtype == PRATCHYA_DT_BF16 ? 8 : 4) ||
       (reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) % 16 ||
       reinterpret_cast<uintptr_t>(C) % 16)
     return pratchya_set_error(PRATCHYA_EINVAL, "gemm: leading dimensions / alignment not supported");
@@ -698,27 +715,30 @@ extern "C" int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t*
       (N / b_rdiv) * b_sr + nk * b_sk > (int64_t)UINT32_MAX)
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: scale arrays beyond 2^32 blocks");
   // The stage DMA reads each row's e8m0 byte as the aligned 4-byte word that
-  // holds it, so the byte count of each e8m0 array (last block + 1) must be a
-  // multiple of 4 (true for every quantizer layout with >= 4 blocks per slice
-  // row multiple of 4; anything else is reported).
+  // holds it: the e8m0 arrays are read up to the next multiple of 4 bytes
+  // (the caller's buffers are readable that far).
   const int64_t last_a = ((M - 1) / a_rdiv) * a_sr + (nk - 1) * a_sk;
   const int64_t last_b = ((N - 1) / b_rdiv) * b_sr + (nk - 1) * b_sk;
-  if ((last_a + 1) % 4 || (last_b + 1) % 4)
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: e8m0 arrays must hold a multiple of 4 blocks");
+  const int64_t ea_bytes = (last_a + 4) & ~(int64_t)3, eb_bytes = (last_b + 4) & ~(int64_t)3;
   // B's group max per lane: one per 32 output columns, or one per 4 columns.
   const bool fine_b = b_rdiv % 32 != 0;
+  if (fine_b && N % 4)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: N must be a multiple of 4 for B scale groups narrower "
+                              "than 32 rows (got %lld)", (long long)N);
   if (fine_b && !(b_rdiv % 4 == 0 || (b_rdiv == 1 && b_kg % (4 * b_sr) == 0 && b_sk % (4 * b_sr) == 0)))
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: B scale groups narrower than 4 columns");
   // span: both operands' group maxima are constant over it
   const int64_t span = std::gcd(group_span(sa, M, nk), group_span(sb, N, nk));
-  // buffer resources address bytes with 32-bit offsets
-  const int64_t a_bytes = (M - 1) * lda + K, b_bytes = (N - 1) * ldb + K;
+  // buffer resources address bytes with 32-bit offsets; an operand of fewer
+  // than 256 rows is read as 256 (the caller's buffer holds that many)
+  const int64_t Ma = M < BM ? BM : M, Na = N < BN ? BN : N;
+  const int64_t a_bytes = (Ma - 1) * lda + K, b_bytes = (Na - 1) * ldb + K;
   const int64_t ga_bytes = (last_a / a_kg + 1) * 4, gb_bytes = (last_b / b_kg + 1) * 4;
   if (a_bytes > (int64_t)INT32_MAX || b_bytes > (int64_t)INT32_MAX || last_a + 1 > INT32_MAX ||
       last_b + 1 > INT32_MAX)
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: operands beyond 2 GiB");
-  const int64_t tiles_n = N / BN;
-  const int64_t tiles = (M / BM) * tiles_n;
+  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int64_t tiles = tiles_m * tiles_n;
   if (tiles > INT32_MAX) return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: too many output tiles");
   // persistent grid: one workgroup per CU (the kernel's LDS allows no more), a
   // multiple of the 8 XCDs
@@ -726,9 +746,9 @@ extern "C" int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t*
   const int64_t grid = tiles < cus ? tiles : cus;
 #define PRATCHYA_GEMM(BF, FB)                                                                   \
   hipLaunchKernelGGL((k_gemm_bs_nt<BF, FB>), dim3((unsigned)grid), dim3(NTHREADS), 0, stream, A, lda, \
-                     B, ldb, sa, sb, C, ldc, (int)K, (int)span, (int)(M / BM), (int)tiles_n,   \
-                     (uint32_t)a_bytes, (uint32_t)b_bytes, (uint32_t)(last_a + 1),              \
-                     (uint32_t)(last_b + 1), (uint32_t)ga_bytes, (uint32_t)gb_bytes)
+                     B, ldb, sa, sb, C, ldc, (int)K, (int)span, (int)tiles_m, (int)tiles_n,     \
+                     (uint32_t)a_bytes, (uint32_t)b_bytes, (uint32_t)ea_bytes, (uint32_t)eb_bytes,    \
+                     (uint32_t)ga_bytes, (uint32_t)gb_bytes, (int)M, (int)N)
   const bool bf = c_dtype == PRATCHYA_DT_BF16;
   if (bf && !fine_b) PRATCHYA_GEMM(true, false);
   else if (bf) PRATCHYA_GEMM(true, true);
@@ -750,8 +770,10 @@ namespace {
 __global__ __launch_bounds__(256) void k_transpose_u8(const uint8_t* __restrict__ src, int64_t rows,
                                                       int64_t cols, uint8_t* __restrict__ dst) {
   __shared__ uint32_t tile[64][17];   // 64 rows x 64 bytes (+1 word pad)
-  // one-dimensional grid over the 64x64 tiles (no 65535 limit on either axis)
-  const int64_t tiles_c = cols / 64;
+  // one-dimensional grid over the 64x64 tiles (no 65535 limit on either
+  // axis); partial tiles at the edges (sizes are multiples of 16) move only
+  // whole 16-byte pieces inside the matrix
+  const int64_t tiles_c = (cols + 63) / 64;
   const int64_t r0 = ((int64_t)blockIdx.x / tiles_c) * 64, c0 = ((int64_t)blockIdx.x % tiles_c) * 64;
   const int t = threadIdx.x;
   {
@@ -790,10 +812,10 @@ extern "C" int pratchya_transpose_u8(const uint8_t* src, int64_t rows, int64_t c
                                      hipStream_t stream) {
   if (rows < 0 || cols < 0) return pratchya_set_error(PRATCHYA_EINVAL, "transpose: negative size");
   if (rows == 0 || cols == 0) return PRATCHYA_OK;
-  if (rows % 64 || cols % 64 || reinterpret_cast<uintptr_t>(src) % 16 || reinterpret_cast<uintptr_t>(dst) % 16)
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "transpose: sizes must be multiples of 64, buffers 16-byte aligned");
+  if (rows % 16 || cols % 16 || reinterpret_cast<uintptr_t>(src) % 16 || reinterpret_cast<uintptr_t>(dst) % 16)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "transpose: sizes must be multiples of 16, buffers 16-byte aligned");
   if (!src || !dst) return pratchya_set_error(PRATCHYA_EINVAL, "transpose: null buffer");
-  const int64_t tiles = (rows / 64) * (cols / 64);
+  const int64_t tiles = ((rows + 63) / 64) * ((cols + 63) / 64);
   if (tiles > INT32_MAX) return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "transpose: more than 2^31 64x64 tiles");
   hipLaunchKernelGGL(k_transpose_u8, dim3((unsigned)tiles), dim3(256), 0, stream, src, rows, cols, dst);
   hipError_t e = hipGetLastError();

@@ -182,7 +182,8 @@ _GEMM_TILE_MN, _GEMM_TILE_K = 256, 128
 
 
 def _lhs_operand(x8, s8, s32, grid):
-    """x [..., M, K] quantized (a, 128) as a K-contiguous GEMM operand, or None."""
+    """x [..., M, K] quantized (a, 128) as a K-contiguous GEMM operand, or None
+    (a grid whose blocks are not 128 wide along K)."""
     if x8.dim() < 2 or tuple(grid)[1] != 128:
         return None
     M, Kd = int(x8.shape[-2]), int(x8.shape[-1])
@@ -194,23 +195,38 @@ def _lhs_operand(x8, s8, s32, grid):
     # leading slices flatten into rows when the group size does not depend on them
     if lead > 1 and K.group_layout(rows, Kd, grid)[1] != K.group_layout(M, Kd, grid)[1]:
         return None
-    if rows % _GEMM_TILE_MN or Kd % _GEMM_TILE_K or a > M or M % a:
+    if Kd % _GEMM_TILE_K or a > M or M % a:
         return None
     return K.Operand(x8.reshape(rows, Kd), s8, s32, (a, Kd // 128, 1, K.group_layout(rows, Kd, grid)[1]))
 
 
 def _rhs_operand(y8, s8, s32, grid):
-    """y [K, N] quantized (128, b) as the transposed GEMM operand, or None."""
+    """y [K, N] quantized (128, b) as the transposed GEMM operand, or None.
+    The byte transpose is made once per quantization and cached on the
+    payload; a weight of fewer than 256 columns (a LoRA rank) is transposed
+    into a buffer of 256 rows, which the kernel reads as one full tile."""
     if y8.dim() != 2 or tuple(grid)[0] != 128:
         return None
     Kd, N = int(y8.shape[0]), int(y8.shape[1])
-    if N % _GEMM_TILE_MN or Kd % _GEMM_TILE_K:
+    if Kd % _GEMM_TILE_K or N % 16:
         return None
     pt = getattr(y8, _PAYLOAD_T, None)
     if pt is None:
-        pt = K.transpose_u8(y8)
+        if N < _GEMM_TILE_MN:
+            full = torch.zeros((_GEMM_TILE_MN, Kd), dtype=torch.uint8, device=y8.device)
+            _lib_transpose_into(y8, full)
+            pt = full[:N]
+        else:
+            pt = K.transpose_u8(y8)
         setattr(y8, _PAYLOAD_T, pt)     # a weight is transposed once per quantization
     return K.operand_transposed(y8, s8, s32, grid, payload_t=pt)
+
+
+def _lib_transpose_into(y8, dst):
+    """Byte-transpose the [K, N] payload y8 into the first N rows of dst [>= N, K]."""
+    Kd, N = int(y8.shape[0]), int(y8.shape[1])
+    src = K._u8(y8).contiguous()
+    K._lib.check(K._lib.load().pratchya_transpose_u8(K._ptr(src), Kd, N, K._ptr(dst), K._stream(src)), "transpose")
 
 
 def _try_gemm(op_a, op_b) -> Optional[torch.Tensor]:
@@ -226,10 +242,11 @@ def _try_gemm(op_a, op_b) -> Optional[torch.Tensor]:
 
 
 def _matmul_forward(x8, xs8, xs32, y8, ys8, ys32, gx, gy) -> torch.Tensor:
-    """f32 dequant(x) @ dequant(y) (Q:605-608): the FP8 MFMA GEMM when both
-    operands' block grids and shapes fit it ((a, 128) x (128, b) grids, M and N
-    multiples of 256, K of 128), else the reference's own f32 dot of the
-    operands dequantized by the kernels."""
+    """f32 dequant(x) @ dequant(y) (Q:605-608): the FP8 MFMA GEMM for every
+    (a, 128) x (128, b) pair of block grids (any M, N; K a multiple of 128);
+    grids whose blocks are not 128 wide along K (blksize 16 / 32 presets)
+    take the reference's own f32 dot of the operands dequantized by the
+    kernels."""
     op_a = _lhs_operand(x8, xs8, xs32, gx)
     op_b = _rhs_operand(y8, ys8, ys32, gy) if op_a is not None else None
     out = _try_gemm(op_a, op_b)
@@ -249,7 +266,8 @@ def _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y, pre=N
         return None
     Kd, N = int(y8.shape[0]), int(y8.shape[1])
     rows = g.numel() // N
-    if rows % _GEMM_TILE_MN or Kd % _GEMM_TILE_MN or N % _GEMM_TILE_MN:
+    # dgrad contracts over N (blocks of 128), wgrad over the tokens (blocks of 128)
+    if rows % _GEMM_TILE_K or N % _GEMM_TILE_K or Kd % 16:
         return None
     g2 = g.reshape(rows, N)
     gxf = gyf = None

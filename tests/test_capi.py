@@ -67,7 +67,7 @@ def test_transpose_arguments_without_gpu():
     lib = _lib.load()
     fake = ctypes.c_void_p(1 << 20)          # aligned, never dereferenced
     assert lib.pratchya_transpose_u8(fake, 0, 64, fake, None) == 0
-    assert lib.pratchya_transpose_u8(fake, 96, 64, fake, None) == _lib.EUNSUPPORTED
+    assert lib.pratchya_transpose_u8(fake, 100, 64, fake, None) == _lib.EUNSUPPORTED
     assert lib.pratchya_transpose_u8(None, 64, 64, None, None) == _lib.EINVAL
     assert lib.pratchya_transpose_u8(fake, 64 << 31, 128, fake, None) == _lib.EUNSUPPORTED
     assert b"2^31" in lib.pratchya_last_error()

@@ -299,9 +299,60 @@ def test_config4_full_shape_sampled_rows():
     check(dw[torch.from_numpy(ch).cuda()], a_rows @ g_all.T, F32_TOL, "config 4 wgrad sampled")
 
 
+EDGE_SHAPES = [
+    # (M, K, N, weight grid): tiles that overhang M and / or N
+    (300, 512, 384, (128, 128)),     # last tile row and column moved back into the matrix
+    (100, 256, 128, (128, 128)),     # both dimensions below one tile
+    (1, 128, 32, (128, 1)),          # a single token against a LoRA rank
+    (257, 384, 1008, (128, 1)),      # lm_head-like vocabulary, one row past a tile
+    (640, 1024, 48, (128, 1)),
+]
+
+
+@pytest.mark.parametrize("out", ["bf16", "f32"])
+@pytest.mark.parametrize("shape", EDGE_SHAPES, ids=lambda s: "x".join(map(str, s[:3])))
+def test_edge_tiles(shape, out):
+    """Shapes whose M or N is not a multiple of the 256x256 output tile:
+    x (1,128) @ W, every output element against the oracle (rows and columns
+    outside the matrix are never written: the output is filled with NaN
+    first and must hold no NaN afterwards)."""
+    K = _K()
+    M_, K_, N_, wg = shape
+    x = O.activation_input(M_, K_, seed=40 + M_)
+    w = O.normal_input((K_, N_), 0.02, seed=41 + N_)
+    xq = quant_dev(x, (1, 128))
+    wq = quant_dev(w, wg)
+    dt = torch.bfloat16 if out == "bf16" else torch.float32
+    C = torch.full((M_, N_), float("nan"), dtype=dt, device="cuda")
+    K.gemm_nt(K.operand_rows(*xq, (1, 128)), K.operand_transposed(*wq, wg), dt, out=C)
+    torch.cuda.synchronize()
+    assert not torch.isnan(C).any()
+    ref = deq_host(*xq, (1, 128)) @ deq_host(*wq, wg)
+    check(C, ref, BF16_TOL if out == "bf16" else F32_TOL, f"edge {shape} {out}")
+
+
+def test_edge_tile_output_stride():
+    """An output written into the left part of a wider buffer (ldc > N) leaves
+    the columns past N untouched."""
+    K = _K()
+    M_, K_, N_ = 300, 256, 96
+    xq = quant_dev(O.activation_input(M_, K_, seed=3), (1, 128))
+    wq = quant_dev(O.normal_input((K_, N_), 0.02, seed=4), (128, 1))
+    wide = torch.full((M_, 160), -7.0, dtype=torch.float32, device="cuda")
+    K.gemm_nt(K.operand_rows(*xq, (1, 128)), K.operand_transposed(*wq, (128, 1)), torch.float32,
+              out=wide[:, :N_])
+    torch.cuda.synchronize()
+    assert torch.all(wide[:, N_:] == -7.0)
+    check(wide[:, :N_], deq_host(*xq, (1, 128)) @ deq_host(*wq, (128, 1)), F32_TOL, "strided output")
+
+
 def test_unsupported_shape_is_reported():
+    """K must be a whole number of 128-wide blocks; a width below one tile must
+    end on a 16-byte output chunk."""
     K = _K()
     xq = quant_dev(O.activation_input(128, 256, seed=1), (1, 128))
-    wq = quant_dev(O.normal_input((256, 256), 0.02, seed=1), (128, 128))
-    with pytest.raises(Exception, match="multiples of 256"):
-        K.gemm_nt(K.operand_rows(*xq, (1, 128)), K.operand_transposed(*wq, (128, 128)))
+    wq = quant_dev(O.normal_input((256, 32), 0.02, seed=1), (128, 1))
+    a = K.operand_rows(*xq, (1, 128))
+    b = K.operand_transposed(*wq, (128, 1))
+    with pytest.raises(Exception, match="multiple of 8"):
+        K.gemm_nt(a, K.Operand(b.payload[:20], b.sc8, b.sc32, b.desc), torch.bfloat16)

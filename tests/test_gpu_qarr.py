@@ -145,20 +145,28 @@ def test_linear_forward_backward(Q, mode):
 # lm_head: Linear(hidden, vocab, (blksize, 1)) (_model.py:77); LoRA:
 # Linear(hidden, rank, (a, 1)) then Linear(rank, hidden, (b, 1)) (M:75-88).
 # The product's grid is (1, 1): every element is its own group.
-ODD_LINEARS = {"lm_head": (256, 512), "lora_down": (1024, 128), "lora_up": (128, 1024)}
+# (K, N, tokens): widths below one 256-wide tile (LoRA ranks 32 and 128) and
+# not a multiple of it (a 1008-entry vocabulary, 300 tokens) run on the FP8
+# kernel's edge tiles.
+ODD_LINEARS = {"lm_head": (256, 512, 256), "lm_head_ragged": (256, 1008, 300), "lora_down": (1024, 128, 256),
+               "lora_down_r32": (1024, 32, 300), "lora_up": (128, 1024, 256)}
 
 
 @pytest.mark.parametrize("mode", ["f32", "fp8"])
 @pytest.mark.parametrize("case", sorted(ODD_LINEARS))
-def test_odd_grid_linears(Q, mode, case):
+def test_odd_grid_linears(Q, mode, case, monkeypatch):
     Q.set_matmul_backward(mode)
-    Kd, N = ODD_LINEARS[case]
-    xb, wb, gb = _linear_case(seed=31, M=256, Kd=Kd, N=N)
+    Kd, N, M = ODD_LINEARS[case]
+    calls = []
+    real = Q.K.gemm_nt
+    monkeypatch.setattr(Q.K, "gemm_nt", lambda *a, **k: calls.append(1) or real(*a, **k))
+    xb, wb, gb = _linear_case(seed=31, M=M, Kd=Kd, N=N)
     x = to_dev_bf16(xb).requires_grad_(True)
     w = to_dev_bf16(wb).requires_grad_(True)
     out = Q.QArrayImpl(x, (1, 128)) @ Q.QArrayImpl(w, (128, 1))
     assert out.tgrid == (1, 1)
     y = out.astype(torch.bfloat16)
+    assert len(calls) == 1                   # the forward ran on the FP8 kernel
     y.backward(to_dev_bf16(gb))
     _, o8, o32 = triple(out)
     xq, wq = oq(O.bf16_bits_to_f32(xb), (1, 128)), oq(O.bf16_bits_to_f32(wb), (128, 1))

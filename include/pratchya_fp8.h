@@ -276,6 +276,32 @@ int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, con
                         int64_t M, int64_t N, int64_t K, void* C, int64_t ldc, int c_dtype,
                         hipStream_t stream);
 
+/* The GEMM with the product's requantization in its epilogue: replaces
+ *   QArrayImpl(matmul_impl(x, y), (1, 128)).astype(dtype)
+ * (Q:605-608, then quantize_impl Q:458-506 and dequantize_impl Q:541-569), the
+ * quantized Linear's output (pratchya/_nnx_impl/_module.py:46-50); with
+ * fix_nan = 1, quantize_impl_bwd's dequantization of a requantized cotangent
+ * instead (an e8m0 byte 255 read as 1.0, Q:521-526: the dgrad output).
+ * Operands, M, K and ldc as pratchya_gemm_bs_nt (B's scale groups at least 32
+ * rows).  N must be a multiple of 1024: a (1, 128) group of the [M, N] output
+ * is 8 blocks of one row, and the kernel exchanges block maxima between the
+ * four 256-column tiles of a group.  C [M, N] (ldc) receives the dequantized
+ * values in c_dtype (f32 or bf16), c_sc8 [M * N / 128] and c_sc32 [M * N / 1024]
+ * the scales quantize_impl(C_f32, (1, 128)) returns.  The results equal
+ * pratchya_gemm_bs_nt to f32 followed by pratchya_quantize_dequantize bit for
+ * bit.  workspace: pratchya_gemm_bs_nt_fq_workspace_bytes(M, N) bytes, 4-byte
+ * aligned, cleared by a kernel of this call (calls sharing one workspace must
+ * not overlap); its last word is set to 1 if the kernel's bounded wait for a
+ * group's four tiles ran out (never expected: results are then invalid). */
+int64_t pratchya_gemm_bs_nt_fq_workspace_bytes(int64_t M, int64_t N);
+int pratchya_gemm_bs_nt_fq(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, const float* a_sc32,
+                           int64_t a_rdiv, int64_t a_sr, int64_t a_sk, int64_t a_kg,
+                           const uint8_t* B, int64_t ldb, const uint8_t* b_sc8, const float* b_sc32,
+                           int64_t b_rdiv, int64_t b_sr, int64_t b_sk, int64_t b_kg,
+                           int64_t M, int64_t N, int64_t K, void* C, int64_t ldc, int c_dtype, int fix_nan,
+                           uint8_t* c_sc8, float* c_sc32, void* workspace, int64_t workspace_bytes,
+                           hipStream_t stream);
+
 /* Span of an operand's scale layout: the largest P such that every row's group
  * index is constant over each aligned run of P 128-wide K blocks (the GEMM
  * reloads group maxima and rescales its accumulator at multiples of it);

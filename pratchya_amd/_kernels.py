@@ -536,6 +536,44 @@ def gemm_nt(a: Operand, b: Operand, out_dtype: torch.dtype = torch.bfloat16,
     return out
 
 
+def gemm_nt_fq(a: Operand, b: Operand, out_dtype: torch.dtype, fix_nan: bool = False, lead=None):
+    """``QArrayImpl(dequant(a) @ dequant(b)^T, (1, 128)).astype(out_dtype)``
+    with the requantization in the GEMM's epilogue: returns ``(y [M, N],
+    sc_fp8, sc_fp32)`` bit-identical to ``quantize_dequantize(gemm_nt(a, b,
+    float32), (1, 128), out_dtype, fix_nan)``.  ``lead``: leading dimensions
+    of the product (its rows are ``prod(lead) * H`` flattened; the scales are
+    shaped per slice as quantize_impl returns them).  Raises
+    ``PratchyaUnsupported`` unless N is a multiple of 1024 and B's scale
+    groups span at least 32 rows."""
+    _require_gpu(a.payload, b.payload)
+    if a.k != b.k:
+        raise ValueError(f"contraction mismatch: {a.k} vs {b.k}")
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"gemm_nt_fq: output dtype {out_dtype} is not float32 or bfloat16")
+    M, N, K = a.rows, b.rows, a.k
+    lib = _lib.load()
+    ws_bytes = lib.pratchya_gemm_bs_nt_fq_workspace_bytes(M, N)
+    if ws_bytes <= 0:
+        raise PratchyaUnsupported(f"gemm_fq: N must be a multiple of 1024 (got {N})")
+    ap, bp = _tile_readable(_u8(a.payload).contiguous()), _tile_readable(_u8(b.payload).contiguous())
+    as8, bs8 = _word_readable(_u8(a.sc8).contiguous()), _word_readable(_u8(b.sc8).contiguous())
+    as32, bs32 = a.sc32.contiguous().float(), b.sc32.contiguous().float()
+    lead = tuple(lead) if lead else (1,)
+    S = 1
+    for d in lead[:-1]:
+        S *= int(d)
+    H = M // S
+    y = torch.empty((M, N), dtype=out_dtype, device=ap.device)
+    sc8 = torch.empty(tuple(lead[:-1]) + (H * N // 1024, 8), dtype=torch.uint8, device=ap.device)
+    sc32 = torch.empty(tuple(lead[:-1]) + (H * N // 1024, 1, 1), dtype=torch.float32, device=ap.device)
+    ws = torch.empty(int(ws_bytes), dtype=torch.uint8, device=ap.device)
+    _lib.check(lib.pratchya_gemm_bs_nt_fq(_ptr(ap), K, _ptr(as8), _ptr(as32), *a.desc,
+                                          _ptr(bp), K, _ptr(bs8), _ptr(bs32), *b.desc,
+                                          M, N, K, _ptr(y), N, _dtype_code(out_dtype), 1 if fix_nan else 0,
+                                          _ptr(sc8), _ptr(sc32), _ptr(ws), int(ws_bytes), _stream(ap)), "gemm_fq")
+    return y, sc8.view(E8M0), sc32
+
+
 def _as_operand(x, what):
     """(tensor, dtype code, sc8, sc32) of an optimizer operand: an fp8 payload
     given as a (payload, sc8, sc32) triple, or a bf16 / f32 tensor."""

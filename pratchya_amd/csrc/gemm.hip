@@ -42,6 +42,7 @@
 #include <numeric>
 
 #include "pratchya_fp8.h"
+#include "quant_device.h"
 
 int pratchya_set_error(int code, const char* fmt, ...);
 
@@ -305,6 +306,40 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int* 
   *tn = w / rows_in_band;
 }
 
+// Output requantization in the epilogue (pratchya_gemm_bs_nt_fq): the output
+// is fake-quantized with tgrid (1, 128), whose groups are 1024 columns of one
+// row, i.e. one "strip" of four 256-wide tiles.  The four workgroups of a
+// strip run in the same round of the persistent schedule and exchange their
+// row maxima through `gmax` (device-scope atomic max of |x| bits) and an
+// arrival count per strip; both are zeroed before the launch.
+struct FqArgs {
+  uint8_t* sc8;        // output e8m0 bytes [M, N / 128]
+  float* sc32;         // output group maxima [M, N / 1024]
+  uint32_t* gmax;      // per strip: 256 row group maxima (|x| bits)
+  uint32_t* arrive;    // per strip: workgroups that published their maxima
+  uint32_t* status;    // set to 1 if a strip's partners did not arrive in time
+  int xcd;             // strip partners: workgroups b, b+8, b+16, b+24 (1) or b..b+3 (0)
+};
+
+// Output tile of workgroup-tile counter `bid` with output requantization: the
+// four tiles of a strip get consecutive numbers L (L % 4 = tile in the strip),
+// and L is XCD-aware as in tile_of when `xcd` (the counters b, b+8, b+16, b+24
+// of the workgroups on one XCD then hold one strip); bands of up to 4 tile rows
+// are walked strip by strip.
+__device__ __forceinline__ void tile_of_fq(int bid, int tiles_m, int tiles_n, bool xcd, int* tm, int* tn) {
+  const int T = tiles_m * tiles_n;
+  int L = xcd ? (bid % 8) * (T / 8) + bid / 8 : bid;
+  const int q = L & 3;
+  L >>= 2;
+  const int S = tiles_n >> 2;              // strips per tile row
+  const int GM = tiles_m < 4 ? tiles_m : 4;
+  const int band = L / (GM * S);
+  const int rows_in_band = (tiles_m - band * GM) < GM ? (tiles_m - band * GM) : GM;
+  const int w = L - band * GM * S;
+  *tm = band * GM + w % rows_in_band;
+  *tn = (w / rows_in_band) * 4 + q;
+}
+
 // First row of tile t along a dimension of n rows: t * 256, except that the
 // last tile of a dimension of at least 256 rows that is not a multiple of 256
 // is moved back to end at row n: it overlaps the previous tile, whose outputs
@@ -381,13 +416,145 @@ __device__ __forceinline__ void store_tile(const v16f (&acc)[2][4], const float 
   }
 }
 
-template <bool OUT_BF16, bool FINE_B>
+// Output requantization, QArrayImpl(C, (1, 128)).astype(dtype) (Q:458-506
+// then Q:541-569; with FIXNAN, quantize_impl_bwd's dequantization that reads
+// an e8m0 byte 255 as 1.0, Q:521-526), in two steps.
+//
+// fq_row_scales: the f32 product (acc scaled as the plain epilogue scales
+// it), each row's max |x| over this wave's 128 columns (one block; lanes l32
+// and l32 + 32 hold row mi * 32 + l32's values, 64 each), the group max over
+// the strip's 8 blocks by the exchange described at FqArgs, and the scales of
+// row lhi * 32 + l32 into this wave's 64-entry table in LDS (y, S, dq, e and
+// whether G is finite, 16 bytes per row).  Writes the output scales of rows
+// below M.
+constexpr int FQ_TABLE_BYTES = 8 * 64 * 16;
+
+template <bool FIXNAN>
+__device__ __forceinline__ void fq_row_scales(v16f (&acc)[2][4], const float (&gA)[2], const float (&gB)[4][1],
+                                              const FqArgs& fq, uint8_t* table, int strip, int tn, int wm,
+                                              int wn, int lane, int row0, int col0, int M, int N) {
+  const int l32 = lane & 31, lhi = lane >> 5;
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
+      const float f = gA[mi] * gB[ni][0] * 6.103515625e-05f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mi][ni][v] *= f;
+    }
+  // block maxima as |x| bits (an unsigned max propagates NaN)
+  uint32_t m[2];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+    uint32_t a = 0;
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) a = umax(a, f2u(acc[mi][ni][v]) & 0x7FFFFFFFu);
+    m[mi] = umax(a, shfl_xor_u32(a, 32));
+  }
+  const uint32_t mb = lhi ? m[1] : m[0];      // this lane's row: lhi * 32 + l32
+  uint32_t* gm = fq.gmax + (int64_t)strip * 256 + wm * 64 + lhi * 32 + l32;
+  __hip_atomic_fetch_max(gm, mb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0x0F70);       // vmcnt(0): this wave's maxima are performed
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t* cnt = fq.arrive + strip;
+    __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the partners run in the same round of the schedule; the bound only keeps
+    // a broken launch from spinning forever (the status word reports it)
+    for (int it = 0; __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < 4u; ++it) {
+      if (it >= (1 << 20)) {
+        __hip_atomic_store(fq.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+  }
+  __syncthreads();
+  const uint32_t Gb = __hip_atomic_load(gm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const float G = u2f(Gb);
+  const bool fin = (Gb >> 23) < 255u;
+  BlockScale bs;
+  if (fin) {
+    bs = block_scale(mb, Gb, __builtin_amdgcn_rcpf(G * 0.0078125f));
+  } else {
+    bs.e = e8m0_of(u2f(mb), G);
+    bs.y = 0.0f;
+    bs.clamped = false;
+  }
+  const uint32_t ed = (FIXNAN && bs.e == 0xFFu) ? 0x7Fu : bs.e;
+  *reinterpret_cast<v4f*>(table + (lhi * 32 + l32) * 16) =
+      v4f{bs.y, quant_scale(bs.e, G), e8m0_decode(ed) * G, u2f(fin ? 1u : 0u)};
+  // scales of the lane's row: its e8m0 byte for this block, and its group
+  // max from the strip's first tile, left wave
+  const int row = row0 + lhi * 32 + l32;
+  if (row < M) {
+    fq.sc8[(int64_t)row * (N >> 7) + (col0 >> 7)] = (uint8_t)bs.e;
+    if ((tn & 3) == 0 && wn == 0) fq.sc32[(int64_t)row * (N >> 10) + (tn >> 2)] = G;
+  }
+}
+
+// Epilogue of the output-requantizing GEMM: acc holds the f32 product; the
+// waves stage 16 rows x 128 columns at a time (f32) in the free stage buffer,
+// each lane takes a 4-column chunk of one row, fake-quantizes it with its row's
+// scales from the table (fake_quant4), and stores the dequantized values
+// (16 or 8 bytes; a row's 32 lanes write its 128 columns contiguously).
+template <bool OUT_BF16>
+__device__ __forceinline__ void store_tile_fq(const v16f (&acc)[2][4], uint8_t* stage, const uint8_t* table,
+                                              int wave, int lane, void* C, int64_t ldc, int row0, int col0,
+                                              int M) {
+  const int l32 = lane & 31, lhi = lane >> 5;
+  constexpr int OSZ = OUT_BF16 ? 2 : 4;
+  constexpr int PITCH = 512 + 16;           // 128 f32 + padding
+  constexpr int RP = 16;                    // rows staged per pass
+  static_assert(8 * RP * PITCH <= STAGE_BYTES, "staging must fit one stage buffer");
+  uint8_t* stg = stage + wave * (RP * PITCH);
+  __syncthreads();                          // every wave is done with the stage buffer
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      if ((l32 >> 4) == p) {
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<v4f*>(stg + (l32 & 15) * PITCH + (ni * 32 + 8 * j + 4 * lhi) * 4) =
+                v4f{acc[mi][ni][4 * j], acc[mi][ni][4 * j + 1], acc[mi][ni][4 * j + 2], acc[mi][ni][4 * j + 3]};
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): staging writes done
+#pragma unroll 1
+      for (int it = 0; it < 8; ++it) {
+        const int r = it * 2 + lhi;         // staged row; chunk l32
+        const int rw = mi * 32 + p * 16 + r;   // row within the wave's 64
+        v4f x = *reinterpret_cast<const v4f*>(stg + r * PITCH + l32 * 16);
+        const v4f sc = *reinterpret_cast<const v4f*>(table + rw * 16);
+        float x0 = x.x, x1 = x.y, x2 = x.z, x3 = x.w;
+        fake_quant4(x0, x1, x2, x3, sc.x, sc.y, f2u(sc.w) != 0u, sc.z);
+        if (row0 + rw < M) {
+          uint8_t* dst = static_cast<uint8_t*>(C) + ((int64_t)(row0 + rw) * ldc + col0 + l32 * 4) * OSZ;
+          if constexpr (OUT_BF16) {
+            __builtin_nontemporal_store(u32x2_t{pack_bf16x2(x0, x1), pack_bf16x2(x2, x3)},
+                                        reinterpret_cast<u32x2_t*>(dst));
+          } else {
+            __builtin_nontemporal_store(u32x4_t{f2u(x0), f2u(x1), f2u(x2), f2u(x3)},
+                                        reinterpret_cast<u32x4_t*>(dst));
+          }
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);   // staging reads done before the next pass overwrites
+    }
+  }
+}
+
+template <bool OUT_BF16, bool FINE_B, int FQ>
 __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     Scales sa, Scales sb, void* __restrict__ C, int64_t ldc, int K, int span, int tiles_m,
     int tiles_n, uint32_t a_bytes, uint32_t b_bytes, uint32_t ea_bytes, uint32_t eb_bytes,
-    uint32_t ga_bytes, uint32_t gb_bytes, int M, int N) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+    uint32_t ga_bytes, uint32_t gb_bytes, int M, int N, FqArgs fq) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + (FQ != 0 ? FQ_TABLE_BYTES : 0)];
   constexpr int NJ = FINE_B ? 4 : 1;
   const OperandRsrc ra = make_rsrc(A, a_bytes, sa, ea_bytes, ga_bytes);
   const OperandRsrc rb = make_rsrc(B, b_bytes, sb, eb_bytes, gb_bytes);
@@ -451,7 +618,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   // covered by the epilogue, which stages the output in the other buffer.
   int t = blockIdx.x;
   int tm, tn;
-  tile_of(t, tiles_m, tiles_n, &tm, &tn);
+  auto next_tile = [&](int t_, int* tm_, int* tn_) {
+    if constexpr (FQ != 0) tile_of_fq(t_, tiles_m, tiles_n, fq.xcd != 0, tm_, tn_);
+    else tile_of(t_, tiles_m, tiles_n, tm_, tn_);
+  };
+  next_tile(t, &tm, &tn);
   DmaRows cur = rows_of(tm, tn);
   int par = 0;                            // stage buffer of the tile's K block 0
 
@@ -476,7 +647,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     int tm2 = 0, tn2 = 0;
     DmaRows nxt = cur;
     if (has_next) {
-      tile_of(t_next, tiles_m, tiles_n, &tm2, &tn2);
+      next_tile(t_next, &tm2, &tn2);
       nxt = rows_of(tm2, tn2);
     }
     if (grp == 1) {
@@ -619,8 +790,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     // stage the output there
     float gA[2], gB[4][NJ];
     load_units<FINE_B>(lds + OFF_UA, lds + OFF_UB, wm, wn, lane, gA, gB);
-    store_tile<OUT_BF16, FINE_B>(acc, gA, gB, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc,
-                                 m0 + wm * 64, n0 + wn * 128, M, N);
+    if constexpr (FQ != 0) {
+      static_assert(!FINE_B, "output requantization takes B scale groups of 32 rows or more");
+      uint8_t* table = lds + LDS_BYTES + wave * 64 * 16;
+      fq_row_scales<FQ == 2>(acc, gA, gB, fq, table, tm * (tiles_n >> 2) + (tn >> 2), tn, wm, wn, lane,
+                             m0 + wm * 64, n0 + wn * 128, M, N);
+      store_tile_fq<OUT_BF16>(acc, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, table, wave, lane, C, ldc,
+                              m0 + wm * 64, n0 + wn * 128, M);
+    } else {
+      store_tile<OUT_BF16, FINE_B>(acc, gA, gB, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc,
+                                   m0 + wm * 64, n0 + wn * 128, M, N);
+    }
     if (!has_next) break;
     t = t_next;
     tm = tm2;
@@ -682,6 +862,103 @@ extern "C" int64_t pratchya_gemm_span(int64_t rows, int64_t K, int64_t r_div, in
   return group_span(s, rows, K / BK);
 }
 
+namespace {
+
+// Validated launch parameters of one GEMM call.
+struct GemmPlan {
+  Scales sa, sb;
+  int64_t span, tiles_m, tiles_n, grid;
+  int64_t a_bytes, b_bytes, ea_bytes, eb_bytes, ga_bytes, gb_bytes;
+  bool fine_b;
+};
+
+int gemm_plan(const char* who, const uint8_t* A, int64_t lda, const uint8_t* a_sc8, const float* a_sc32,
+              int64_t a_rdiv, int64_t a_sr, int64_t a_sk, int64_t a_kg, const uint8_t* B, int64_t ldb,
+              const uint8_t* b_sc8, const float* b_sc32, int64_t b_rdiv, int64_t b_sr, int64_t b_sk,
+              int64_t b_kg, int64_t M, int64_t N, int64_t K, const void* C, int64_t ldc, int c_dtype,
+              GemmPlan* P) {
+  if (K % BK)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: K must be a multiple of 128 (got %lld)", who,
+                              (long long)K);
+  // outputs are stored in 16-byte chunks: a dimension below one tile must end on a chunk
+  if (N < BN && N % (c_dtype == PRATCHYA_DT_BF16 ? 8 : 4))
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: N below 256 must be a multiple of %d (got %lld)", who,
+                              c_dtype == PRATCHYA_DT_BF16 ? 8 : 4, (long long)N);
+  if (!A || !B || !a_sc8 || !a_sc32 || !b_sc8 || !b_sc32 || !C)
+    return pratchya_set_error(PRATCHYA_EINVAL, "%s: null buffer", who);
+  if (c_dtype != PRATCHYA_DT_F32 && c_dtype != PRATCHYA_DT_BF16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "%s: unsupported output dtype %d", who, c_dtype);
+  if (lda < K || ldb < K || ldc < N || lda % 16 || ldb % 16 || ldc % (c_dtype == PRATCHYA_DT_BF16 ? 8 : 4) ||
+      (reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) % 16 ||
+      reinterpret_cast<uintptr_t>(C) % 16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "%s: leading dimensions / alignment not supported", who);
+  if (a_rdiv < 1 || b_rdiv < 1 || a_kg < 1 || b_kg < 1 || a_sr < 0 || a_sk < 0 || b_sr < 0 || b_sk < 0)
+    return pratchya_set_error(PRATCHYA_EINVAL, "%s: bad scale layout", who);
+  P->sa = Scales{a_sc8, a_sc32, a_rdiv, a_sr, a_sk, a_kg};
+  P->sb = Scales{b_sc8, b_sc32, b_rdiv, b_sr, b_sk, b_kg};
+  const int64_t nk = K / BK;
+  if ((M / a_rdiv) * a_sr + nk * a_sk > (int64_t)UINT32_MAX ||
+      (N / b_rdiv) * b_sr + nk * b_sk > (int64_t)UINT32_MAX)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: scale arrays beyond 2^32 blocks", who);
+  // The stage DMA reads each row's e8m0 byte as the aligned 4-byte word that
+  // holds it: the e8m0 arrays are read up to the next multiple of 4 bytes
+  // (the caller's buffers are readable that far).
+  const int64_t last_a = ((M - 1) / a_rdiv) * a_sr + (nk - 1) * a_sk;
+  const int64_t last_b = ((N - 1) / b_rdiv) * b_sr + (nk - 1) * b_sk;
+  P->ea_bytes = (last_a + 4) & ~(int64_t)3;
+  P->eb_bytes = (last_b + 4) & ~(int64_t)3;
+  // B's group max per lane: one per 32 output columns, or one per 4 columns.
+  P->fine_b = b_rdiv % 32 != 0;
+  if (P->fine_b && N % 4)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: N must be a multiple of 4 for B scale groups narrower "
+                              "than 32 rows (got %lld)", who, (long long)N);
+  if (P->fine_b && !(b_rdiv % 4 == 0 || (b_rdiv == 1 && b_kg % (4 * b_sr) == 0 && b_sk % (4 * b_sr) == 0)))
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: B scale groups narrower than 4 columns", who);
+  // span: both operands' group maxima are constant over it
+  P->span = std::gcd(group_span(P->sa, M, nk), group_span(P->sb, N, nk));
+  // buffer resources address bytes with 32-bit offsets; an operand of fewer
+  // than 256 rows is read as 256 (the caller's buffer holds that many)
+  const int64_t Ma = M < BM ? BM : M, Na = N < BN ? BN : N;
+  P->a_bytes = (Ma - 1) * lda + K;
+  P->b_bytes = (Na - 1) * ldb + K;
+  P->ga_bytes = (last_a / a_kg + 1) * 4;
+  P->gb_bytes = (last_b / b_kg + 1) * 4;
+  if (P->a_bytes > (int64_t)INT32_MAX || P->b_bytes > (int64_t)INT32_MAX || last_a + 1 > INT32_MAX ||
+      last_b + 1 > INT32_MAX)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: operands beyond 2 GiB", who);
+  P->tiles_m = (M + BM - 1) / BM;
+  P->tiles_n = (N + BN - 1) / BN;
+  if (P->tiles_m * P->tiles_n > INT32_MAX)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: too many output tiles", who);
+  // persistent grid: one workgroup per CU (the kernel's LDS allows no more), a
+  // multiple of the 8 XCDs
+  const int64_t tiles = P->tiles_m * P->tiles_n, cus = gemm_num_cus();
+  P->grid = tiles < cus ? tiles : cus;
+  return PRATCHYA_OK;
+}
+
+template <bool BF, bool FB, int FQ>
+void gemm_launch(const GemmPlan& P, const uint8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, void* C,
+                 int64_t ldc, int64_t M, int64_t N, int64_t K, const FqArgs& fq, hipStream_t stream) {
+  hipLaunchKernelGGL((k_gemm_bs_nt<BF, FB, FQ>), dim3((unsigned)P.grid), dim3(NTHREADS), 0, stream, A, lda, B,
+                     ldb, P.sa, P.sb, C, ldc, (int)K, (int)P.span, (int)P.tiles_m, (int)P.tiles_n,
+                     (uint32_t)P.a_bytes, (uint32_t)P.b_bytes, (uint32_t)P.ea_bytes, (uint32_t)P.eb_bytes,
+                     (uint32_t)P.ga_bytes, (uint32_t)P.gb_bytes, (int)M, (int)N, fq);
+}
+
+int launch_status(const char* who) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return pratchya_set_error(PRATCHYA_EHIP, "%s: launch failed: %s", who, hipGetErrorString(e));
+  return PRATCHYA_OK;
+}
+
+// Workspace of the output-requantizing GEMM: per strip (256 rows x 1024
+// columns) 256 row maxima and an arrival count, then one status word.
+int64_t fq_strips(int64_t M, int64_t N) { return ((M + BM - 1) / BM) * (N / 1024); }
+int64_t fq_workspace_words(int64_t M, int64_t N) { return fq_strips(M, N) * 257 + 1; }
+
+}  // namespace
+
 extern "C" int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t* a_sc8,
                                    const float* a_sc32, int64_t a_rdiv, int64_t a_sr, int64_t a_sk,
                                    int64_t a_kg, const uint8_t* B, int64_t ldb, const uint8_t* b_sc8,
@@ -692,73 +969,76 @@ extern "C" int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t*
     if (M < 0 || N < 0 || K < 0) return pratchya_set_error(PRATCHYA_EINVAL, "gemm: negative size");
     return PRATCHYA_OK;
   }
-  if (K % BK)
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: K must be a multiple of 128 (got %lld)", (long long)K);
-  // outputs are stored in 16-byte chunks: a dimension below one tile must end on a chunk
-  if (N < BN && N % (c_dtype == PRATCHYA_DT_BF16 ? 8 : 4))
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: N below 256 must be a multiple of %d (got %lld)",
-                              c_dtype == PRATCHYA_DT_BF16 ? 8 : 4, (long long)N);
-  if (!A || !B || !a_sc8 || !a_sc32 || !b_sc8 || !b_sc32 || !C)
-    return pratchya_set_error(PRATCHYA_EINVAL, "gemm: null buffer");
-  if (c_dtype != PRATCHYA_DT_F32 && c_dtype != PRATCHYA_DT_BF16)
-    return pratchya_set_error(PRATCHYA_EINVAL, "gemm: unsupported output dtype %d", c_dtype);
-  if (lda < K || ldb < K || ldc < N || lda % 16 || ldb % 16 || ldc % (c_dtype == PRATCHYA_DT_BF16 ? 8 : 4) ||
-      (reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) % 16 ||
-      reinterpret_cast<uintptr_t>(C) % 16)
-    return pratchya_set_error(PRATCHYA_EINVAL, "gemm: leading dimensions / alignment not supported");
-  if (a_rdiv < 1 || b_rdiv < 1 || a_kg < 1 || b_kg < 1 || a_sr < 0 || a_sk < 0 || b_sr < 0 || b_sk < 0)
-    return pratchya_set_error(PRATCHYA_EINVAL, "gemm: bad scale layout");
-  Scales sa{a_sc8, a_sc32, a_rdiv, a_sr, a_sk, a_kg};
-  Scales sb{b_sc8, b_sc32, b_rdiv, b_sr, b_sk, b_kg};
-  const int64_t nk = K / BK;
-  if ((M / a_rdiv) * a_sr + nk * a_sk > (int64_t)UINT32_MAX ||
-      (N / b_rdiv) * b_sr + nk * b_sk > (int64_t)UINT32_MAX)
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: scale arrays beyond 2^32 blocks");
-  // The stage DMA reads each row's e8m0 byte as the aligned 4-byte word that
-  // holds it: the e8m0 arrays are read up to the next multiple of 4 bytes
-  // (the caller's buffers are readable that far).
-  const int64_t last_a = ((M - 1) / a_rdiv) * a_sr + (nk - 1) * a_sk;
-  const int64_t last_b = ((N - 1) / b_rdiv) * b_sr + (nk - 1) * b_sk;
-  const int64_t ea_bytes = (last_a + 4) & ~(int64_t)3, eb_bytes = (last_b + 4) & ~(int64_t)3;
-  // B's group max per lane: one per 32 output columns, or one per 4 columns.
-  const bool fine_b = b_rdiv % 32 != 0;
-  if (fine_b && N % 4)
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: N must be a multiple of 4 for B scale groups narrower "
-                              "than 32 rows (got %lld)", (long long)N);
-  if (fine_b && !(b_rdiv % 4 == 0 || (b_rdiv == 1 && b_kg % (4 * b_sr) == 0 && b_sk % (4 * b_sr) == 0)))
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: B scale groups narrower than 4 columns");
-  // span: both operands' group maxima are constant over it
-  const int64_t span = std::gcd(group_span(sa, M, nk), group_span(sb, N, nk));
-  // buffer resources address bytes with 32-bit offsets; an operand of fewer
-  // than 256 rows is read as 256 (the caller's buffer holds that many)
-  const int64_t Ma = M < BM ? BM : M, Na = N < BN ? BN : N;
-  const int64_t a_bytes = (Ma - 1) * lda + K, b_bytes = (Na - 1) * ldb + K;
-  const int64_t ga_bytes = (last_a / a_kg + 1) * 4, gb_bytes = (last_b / b_kg + 1) * 4;
-  if (a_bytes > (int64_t)INT32_MAX || b_bytes > (int64_t)INT32_MAX || last_a + 1 > INT32_MAX ||
-      last_b + 1 > INT32_MAX)
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: operands beyond 2 GiB");
-  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  const int64_t tiles = tiles_m * tiles_n;
-  if (tiles > INT32_MAX) return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm: too many output tiles");
-  // persistent grid: one workgroup per CU (the kernel's LDS allows no more), a
-  // multiple of the 8 XCDs
-  const int64_t cus = gemm_num_cus();
-  const int64_t grid = tiles < cus ? tiles : cus;
-#define PRATCHYA_GEMM(BF, FB)                                                                   \
-  hipLaunchKernelGGL((k_gemm_bs_nt<BF, FB>), dim3((unsigned)grid), dim3(NTHREADS), 0, stream, A, lda, \
-                     B, ldb, sa, sb, C, ldc, (int)K, (int)span, (int)tiles_m, (int)tiles_n,     \
-                     (uint32_t)a_bytes, (uint32_t)b_bytes, (uint32_t)ea_bytes, (uint32_t)eb_bytes,    \
-                     (uint32_t)ga_bytes, (uint32_t)gb_bytes, (int)M, (int)N)
+  GemmPlan P;
+  int rc = gemm_plan("gemm", A, lda, a_sc8, a_sc32, a_rdiv, a_sr, a_sk, a_kg, B, ldb, b_sc8, b_sc32, b_rdiv,
+                     b_sr, b_sk, b_kg, M, N, K, C, ldc, c_dtype, &P);
+  if (rc) return rc;
+  const FqArgs none{};
   const bool bf = c_dtype == PRATCHYA_DT_BF16;
-  if (bf && !fine_b) PRATCHYA_GEMM(true, false);
-  else if (bf) PRATCHYA_GEMM(true, true);
-  else if (!fine_b) PRATCHYA_GEMM(false, false);
-  else PRATCHYA_GEMM(false, true);
-#undef PRATCHYA_GEMM
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess)
-    return pratchya_set_error(PRATCHYA_EHIP, "gemm: launch failed: %s", hipGetErrorString(e));
-  return PRATCHYA_OK;
+  if (bf && !P.fine_b) gemm_launch<true, false, 0>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
+  else if (bf) gemm_launch<true, true, 0>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
+  else if (!P.fine_b) gemm_launch<false, false, 0>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
+  else gemm_launch<false, true, 0>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
+  return launch_status("gemm");
+}
+
+extern "C" int64_t pratchya_gemm_bs_nt_fq_workspace_bytes(int64_t M, int64_t N) {
+  if (M <= 0 || N <= 0 || N % 1024) return 0;
+  return ((fq_workspace_words(M, N) * 4 + 255) / 256) * 256;
+}
+
+extern "C" int pratchya_gemm_bs_nt_fq(const uint8_t* A, int64_t lda, const uint8_t* a_sc8,
+                                      const float* a_sc32, int64_t a_rdiv, int64_t a_sr, int64_t a_sk,
+                                      int64_t a_kg, const uint8_t* B, int64_t ldb, const uint8_t* b_sc8,
+                                      const float* b_sc32, int64_t b_rdiv, int64_t b_sr, int64_t b_sk,
+                                      int64_t b_kg, int64_t M, int64_t N, int64_t K, void* C, int64_t ldc,
+                                      int c_dtype, int fix_nan, uint8_t* c_sc8, float* c_sc32,
+                                      void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  if (M <= 0 || N <= 0 || K <= 0) {
+    if (M < 0 || N < 0 || K < 0) return pratchya_set_error(PRATCHYA_EINVAL, "gemm_fq: negative size");
+    return PRATCHYA_OK;
+  }
+  if (N % 1024)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_fq: N must be a multiple of 1024 (one (1, 128) "
+                              "group of 8 blocks per row segment; got %lld)", (long long)N);
+  GemmPlan P;
+  int rc = gemm_plan("gemm_fq", A, lda, a_sc8, a_sc32, a_rdiv, a_sr, a_sk, a_kg, B, ldb, b_sc8, b_sc32, b_rdiv,
+                     b_sr, b_sk, b_kg, M, N, K, C, ldc, c_dtype, &P);
+  if (rc) return rc;
+  if (P.fine_b)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_fq: B scale groups narrower than 32 rows");
+  if (!c_sc8 || !c_sc32 || !workspace)
+    return pratchya_set_error(PRATCHYA_EINVAL, "gemm_fq: null buffer");
+  if (workspace_bytes < pratchya_gemm_bs_nt_fq_workspace_bytes(M, N) || reinterpret_cast<uintptr_t>(workspace) % 4)
+    return pratchya_set_error(PRATCHYA_EINVAL, "gemm_fq: workspace of %lld bytes (need %lld, 4-byte aligned)",
+                              (long long)workspace_bytes, (long long)pratchya_gemm_bs_nt_fq_workspace_bytes(M, N));
+  // The four workgroups of a strip work in the same round: XCD-aware partners
+  // b, b+8, b+16, b+24 need whole groups of 32 tiles and workgroups, otherwise
+  // partners are four consecutive workgroups.
+  const int64_t tiles = P.tiles_m * P.tiles_n;
+  FqArgs fq{};
+  fq.xcd = tiles % 32 == 0 && P.grid >= 32 ? 1 : 0;
+  P.grid -= P.grid % (fq.xcd ? 32 : 4);
+  uint32_t* ws = static_cast<uint32_t*>(workspace);
+  const int64_t strips = fq_strips(M, N);
+  fq.sc8 = c_sc8;
+  fq.sc32 = c_sc32;
+  fq.gmax = ws;
+  fq.arrive = ws + strips * 256;
+  fq.status = fq.arrive + strips;
+  // maxima, arrival counts and status start at zero (a kernel, not a memset:
+  // safe under graph capture)
+  const int64_t words = fq_workspace_words(M, N);
+  const int64_t fill_blocks = (words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024;
+  hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)fill_blocks), dim3(256), 0, stream, ws, words, 0u);
+  rc = launch_status("gemm_fq");
+  if (rc) return rc;
+  const bool bf = c_dtype == PRATCHYA_DT_BF16;
+  if (bf && fix_nan) gemm_launch<true, false, 2>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+  else if (bf) gemm_launch<true, false, 1>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+  else if (fix_nan) gemm_launch<false, false, 2>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+  else gemm_launch<false, false, 1>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+  return launch_status("gemm_fq");
 }
 
 // --------------------------------------------------------------------------

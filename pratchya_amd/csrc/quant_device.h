@@ -179,6 +179,53 @@ __device__ __forceinline__ uint32_t near_mid8(float t) {
   return (((f2u(t) + 8u - 0x8000u) & 0xFFFFu) <= 16u) ? 1u : 0u;
 }
 
+// Scales of one block for the division-free cast (the arithmetic of
+// k_quant_g8's finite-G path): mb = the block's max |x| bits, Gb = the group's
+// (finite), rcpG128 = rcp(G / 128).  e: the e8m0 byte (exponent difference,
+// exact; e8m0_of where it does not apply: subnormal or zero maxima, r < 2^-126);
+// y: 128 / S to within a few ulp (t = x * y then lies within a few ulp of
+// RN(x / S) * 128, so a t that is not near a bf16 rounding midpoint rounds as
+// the reference's quotient does); clamped: S is the 1e-7 clamp.
+struct BlockScale {
+  uint32_t e;
+  float y;
+  bool clamped;
+};
+__device__ __forceinline__ BlockScale block_scale(uint32_t mb, uint32_t Gb, float rcpG128) {
+  const float G = u2f(Gb);
+  const uint32_t EG = Gb >> 23, fG = Gb & 0x7FFFFFu;
+  const uint32_t Em = mb >> 23, fm = mb & 0x7FFFFFu;
+  const int ef = (int)Em - (int)EG + 127 - (fm < fG ? 1 : 0);
+  uint32_t er = (uint32_t)ef;
+  if (!(EG >= 1u && Em >= 1u && ef >= 1)) er = mb == 0u ? 0u : e8m0_of(u2f(mb), G);
+  const float sG = e8m0_decode(er) * G;
+  const bool cl = !(sG >= kClamp);
+  return {er, cl ? PRATCHYA_Y_CLAMP : u2f((254u - er) << 23) * rcpG128, cl};
+}
+
+// Fake quantization of 4 f32 values of one block, quantize_impl then
+// dequantize_impl (Q:484-499, Q:562-564): the e4m3fn payload word of
+// (x0..x3), dequantized as (f32(q) * dq) / 128 (dq = 2^(e-127) * G, or the
+// repaired scale of quantize_impl_bwd).  finite (G finite): the division-free
+// cast with y from block_scale, words near a bf16 rounding midpoint redone
+// exactly; otherwise the exact composition.  S = quant_scale(e, G).
+__device__ __forceinline__ void fake_quant4(float& x0, float& x1, float& x2, float& x3, float y, float S,
+                                            bool finite, float dq) {
+  uint32_t w;
+  if (finite) {
+    const float t0 = x0 * y, t1 = x1 * y, t2 = x2 * y, t3 = x3 * y;
+    w = cvt4_hw(t0, t1, t2, t3);
+    if (near_mid8(t0) | near_mid8(t1) | near_mid8(t2) | near_mid8(t3)) w = cvt4_exact(x0, x1, x2, x3, S);
+  } else {
+    w = cvt4_exact(x0, x1, x2, x3, S);
+  }
+  fp8_word(w, x0, x1, x2, x3);
+  x0 = (x0 * dq) * 0.0078125f;
+  x1 = (x1 * dq) * 0.0078125f;
+  x2 = (x2 * dq) * 0.0078125f;
+  x3 = (x3 * dq) * 0.0078125f;
+}
+
 // --------------------------------------------------------------------------
 // Kernels shared by the general (multi-launch) quantize paths: workspace
 // fill, and the per-group scales from the block maxima in the workspace

@@ -255,11 +255,15 @@ def _matmul_forward(x8, xs8, xs32, y8, ys8, ys32, gx, gy) -> torch.Tensor:
     return torch.matmul(_deq32(x8, xs8, xs32, gx), _deq32(y8, ys8, ys32, gy))
 
 
-def _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y, pre=None):
+def _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y, pre=None, x_dtype=None):
     """dgrad / wgrad on the FP8 MFMA kernel (the "fp8" backward), or None
     when the layouts do not fit it.  ``pre``: the (1, 128) scales of the
     product's output quantization when ``g`` is the cotangent of that output
-    before dequantize_impl_bwd (the quantizers apply it in registers)."""
+    before dequantize_impl_bwd (the quantizers apply it in registers).
+    Returns ``(gxf, gyf, gx_final)``: with ``x_dtype`` given and x's rows a
+    multiple of 1024 wide, the dgrad GEMM's epilogue also requantizes x's
+    cotangent with x's grid and dequantizes it to ``x_dtype`` as
+    ``_requant_cotangent`` would (``gx_final`` True), bit for bit."""
     if y8.dim() != 2 or tuple(gx) != (1, 128) or tuple(gy)[1] != 128:
         return None
     if _lhs_operand(x8, xs8, xs32, gx) is None:
@@ -271,19 +275,25 @@ def _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y, pre=N
         return None
     g2 = g.reshape(rows, N)
     gxf = gyf = None
+    gx_final = False
     try:
         if need_x:
             gq = K.requantize_cotangent(g2, *pre) if pre is not None else K.quantize(g2.contiguous(), (1, 128))
             op_g = K.operand_rows(*gq, (1, 128))
             op_w = K.operand_rows(y8, ys8, ys32, gy)          # W [K, N]: rows K, contraction N
-            gxf = K.gemm_nt(op_g, op_w, torch.float32).reshape(tuple(g.shape[:-1]) + (Kd,))
+            if x_dtype is not None and Kd % 1024 == 0:
+                gxf = K.gemm_nt_fq(op_g, op_w, x_dtype, fix_nan=True)[0]
+                gx_final = True
+            else:
+                gxf = K.gemm_nt(op_g, op_w, torch.float32)
+            gxf = gxf.reshape(tuple(g.shape[:-1]) + (Kd,))
         if need_y:
             xt = K.quantize_t128(x8.reshape(rows, Kd), xs8, xs32)   # stored activation, requantized
             gt = K.quantize_t128(g2.contiguous(), *(pre if pre is not None else ()))
             gyf = K.gemm_nt(K.operand_t128(*xt), K.operand_t128(*gt), torch.float32)
     except K.PratchyaUnsupported:
         return None
-    return gxf, gyf
+    return gxf, gyf, gx_final
 
 
 def _matmul_cotangents(g, saved, grids, need_x, need_y):
@@ -296,7 +306,7 @@ def _matmul_cotangents(g, saved, grids, need_x, need_y):
     res = _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y) \
         if _backward_mode == "fp8" else None
     if res is not None:
-        return res
+        return res[:2]
     g = g.float()
     gxf = g @ _deq32(y8, ys8, ys32, gy).transpose(-1, -2) if need_x else None
     gyf = _deq32(x8, xs8, xs32, gx).transpose(-1, -2) @ g if need_y else None
@@ -325,6 +335,28 @@ class _Matmul(torch.autograd.Function):
         return grad_x, grad_y, None, None, None, None, None, None, None, None
 
 
+def _linear_forward_fused(x8, xs8, xs32, y8, ys8, ys32, gx, gy, go, dtype):
+    """``QArrayImpl(matmul_impl(x, y), (1, 128)).astype(dtype)`` with the
+    requantization in the GEMM's epilogue: ``(y, sc_fp8, sc_fp32)`` bit-identical
+    to the f32 product followed by ``quantize_dequantize``, or None when the
+    layouts do not fit (grid other than (1, 128), N not a multiple of 1024,
+    operands the GEMM does not tile)."""
+    if tuple(go) != (1, 128) or dtype not in (torch.float32, torch.bfloat16) or y8.dim() != 2:
+        return None
+    N = int(y8.shape[1])
+    if N % 1024:
+        return None
+    op_a = _lhs_operand(x8, xs8, xs32, gx)
+    op_b = _rhs_operand(y8, ys8, ys32, gy) if op_a is not None else None
+    if op_a is None or op_b is None:
+        return None
+    try:
+        res, s8, s32 = K.gemm_nt_fq(op_a, op_b, dtype, lead=tuple(x8.shape[:-1]))
+    except K.PratchyaUnsupported:
+        return None
+    return res.reshape(tuple(x8.shape[:-1]) + (N,)), s8, s32
+
+
 class _QLinear(torch.autograd.Function):
     """``QArrayImpl(matmul_impl(x, y), go).astype(dtype)`` as one node: the
     composition a quantized Linear runs (pratchya/_nnx_impl/_module.py:46-50;
@@ -341,8 +373,12 @@ class _QLinear(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, src_x, src_y, x8, xs8, xs32, y8, ys8, ys32, gx, gy, go, dtype):
-        out = _matmul_forward(x8, xs8, xs32, y8, ys8, ys32, gx, gy)
-        res, os8, os32 = K.quantize_dequantize(out, go, dtype)
+        fused = _linear_forward_fused(x8, xs8, xs32, y8, ys8, ys32, gx, gy, go, dtype)
+        if fused is not None:
+            res, os8, os32 = fused
+        else:
+            out = _matmul_forward(x8, xs8, xs32, y8, ys8, ys32, gx, gy)
+            res, os8, os32 = K.quantize_dequantize(out, go, dtype)
         ctx.saved = (x8, xs8, xs32, y8, ys8, ys32)
         ctx.out_scales = (os8, os32)
         ctx.grids = (gx, gy, go)
@@ -362,15 +398,16 @@ class _QLinear(torch.autograd.Function):
             # the FP8 dgrad / wgrad quantizers take the cotangent through the
             # output's dequantize_impl_bwd themselves (8-block groups: the
             # output's scales index the same way for the flattened rows)
-            res = _fp8_backward(g, *ctx.saved, gx, gy, need_x, need_y, pre=(os8, os32))
+            res = _fp8_backward(g, *ctx.saved, gx, gy, need_x, need_y, pre=(os8, os32), x_dtype=ctx.dtypes[0])
+        gx_final = False
         if res is not None:
-            gxf, gyf = res
+            gxf, gyf, gx_final = res
         else:
             g1 = K.dequantize_bwd(g, os8, os32, go)
             gxf, gyf = _matmul_cotangents(g1, ctx.saved, (gx, gy), need_x, need_y)
         grad_x = grad_y = None
         if need_x:
-            grad_x = _requant_cotangent(_reduce_broadcast(gxf, x8.shape), gx, ctx.dtypes[0])
+            grad_x = gxf if gx_final else _requant_cotangent(_reduce_broadcast(gxf, x8.shape), gx, ctx.dtypes[0])
         if need_y:
             grad_y = _requant_cotangent(_reduce_broadcast(gyf, y8.shape), gy, ctx.dtypes[1])
         return (grad_x, grad_y) + (None,) * 10

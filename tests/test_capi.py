@@ -90,6 +90,33 @@ def test_noalloc_quantize_arguments_without_gpu():
                                          None) == _lib.EINVAL
 
 
+def test_gemm_fq_arguments_without_gpu():
+    """pratchya_gemm_bs_nt_fq: workspace query, and argument checks that
+    return before any launch (N not a multiple of 1024, narrow B groups, null
+    or short workspace)."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    # per 256-row x 1024-column strip: 256 maxima + one count, then a status word; 256-byte multiple
+    assert lib.pratchya_gemm_bs_nt_fq_workspace_bytes(512, 2048) == ((2 * 2 * 257 + 1) * 4 + 255) // 256 * 256
+    assert lib.pratchya_gemm_bs_nt_fq_workspace_bytes(300, 1024) == ((2 * 257 + 1) * 4 + 255) // 256 * 256
+    assert lib.pratchya_gemm_bs_nt_fq_workspace_bytes(512, 768) == 0
+    fake = ctypes.c_void_p(1 << 20)          # aligned, never dereferenced
+    act = (1, 2, 1, 8)                       # (1,128) rows, K = 256
+    wgt = (128, 1, 8, 1024)                  # (128,128) weight used transposed
+    args = lambda N, bdesc, ws, ws_bytes: (fake, 256, fake, fake, *act, fake, 256, fake, fake, *bdesc,
+                                           512, N, 256, fake, N, _lib.DT_BF16, 0, fake, fake, ws, ws_bytes, None)
+    need = lib.pratchya_gemm_bs_nt_fq_workspace_bytes(512, 1024)
+    assert lib.pratchya_gemm_bs_nt_fq(*args(768, wgt, fake, need)) == _lib.EUNSUPPORTED
+    assert b"1024" in lib.pratchya_last_error()
+    assert lib.pratchya_gemm_bs_nt_fq(*args(1024, (1, 1, 1024, 8), fake, need)) == _lib.EUNSUPPORTED
+    assert lib.pratchya_gemm_bs_nt_fq(*args(1024, wgt, None, need)) == _lib.EINVAL
+    assert lib.pratchya_gemm_bs_nt_fq(*args(1024, wgt, fake, need - 4)) == _lib.EINVAL
+    assert b"workspace" in lib.pratchya_last_error()
+    empty = (fake, 256, fake, fake, *act, fake, 256, fake, fake, *wgt, 0, 1024, 256, fake, 1024, _lib.DT_BF16, 0,
+             fake, fake, fake, 0, None)
+    assert lib.pratchya_gemm_bs_nt_fq(*empty) == 0
+
+
 def test_invalid_tgrid_is_einval_without_launch():
     from pratchya_amd import _lib
     lib = _lib.load()

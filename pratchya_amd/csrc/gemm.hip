@@ -424,8 +424,8 @@ __device__ __forceinline__ void store_tile(const v16f (&acc)[2][4], const float 
 // it), each row's max |x| over this wave's 128 columns (one block; lanes l32
 // and l32 + 32 hold row mi * 32 + l32's values, 64 each), the group max over
 // the strip's 8 blocks by the exchange described at FqArgs, and the scales of
-// row lhi * 32 + l32 into this wave's 64-entry table in LDS (y, S, dq, e and
-// whether G is finite, 16 bytes per row).  Writes the output scales of rows
+// row lhi * 32 + l32 into this wave's 64-entry table in LDS (16 bytes per
+// row: y, S, the dequantization factor, and flags: G finite, one multiply).  Writes the output scales of rows
 // below M.
 constexpr int FQ_TABLE_BYTES = 8 * 64 * 16;
 
@@ -484,8 +484,10 @@ __device__ __forceinline__ void fq_row_scales(v16f (&acc)[2][4], const float (&g
     bs.clamped = false;
   }
   const uint32_t ed = (FIXNAN && bs.e == 0xFFu) ? 0x7Fu : bs.e;
+  const float dq = e8m0_decode(ed) * G;
+  const bool one = dequant_one_mul(dq);
   *reinterpret_cast<v4f*>(table + (lhi * 32 + l32) * 16) =
-      v4f{bs.y, quant_scale(bs.e, G), e8m0_decode(ed) * G, u2f(fin ? 1u : 0u)};
+      v4f{bs.y, quant_scale(bs.e, G), one ? dq * 0.0078125f : dq, u2f((fin ? 1u : 0u) | (one ? 2u : 0u))};
   // scales of the lane's row: its e8m0 byte for this block, and its group
   // max from the strip's first tile, left wave
   const int row = row0 + lhi * 32 + l32;
@@ -510,6 +512,8 @@ __device__ __forceinline__ void store_tile_fq(const v16f (&acc)[2][4], uint8_t* 
   constexpr int RP = 16;                    // rows staged per pass
   static_assert(8 * RP * PITCH <= STAGE_BYTES, "staging must fit one stage buffer");
   uint8_t* stg = stage + wave * (RP * PITCH);
+  // the wave's output rows start at Cw; a row offset fits 32 bits (64 rows, ldc below 2^23)
+  uint8_t* const Cw = static_cast<uint8_t*>(C) + ((int64_t)row0 * ldc + col0) * OSZ;
   __syncthreads();                          // every wave is done with the stage buffer
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi) {
@@ -530,10 +534,11 @@ __device__ __forceinline__ void store_tile_fq(const v16f (&acc)[2][4], uint8_t* 
         const int rw = mi * 32 + p * 16 + r;   // row within the wave's 64
         v4f x = *reinterpret_cast<const v4f*>(stg + r * PITCH + l32 * 16);
         const v4f sc = *reinterpret_cast<const v4f*>(table + rw * 16);
+        const uint32_t flags = f2u(sc.w);
         float x0 = x.x, x1 = x.y, x2 = x.z, x3 = x.w;
-        fake_quant4(x0, x1, x2, x3, sc.x, sc.y, f2u(sc.w) != 0u, sc.z);
+        fake_quant4(x0, x1, x2, x3, sc.x, sc.y, (flags & 1u) != 0u, sc.z, (flags & 2u) != 0u);
         if (row0 + rw < M) {
-          uint8_t* dst = static_cast<uint8_t*>(C) + ((int64_t)(row0 + rw) * ldc + col0 + l32 * 4) * OSZ;
+          uint8_t* dst = Cw + (uint32_t)((rw * (int)ldc + l32 * 4) * OSZ);
           if constexpr (OUT_BF16) {
             __builtin_nontemporal_store(u32x2_t{pack_bf16x2(x0, x1), pack_bf16x2(x2, x3)},
                                         reinterpret_cast<u32x2_t*>(dst));
@@ -1007,6 +1012,8 @@ extern "C" int pratchya_gemm_bs_nt_fq(const uint8_t* A, int64_t lda, const uint8
   if (rc) return rc;
   if (P.fine_b)
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_fq: B scale groups narrower than 32 rows");
+  if (ldc >= (int64_t)1 << 23)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_fq: output row stride of 2^23 elements or more");
   if (!c_sc8 || !c_sc32 || !workspace)
     return pratchya_set_error(PRATCHYA_EINVAL, "gemm_fq: null buffer");
   if (workspace_bytes < pratchya_gemm_bs_nt_fq_workspace_bytes(M, N) || reinterpret_cast<uintptr_t>(workspace) % 4)

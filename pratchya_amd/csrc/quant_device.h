@@ -207,23 +207,43 @@ __device__ __forceinline__ BlockScale block_scale(uint32_t mb, uint32_t Gb, floa
 // dequantize_impl (Q:484-499, Q:562-564): the e4m3fn payload word of
 // (x0..x3), dequantized as (f32(q) * dq) / 128 (dq = 2^(e-127) * G, or the
 // repaired scale of quantize_impl_bwd).  finite (G finite): the division-free
-// cast with y from block_scale, words near a bf16 rounding midpoint redone
-// exactly; otherwise the exact composition.  S = quant_scale(e, G).
+// cast with y from block_scale, a word with a value near a bf16 rounding
+// midpoint (the near_mid8 test, as one compare of the smallest distance)
+// redone exactly; otherwise the exact composition.  S = quant_scale(e, G).
+// dqx = dq / 128 when one_mul (see dequant_one_mul), else dq.
 __device__ __forceinline__ void fake_quant4(float& x0, float& x1, float& x2, float& x3, float y, float S,
-                                            bool finite, float dq) {
+                                            bool finite, float dqx, bool one_mul) {
   uint32_t w;
   if (finite) {
     const float t0 = x0 * y, t1 = x1 * y, t2 = x2 * y, t3 = x3 * y;
     w = cvt4_hw(t0, t1, t2, t3);
-    if (near_mid8(t0) | near_mid8(t1) | near_mid8(t2) | near_mid8(t3)) w = cvt4_exact(x0, x1, x2, x3, S);
+    const uint32_t d0 = (f2u(t0) + 0x8008u) & 0xFFFFu, d1 = (f2u(t1) + 0x8008u) & 0xFFFFu;
+    const uint32_t d2 = (f2u(t2) + 0x8008u) & 0xFFFFu, d3 = (f2u(t3) + 0x8008u) & 0xFFFFu;
+    const uint32_t dmin = d0 < d1 ? d0 : d1, dmin2 = d2 < d3 ? d2 : d3;
+    if ((dmin < dmin2 ? dmin : dmin2) <= 16u) w = cvt4_exact(x0, x1, x2, x3, S);
   } else {
     w = cvt4_exact(x0, x1, x2, x3, S);
   }
   fp8_word(w, x0, x1, x2, x3);
-  x0 = (x0 * dq) * 0.0078125f;
-  x1 = (x1 * dq) * 0.0078125f;
-  x2 = (x2 * dq) * 0.0078125f;
-  x3 = (x3 * dq) * 0.0078125f;
+  if (one_mul) {
+    x0 *= dqx;
+    x1 *= dqx;
+    x2 *= dqx;
+    x3 *= dqx;
+  } else {
+    x0 = (x0 * dqx) * 0.0078125f;
+    x1 = (x1 * dqx) * 0.0078125f;
+    x2 = (x2 * dqx) * 0.0078125f;
+    x3 = (x3 * dqx) * 0.0078125f;
+  }
+}
+
+// (f32(q) * dq) / 128 equals f32(q) * (dq / 128) for every e4m3fn q when
+// 2^-110 <= dq < 2^118: dq / 128 is exact, no product of a nonzero q
+// (2^-9 <= |q| <= 448) is subnormal or overflows in either order, and scaling
+// by 2^-7 commutes with rounding for normal results (NaN and zero q agree).
+__device__ __forceinline__ bool dequant_one_mul(float dq) {
+  return dq >= 0x1p-110f && dq < 0x1p118f;
 }
 
 // --------------------------------------------------------------------------

@@ -302,6 +302,22 @@ int pratchya_gemm_bs_nt_fq(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, 
                            uint8_t* c_sc8, float* c_sc32, void* workspace, int64_t workspace_bytes,
                            hipStream_t stream);
 
+/* bf16 GEMM, "NT" form:                  replaces the bf16 dots of newton_schulz
+ *   C[m, n] = sum_k A[m, k] * B[n, k]     (pratchya/_nnx_impl/_optimizer.py:20-22,
+ * A @ A.T and (A @ A.T) @ A in the leaf's dtype; jnp's bf16 dot accumulates in f32)
+ * with f32 accumulation.  A: bf16 [M, K] (row stride lda elements), B: bf16
+ * [N, K] (ldb); lda, ldb multiples of 8, buffers 16-byte aligned.  C: [M, N]
+ * (ldc), c_dtype f32 or bf16 (rounded once, RNE).  K a multiple of 64
+ * (PRATCHYA_EUNSUPPORTED otherwise); M, N and short operands as
+ * pratchya_gemm_bs_nt (an operand of fewer than 256 rows is read as 256). */
+int pratchya_gemm_bf16_nt(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
+                          int64_t K, void* C, int64_t ldc, int c_dtype, hipStream_t stream);
+
+/* 16-bit transpose: src [rows, cols] -> dst [cols, rows] (bf16 X -> X.T, the
+ * K-contiguous operand of the Newton-Schulz product (X X^T) X,
+ * _optimizer.py:21).  rows and cols multiples of 8, buffers 16-byte aligned. */
+int pratchya_transpose_b16(const void* src, int64_t rows, int64_t cols, void* dst, hipStream_t stream);
+
 /* Span of an operand's scale layout: the largest P such that every row's group
  * index is constant over each aligned run of P 128-wide K blocks (the GEMM
  * reloads group maxima and rescales its accumulator at multiples of it);

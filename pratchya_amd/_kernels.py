@@ -494,7 +494,7 @@ def _tile_readable(p: torch.Tensor) -> torch.Tensor:
     if rows >= GEMM_TILE_ROWS:
         return p
     avail = p.untyped_storage().nbytes() - p.storage_offset() * p.element_size()
-    if avail >= GEMM_TILE_ROWS * K:
+    if avail >= GEMM_TILE_ROWS * K * p.element_size():
         return p
     padded = torch.zeros((GEMM_TILE_ROWS, K), dtype=p.dtype, device=p.device)
     padded[:rows].copy_(p)
@@ -533,6 +533,38 @@ def gemm_nt(a: Operand, b: Operand, out_dtype: torch.dtype = torch.bfloat16,
                                        _ptr(bp), K, _ptr(bs8), _ptr(bs32), *b.desc,
                                        M, N, K, _ptr(out), out.stride(0), _dtype_code(out.dtype),
                                        _stream(ap)), "gemm")
+    return out
+
+
+def gemm_bf16_nt(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """C[M, N] = a @ b^T for bf16 ``a`` [M, K] and ``b`` [N, K] with f32
+    accumulation, rounded once to ``out_dtype``: the bf16 dots of
+    newton_schulz (pratchya/_nnx_impl/_optimizer.py:20-22) on the MFMA kernel.
+    K must be a multiple of 64 (``PratchyaUnsupported`` otherwise)."""
+    _require_gpu(a, b)
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16 or a.dim() != 2 or b.dim() != 2:
+        raise ValueError("gemm_bf16_nt: a and b must be 2-D bfloat16")
+    if a.shape[1] != b.shape[1]:
+        raise ValueError(f"contraction mismatch: {a.shape[1]} vs {b.shape[1]}")
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"gemm_bf16_nt: output dtype {out_dtype} is not float32 or bfloat16")
+    M, N, Kd = int(a.shape[0]), int(b.shape[0]), int(a.shape[1])
+    ap, bp = _tile_readable(a.contiguous()), _tile_readable(b.contiguous())
+    out = torch.empty((M, N), dtype=out_dtype, device=ap.device)
+    _lib.check(_lib.load().pratchya_gemm_bf16_nt(_ptr(ap), Kd, _ptr(bp), Kd, M, N, Kd, _ptr(out), N,
+                                                 _dtype_code(out_dtype), _stream(ap)), "gemm_bf16")
+    return out
+
+
+def transpose_b16(x: torch.Tensor) -> torch.Tensor:
+    """[rows, cols] 16-bit matrix -> its transpose [cols, rows], contiguous."""
+    _require_gpu(x)
+    if x.dim() != 2 or x.element_size() != 2:
+        raise ValueError("transpose_b16: a 2-D 16-bit tensor is required")
+    src = x.contiguous()
+    R, C = int(src.shape[0]), int(src.shape[1])
+    out = torch.empty((C, R), dtype=x.dtype, device=src.device)
+    _lib.check(_lib.load().pratchya_transpose_b16(_ptr(src), R, C, _ptr(out), _stream(src)), "transpose_b16")
     return out
 
 

@@ -69,6 +69,9 @@ SIGNATURES = {
                                         _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_int, _c_int, _c_p, _c_p,
                                         _c_p, _c_i64, _c_p]),
     "pratchya_gemm_bs_nt_fq_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "pratchya_gemm_bf16_nt": (_c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64,
+                                       _c_int, _c_p]),
+    "pratchya_transpose_b16": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "pratchya_gemm_span": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
     "pratchya_transpose_u8": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "pratchya_debug_bf16_to_e4m3": (_c_int, [_c_p, _c_p, _c_i64, _c_int, _c_p]),

@@ -109,20 +109,34 @@ __device__ __forceinline__ v8i read_frag2(const uint8_t* base_lo, const uint8_t*
 }
 
 // One 32x32x64 MFMA of output tile (MI, NI): a-operand = B rows (e8m0 byte NI
-// of eB), b-operand = A rows (byte MI of eA); op_sel picks the byte.
-template <int MI, int NI>
+// of eB), b-operand = A rows (byte MI of eA); op_sel picks the byte.  BF: the
+// operands are bf16 (a 32-byte fragment is 16 K values), two 32x32x16 bf16
+// MFMAs on the fragments' first and second 16 bytes (A and B present their K
+// values in the same order, so the dot product is the same).
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+template <int MI, int NI, bool BF = false>
 __device__ __forceinline__ void mfma_tile(v16f (&acc)[2][4], const v8i (&fa)[2], const v8i (&fb)[4],
                                           uint32_t eA, uint32_t eB) {
-  acc[MI][NI] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[NI], fa[MI], acc[MI][NI], 0, 0, NI,
-                                                               (int)eB, MI, (int)eA);
+  if constexpr (BF) {
+    const v8i a = fb[NI], b = fa[MI];
+    const bf16x8_t a0 = __builtin_bit_cast(bf16x8_t, v4i{a.s0, a.s1, a.s2, a.s3});
+    const bf16x8_t a1 = __builtin_bit_cast(bf16x8_t, v4i{a.s4, a.s5, a.s6, a.s7});
+    const bf16x8_t b0 = __builtin_bit_cast(bf16x8_t, v4i{b.s0, b.s1, b.s2, b.s3});
+    const bf16x8_t b1 = __builtin_bit_cast(bf16x8_t, v4i{b.s4, b.s5, b.s6, b.s7});
+    acc[MI][NI] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc[MI][NI], 0, 0, 0);
+    acc[MI][NI] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc[MI][NI], 0, 0, 0);
+  } else {
+    acc[MI][NI] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[NI], fa[MI], acc[MI][NI], 0, 0, NI,
+                                                                 (int)eB, MI, (int)eA);
+  }
 }
 
 // One MFMA whose result is pinned right after it: the asm's memory clobber
 // keeps the stage DMA issued between MFMAs from being reordered around it.
-template <int MI, int NI>
+template <int MI, int NI, bool BF = false>
 __device__ __forceinline__ void mfma_pinned(v16f (&acc)[2][4], const v8i (&fa)[2], const v8i (&fb)[4],
                                             uint32_t eA, uint32_t eB) {
-  mfma_tile<MI, NI>(acc, fa, fb, eA, eB);
+  mfma_tile<MI, NI, BF>(acc, fa, fb, eA, eB);
   asm volatile("" : "+v"(acc[MI][NI]) : : "memory");
 }
 
@@ -553,7 +567,7 @@ __device__ __forceinline__ void store_tile_fq(const v16f (&acc)[2][4], uint8_t* 
   }
 }
 
-template <bool OUT_BF16, bool FINE_B, int FQ>
+template <bool OUT_BF16, bool FINE_B, int FQ, bool BF = false>
 __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     Scales sa, Scales sb, void* __restrict__ C, int64_t ldc, int K, int span, int tiles_m,
@@ -637,12 +651,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   // buffer g_st, g_first (a tile's K block 0).
 #pragma unroll
   for (int i = 0; i < 8; ++i) dma_rows(h, cur, lds, 0, i);
-  dma_scales(h, cur, lds, 0);
-  float g_ld = load_g(h, cur, 0), u_prev = 1.0f;
+  float g_ld = 0.0f, u_prev = 1.0f;
+  if constexpr (!BF) {
+    dma_scales(h, cur, lds, 0);
+    g_ld = load_g(h, cur, 0);
+  }
   uint8_t* g_st = lds;
   bool g_first = true, g_pub = true;
   __builtin_amdgcn_s_waitcnt(0);
-  publish_g(h, lds, g_st, g_ld, g_first, u_prev);
+  if constexpr (!BF) publish_g(h, lds, g_st, g_ld, g_first, u_prev);
   __syncthreads();
 
   for (;;) {
@@ -660,9 +677,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
         uint8_t* s1 = lds + ((1 + par) & 1) * STAGE_BYTES;
 #pragma unroll
         for (int i = 0; i < 8; ++i) dma_rows(h, cur, s1, 1, i);
-        dma_scales(h, cur, s1, 1);
-        g_pub = span == 1;
-        if (g_pub) g_ld = load_g(h, cur, 1);
+        if constexpr (!BF) {
+          dma_scales(h, cur, s1, 1);
+          g_pub = span == 1;
+          if (g_pub) g_ld = load_g(h, cur, 1);
+        }
         g_st = s1;
         g_first = false;
       }
@@ -671,11 +690,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     // e8m0 byte position inside the DMA'd word of each compute row at kb = 0,
     // 2 bits per row: A rows i = 0, 1 in bits 2i, B rows i = 0..3 in bits 4 + 2i
     uint32_t epos = 0;
+    if constexpr (!BF) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) epos |= ((uint32_t)blk_index(sa, m0 + wm * 64 + i * 32 + l32, 0) & 3u) << (2 * i);
+      for (int i = 0; i < 2; ++i)
+        epos |= ((uint32_t)blk_index(sa, m0 + wm * 64 + i * 32 + l32, 0) & 3u) << (2 * i);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      epos |= ((uint32_t)blk_index(sb, n0 + wn * 128 + i * 32 + l32, 0) & 3u) << (4 + 2 * i);
+      for (int i = 0; i < 4; ++i)
+        epos |= ((uint32_t)blk_index(sb, n0 + wn * 128 + i * 32 + l32, 0) & 3u) << (4 + 2 * i);
+    }
 
     v16f acc[2][4];
 #pragma unroll
@@ -689,7 +711,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         // ---- memory phase ----
-        if (ks == 0) {
+        if (ks == 0 && !BF) {
           // group 0 publishes its half of stage kt here (it landed at the end
           // of the previous phase); its own waves read only their own rows'
           // ratios, group 1 reads them one phase later
@@ -739,7 +761,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
         fb[3] = read_frag2<OFF_B + 96 * BK>(blo, bhi);
         if (grp == 1 && ks == 1 && kt + 1 < nk) {
           PINNED_WAITCNT(0);        // also group 1's half of stage kt+1 landed
-          if (g_pub) publish_g(h, lds, g_st, g_ld, g_first, u_prev);
+          if (!BF && g_pub) publish_g(h, lds, g_st, g_ld, g_first, u_prev);
         }
         PINNED_WAITCNT(0xC07F);     // lgkmcnt(0): operands in registers, stage reads (and writes) done
         wg_barrier();
@@ -765,25 +787,25 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
         const uint32_t soff0 = dr.row0 * h.ld + (uint32_t)lkt * BK;
         uint8_t* const lds0 = dst + h.lds_pay;
         pin_frags(fa, fb);
-        mfma_pinned<0, 0>(acc, fa, fb, eA, eB);
+        mfma_pinned<0, 0, BF>(acc, fa, fb, eA, eB);
         if (dma_now) { dma_rows_at(h, soff0, lds0, 0); dma_rows_at(h, soff0, lds0, 1); }
-        mfma_pinned<0, 1>(acc, fa, fb, eA, eB);
+        mfma_pinned<0, 1, BF>(acc, fa, fb, eA, eB);
         if (dma_now) { dma_rows_at(h, soff0, lds0, 2); dma_rows_at(h, soff0, lds0, 3); }
-        mfma_pinned<0, 2>(acc, fa, fb, eA, eB);
+        mfma_pinned<0, 2, BF>(acc, fa, fb, eA, eB);
         if (dma_now) { dma_rows_at(h, soff0, lds0, 4); dma_rows_at(h, soff0, lds0, 5); }
-        mfma_pinned<0, 3>(acc, fa, fb, eA, eB);
+        mfma_pinned<0, 3, BF>(acc, fa, fb, eA, eB);
         if (dma_now) { dma_rows_at(h, soff0, lds0, 6); dma_rows_at(h, soff0, lds0, 7); }
-        mfma_pinned<1, 0>(acc, fa, fb, eA, eB);
-        if (dma_now) {
+        mfma_pinned<1, 0, BF>(acc, fa, fb, eA, eB);
+        if (dma_now && !BF) {
           dma_scales(h, dr, dst, lkt);
           g_pub = lkt % span == 0;
           if (g_pub) g_ld = load_g(h, dr, lkt);
           g_st = dst;
           g_first = lkt == 0;
         }
-        mfma_pinned<1, 1>(acc, fa, fb, eA, eB);
-        mfma_pinned<1, 2>(acc, fa, fb, eA, eB);
-        mfma_pinned<1, 3>(acc, fa, fb, eA, eB);
+        mfma_pinned<1, 1, BF>(acc, fa, fb, eA, eB);
+        mfma_pinned<1, 2, BF>(acc, fa, fb, eA, eB);
+        mfma_pinned<1, 3, BF>(acc, fa, fb, eA, eB);
         pin_acc(acc);
         if (grp == 0 && ks == 1 && kt + 1 < nk) PINNED_WAITCNT(0);   // group 0's half of stage kt+1 landed
         wg_barrier();
@@ -794,7 +816,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     // units of the last span; the last stage's buffer holds no pending load:
     // stage the output there
     float gA[2], gB[4][NJ];
-    load_units<FINE_B>(lds + OFF_UA, lds + OFF_UB, wm, wn, lane, gA, gB);
+    if constexpr (BF) {
+      // no scales: gA * gB / 2^14 = 1
+#pragma unroll
+      for (int i = 0; i < 2; ++i) gA[i] = 128.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) gB[i][j] = 128.0f;
+    } else {
+      load_units<FINE_B>(lds + OFF_UA, lds + OFF_UB, wm, wn, lane, gA, gB);
+    }
     if constexpr (FQ != 0) {
       static_assert(!FINE_B, "output requantization takes B scale groups of 32 rows or more");
       uint8_t* table = lds + LDS_BYTES + wave * 64 * 16;
@@ -815,7 +847,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     // the next tile's stage 0 (and this tile's output stores) complete, and
     // every wave is done with the staging buffer
     __builtin_amdgcn_s_waitcnt(0);
-    publish_g(h, lds, g_st, g_ld, g_first, u_prev);
+    if constexpr (!BF) publish_g(h, lds, g_st, g_ld, g_first, u_prev);
     __syncthreads();
   }
 }
@@ -1048,6 +1080,55 @@ extern "C" int pratchya_gemm_bs_nt_fq(const uint8_t* A, int64_t lda, const uint8
   return launch_status("gemm_fq");
 }
 
+extern "C" int pratchya_gemm_bf16_nt(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
+                                     int64_t K, void* C, int64_t ldc, int c_dtype, hipStream_t stream) {
+  if (M <= 0 || N <= 0 || K <= 0) {
+    if (M < 0 || N < 0 || K < 0) return pratchya_set_error(PRATCHYA_EINVAL, "gemm_bf16: negative size");
+    return PRATCHYA_OK;
+  }
+  if (K % 64)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_bf16: K must be a multiple of 64 (got %lld)", (long long)K);
+  const bool bf = c_dtype == PRATCHYA_DT_BF16;
+  if (c_dtype != PRATCHYA_DT_F32 && !bf)
+    return pratchya_set_error(PRATCHYA_EINVAL, "gemm_bf16: unsupported output dtype %d", c_dtype);
+  if (N < BN && N % (bf ? 8 : 4))
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_bf16: N below 256 must be a multiple of %d (got %lld)",
+                              bf ? 8 : 4, (long long)N);
+  if (!A || !B || !C) return pratchya_set_error(PRATCHYA_EINVAL, "gemm_bf16: null buffer");
+  if (lda < K || ldb < K || ldc < N || lda % 8 || ldb % 8 || ldc % (bf ? 8 : 4) ||
+      (reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C)) % 16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "gemm_bf16: leading dimensions / alignment not supported");
+  // the kernel addresses the operands as byte matrices: a 128-byte stage row
+  // holds 64 bf16 values of K
+  GemmPlan P{};
+  P.sa = Scales{nullptr, nullptr, 1, 0, 0, 1};
+  P.sb = P.sa;
+  P.span = 1;
+  P.fine_b = false;
+  const int64_t Ma = M < BM ? BM : M, Na = N < BN ? BN : N;
+  P.a_bytes = ((Ma - 1) * lda + K) * 2;
+  P.b_bytes = ((Na - 1) * ldb + K) * 2;
+  if (P.a_bytes > (int64_t)INT32_MAX || P.b_bytes > (int64_t)INT32_MAX)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_bf16: operands beyond 2 GiB");
+  P.tiles_m = (M + BM - 1) / BM;
+  P.tiles_n = (N + BN - 1) / BN;
+  if (P.tiles_m * P.tiles_n > INT32_MAX)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_bf16: too many output tiles");
+  const int64_t tiles = P.tiles_m * P.tiles_n, cus = gemm_num_cus();
+  P.grid = tiles < cus ? tiles : cus;
+  const FqArgs none{};
+  const uint8_t* a8 = static_cast<const uint8_t*>(A);
+  const uint8_t* b8 = static_cast<const uint8_t*>(B);
+#define PRATCHYA_GEMM_BF16(OB)                                                                              \
+  hipLaunchKernelGGL((k_gemm_bs_nt<OB, false, 0, true>), dim3((unsigned)P.grid), dim3(NTHREADS), 0, stream, a8, \
+                     lda * 2, b8, ldb * 2, P.sa, P.sb, C, ldc, (int)(K * 2), 1, (int)P.tiles_m, (int)P.tiles_n,    \
+                     (uint32_t)P.a_bytes, (uint32_t)P.b_bytes, 0u, 0u, 0u, 0u, (int)M, (int)N, none)
+  if (bf) PRATCHYA_GEMM_BF16(true);
+  else PRATCHYA_GEMM_BF16(false);
+#undef PRATCHYA_GEMM_BF16
+  return launch_status("gemm_bf16");
+}
+
 // --------------------------------------------------------------------------
 // Byte transpose [rows, cols] -> [cols, rows] (fp8 payloads: W [K, N] to the
 // K-contiguous [N, K] operand layout, token-major payloads to channel-major).
@@ -1093,7 +1174,61 @@ __global__ __launch_bounds__(256) void k_transpose_u8(const uint8_t* __restrict_
       *reinterpret_cast<uint4*>(dst + gr * rows + gc) = make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
+
+// 16-bit transpose [rows, cols] -> [cols, rows] (bf16 matrices: the
+// K-contiguous layout of X^T for the Newton-Schulz products).  64x64 tiles
+// through LDS (rows padded to 33 words: the column gathers hit 32 banks);
+// 16-byte global loads and stores of 8 elements.
+__global__ __launch_bounds__(256) void k_transpose_u16(const uint16_t* __restrict__ src, int64_t rows,
+                                                       int64_t cols, uint16_t* __restrict__ dst) {
+  __shared__ uint32_t tile[64][33];   // 64 rows x 64 elements (+1 word pad)
+  const int64_t tiles_c = (cols + 63) / 64;
+  const int64_t r0 = ((int64_t)blockIdx.x / tiles_c) * 64, c0 = ((int64_t)blockIdx.x % tiles_c) * 64;
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int i = t + 256 * h, r = i >> 3, q = i & 7;   // row r, 8-element piece q
+    const int64_t gr = r0 + r, gc = c0 + q * 8;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (gr < rows && gc + 8 <= cols) v = *reinterpret_cast<const uint4*>(src + gr * cols + gc);
+    tile[r][q * 4 + 0] = v.x;
+    tile[r][q * 4 + 1] = v.y;
+    tile[r][q * 4 + 2] = v.z;
+    tile[r][q * 4 + 3] = v.w;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int i = t + 256 * h, c = i >> 3, q = i & 7;   // output row c (= input column), input rows 8q..8q+7
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t lo = tile[q * 8 + 2 * k][c >> 1], hi = tile[q * 8 + 2 * k + 1][c >> 1];
+      const int sh = 16 * (c & 1);
+      w[k] = ((lo >> sh) & 0xFFFFu) | (((hi >> sh) & 0xFFFFu) << 16);
+    }
+    const int64_t gr = c0 + c, gc = r0 + q * 8;
+    if (gr < cols && gc + 8 <= rows)
+      *reinterpret_cast<uint4*>(dst + gr * rows + gc) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
 }  // namespace
+
+extern "C" int pratchya_transpose_b16(const void* src, int64_t rows, int64_t cols, void* dst, hipStream_t stream) {
+  if (rows < 0 || cols < 0) return pratchya_set_error(PRATCHYA_EINVAL, "transpose_b16: negative size");
+  if (rows == 0 || cols == 0) return PRATCHYA_OK;
+  if (!src || !dst) return pratchya_set_error(PRATCHYA_EINVAL, "transpose_b16: null buffer");
+  if (rows % 8 || cols % 8 || reinterpret_cast<uintptr_t>(src) % 16 || reinterpret_cast<uintptr_t>(dst) % 16)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED,
+                              "transpose_b16: sizes must be multiples of 8, buffers 16-byte aligned");
+  const int64_t tiles = ((rows + 63) / 64) * ((cols + 63) / 64);
+  if (tiles > INT32_MAX) return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "transpose_b16: more than 2^31 tiles");
+  hipLaunchKernelGGL(k_transpose_u16, dim3((unsigned)tiles), dim3(256), 0, stream,
+                     static_cast<const uint16_t*>(src), rows, cols, static_cast<uint16_t*>(dst));
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return pratchya_set_error(PRATCHYA_EHIP, "transpose_b16: %s", hipGetErrorString(e));
+  return PRATCHYA_OK;
+}
 
 extern "C" int pratchya_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* dst,
                                      hipStream_t stream) {

@@ -13,8 +13,9 @@ Per quantized leaf the step is
     momentum from the quantized momentum and gradient in one kernel, the new
     momentum requantized with the parameter's block grid;
   * Muon for 2-D slices not named ``embed_tokens`` / ``lm_head``:
-    ``newton_schulz(c)`` (5 iterations of two GEMMs on the BLAS library),
-    scaled by ``sqrt(max(N, M))``; Lion otherwise: ``sign(c)``;
+    ``newton_schulz(c)`` (5 iterations of two GEMMs: bf16 on the bf16 MFMA
+    kernel, f32 on the BLAS library), scaled by ``sqrt(max(N, M))``; Lion
+    otherwise: ``sign(c)``;
   * the update pass on the GPU (``pratchya_apply_update``):
     ``-(lr * u + lr * wd * p)`` with the quantized parameter dequantized in
     registers.
@@ -51,7 +52,8 @@ def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
     """Orthogonalization by the cubic Newton-Schulz iteration
     (``_optimizer.py:11-29``): ``X = G / (||G||_F + 1e-7)`` (the transpose of a
     tall ``G``), then ``steps`` times ``X = 1.5 X - 0.5 (X X^T) X``, in ``G``'s
-    dtype.  The products run on the BLAS library (f32 accumulation)."""
+    dtype.  bf16 products run on the bf16 MFMA kernel (``pratchya_gemm_bf16_nt``),
+    others on the BLAS library (f32 accumulation)."""
     m, n = G.shape
     transpose = m > n
     # A tall G is iterated untransposed: with Y = X^T = G / (||G|| + eps),
@@ -62,8 +64,19 @@ def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
     X = G.contiguous()
     X = X / (torch.sqrt(torch.sum(X * X)) + 1e-7)
     fused = X.dtype in (torch.bfloat16, torch.float32)
+    # bf16 leaves run both products on the bf16 MFMA kernel (NT form: rows of
+    # both operands K-contiguous), with one transposing copy per iteration;
+    # other dtypes and sizes use the BLAS library (f32 accumulation either way).
+    on_kernel = X.dtype == torch.bfloat16 and m % 64 == 0 and n % 64 == 0
     for _ in range(steps):
-        if transpose:
+        if on_kernel and transpose:
+            Xt = K.transpose_b16(X)                  # [n, m]
+            A = K.gemm_bf16_nt(Xt, Xt)               # X^T X        [n, n]
+            B = K.gemm_bf16_nt(X, A)                 # X A (A = A^T) [m, n]
+        elif on_kernel:
+            A = K.gemm_bf16_nt(X, X)                 # X X^T        [m, m]
+            B = K.gemm_bf16_nt(A, K.transpose_b16(X))   # A X       [m, n]
+        elif transpose:
             A = X.T @ X
             B = X @ A
         else:

@@ -117,6 +117,27 @@ def test_gemm_fq_arguments_without_gpu():
     assert lib.pratchya_gemm_bs_nt_fq(*empty) == 0
 
 
+def test_bf16_gemm_and_transpose_arguments_without_gpu():
+    """pratchya_gemm_bf16_nt and pratchya_transpose_b16 reject unsupported
+    shapes and bad arguments before any launch."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)          # aligned, never dereferenced
+    assert lib.pratchya_gemm_bf16_nt(fake, 96, fake, 96, 256, 256, 96, fake, 256, _lib.DT_BF16,
+                                     None) == _lib.EUNSUPPORTED
+    assert b"multiple of 64" in lib.pratchya_last_error()
+    assert lib.pratchya_gemm_bf16_nt(fake, 128, fake, 128, 256, 100, 128, fake, 100, _lib.DT_BF16,
+                                     None) == _lib.EUNSUPPORTED
+    assert lib.pratchya_gemm_bf16_nt(None, 128, fake, 128, 256, 256, 128, fake, 256, _lib.DT_F32,
+                                     None) == _lib.EINVAL
+    assert lib.pratchya_gemm_bf16_nt(fake, 100, fake, 128, 256, 256, 64, fake, 256, _lib.DT_F32,
+                                     None) == _lib.EINVAL
+    assert lib.pratchya_gemm_bf16_nt(fake, 128, fake, 128, 0, 256, 128, fake, 256, _lib.DT_F32, None) == 0
+    assert lib.pratchya_transpose_b16(fake, 12, 64, fake, None) == _lib.EUNSUPPORTED
+    assert lib.pratchya_transpose_b16(None, 64, 64, None, None) == _lib.EINVAL
+    assert lib.pratchya_transpose_b16(fake, 0, 64, fake, None) == 0
+
+
 def test_invalid_tgrid_is_einval_without_launch():
     from pratchya_amd import _lib
     lib = _lib.load()

@@ -313,6 +313,26 @@ int pratchya_gemm_bs_nt_fq(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, 
 int pratchya_gemm_bf16_nt(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
                           int64_t K, void* C, int64_t ldc, int c_dtype, hipStream_t stream);
 
+/* f32 operands of pratchya_gemm_bf16_nt:    for the f32 products of the mixed
+ * matmuls (Q:645-712, jnp.matmul of a dequantized array and an f32 array) and
+ * of matmul_impl's backward (Q:618-622).  An f32 value v is the exact sum of
+ * the bf16 pieces p0 = trunc_bf16(v), p1 = trunc_bf16(v - p0), p2 = v - p0 - p1,
+ * and piece products are exact in f32, so an f32 dot product is a bf16 dot
+ * product over piece pairs placed side by side along K ((0,0) (0,1) (1,0)
+ * (0,2) (1,1) (2,0) drop only terms below 2^-24 of the largest product).
+ * src: f32 or bf16 [rows, cols] (row stride ld_src elements).  Writes dst,
+ * bf16 [out_rows, ld_dst] (ld_dst a multiple of 8, dst 16-byte aligned), with
+ * out_rows = rows (transpose = 0: segments run along src rows) or cols
+ * (transpose = 1: along src columns); segment s (nseg <= 16) holds piece
+ * planes[s] of its source vector in columns [s*kp, s*kp + len), zeros up to
+ * (s+1)*kp; kp a multiple of 64 covering len = cols (or rows).  Planes 0, 1, 2
+ * are the pieces (a non-finite value is its own piece 0, its other pieces 0);
+ * plane 3 is piece 0 with non-finite values written as 0 (for every pair but
+ * (0,0), so that inf meets only the other operand's leading piece). */
+int pratchya_split_pack_bf16(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t ld_src,
+                             int transpose, int nseg, const int* planes, void* dst, int64_t ld_dst, int64_t kp,
+                             hipStream_t stream);
+
 /* 16-bit transpose: src [rows, cols] -> dst [cols, rows] (bf16 X -> X.T, the
  * K-contiguous operand of the Newton-Schulz product (X X^T) X,
  * _optimizer.py:21).  rows and cols multiples of 8, buffers 16-byte aligned. */

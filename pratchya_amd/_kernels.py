@@ -556,6 +556,68 @@ def gemm_bf16_nt(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype = torc
     return out
 
 
+# bf16 piece pairs of an f32 product (see pratchya_split_pack_bf16): the six
+# pairs whose weight is at least 2^-24 of the leading product
+_F32_PAIRS = ((0, 0), (0, 1), (1, 0), (0, 2), (1, 1), (2, 0))
+
+
+def _split_pack(src: torch.Tensor, transpose: bool, planes, kp: int, out_rows_min: int = 0) -> torch.Tensor:
+    """bf16 [max(out_rows, out_rows_min), len(planes) * kp] operand of the
+    bf16 GEMM: segment s holds piece planes[s] of each source row (or column,
+    ``transpose``); rows beyond the source's are zero."""
+    src = src.contiguous()
+    R, C = int(src.shape[0]), int(src.shape[1])
+    out_rows = C if transpose else R
+    rows = max(out_rows, out_rows_min)
+    dst = (torch.zeros if rows > out_rows else torch.empty)((rows, len(planes) * kp), dtype=torch.bfloat16,
+                                                             device=src.device)
+    pl = (ctypes.c_int * len(planes))(*planes)
+    _lib.check(_lib.load().pratchya_split_pack_bf16(_ptr(src), _dtype_code(src.dtype), R, C, C, 1 if transpose else 0,
+                                                    len(planes), pl, _ptr(dst), len(planes) * kp, kp, _stream(src)),
+               "split_pack")
+    return dst
+
+
+def matmul_f32(a: torch.Tensor, b: torch.Tensor, a_t: bool = False, b_t: bool = False) -> torch.Tensor:
+    """f32 ``op(a) @ op(b)`` for 2-D f32 / bf16 tensors on the bf16 MFMA
+    kernel: ``op(a)`` is ``a`` [M, K] (``a_t``: ``a`` is [K, M] and is used
+    transposed), ``op(b)`` is ``b`` [K, N] (``b_t``: ``b`` is [N, K]).  Each
+    f32 operand is split into three exact bf16 pieces and the piece products
+    of weight >= 2^-24 run as one bf16 GEMM along a K six times as long (three
+    times for a bf16 operand, once for two): f32 products to f32 accuracy, up
+    to summation order (the f32 dots of pratchya/_qualia/_qarr.py:645-712,
+    :618-622)."""
+    _require_gpu(a, b)
+    if a.dim() != 2 or b.dim() != 2:
+        raise ValueError("matmul_f32: 2-D operands expected")
+    for t in (a, b):
+        if t.dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError(f"matmul_f32: unsupported dtype {t.dtype}")
+    M, Kd = (int(a.shape[1]), int(a.shape[0])) if a_t else (int(a.shape[0]), int(a.shape[1]))
+    Kb, N = (int(b.shape[1]), int(b.shape[0])) if b_t else (int(b.shape[0]), int(b.shape[1]))
+    if Kd != Kb:
+        raise ValueError(f"contraction mismatch: {Kd} vs {Kb}")
+    if M == 0 or N == 0:
+        return torch.empty((M, N), dtype=torch.float32, device=a.device)
+    if Kd == 0:
+        return torch.zeros((M, N), dtype=torch.float32, device=a.device)
+    na = 1 if a.dtype == torch.bfloat16 else 3
+    nb = 1 if b.dtype == torch.bfloat16 else 3
+    pairs = [(i, j) for i, j in _F32_PAIRS if i < na and j < nb]
+    # a non-finite value takes part only in the (0, 0) pair (plane 3: piece 0
+    # with non-finite values as 0)
+    a_planes = [3 if (i == 0 and j > 0) else i for i, j in pairs]
+    b_planes = [3 if (j == 0 and i > 0) else j for i, j in pairs]
+    kp = (Kd + 63) // 64 * 64
+    # the GEMM's operand rows: A = op(a) rows, B = op(b) columns (N-major);
+    # an N below one tile is padded to a multiple of 4 with zero rows
+    n_rows = N if N >= GEMM_TILE_ROWS else (N + 3) // 4 * 4
+    A = _split_pack(a, a_t, a_planes, kp)
+    B = _split_pack(b, not b_t, b_planes, kp, n_rows)
+    c = gemm_bf16_nt(A, B, torch.float32)
+    return c if n_rows == N else c[:, :N]
+
+
 def transpose_b16(x: torch.Tensor) -> torch.Tensor:
     """[rows, cols] 16-bit matrix -> its transpose [cols, rows], contiguous."""
     _require_gpu(x)

@@ -72,6 +72,8 @@ SIGNATURES = {
     "pratchya_gemm_bf16_nt": (_c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64,
                                        _c_int, _c_p]),
     "pratchya_transpose_b16": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "pratchya_split_pack_bf16": (_c_int, [_c_p, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
+                                          ctypes.POINTER(_c_int), _c_p, _c_i64, _c_i64, _c_p]),
     "pratchya_gemm_span": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
     "pratchya_transpose_u8": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "pratchya_debug_bf16_to_e4m3": (_c_int, [_c_p, _c_p, _c_i64, _c_int, _c_p]),

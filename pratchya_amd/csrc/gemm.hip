@@ -1230,6 +1230,117 @@ extern "C" int pratchya_transpose_b16(const void* src, int64_t rows, int64_t col
   return PRATCHYA_OK;
 }
 
+// --------------------------------------------------------------------------
+// f32 operands for the bf16 GEMM: an f32 value v is the exact sum of three
+// bf16 pieces p1 = trunc(v), p2 = trunc(v - p1), p3 = v - p1 - p2 (trunc:
+// the top 8 significand bits; each difference is exact in f32, the pieces
+// share v's sign and never overflow), and a product of two pieces is exact in
+// f32.  A non-finite v is its own first piece (the others are 0), and only the
+// (0,0) pair may carry it: plane 3 is piece 0 with non-finite values as 0, for
+// the pairs (0,j>0) and (i>0,0), where it would meet the other operand's
+// lower pieces (inf * 0 would make a NaN the f32 product does not have).  So
+// dot(a, b) over f32 vectors equals the sum of the piece products, and the
+// six pairs (1,1) (1,2) (2,1) (1,3) (2,2) (3,1) leave out only terms below
+// 2^-24 of the largest product: one bf16 GEMM over the pieces placed side by
+// side along K computes an f32 product to f32 accuracy (up to summation
+// order).  k_split_pack writes those K-contiguous operands: segment s of each
+// output row holds piece plane[s] of a source row (or column, transposed),
+// zero-padded to kp values.
+// --------------------------------------------------------------------------
+namespace {
+__device__ __forceinline__ float bf16_trunc(float v) { return pfp8::u2f(pfp8::f2u(v) & 0xFFFF0000u); }
+__device__ __forceinline__ float bf16_piece(float v, int p) {
+  if (!pfp8::is_finite_f(v)) return p == 0 ? v : 0.0f;
+  if (p == 3) p = 0;
+  const float p1 = bf16_trunc(v);
+  if (p == 0) return p1;
+  const float r1 = v - p1;
+  const float p2 = bf16_trunc(r1);
+  if (p == 1) return p2;
+  return r1 - p2;                     // at most 8 significant bits: exact in bf16
+}
+
+// src: f32 or bf16 [rows, cols] with row stride lds elements.  Not TRANSPOSED:
+// output row r, segment s, column k < cols is piece plane[s] of src[r][k];
+// TRANSPOSED: output row c, column k < rows is piece plane[s] of src[k][c].
+// One 64 x 64 source tile per workgroup through LDS; columns kp > len of a
+// segment are zero.  planes: 2 bits per segment (bits 2s, 2s+1).
+template <bool SRC_BF16, bool TRANSPOSED>
+__global__ __launch_bounds__(256) void k_split_pack(const void* __restrict__ src, int64_t rows, int64_t cols,
+                                                    int64_t lds, int nseg, uint32_t planes, uint16_t* __restrict__ dst,
+                                                    int64_t ldd, int64_t kp) {
+  __shared__ float tile[64][65];
+  const int64_t out_rows = TRANSPOSED ? cols : rows, seg_len = TRANSPOSED ? rows : cols;
+  const int64_t tiles_k = (kp + 63) / 64;            // tiles along the (padded) segment
+  const int64_t r0 = ((int64_t)blockIdx.x / tiles_k) * 64, k0 = ((int64_t)blockIdx.x % tiles_k) * 64;
+  const int t = threadIdx.x;
+  // load the source tile: (output row r0 + i, segment column k0 + j)
+#pragma unroll
+  for (int h = 0; h < 16; ++h) {
+    const int e = t + 256 * h, a = e >> 6, b = e & 63;   // source-contiguous index b
+    int64_t sr, sc;
+    if (TRANSPOSED) { sr = k0 + a; sc = r0 + b; } else { sr = r0 + a; sc = k0 + b; }
+    float v = 0.0f;
+    if (sr < rows && sc < cols) {
+      if constexpr (SRC_BF16) v = (float)static_cast<const __bf16*>(src)[sr * lds + sc];
+      else v = static_cast<const float*>(src)[sr * lds + sc];
+    }
+    if (TRANSPOSED) tile[b][a] = v; else tile[a][b] = v;   // tile[i][j]: output row i, column j
+  }
+  __syncthreads();
+  (void)seg_len;
+  // write: thread t -> output row i = t >> 2, 16 columns (t & 3) * 16 .. +16 of each segment
+  const int i = t >> 2, j0 = (t & 3) * 16;
+  if (r0 + i >= out_rows) return;
+  for (int s = 0; s < nseg; ++s) {
+    const int p = (planes >> (2 * s)) & 3;
+    uint32_t w[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float a = bf16_piece(tile[i][j0 + 2 * q], p), b = bf16_piece(tile[i][j0 + 2 * q + 1], p);
+      w[q] = (pfp8::f2u(a) >> 16) | (pfp8::f2u(b) & 0xFFFF0000u);   // pieces are bf16 values
+    }
+    const int64_t col = (int64_t)s * kp + k0 + j0;     // kp is a multiple of 64: whole 16-value pieces
+    uint4* d = reinterpret_cast<uint4*>(dst + (r0 + i) * ldd + col);
+    d[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    d[1] = make_uint4(w[4], w[5], w[6], w[7]);
+  }
+}
+}  // namespace
+
+extern "C" int pratchya_split_pack_bf16(const void* src, int src_dtype, int64_t rows, int64_t cols, int64_t ld_src,
+                                        int transpose, int nseg, const int* planes, void* dst, int64_t ld_dst,
+                                        int64_t kp, hipStream_t stream) {
+  if (rows < 0 || cols < 0 || kp < 0) return pratchya_set_error(PRATCHYA_EINVAL, "split_pack: negative size");
+  if (src_dtype != PRATCHYA_DT_F32 && src_dtype != PRATCHYA_DT_BF16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "split_pack: source dtype must be f32 or bf16 (got %d)", src_dtype);
+  if (nseg < 1 || nseg > 16 || !planes) return pratchya_set_error(PRATCHYA_EINVAL, "split_pack: 1 to 16 segments");
+  const int64_t out_rows = transpose ? cols : rows, seg_len = transpose ? rows : cols;
+  if (kp % 64 || kp < seg_len || ld_dst < nseg * kp || ld_src < cols)
+    return pratchya_set_error(PRATCHYA_EINVAL, "split_pack: segment length %lld must be a multiple of 64 covering "
+                              "%lld values, ld_dst >= nseg * kp", (long long)kp, (long long)seg_len);
+  if (out_rows == 0 || kp == 0) return PRATCHYA_OK;
+  if (!src || !dst || reinterpret_cast<uintptr_t>(dst) % 16 || ld_dst % 8)
+    return pratchya_set_error(PRATCHYA_EINVAL, "split_pack: null or misaligned buffer");
+  uint32_t pl = 0;
+  for (int s = 0; s < nseg; ++s) {
+    if (planes[s] < 0 || planes[s] > 3) return pratchya_set_error(PRATCHYA_EINVAL, "split_pack: plane must be 0 to 3");
+    pl |= (uint32_t)planes[s] << (2 * s);
+  }
+  const int64_t tiles = ((out_rows + 63) / 64) * (kp / 64);
+  if (tiles > INT32_MAX) return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "split_pack: too many tiles");
+  const bool bf = src_dtype == PRATCHYA_DT_BF16;
+  uint16_t* d = static_cast<uint16_t*>(dst);
+#define PRATCHYA_SPLIT(B, T) hipLaunchKernelGGL((k_split_pack<B, T>), dim3((unsigned)tiles), dim3(256), 0, stream, \
+                                                src, rows, cols, ld_src, nseg, pl, d, ld_dst, kp)
+  if (bf && transpose) PRATCHYA_SPLIT(true, true);
+  else if (bf) PRATCHYA_SPLIT(true, false);
+  else if (transpose) PRATCHYA_SPLIT(false, true);
+  else PRATCHYA_SPLIT(false, false);
+#undef PRATCHYA_SPLIT
+  return launch_status("split_pack");
+}
+
 extern "C" int pratchya_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* dst,
                                      hipStream_t stream) {
   if (rows < 0 || cols < 0) return pratchya_set_error(PRATCHYA_EINVAL, "transpose: negative size");

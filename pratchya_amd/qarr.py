@@ -175,6 +175,36 @@ def _deq32(x8, s8, s32, tgrid) -> torch.Tensor:
     return K.dequantize(x8, s8, s32, torch.float32, tuple(tgrid))
 
 
+def _mm_f32(a: torch.Tensor, b: torch.Tensor, a_t: bool = False, b_t: bool = False) -> torch.Tensor:
+    """f32 ``op(a) @ op(b)`` with torch.matmul's batch broadcasting (``op``
+    transposes the last two axes when ``a_t`` / ``b_t``), every 2-D product on
+    the bf16 MFMA kernel over exact bf16 pieces (``K.matmul_f32``): the f32
+    dots of the reference's mixed matmuls and matmul_impl backward.  Operands
+    other than f32 / bf16 are converted to f32 first."""
+    if a.dtype not in (torch.float32, torch.bfloat16):
+        a = a.float()
+    if b.dtype not in (torch.float32, torch.bfloat16):
+        b = b.float()
+    if a.dim() < 2 or b.dim() < 2:
+        # vector operands: matmul's 1-D promotion, then drop the added axis
+        if a.dim() == 1 and b.dim() == 1:
+            return _mm_f32(a[None, :], b[:, None]).reshape(())
+        if a.dim() == 1:
+            return _mm_f32(a[None, :], b, False, b_t).squeeze(-2)
+        return _mm_f32(a, b[:, None], a_t, False).squeeze(-1)
+    if b.dim() == 2 and not a_t:
+        lead = tuple(a.shape[:-2])
+        out = K.matmul_f32(a.reshape(-1, a.shape[-1]), b, False, b_t)
+        return out.reshape(lead + (a.shape[-2], out.shape[-1]))
+    if a.dim() == 2 and b.dim() == 2:
+        return K.matmul_f32(a, b, a_t, b_t)
+    batch = torch.broadcast_shapes(tuple(a.shape[:-2]), tuple(b.shape[:-2]))
+    ab = a.expand(batch + tuple(a.shape[-2:])).reshape((-1,) + tuple(a.shape[-2:]))
+    bb = b.expand(batch + tuple(b.shape[-2:])).reshape((-1,) + tuple(b.shape[-2:]))
+    outs = [K.matmul_f32(ab[i], bb[i], a_t, b_t) for i in range(ab.shape[0])]
+    return torch.stack(outs).reshape(batch + tuple(outs[0].shape))
+
+
 # --------------------------------------------------------------------------
 # Block-scaled GEMM planning
 # --------------------------------------------------------------------------
@@ -252,7 +282,7 @@ def _matmul_forward(x8, xs8, xs32, y8, ys8, ys32, gx, gy) -> torch.Tensor:
     out = _try_gemm(op_a, op_b)
     if out is not None:
         return out.reshape(tuple(x8.shape[:-1]) + (int(y8.shape[1]),))
-    return torch.matmul(_deq32(x8, xs8, xs32, gx), _deq32(y8, ys8, ys32, gy))
+    return _mm_f32(_deq32(x8, xs8, xs32, gx), _deq32(y8, ys8, ys32, gy))
 
 
 def _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y, pre=None, x_dtype=None):
@@ -307,9 +337,10 @@ def _matmul_cotangents(g, saved, grids, need_x, need_y):
         if _backward_mode == "fp8" else None
     if res is not None:
         return res[:2]
-    g = g.float()
-    gxf = g @ _deq32(y8, ys8, ys32, gy).transpose(-1, -2) if need_x else None
-    gyf = _deq32(x8, xs8, xs32, gx).transpose(-1, -2) @ g if need_y else None
+    if g.dtype != torch.bfloat16:
+        g = g.float()
+    gxf = _mm_f32(g, _deq32(y8, ys8, ys32, gy), b_t=True) if need_x else None
+    gyf = _mm_f32(_deq32(x8, xs8, xs32, gx), g, a_t=True) if need_y else None
     return gxf, gyf
 
 
@@ -429,7 +460,7 @@ class _MatmulMixed(torch.autograd.Function):
     def forward(ctx, src_x, y, x8, xs8, xs32, gx):
         ctx.saved = (x8, xs8, xs32, y.detach())
         ctx.gx = gx
-        return torch.matmul(_deq32(x8, xs8, xs32, gx), y.detach().float())
+        return _mm_f32(_deq32(x8, xs8, xs32, gx), y.detach())
 
     @staticmethod
     def backward(ctx, g):
@@ -437,10 +468,10 @@ class _MatmulMixed(torch.autograd.Function):
         g = g.float()
         grad_x = grad_y = None
         if ctx.needs_input_grad[0]:
-            gxf = _reduce_broadcast(g @ y.float().transpose(-1, -2), x8.shape)
+            gxf = _reduce_broadcast(_mm_f32(g, y, b_t=True), x8.shape)
             grad_x = _requant_cotangent(gxf, ctx.gx)
         if ctx.needs_input_grad[1]:
-            grad_y = _deq32(x8, xs8, xs32, ctx.gx).transpose(-1, -2) @ g
+            grad_y = _mm_f32(_deq32(x8, xs8, xs32, ctx.gx), g, a_t=True)
         return grad_x, grad_y, None, None, None, None
 
 
@@ -449,7 +480,7 @@ def matmul_mixed_impl(x_fp8, x_sc8, x_sc32, y_f32, block_grid_x: Tuple):
     sx = _src(x_fp8)
     if sx is not None or (torch.is_grad_enabled() and y_f32.requires_grad):
         return _MatmulMixed.apply(sx, y_f32, x_fp8, x_sc8, x_sc32, gx)
-    return torch.matmul(_deq32(x_fp8, x_sc8, x_sc32, gx), y_f32.float())
+    return _mm_f32(_deq32(x_fp8, x_sc8, x_sc32, gx), y_f32)
 
 
 class _RMatmulMixed(torch.autograd.Function):
@@ -459,7 +490,7 @@ class _RMatmulMixed(torch.autograd.Function):
     def forward(ctx, x, src_y, y8, ys8, ys32, gy):
         ctx.saved = (x.detach(), y8, ys8, ys32)
         ctx.gy = gy
-        return torch.matmul(x.detach().float(), _deq32(y8, ys8, ys32, gy))
+        return _mm_f32(x.detach(), _deq32(y8, ys8, ys32, gy))
 
     @staticmethod
     def backward(ctx, g):
@@ -467,9 +498,9 @@ class _RMatmulMixed(torch.autograd.Function):
         g = g.float()
         grad_x = grad_y = None
         if ctx.needs_input_grad[0]:
-            grad_x = g @ _deq32(y8, ys8, ys32, ctx.gy).transpose(-1, -2)
+            grad_x = _mm_f32(g, _deq32(y8, ys8, ys32, ctx.gy), b_t=True)
         if ctx.needs_input_grad[1]:
-            gyf = _reduce_broadcast(x.float().transpose(-1, -2) @ g, y8.shape)
+            gyf = _reduce_broadcast(_mm_f32(x, g, a_t=True), y8.shape)
             grad_y = _requant_cotangent(gyf, ctx.gy)
         return grad_x, grad_y, None, None, None, None
 
@@ -479,7 +510,7 @@ def rmatmul_mixed_impl(x_f32, y_fp8, y_sc8, y_sc32, block_grid_y: Tuple):
     sy = _src(y_fp8)
     if sy is not None or (torch.is_grad_enabled() and x_f32.requires_grad):
         return _RMatmulMixed.apply(x_f32, sy, y_fp8, y_sc8, y_sc32, gy)
-    return torch.matmul(x_f32.float(), _deq32(y_fp8, y_sc8, y_sc32, gy))
+    return _mm_f32(x_f32, _deq32(y_fp8, y_sc8, y_sc32, gy))
 
 
 # --------------------------------------------------------------------------

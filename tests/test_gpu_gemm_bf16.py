@@ -112,3 +112,76 @@ def test_newton_schulz_leaf_against_library():
     torch.cuda.synchronize()
     err = (got.float() - X.float()).norm() / X.float().norm()
     assert err.item() <= 3e-2
+
+
+# ---- f32 products over exact bf16 pieces (pratchya_split_pack_bf16) ----
+
+F32_SHAPES = [(256, 256, 256), (300, 1000, 100), (64, 40, 7), (1, 1, 1), (1024, 768, 4096), (513, 3, 65)]
+
+
+@pytest.mark.parametrize("a_t", [False, True], ids=["a", "aT"])
+@pytest.mark.parametrize("b_t", [False, True], ids=["b", "bT"])
+@pytest.mark.parametrize("shape", F32_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_matmul_f32_against_f64(shape, a_t, b_t):
+    """op(a) @ op(b) for f32 operands with heavy-tailed magnitudes: the f32
+    product's error against float64 stays at the f32 accumulation level
+    (relative Frobenius <= 2e-6, far below bf16's 4e-3)."""
+    K = _K()
+    M, N, Kd = shape
+    rng = np.random.default_rng(11)
+    A = (rng.standard_normal((M, Kd)) * np.exp2(rng.integers(-8, 8, (M, Kd)))).astype(np.float32)
+    B = (rng.standard_normal((Kd, N)) * np.exp2(rng.integers(-8, 8, (Kd, N)))).astype(np.float32)
+    a = torch.from_numpy(A.T.copy() if a_t else A).cuda()
+    b = torch.from_numpy(B.T.copy() if b_t else B).cuda()
+    c = K.matmul_f32(a, b, a_t, b_t)
+    torch.cuda.synchronize()
+    assert tuple(c.shape) == (M, N) and c.dtype == torch.float32
+    ref = A.astype(np.float64) @ B.astype(np.float64)
+    assert O.rel_fro(f32(c), ref) <= 2e-6
+
+
+@pytest.mark.parametrize("dt", ["bf16_a", "bf16_b", "bf16_both"])
+def test_matmul_f32_bf16_operands(dt):
+    """A bf16 operand is its own single piece (fewer pairs); the result is the
+    same f32 product."""
+    K = _K()
+    rng = np.random.default_rng(12)
+    A = O.bf16_round(rng.standard_normal((384, 512)).astype(np.float32))
+    B = rng.standard_normal((512, 320)).astype(np.float32)
+    if dt != "bf16_a":
+        B = O.bf16_round(B)
+    a = torch.from_numpy(A).cuda()
+    b = torch.from_numpy(B).cuda()
+    if dt in ("bf16_a", "bf16_both"):
+        a = a.to(torch.bfloat16)
+    if dt in ("bf16_b", "bf16_both"):
+        b = b.to(torch.bfloat16)
+    c = K.matmul_f32(a, b)
+    torch.cuda.synchronize()
+    assert O.rel_fro(f32(c), A.astype(np.float64) @ B.astype(np.float64)) <= 2e-6
+
+
+def test_matmul_f32_exact_and_special_values():
+    """24-bit integers (every piece product and sum exact) give the exact
+    product; inf and NaN propagate as in an f32 dot product."""
+    K = _K()
+    rng = np.random.default_rng(13)
+    A = rng.integers(-512, 512, (256, 32)).astype(np.float32)         # 10 bits: two pieces
+    B = rng.integers(-3, 4, (32, 256)).astype(np.float32) * 257.0     # 9-bit values: two pieces
+    c = K.matmul_f32(torch.from_numpy(A).cuda(), torch.from_numpy(B).cuda())
+    torch.cuda.synchronize()
+    want = (A.astype(np.int64) @ B.astype(np.int64)).astype(np.float64)
+    assert np.all(np.abs(want) < 2 ** 24)
+    assert np.array_equal(f32(c).astype(np.float64), want)
+    A2 = np.ones((256, 64), np.float32)
+    A2[3, 5] = np.inf
+    A2[7, 9] = np.nan
+    B2 = np.full((64, 256), 1.5, np.float32)               # exact in bf16: lower pieces are 0
+    B2[11, 17] = -np.inf
+    c2 = f32(K.matmul_f32(torch.from_numpy(A2).cuda(), torch.from_numpy(B2).cuda()))
+    torch.cuda.synchronize()
+    with np.errstate(invalid="ignore"):
+        want2 = A2.astype(np.float64) @ B2.astype(np.float64)
+    assert np.array_equal(np.isnan(c2), np.isnan(want2))   # row 7; (3, 17): inf - inf
+    fin = ~np.isnan(want2)
+    assert np.array_equal(c2[fin], want2[fin].astype(np.float32))   # +inf in row 3, -inf in column 17

@@ -249,6 +249,22 @@ int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t* x_sc8, con
                            int64_t slices, int64_t T, int64_t C, uint8_t* xt_fp8, uint8_t* sc_fp8,
                            float* sc_fp32, hipStream_t stream);
 
+/* Transposed quantize, tgrid (1, 128) of the transposed tensor:
+ *                                         replaces quantize_impl(x^T, (1, 128)),
+ * Q:458-506, as fp8_matmul's backward quantizes its transposed raw inputs
+ * (Q:786-788), without materialising x^T.
+ * x: [slices, T, C] as for pratchya_quantize_t128 (bf16, f32, or an e4m3fn
+ * payload with its (1, 128) scales; a bf16 x with scales goes through
+ * dequantize_impl_bwd first).  Blocks are 128 tokens of one channel, groups 8
+ * consecutive blocks of one channel (T a multiple of 1024, else
+ * PRATCHYA_EUNSUPPORTED).  Outputs exactly quantize_impl(x^T, (1, 128)) per
+ * slice: xt_fp8 [slices, C, T], sc_fp8 [slices * C * T / 128] (8-byte
+ * aligned), sc_fp32 [slices * C * T / 1024].  C a multiple of 8 (128 with
+ * input scales). */
+int pratchya_quantize_t1x128(const void* x, int x_dtype, const uint8_t* x_sc8, const float* x_sc32,
+                             int64_t slices, int64_t T, int64_t C, uint8_t* xt_fp8, uint8_t* sc_fp8,
+                             float* sc_fp32, hipStream_t stream);
+
 /* Block-scaled FP8 GEMM, "NT" form:                         replaces the f32 dot
  *   C[m, n] = sum_k dequant(A)[m, k] * dequant(B)[n, k]      of matmul_impl
  * (Q:605-608) and of its backward (Q:621-622), with FP8 operands.

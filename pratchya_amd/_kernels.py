@@ -193,6 +193,58 @@ def _u8(t: torch.Tensor) -> torch.Tensor:
     return t.view(torch.uint8) if t.dtype != torch.uint8 else t
 
 
+def quantize_t1x128(x: torch.Tensor, x_sc8: torch.Tensor = None, x_sc32: torch.Tensor = None):
+    """``quantize_impl(x^T, (1, 128))`` (pratchya/_qualia/_qarr.py:458-506)
+    of a [T, C] tensor, without materialising x^T: fp8_matmul's quantization
+    of its transposed raw inputs (Q:786-788).  Blocks are 128 tokens of one
+    channel, groups 8 consecutive blocks of one channel.  ``x`` and the input
+    scales as for ``quantize_t128``.  Returns ``(xt_fp8 [C, T] e4m3fn,
+    sc_fp8 [C*T/1024, 8] e8m0, sc_fp32 [C*T/1024, 1, 1] f32)``, the
+    K-contiguous (1, 128) row operand of a GEMM that contracts over tokens.
+    The kernel takes T a multiple of 1024; other token counts go through the
+    general quantizer on the explicitly transposed (dequantized) tensor."""
+    _require_gpu(x)
+    if x.dim() != 2:
+        raise ValueError("quantize_t1x128 needs a [T, C] tensor")
+    T, C = int(x.shape[0]), int(x.shape[1])
+    if x.dtype in (E4M3, torch.uint8):
+        if x_sc8 is None or x_sc32 is None:
+            raise ValueError("an fp8 input needs its (1, 128) scales")
+        code, xin = _lib.DT_E4M3, _u8(x)
+        xs8, xs32 = _u8(x_sc8).contiguous(), x_sc32.contiguous().float()
+    elif x.dtype == torch.bfloat16 and x_sc8 is not None and x_sc32 is not None:
+        code, xin = _lib.DT_BF16, x
+        xs8, xs32 = _u8(x_sc8).contiguous(), x_sc32.contiguous().float()
+    else:
+        if x_sc8 is not None or x_sc32 is not None:
+            raise ValueError("input scales apply to an fp8 payload or a bf16 cotangent only")
+        xin = x if x.dtype in (torch.float32, torch.bfloat16) else x.float()
+        code = _dtype_code(xin.dtype)
+        xs8 = xs32 = None
+    if T % 1024 or C % 8:
+        # the reference's composition: the values (dequantized / taken through
+        # dequantize_impl_bwd as the kernel does), transposed, quantized
+        if code == _lib.DT_E4M3:
+            v = dequantize(xin.view(E4M3), xs8.view(E8M0), xs32, torch.float32, (1, 128))
+        elif xs8 is not None:
+            v = dequantize_bwd(xin, xs8.view(E8M0), xs32, (1, 128))
+        else:
+            v = xin
+        return quantize(v.t().contiguous(), (1, 128))
+    if not xin.is_contiguous() or not _aligned(xin, 16):
+        xin = xin.contiguous() if not xin.is_contiguous() else xin.clone()
+    M = C * T // 1024
+    xt8 = torch.empty((C, T), dtype=torch.uint8, device=x.device)
+    sc8 = torch.empty((M, 8), dtype=torch.uint8, device=x.device)
+    sc32 = torch.empty((M, 1, 1), dtype=torch.float32, device=x.device)
+    _lib.check(_lib.load().pratchya_quantize_t1x128(_ptr(xin), code,
+                                                    _ptr(xs8) if xs8 is not None else None,
+                                                    _ptr(xs32) if xs32 is not None else None,
+                                                    1, T, C, _ptr(xt8), _ptr(sc8), _ptr(sc32), _stream(xin)),
+               "quantize_t1x128")
+    return xt8.view(E4M3), sc8.view(E8M0), sc32
+
+
 def quantize_t128(x: torch.Tensor, x_sc8: torch.Tensor = None, x_sc32: torch.Tensor = None, out=None):
     """``quantize_impl(x, (128, 1))`` (pratchya/_qualia/_qarr.py:458-506) with
     the payload transposed per slice.

@@ -60,18 +60,20 @@ constexpr int NTHREADS = 512;
 // LDS stage: A tile | B tile | A e8m0 words | B e8m0 words | A unit ratios |
 // B unit ratios.  After the two stages: A units | B units (of the latest span
 // start).  The ratio and unit arrays are in the order the MFMA lanes read
-// them: A per row as [band wm][l32][mi] (one 8-byte read per lane), B per 4
-// rows as [wn][ni][lhi][j] (one 16-byte read per 32-column tile).
+// them: A per row as [band wm][l32][mi] (one 8-byte read per lane); B per 32
+// rows, per 4 rows as [wn][ni][lhi][j] (one 16-byte read per 32-column tile),
+// or per row as [wn][ni][lhi][j][i] (four 16-byte reads), by the B group
+// granularity BG (0, 1, 2; see load_units).
 constexpr int OFF_B = TILE_BYTES;
 constexpr int OFF_EA = 2 * TILE_BYTES;
 constexpr int OFF_EB = OFF_EA + 4 * BM;
 constexpr int OFF_RA = OFF_EB + 4 * BN;
 constexpr int OFF_RB = OFF_RA + 4 * BM;
-constexpr int STAGE_BYTES = 69632;             // OFF_RB + BN, rounded up to 1 KB
+constexpr int STAGE_BYTES = 69632;             // OFF_RB + 4 * BN
 constexpr int OFF_UA = 2 * STAGE_BYTES;
 constexpr int OFF_UB = OFF_UA + 4 * BM;
-constexpr int LDS_BYTES = OFF_UB + BN;
-static_assert(OFF_RB + BN <= STAGE_BYTES && LDS_BYTES <= 160 * 1024, "LDS layout");
+constexpr int LDS_BYTES = OFF_UB + 4 * BN;
+static_assert(OFF_RB + 4 * BN <= STAGE_BYTES && LDS_BYTES <= 160 * 1024, "LDS layout");
 
 struct Scales {
   const uint8_t* e8;   // e8m0 bytes
@@ -283,19 +285,37 @@ __device__ __forceinline__ void pin_acc(v16f (&acc)[2][4]) {
 __device__ __forceinline__ uint32_t lds_u32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
 __device__ __forceinline__ float lds_f32(const uint8_t* p) { return *reinterpret_cast<const float*>(p); }
 
+// B group maxima granularity BG: one per 32 B rows (0), per 4 rows (1), or
+// per row (2); the lane holds NJ values per 32-column tile ni.
+template <int BG>
+struct BGran {
+  static constexpr int NJ = BG == 0 ? 1 : (BG == 1 ? 4 : 16);
+  // index of accumulator element v (B row 8 * (v >> 2) + 4 * lhi + (v & 3))
+  static constexpr int j_of(int v) { return BG == 0 ? 0 : (BG == 1 ? (v >> 2) : v); }
+};
+
 // The lane's entries of a stage's unit (or unit ratio) arrays: its A rows
 // wm*64 + mi*32 + l32 (mi = 0, 1), and its B rows wn*128 + ni*32 + 8j + 4*lhi
-// (FINE_B: j = 0..3, for scale groups narrower than 32 rows) or wn*128 + ni*32.
-template <bool FINE_B>
+// (+ i = 0..3 with BG 2; j = 0..3 with BG 1, 2) or wn*128 + ni*32 (BG 0).
+template <int BG>
 __device__ __forceinline__ void load_units(const uint8_t* a, const uint8_t* b, int wm, int wn, int lane,
-                                           float (&uA)[2], float (&uB)[4][FINE_B ? 4 : 1]) {
+                                           float (&uA)[2], float (&uB)[4][BGran<BG>::NJ]) {
   const int l32 = lane & 31, lhi = lane >> 5;
   const v2f va = *reinterpret_cast<const v2f*>(a + (wm * 64 + l32 * 2) * 4);
   uA[0] = va.x;
   uA[1] = va.y;
 #pragma unroll
   for (int ni = 0; ni < 4; ++ni) {
-    if constexpr (FINE_B) {
+    if constexpr (BG == 2) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const v4f vb = *reinterpret_cast<const v4f*>(b + (wn * 128 + (ni * 2 + lhi) * 16 + j * 4) * 4);
+        uB[ni][4 * j + 0] = vb.x;
+        uB[ni][4 * j + 1] = vb.y;
+        uB[ni][4 * j + 2] = vb.z;
+        uB[ni][4 * j + 3] = vb.w;
+      }
+    } else if constexpr (BG == 1) {
       const v4f vb = *reinterpret_cast<const v4f*>(b + (wn * 32 + (ni * 2 + lhi) * 4) * 4);
       uB[ni][0] = vb.x;
       uB[ni][1] = vb.y;
@@ -304,6 +324,43 @@ __device__ __forceinline__ void load_units(const uint8_t* a, const uint8_t* b, i
     } else {
       uB[ni][0] = lds_f32(b + (wn * 32 + ni * 8) * 4);
     }
+  }
+}
+
+// acc[mi][ni][v] *= uA(row) * uB(column) with the unit (ratio) arrays at a, b.
+// Per-row B values (BG 2) are read 4 at a time (one 16-byte read per lane),
+// with scheduling barriers between the reads so that the compiler does not
+// hold all 64 beside the accumulator (the kernel is at its register limit).
+template <int BG>
+__device__ __forceinline__ void scale_by_units(v16f (&acc)[2][4], const uint8_t* a, const uint8_t* b, int wm,
+                                               int wn, int lane) {
+  if constexpr (BG == 2) {
+    const int l32 = lane & 31, lhi = lane >> 5;
+    const v2f va = *reinterpret_cast<const v2f*>(a + (wm * 64 + l32 * 2) * 4);
+    const uint8_t* bl = b + (wn * 128 + lhi * 16) * 4;
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        __builtin_amdgcn_sched_barrier(0);
+        const v4f vb = *reinterpret_cast<const v4f*>(bl + (ni * 32 + j * 4) * 4);
+        const float u[4] = {vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[0][ni][4 * j + i] *= va.x * u[i];
+          acc[1][ni][4 * j + i] *= va.y * u[i];
+        }
+      }
+    __builtin_amdgcn_sched_barrier(0);
+  } else {
+    float rA[2], rB[4][BGran<BG>::NJ];
+    load_units<BG>(a, b, wm, wn, lane, rA, rB);
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[mi][ni][v] *= rA[mi] * rB[ni][BGran<BG>::j_of(v)];
   }
 }
 
@@ -368,14 +425,16 @@ __device__ __forceinline__ int tile_base(int t, int n) {
 }
 
 // Epilogue: C[m][n] = acc * gA * gB / 2^14 (the two /128 of the dequant) for
-// this wave's 64 x 128 sub-tile at (row0, col0).  The waves stage RP rows x
+// this wave's 64 x 128 sub-tile at (row0, col0); with per-row B units (BG 2)
+// gB comes from the unit array at ub (the lane's entries, see load_units),
+// read 4 columns at a time where they are applied.  The waves stage RP rows x
 // 128 columns each at a time in one LDS stage buffer (free once every wave has
 // passed the barrier below) and write them back as full 16-byte lane chunks
 // covering whole rows, with non-temporal stores (the output is not read again
 // by this kernel; streaming it keeps the operand panels in L2).
-template <bool OUT_BF16, bool FINE_B>
+template <bool OUT_BF16, int BG>
 __device__ __forceinline__ void store_tile(const v16f (&acc)[2][4], const float (&gA)[2],
-                                           const float (&gB)[4][FINE_B ? 4 : 1],
+                                           const float (&gB)[4][BG == 1 ? 4 : 1], const uint8_t* ub,
                                            uint8_t* stage, int wave, int lane, void* C, int64_t ldc, int row0,
                                            int col0, int M, int N) {
   const int l32 = lane & 31, lhi = lane >> 5;
@@ -397,9 +456,19 @@ __device__ __forceinline__ void store_tile(const v16f (&acc)[2][4], const float 
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int col = ni * 32 + 8 * j + 4 * lhi;
-            const float f = gA[mi] * gB[ni][FINE_B ? j : 0] * 6.103515625e-05f;
-            const float c0 = acc[mi][ni][4 * j + 0] * f, c1 = acc[mi][ni][4 * j + 1] * f;
-            const float c2 = acc[mi][ni][4 * j + 2] * f, c3 = acc[mi][ni][4 * j + 3] * f;
+            float f0, f1, f2, f3;
+            if constexpr (BG == 2) {
+              const v4f u = *reinterpret_cast<const v4f*>(ub + (ni * 32 + j * 4) * 4);
+              const float fa = gA[mi] * 6.103515625e-05f;
+              f0 = fa * u.x;
+              f1 = fa * u.y;
+              f2 = fa * u.z;
+              f3 = fa * u.w;
+            } else {
+              f0 = f1 = f2 = f3 = gA[mi] * gB[ni][BG == 1 ? j : 0] * 6.103515625e-05f;
+            }
+            const float c0 = acc[mi][ni][4 * j + 0] * f0, c1 = acc[mi][ni][4 * j + 1] * f1;
+            const float c2 = acc[mi][ni][4 * j + 2] * f2, c3 = acc[mi][ni][4 * j + 3] * f3;
             uint8_t* dst = stg + (l32 % RP) * PITCH + col * ESZ;
             if constexpr (OUT_BF16) {
               typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -469,24 +538,37 @@ __device__ __forceinline__ void fq_row_scales(v16f (&acc)[2][4], const float (&g
   }
   const uint32_t mb = lhi ? m[1] : m[0];      // this lane's row: lhi * 32 + l32
   uint32_t* gm = fq.gmax + (int64_t)strip * 256 + wm * 64 + lhi * 32 + l32;
-  __hip_atomic_fetch_max(gm, mb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __builtin_amdgcn_s_waitcnt(0x0F70);       // vmcnt(0): this wave's maxima are performed
+  // Every access of the exchange is a device-scope read-modify-write atomic:
+  // those on one address are serialized where they are performed, and one
+  // that returns a value has been performed when the value arrives.  So a
+  // workgroup's maxima are performed before its arrival is counted (the
+  // returned values are awaited before the barrier), and a partner that has
+  // read a count of 4 reads the group maxima after all of them -- with no
+  // assumption about the visibility of plain stores or loads across XCDs.
+  const uint32_t prev = __hip_atomic_fetch_max(gm, mb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("" ::"v"(prev));             // wait for the returned value
   __syncthreads();
   if (threadIdx.x == 0) {
     uint32_t* cnt = fq.arrive + strip;
-    __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t n = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     // the partners run in the same round of the schedule; the bound only keeps
-    // a broken launch from spinning forever (the status word reports it)
-    for (int it = 0; __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < 4u; ++it) {
+    // a broken launch from spinning forever.  A timeout sets the status word
+    // and raises the strip's maxima to a NaN pattern, so the strip's outputs
+    // and scales come out NaN instead of quietly using a partial maximum.
+    for (int it = 0; n < 4u; ++it) {
       if (it >= (1 << 20)) {
-        __hip_atomic_store(fq.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_or(fq.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t* g0 = fq.gmax + (int64_t)strip * 256;
+        for (int r = 0; r < 256; ++r)
+          __hip_atomic_fetch_max(g0 + r, 0x7FFFFFFFu, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
       __builtin_amdgcn_s_sleep(2);
+      n = __hip_atomic_fetch_add(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   __syncthreads();
-  const uint32_t Gb = __hip_atomic_load(gm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t Gb = __hip_atomic_fetch_max(gm, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const float G = u2f(Gb);
   const bool fin = (Gb >> 23) < 255u;
   BlockScale bs;
@@ -567,14 +649,13 @@ __device__ __forceinline__ void store_tile_fq(const v16f (&acc)[2][4], uint8_t* 
   }
 }
 
-template <bool OUT_BF16, bool FINE_B, int FQ, bool BF = false>
+template <bool OUT_BF16, int BG, int FQ, bool BF = false>
 __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     Scales sa, Scales sb, void* __restrict__ C, int64_t ldc, int K, int span, int tiles_m,
     int tiles_n, uint32_t a_bytes, uint32_t b_bytes, uint32_t ea_bytes, uint32_t eb_bytes,
     uint32_t ga_bytes, uint32_t gb_bytes, int M, int N, FqArgs fq) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + (FQ != 0 ? FQ_TABLE_BYTES : 0)];
-  constexpr int NJ = FINE_B ? 4 : 1;
   const OperandRsrc ra = make_rsrc(A, a_bytes, sa, ea_bytes, ga_bytes);
   const OperandRsrc rb = make_rsrc(B, b_bytes, sb, eb_bytes, gb_bytes);
 
@@ -607,8 +688,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     if (grp == 0) {
       h.pub = (w4 * 64 + l32 * 2 + lhi) * 4;              // A row w4*64 + lane: band w4, mi = lhi
     } else {
-      const int r = w4 * 64 + lane, c = r & 127, q = c & 31;   // B row: wn = r / 128, ni = c / 32
-      h.pub = ((r >> 7) * 32 + ((c >> 5) * 2 + ((q >> 2) & 1)) * 4 + (q >> 3)) * 4;
+      // B row r: wn = r / 128, ni = c / 32, lhi = (q >> 2) & 1, j = q >> 3, i = q & 3
+      const int r = w4 * 64 + lane, c = r & 127, q = c & 31;
+      const int e4 = (r >> 7) * 32 + ((c >> 5) * 2 + ((q >> 2) & 1)) * 4 + (q >> 3);
+      h.pub = (BG == 2 ? e4 * 4 + (q & 3) : e4) * 4;
     }
   }
   auto rows_of = [&](int tm_, int tn_) {
@@ -736,14 +819,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
           }
           if (kt > 0 && kt % span == 0) {
             // a new span of group maxima: move the accumulator into its units
-            float rA[2], rB[4][NJ];
-            load_units<FINE_B>(st + OFF_RA, st + OFF_RB, wm, wn, lane, rA, rB);
-#pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-              for (int ni = 0; ni < 4; ++ni)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) acc[mi][ni][v] *= rA[mi] * rB[ni][FINE_B ? (v >> 2) : 0];
+            scale_by_units<BG>(acc, st + OFF_RA, st + OFF_RB, wm, wn, lane);
           }
         }
         // rows of this lane: A wm*64 + i*32 + l32, B wn*128 + i*32 + l32; the
@@ -815,7 +891,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
 
     // units of the last span; the last stage's buffer holds no pending load:
     // stage the output there
-    float gA[2], gB[4][NJ];
+    float gA[2], gB[4][BG == 1 ? 4 : 1];
     if constexpr (BF) {
       // no scales: gA * gB / 2^14 = 1
 #pragma unroll
@@ -823,19 +899,25 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) gB[i][j] = 128.0f;
+        for (int j = 0; j < (BG == 1 ? 4 : 1); ++j) gB[i][j] = 128.0f;
+    } else if constexpr (BG == 2) {
+      // A units here, per-row B units where the store applies them
+      const v2f va = *reinterpret_cast<const v2f*>(lds + OFF_UA + (wm * 64 + l32 * 2) * 4);
+      gA[0] = va.x;
+      gA[1] = va.y;
+      gB[0][0] = gB[1][0] = gB[2][0] = gB[3][0] = 1.0f;
     } else {
-      load_units<FINE_B>(lds + OFF_UA, lds + OFF_UB, wm, wn, lane, gA, gB);
+      load_units<BG>(lds + OFF_UA, lds + OFF_UB, wm, wn, lane, gA, gB);
     }
     if constexpr (FQ != 0) {
-      static_assert(!FINE_B, "output requantization takes B scale groups of 32 rows or more");
+      static_assert(BG == 0, "output requantization takes B scale groups of 32 rows or more");
       uint8_t* table = lds + LDS_BYTES + wave * 64 * 16;
       fq_row_scales<FQ == 2>(acc, gA, gB, fq, table, tm * (tiles_n >> 2) + (tn >> 2), tn, wm, wn, lane,
                              m0 + wm * 64, n0 + wn * 128, M, N);
       store_tile_fq<OUT_BF16>(acc, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, table, wave, lane, C, ldc,
                               m0 + wm * 64, n0 + wn * 128, M);
     } else {
-      store_tile<OUT_BF16, FINE_B>(acc, gA, gB, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc,
+      store_tile<OUT_BF16, BG>(acc, gA, gB, lds + OFF_UB + (wn * 128 + lhi * 16) * 4, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc,
                                    m0 + wm * 64, n0 + wn * 128, M, N);
     }
     if (!has_next) break;
@@ -906,7 +988,7 @@ struct GemmPlan {
   Scales sa, sb;
   int64_t span, tiles_m, tiles_n, grid;
   int64_t a_bytes, b_bytes, ea_bytes, eb_bytes, ga_bytes, gb_bytes;
-  bool fine_b;
+  int bg;              // B group maxima per 32 rows (0), 4 rows (1) or row (2)
 };
 
 int gemm_plan(const char* who, const uint8_t* A, int64_t lda, const uint8_t* a_sc8, const float* a_sc32,
@@ -944,13 +1026,16 @@ int gemm_plan(const char* who, const uint8_t* A, int64_t lda, const uint8_t* a_s
   const int64_t last_b = ((N - 1) / b_rdiv) * b_sr + (nk - 1) * b_sk;
   P->ea_bytes = (last_a + 4) & ~(int64_t)3;
   P->eb_bytes = (last_b + 4) & ~(int64_t)3;
-  // B's group max per lane: one per 32 output columns, or one per 4 columns.
-  P->fine_b = b_rdiv % 32 != 0;
-  if (P->fine_b && N % 4)
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: N must be a multiple of 4 for B scale groups narrower "
-                              "than 32 rows (got %lld)", who, (long long)N);
-  if (P->fine_b && !(b_rdiv % 4 == 0 || (b_rdiv == 1 && b_kg % (4 * b_sr) == 0 && b_sk % (4 * b_sr) == 0)))
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: B scale groups narrower than 4 columns", who);
+  // B's group max per lane: one per 32 output columns where B's block rows
+  // are 32 rows or more, one per 4 columns where every 4 consecutive rows
+  // (from a multiple of 4, N a multiple of 4) share their groups, else one
+  // per column (16 per lane and 32-column tile).
+  if (b_rdiv % 32 == 0)
+    P->bg = 0;
+  else if (N % 4 == 0 && (b_rdiv % 4 == 0 || (b_rdiv == 1 && b_kg % (4 * b_sr) == 0 && b_sk % (4 * b_sr) == 0)))
+    P->bg = 1;
+  else
+    P->bg = 2;
   // span: both operands' group maxima are constant over it
   P->span = std::gcd(group_span(P->sa, M, nk), group_span(P->sb, N, nk));
   // buffer resources address bytes with 32-bit offsets; an operand of fewer
@@ -974,10 +1059,10 @@ int gemm_plan(const char* who, const uint8_t* A, int64_t lda, const uint8_t* a_s
   return PRATCHYA_OK;
 }
 
-template <bool BF, bool FB, int FQ>
+template <bool BF, int BG, int FQ>
 void gemm_launch(const GemmPlan& P, const uint8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, void* C,
                  int64_t ldc, int64_t M, int64_t N, int64_t K, const FqArgs& fq, hipStream_t stream) {
-  hipLaunchKernelGGL((k_gemm_bs_nt<BF, FB, FQ>), dim3((unsigned)P.grid), dim3(NTHREADS), 0, stream, A, lda, B,
+  hipLaunchKernelGGL((k_gemm_bs_nt<BF, BG, FQ>), dim3((unsigned)P.grid), dim3(NTHREADS), 0, stream, A, lda, B,
                      ldb, P.sa, P.sb, C, ldc, (int)K, (int)P.span, (int)P.tiles_m, (int)P.tiles_n,
                      (uint32_t)P.a_bytes, (uint32_t)P.b_bytes, (uint32_t)P.ea_bytes, (uint32_t)P.eb_bytes,
                      (uint32_t)P.ga_bytes, (uint32_t)P.gb_bytes, (int)M, (int)N, fq);
@@ -1012,10 +1097,15 @@ extern "C" int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t*
   if (rc) return rc;
   const FqArgs none{};
   const bool bf = c_dtype == PRATCHYA_DT_BF16;
-  if (bf && !P.fine_b) gemm_launch<true, false, 0>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
-  else if (bf) gemm_launch<true, true, 0>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
-  else if (!P.fine_b) gemm_launch<false, false, 0>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
-  else gemm_launch<false, true, 0>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
+  if (bf) {
+    if (P.bg == 0) gemm_launch<true, 0, 0>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
+    else if (P.bg == 1) gemm_launch<true, 1, 0>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
+    else gemm_launch<true, 2, 0>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
+  } else {
+    if (P.bg == 0) gemm_launch<false, 0, 0>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
+    else if (P.bg == 1) gemm_launch<false, 1, 0>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
+    else gemm_launch<false, 2, 0>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
+  }
   return launch_status("gemm");
 }
 
@@ -1042,7 +1132,7 @@ extern "C" int pratchya_gemm_bs_nt_fq(const uint8_t* A, int64_t lda, const uint8
   int rc = gemm_plan("gemm_fq", A, lda, a_sc8, a_sc32, a_rdiv, a_sr, a_sk, a_kg, B, ldb, b_sc8, b_sc32, b_rdiv,
                      b_sr, b_sk, b_kg, M, N, K, C, ldc, c_dtype, &P);
   if (rc) return rc;
-  if (P.fine_b)
+  if (P.bg != 0)
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_fq: B scale groups narrower than 32 rows");
   if (ldc >= (int64_t)1 << 23)
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_fq: output row stride of 2^23 elements or more");
@@ -1073,10 +1163,10 @@ extern "C" int pratchya_gemm_bs_nt_fq(const uint8_t* A, int64_t lda, const uint8
   rc = launch_status("gemm_fq");
   if (rc) return rc;
   const bool bf = c_dtype == PRATCHYA_DT_BF16;
-  if (bf && fix_nan) gemm_launch<true, false, 2>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
-  else if (bf) gemm_launch<true, false, 1>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
-  else if (fix_nan) gemm_launch<false, false, 2>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
-  else gemm_launch<false, false, 1>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+  if (bf && fix_nan) gemm_launch<true, 0, 2>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+  else if (bf) gemm_launch<true, 0, 1>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+  else if (fix_nan) gemm_launch<false, 0, 2>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+  else gemm_launch<false, 0, 1>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
   return launch_status("gemm_fq");
 }
 
@@ -1104,7 +1194,7 @@ extern "C" int pratchya_gemm_bf16_nt(const void* A, int64_t lda, const void* B, 
   P.sa = Scales{nullptr, nullptr, 1, 0, 0, 1};
   P.sb = P.sa;
   P.span = 1;
-  P.fine_b = false;
+  P.bg = 0;
   const int64_t Ma = M < BM ? BM : M, Na = N < BN ? BN : N;
   P.a_bytes = ((Ma - 1) * lda + K) * 2;
   P.b_bytes = ((Na - 1) * ldb + K) * 2;
@@ -1120,7 +1210,7 @@ extern "C" int pratchya_gemm_bf16_nt(const void* A, int64_t lda, const void* B, 
   const uint8_t* a8 = static_cast<const uint8_t*>(A);
   const uint8_t* b8 = static_cast<const uint8_t*>(B);
 #define PRATCHYA_GEMM_BF16(OB)                                                                              \
-  hipLaunchKernelGGL((k_gemm_bs_nt<OB, false, 0, true>), dim3((unsigned)P.grid), dim3(NTHREADS), 0, stream, a8, \
+  hipLaunchKernelGGL((k_gemm_bs_nt<OB, 0, 0, true>), dim3((unsigned)P.grid), dim3(NTHREADS), 0, stream, a8, \
                      lda * 2, b8, ldb * 2, P.sa, P.sb, C, ldc, (int)(K * 2), 1, (int)P.tiles_m, (int)P.tiles_n,    \
                      (uint32_t)P.a_bytes, (uint32_t)P.b_bytes, 0u, 0u, 0u, 0u, (int)M, (int)N, none)
   if (bf) PRATCHYA_GEMM_BF16(true);

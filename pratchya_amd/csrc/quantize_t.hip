@@ -25,6 +25,10 @@
 // bf16 inputs; for f32 / fp8 inputs and clamped blocks every element is
 // checked against the bf16 rounding midpoint, and a lane's 16-element chunk
 // holding a close one is recast with IEEE division).
+//
+// pratchya_quantize_t1x128: quantize_impl(x^T, (1, 128)) instead, the same
+// blocks grouped 8 along the tokens of one channel (see k_quant_t128's GT
+// form and k_quant_t1x128_fp8).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -108,8 +112,17 @@ __device__ __forceinline__ float row_elem(const uint32_t (&w)[InTraits<IN>::NW],
 
 // TOK consecutive tokens per lane; RS = 128 / TOK lanes cover a 128-token
 // block, CGW = 64 / RS groups of 8 channels per wave.
-template <int IN, bool HW, int TOK>
-__global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ x,
+//
+// GT: quantize_impl(x^T, (1, 128)) instead (fp8_matmul's quantization of a
+// transposed operand, _qarr.py:784-789) of a bf16 or f32 input: the same
+// blocks (128 tokens of one channel) grouped 8 along the tokens of one
+// channel (T a multiple of 1024).  A workgroup is 8 waves, one per 128-token
+// block of a 1024-token group, all over the same 8 * CGW channels (one
+// 128-byte line of each row); they exchange their channel maxima through LDS,
+// so each channel has its own group max, and wave 0 writes each channel's 8
+// e8m0 bytes (one 8-byte store) and group max.
+template <int IN, bool HW, int TOK, bool GT = false>
+__global__ __launch_bounds__(GT ? 512 : 256) void k_quant_t128(const uint8_t* __restrict__ x,
                                                     const uint8_t* __restrict__ x_sc8,
                                                     const float* __restrict__ x_sc32, int kg_shift,
                                                     int64_t T, int64_t C, uint8_t* __restrict__ qt,
@@ -120,17 +133,34 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
   const int lane = threadIdx.x & 63;
   constexpr int RS = 128 / TOK, CGW = 64 / RS;
   const int cg = lane % CGW, rs = lane / CGW;
-  const int64_t c0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * (8 * CGW) + cg * 8;
+  const int wv = (int)(threadIdx.x >> 6);
+  // GT: the workgroups of neighbouring channel chunks read neighbouring bytes
+  // of the same input scale rows (one byte per token row and 128 channels).
+  // Workgroups are dispatched to the 8 XCDs round-robin in linear order; the
+  // linear index is remapped so that neighbours run on one XCD (one L2).
+  uint32_t bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+  if constexpr (GT) {
+    const uint32_t gx = gridDim.x, gy = gridDim.y, n = gx * gy * gridDim.z;
+    uint32_t b = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+    if (n % 8 == 0) b = (b % 8) * (n / 8) + b / 8;
+    bx = b % gx;
+    by = (b / gx) % gy;
+    bz = b / (gx * gy);
+  }
+  const int64_t c0 = GT ? (int64_t)bx * (8 * CGW) + cg * 8 : ((int64_t)bx * 4 + wv) * (8 * CGW) + cg * 8;
   // C is a multiple of 8, so a lane owns a whole group or nothing; the xor
   // partners of a lane (same cg) share its fate.  (Inputs with scales: C is a
   // multiple of 128, so a wave is wholly inside or outside; fp8 inputs: every
   // wave of the grid is inside.  Their waves outside return after the
   // workgroup barrier below.)
   constexpr bool SCALED = IN == IN_FP8 || IN == IN_BF16S;
-  if constexpr (!SCALED) {
+  if constexpr (!SCALED && !GT) {
     if (c0 >= C) return;
   }
-  const int64_t s = blockIdx.z, tb = blockIdx.y;
+  // GT: every wave reaches the maxima exchange; lanes beyond C only skip
+  // their loads and stores
+  const bool live = c0 < C;
+  const int64_t s = bz, tb = GT ? (int64_t)by * 8 + wv : (int64_t)by;
   const int64_t t0 = tb * 128 + rs * TOK;
 
   // (1, 128) input scales of the workgroup's 128 token rows and NB channel
@@ -139,10 +169,18 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
   // group of a block is its slice-global index >> kg_shift.  32-bit indices:
   // the host checks slices * T * C / 128 < 2^32.
   constexpr int NB = SCALED ? (4 * 8 * CGW) / 128 : 1;
-  __shared__ float sdq[NB][128];
-  if constexpr (SCALED) {
+  __shared__ float sdq[GT ? 1 : NB][GT ? 1024 : 128];
+  if constexpr (SCALED && GT) {
+    // the workgroup's 1024 token rows of its one 128-channel scale block
     const uint32_t nbr = (uint32_t)(C >> 7);
-    const uint32_t cb0 = (uint32_t)blockIdx.x * NB;
+    const uint32_t cb = (uint32_t)(((int64_t)bx * (8 * CGW)) >> 7);
+    for (int i = (int)threadIdx.x; i < 1024; i += 512) {
+      const uint32_t blk = (uint32_t)(s * T + (int64_t)by * 1024 + i) * nbr + cb;
+      sdq[0][i] = e8m0_decode(x_sc8[blk]) * x_sc32[blk >> kg_shift];
+    }
+  } else if constexpr (SCALED) {
+    const uint32_t nbr = (uint32_t)(C >> 7);
+    const uint32_t cb0 = bx * NB;
     for (int i = (int)threadIdx.x; i < NB * 128; i += 256) {
       const uint32_t b = (uint32_t)i >> 7, row = (uint32_t)i & 127u;
       float v = 0.0f;
@@ -155,7 +193,21 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
   }
 
   uint32_t w[TOK][NW];
-  if constexpr (IN == IN_FP8) {
+  if constexpr (GT) {
+    // direct row loads (the waves of a workgroup cover different tokens of
+    // the same channels)
+    if (live) {
+      const uint8_t* xr = x + ((s * T + t0) * C + c0) * ESZ;
+#pragma unroll
+      for (int r = 0; r < TOK; ++r) load_row<IN>(xr + (int64_t)r * C * ESZ, w[r]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < TOK; ++r)
+#pragma unroll
+        for (int k = 0; k < NW; ++k) w[r][k] = 0u;
+    }
+    if constexpr (SCALED) __syncthreads();   // the staged scales are visible
+  } else if constexpr (IN == IN_FP8) {
     // A lane's rows are 8-byte pieces; read from global memory directly, a
     // wave's row segments would be 32 bytes.  The workgroup's 128 tokens x
     // 128 channels are staged through LDS instead, with 16-byte loads that
@@ -163,7 +215,7 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
     static_assert(TOK == 8 && CGW == 4, "the fp8 tile is 128 tokens x 4 waves x 32 channels");
     constexpr int kPitch = 136;              // bytes per staged row (8-byte aligned, fewer bank conflicts)
     __shared__ __attribute__((aligned(16))) uint8_t tile[128 * kPitch];
-    const int64_t cw = (int64_t)blockIdx.x * 128;
+    const int64_t cw = (int64_t)bx * 128;
     const uint8_t* xt = x + (s * T + tb * 128) * C + cw;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -196,8 +248,11 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
   float dq[TOK];
 #pragma unroll
   for (int r = 0; r < TOK; ++r) dq[r] = 1.0f;
-  if constexpr (SCALED) {
-    const int b = (int)((c0 >> 7) - (int64_t)blockIdx.x * NB);
+  if constexpr (SCALED && GT) {
+#pragma unroll
+    for (int r = 0; r < TOK; ++r) dq[r] = sdq[0][wv * 128 + rs * TOK + r];
+  } else if constexpr (SCALED) {
+    const int b = (int)((c0 >> 7) - (int64_t)bx * NB);
 #pragma unroll
     for (int r = 0; r < TOK; ++r) dq[r] = sdq[b][rs * TOK + r];
   }
@@ -226,11 +281,30 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
     for (int sh = CGW; sh < 64; sh <<= 1) m = umax(m, shfl_xor_u32(m, sh));
     mx[j] = m;
   });
-  uint32_t Gb = 0;
+  // group maxima: of the lane's 8 channels (tgrid (128, 1)), or per channel
+  // over the workgroup's 8 token blocks (GT)
+  float Gc[8];
+  constexpr int CPW = 8 * CGW;
+  __shared__ uint32_t mxs[GT ? CPW : 1][GT ? 8 : 1];
+  if constexpr (GT) {
+    if (rs == 0) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) Gb = umax(Gb, mx[j]);
-  const float G = u2f(Gb);
-  const bool G_finite = (Gb >> 23) < 255u;
+      for (int j = 0; j < 8; ++j) mxs[cg * 8 + j][wv] = mx[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint4 a = *reinterpret_cast<const uint4*>(&mxs[cg * 8 + j][0]);
+      const uint4 b = *reinterpret_cast<const uint4*>(&mxs[cg * 8 + j][4]);
+      Gc[j] = u2f(umax(umax(umax(a.x, a.y), umax(a.z, a.w)), umax(umax(b.x, b.y), umax(b.z, b.w))));
+    }
+  } else {
+    uint32_t Gb = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) Gb = umax(Gb, mx[j]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) Gc[j] = u2f(Gb);
+  }
 
   // e8m0 bytes and y ~ 128 / S per channel; then the division-free cast,
   // chunk by chunk (channel j, this lane's 16 tokens).  A chunk is recast with
@@ -239,14 +313,14 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
   // midpoint after the multiply -- rare, and only that chunk pays for it.
   uint32_t e[8];
   float y[8];
-  const float rcpG128 = __builtin_amdgcn_rcpf(G * 0.0078125f);
   uint32_t clamped = 0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
+    const float G = Gc[j];
     e[j] = e8m0_of(u2f(mx[j]), G);
     const float sG = e8m0_decode(e[j]) * G;
     const bool cl = !(sG >= kClamp);
-    y[j] = cl ? PRATCHYA_Y_CLAMP : u2f((254u - e[j]) << 23) * rcpG128;
+    y[j] = cl ? PRATCHYA_Y_CLAMP : u2f((254u - e[j]) << 23) * __builtin_amdgcn_rcpf(G * 0.0078125f);
     clamped |= cl ? 1u : 0u;
   }
   const bool check = INC != IN_BF16 || __any(clamped);
@@ -265,8 +339,8 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
       if (check) near |= near_mid8(t0v) | near_mid8(t1v) | near_mid8(t2v) | near_mid8(t3v);
       o[k] = cvt4<HW>(t0v, t1v, t2v, t3v);
     }
-    if (near || !G_finite) {
-      const float S = quant_scale(e[j], G);
+    if (near || !((f2u(Gc[j]) >> 23) < 255u)) {
+      const float S = quant_scale(e[j], Gc[j]);
 #pragma unroll
       for (int k = 0; k < TOK / 4; ++k)
         o[k] = cvt4_exact(row_elem<INC, j>(w[4 * k + 0], dq[4 * k + 0]),
@@ -274,23 +348,194 @@ __global__ __launch_bounds__(256) void k_quant_t128(const uint8_t* __restrict__ 
                           row_elem<INC, j>(w[4 * k + 2], dq[4 * k + 2]),
                           row_elem<INC, j>(w[4 * k + 3], dq[4 * k + 3]), S);
     }
-    if constexpr (TOK == 16) {
-      const u32x4_t v = {o[0], o[1], o[2], o[3]};
-      __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(qo + (int64_t)j * T));
-    } else {
-      static_assert(TOK == 8, "8 or 16 tokens per lane");
-      const u32x2_t v = {o[0], o[1]};
-      __builtin_nontemporal_store(v, reinterpret_cast<u32x2_t*>(qo + (int64_t)j * T));
+    if (live) {
+      if constexpr (TOK == 16) {
+        const u32x4_t v = {o[0], o[1], o[2], o[3]};
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(qo + (int64_t)j * T));
+      } else {
+        static_assert(TOK == 8, "8 or 16 tokens per lane");
+        const u32x2_t v = {o[0], o[1]};
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x2_t*>(qo + (int64_t)j * T));
+      }
     }
   });
-  if (rs == 0) {
+  if constexpr (GT) {
+    // quantize_impl(x^T, (1, 128)) on [C, T]: block (c, tb) is c * T/128 + tb;
+    // a channel's 8 blocks of this group are consecutive bytes
+    if (wv == 0 && rs == 0 && live) {
+      const int64_t nbr = T / 128, nb = C * nbr;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+          const uint32_t eb = e8m0_of(u2f(mxs[cg * 8 + j][b]), Gc[j]);
+          if (b < 4) lo |= eb << (8 * b);
+          else hi |= eb << (8 * (b - 4));
+        }
+        const int64_t c = c0 + j;
+        *reinterpret_cast<u32x2_t*>(sc8 + s * nb + c * nbr + (int64_t)by * 8) = u32x2_t{lo, hi};
+        sc32[s * (nb / 8) + c * (nbr / 8) + by] = Gc[j];
+      }
+    }
+  } else if (rs == 0) {
     // blocks (tb, c0 .. c0 + 7) are consecutive; they form group (tb*C + c0) / 8
     const int64_t nb = (T / 128) * C;
     const int64_t blk = tb * C + c0;
     uint32_t* e8 = reinterpret_cast<uint32_t*>(sc8 + s * nb + blk);
     e8[0] = e[0] | (e[1] << 8) | (e[2] << 16) | (e[3] << 24);
     e8[1] = e[4] | (e[5] << 8) | (e[6] << 16) | (e[7] << 24);
-    sc32[s * (nb / 8) + blk / 8] = G;
+    sc32[s * (nb / 8) + blk / 8] = Gc[0];
+  }
+}
+
+// quantize_impl(x^T, (1, 128)) of a stored (1, 128) fp8 tensor x [T, C]
+// (its dequantize_impl, Q:541-569, requantized, Q:458-506): the wgrad operand
+// of the stored activation.  A workgroup takes one 128-channel column (one
+// input scale block per token row) of one 1024-token group: 4 waves x 32
+// channels, each lane 8 channels x 8 tokens of a 128-token block, as in
+// k_quant_t128's fp8 tile.  Two passes over the group's 8 token blocks, each
+// block staged through LDS with 16-byte loads of whole 128-byte rows: the
+// first pass takes every channel's block maxima, the second (whose loads find
+// the group in the caches) casts and stores.  The loads of the next two
+// blocks are in flight while a block is processed.
+__global__ __launch_bounds__(256) void k_quant_t1x128_fp8(const uint8_t* __restrict__ x,
+                                                          const uint8_t* __restrict__ x_sc8,
+                                                          const float* __restrict__ x_sc32, int kg_shift,
+                                                          int64_t T, int64_t C, uint8_t* __restrict__ qt,
+                                                          uint8_t* __restrict__ sc8, float* __restrict__ sc32) {
+  constexpr int TOK = 8, CGW = 4, kPitch = 136;
+  const int lane = threadIdx.x & 63, wv = (int)(threadIdx.x >> 6);
+  const int cg = lane % CGW, rs = lane / CGW;
+  // workgroups of neighbouring columns share no lines here, but those of one
+  // XCD share its L2 for the second pass: consecutive columns on one XCD
+  uint32_t b = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  const uint32_t n = gridDim.x * gridDim.y * gridDim.z;
+  if (n % 8 == 0) b = (b % 8) * (n / 8) + b / 8;
+  const uint32_t bx = b % gridDim.x, by = (b / gridDim.x) % gridDim.y, bz = b / (gridDim.x * gridDim.y);
+  const int lc = wv * 32 + cg * 8;                 // the lane's first channel in the column
+  const int64_t s = bz, tg = (int64_t)by * 1024;   // slice, first token of the group
+  __shared__ float sdq[1024];                      // input scale of each token row (this column's block)
+  __shared__ __attribute__((aligned(16))) uint8_t tile[128 * kPitch];
+  __shared__ __attribute__((aligned(16))) uint32_t bm[128][8];   // block maxima, |x| bits
+  {
+    const uint32_t nbr = (uint32_t)(C >> 7);
+    for (int i = (int)threadIdx.x; i < 1024; i += 256) {
+      const uint32_t blk = (uint32_t)(s * T + tg + i) * nbr + bx;
+      sdq[i] = e8m0_decode(x_sc8[blk]) * x_sc32[blk >> kg_shift];
+    }
+  }
+  const uint8_t* xg = x + (s * T + tg) * C + (int64_t)bx * 128;
+  // 16-byte pieces of block tb: thread t loads rows (i * 256 + t) / 8, i < 4;
+  // two blocks are in flight ahead of the one processed
+  uint4 v[2][4];
+  auto load_block = [&](int tb, uint4 (&vv)[4]) {
+    const uint8_t* xt = xg + (int64_t)tb * 128 * C;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = i * 256 + (int)threadIdx.x;
+      vv[i] = load_stream16(reinterpret_cast<const char*>(xt + (int64_t)(q >> 3) * C + (q & 7) * 16));
+    }
+  };
+  // block tb's tile into LDS (after every wave is done with the previous
+  // one), the loads of block `next` into the freed registers, and the lane's
+  // 8 tokens x 8 channels with their input scales out of the tile
+  uint32_t w[TOK][2];
+  float dq[TOK];
+  auto stage = [&](int tb, uint4 (&vc)[4], int next) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = i * 256 + (int)threadIdx.x;
+      uint2* d = reinterpret_cast<uint2*>(tile + (q >> 3) * kPitch + (q & 7) * 16);
+      d[0] = make_uint2(vc[i].x, vc[i].y);
+      d[1] = make_uint2(vc[i].z, vc[i].w);
+    }
+    if (next < 8) load_block(next, vc);
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < TOK; ++r) {
+      const uint2 t2 = *reinterpret_cast<const uint2*>(tile + (rs * TOK + r) * kPitch + lc);
+      w[r][0] = t2.x;
+      w[r][1] = t2.y;
+      dq[r] = sdq[tb * 128 + rs * TOK + r];
+    }
+  };
+  load_block(0, v[0]);
+  load_block(1, v[1]);
+  // pass 1: the block maxima of the lane's 8 channels (the last two blocks'
+  // loads start the second pass: blocks 0 and 1 again)
+#pragma unroll 2
+  for (int tb = 0; tb < 8; ++tb) {
+    stage(tb, v[tb & 1], tb + 2 < 8 ? tb + 2 : tb - 6);
+    static_for<8>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      uint32_t m = 0;
+#pragma unroll
+      for (int r = 0; r < TOK; ++r) m = umax(m, row_abs_bits<IN_FP8, j>(w[r], dq[r]));
+#pragma unroll
+      for (int sh = CGW; sh < 64; sh <<= 1) m = umax(m, shfl_xor_u32(m, sh));
+      if (rs == 0) bm[lc + j][tb] = m;
+    });
+  }
+  __syncthreads();
+  // group maxima; the lanes of token sub-block 0 write the scales: a channel's
+  // 8 e8m0 bytes of this group are consecutive (block (c, tb) of x^T [C, T]
+  // is c * T/128 + tb)
+  float Gc[8];
+  {
+    const int64_t nbr = T / 128, nb = C * nbr;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint4 a = *reinterpret_cast<const uint4*>(&bm[lc + j][0]);
+      const uint4 c = *reinterpret_cast<const uint4*>(&bm[lc + j][4]);
+      Gc[j] = u2f(umax(umax(umax(a.x, a.y), umax(a.z, a.w)), umax(umax(c.x, c.y), umax(c.z, c.w))));
+      if (rs == 0) {
+        const uint32_t lo = e8m0_of(u2f(a.x), Gc[j]) | (e8m0_of(u2f(a.y), Gc[j]) << 8) |
+                            (e8m0_of(u2f(a.z), Gc[j]) << 16) | (e8m0_of(u2f(a.w), Gc[j]) << 24);
+        const uint32_t hi = e8m0_of(u2f(c.x), Gc[j]) | (e8m0_of(u2f(c.y), Gc[j]) << 8) |
+                            (e8m0_of(u2f(c.z), Gc[j]) << 16) | (e8m0_of(u2f(c.w), Gc[j]) << 24);
+        const int64_t ch = (int64_t)bx * 128 + lc + j;
+        *reinterpret_cast<u32x2_t*>(sc8 + s * nb + ch * nbr + (int64_t)by * 8) = u32x2_t{lo, hi};
+        sc32[s * (nb / 8) + ch * (nbr / 8) + by] = Gc[j];
+      }
+    }
+  }
+  // pass 2: the cast of each block (the arithmetic of k_quant_t128)
+  uint8_t* const qo = qt + (s * C + (int64_t)bx * 128 + lc) * T + tg + rs * TOK;
+#pragma unroll 2
+  for (int tb = 0; tb < 8; ++tb) {
+    stage(tb, v[tb & 1], tb + 2);
+    static_for<8>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      const float G = Gc[j];
+      const uint32_t e = e8m0_of(u2f(bm[lc + j][tb]), G);
+      const float sG = e8m0_decode(e) * G;
+      const float y =
+          !(sG >= kClamp) ? PRATCHYA_Y_CLAMP : u2f((254u - e) << 23) * __builtin_amdgcn_rcpf(G * 0.0078125f);
+      uint32_t o[TOK / 4];
+      uint32_t near = 0;
+#pragma unroll
+      for (int k = 0; k < TOK / 4; ++k) {
+        const float t0v = row_elem<IN_FP8, j>(w[4 * k + 0], dq[4 * k + 0]) * y;
+        const float t1v = row_elem<IN_FP8, j>(w[4 * k + 1], dq[4 * k + 1]) * y;
+        const float t2v = row_elem<IN_FP8, j>(w[4 * k + 2], dq[4 * k + 2]) * y;
+        const float t3v = row_elem<IN_FP8, j>(w[4 * k + 3], dq[4 * k + 3]) * y;
+        near |= near_mid8(t0v) | near_mid8(t1v) | near_mid8(t2v) | near_mid8(t3v);
+        o[k] = cvt4<true>(t0v, t1v, t2v, t3v);
+      }
+      if (near || !((f2u(G) >> 23) < 255u)) {
+        const float S = quant_scale(e, G);
+#pragma unroll
+        for (int k = 0; k < TOK / 4; ++k)
+          o[k] = cvt4_exact(row_elem<IN_FP8, j>(w[4 * k + 0], dq[4 * k + 0]),
+                            row_elem<IN_FP8, j>(w[4 * k + 1], dq[4 * k + 1]),
+                            row_elem<IN_FP8, j>(w[4 * k + 2], dq[4 * k + 2]),
+                            row_elem<IN_FP8, j>(w[4 * k + 3], dq[4 * k + 3]), S);
+      }
+      const u32x2_t ov = {o[0], o[1]};
+      __builtin_nontemporal_store(ov, reinterpret_cast<u32x2_t*>(qo + (int64_t)j * T + tb * 128));
+    });
   }
 }
 
@@ -363,5 +608,63 @@ extern "C" int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t*
   hipError_t err = hipGetLastError();
   if (err != hipSuccess)
     return pratchya_set_error(PRATCHYA_EHIP, "quantize_t128: launch failed: %s", hipGetErrorString(err));
+  return PRATCHYA_OK;
+}
+
+extern "C" int pratchya_quantize_t1x128(const void* x, int x_dtype, const uint8_t* x_sc8, const float* x_sc32,
+                                        int64_t slices, int64_t T, int64_t C, uint8_t* xt_fp8, uint8_t* sc_fp8,
+                                        float* sc_fp32, hipStream_t stream) {
+  if (slices < 0 || T < 0 || C < 0) return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t1x128: negative size");
+  if (x_dtype != PRATCHYA_DT_F32 && x_dtype != PRATCHYA_DT_BF16 && x_dtype != PRATCHYA_DT_E4M3)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t1x128: unsupported input dtype %d", x_dtype);
+  if (T % 128)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t1x128: tgrid (1, 128) does not divide %lld tokens",
+                              (long long)T);
+  const bool scaled = x_dtype == PRATCHYA_DT_E4M3 || (x_dtype == PRATCHYA_DT_BF16 && x_sc8 && x_sc32);
+  if (scaled && C % 128)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t1x128: tgrid (1, 128) of the input scales does not "
+                              "divide %lld channels", (long long)C);
+  if (slices == 0 || T == 0 || C == 0) return PRATCHYA_OK;
+  if (T % 1024)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t1x128: tokens must be a multiple of 1024 (one "
+                              "group of 8 blocks per channel; got %lld)", (long long)T);
+  if (C % 8)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t1x128: channels must be a multiple of 8 (got %lld)",
+                              (long long)C);
+  if (!x || !xt_fp8 || !sc_fp8 || !sc_fp32 || (x_dtype == PRATCHYA_DT_E4M3 && (!x_sc8 || !x_sc32)))
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t1x128: null buffer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(xt_fp8) % 16 ||
+      reinterpret_cast<uintptr_t>(sc_fp8) % 8 || reinterpret_cast<uintptr_t>(sc_fp32) % 4)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t1x128: buffers are not aligned");
+  if (T / 1024 > 65535 || slices > 65535)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t1x128: too many token groups or slices");
+  if (scaled && (slices * T) * (C / 128) >= ((int64_t)1 << 32))
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t1x128: input scales beyond 2^32 blocks");
+  // workgroups of 8 waves: one per 128-token block of a 1024-token group, over
+  // 64 (bf16) or 32 (f32, fp8) channels
+  auto grid_for_tok = [&](int tok) {
+    const int cpw = 8 * (64 / (128 / tok));
+    return dim3((unsigned)((C + cpw - 1) / cpw), (unsigned)(T / 1024), (unsigned)slices);
+  };
+  const uint8_t* xb = static_cast<const uint8_t*>(x);
+  const int64_t kg = scaled ? gcd64(8, T * (C / 128)) : 1;
+  const int kg_shift = kg == 8 ? 3 : (kg == 4 ? 2 : (kg == 2 ? 1 : 0));
+  if (x_dtype == PRATCHYA_DT_BF16 && scaled) {
+    hipLaunchKernelGGL((k_quant_t128<IN_BF16S, true, 16, true>), grid_for_tok(16), dim3(512), 0, stream, xb, x_sc8,
+                       x_sc32, kg_shift, T, C, xt_fp8, sc_fp8, sc_fp32);
+  } else if (x_dtype == PRATCHYA_DT_BF16) {
+    hipLaunchKernelGGL((k_quant_t128<IN_BF16, true, 16, true>), grid_for_tok(16), dim3(512), 0, stream, xb, nullptr,
+                       nullptr, 0, T, C, xt_fp8, sc_fp8, sc_fp32);
+  } else if (x_dtype == PRATCHYA_DT_F32) {
+    hipLaunchKernelGGL((k_quant_t128<IN_F32, true, 8, true>), grid_for_tok(8), dim3(512), 0, stream, xb, nullptr,
+                       nullptr, 0, T, C, xt_fp8, sc_fp8, sc_fp32);
+  } else {
+    // one workgroup per 128-channel column and 1024-token group
+    hipLaunchKernelGGL(k_quant_t1x128_fp8, dim3((unsigned)(C / 128), (unsigned)(T / 1024), (unsigned)slices),
+                       dim3(256), 0, stream, xb, x_sc8, x_sc32, kg_shift, T, C, xt_fp8, sc_fp8, sc_fp32);
+  }
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess)
+    return pratchya_set_error(PRATCHYA_EHIP, "quantize_t1x128: launch failed: %s", hipGetErrorString(err));
   return PRATCHYA_OK;
 }

@@ -1017,10 +1017,22 @@ for _cls in (QArrayImpl, _LazyProduct):      # a lazy product flattens to its ma
 # --------------------------------------------------------------------------
 # fp8_matmul (Q:766-793)
 # --------------------------------------------------------------------------
+def _quantized_transpose(x, tgrid):
+    """``QArrayImpl(x^T, tgrid)`` of a 2-D x [T, C] (the transposed operands
+    of fp8_matmul's backward, Q:786-788).  With tgrid (1, 128), f32 / bf16
+    values, T a multiple of 1024 and C of 8, quantize_t1x128 writes the same
+    bytes without materialising x^T."""
+    if (tuple(tgrid) == (1, 128) and x.dim() == 2 and x.dtype in (torch.float32, torch.bfloat16)
+            and int(x.shape[0]) % 1024 == 0 and int(x.shape[1]) % 8 == 0):
+        return QArrayImpl._tree_unflatten((True, (1, 128)), K.quantize_t1x128(x.contiguous()))
+    return QArrayImpl(x.transpose(-1, -2), tgrid)
+
+
 def _fp8_matmul_value(x, y, tgrid):
     with torch.no_grad():
-        out = QArrayImpl(x, tgrid) @ QArrayImpl(y, tgrid)
-        return out.dequantize(torch.float32)
+        qx = x if isinstance(x, QArrayImpl) else QArrayImpl(x, tgrid)
+        qy = y if isinstance(y, QArrayImpl) else QArrayImpl(y, tgrid)
+        return (qx @ qy).dequantize(torch.float32)
 
 
 class _FP8Matmul(torch.autograd.Function):
@@ -1035,8 +1047,10 @@ class _FP8Matmul(torch.autograd.Function):
         x, y = ctx.saved_tensors
         # Q:777-789: both gradients through the same quantized matmul, with the
         # raw inputs transposed in f32 and quantized along the transposed axis
-        g_x = _fp8_matmul_value(g, y.transpose(-1, -2), ctx.tgrid) if ctx.needs_input_grad[0] else None
-        g_y = _fp8_matmul_value(x.transpose(-1, -2), g, ctx.tgrid) if ctx.needs_input_grad[1] else None
+        g_x = _fp8_matmul_value(g, _quantized_transpose(y, ctx.tgrid), ctx.tgrid) \
+            if ctx.needs_input_grad[0] else None
+        g_y = _fp8_matmul_value(_quantized_transpose(x, ctx.tgrid), g, ctx.tgrid) \
+            if ctx.needs_input_grad[1] else None
         return g_x, g_y, None
 
 

@@ -206,6 +206,28 @@ def test_quantize_t128_argument_codes_without_gpu():
     assert f(None, _lib.DT_BF16, None, None, 0, 128, 64, None, None, None, None) == _lib.OK
 
 
+def test_quantize_t1x128_argument_codes_without_gpu():
+    """pratchya_quantize_t1x128 reports shape and argument errors before
+    anything touches a buffer."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    f = lib.pratchya_quantize_t1x128
+    fake = ctypes.c_void_p(1 << 20)
+    assert f(None, _lib.DT_BF16, None, None, 1, -1, 64, None, None, None, None) == _lib.EINVAL
+    # 100 tokens: tgrid (1, 128) of x^T does not divide them
+    assert f(None, _lib.DT_BF16, None, None, 1, 100, 64, None, None, None, None) == _lib.EINVAL
+    # fp8 input whose (1, 128) grid does not divide the channels
+    assert f(None, _lib.DT_E4M3, None, None, 1, 1024, 64, None, None, None, None) == _lib.EINVAL
+    # below 1024 tokens a group of 8 token blocks straddles channels
+    assert f(None, _lib.DT_BF16, None, None, 1, 512, 64, None, None, None, None) == _lib.EUNSUPPORTED
+    assert b"1024" in lib.pratchya_last_error()
+    # 12 channels: not a multiple of 8
+    assert f(None, _lib.DT_BF16, None, None, 1, 1024, 12, None, None, None, None) == _lib.EUNSUPPORTED
+    assert f(None, 7, None, None, 1, 1024, 64, None, None, None, None) == _lib.EINVAL
+    assert f(fake, _lib.DT_BF16, None, None, 1, 1024, 64, None, fake, fake, None) == _lib.EINVAL   # null output
+    assert f(None, _lib.DT_BF16, None, None, 0, 1024, 64, None, None, None, None) == _lib.OK     # empty
+
+
 def test_quantize_dequantize_codes_without_gpu():
     """Workspace query and argument errors of the one-pass fake quantization."""
     from pratchya_amd import _lib

@@ -192,6 +192,89 @@ def test_wgrad_from_transposed_requantize():
     check(C, ref, F32_TOL, "wgrad via quantize_t128")
 
 
+def test_per_column_b_groups_exact():
+    """B quantized (1, 128) as rows: every output column has its own group
+    maxima, which change between the two 1024-wide K spans differently per
+    column (the per-row B units).  Lossless small-integer data: the product
+    must be exact bit for bit."""
+    K = _K()
+    M_, K_, N_ = 256, 2048, 384
+    rng = np.random.default_rng(41)
+    x = rng.integers(-8, 9, size=(M_, K_)).astype(np.float32)
+    x[:, ::128] = 8.0
+    y = rng.integers(-4, 5, size=(N_, K_)).astype(np.float32)
+    y[:, ::128] = 4.0
+    y *= np.exp2(np.arange(N_) % 5 - 2.0).astype(np.float32)[:, None]     # G = 4 * 2^p per column
+    y[1::2, 1024:] *= 2.0                                                 # odd columns: second span 2x
+    y[7, :1024] = 0.0                                                     # an all-zero span
+    xq = quant_dev(x, (1, 128), bf16=False)
+    yq = quant_dev(y, (1, 128), bf16=False)
+    assert np.array_equal(deq_host(*xq, (1, 128)), x) and np.array_equal(deq_host(*yq, (1, 128)), y)
+    C = K.gemm_nt(K.operand_rows(*xq, (1, 128)), K.operand_rows(*yq, (1, 128)), torch.float32)
+    torch.cuda.synchronize()
+    exact = (x.astype(np.float64) @ y.astype(np.float64).T).astype(np.float32)
+    assert np.array_equal(f32(C), exact)
+
+
+@pytest.mark.parametrize("shape", [(512, 4096, 300), (300, 2048, 1028)], ids=lambda s: "x".join(map(str, s)))
+def test_per_column_b_groups_heavy_tailed(shape):
+    """Rows of both operands scaled over 2^-20 .. 2^20 (each row its own
+    group maxima), an N that is not a multiple of 8 or 32, edge tiles."""
+    K = _K()
+    M_, K_, N_ = shape
+    rng = np.random.default_rng(42)
+    x = (rng.standard_normal((M_, K_)) * np.exp2(rng.integers(-20, 21, (M_, 1)))).astype(np.float32)
+    y = (rng.standard_normal((N_, K_)) * np.exp2(rng.integers(-20, 21, (N_, 1)))).astype(np.float32)
+    y[:, K_ // 2:] *= np.exp2(rng.integers(-6, 7, (N_, 1))).astype(np.float32)
+    xq = quant_dev(x, (1, 128), bf16=False)
+    yq = quant_dev(y, (1, 128), bf16=False)
+    C = K.gemm_nt(K.operand_rows(*xq, (1, 128)), K.operand_rows(*yq, (1, 128)), torch.float32)
+    torch.cuda.synchronize()
+    ref = deq_host(*xq, (1, 128)) @ deq_host(*yq, (1, 128)).T
+    # per-element relative check as well: columns span 2^40 in magnitude
+    scale = np.abs(deq_host(*xq, (1, 128))).max(1)[:, None] * np.abs(deq_host(*yq, (1, 128))).max(1)[None, :]
+    assert np.all(np.abs(f32(C) - ref) <= 1e-3 * scale * np.sqrt(K_))
+    check(C, ref, F32_TOL, "per-column groups")
+
+
+def test_b_groups_straddling_rows():
+    """B [N, 512] quantized (1, 128): a group of 8 blocks covers two rows, so
+    B's group maxima change every 2 columns."""
+    K = _K()
+    M_, K_, N_ = 256, 512, 520
+    rng = np.random.default_rng(43)
+    x = rng.standard_normal((M_, K_)).astype(np.float32)
+    y = (rng.standard_normal((N_, K_)) * np.exp2(rng.integers(-8, 9, (N_, 1)))).astype(np.float32)
+    xq = quant_dev(x, (1, 128), bf16=False)
+    yq = quant_dev(y, (1, 128), bf16=False)
+    assert yq[2].numel() == N_ // 2
+    C = K.gemm_nt(K.operand_rows(*xq, (1, 128)), K.operand_rows(*yq, (1, 128)), torch.float32)
+    torch.cuda.synchronize()
+    check(C, deq_host(*xq, (1, 128)) @ deq_host(*yq, (1, 128)).T, F32_TOL, "straddling B groups")
+
+
+def test_wgrad_from_t1x128_requantize():
+    """The fp8-mode wgrad chain: the stored (1,128) activation and dY, each
+    transposed and quantized (1, 128) along the tokens (quantize_t1x128),
+    then contracted over the tokens (span 8, per-row group maxima on both
+    operands)."""
+    K = _K()
+    T, Cin, N_ = 2048, 512, 768
+    a_bits = O.activation_input(T, Cin, seed=5)
+    dy_bits = O.normal_input((T, N_), 1e-3, seed=6)
+    a8 = K.quantize(to_dev_bf16(a_bits), (1, 128))
+    at = K.quantize_t1x128(*a8)
+    dt = K.quantize_t1x128(to_dev_bf16(dy_bits))
+    C = K.gemm_nt(K.operand_rows(*at, (1, 128)), K.operand_rows(*dt, (1, 128)), torch.float32)
+    torch.cuda.synchronize()
+    a_deq = O.dequantize_impl(u8(a8[0]), u8(a8[1]), f32(a8[2]), "float32", (1, 128))
+    aq = O.quantize_impl(np.ascontiguousarray(a_deq.T), (1, 128))
+    dq = O.quantize_impl(np.ascontiguousarray(O.bf16_bits_to_f32(dy_bits).T), (1, 128))
+    ref = (O.dequantize_impl(*aq, "float32", (1, 128)).astype(np.float64)
+           @ O.dequantize_impl(*dq, "float32", (1, 128)).astype(np.float64).T)
+    check(C, ref, F32_TOL, "wgrad via quantize_t1x128")
+
+
 def test_group_maxima_change_across_spans():
     """Rows whose 1024-wide K spans differ by orders of magnitude, all-zero
     spans, and a weight with two groups (the accumulator rescaling path)."""

@@ -303,6 +303,30 @@ def test_fp8_matmul(Q):
     assert rel(f32(yd.grad), fwd(x.T.copy(), g)) <= TOL
 
 
+def test_fp8_matmul_transposed_quantizer(Q):
+    """Token counts that are multiples of 1024: the backward's transposed
+    operands are quantized by quantize_t1x128 (x^T and y^T), with the same
+    expected values as the general path."""
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((1024, 1024)).astype(np.float32)
+    y = rng.standard_normal((1024, 512)).astype(np.float32)
+    g = rng.standard_normal((1024, 512)).astype(np.float32)
+    xd = to_dev_f32(x).requires_grad_(True)
+    yd = to_dev_f32(y).requires_grad_(True)
+    out = Q.fp8_matmul(xd, yd, (1, 128))
+
+    def fwd(a, b):
+        p = odq(oq(a, (1, 128)), (1, 128)).astype(np.float64) @ odq(oq(b, (1, 128)), (1, 128)).astype(np.float64)
+        return odq(oq(p.astype(np.float32), (1, 128)), (1, 128))
+
+    out.backward(to_dev_f32(g))
+    assert rel(f32(xd.grad), fwd(g, y.T.copy())) <= TOL
+    assert rel(f32(yd.grad), fwd(x.T.copy(), g)) <= TOL
+    # the quantized transpose is the general quantizer's, byte for byte
+    qt = Q._quantized_transpose(xd.detach(), (1, 128))
+    assert_triple(qt, oq(np.ascontiguousarray(x.T), (1, 128)), "x^T")
+
+
 # ------------------------------------------------------------ elementwise
 @pytest.mark.parametrize("opname", ["add", "sub", "mul", "truediv"])
 def test_elementwise_bit_exact(Q, opname):

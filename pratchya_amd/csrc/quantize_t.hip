@@ -270,13 +270,33 @@ __global__ __launch_bounds__(GT ? 512 : 256) void k_quant_t128(const uint8_t* __
   }
   constexpr int INC = IN == IN_BF16S ? IN_BF16 : IN;   // element kind after the prologue
 
+  // fp8 input: each element is dequantized once, for its channel's maximum
+  // and its cast (the VALU, not memory, bounds this input's kernel); the
+  // other inputs recompute the cheap widening instead of holding 64 values
+  constexpr bool ONCE = INC == IN_FP8;
+  float vv[ONCE ? TOK : 1][ONCE ? 8 : 1];
+  if constexpr (ONCE) {
+    static_for<8>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+#pragma unroll
+      for (int r = 0; r < TOK; ++r) vv[r][j] = row_elem<INC, j>(w[r], dq[r]);
+    });
+  }
+  auto val = [&](auto jc, int r) -> float {
+    constexpr int j = decltype(jc)::value;
+    if constexpr (ONCE) return vv[r][j];
+    else return row_elem<INC, j>(w[r], dq[r]);
+  };
   // channel maxima (as |x| bits: unsigned order, NaN above inf) and group max
   uint32_t mx[8];
   static_for<8>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
     uint32_t m = 0;
 #pragma unroll
-    for (int r = 0; r < TOK; ++r) m = umax(m, row_abs_bits<INC, j>(w[r], dq[r]));
+    for (int r = 0; r < TOK; ++r) {
+      if constexpr (ONCE) m = umax(m, f2u(vv[r][j]) & 0x7FFFFFFFu);
+      else m = umax(m, row_abs_bits<INC, j>(w[r], dq[r]));
+    }
 #pragma unroll
     for (int sh = CGW; sh < 64; sh <<= 1) m = umax(m, shfl_xor_u32(m, sh));
     mx[j] = m;
@@ -332,10 +352,10 @@ __global__ __launch_bounds__(GT ? 512 : 256) void k_quant_t128(const uint8_t* __
     uint32_t near = 0;
 #pragma unroll
     for (int k = 0; k < TOK / 4; ++k) {
-      const float t0v = row_elem<INC, j>(w[4 * k + 0], dq[4 * k + 0]) * y[j];
-      const float t1v = row_elem<INC, j>(w[4 * k + 1], dq[4 * k + 1]) * y[j];
-      const float t2v = row_elem<INC, j>(w[4 * k + 2], dq[4 * k + 2]) * y[j];
-      const float t3v = row_elem<INC, j>(w[4 * k + 3], dq[4 * k + 3]) * y[j];
+      const float t0v = val(jc, 4 * k + 0) * y[j];
+      const float t1v = val(jc, 4 * k + 1) * y[j];
+      const float t2v = val(jc, 4 * k + 2) * y[j];
+      const float t3v = val(jc, 4 * k + 3) * y[j];
       if (check) near |= near_mid8(t0v) | near_mid8(t1v) | near_mid8(t2v) | near_mid8(t3v);
       o[k] = cvt4<HW>(t0v, t1v, t2v, t3v);
     }
@@ -343,10 +363,7 @@ __global__ __launch_bounds__(GT ? 512 : 256) void k_quant_t128(const uint8_t* __
       const float S = quant_scale(e[j], Gc[j]);
 #pragma unroll
       for (int k = 0; k < TOK / 4; ++k)
-        o[k] = cvt4_exact(row_elem<INC, j>(w[4 * k + 0], dq[4 * k + 0]),
-                          row_elem<INC, j>(w[4 * k + 1], dq[4 * k + 1]),
-                          row_elem<INC, j>(w[4 * k + 2], dq[4 * k + 2]),
-                          row_elem<INC, j>(w[4 * k + 3], dq[4 * k + 3]), S);
+        o[k] = cvt4_exact(val(jc, 4 * k + 0), val(jc, 4 * k + 1), val(jc, 4 * k + 2), val(jc, 4 * k + 3), S);
     }
     if (live) {
       if constexpr (TOK == 16) {

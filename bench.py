@@ -601,7 +601,9 @@ def bench_optimizer(steps: int):
                                 "frac_of_hbm_peak": round(upd_gbs / HBM_PEAK_GBS, 4), "bytes": upd_bytes},
             "ffn_down_newton_schulz": {"ms": round(ns_ms, 3), "TFLOP/s": round(ns_tf, 1),
                                        "frac_of_bf16_peak": round(ns_tf / BF16_PEAK_TFLOPS, 4),
-                                       "flop": leaf_ns_flop, "library": "torch.matmul (hipBLASLt)"},
+                                       "flop": leaf_ns_flop,
+                                       "kernels": "pratchya_gemm_bf16_nt x 2 + pratchya_transpose_b16 + "
+                                                  "pratchya_ns_combine per iteration"},
             "steps": steps}
 
 

@@ -239,7 +239,14 @@ __global__ __launch_bounds__(256) void k_quant_g8(const void* __restrict__ xv,
   constexpr int GROUP_BYTES = 1024 * (IS_BF16 ? 2 : 4);
   const int lane = threadIdx.x & 63;
   const int64_t wstride = (int64_t)gridDim.x * (blockDim.x >> 6);
-  int64_t g = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  // Workgroups are dispatched to the 8 XCDs round-robin; neighbouring groups
+  // write neighbouring bytes of the same scale lines (8 groups' e8m0 bytes,
+  // 16 groups' maxima per 64 bytes).  In each window of 128 workgroups, XCD x
+  // takes the 16 consecutive indices 16x .. 16x + 15, so one L2 writes each
+  // scale line back once, while the window still streams one contiguous range
+  int64_t wb = blockIdx.x;
+  if (gridDim.x % 128 == 0) wb = (blockIdx.x & ~127u) + (blockIdx.x % 8) * 16 + (blockIdx.x % 128) / 8;
+  int64_t g = wb * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (g >= n_groups) return;
   const char* xb = static_cast<const char*>(xv);
   // scale arrays as raw buffers (byte counts below 2^32 - 16, checked on the host)

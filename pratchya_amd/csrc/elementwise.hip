@@ -175,7 +175,13 @@ __global__ __launch_bounds__(256) void k_ew_rowgroup(QOperand X, QOperand Y, uin
                                                      uint8_t* __restrict__ sc8, float* __restrict__ sc32,
                                                      int64_t n, int64_t W, int bl_log2, int gl_log2) {
   const int lane = threadIdx.x & 63;
-  const int64_t base = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * 1024;
+  // Workgroups are dispatched to the 8 XCDs round-robin, and neighbouring
+  // waves read and write neighbouring bytes of the same scale lines: in each
+  // window of 128 workgroups XCD x takes the 16 consecutive indices
+  // 16x .. 16x + 15, so each scale line passes through one L2
+  int64_t wb = blockIdx.x;
+  if (gridDim.x % 128 == 0) wb = (blockIdx.x & ~127u) + (blockIdx.x % 8) * 16 + (blockIdx.x % 128) / 8;
+  const int64_t base = (wb * (blockDim.x >> 6) + (threadIdx.x >> 6)) * 1024;
   if (base >= n) return;
   const int64_t off = base + (int64_t)lane * 16;
   const bool live = off < n;

@@ -52,6 +52,7 @@ __device__ __forceinline__ bool near_bf16_midpoint(float t) {
 }
 
 __device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint32_t umin(uint32_t a, uint32_t b) { return a < b ? a : b; }
 
 __device__ __forceinline__ uint32_t shfl_xor_u32(uint32_t v, int m) {
   return (uint32_t)__shfl_xor((int)v, m, 64);
@@ -174,9 +175,16 @@ __device__ __forceinline__ uint32_t absmax8_bf16(const uint4& v) {
 // f32(128 / 1e-7f) rounded to nearest: the y of a clamped block.
 #define PRATCHYA_Y_CLAMP 1.28e9f
 
-// Near a bf16 rounding midpoint (low 16 bits within 8 of 0x8000).
-__device__ __forceinline__ uint32_t near_mid8(float t) {
-  return (((f2u(t) + 8u - 0x8000u) & 0xFFFFu) <= 16u) ? 1u : 0u;
+// Near a bf16 rounding midpoint: the low 16 bits within 8 of 0x8000, i.e.
+// (bits + 0x8008) mod 2^16 <= 16.  mid_key moves those 16 bits to the top
+// (one add-and-shift), so that t is near iff mid_key(t) <= kMidKey and the
+// minimum of several keys tests them all with one compare.
+constexpr uint32_t kMidKey = 16u << 16;
+__device__ __forceinline__ uint32_t mid_key(float t) { return (f2u(t) + 0x8008u) << 16; }
+__device__ __forceinline__ uint32_t mid_key4(float t0, float t1, float t2, float t3) {
+  const uint32_t a = mid_key(t0), b = mid_key(t1), c = mid_key(t2), d = mid_key(t3);
+  const uint32_t ab = a < b ? a : b, cd = c < d ? c : d;
+  return ab < cd ? ab : cd;
 }
 
 // Scales of one block for the division-free cast (the arithmetic of
@@ -208,7 +216,7 @@ __device__ __forceinline__ BlockScale block_scale(uint32_t mb, uint32_t Gb, floa
 // (x0..x3), dequantized as (f32(q) * dq) / 128 (dq = 2^(e-127) * G, or the
 // repaired scale of quantize_impl_bwd).  finite (G finite): the division-free
 // cast with y from block_scale, a word with a value near a bf16 rounding
-// midpoint (the near_mid8 test, as one compare of the smallest distance)
+// midpoint (the mid_key test, as one compare of the smallest key)
 // redone exactly; otherwise the exact composition.  S = quant_scale(e, G).
 // dqx = dq / 128 when one_mul (see dequant_one_mul), else dq.
 __device__ __forceinline__ void fake_quant4(float& x0, float& x1, float& x2, float& x3, float y, float S,
@@ -217,10 +225,7 @@ __device__ __forceinline__ void fake_quant4(float& x0, float& x1, float& x2, flo
   if (finite) {
     const float t0 = x0 * y, t1 = x1 * y, t2 = x2 * y, t3 = x3 * y;
     w = cvt4_hw(t0, t1, t2, t3);
-    const uint32_t d0 = (f2u(t0) + 0x8008u) & 0xFFFFu, d1 = (f2u(t1) + 0x8008u) & 0xFFFFu;
-    const uint32_t d2 = (f2u(t2) + 0x8008u) & 0xFFFFu, d3 = (f2u(t3) + 0x8008u) & 0xFFFFu;
-    const uint32_t dmin = d0 < d1 ? d0 : d1, dmin2 = d2 < d3 ? d2 : d3;
-    if ((dmin < dmin2 ? dmin : dmin2) <= 16u) w = cvt4_exact(x0, x1, x2, x3, S);
+    if (mid_key4(t0, t1, t2, t3) <= kMidKey) w = cvt4_exact(x0, x1, x2, x3, S);
   } else {
     w = cvt4_exact(x0, x1, x2, x3, S);
   }

@@ -353,7 +353,7 @@ __global__ __launch_bounds__(256) void k_quant_g8(const void* __restrict__ xv,
             const float x2 = elem_f32<IS_BF16>(v[r], 4 * j + 2), x3 = elem_f32<IS_BF16>(v[r], 4 * j + 3);
             const float t0 = x0 * y[r], t1 = x1 * y[r], t2 = x2 * y[r], t3 = x3 * y[r];
             out[r][j] = cvt4<HW>(t0, t1, t2, t3);
-            if (near_mid8(t0) | near_mid8(t1) | near_mid8(t2) | near_mid8(t3))
+            if (mid_key4(t0, t1, t2, t3) <= kMidKey)
               out[r][j] = cvt4_exact(x0, x1, x2, x3, quant_scale(e[r], G));
           }
         }

@@ -127,7 +127,7 @@ __global__ __launch_bounds__(GT ? 512 : 256) void k_quant_t128(const uint8_t* __
                                                     const float* __restrict__ x_sc32, int kg_shift,
                                                     int64_t T, int64_t C, uint8_t* __restrict__ qt,
                                                     uint8_t* __restrict__ sc8,
-                                                    float* __restrict__ sc32) {
+                                                    float* __restrict__ sc32, int tok_major) {
   constexpr int ESZ = InTraits<IN>::ESZ;
   constexpr int NW = InTraits<IN>::NW;
   const int lane = threadIdx.x & 63;
@@ -139,6 +139,11 @@ __global__ __launch_bounds__(GT ? 512 : 256) void k_quant_t128(const uint8_t* __
   // Workgroups are dispatched to the 8 XCDs round-robin in linear order; the
   // linear index is remapped so that neighbours run on one XCD (one L2).
   uint32_t bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+  if (!GT && tok_major) {
+    // the grid's x axis walks the token blocks of one channel chunk
+    bx = blockIdx.y;
+    by = blockIdx.x;
+  }
   if constexpr (GT) {
     const uint32_t gx = gridDim.x, gy = gridDim.y, n = gx * gy * gridDim.z;
     uint32_t b = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
@@ -336,12 +341,21 @@ __global__ __launch_bounds__(GT ? 512 : 256) void k_quant_t128(const uint8_t* __
   uint32_t clamped = 0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
+    // finite G: the exponent-difference e8m0 of block_scale (exact; its
+    // division fallback covers subnormal and zero maxima); a non-finite G
+    // takes the exact cast below, and counts as clamped for the check
     const float G = Gc[j];
-    e[j] = e8m0_of(u2f(mx[j]), G);
-    const float sG = e8m0_decode(e[j]) * G;
-    const bool cl = !(sG >= kClamp);
-    y[j] = cl ? PRATCHYA_Y_CLAMP : u2f((254u - e[j]) << 23) * __builtin_amdgcn_rcpf(G * 0.0078125f);
-    clamped |= cl ? 1u : 0u;
+    const uint32_t Gbj = f2u(G);
+    if ((Gbj >> 23) < 255u) {
+      const BlockScale bs = block_scale(mx[j], Gbj, __builtin_amdgcn_rcpf(G * 0.0078125f));
+      e[j] = bs.e;
+      y[j] = bs.y;
+      clamped |= bs.clamped ? 1u : 0u;
+    } else {
+      e[j] = e8m0_of(u2f(mx[j]), G);
+      y[j] = PRATCHYA_Y_CLAMP;
+      clamped = 1u;
+    }
   }
   const bool check = INC != IN_BF16 || __any(clamped);
 
@@ -349,17 +363,17 @@ __global__ __launch_bounds__(GT ? 512 : 256) void k_quant_t128(const uint8_t* __
   static_for<8>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
     uint32_t o[TOK / 4];
-    uint32_t near = 0;
+    uint32_t key = 0xFFFFFFFFu;                  // smallest midpoint key of the chunk
 #pragma unroll
     for (int k = 0; k < TOK / 4; ++k) {
       const float t0v = val(jc, 4 * k + 0) * y[j];
       const float t1v = val(jc, 4 * k + 1) * y[j];
       const float t2v = val(jc, 4 * k + 2) * y[j];
       const float t3v = val(jc, 4 * k + 3) * y[j];
-      if (check) near |= near_mid8(t0v) | near_mid8(t1v) | near_mid8(t2v) | near_mid8(t3v);
+      if (check) key = umin(key, mid_key4(t0v, t1v, t2v, t3v));
       o[k] = cvt4<HW>(t0v, t1v, t2v, t3v);
     }
-    if (near || !((f2u(Gc[j]) >> 23) < 255u)) {
+    if (key <= kMidKey || !((f2u(Gc[j]) >> 23) < 255u)) {
       const float S = quant_scale(e[j], Gc[j]);
 #pragma unroll
       for (int k = 0; k < TOK / 4; ++k)
@@ -526,22 +540,29 @@ __global__ __launch_bounds__(256) void k_quant_t1x128_fp8(const uint8_t* __restr
     static_for<8>([&](auto jc) {
       constexpr int j = decltype(jc)::value;
       const float G = Gc[j];
-      const uint32_t e = e8m0_of(u2f(bm[lc + j][tb]), G);
-      const float sG = e8m0_decode(e) * G;
-      const float y =
-          !(sG >= kClamp) ? PRATCHYA_Y_CLAMP : u2f((254u - e) << 23) * __builtin_amdgcn_rcpf(G * 0.0078125f);
+      const uint32_t Gbj = f2u(G), mb = bm[lc + j][tb];
+      uint32_t e;
+      float y;
+      if ((Gbj >> 23) < 255u) {                 // finite: exponent-difference e8m0
+        const BlockScale bs = block_scale(mb, Gbj, __builtin_amdgcn_rcpf(G * 0.0078125f));
+        e = bs.e;
+        y = bs.y;
+      } else {                                  // the exact cast below
+        e = e8m0_of(u2f(mb), G);
+        y = PRATCHYA_Y_CLAMP;
+      }
       uint32_t o[TOK / 4];
-      uint32_t near = 0;
+      uint32_t key = 0xFFFFFFFFu;                // smallest midpoint key of the chunk
 #pragma unroll
       for (int k = 0; k < TOK / 4; ++k) {
         const float t0v = row_elem<IN_FP8, j>(w[4 * k + 0], dq[4 * k + 0]) * y;
         const float t1v = row_elem<IN_FP8, j>(w[4 * k + 1], dq[4 * k + 1]) * y;
         const float t2v = row_elem<IN_FP8, j>(w[4 * k + 2], dq[4 * k + 2]) * y;
         const float t3v = row_elem<IN_FP8, j>(w[4 * k + 3], dq[4 * k + 3]) * y;
-        near |= near_mid8(t0v) | near_mid8(t1v) | near_mid8(t2v) | near_mid8(t3v);
+        key = umin(key, mid_key4(t0v, t1v, t2v, t3v));
         o[k] = cvt4<true>(t0v, t1v, t2v, t3v);
       }
-      if (near || !((f2u(G) >> 23) < 255u)) {
+      if (key <= kMidKey || !((f2u(G) >> 23) < 255u)) {
         const float S = quant_scale(e, G);
 #pragma unroll
         for (int k = 0; k < TOK / 4; ++k)
@@ -601,9 +622,14 @@ extern "C" int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t*
   // f32 and fp8 inputs, where occupancy matters more than segment length
   // (measured on [16384, 2048] and [16384, 8192]: bf16 85 vs 106 us, fp8 44 vs
   // 36 us, f32 57 vs 48 us for 16 vs 8 tokens)
+  // bf16 inputs of 8192 channels or more walk the token blocks of one channel
+  // chunk along the grid's x axis (measured on [32768, 16384] with scales:
+  // 365 -> 291 us; slower for fewer channels and for fp8 inputs)
+  const int tok_major = x_dtype == PRATCHYA_DT_BF16 && C >= 8192 && C / 256 <= 65535 ? 1 : 0;
   auto grid_for_tok = [&](int tok) {
     const int cpw = 8 * (64 / (128 / tok));             // channels per wave
-    return dim3((unsigned)((C + 4 * cpw - 1) / (4 * cpw)), (unsigned)(T / 128), (unsigned)slices);
+    const unsigned nc = (unsigned)((C + 4 * cpw - 1) / (4 * cpw)), nt = (unsigned)(T / 128);
+    return tok_major ? dim3(nt, nc, (unsigned)slices) : dim3(nc, nt, (unsigned)slices);
   };
   const uint8_t* xb = static_cast<const uint8_t*>(x);
   // blocks per group of a (1, 128) input: gcd(8, n_blk), a power of two
@@ -611,16 +637,16 @@ extern "C" int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t*
   const int kg_shift = kg == 8 ? 3 : (kg == 4 ? 2 : (kg == 2 ? 1 : 0));
   if (x_dtype == PRATCHYA_DT_BF16 && scaled) {
     hipLaunchKernelGGL((k_quant_t128<IN_BF16S, true, 16>), grid_for_tok(16), dim3(256), 0, stream, xb, x_sc8, x_sc32, kg_shift,
-                       T, C, xt_fp8, sc_fp8, sc_fp32);
+                       T, C, xt_fp8, sc_fp8, sc_fp32, tok_major);
   } else if (x_dtype == PRATCHYA_DT_BF16) {
     hipLaunchKernelGGL((k_quant_t128<IN_BF16, true, 16>), grid_for_tok(16), dim3(256), 0, stream, xb, nullptr, nullptr, 0,
-                       T, C, xt_fp8, sc_fp8, sc_fp32);
+                       T, C, xt_fp8, sc_fp8, sc_fp32, tok_major);
   } else if (x_dtype == PRATCHYA_DT_F32) {
     hipLaunchKernelGGL((k_quant_t128<IN_F32, true, 8>), grid_for_tok(8), dim3(256), 0, stream, xb, nullptr, nullptr, 0,
-                       T, C, xt_fp8, sc_fp8, sc_fp32);
+                       T, C, xt_fp8, sc_fp8, sc_fp32, tok_major);
   } else {
     hipLaunchKernelGGL((k_quant_t128<IN_FP8, true, 8>), grid_for_tok(8), dim3(256), 0, stream, xb, x_sc8, x_sc32, kg_shift,
-                       T, C, xt_fp8, sc_fp8, sc_fp32);
+                       T, C, xt_fp8, sc_fp8, sc_fp32, tok_major);
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess)
@@ -668,13 +694,13 @@ extern "C" int pratchya_quantize_t1x128(const void* x, int x_dtype, const uint8_
   const int kg_shift = kg == 8 ? 3 : (kg == 4 ? 2 : (kg == 2 ? 1 : 0));
   if (x_dtype == PRATCHYA_DT_BF16 && scaled) {
     hipLaunchKernelGGL((k_quant_t128<IN_BF16S, true, 16, true>), grid_for_tok(16), dim3(512), 0, stream, xb, x_sc8,
-                       x_sc32, kg_shift, T, C, xt_fp8, sc_fp8, sc_fp32);
+                       x_sc32, kg_shift, T, C, xt_fp8, sc_fp8, sc_fp32, 0);
   } else if (x_dtype == PRATCHYA_DT_BF16) {
     hipLaunchKernelGGL((k_quant_t128<IN_BF16, true, 16, true>), grid_for_tok(16), dim3(512), 0, stream, xb, nullptr,
-                       nullptr, 0, T, C, xt_fp8, sc_fp8, sc_fp32);
+                       nullptr, 0, T, C, xt_fp8, sc_fp8, sc_fp32, 0);
   } else if (x_dtype == PRATCHYA_DT_F32) {
     hipLaunchKernelGGL((k_quant_t128<IN_F32, true, 8, true>), grid_for_tok(8), dim3(512), 0, stream, xb, nullptr,
-                       nullptr, 0, T, C, xt_fp8, sc_fp8, sc_fp32);
+                       nullptr, 0, T, C, xt_fp8, sc_fp8, sc_fp32, 0);
   } else {
     // one workgroup per 128-channel column and 1024-token group
     hipLaunchKernelGGL(k_quant_t1x128_fp8, dim3((unsigned)(C / 128), (unsigned)(T / 1024), (unsigned)slices),

@@ -386,6 +386,47 @@ def bench_gemm_ffn():
             "hipblaslt_fp8_no_block_scales": bench_library_fp8(10, (M, Kd, N))}, sample
 
 
+def bench_mfma_ceiling():
+    """The MFMA pipes' sustained rate on the GEMMs' own operand bytes with no
+    memory traffic (``pratchya_mfma_ceiling``: the GEMM kernel's MFMA sequence
+    back to back on every SIMD), next to the datasheet peaks: fp8 on config 3's
+    A payload and transposed W payload, bf16 on two N(0, 1) bf16 [4096, 16384]
+    matrices (a Newton-Schulz leaf's shape).  Each launch runs ~25 ms so that
+    the clock settles under the load; median of 5 event-timed launches after
+    one untimed one."""
+    import torch
+    from oracle import qarr_oracle as O
+    from pratchya_amd import _kernels as K
+    M, Kd, N = 16384, 2048, 8192
+    x = torch.from_numpy(O.activation_input(M, Kd, seed=2).view(np.int16)).view(torch.bfloat16).cuda()
+    w = torch.from_numpy(O.normal_input((Kd, N), 0.02, seed=3).view(np.int16)).view(torch.bfloat16).cuda()
+    a8 = K.quantize(x, (1, 128))[0].view(torch.uint8)
+    b8 = K.operand_transposed(*K.quantize(w, (128, 128)), (128, 128)).payload.view(torch.uint8)
+    g = torch.Generator(device="cuda").manual_seed(7)
+    abf = torch.randn((4096, 16384), generator=g, device="cuda").to(torch.bfloat16)
+    bbf = torch.randn((4096, 16384), generator=g, device="cuda").to(torch.bfloat16)
+    st = torch.cuda.current_stream()
+    res = {}
+    for name, a, b, bf, iters, peak in (("fp8", a8, b8, False, 24000, FP8_PEAK_TFLOPS),
+                                        ("bf16", abf, bbf, True, 24000, BF16_PEAK_TFLOPS)):
+        flop = K.mfma_ceiling(a, b, bf, iters)
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            K.mfma_ceiling(a, b, bf, iters)
+            e1.record(st)
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1))
+        ms = float(np.median(times))
+        tf = flop / (ms * 1e-3) / 1e12
+        res[name] = {"TFLOP/s": round(tf, 1), "frac_of_peak": round(tf / peak, 4), "ms_per_launch": round(ms, 3)}
+    res["operands"] = ("fp8: config 3's A and transposed W payloads; bf16: two N(0,1) [4096,16384]; "
+                       "no memory traffic, LDS or barriers in the timed loop")
+    return res
+
+
 def bench_library_fp8(steps: int, shape=(16384, 2048, 8192)):
     """Reference point for the GEMM: hipBLASLt's plain FP8 GEMM
     (``torch._scaled_mm``, e4m3fn operands, one scale per tensor, bf16 out) at
@@ -856,7 +897,8 @@ def main():
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--counter-workload", action="store_true",
                     help="only run the direct-launch workload used for rocprofv3 --pmc runs")
-    ap.add_argument("--only", choices=["cfg3", "ffn", "cfg4", "cfg5", "optim", "elementwise", "embedding"],
+    ap.add_argument("--only", choices=["cfg3", "ffn", "cfg4", "cfg5", "optim", "elementwise", "embedding",
+                                       "ceiling"],
                     default=None,
                     help="run one secondary configuration alone (for profiling) and print its result")
     args = ap.parse_args()
@@ -887,6 +929,8 @@ def main():
             res = bench_elementwise(max(20, args.steps // 2), max(4, args.warmup // 4))
         elif args.only == "embedding":
             res = bench_embedding(max(20, args.steps // 4), max(4, args.warmup // 4))
+        elif args.only == "ceiling":
+            res = bench_mfma_ceiling()
         else:
             res = bench_config5()
         print(json.dumps({args.only: res}), flush=True)
@@ -906,6 +950,10 @@ def main():
     extra["elementwise_add"] = bench_elementwise(max(20, args.steps // 2), max(4, args.warmup // 4))
     _log(f"elementwise add: {extra['elementwise_add']['us']} us")
     if not args.no_gemm:
+        _log("mfma ceiling: start")
+        extra["mfma_ceiling"] = bench_mfma_ceiling()
+        _log(f"mfma ceiling: fp8 {extra['mfma_ceiling']['fp8']['TFLOP/s']} TFLOP/s, "
+             f"bf16 {extra['mfma_ceiling']['bf16']['TFLOP/s']} TFLOP/s")
         _log("config 3 gemm fwd: start")
         gms, tflops, cfg3_sample = bench_gemm_fwd()
         _log(f"config 3 gemm fwd: {gms * 1e3:.1f} us, {tflops:.1f} TFLOP/s")

@@ -367,6 +367,18 @@ int64_t pratchya_gemm_span(int64_t rows, int64_t K, int64_t r_div, int64_t s_r, 
 int pratchya_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* dst,
                           hipStream_t stream);
 
+/* Measurement aid, no counterpart in the reference: the GEMM kernel's MFMA
+ * sequence (fp8: v_mfma_scale_f32_32x32x64_f8f6f4; bf16 != 0: two
+ * v_mfma_f32_32x32x16_bf16 per 64 bytes of K) run back to back on operand
+ * bytes from A and B (the first 256 rows, 128 bytes of each; ld the row
+ * stride in bytes, >= 128), `iters` times per wave on every compute unit, with
+ * no memory traffic in the loop: the sustained MFMA rate on such data, which a
+ * power-limited clock sets below the datasheet peak.  *flop receives the FLOP
+ * count of the launch (for timing by the caller); out (one float, device) is
+ * written only to keep the loop alive. */
+int pratchya_mfma_ceiling(const void* A, const void* B, int64_t ld, int bf16, int64_t iters, float* out,
+                          int64_t* flop, hipStream_t stream);
+
 /* Test hooks for the element conversions the kernels use (no reference
  * counterpart; they let the tests check the device arithmetic exhaustively).
  *   mode 0: software bit arithmetic, mode 1: gfx950 conversion instructions.

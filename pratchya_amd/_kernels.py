@@ -682,6 +682,24 @@ def transpose_b16(x: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def mfma_ceiling(a: torch.Tensor, b: torch.Tensor, bf16: bool, iters: int) -> int:
+    """Launch the MFMA-rate probe (``pratchya_mfma_ceiling``, a measurement aid
+    with no reference counterpart) on the bytes of ``a`` and ``b`` (2-D,
+    contiguous, at least 256 rows of 128 bytes); returns the launch's FLOP count
+    for the caller's timing."""
+    _require_gpu(a, b)
+    if a.dim() != 2 or b.dim() != 2 or a.shape[0] < 256 or b.shape[0] < 256:
+        raise ValueError("mfma_ceiling: operands of at least 256 rows")
+    ld = int(a.stride(0)) * a.element_size()
+    if int(b.stride(0)) * b.element_size() != ld:
+        raise ValueError("mfma_ceiling: a and b need the same row stride")
+    sink = torch.empty(1, dtype=torch.float32, device=a.device)
+    flop = ctypes.c_int64(0)
+    _lib.check(_lib.load().pratchya_mfma_ceiling(_ptr(a), _ptr(b), ld, 1 if bf16 else 0, int(iters), _ptr(sink),
+                                                 ctypes.byref(flop), _stream(a)), "mfma_ceiling")
+    return int(flop.value)
+
+
 def gemm_nt_fq(a: Operand, b: Operand, out_dtype: torch.dtype, fix_nan: bool = False, lead=None):
     """``QArrayImpl(dequant(a) @ dequant(b)^T, (1, 128)).astype(out_dtype)``
     with the requantization in the GEMM's epilogue: returns ``(y [M, N],

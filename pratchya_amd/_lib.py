@@ -78,6 +78,7 @@ SIGNATURES = {
                                           ctypes.POINTER(_c_int), _c_p, _c_i64, _c_i64, _c_p]),
     "pratchya_gemm_span": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
     "pratchya_transpose_u8": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "pratchya_mfma_ceiling": (_c_int, [_c_p, _c_p, _c_i64, _c_int, _c_i64, _c_p, ctypes.POINTER(_c_i64), _c_p]),
     "pratchya_debug_bf16_to_e4m3": (_c_int, [_c_p, _c_p, _c_i64, _c_int, _c_p]),
     "pratchya_debug_f32_to_bf16": (_c_int, [_c_p, _c_p, _c_i64, _c_int, _c_p]),
 }

@@ -534,7 +534,7 @@ __device__ __forceinline__ void fq_row_scales(v16f (&acc)[2][4], const float (&g
     for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
       for (int v = 0; v < 16; ++v) a = umax(a, f2u(acc[mi][ni][v]) & 0x7FFFFFFFu);
-    m[mi] = umax(a, shfl_xor_u32(a, 32));
+    m[mi] = xor_max_u32<32>(a);
   }
   const uint32_t mb = lhi ? m[1] : m[0];      // this lane's row: lhi * 32 + l32
   uint32_t* gm = fq.gmax + (int64_t)strip * 256 + wm * 64 + lhi * 32 + l32;
@@ -932,6 +932,61 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     if constexpr (!BF) publish_g(h, lds, g_st, g_ld, g_first, u_prev);
     __syncthreads();
   }
+}
+
+// Measurement aid (no counterpart in the reference): the sustained rate of
+// the GEMM's own MFMA sequence on given operand bytes, with no memory traffic,
+// LDS or barriers in the loop -- the ceiling a GEMM on these operands can
+// approach on this part.  Each wave loads two sets of the fragments the GEMM's
+// wave would read (its 64 A rows and 128 B rows of the first 256, 32 bytes of
+// K per lane, two 64-byte K slices), then issues mfma_all on them
+// alternately, `iters` times each; both waves of every SIMD issue, so the
+// MFMA pipes never wait on an operand.  The e8m0 bytes are 2^-7 and 2^-8 (as
+// in real data, the scale does not change the work).
+template <bool BF>
+__global__ __launch_bounds__(NTHREADS, 1) void k_mfma_ceiling(const uint8_t* __restrict__ A,
+                                                             const uint8_t* __restrict__ B, int64_t ld,
+                                                             int iters, float* __restrict__ out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l32 = lane & 31, lhi = lane >> 5;
+  v8i fa[2][2], fb[2][4];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+      fa[s][mi] = *reinterpret_cast<const v8i*>(A + (int64_t)((wave & 3) * 64 + mi * 32 + l32) * ld + s * 64 + lhi * 32);
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+      fb[s][ni] = *reinterpret_cast<const v8i*>(B + (int64_t)((wave >> 2) * 128 + ni * 32 + l32) * ld + s * 64 + lhi * 32);
+  }
+  v16f acc[2][4];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = v16f{0};
+  const uint32_t eA = 0x78787878u, eB = 0x77777777u;
+  for (int it = 0; it < iters; ++it) {
+    pin_frags(fa[0], fb[0]);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      mfma_tile<0, 0, BF>(acc, fa[s], fb[s], eA, eB);
+      mfma_tile<0, 1, BF>(acc, fa[s], fb[s], eA, eB);
+      mfma_tile<0, 2, BF>(acc, fa[s], fb[s], eA, eB);
+      mfma_tile<0, 3, BF>(acc, fa[s], fb[s], eA, eB);
+      mfma_tile<1, 0, BF>(acc, fa[s], fb[s], eA, eB);
+      mfma_tile<1, 1, BF>(acc, fa[s], fb[s], eA, eB);
+      mfma_tile<1, 2, BF>(acc, fa[s], fb[s], eA, eB);
+      mfma_tile<1, 3, BF>(acc, fa[s], fb[s], eA, eB);
+    }
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sum += acc[mi][ni][v];
+  if (sum == 1.2345e-38f) out[0] = sum;    // keeps the loop; never true for these operands in practice
 }
 
 // Compute units of the current device (cached per device), rounded down to a
@@ -1429,6 +1484,31 @@ extern "C" int pratchya_split_pack_bf16(const void* src, int src_dtype, int64_t 
   else PRATCHYA_SPLIT(false, false);
 #undef PRATCHYA_SPLIT
   return launch_status("split_pack");
+}
+
+extern "C" int pratchya_mfma_ceiling(const void* A, const void* B, int64_t ld, int bf16, int64_t iters,
+                                     float* out, int64_t* flop, hipStream_t stream) {
+  if (!A || !B || !out || !flop) return pratchya_set_error(PRATCHYA_EINVAL, "mfma_ceiling: null pointer");
+  if (ld < 128 || ld % 16 || iters < 1 || iters > INT32_MAX ||
+      (reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) % 16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "mfma_ceiling: ld must be >= 128 and a multiple of 16, buffers "
+                              "16-byte aligned, iters in [1, 2^31)");
+  const int64_t grid = gemm_num_cus();
+  // per wave and iteration: 16 mfma_tile calls, each 32 x 32 x 64 bytes of K
+  // (fp8: one 32x32x64 MFMA, 131072 FLOP; bf16: two 32x32x16, 65536 FLOP)
+  *flop = grid * (NTHREADS / 64) * iters * 16 * (bf16 ? 65536 : 131072);
+  const uint8_t* a8 = static_cast<const uint8_t*>(A);
+  const uint8_t* b8 = static_cast<const uint8_t*>(B);
+  if (bf16)
+    hipLaunchKernelGGL((k_mfma_ceiling<true>), dim3((unsigned)grid), dim3(NTHREADS), 0, stream, a8, b8, ld,
+                       (int)iters, out);
+  else
+    hipLaunchKernelGGL((k_mfma_ceiling<false>), dim3((unsigned)grid), dim3(NTHREADS), 0, stream, a8, b8, ld,
+                       (int)iters, out);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess)
+    return pratchya_set_error(PRATCHYA_EHIP, "mfma_ceiling: launch failed: %s", hipGetErrorString(err));
+  return PRATCHYA_OK;
 }
 
 extern "C" int pratchya_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* dst,

@@ -92,6 +92,24 @@ __device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v) {
   return umax(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true));
 }
 
+// Max with the lane X = 16 or 32 positions away (lane ^ X), by gfx950's row
+// swaps: v_permlane16_swap exchanges the odd 16-lane rows of one register with
+// the even rows of the other, v_permlane32_swap the upper half of one with the
+// lower half of the other; with the same value in both, the two results hold
+// each lane's own value and its partner's, in some order.  VALU operations,
+// where a __shfl_xor is an LDS permute with its latency.
+template <int X>
+__device__ __forceinline__ uint32_t xor_max_u32(uint32_t v) {
+  static_assert(X == 16 || X == 32, "row swaps exchange 16 or 32 lanes");
+  if constexpr (X == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return umax(p[0], p[1]);
+  } else {
+    const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return umax(p[0], p[1]);
+  }
+}
+
 // Max over aligned groups of BL lanes; every lane of the group gets the result.
 template <int BL>
 __device__ __forceinline__ uint32_t lane_group_max(uint32_t v) {
@@ -99,9 +117,21 @@ __device__ __forceinline__ uint32_t lane_group_max(uint32_t v) {
   if constexpr (BL >= 4) v = dpp_max_u32<0x4E>(v);   // quad_perm [2,3,0,1]
   if constexpr (BL >= 8) v = dpp_max_u32<0x141>(v);  // row_half_mirror
   if constexpr (BL >= 16) v = dpp_max_u32<0x140>(v); // row_mirror
-  if constexpr (BL >= 32) v = umax(v, shfl_xor_u32(v, 16));
-  if constexpr (BL >= 64) v = umax(v, shfl_xor_u32(v, 32));
+  if constexpr (BL >= 32) v = xor_max_u32<16>(v);
+  if constexpr (BL >= 64) v = xor_max_u32<32>(v);
   return v;
+}
+
+// Max over the 64 / W lanes that share lane % W (W = 4 or 8), for every lane:
+// within each 16-lane row by DPP row rotations (by 4 and 8 lanes: together
+// they reach the row's lanes of the same residue), across rows by the swaps.
+template <int W>
+__device__ __forceinline__ uint32_t strided_lane_max(uint32_t v) {
+  static_assert(W == 4 || W == 8, "lane stride 4 or 8");
+  if constexpr (W == 4) v = dpp_max_u32<0x124>(v);   // row_ror:4
+  v = dpp_max_u32<0x128>(v);                          // row_ror:8
+  v = xor_max_u32<16>(v);
+  return xor_max_u32<32>(v);
 }
 
 __device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int lane) {

@@ -302,8 +302,7 @@ __global__ __launch_bounds__(GT ? 512 : 256) void k_quant_t128(const uint8_t* __
       if constexpr (ONCE) m = umax(m, f2u(vv[r][j]) & 0x7FFFFFFFu);
       else m = umax(m, row_abs_bits<INC, j>(w[r], dq[r]));
     }
-#pragma unroll
-    for (int sh = CGW; sh < 64; sh <<= 1) m = umax(m, shfl_xor_u32(m, sh));
+    m = strided_lane_max<CGW>(m);
     mx[j] = m;
   });
   // group maxima: of the lane's 8 channels (tgrid (128, 1)), or per channel
@@ -504,8 +503,7 @@ __global__ __launch_bounds__(256) void k_quant_t1x128_fp8(const uint8_t* __restr
       uint32_t m = 0;
 #pragma unroll
       for (int r = 0; r < TOK; ++r) m = umax(m, row_abs_bits<IN_FP8, j>(w[r], dq[r]));
-#pragma unroll
-      for (int sh = CGW; sh < 64; sh <<= 1) m = umax(m, shfl_xor_u32(m, sh));
+      m = strided_lane_max<CGW>(m);
       if (rs == 0) bm[lc + j][tb] = m;
     });
   }

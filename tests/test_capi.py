@@ -337,3 +337,15 @@ def test_gather_quantize_codes_without_gpu():
     assert f(None, None, None, 0, 256, 1, 128, None, 1, 40, 8, 128, None, None, None, None, 0, None) == _lib.EINVAL
     assert f(None, None, None, 512, 256, 128, 128, None, 1, 40, 8, 128, None, None, None, None, 0, None) == _lib.EINVAL
     assert b"null buffer" in lib.pratchya_last_error()
+
+
+def test_mfma_ceiling_argument_codes_without_gpu():
+    """The MFMA-rate probe rejects null pointers and short rows before any launch."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    flop = ctypes.c_int64(0)
+    p = ctypes.c_void_p(16)
+    assert lib.pratchya_mfma_ceiling(None, p, 128, 0, 1, p, ctypes.byref(flop), None) == _lib.EINVAL
+    assert lib.pratchya_mfma_ceiling(p, p, 64, 0, 1, p, ctypes.byref(flop), None) == _lib.EINVAL
+    assert lib.pratchya_mfma_ceiling(p, p, 128, 0, 0, p, ctypes.byref(flop), None) == _lib.EINVAL
+    assert lib.pratchya_mfma_ceiling(p, p, 128, 1, 1, p, None, None) == _lib.EINVAL

@@ -99,6 +99,35 @@ def test_fp8_input_requantized_along_tokens(T, C):
     check(dev8, deq, f"fp8 [{T},{C}]", torch.from_numpy(s8).cuda(), torch.from_numpy(s32).cuda())
 
 
+def test_fp8_input_many_tiles_sampled_token_blocks():
+    """An fp8 input with more 128 x 128 tiles than the streaming kernel's grid
+    (2 slices x 64 token blocks x 16 channel blocks = 2048 tiles), so that each
+    workgroup walks several tiles through both LDS buffers: sampled 128-token
+    slabs of each slice against the oracle's dequantize -> (128, 1) quantize of
+    the same slab (its groups lie inside the slab)."""
+    S, T, C = 2, 8192, 2048
+    g = torch.Generator(device="cuda").manual_seed(23)
+    x = torch.randn((S, T, C), generator=g, device="cuda")
+    x[:, :, 5] *= 50.0
+    x8, s8, s32 = _K().quantize(x.to(torch.bfloat16), (1, 128))
+    xt, t8, t32 = _K().quantize_t128(x8, s8, s32)
+    torch.cuda.synchronize()
+    x8_h, s8_h, s32_h = u8(x8), u8(s8).reshape(S, -1), f32(s32).reshape(S, -1)
+    xt_h, t8_h, t32_h = u8(xt), u8(t8).reshape(S, -1), f32(t32).reshape(S, -1)
+    gpr = C // 1024                             # input groups per token row
+    for s in range(S):
+        for tb in (0, 1, 31, 63):
+            rows = slice(tb * 128, (tb + 1) * 128)
+            g0 = tb * 128 * gpr
+            deq = O.dequantize_impl(x8_h[s, rows], s8_h[s, g0 * 8:(g0 + 128 * gpr) * 8].reshape(-1, 8),
+                                    s32_h[s, g0:g0 + 128 * gpr].reshape(-1, 1, 1), "float32", (1, 128))
+            r8, rs8, rs32 = oracle_t128(deq)
+            what = f"slice {s} slab {tb}"
+            assert_payload_equal(xt_h[s, :, rows], r8, f"{what} payload")
+            assert_bytes_equal(t8_h[s, tb * C:(tb + 1) * C], rs8.reshape(-1), f"{what} e8m0")
+            assert_f32_bits_equal(t32_h[s, tb * C // 8:(tb + 1) * C // 8], rs32.reshape(-1), f"{what} G")
+
+
 def test_fp8_input_every_payload_byte():
     """Every finite e4m3fn byte (normals, subnormals, zeros of both signs) as
     the stored payload, under several block scales; then the NaN bytes."""

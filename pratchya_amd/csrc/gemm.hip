@@ -909,6 +909,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     } else {
       load_units<BG>(lds + OFF_UA, lds + OFF_UB, wm, wn, lane, gA, gB);
     }
+    // the next tile's stage 0 and group maxima (loaded during the last K steps)
+    // land before the epilogue issues its stores, so that the tile end waits
+    // for LDS work only
+    __builtin_amdgcn_s_waitcnt(0x0F70);      // vmcnt(0)
+    asm volatile("" ::"v"(g_ld));
     if constexpr (FQ != 0) {
       static_assert(BG == 0, "output requantization takes B scale groups of 32 rows or more");
       uint8_t* table = lds + LDS_BYTES + wave * 64 * 16;
@@ -926,11 +931,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     tn = tn2;
     cur = nxt;
     par = (par + nk) & 1;
-    // the next tile's stage 0 (and this tile's output stores) complete, and
-    // every wave is done with the staging buffer
-    __builtin_amdgcn_s_waitcnt(0);
+    // every wave is done with the staging buffer (its LDS reads); the next
+    // tile's stage 0 landed before the epilogue, and the output stores are not
+    // waited for: they drain while the next tile starts
+    PINNED_WAITCNT(0xC07F);
     if constexpr (!BF) publish_g(h, lds, g_st, g_ld, g_first, u_prev);
-    __syncthreads();
+    PINNED_WAITCNT(0xC07F);
+    wg_barrier();
   }
 }
 

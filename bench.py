@@ -643,8 +643,9 @@ def bench_optimizer(steps: int):
             "ffn_down_newton_schulz": {"ms": round(ns_ms, 3), "TFLOP/s": round(ns_tf, 1),
                                        "frac_of_bf16_peak": round(ns_tf / BF16_PEAK_TFLOPS, 4),
                                        "flop": leaf_ns_flop,
-                                       "kernels": "pratchya_gemm_bf16_nt x 2 + pratchya_transpose_b16 + "
-                                                  "pratchya_ns_combine per iteration"},
+                                       "kernels": "pratchya_transpose_b16 + pratchya_gemm_bf16_nt + "
+                                                  "pratchya_gemm_bf16_nt_ns (the 1.5X - 0.5B combination in "
+                                                  "the second product's epilogue) per iteration"},
             "steps": steps}
 
 

@@ -329,6 +329,17 @@ int pratchya_gemm_bs_nt_fq(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, 
 int pratchya_gemm_bf16_nt(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
                           int64_t K, void* C, int64_t ldc, int c_dtype, hipStream_t stream);
 
+/* One Newton-Schulz step on the bf16 MFMA kernel: C = 1.5 X - 0.5 bf16(A . B^T),
+ * the product of pratchya_gemm_bf16_nt (_optimizer.py:20-22, rounded once to
+ * bf16) combined with X in its epilogue exactly as pratchya_ns_combine
+ * (_optimizer.py:26-27: 1.5 x and 0.5 b each rounded to bf16, then their
+ * difference), so that B never goes through HBM.  A, B, M, N, K as
+ * pratchya_gemm_bf16_nt with a bf16 output; X: bf16 [M, N] (row stride ldx, a
+ * multiple of 8; 16-byte aligned); C: bf16 [M, N] (ldc), not overlapping X
+ * (PRATCHYA_EINVAL otherwise). */
+int pratchya_gemm_bf16_nt_ns(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
+                             int64_t K, const void* X, int64_t ldx, void* C, int64_t ldc, hipStream_t stream);
+
 /* f32 operands of pratchya_gemm_bf16_nt:    for the f32 products of the mixed
  * matmuls (Q:645-712, jnp.matmul of a dequantized array and an f32 array) and
  * of matmul_impl's backward (Q:618-622).  An f32 value v is the exact sum of

@@ -390,6 +390,10 @@ struct FqArgs {
   uint32_t* arrive;    // per strip: workgroups that published their maxima
   uint32_t* status;    // set to 1 if a strip's partners did not arrive in time
   int xcd;             // strip partners: workgroups b, b+8, b+16, b+24 (1) or b..b+3 (0)
+  // Newton-Schulz combination in the epilogue (FQ == 3): X [M, N] bf16 (row
+  // stride ldx elements), read where the tile's product is stored
+  const uint16_t* ns_x;
+  int64_t ldx;
 };
 
 // Output tile of workgroup-tile counter `bid` with output requantization: the
@@ -649,13 +653,80 @@ __device__ __forceinline__ void store_tile_fq(const v16f (&acc)[2][4], uint8_t* 
   }
 }
 
+// Epilogue of the bf16 product fused with the Newton-Schulz combination
+// X <- 1.5 X - 0.5 B (pratchya/_nnx_impl/_optimizer.py:26-27): the product B
+// is rounded to bf16 as the plain epilogue rounds it, staged through LDS like
+// store_tile's bf16 path, and each 16-byte chunk (8 values of one row) is
+// combined with the same chunk of X as k_ns_combine does it -- 1.5 x and 0.5 b
+// each rounded to bf16, their difference rounded to bf16 -- and stored to C
+// (which may be X itself when X is not an operand of the product: each chunk
+// is read before it is written, by the same lane).
+__device__ __forceinline__ uint32_t ns_combine2(uint32_t xw, uint32_t bw) {
+  const float x0 = u2f(xw << 16), x1 = u2f(xw & 0xFFFF0000u);
+  const float b0 = u2f(bw << 16), b1 = u2f(bw & 0xFFFF0000u);
+  const uint32_t xr = pack_bf16x2(1.5f * x0, 1.5f * x1);
+  const uint32_t br = pack_bf16x2(0.5f * b0, 0.5f * b1);
+  return pack_bf16x2(u2f(xr << 16) - u2f(br << 16), u2f(xr & 0xFFFF0000u) - u2f(br & 0xFFFF0000u));
+}
+
+__device__ __forceinline__ void store_tile_ns(const v16f (&acc)[2][4], uint8_t* stage, int wave, int lane,
+                                              void* C, int64_t ldc, const uint16_t* X, int64_t ldx, int row0,
+                                              int col0, int M, int N) {
+  const int l32 = lane & 31, lhi = lane >> 5;
+  constexpr int ROWB = 256;                 // 128 bf16 columns
+  constexpr int PITCH = ROWB + 16;
+  constexpr int CHUNKS = ROWB / 16;
+  constexpr int RP = 32;
+  uint8_t* stg = stage + wave * (RP * PITCH);
+  __syncthreads();                          // every wave is done with the stage buffer
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+    // this pass's chunks of X first (8 per lane), so that their latency
+    // overlaps the staging
+    v4i xv[(RP * CHUNKS) / 64];
+    const uint16_t* Xb = X + (int64_t)(row0 + mi * 32) * ldx + col0;
+#pragma unroll
+    for (int it = 0; it < (RP * CHUNKS) / 64; ++it) {
+      const int q = it * 64 + lane;
+      const int r = q / CHUNKS, c = q % CHUNKS;
+      xv[it] = v4i{0, 0, 0, 0};
+      if (row0 + mi * 32 + r < M && col0 + c * 8 < N)
+        xv[it] = *reinterpret_cast<const v4i*>(Xb + (int64_t)r * ldx + c * 8);
+    }
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int col = ni * 32 + 8 * j + 4 * lhi;
+        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+        const bf16x2 p0 = {(__bf16)acc[mi][ni][4 * j + 0], (__bf16)acc[mi][ni][4 * j + 1]};
+        const bf16x2 p1 = {(__bf16)acc[mi][ni][4 * j + 2], (__bf16)acc[mi][ni][4 * j + 3]};
+        *reinterpret_cast<uint2*>(stg + l32 * PITCH + col * 2) =
+            make_uint2(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1));
+      }
+    __builtin_amdgcn_s_waitcnt(0xC07F);     // lgkmcnt(0): this wave's staging writes are done
+    uint8_t* Cb = static_cast<uint8_t*>(C) + ((int64_t)(row0 + mi * 32) * ldc + col0) * 2;
+#pragma unroll
+    for (int it = 0; it < (RP * CHUNKS) / 64; ++it) {
+      const int q = it * 64 + lane;
+      const int r = q / CHUNKS, c = q % CHUNKS;
+      const v4i b = *reinterpret_cast<const v4i*>(stg + r * PITCH + c * 16);
+      const v4i o = {(int)ns_combine2((uint32_t)xv[it].x, (uint32_t)b.x), (int)ns_combine2((uint32_t)xv[it].y, (uint32_t)b.y),
+                     (int)ns_combine2((uint32_t)xv[it].z, (uint32_t)b.z), (int)ns_combine2((uint32_t)xv[it].w, (uint32_t)b.w)};
+      if (row0 + mi * 32 + r < M && col0 + c * 8 < N)
+        __builtin_nontemporal_store(o, reinterpret_cast<v4i*>(Cb + (int64_t)r * ldc * 2 + c * 16));
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);     // staging reads done before the next pass overwrites
+  }
+}
+
 template <bool OUT_BF16, int BG, int FQ, bool BF = false>
 __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     Scales sa, Scales sb, void* __restrict__ C, int64_t ldc, int K, int span, int tiles_m,
     int tiles_n, uint32_t a_bytes, uint32_t b_bytes, uint32_t ea_bytes, uint32_t eb_bytes,
     uint32_t ga_bytes, uint32_t gb_bytes, int M, int N, FqArgs fq) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + (FQ != 0 ? FQ_TABLE_BYTES : 0)];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + ((FQ == 1 || FQ == 2) ? FQ_TABLE_BYTES : 0)];
   const OperandRsrc ra = make_rsrc(A, a_bytes, sa, ea_bytes, ga_bytes);
   const OperandRsrc rb = make_rsrc(B, b_bytes, sb, eb_bytes, gb_bytes);
 
@@ -721,7 +792,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   int t = blockIdx.x;
   int tm, tn;
   auto next_tile = [&](int t_, int* tm_, int* tn_) {
-    if constexpr (FQ != 0) tile_of_fq(t_, tiles_m, tiles_n, fq.xcd != 0, tm_, tn_);
+    if constexpr (FQ == 1 || FQ == 2) tile_of_fq(t_, tiles_m, tiles_n, fq.xcd != 0, tm_, tn_);
     else tile_of(t_, tiles_m, tiles_n, tm_, tn_);
   };
   next_tile(t, &tm, &tn);
@@ -914,7 +985,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     // for LDS work only
     __builtin_amdgcn_s_waitcnt(0x0F70);      // vmcnt(0)
     asm volatile("" ::"v"(g_ld));
-    if constexpr (FQ != 0) {
+    if constexpr (FQ == 3) {
+      static_assert(BF && OUT_BF16, "the Newton-Schulz epilogue combines bf16 products");
+      store_tile_ns(acc, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc, fq.ns_x, fq.ldx,
+                    m0 + wm * 64, n0 + wn * 128, M, N);
+    } else if constexpr (FQ != 0) {
       static_assert(BG == 0, "output requantization takes B scale groups of 32 rows or more");
       uint8_t* table = lds + LDS_BYTES + wave * 64 * 16;
       fq_row_scales<FQ == 2>(acc, gA, gB, fq, table, tm * (tiles_n >> 2) + (tn >> 2), tn, wm, wn, lane,
@@ -1232,53 +1307,95 @@ extern "C" int pratchya_gemm_bs_nt_fq(const uint8_t* A, int64_t lda, const uint8
   return launch_status("gemm_fq");
 }
 
-extern "C" int pratchya_gemm_bf16_nt(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
-                                     int64_t K, void* C, int64_t ldc, int c_dtype, hipStream_t stream) {
+namespace {
+
+// Validated plan of a bf16 product C [M, N] = A [M, K] . B [N, K]^T (returns
+// a status; *empty when there is nothing to compute).
+int bf16_plan(const char* who, const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
+              int64_t K, const void* C, int64_t ldc, bool bf, GemmPlan* P, bool* empty) {
+  *empty = false;
   if (M <= 0 || N <= 0 || K <= 0) {
-    if (M < 0 || N < 0 || K < 0) return pratchya_set_error(PRATCHYA_EINVAL, "gemm_bf16: negative size");
+    if (M < 0 || N < 0 || K < 0) return pratchya_set_error(PRATCHYA_EINVAL, "%s: negative size", who);
+    *empty = true;
     return PRATCHYA_OK;
   }
   if (K % 64)
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_bf16: K must be a multiple of 64 (got %lld)", (long long)K);
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: K must be a multiple of 64 (got %lld)", who, (long long)K);
+  if (N < BN && N % (bf ? 8 : 4))
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: N below 256 must be a multiple of %d (got %lld)", who,
+                              bf ? 8 : 4, (long long)N);
+  if (!A || !B || !C) return pratchya_set_error(PRATCHYA_EINVAL, "%s: null buffer", who);
+  if (lda < K || ldb < K || ldc < N || lda % 8 || ldb % 8 || ldc % (bf ? 8 : 4) ||
+      (reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C)) % 16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "%s: leading dimensions / alignment not supported", who);
+  // the kernel addresses the operands as byte matrices: a 128-byte stage row
+  // holds 64 bf16 values of K
+  *P = GemmPlan{};
+  P->sa = Scales{nullptr, nullptr, 1, 0, 0, 1};
+  P->sb = P->sa;
+  P->span = 1;
+  P->bg = 0;
+  const int64_t Ma = M < BM ? BM : M, Na = N < BN ? BN : N;
+  P->a_bytes = ((Ma - 1) * lda + K) * 2;
+  P->b_bytes = ((Na - 1) * ldb + K) * 2;
+  if (P->a_bytes > (int64_t)INT32_MAX || P->b_bytes > (int64_t)INT32_MAX)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: operands beyond 2 GiB", who);
+  P->tiles_m = (M + BM - 1) / BM;
+  P->tiles_n = (N + BN - 1) / BN;
+  if (P->tiles_m * P->tiles_n > INT32_MAX)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: too many output tiles", who);
+  const int64_t tiles = P->tiles_m * P->tiles_n, cus = gemm_num_cus();
+  P->grid = tiles < cus ? tiles : cus;
+  return PRATCHYA_OK;
+}
+
+template <bool OB, int FQ>
+void bf16_launch(const GemmPlan& P, const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
+                 int64_t M, int64_t N, int64_t K, const FqArgs& fq, hipStream_t stream) {
+  hipLaunchKernelGGL((k_gemm_bs_nt<OB, 0, FQ, true>), dim3((unsigned)P.grid), dim3(NTHREADS), 0, stream,
+                     static_cast<const uint8_t*>(A), lda * 2, static_cast<const uint8_t*>(B), ldb * 2, P.sa, P.sb,
+                     C, ldc, (int)(K * 2), 1, (int)P.tiles_m, (int)P.tiles_n, (uint32_t)P.a_bytes,
+                     (uint32_t)P.b_bytes, 0u, 0u, 0u, 0u, (int)M, (int)N, fq);
+}
+
+}  // namespace
+
+extern "C" int pratchya_gemm_bf16_nt(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
+                                     int64_t K, void* C, int64_t ldc, int c_dtype, hipStream_t stream) {
   const bool bf = c_dtype == PRATCHYA_DT_BF16;
   if (c_dtype != PRATCHYA_DT_F32 && !bf)
     return pratchya_set_error(PRATCHYA_EINVAL, "gemm_bf16: unsupported output dtype %d", c_dtype);
-  if (N < BN && N % (bf ? 8 : 4))
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_bf16: N below 256 must be a multiple of %d (got %lld)",
-                              bf ? 8 : 4, (long long)N);
-  if (!A || !B || !C) return pratchya_set_error(PRATCHYA_EINVAL, "gemm_bf16: null buffer");
-  if (lda < K || ldb < K || ldc < N || lda % 8 || ldb % 8 || ldc % (bf ? 8 : 4) ||
-      (reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C)) % 16)
-    return pratchya_set_error(PRATCHYA_EINVAL, "gemm_bf16: leading dimensions / alignment not supported");
-  // the kernel addresses the operands as byte matrices: a 128-byte stage row
-  // holds 64 bf16 values of K
-  GemmPlan P{};
-  P.sa = Scales{nullptr, nullptr, 1, 0, 0, 1};
-  P.sb = P.sa;
-  P.span = 1;
-  P.bg = 0;
-  const int64_t Ma = M < BM ? BM : M, Na = N < BN ? BN : N;
-  P.a_bytes = ((Ma - 1) * lda + K) * 2;
-  P.b_bytes = ((Na - 1) * ldb + K) * 2;
-  if (P.a_bytes > (int64_t)INT32_MAX || P.b_bytes > (int64_t)INT32_MAX)
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_bf16: operands beyond 2 GiB");
-  P.tiles_m = (M + BM - 1) / BM;
-  P.tiles_n = (N + BN - 1) / BN;
-  if (P.tiles_m * P.tiles_n > INT32_MAX)
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_bf16: too many output tiles");
-  const int64_t tiles = P.tiles_m * P.tiles_n, cus = gemm_num_cus();
-  P.grid = tiles < cus ? tiles : cus;
+  GemmPlan P;
+  bool empty;
+  int rc = bf16_plan("gemm_bf16", A, lda, B, ldb, M, N, K, C, ldc, bf, &P, &empty);
+  if (rc || empty) return rc;
   const FqArgs none{};
-  const uint8_t* a8 = static_cast<const uint8_t*>(A);
-  const uint8_t* b8 = static_cast<const uint8_t*>(B);
-#define PRATCHYA_GEMM_BF16(OB)                                                                              \
-  hipLaunchKernelGGL((k_gemm_bs_nt<OB, 0, 0, true>), dim3((unsigned)P.grid), dim3(NTHREADS), 0, stream, a8, \
-                     lda * 2, b8, ldb * 2, P.sa, P.sb, C, ldc, (int)(K * 2), 1, (int)P.tiles_m, (int)P.tiles_n,    \
-                     (uint32_t)P.a_bytes, (uint32_t)P.b_bytes, 0u, 0u, 0u, 0u, (int)M, (int)N, none)
-  if (bf) PRATCHYA_GEMM_BF16(true);
-  else PRATCHYA_GEMM_BF16(false);
-#undef PRATCHYA_GEMM_BF16
+  if (bf) bf16_launch<true, 0>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
+  else bf16_launch<false, 0>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
   return launch_status("gemm_bf16");
+}
+
+extern "C" int pratchya_gemm_bf16_nt_ns(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
+                                        int64_t N, int64_t K, const void* X, int64_t ldx, void* C, int64_t ldc,
+                                        hipStream_t stream) {
+  GemmPlan P;
+  bool empty;
+  int rc = bf16_plan("gemm_bf16_ns", A, lda, B, ldb, M, N, K, C, ldc, true, &P, &empty);
+  if (rc || empty) return rc;
+  if (!X || ldx < N || ldx % 8 || reinterpret_cast<uintptr_t>(X) % 16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "gemm_bf16_ns: X must be a 16-byte aligned [M, N] bf16 matrix "
+                              "with a row stride that is a multiple of 8");
+  // C must not overlap X: an edge tile recomputes part of its neighbour, which
+  // would then combine an already combined value
+  const uintptr_t x0 = reinterpret_cast<uintptr_t>(X), x1 = x0 + (uintptr_t)(((M - 1) * ldx + N) * 2);
+  const uintptr_t c0 = reinterpret_cast<uintptr_t>(C), c1 = c0 + (uintptr_t)(((M - 1) * ldc + N) * 2);
+  if (c0 < x1 && x0 < c1)
+    return pratchya_set_error(PRATCHYA_EINVAL, "gemm_bf16_ns: the output overlaps X");
+  FqArgs fq{};
+  fq.ns_x = static_cast<const uint16_t*>(X);
+  fq.ldx = ldx;
+  bf16_launch<true, 3>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+  return launch_status("gemm_bf16_ns");
 }
 
 // --------------------------------------------------------------------------

@@ -69,13 +69,17 @@ def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
     # other dtypes and sizes use the BLAS library (f32 accumulation either way).
     on_kernel = X.dtype == torch.bfloat16 and m % 64 == 0 and n % 64 == 0
     for _ in range(steps):
+        # on the kernel, the second product's epilogue also forms
+        # 1.5 X - 0.5 B (the bits of ns_combine), into a new buffer
         if on_kernel and transpose:
             Xt = K.transpose_b16(X)                  # [n, m]
             A = K.gemm_bf16_nt(Xt, Xt)               # X^T X        [n, n]
-            B = K.gemm_bf16_nt(X, A)                 # X A (A = A^T) [m, n]
+            X = K.gemm_bf16_nt_ns(X, A, X)           # 1.5 X - 0.5 X A (A = A^T)
+            continue
         elif on_kernel:
             A = K.gemm_bf16_nt(X, X)                 # X X^T        [m, m]
-            B = K.gemm_bf16_nt(A, K.transpose_b16(X))   # A X       [m, n]
+            X = K.gemm_bf16_nt_ns(A, K.transpose_b16(X), X)   # 1.5 X - 0.5 A X
+            continue
         elif transpose:
             A = X.T @ X
             B = X @ A

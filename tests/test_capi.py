@@ -349,3 +349,20 @@ def test_mfma_ceiling_argument_codes_without_gpu():
     assert lib.pratchya_mfma_ceiling(p, p, 64, 0, 1, p, ctypes.byref(flop), None) == _lib.EINVAL
     assert lib.pratchya_mfma_ceiling(p, p, 128, 0, 0, p, ctypes.byref(flop), None) == _lib.EINVAL
     assert lib.pratchya_mfma_ceiling(p, p, 128, 1, 1, p, None, None) == _lib.EINVAL
+
+
+def test_gemm_bf16_ns_argument_codes_without_gpu():
+    """The fused Newton-Schulz GEMM rejects an output overlapping X, a bad X
+    and K not a multiple of 64 before any launch."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)
+    other = ctypes.c_void_p(1 << 30)
+    assert lib.pratchya_gemm_bf16_nt_ns(fake, 128, fake, 128, 256, 256, 128, other, 256, other, 256,
+                                        None) == _lib.EINVAL
+    assert b"overlaps" in lib.pratchya_last_error()
+    assert lib.pratchya_gemm_bf16_nt_ns(fake, 128, fake, 128, 256, 256, 128, None, 256, other, 256,
+                                        None) == _lib.EINVAL
+    assert lib.pratchya_gemm_bf16_nt_ns(fake, 96, fake, 96, 256, 256, 96, fake, 256, other, 256,
+                                        None) == _lib.EUNSUPPORTED
+    assert lib.pratchya_gemm_bf16_nt_ns(fake, 128, fake, 128, 0, 256, 128, fake, 256, other, 256, None) == 0

@@ -84,6 +84,29 @@ def test_transpose_b16(shape):
     assert torch.equal(got.view(torch.int16), x.t().contiguous().view(torch.int16))
 
 
+@pytest.mark.parametrize("shape", SHAPES + [(16384, 4096, 4096)], ids=lambda s: "x".join(map(str, s)))
+def test_gemm_bf16_ns_equals_product_then_combine(shape):
+    """pratchya_gemm_bf16_nt_ns: the product's epilogue forms 1.5 X - 0.5 B
+    with the same bits as pratchya_ns_combine applied to the bf16 product,
+    including edge tiles and short operands; run twice into the same output."""
+    M, N, Kd = shape
+    K = _K()
+    a, b, x = _bf16((M, Kd), 31, 0.05), _bf16((N, Kd), 32, 0.05), _bf16((M, N), 33)
+    want = K.ns_combine(x, K.gemm_bf16_nt(a, b))
+    out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    for _ in range(2):
+        got = K.gemm_bf16_nt_ns(a, b, x, out=out)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_gemm_bf16_ns_rejects_output_over_x():
+    K = _K()
+    a, b, x = _bf16((256, 128), 1), _bf16((256, 128), 2), _bf16((256, 256), 3)
+    with pytest.raises(ValueError, match="overlaps"):
+        K.gemm_bf16_nt_ns(a, b, x, out=x)
+
+
 @pytest.mark.parametrize("shape", [(1024, 2048), (2048, 1024)])
 def test_newton_schulz_kernel_against_oracle(shape):
     from pratchya_amd.optim import newton_schulz

@@ -936,10 +936,10 @@ def main():
             res = bench_config5()
         print(json.dumps({args.only: res}), flush=True)
         return
-    _log("config 2 quantize: start")
-    ms, wall, ok = bench_quantize(args.steps, args.warmup)
-    _log(f"config 2 quantize: {ms * 1e3:.2f} us/step, parity spot check {'ok' if ok else 'FAILED'}")
-    gbs = CFG2_BYTES / (ms * 1e-3) / 1e9
+    # The small secondary legs run first: a process's first GPU measurement
+    # runs several percent slow (measured: 19.4 vs 18.1 us per quantize for the
+    # same graph replay timed first and third), so the headline is timed after
+    # them, with its own W warmup steps and exactly K timed steps.
     extra = {}
     _log("config 1 round trip: start")
     extra["config1_round_trip"] = bench_config1(max(20, args.steps // 4), max(4, args.warmup // 4))
@@ -950,6 +950,10 @@ def main():
     _log("elementwise add: start")
     extra["elementwise_add"] = bench_elementwise(max(20, args.steps // 2), max(4, args.warmup // 4))
     _log(f"elementwise add: {extra['elementwise_add']['us']} us")
+    _log("config 2 quantize: start")
+    ms, wall, ok = bench_quantize(args.steps, args.warmup)
+    _log(f"config 2 quantize: {ms * 1e3:.2f} us/step, parity spot check {'ok' if ok else 'FAILED'}")
+    gbs = CFG2_BYTES / (ms * 1e-3) / 1e9
     if not args.no_gemm:
         _log("mfma ceiling: start")
         extra["mfma_ceiling"] = bench_mfma_ceiling()

@@ -439,3 +439,25 @@ def test_unsupported_shape_is_reported():
     b = K.operand_transposed(*wq, (128, 1))
     with pytest.raises(Exception, match="multiple of 8"):
         K.gemm_nt(a, K.Operand(b.payload[:20], b.sc8, b.sc32, b.desc), torch.bfloat16)
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["fp8", "bf16"])
+def test_mfma_ceiling_probe_runs(bf16):
+    """pratchya_mfma_ceiling (the bench's measurement aid) launches on real
+    operand bytes, completes, and reports the FLOP count of its MFMA sequence:
+    CUs (rounded down to a multiple of 8) x 8 waves x iters x 16 fragment pairs
+    x 131072 (fp8 32x32x64) or 65536 (two bf16 32x32x16) FLOP."""
+    K = _K()
+    g = torch.Generator(device="cuda").manual_seed(3)
+    a = torch.randint(0, 255, (256, 256), generator=g, device="cuda", dtype=torch.uint8)
+    b = torch.randint(0, 255, (256, 256), generator=g, device="cuda", dtype=torch.uint8)
+    if bf16:
+        a = torch.randn((256, 128), generator=g, device="cuda").to(torch.bfloat16)
+        b = torch.randn((256, 128), generator=g, device="cuda").to(torch.bfloat16)
+    else:
+        a[(a & 0x7F) == 0x7F] = 0           # no NaN bytes
+        b[(b & 0x7F) == 0x7F] = 0
+    flop = K.mfma_ceiling(a, b, bf16, 10)
+    torch.cuda.synchronize()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert flop == (cus - cus % 8) * 8 * 10 * 16 * (65536 if bf16 else 131072)

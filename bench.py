@@ -625,6 +625,13 @@ def bench_optimizer(steps: int):
                                           0.010009765625), 10)
     u = newton_schulz(c, 5)
     ns_ms = _event_ms(lambda: newton_schulz(c, 5), 3)
+    # the Gram product of one iteration alone: X^T X of the [16384, 4096]
+    # iterate (its transpose [4096, 16384] is the kernel's operand), on the
+    # symmetric kernel (upper-triangle tiles) and on the plain NT kernel
+    xt = K.transpose_b16(c)
+    gram_ms = _event_ms(lambda: K.gemm_bf16_gram(xt), 10)
+    gram_nt_ms = _event_ms(lambda: K.gemm_bf16_nt(xt, xt), 10)
+    gram_flop = 2 * din * dout * min(din, dout)
     upd_ms = _event_ms(lambda: K.apply_update(u, False, 128.0, sl(p_t), tg, bf, 0.05, 0.005, bf), 10)
     mom_bytes = n * (1 + 1 + 2 + 2)          # fp8 momentum + fp8 gradient in, bf16 c + bf16 new momentum out
     upd_bytes = n * (2 + 1 + 2)              # bf16 u + fp8 parameter in, bf16 update out
@@ -643,9 +650,18 @@ def bench_optimizer(steps: int):
             "ffn_down_newton_schulz": {"ms": round(ns_ms, 3), "TFLOP/s": round(ns_tf, 1),
                                        "frac_of_bf16_peak": round(ns_tf / BF16_PEAK_TFLOPS, 4),
                                        "flop": leaf_ns_flop,
-                                       "kernels": "pratchya_transpose_b16 + pratchya_gemm_bf16_nt + "
+                                       "kernels": "pratchya_transpose_b16 + pratchya_gemm_bf16_gram (the "
+                                                  "Gram product's 136 upper-triangle tiles of 256, mirrored) + "
                                                   "pratchya_gemm_bf16_nt_ns (the 1.5X - 0.5B combination in "
-                                                  "the second product's epilogue) per iteration"},
+                                                  "the second product's epilogue) per iteration; flop counts "
+                                                  "both products in full, as the reference computes them"},
+            "ffn_down_gram_product": {"us": round(gram_ms * 1e3, 1),
+                                      "frac_of_bf16_peak": round(gram_flop / (gram_ms * 1e-3) / 1e12
+                                                                 / BF16_PEAK_TFLOPS, 4),
+                                      "nt_kernel_us": round(gram_nt_ms * 1e3, 1),
+                                      "nt_frac_of_bf16_peak": round(gram_flop / (gram_nt_ms * 1e-3) / 1e12
+                                                                    / BF16_PEAK_TFLOPS, 4),
+                                      "flop": gram_flop},
             "steps": steps}
 
 

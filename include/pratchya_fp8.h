@@ -340,6 +340,25 @@ int pratchya_gemm_bf16_nt(const void* A, int64_t lda, const void* B, int64_t ldb
 int pratchya_gemm_bf16_nt_ns(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
                              int64_t K, const void* X, int64_t ldx, void* C, int64_t ldc, hipStream_t stream);
 
+/* Symmetric bf16 product C = A . A^T:     replaces the Gram product of newton_schulz
+ *   C[m, n] = sum_k A[m, k] * A[n, k]      (pratchya/_nnx_impl/_optimizer.py:20-22,
+ * A @ A.T of the wide iterate, and A.T @ A of a tall one with A its transpose)
+ * with f32 accumulation, rounded once to bf16.  Only the tiles on and above
+ * the diagonal are computed (stream-K: every CU takes an equal share of
+ * their K steps; a tile split between CUs is summed in f32 by the CU holding
+ * its first steps, in a fixed order, so results are deterministic), and the
+ * lower triangle is written as the transposed upper one (C == C^T exactly).
+ * A: bf16 [M, K] (lda, a multiple of 8; 16-byte aligned); M a multiple of 256
+ * and K of 64 (PRATCHYA_EUNSUPPORTED otherwise).  C: bf16 [M, M] (ldc), not
+ * overlapping A.  workspace: device memory of
+ * pratchya_gemm_bf16_gram_workspace_bytes(M, K) bytes (f32 partial tiles and
+ * flags, ~64 MB on a 256-CU device), 16-byte aligned; its last word is set to
+ * 1 if a partial tile did not arrive in time (that tile is then NaN).  Calls
+ * that share a workspace must not overlap. */
+int64_t pratchya_gemm_bf16_gram_workspace_bytes(int64_t M, int64_t K);
+int pratchya_gemm_bf16_gram(const void* A, int64_t lda, int64_t M, int64_t K, void* C, int64_t ldc,
+                            void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
 /* f32 operands of pratchya_gemm_bf16_nt:    for the f32 products of the mixed
  * matmuls (Q:645-712, jnp.matmul of a dequantized array and an f32 array) and
  * of matmul_impl's backward (Q:618-622).  An f32 value v is the exact sum of

@@ -682,6 +682,38 @@ def transpose_b16(x: torch.Tensor) -> torch.Tensor:
     return out
 
 
+_GRAM_WS = {}
+
+
+def gemm_bf16_gram(a: torch.Tensor) -> torch.Tensor:
+    """The symmetric bf16 product ``a @ a^T`` (f32 accumulation, rounded once
+    to bf16) of a bf16 ``a`` [M, K], the Gram product of newton_schulz
+    (pratchya/_nnx_impl/_optimizer.py:20-22): only the tiles on and above the
+    diagonal are computed and the lower triangle is their transpose, so the
+    result is exactly symmetric.  M must be a multiple of 256 and K of 64
+    (``PratchyaUnsupported`` otherwise).  The partial-tile workspace is kept
+    per device and stream; calls on one stream run in order."""
+    _require_gpu(a)
+    if a.dtype != torch.bfloat16 or a.dim() != 2:
+        raise ValueError("gemm_bf16_gram: a must be 2-D bfloat16")
+    M, Kd = int(a.shape[0]), int(a.shape[1])
+    lib = _lib.load()
+    ws_bytes = int(lib.pratchya_gemm_bf16_gram_workspace_bytes(M, Kd))
+    if ws_bytes <= 0:
+        raise PratchyaUnsupported(f"gemm_bf16_gram: M must be a multiple of 256 and K of 64 (got {M}, {Kd})")
+    ap = a.contiguous()
+    stream = torch.cuda.current_stream(ap.device)
+    key = (ap.device.index, stream.cuda_stream)
+    ws = _GRAM_WS.get(key)
+    if ws is None or ws.numel() < ws_bytes:
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=ap.device)
+        _GRAM_WS[key] = ws
+    out = torch.empty((M, M), dtype=torch.bfloat16, device=ap.device)
+    _lib.check(lib.pratchya_gemm_bf16_gram(_ptr(ap), Kd, M, Kd, _ptr(out), M, _ptr(ws), int(ws.numel()),
+                                           _stream(ap)), "gemm_bf16_gram")
+    return out
+
+
 def gemm_bf16_nt_ns(a: torch.Tensor, b: torch.Tensor, x: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
     """One Newton-Schulz step ``1.5 x - 0.5 (a @ b^T)`` (pratchya/_nnx_impl/
     _optimizer.py:20-27) with the combination in the bf16 GEMM's epilogue: the

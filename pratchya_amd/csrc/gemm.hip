@@ -204,6 +204,7 @@ struct DmaHalf {
 // row index) and the e8m0 block index of the lane's row at kb = 0.
 struct DmaRows {
   uint32_t row0, e_word;
+  int kb;                      // K block of the unit's first step (a Gram segment; else 0)
 };
 
 // Row group i (8 rows) of a stage load whose row group 0 starts at byte
@@ -394,7 +395,165 @@ struct FqArgs {
   // stride ldx elements), read where the tile's product is stored
   const uint16_t* ns_x;
   int64_t ldx;
+  // Symmetric product C = A A^T (FQ == 4, pratchya_gemm_bf16_gram): only the
+  // tri * (tri + 1) / 2 tiles (i, j), i <= j, of the tile grid are computed.
+  // Their K steps (steps per tile) form one sequence of iters = tiles * steps
+  // steps, numbered tile by tile; workgroup r takes the contiguous range
+  // [r * iters / G, (r + 1) * iters / G) ("stream-K"), so every workgroup does
+  // the same work.  A tile split between ranges is finished by the range that
+  // holds its first step (its "head", the last unit of that range): the later
+  // ranges that hold the rest of its steps reach them first, store the f32
+  // accumulators of each wave in part (slot = range), and raise flags[range *
+  // 8 + wave]; the head adds those partials in range order and stores the
+  // tile.  A flag not raised in time sets the status word and makes the
+  // tile's sums NaN.
+  float* part;
+  uint32_t* flags;
+  int64_t iters;
+  int steps;
+  int tri;
+  int order16;          // tiles in kGramOrder16's order (tri 16, 256 ranges, steps % 32 == 0)
 };
+
+// Tile order of the 16 x 16 tile grid (M = 4096) on 256 ranges with a
+// multiple of 32 steps per tile: range r starts at step 17 r S / 32, so the
+// ranges r = m + 32 n (n = 0..7), which run on one XCD, are at the same K
+// step at all times, on tiles q0 + 17 n.  The order makes each such set
+// {a + 17 n} a block of tiles over at most 6 panels (mostly 2 x 4 tiles;
+// one set of 8 diagonal-adjacent tiles), so the 8 workgroups read the same
+// K slices of few panels and share them in their XCD's L2.  Entry q is
+// 16 i + j of tile (i, j).
+__constant__ uint8_t kGramOrder16[136] = {
+    2, 6, 10, 36, 40, 44, 70, 74, 104, 108, 138, 172, 0, 68, 136, 204, 35,
+    3, 7, 11, 37, 41, 45, 71, 75, 105, 109, 139, 173, 1, 69, 137, 205, 51,
+    4, 8, 12, 38, 42, 46, 72, 76, 106, 110, 140, 174, 17, 85, 153, 221, 103,
+    5, 9, 13, 39, 43, 47, 73, 77, 107, 111, 141, 175, 14, 78, 142, 206, 119,
+    18, 22, 26, 52, 56, 60, 86, 90, 120, 124, 154, 188, 15, 79, 143, 207, 171,
+    19, 23, 27, 53, 57, 61, 87, 91, 121, 125, 155, 189, 30, 94, 158, 222, 187,
+    20, 24, 28, 54, 58, 62, 88, 92, 122, 126, 156, 190, 31, 95, 159, 223, 239,
+    21, 25, 29, 55, 59, 63, 89, 93, 123, 127, 157, 191, 34, 102, 170, 238, 255,
+};
+
+// Upper-triangle tile q of a tri x tri tile grid: by kGramOrder16 (order16),
+// else numbered row by row.
+__device__ __forceinline__ void tri_of(int q, int tri, bool order16, int* ti, int* tj) {
+  if (order16) {
+    const int v = kGramOrder16[q];
+    *ti = v >> 4;
+    *tj = v & 15;
+    return;
+  }
+  int i = 0, base = 0;
+  while (q >= base + (tri - i)) {
+    base += tri - i;
+    ++i;
+  }
+  *ti = i;
+  *tj = i + (q - base);
+}
+
+// Gram partials: wave `wave` of range r holds its 128 accumulators per lane
+// in 32 float4 columns of 64 lanes (1 KB each, coalesced).
+//
+// The exchange crosses XCDs, whose L2 caches are not coherent with each
+// other.  Every partial store and load is issued at device scope (the sc1
+// cache policy, which is also how device-scope atomic loads and stores are
+// issued): a store is written through to the device's coherence point and is
+// counted complete (vmcnt) only once performed there, and a load is served
+// from that point, never from a stale line of this XCD's L2.  So the writer
+// waits for its stores to complete and then raises the flag (an atomic), and
+// a reader that has seen the flag reads the partial directly -- without the
+// device-scope release and acquire fences, which write back and invalidate
+// the whole L2 (measured: 18% of the kernel's time).
+constexpr int kSc1 = 16;           // cache policy bit sc1 of buffer loads and stores
+
+__device__ __forceinline__ float* gram_slot(const FqArgs& fq, int r, int wave) {
+  return fq.part + ((int64_t)r * 8 + wave) * (32 * 256);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gram_rsrc(const FqArgs& fq, int r, int wave) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)gram_slot(fq, r, wave), 0, 32 * 1024, 0x00020000);
+}
+
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void gram_put_partial(const v16f (&acc)[2][4], const FqArgs& fq, int r, int wave,
+                                                 int lane) {
+  const __amdgpu_buffer_rsrc_t rs = gram_rsrc(fq, r, wave);
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4) {
+        // (a whole-vector cast: hipcc miscompiles __builtin_bit_cast of a
+        // vector element lvalue into a cast of element 0)
+        const v4u d = __builtin_bit_cast(
+            v4u, v4f{acc[mi][ni][4 * v4], acc[mi][ni][4 * v4 + 1], acc[mi][ni][4 * v4 + 2], acc[mi][ni][4 * v4 + 3]});
+        __builtin_amdgcn_raw_buffer_store_b128(d, rs, (((mi * 4 + ni) * 4 + v4) * 256 + lane * 4) * 4, 0, kSc1);
+      }
+  // vmcnt(0): the partial is performed at device scope before the flag (the
+  // memory clobbers keep the compiler from moving either across the wait)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  asm volatile("" ::: "memory");
+  if (lane == 0) __hip_atomic_fetch_add(fq.flags + r * 8 + wave, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The head of tile q (range r of G) adds the partials of the later ranges
+// that hold steps of q, in range order.
+__device__ __forceinline__ void gram_add_partials(v16f (&acc)[2][4], const FqArgs& fq, int r, int G, int q,
+                                                  int wave, int lane) {
+  const int64_t tile_end = (int64_t)(q + 1) * fq.steps;
+  for (int r2 = r + 1; r2 < G && (int64_t)r2 * fq.iters / G < tile_end; ++r2) {
+    uint32_t ok = 1;
+    if (lane == 0) {
+      uint32_t* f = fq.flags + r2 * 8 + wave;
+      // the later ranges are resident (one workgroup per CU, grid <= CUs) and
+      // reach this tile's steps first; the bound only keeps a broken launch
+      // from spinning forever.  The flag is read with a returning atomic, as
+      // it was raised with one (both performed where atomics on it are
+      // serialized).
+      for (int it = 0; __hip_atomic_fetch_add(f, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u; ++it) {
+        if (it >= (1 << 20)) {
+          __hip_atomic_fetch_or(fq.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ok = 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    if (!__builtin_amdgcn_readfirstlane(ok)) {
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[mi][ni][v] = __builtin_nanf("");
+      continue;
+    }
+    asm volatile("" ::: "memory");         // the partial's loads stay after the flag was seen
+    const __amdgpu_buffer_rsrc_t rs = gram_rsrc(fq, r2, wave);
+    // one 16-value accumulator block at a time (the memory clobber keeps the
+    // next block's loads after this block's adds: the accumulators leave no
+    // room for more loaded values)
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) {
+        v4f p[4];
+#pragma unroll
+        for (int v4 = 0; v4 < 4; ++v4)
+          p[v4] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rs, (((mi * 4 + ni) * 4 + v4) * 256 + lane * 4) * 4, 0, kSc1));
+#pragma unroll
+        for (int v4 = 0; v4 < 4; ++v4)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[mi][ni][4 * v4 + e] += p[v4][e];
+        asm volatile("" ::: "memory");
+      }
+  }
+}
 
 // Output tile of workgroup-tile counter `bid` with output requantization: the
 // four tiles of a strip get consecutive numbers L (L % 4 = tile in the strip),
@@ -735,7 +894,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // waves w, w+4 share SIMD w
   const int grp = wave >> 2;              // ping-pong group
   const int wm = wave & 3, wn = grp;      // 64-row band wm, 128-column half wn
-  const int nk = K / BK;
+  int nk = K / BK;                        // K steps of the current unit
   const int T = tiles_m * tiles_n;
   const int l32 = lane & 31, lhi = lane >> 5;
 
@@ -765,12 +924,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
       h.pub = (BG == 2 ? e4 * 4 + (q & 3) : e4) * 4;
     }
   }
-  auto rows_of = [&](int tm_, int tn_) {
+  auto rows_of = [&](int tm_, int tn_, int kb_) {
     DmaRows r;
     r.row0 = (uint32_t)((grp == 0 ? tile_base(tm_, M) : tile_base(tn_, N)) + w4 * 64);
     r.e_word = (uint32_t)blk_index(so, (int64_t)r.row0 + lane, 0);
+    r.kb = kb_;
     return r;
   };
+  // K block of a unit's first step: 0 except for the segments of a Gram range
+  auto kb_of = [&](const DmaRows& r) { return FQ == 4 ? r.kb : 0; };
   const uint32_t skA = (uint32_t)sa.s_k, skB = (uint32_t)sb.s_k;
   // physical 16-byte chunk offsets of this lane's operand halves: K half ks,
   // lo/hi chunk (logical 4*ks + 2*lhi + h, XOR-swizzled by the lane's row)
@@ -789,22 +951,43 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   // the next tile's first stage is loaded during the current tile's last K
   // steps into the stage buffer they no longer read, and its latency is
   // covered by the epilogue, which stages the output in the other buffer.
+  //
+  // Gram (FQ == 4): the units are the segments of this workgroup's range of
+  // the stream-K step sequence (see FqArgs): a unit is the part of one tile's
+  // K steps inside the range, at most two per range.
   int t = blockIdx.x;
-  int tm, tn;
+  int tm, tn, kb = 0;
+  int64_t g = 0, g_end = 0;               // Gram: the range's next and end steps
   auto next_tile = [&](int t_, int* tm_, int* tn_) {
     if constexpr (FQ == 1 || FQ == 2) tile_of_fq(t_, tiles_m, tiles_n, fq.xcd != 0, tm_, tn_);
     else tile_of(t_, tiles_m, tiles_n, tm_, tn_);
   };
-  next_tile(t, &tm, &tn);
-  DmaRows cur = rows_of(tm, tn);
-  int par = 0;                            // stage buffer of the tile's K block 0
+  // Gram unit starting at step g_: tile q_, its K blocks [kb_, kb_ + nk_)
+  auto gram_unit = [&](int64_t g_, int* q_, int* tm_, int* tn_, int* kb_, int* nk_) {
+    const int64_t qq = g_ / fq.steps;
+    const int k0 = (int)(g_ - qq * fq.steps);
+    const int64_t left = g_end - g_;
+    *nk_ = (int)((int64_t)(fq.steps - k0) < left ? (int64_t)(fq.steps - k0) : left);
+    *kb_ = k0;
+    *q_ = (int)qq;
+    tri_of((int)qq, fq.tri, fq.order16 != 0, tm_, tn_);
+  };
+  if constexpr (FQ == 4) {
+    g = (int64_t)blockIdx.x * fq.iters / gridDim.x;
+    g_end = ((int64_t)blockIdx.x + 1) * fq.iters / gridDim.x;
+    gram_unit(g, &t, &tm, &tn, &kb, &nk);
+  } else {
+    next_tile(t, &tm, &tn);
+  }
+  DmaRows cur = rows_of(tm, tn, kb);
+  int par = 0;                            // stage buffer of the unit's first K block
 
   // prologue: both halves of stage 0; group 1 then starts its half of stage 1
   // (it is one stage ahead of group 0 throughout).  The wave's last stage
   // DMA, not yet published: g_pub (a span start), its group max g_ld, its
   // buffer g_st, g_first (a tile's K block 0).
 #pragma unroll
-  for (int i = 0; i < 8; ++i) dma_rows(h, cur, lds, 0, i);
+  for (int i = 0; i < 8; ++i) dma_rows(h, cur, lds, kb_of(cur), i);
   float g_ld = 0.0f, u_prev = 1.0f;
   if constexpr (!BF) {
     dma_scales(h, cur, lds, 0);
@@ -818,19 +1001,22 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
 
   for (;;) {
     const int m0 = tile_base(tm, M), n0 = tile_base(tn, N);
-    const int t_next = t + (int)gridDim.x;
-    const bool has_next = t_next < T;
+    int t_next = t + (int)gridDim.x, kb2 = 0, nk2 = nk;
+    bool has_next;
+    if constexpr (FQ == 4) has_next = g + nk < g_end;
+    else has_next = t_next < T;
     int tm2 = 0, tn2 = 0;
     DmaRows nxt = cur;
     if (has_next) {
-      next_tile(t_next, &tm2, &tn2);
-      nxt = rows_of(tm2, tn2);
+      if constexpr (FQ == 4) gram_unit(g + nk, &t_next, &tm2, &tn2, &kb2, &nk2);
+      else next_tile(t_next, &tm2, &tn2);
+      nxt = rows_of(tm2, tn2, kb2);
     }
     if (grp == 1) {
       if (1 < nk) {
         uint8_t* s1 = lds + ((1 + par) & 1) * STAGE_BYTES;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) dma_rows(h, cur, s1, 1, i);
+        for (int i = 0; i < 8; ++i) dma_rows(h, cur, s1, 1 + kb_of(cur), i);
         if constexpr (!BF) {
           dma_scales(h, cur, s1, 1);
           g_pub = span == 1;
@@ -931,7 +1117,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
         const DmaRows& dr = to_next ? nxt : cur;
         const int lkt = to_next ? 0 : dkt;            // K block inside the tile loaded
         uint8_t* dst = lds + ((dkt + par) & 1) * STAGE_BYTES;
-        const uint32_t soff0 = dr.row0 * h.ld + (uint32_t)lkt * BK;
+        const uint32_t soff0 = dr.row0 * h.ld + (uint32_t)(lkt + kb_of(dr)) * BK;
         uint8_t* const lds0 = dst + h.lds_pay;
         pin_frags(fa, fb);
         mfma_pinned<0, 0, BF>(acc, fa, fb, eA, eB);
@@ -985,11 +1171,21 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     // for LDS work only
     __builtin_amdgcn_s_waitcnt(0x0F70);      // vmcnt(0)
     asm volatile("" ::"v"(g_ld));
-    if constexpr (FQ == 3) {
+    if constexpr (FQ == 4) {
+      static_assert(BF && OUT_BF16, "the Gram product is a bf16 product");
+      if (kb != 0) {
+        // the rest of a tile whose head is an earlier range's
+        gram_put_partial(acc, fq, (int)blockIdx.x, wave, lane);
+      } else {
+        gram_add_partials(acc, fq, (int)blockIdx.x, (int)gridDim.x, t, wave, lane);
+        store_tile<true, 0>(acc, gA, gB, nullptr, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc,
+                            m0 + wm * 64, n0 + wn * 128, M, N);
+      }
+    } else if constexpr (FQ == 3) {
       static_assert(BF && OUT_BF16, "the Newton-Schulz epilogue combines bf16 products");
       store_tile_ns(acc, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc, fq.ns_x, fq.ldx,
                     m0 + wm * 64, n0 + wn * 128, M, N);
-    } else if constexpr (FQ != 0) {
+    } else if constexpr (FQ == 1 || FQ == 2) {
       static_assert(BG == 0, "output requantization takes B scale groups of 32 rows or more");
       uint8_t* table = lds + LDS_BYTES + wave * 64 * 16;
       fq_row_scales<FQ == 2>(acc, gA, gB, fq, table, tm * (tiles_n >> 2) + (tn >> 2), tn, wm, wn, lane,
@@ -1006,6 +1202,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     tn = tn2;
     cur = nxt;
     par = (par + nk) & 1;
+    if constexpr (FQ == 4) {
+      g += nk;
+      kb = kb2;
+      nk = nk2;
+    }
     // every wave is done with the staging buffer (its LDS reads); the next
     // tile's stage 0 landed before the epilogue, and the output stores are not
     // waited for: they drain while the next tile starts
@@ -1396,6 +1597,111 @@ extern "C" int pratchya_gemm_bf16_nt_ns(const void* A, int64_t lda, const void* 
   fq.ldx = ldx;
   bf16_launch<true, 3>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
   return launch_status("gemm_bf16_ns");
+}
+
+// --------------------------------------------------------------------------
+// Symmetric product C = A A^T (the Gram matrix of Newton-Schulz's first
+// product): the kernel computes the upper-triangle tiles by stream-K (see
+// FqArgs), then k_mirror_lower_b16 copies the transposed upper triangle into
+// the lower one, so C is exactly symmetric.
+// --------------------------------------------------------------------------
+namespace {
+
+// C[r][c] = C[c][r] for r > c, by 64 x 64 blocks (bi, bj), bi >= bj, of the
+// lower triangle numbered row by row: block (bj, bi) is read through LDS and
+// written transposed to (bi, bj) (on the diagonal only below it).
+__global__ __launch_bounds__(256) void k_mirror_lower_b16(uint16_t* __restrict__ C, int64_t ldc) {
+  __shared__ uint16_t tile[64][64 + 2];
+  int q = (int)blockIdx.x, bi = 0;
+  while (q > bi) {
+    q -= bi + 1;
+    ++bi;
+  }
+  const int bj = q;
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int c = it * 256 + (int)threadIdx.x, r = c >> 3, ch = c & 7;
+    const v4i v = *reinterpret_cast<const v4i*>(C + (int64_t)(bj * 64 + r) * ldc + bi * 64 + ch * 8);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      tile[r][ch * 8 + 2 * e] = (uint16_t)((uint32_t)v[e] & 0xFFFFu);
+      tile[r][ch * 8 + 2 * e + 1] = (uint16_t)((uint32_t)v[e] >> 16);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int c = it * 256 + (int)threadIdx.x, r = c >> 3, ch = c & 7;
+    v4i o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c0 = ch * 8 + 2 * e;
+      // on the diagonal block, elements on or above the diagonal stay
+      const uint32_t lo = (bi > bj || r > c0) ? tile[c0][r] : tile[r][c0];
+      const uint32_t hi = (bi > bj || r > c0 + 1) ? tile[c0 + 1][r] : tile[r][c0 + 1];
+      o[e] = (int)(lo | (hi << 16));
+    }
+    *reinterpret_cast<v4i*>(C + (int64_t)(bi * 64 + r) * ldc + bj * 64 + ch * 8) = o;
+  }
+}
+
+// Workgroups of the Gram product: one range per CU, at most two per tile
+// (each range then holds at least half a tile's steps, so a tile has at most
+// three contributors) and at most one per step.
+int64_t gram_grid(int64_t M, int64_t K) {
+  const int64_t tri = M / BM, tiles = tri * (tri + 1) / 2, iters = tiles * (K / 64);
+  int64_t g = gemm_num_cus();
+  if (g > 2 * tiles) g = 2 * tiles;
+  if (g > iters) g = iters;
+  return g;
+}
+
+}  // namespace
+
+extern "C" int64_t pratchya_gemm_bf16_gram_workspace_bytes(int64_t M, int64_t K) {
+  if (M <= 0 || K <= 0 || M % BM || K % 64) return 0;
+  const int64_t G = gram_grid(M, K);
+  return G * 8 * (32 * 256) * 4 + (G * 8 + 1) * 4;
+}
+
+extern "C" int pratchya_gemm_bf16_gram(const void* A, int64_t lda, int64_t M, int64_t K, void* C, int64_t ldc,
+                                       void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  GemmPlan P;
+  bool empty;
+  int rc = bf16_plan("gemm_bf16_gram", A, lda, A, lda, M, M, K, C, ldc, true, &P, &empty);
+  if (rc || empty) return rc;
+  if (M % BM)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_bf16_gram: M must be a multiple of 256 (got %lld)",
+                              (long long)M);
+  const int64_t need = pratchya_gemm_bf16_gram_workspace_bytes(M, K);
+  if (!workspace || workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "gemm_bf16_gram: workspace of %lld bytes (need %lld, 16-byte aligned)",
+                              (long long)workspace_bytes, (long long)need);
+  const int64_t tri = M / BM, tiles = tri * (tri + 1) / 2, G = gram_grid(M, K);
+  if (tiles * (K / 64) > INT32_MAX)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_bf16_gram: too many K steps");
+  FqArgs fq{};
+  fq.part = static_cast<float*>(workspace);
+  fq.flags = reinterpret_cast<uint32_t*>(fq.part + G * 8 * (32 * 256));
+  fq.status = fq.flags + G * 8;
+  fq.iters = tiles * (K / 64);
+  fq.steps = (int)(K / 64);
+  fq.tri = (int)tri;
+  fq.order16 = tri == 16 && G == 256 && fq.steps % 32 == 0 ? 1 : 0;
+  // flags and status start at zero (a kernel, not a memset: safe under graph
+  // capture)
+  const int64_t words = G * 8 + 1;
+  hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream, fq.flags, words, 0u);
+  rc = launch_status("gemm_bf16_gram");
+  if (rc) return rc;
+  P.grid = G;
+  bf16_launch<true, 4>(P, A, lda, A, lda, C, ldc, M, M, K, fq, stream);
+  rc = launch_status("gemm_bf16_gram");
+  if (rc) return rc;
+  const int64_t nb = M / 64;
+  hipLaunchKernelGGL(k_mirror_lower_b16, dim3((unsigned)(nb * (nb + 1) / 2)), dim3(256), 0, stream,
+                     static_cast<uint16_t*>(C), ldc);
+  return launch_status("gemm_bf16_gram");
 }
 
 // --------------------------------------------------------------------------

@@ -52,8 +52,9 @@ def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
     """Orthogonalization by the cubic Newton-Schulz iteration
     (``_optimizer.py:11-29``): ``X = G / (||G||_F + 1e-7)`` (the transpose of a
     tall ``G``), then ``steps`` times ``X = 1.5 X - 0.5 (X X^T) X``, in ``G``'s
-    dtype.  bf16 products run on the bf16 MFMA kernel (``pratchya_gemm_bf16_nt``),
-    others on the BLAS library (f32 accumulation)."""
+    dtype.  bf16 products run on the bf16 MFMA kernel (``pratchya_gemm_bf16_nt``;
+    the Gram product on ``pratchya_gemm_bf16_gram`` where its side is a
+    multiple of 256), others on the BLAS library (f32 accumulation)."""
     m, n = G.shape
     transpose = m > n
     # A tall G is iterated untransposed: with Y = X^T = G / (||G|| + eps),
@@ -68,16 +69,20 @@ def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
     # both operands K-contiguous), with one transposing copy per iteration;
     # other dtypes and sizes use the BLAS library (f32 accumulation either way).
     on_kernel = X.dtype == torch.bfloat16 and m % 64 == 0 and n % 64 == 0
+    # the Gram product computes only its upper-triangle tiles (exactly
+    # symmetric result) where its side is a multiple of 256
+    gram_side = n if transpose else m
+    gram = K.gemm_bf16_gram if gram_side % 256 == 0 else (lambda a: K.gemm_bf16_nt(a, a))
     for _ in range(steps):
         # on the kernel, the second product's epilogue also forms
         # 1.5 X - 0.5 B (the bits of ns_combine), into a new buffer
         if on_kernel and transpose:
             Xt = K.transpose_b16(X)                  # [n, m]
-            A = K.gemm_bf16_nt(Xt, Xt)               # X^T X        [n, n]
+            A = gram(Xt)                             # X^T X        [n, n]
             X = K.gemm_bf16_nt_ns(X, A, X)           # 1.5 X - 0.5 X A (A = A^T)
             continue
         elif on_kernel:
-            A = K.gemm_bf16_nt(X, X)                 # X X^T        [m, m]
+            A = gram(X)                              # X X^T        [m, m]
             X = K.gemm_bf16_nt_ns(A, K.transpose_b16(X), X)   # 1.5 X - 0.5 A X
             continue
         elif transpose:

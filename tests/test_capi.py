@@ -351,6 +351,29 @@ def test_mfma_ceiling_argument_codes_without_gpu():
     assert lib.pratchya_mfma_ceiling(p, p, 128, 1, 1, p, None, None) == _lib.EINVAL
 
 
+def test_gemm_bf16_gram_argument_codes_without_gpu():
+    """The symmetric product sizes its workspace from M, K and the device's CUs
+    (256 without a device), and rejects M not a multiple of 256, K not a
+    multiple of 64 and a short workspace before any launch."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)
+    other = ctypes.c_void_p(1 << 30)
+    ws = lib.pratchya_gemm_bf16_gram_workspace_bytes(4096, 16384)
+    # 256 ranges, 8 waves of 32 KB of partials each, then 2048 flags and a status word
+    assert ws == 256 * 8 * 32768 + (256 * 8 + 1) * 4
+    # one tile of one 64-wide step: a single range
+    assert lib.pratchya_gemm_bf16_gram_workspace_bytes(256, 64) == 8 * 32768 + 9 * 4
+    assert lib.pratchya_gemm_bf16_gram_workspace_bytes(300, 64) == 0
+    assert lib.pratchya_gemm_bf16_gram_workspace_bytes(256, 96) == 0
+    assert lib.pratchya_gemm_bf16_gram(fake, 128, 304, 128, other, 304, other, 1 << 30, None) == _lib.EUNSUPPORTED
+    assert lib.pratchya_gemm_bf16_gram(fake, 96, 256, 96, other, 256, other, 1 << 30, None) == _lib.EUNSUPPORTED
+    assert lib.pratchya_gemm_bf16_gram(fake, 128, 256, 128, other, 256, other, 16, None) == _lib.EINVAL
+    assert b"workspace" in lib.pratchya_last_error()
+    assert lib.pratchya_gemm_bf16_gram(fake, 128, 256, 128, other, 256, None, 1 << 30, None) == _lib.EINVAL
+    assert lib.pratchya_gemm_bf16_gram(fake, 128, 0, 128, other, 256, None, 0, None) == 0
+
+
 def test_gemm_bf16_ns_argument_codes_without_gpu():
     """The fused Newton-Schulz GEMM rejects an output overlapping X, a bad X
     and K not a multiple of 64 before any launch."""

@@ -1,0 +1,108 @@
+"""GPU parity of the symmetric bf16 product behind newton_schulz's Gram
+product (pratchya/_nnx_impl/_optimizer.py:20-22: ``A = X @ X.T`` in bf16
+with f32 accumulation), pratchya_gemm_bf16_gram.
+
+* Small integers: every product and partial sum is exact in f32 whatever the
+  split of K between workgroups, so the result is bit for bit the integer
+  Gram matrix rounded once to bf16 (tile numbering, the K ranges of the
+  stream-K split, the partial sums and the mirrored lower triangle).
+* Normal inputs: within one bf16 rounding of the float64 product (relative
+  Frobenius error <= 4e-3, the bf16 output's rounding) and within one bf16
+  ulp (plus 2^-20 for values that cancel to near zero) of
+  pratchya_gemm_bf16_nt's result on every element (the two differ only in how
+  K is split before the f32 sums are added); exactly symmetric;
+  identical bits on a repeated call (the partials are added in a fixed order).
+* Shapes cover one tile (a single range), tiles split between two or three
+  ranges, K of a single step (no split), and newton_schulz's [4096, 16384].
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import qarr_oracle as O
+from tests.helpers import f32
+
+pytestmark = pytest.mark.gpu
+
+
+def _K():
+    from pratchya_amd import _kernels
+    return _kernels
+
+
+def _bf16(shape, seed, scale=1.0):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    return (torch.randn(shape, generator=g, device="cuda") * scale).to(torch.bfloat16)
+
+
+# (M, K): one tile; K of one 64-wide step (every range one whole tile);
+# three tiles per side with 3 steps each (ranges of 1-2 steps); 10 tiles with
+# 32 steps on 20 ranges; the Newton-Schulz shapes
+SHAPES = [(256, 512), (768, 64), (768, 192), (1024, 2048), (2048, 1024), (4096, 4096), (4096, 16384)]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_gram_exact_integers(shape):
+    M, Kd = shape
+    print(f"gram exact integers M={M} K={Kd}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(M + Kd)
+    a = torch.randint(-4, 5, (M, Kd), generator=g, device="cuda").to(torch.bfloat16)
+    c = _K().gemm_bf16_gram(a)
+    ad = a.double()
+    ref = (ad @ ad.T).to(torch.bfloat16)        # exact integers, rounded once (RNE)
+    torch.cuda.synchronize()
+    assert torch.equal(c.view(torch.int16), ref.view(torch.int16)), \
+        f"{(c != ref).sum().item()} elements differ"
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_gram_normal_against_f64_and_nt(shape):
+    M, Kd = shape
+    print(f"gram normal M={M} K={Kd}", flush=True)
+    K = _K()
+    a = _bf16((M, Kd), 7, 1.0 / np.sqrt(Kd))
+    c = K.gemm_bf16_gram(a)
+    c2 = K.gemm_bf16_gram(a)
+    nt = K.gemm_bf16_nt(a, a, torch.bfloat16)
+    ad = a.double()
+    ref = (ad @ ad.T).cpu().numpy()
+    torch.cuda.synchronize()
+    assert torch.equal(c.view(torch.int16), c2.view(torch.int16)), "repeated calls differ"
+    assert torch.equal(c.view(torch.int16), c.T.contiguous().view(torch.int16)), "not exactly symmetric"
+    got = f32(c).astype(np.float64)
+    assert O.rel_fro(got, ref) <= 4e-3
+    # against the NT kernel's upper triangle: one bf16 ulp of the larger
+    # magnitude, plus the f32 sums' own rounding where a value cancels to
+    # near zero (|sum| of the products of a row pair is about 1 here, so
+    # differently split f32 sums differ by a few 2^-24)
+    other = f32(nt).astype(np.float64)
+    iu = np.triu_indices(M)
+    d = np.abs(got[iu] - other[iu])
+    tol = np.maximum(np.abs(got[iu]), np.abs(other[iu])) * 2.0 ** -7 + 2.0 ** -20
+    assert np.all(d <= tol), f"max excess {np.max(d - tol)}"
+
+
+def test_gram_rejects_bad_shapes():
+    from pratchya_amd._lib import PratchyaUnsupported
+    K = _K()
+    with pytest.raises(PratchyaUnsupported):
+        K.gemm_bf16_gram(torch.zeros((300, 128), dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(PratchyaUnsupported):
+        K.gemm_bf16_gram(torch.zeros((256, 96), dtype=torch.bfloat16, device="cuda"))
+
+
+def test_gram_two_streams_keep_their_workspaces():
+    """Calls on two streams at once use separate partial-tile workspaces."""
+    K = _K()
+    a = _bf16((2048, 4096), 11, 1.0 / 64)
+    b = _bf16((2048, 4096), 12, 1.0 / 64)
+    ref_a, ref_b = K.gemm_bf16_gram(a), K.gemm_bf16_gram(b)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    with torch.cuda.stream(s1):
+        ca = K.gemm_bf16_gram(a)
+    with torch.cuda.stream(s2):
+        cb = K.gemm_bf16_gram(b)
+    torch.cuda.synchronize()
+    assert torch.equal(ca.view(torch.int16), ref_a.view(torch.int16))
+    assert torch.equal(cb.view(torch.int16), ref_b.view(torch.int16))

@@ -662,6 +662,67 @@ __device__ __forceinline__ void store_tile(const v16f (&acc)[2][4], const float 
   }
 }
 
+// Epilogue of the Gram product (bf16 output): the tile as store_tile writes
+// it and, for a tile off the diagonal (mirror), its transpose at the mirrored
+// position: from each pass's 32 staged rows, a lane takes a column pair and
+// 8 rows and writes the two transposed 16-byte row chunks.  (A diagonal tile
+// is symmetric as computed: its two triangles hold the same products,
+// summed in the same order.)
+__device__ __forceinline__ void store_tile_gram(const v16f (&acc)[2][4], uint8_t* stage, int wave, int lane,
+                                                void* C, int64_t ldc, int row0, int col0, bool mirror) {
+  const int l32 = lane & 31, lhi = lane >> 5;
+  constexpr int ROWB = 256;                 // 128 bf16 columns
+  constexpr int PITCH = ROWB + 16;
+  constexpr int CHUNKS = ROWB / 16;
+  constexpr int RP = 32;
+  uint8_t* stg = stage + wave * (RP * PITCH);
+  __syncthreads();                          // every wave is done with the stage buffer
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int col = ni * 32 + 8 * j + 4 * lhi;
+        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+        const bf16x2 p0 = {(__bf16)acc[mi][ni][4 * j + 0], (__bf16)acc[mi][ni][4 * j + 1]};
+        const bf16x2 p1 = {(__bf16)acc[mi][ni][4 * j + 2], (__bf16)acc[mi][ni][4 * j + 3]};
+        *reinterpret_cast<uint2*>(stg + l32 * PITCH + col * 2) =
+            make_uint2(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1));
+      }
+    __builtin_amdgcn_s_waitcnt(0xC07F);     // lgkmcnt(0): this wave's staging writes are done
+    uint8_t* Cb = static_cast<uint8_t*>(C) + ((int64_t)(row0 + mi * 32) * ldc + col0) * 2;
+#pragma unroll
+    for (int it = 0; it < (RP * CHUNKS) / 64; ++it) {
+      const int q = it * 64 + lane;
+      const int r = q / CHUNKS, c = q % CHUNKS;
+      const v4i v = *reinterpret_cast<const v4i*>(stg + r * PITCH + c * 16);
+      __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(Cb + (int64_t)r * ldc * 2 + c * 16));
+    }
+    if (mirror) {
+      // output rows col0 + [0, 128), columns row0 + mi * 32 + [0, 32)
+      uint8_t* Ct = static_cast<uint8_t*>(C) + ((int64_t)col0 * ldc + row0 + mi * 32) * 2;
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int q = it * 64 + lane;
+        const int cp = q >> 2, k = q & 3;   // columns 2 cp, 2 cp + 1; staged rows 8 k .. 8 k + 7
+        uint32_t w[8];
+#pragma unroll
+        for (int x = 0; x < 8; ++x) w[x] = *reinterpret_cast<const uint32_t*>(stg + (8 * k + x) * PITCH + cp * 4);
+        v4i lo, hi;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lo[e] = (int)__builtin_amdgcn_perm(w[2 * e + 1], w[2 * e], 0x05040100u);
+          hi[e] = (int)__builtin_amdgcn_perm(w[2 * e + 1], w[2 * e], 0x07060302u);
+        }
+        __builtin_nontemporal_store(lo, reinterpret_cast<v4i*>(Ct + (int64_t)(2 * cp) * ldc * 2 + k * 16));
+        __builtin_nontemporal_store(hi, reinterpret_cast<v4i*>(Ct + (int64_t)(2 * cp + 1) * ldc * 2 + k * 16));
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);     // staging reads done before the next pass overwrites
+  }
+}
+
 // Output requantization, QArrayImpl(C, (1, 128)).astype(dtype) (Q:458-506
 // then Q:541-569; with FIXNAN, quantize_impl_bwd's dequantization that reads
 // an e8m0 byte 255 as 1.0, Q:521-526), in two steps.
@@ -1178,8 +1239,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
         gram_put_partial(acc, fq, (int)blockIdx.x, wave, lane);
       } else {
         gram_add_partials(acc, fq, (int)blockIdx.x, (int)gridDim.x, t, wave, lane);
-        store_tile<true, 0>(acc, gA, gB, nullptr, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc,
-                            m0 + wm * 64, n0 + wn * 128, M, N);
+        store_tile_gram(acc, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc, m0 + wm * 64,
+                        n0 + wn * 128, tm != tn);
       }
     } else if constexpr (FQ == 3) {
       static_assert(BF && OUT_BF16, "the Newton-Schulz epilogue combines bf16 products");
@@ -1602,48 +1663,10 @@ extern "C" int pratchya_gemm_bf16_nt_ns(const void* A, int64_t lda, const void* 
 // --------------------------------------------------------------------------
 // Symmetric product C = A A^T (the Gram matrix of Newton-Schulz's first
 // product): the kernel computes the upper-triangle tiles by stream-K (see
-// FqArgs), then k_mirror_lower_b16 copies the transposed upper triangle into
-// the lower one, so C is exactly symmetric.
+// FqArgs) and writes each off-diagonal tile also transposed, so C is exactly
+// symmetric.
 // --------------------------------------------------------------------------
 namespace {
-
-// C[r][c] = C[c][r] for r > c, by 64 x 64 blocks (bi, bj), bi >= bj, of the
-// lower triangle numbered row by row: block (bj, bi) is read through LDS and
-// written transposed to (bi, bj) (on the diagonal only below it).
-__global__ __launch_bounds__(256) void k_mirror_lower_b16(uint16_t* __restrict__ C, int64_t ldc) {
-  __shared__ uint16_t tile[64][64 + 2];
-  int q = (int)blockIdx.x, bi = 0;
-  while (q > bi) {
-    q -= bi + 1;
-    ++bi;
-  }
-  const int bj = q;
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int c = it * 256 + (int)threadIdx.x, r = c >> 3, ch = c & 7;
-    const v4i v = *reinterpret_cast<const v4i*>(C + (int64_t)(bj * 64 + r) * ldc + bi * 64 + ch * 8);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      tile[r][ch * 8 + 2 * e] = (uint16_t)((uint32_t)v[e] & 0xFFFFu);
-      tile[r][ch * 8 + 2 * e + 1] = (uint16_t)((uint32_t)v[e] >> 16);
-    }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int c = it * 256 + (int)threadIdx.x, r = c >> 3, ch = c & 7;
-    v4i o;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int c0 = ch * 8 + 2 * e;
-      // on the diagonal block, elements on or above the diagonal stay
-      const uint32_t lo = (bi > bj || r > c0) ? tile[c0][r] : tile[r][c0];
-      const uint32_t hi = (bi > bj || r > c0 + 1) ? tile[c0 + 1][r] : tile[r][c0 + 1];
-      o[e] = (int)(lo | (hi << 16));
-    }
-    *reinterpret_cast<v4i*>(C + (int64_t)(bi * 64 + r) * ldc + bj * 64 + ch * 8) = o;
-  }
-}
 
 // Workgroups of the Gram product: one range per CU, at most two per tile
 // (each range then holds at least half a tile's steps, so a tile has at most
@@ -1696,11 +1719,6 @@ extern "C" int pratchya_gemm_bf16_gram(const void* A, int64_t lda, int64_t M, in
   if (rc) return rc;
   P.grid = G;
   bf16_launch<true, 4>(P, A, lda, A, lda, C, ldc, M, M, K, fq, stream);
-  rc = launch_status("gemm_bf16_gram");
-  if (rc) return rc;
-  const int64_t nb = M / 64;
-  hipLaunchKernelGGL(k_mirror_lower_b16, dim3((unsigned)(nb * (nb + 1) / 2)), dim3(256), 0, stream,
-                     static_cast<uint16_t*>(C), ldc);
   return launch_status("gemm_bf16_gram");
 }
 

@@ -37,8 +37,11 @@ def _bf16(shape, seed, scale=1.0):
 
 # (M, K): one tile; K of one 64-wide step (every range one whole tile);
 # three tiles per side with 3 steps each (ranges of 1-2 steps); 10 tiles with
-# 32 steps on 20 ranges; the Newton-Schulz shapes
-SHAPES = [(256, 512), (768, 64), (768, 192), (1024, 2048), (2048, 1024), (4096, 4096), (4096, 16384)]
+# 32 steps on 20 ranges; the Newton-Schulz shapes (the 16 x 16 tile grid in
+# its L2-aware order); 528 tiles of 4 steps on 256 ranges (a range holds the
+# end of one tile, whole tiles and the start of another)
+SHAPES = [(256, 512), (768, 64), (768, 192), (1024, 2048), (2048, 1024), (4096, 4096), (4096, 16384),
+          (8192, 256)]
 
 
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))

@@ -3,7 +3,8 @@ each replay, with new inputs copied in eagerly between replays, gives the
 bytes of the same calls made eagerly.  This covers the contract that the
 entry points only enqueue work (no allocation, no host synchronisation, no
 memset nodes): the general quantizer clears its block-max workspace with a
-kernel on every replay, and the fused elementwise general path likewise."""
+kernel on every replay, and the fused elementwise general path and the Gram
+product's partial-tile flags likewise."""
 import numpy as np
 import pytest
 import torch
@@ -48,7 +49,9 @@ def test_graph_replays_match_eager():
         d = K.elementwise("mul", xq, (1, 128), yq, (1, 128), (4, 64))   # fused, general path
         t = K.quantize_t128(x)                                          # transposed requantize
         q = K.dequantize(*xq, torch.float32, (1, 128))
-        return [*xq, *wq, c, *s, *d, *t, q]
+        gr = K.gemm_bf16_gram(x)                                        # stream-K, flags cleared by a kernel
+        ns = K.gemm_bf16_nt_ns(x, x, gr)                                # Newton-Schulz epilogue
+        return [*xq, *wq, c, *s, *d, *t, q, gr, ns]
 
     fill()
     torch.cuda.synchronize()

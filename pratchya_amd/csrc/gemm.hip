@@ -30,7 +30,11 @@
 //     set suffices; the epilogue multiplies by gA gB / 2^14;
 //   * tiles are numbered so that the workgroups resident on one XCD (the
 //     dispatcher deals workgroups round-robin to the 8 XCDs) cover a 4 x 8
-//     block of output tiles and share A and B panels in that XCD's L2.
+//     block of output tiles and share A and B panels in that XCD's L2;
+//   * the same pipeline also runs the bf16 products of Newton-Schulz (BF),
+//     with its 1.5 X - 0.5 B combination in the epilogue (FQ 3), and the
+//     symmetric product A A^T on the upper-triangle tiles only, split by K
+//     between workgroups (FQ 4, see FqArgs).
 //
 // Differences from the reference's f32 dequant-then-matmul: summation order,
 // and blocks whose e8m0 byte is 0 (block max below 2^-126 of its group max):
@@ -419,9 +423,9 @@ struct FqArgs {
 // multiple of 32 steps per tile: range r starts at step 17 r S / 32, so the
 // ranges r = m + 32 n (n = 0..7), which run on one XCD, are at the same K
 // step at all times, on tiles q0 + 17 n.  The order makes each such set
-// {a + 17 n} a block of tiles over at most 6 panels (mostly 2 x 4 tiles;
-// one set of 8 diagonal-adjacent tiles), so the 8 workgroups read the same
-// K slices of few panels and share them in their XCD's L2.  Entry q is
+// {a + 17 n} a block of tiles over 4 to 6 panels (mostly 2 x 4 tiles; one
+// set of near-diagonal tiles spans 8), so the 8 workgroups read the same K
+// slices of few panels and share them in their XCD's L2.  Entry q is
 // 16 i + j of tile (i, j).
 __constant__ uint8_t kGramOrder16[136] = {
     2, 6, 10, 36, 40, 44, 70, 74, 104, 108, 138, 172, 0, 68, 136, 204, 35,

@@ -342,21 +342,23 @@ int pratchya_gemm_bf16_nt_ns(const void* A, int64_t lda, const void* B, int64_t 
 
 /* Symmetric bf16 product C = A . A^T:     replaces the Gram product of newton_schulz
  *   C[m, n] = sum_k A[m, k] * A[n, k]      (pratchya/_nnx_impl/_optimizer.py:20-22,
- * A @ A.T of the wide iterate, and A.T @ A of a tall one with A its transpose)
+ * A @ A.T of the wide iterate, and A.T @ A of a tall one, whose transpose is A)
  * with f32 accumulation, rounded once to bf16.  Only the tiles on and above
  * the diagonal are computed (stream-K: every CU takes an equal share of
  * their K steps; a tile split between CUs is summed in f32 by the CU holding
  * its first steps, in a fixed order, so results are deterministic), and the
  * lower triangle is written as the transposed upper one (C == C^T exactly).
- * A: bf16 [M, K] (lda, a multiple of 8; 16-byte aligned); M a multiple of 256
- * and K of 64 (PRATCHYA_EUNSUPPORTED otherwise).  C: bf16 [M, M] (ldc), not
- * overlapping A.  workspace: device memory of
+ * A: bf16 [M, K] (row stride lda), or with a_kmajor its K-major layout, the
+ * [K, M] matrix A^T (row stride lda >= M): the tall iterate itself, read
+ * through the LDS transposing loads instead of a transposed copy; lda a
+ * multiple of 8, 16-byte aligned; M a multiple of 256 and K of 64
+ * (PRATCHYA_EUNSUPPORTED otherwise).  C: bf16 [M, M] (ldc), not overlapping A.  workspace: device memory of
  * pratchya_gemm_bf16_gram_workspace_bytes(M, K) bytes (f32 partial tiles and
  * flags, ~64 MB on a 256-CU device), 16-byte aligned; its last word is set to
  * 1 if a partial tile did not arrive in time (that tile is then NaN).  Calls
  * that share a workspace must not overlap. */
 int64_t pratchya_gemm_bf16_gram_workspace_bytes(int64_t M, int64_t K);
-int pratchya_gemm_bf16_gram(const void* A, int64_t lda, int64_t M, int64_t K, void* C, int64_t ldc,
+int pratchya_gemm_bf16_gram(const void* A, int64_t lda, int64_t M, int64_t K, int a_kmajor, void* C, int64_t ldc,
                             void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /* f32 operands of pratchya_gemm_bf16_nt:    for the f32 products of the mixed

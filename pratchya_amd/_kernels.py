@@ -685,18 +685,21 @@ def transpose_b16(x: torch.Tensor) -> torch.Tensor:
 _GRAM_WS = {}
 
 
-def gemm_bf16_gram(a: torch.Tensor) -> torch.Tensor:
+def gemm_bf16_gram(a: torch.Tensor, k_major: bool = False) -> torch.Tensor:
     """The symmetric bf16 product ``a @ a^T`` (f32 accumulation, rounded once
     to bf16) of a bf16 ``a`` [M, K], the Gram product of newton_schulz
     (pratchya/_nnx_impl/_optimizer.py:20-22): only the tiles on and above the
     diagonal are computed and the lower triangle is their transpose, so the
-    result is exactly symmetric.  M must be a multiple of 256 and K of 64
-    (``PratchyaUnsupported`` otherwise).  The partial-tile workspace is kept
-    per device and stream; calls on one stream run in order."""
+    result is exactly symmetric.  With ``k_major``, ``a`` is given as its
+    [K, M] transpose and the result is ``a^T @ a`` [M, M] (the Gram product of
+    a tall iterate, read without a transposed copy).  M must be a multiple of
+    256 and K of 64 (``PratchyaUnsupported`` otherwise).  The partial-tile
+    workspace is kept per device and stream; calls on one stream run in
+    order."""
     _require_gpu(a)
     if a.dtype != torch.bfloat16 or a.dim() != 2:
         raise ValueError("gemm_bf16_gram: a must be 2-D bfloat16")
-    M, Kd = int(a.shape[0]), int(a.shape[1])
+    M, Kd = (int(a.shape[1]), int(a.shape[0])) if k_major else (int(a.shape[0]), int(a.shape[1]))
     lib = _lib.load()
     ws_bytes = int(lib.pratchya_gemm_bf16_gram_workspace_bytes(M, Kd))
     if ws_bytes <= 0:
@@ -709,8 +712,8 @@ def gemm_bf16_gram(a: torch.Tensor) -> torch.Tensor:
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=ap.device)
         _GRAM_WS[key] = ws
     out = torch.empty((M, M), dtype=torch.bfloat16, device=ap.device)
-    _lib.check(lib.pratchya_gemm_bf16_gram(_ptr(ap), Kd, M, Kd, _ptr(out), M, _ptr(ws), int(ws.numel()),
-                                           _stream(ap)), "gemm_bf16_gram")
+    _lib.check(lib.pratchya_gemm_bf16_gram(_ptr(ap), int(ap.stride(0)), M, Kd, 1 if k_major else 0, _ptr(out), M,
+                                           _ptr(ws), int(ws.numel()), _stream(ap)), "gemm_bf16_gram")
     return out
 
 

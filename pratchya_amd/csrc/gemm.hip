@@ -54,6 +54,7 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -111,6 +112,32 @@ template <int OFF>
 __device__ __forceinline__ v8i read_frag2(const uint8_t* base_lo, const uint8_t* base_hi) {
   const v4i lo = *reinterpret_cast<const v4i*>(base_lo + OFF);
   const v4i hi = *reinterpret_cast<const v4i*>(base_hi + OFF);
+  return v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+}
+
+// K-major ("TN") bf16 operand of the Gram product: the stage holds 64 K rows
+// of 256 operand rows each (512 bytes per K row, the operand's natural
+// layout), 16-byte chunks XOR-swizzled by 4 * (k mod 4) so that the
+// transposing reads below are bank-conflict free.  ds_read_b64_tr_b16 lets
+// each lane of a 16-lane group read 4 bf16 of one K row; lane i then holds
+// element i mod 4 of the reads of lanes i / 4 + 4 e (e = 0..3): with lane j of
+// the group reading K row k0 + j / 4 at operand row m0 + 4 (j mod 4), lane i
+// receives operand row m0 + i and K rows k0 .. k0 + 3, the MFMA's layout.
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
+__device__ __forceinline__ v4i tr_pair(const uint8_t* p0, const uint8_t* p1) {
+  const v4s a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)p0);
+  const v4s b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)p1);
+  const v2i x = __builtin_bit_cast(v2i, a), y = __builtin_bit_cast(v2i, b);
+  return v4i{x.x, x.y, y.x, y.y};
+}
+// 32-byte fragment of 32 operand rows at `base` (the lane's row and K-row
+// offsets folded in): K rows +0..7 / +8..15 (lane halves) for the first MFMA,
+// +16..23 / +24..31 for the second.
+template <int OFF>
+__device__ __forceinline__ v8i read_frag_tn(const uint8_t* base) {
+  const v4i lo = tr_pair(base + OFF, base + OFF + 4 * 512);
+  const v4i hi = tr_pair(base + OFF + 16 * 512, base + OFF + 20 * 512);
   return v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 }
 
@@ -188,6 +215,18 @@ __device__ __forceinline__ void dma_offsets(int64_t ld, int lane, uint32_t (&off
   }
 }
 
+// K-major operand (TN): instruction i of a wave loads K rows 2i, 2i + 1 of
+// its 16 (512 bytes each): lane -> K row (lane >> 5), LDS chunk lane & 31,
+// which holds the operand's chunk (lane & 31) ^ 4 (k mod 4) of that row.
+__device__ __forceinline__ void dma_offsets_tn(int64_t ld, int lane, uint32_t (&off)[2]) {
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int rp = lane >> 5, c = lane & 31;
+    const int sw = ((2 * par + rp) & 3) << 2;
+    off[par] = (uint32_t)(rp * ld + ((c ^ sw) << 4));
+  }
+}
+
 // One wave's share of a stage's DMA.  The stage load is split between the
 // two ping-pong groups: wave w of group 0 loads A rows [64w, 64w + 64) of the
 // tile, their e8m0 words and group maxima; wave w of group 1 the same for B.
@@ -202,6 +241,7 @@ struct DmaHalf {
   int lds_pay, lds_e;          // stage offsets of this wave's payload rows, e8m0 words
   int lds_r, lds_u;            // offsets of the operand's unit ratio (in a stage) and unit arrays
   int pub;                     // byte offset of the lane's row in those arrays
+  uint32_t krow0;              // TN: the wave's first K row in a stage (16 per wave)
 };
 
 // The rows a wave loads for one output tile: the first of its 64 rows (global
@@ -214,9 +254,18 @@ struct DmaRows {
 // Row group i (8 rows) of a stage load whose row group 0 starts at byte
 // offset soff0 of the operand (row0 * ld + kt * BK) and LDS address lds0:
 // one add per row group, so that little scalar work sits between the MFMAs.
+template <bool TN = false>
 __device__ __forceinline__ void dma_rows_at(const DmaHalf& h, uint32_t soff0, uint8_t* lds0, int i) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(h.pay, (lds_void*)(lds0 + i * 1024), 16, h.off[i & 1],
-                                           soff0 + (uint32_t)i * (8u * h.ld), 0, 0);
+                                           soff0 + (uint32_t)i * ((TN ? 2u : 8u) * h.ld), 0, 0);
+}
+
+// TN: K rows 2i, 2i + 1 of this wave's 16 for K block kt (64 K rows) of the
+// operand rows starting at r.row0, into stage st.
+__device__ __forceinline__ void dma_rows_tn(const DmaHalf& h, const DmaRows& r, uint8_t* st, int kt, int i) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(h.pay, (lds_void*)(st + h.lds_pay + i * 1024), 16, h.off[i & 1],
+                                           r.row0 * 2u + ((uint32_t)kt * 64u + h.krow0 + (uint32_t)(2 * i)) * h.ld,
+                                           0, 0);
 }
 
 // Row group i (8 rows) of this wave's 64 rows for K block kt into stage st.
@@ -961,6 +1010,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   const int wm = wave & 3, wn = grp;      // 64-row band wm, 128-column half wn
   int nk = K / BK;                        // K steps of the current unit
   const int T = tiles_m * tiles_n;
+  // the Gram product (upper-triangle tiles by stream-K), with K-contiguous
+  // (FQ 4) or K-major (FQ 5, "TN") operand rows
+  constexpr bool GRAM = FQ == 4 || FQ == 5;
+  constexpr bool TN = FQ == 5;
+  static_assert(!GRAM || BF, "the Gram product is a bf16 product");
   const int l32 = lane & 31, lhi = lane >> 5;
 
   // this wave's half of every stage load: A rows (group 0) or B rows (group 1)
@@ -975,7 +1029,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     h.ld = (uint32_t)(grp == 0 ? lda : ldb);
     h.s_k = (uint32_t)so.s_k;
     h.kg = (uint32_t)so.kg;
-    dma_offsets(grp == 0 ? lda : ldb, lane, h.off);
+    if constexpr (TN) dma_offsets_tn(grp == 0 ? lda : ldb, lane, h.off);
+    else dma_offsets(grp == 0 ? lda : ldb, lane, h.off);
+    h.krow0 = (uint32_t)(16 * w4);
     h.lds_pay = (grp == 0 ? 0 : OFF_B) + w4 * 8 * 1024;
     h.lds_e = (grp == 0 ? OFF_EA : OFF_EB) + w4 * 256;
     h.lds_r = grp == 0 ? OFF_RA : OFF_RB;
@@ -991,13 +1047,18 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   }
   auto rows_of = [&](int tm_, int tn_, int kb_) {
     DmaRows r;
-    r.row0 = (uint32_t)((grp == 0 ? tile_base(tm_, M) : tile_base(tn_, N)) + w4 * 64);
+    // TN: the tile's first operand row (the wave's share is 16 K rows)
+    r.row0 = (uint32_t)((grp == 0 ? tile_base(tm_, M) : tile_base(tn_, N)) + (TN ? 0 : w4 * 64));
     r.e_word = (uint32_t)blk_index(so, (int64_t)r.row0 + lane, 0);
     r.kb = kb_;
     return r;
   };
   // K block of a unit's first step: 0 except for the segments of a Gram range
-  auto kb_of = [&](const DmaRows& r) { return FQ == 4 ? r.kb : 0; };
+  auto kb_of = [&](const DmaRows& r) { return GRAM ? r.kb : 0; };
+  auto stage_rows = [&](const DmaRows& r, uint8_t* st, int kt, int i) {
+    if constexpr (TN) dma_rows_tn(h, r, st, kt, i);
+    else dma_rows(h, r, st, kt, i);
+  };
   const uint32_t skA = (uint32_t)sa.s_k, skB = (uint32_t)sb.s_k;
   // physical 16-byte chunk offsets of this lane's operand halves: K half ks,
   // lo/hi chunk (logical 4*ks + 2*lhi + h, XOR-swizzled by the lane's row)
@@ -1009,6 +1070,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) ch[ks][hh] = ((ks * 4 + lhi * 2 + hh) ^ sw) << 4;
   }
+  // TN fragment reads (read_frag_tn): in 16-lane group g, lane j reads K row
+  // 8 (g / 2) + j / 4 at operand row 16 (g % 2) + 4 (j % 4) of a 32-row block;
+  // tn_kc is that K row's byte offset plus the row's chunk (c = 2 (g % 2) +
+  // (j % 4) / 2 inside the block's 4 chunks) and byte ((j % 2) 8) offsets, tn_s
+  // the row's swizzle (k mod 4 = j / 4)
+  int tn_kc = 0, tn_s = 0;
+  if constexpr (TN) {
+    const int g16 = lane >> 4, j16 = lane & 15;
+    tn_kc = (8 * (g16 >> 1) + (j16 >> 2)) * 512 + (2 * (g16 & 1) + ((j16 & 3) >> 1)) * 16 + (j16 & 1) * 8;
+    tn_s = j16 >> 2;
+  }
 
   // Persistent: workgroup b computes tiles b, b + G, b + 2G, ... (G = grid
   // size, a multiple of the 8 XCDs, so every tile of a workgroup falls in the
@@ -1017,7 +1089,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   // steps into the stage buffer they no longer read, and its latency is
   // covered by the epilogue, which stages the output in the other buffer.
   //
-  // Gram (FQ == 4): the units are the segments of this workgroup's range of
+  // Gram (FQ 4, 5): the units are the segments of this workgroup's range of
   // the stream-K step sequence (see FqArgs): a unit is the part of one tile's
   // K steps inside the range, at most two per range.
   int t = blockIdx.x;
@@ -1037,7 +1109,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     *q_ = (int)qq;
     tri_of((int)qq, fq.tri, fq.order16 != 0, tm_, tn_);
   };
-  if constexpr (FQ == 4) {
+  if constexpr (GRAM) {
     g = (int64_t)blockIdx.x * fq.iters / gridDim.x;
     g_end = ((int64_t)blockIdx.x + 1) * fq.iters / gridDim.x;
     gram_unit(g, &t, &tm, &tn, &kb, &nk);
@@ -1052,7 +1124,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   // DMA, not yet published: g_pub (a span start), its group max g_ld, its
   // buffer g_st, g_first (a tile's K block 0).
 #pragma unroll
-  for (int i = 0; i < 8; ++i) dma_rows(h, cur, lds, kb_of(cur), i);
+  for (int i = 0; i < 8; ++i) stage_rows(cur, lds, kb_of(cur), i);
   float g_ld = 0.0f, u_prev = 1.0f;
   if constexpr (!BF) {
     dma_scales(h, cur, lds, 0);
@@ -1068,12 +1140,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     const int m0 = tile_base(tm, M), n0 = tile_base(tn, N);
     int t_next = t + (int)gridDim.x, kb2 = 0, nk2 = nk;
     bool has_next;
-    if constexpr (FQ == 4) has_next = g + nk < g_end;
+    if constexpr (GRAM) has_next = g + nk < g_end;
     else has_next = t_next < T;
     int tm2 = 0, tn2 = 0;
     DmaRows nxt = cur;
     if (has_next) {
-      if constexpr (FQ == 4) gram_unit(g + nk, &t_next, &tm2, &tn2, &kb2, &nk2);
+      if constexpr (GRAM) gram_unit(g + nk, &t_next, &tm2, &tn2, &kb2, &nk2);
       else next_tile(t_next, &tm2, &tn2);
       nxt = rows_of(tm2, tn2, kb2);
     }
@@ -1081,7 +1153,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
       if (1 < nk) {
         uint8_t* s1 = lds + ((1 + par) & 1) * STAGE_BYTES;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) dma_rows(h, cur, s1, 1 + kb_of(cur), i);
+        for (int i = 0; i < 8; ++i) stage_rows(cur, s1, 1 + kb_of(cur), i);
         if constexpr (!BF) {
           dma_scales(h, cur, s1, 1);
           g_pub = span == 1;
@@ -1151,12 +1223,25 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
         const uint8_t* blo = st + (wn * 128 + l32) * BK + ch[ks][0];
         const uint8_t* bhi = st + (wn * 128 + l32) * BK + ch[ks][1];
         v8i fa[2], fb[4];
-        fa[0] = read_frag2<0>(alo, ahi);
-        fa[1] = read_frag2<32 * BK>(alo, ahi);
-        fb[0] = read_frag2<OFF_B>(blo, bhi);
-        fb[1] = read_frag2<OFF_B + 32 * BK>(blo, bhi);
-        fb[2] = read_frag2<OFF_B + 64 * BK>(blo, bhi);
-        fb[3] = read_frag2<OFF_B + 96 * BK>(blo, bhi);
+        if constexpr (TN) {
+          // the lane's 32-row block R (A: 2 wm + mi, B: 4 wn + ni): K rows
+          // tn_k (+ 32 ks), operand rows from chunk (4 R + tn_c) ^ (4 tn_s)
+          const uint8_t* kb0 = st + tn_kc + ks * 32 * 512;
+          auto rb = [&](int R) { return kb0 + ((R ^ tn_s) << 6); };
+          fa[0] = read_frag_tn<0>(rb(2 * wm));
+          fa[1] = read_frag_tn<0>(rb(2 * wm + 1));
+          fb[0] = read_frag_tn<OFF_B>(rb(4 * wn));
+          fb[1] = read_frag_tn<OFF_B>(rb(4 * wn + 1));
+          fb[2] = read_frag_tn<OFF_B>(rb(4 * wn + 2));
+          fb[3] = read_frag_tn<OFF_B>(rb(4 * wn + 3));
+        } else {
+          fa[0] = read_frag2<0>(alo, ahi);
+          fa[1] = read_frag2<32 * BK>(alo, ahi);
+          fb[0] = read_frag2<OFF_B>(blo, bhi);
+          fb[1] = read_frag2<OFF_B + 32 * BK>(blo, bhi);
+          fb[2] = read_frag2<OFF_B + 64 * BK>(blo, bhi);
+          fb[3] = read_frag2<OFF_B + 96 * BK>(blo, bhi);
+        }
         if (grp == 1 && ks == 1 && kt + 1 < nk) {
           PINNED_WAITCNT(0);        // also group 1's half of stage kt+1 landed
           if (!BF && g_pub) publish_g(h, lds, g_st, g_ld, g_first, u_prev);
@@ -1182,17 +1267,18 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
         const DmaRows& dr = to_next ? nxt : cur;
         const int lkt = to_next ? 0 : dkt;            // K block inside the tile loaded
         uint8_t* dst = lds + ((dkt + par) & 1) * STAGE_BYTES;
-        const uint32_t soff0 = dr.row0 * h.ld + (uint32_t)(lkt + kb_of(dr)) * BK;
+        const uint32_t soff0 = TN ? dr.row0 * 2u + ((uint32_t)(lkt + kb_of(dr)) * 64u + h.krow0) * h.ld
+                                  : dr.row0 * h.ld + (uint32_t)(lkt + kb_of(dr)) * BK;
         uint8_t* const lds0 = dst + h.lds_pay;
         pin_frags(fa, fb);
         mfma_pinned<0, 0, BF>(acc, fa, fb, eA, eB);
-        if (dma_now) { dma_rows_at(h, soff0, lds0, 0); dma_rows_at(h, soff0, lds0, 1); }
+        if (dma_now) { dma_rows_at<TN>(h, soff0, lds0, 0); dma_rows_at<TN>(h, soff0, lds0, 1); }
         mfma_pinned<0, 1, BF>(acc, fa, fb, eA, eB);
-        if (dma_now) { dma_rows_at(h, soff0, lds0, 2); dma_rows_at(h, soff0, lds0, 3); }
+        if (dma_now) { dma_rows_at<TN>(h, soff0, lds0, 2); dma_rows_at<TN>(h, soff0, lds0, 3); }
         mfma_pinned<0, 2, BF>(acc, fa, fb, eA, eB);
-        if (dma_now) { dma_rows_at(h, soff0, lds0, 4); dma_rows_at(h, soff0, lds0, 5); }
+        if (dma_now) { dma_rows_at<TN>(h, soff0, lds0, 4); dma_rows_at<TN>(h, soff0, lds0, 5); }
         mfma_pinned<0, 3, BF>(acc, fa, fb, eA, eB);
-        if (dma_now) { dma_rows_at(h, soff0, lds0, 6); dma_rows_at(h, soff0, lds0, 7); }
+        if (dma_now) { dma_rows_at<TN>(h, soff0, lds0, 6); dma_rows_at<TN>(h, soff0, lds0, 7); }
         mfma_pinned<1, 0, BF>(acc, fa, fb, eA, eB);
         if (dma_now && !BF) {
           dma_scales(h, dr, dst, lkt);
@@ -1236,7 +1322,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     // for LDS work only
     __builtin_amdgcn_s_waitcnt(0x0F70);      // vmcnt(0)
     asm volatile("" ::"v"(g_ld));
-    if constexpr (FQ == 4) {
+    if constexpr (GRAM) {
       static_assert(BF && OUT_BF16, "the Gram product is a bf16 product");
       if (kb != 0) {
         // the rest of a tile whose head is an earlier range's
@@ -1267,7 +1353,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     tn = tn2;
     cur = nxt;
     par = (par + nk) & 1;
-    if constexpr (FQ == 4) {
+    if constexpr (GRAM) {
       g += nk;
       kb = kb2;
       nk = nk2;
@@ -1691,12 +1777,24 @@ extern "C" int64_t pratchya_gemm_bf16_gram_workspace_bytes(int64_t M, int64_t K)
   return G * 8 * (32 * 256) * 4 + (G * 8 + 1) * 4;
 }
 
-extern "C" int pratchya_gemm_bf16_gram(const void* A, int64_t lda, int64_t M, int64_t K, void* C, int64_t ldc,
-                                       void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+extern "C" int pratchya_gemm_bf16_gram(const void* A, int64_t lda, int64_t M, int64_t K, int a_kmajor, void* C,
+                                       int64_t ldc, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   GemmPlan P;
   bool empty;
-  int rc = bf16_plan("gemm_bf16_gram", A, lda, A, lda, M, M, K, C, ldc, true, &P, &empty);
+  // a K-major A ([K, M], row stride lda >= M) is validated as the plan of its
+  // [M, K] view with the operand sizes of its own layout
+  int rc = bf16_plan("gemm_bf16_gram", A, a_kmajor ? K : lda, A, a_kmajor ? K : lda, M, M, K, C, ldc, true, &P,
+                     &empty);
   if (rc || empty) return rc;
+  if (a_kmajor) {
+    if (lda < M || lda % 8)
+      return pratchya_set_error(PRATCHYA_EINVAL, "gemm_bf16_gram: a K-major A needs a row stride of at least M, "
+                                "a multiple of 8");
+    const int64_t bytes = ((K - 1) * lda + M) * 2;
+    if (bytes > (int64_t)INT32_MAX)
+      return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_bf16_gram: operand beyond 2 GiB");
+    P.a_bytes = P.b_bytes = bytes;
+  }
   if (M % BM)
     return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_bf16_gram: M must be a multiple of 256 (got %lld)",
                               (long long)M);
@@ -1722,7 +1820,8 @@ extern "C" int pratchya_gemm_bf16_gram(const void* A, int64_t lda, int64_t M, in
   rc = launch_status("gemm_bf16_gram");
   if (rc) return rc;
   P.grid = G;
-  bf16_launch<true, 4>(P, A, lda, A, lda, C, ldc, M, M, K, fq, stream);
+  if (a_kmajor) bf16_launch<true, 5>(P, A, lda, A, lda, C, ldc, M, M, K, fq, stream);
+  else bf16_launch<true, 4>(P, A, lda, A, lda, C, ldc, M, M, K, fq, stream);
   return launch_status("gemm_bf16_gram");
 }
 

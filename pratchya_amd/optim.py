@@ -70,19 +70,23 @@ def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
     # other dtypes and sizes use the BLAS library (f32 accumulation either way).
     on_kernel = X.dtype == torch.bfloat16 and m % 64 == 0 and n % 64 == 0
     # the Gram product computes only its upper-triangle tiles (exactly
-    # symmetric result) where its side is a multiple of 256
+    # symmetric result) where its side is a multiple of 256; a tall iterate
+    # is read K-major by it, with no transposed copy
     gram_side = n if transpose else m
-    gram = K.gemm_bf16_gram if gram_side % 256 == 0 else (lambda a: K.gemm_bf16_nt(a, a))
+    gram_ok = gram_side % 256 == 0
     for _ in range(steps):
         # on the kernel, the second product's epilogue also forms
         # 1.5 X - 0.5 B (the bits of ns_combine), into a new buffer
         if on_kernel and transpose:
-            Xt = K.transpose_b16(X)                  # [n, m]
-            A = gram(Xt)                             # X^T X        [n, n]
+            if gram_ok:
+                A = K.gemm_bf16_gram(X, k_major=True)    # X^T X     [n, n]
+            else:
+                Xt = K.transpose_b16(X)                  # [n, m]
+                A = K.gemm_bf16_nt(Xt, Xt)
             X = K.gemm_bf16_nt_ns(X, A, X)           # 1.5 X - 0.5 X A (A = A^T)
             continue
         elif on_kernel:
-            A = gram(X)                              # X X^T        [m, m]
+            A = K.gemm_bf16_gram(X) if gram_ok else K.gemm_bf16_nt(X, X)   # X X^T [m, m]
             X = K.gemm_bf16_nt_ns(A, K.transpose_b16(X), X)   # 1.5 X - 0.5 A X
             continue
         elif transpose:

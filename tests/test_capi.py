@@ -366,12 +366,15 @@ def test_gemm_bf16_gram_argument_codes_without_gpu():
     assert lib.pratchya_gemm_bf16_gram_workspace_bytes(256, 64) == 8 * 32768 + 9 * 4
     assert lib.pratchya_gemm_bf16_gram_workspace_bytes(300, 64) == 0
     assert lib.pratchya_gemm_bf16_gram_workspace_bytes(256, 96) == 0
-    assert lib.pratchya_gemm_bf16_gram(fake, 128, 304, 128, other, 304, other, 1 << 30, None) == _lib.EUNSUPPORTED
-    assert lib.pratchya_gemm_bf16_gram(fake, 96, 256, 96, other, 256, other, 1 << 30, None) == _lib.EUNSUPPORTED
-    assert lib.pratchya_gemm_bf16_gram(fake, 128, 256, 128, other, 256, other, 16, None) == _lib.EINVAL
+    assert lib.pratchya_gemm_bf16_gram(fake, 128, 304, 128, 0, other, 304, other, 1 << 30, None) == _lib.EUNSUPPORTED
+    assert lib.pratchya_gemm_bf16_gram(fake, 96, 256, 96, 0, other, 256, other, 1 << 30, None) == _lib.EUNSUPPORTED
+    assert lib.pratchya_gemm_bf16_gram(fake, 128, 256, 128, 0, other, 256, other, 16, None) == _lib.EINVAL
     assert b"workspace" in lib.pratchya_last_error()
-    assert lib.pratchya_gemm_bf16_gram(fake, 128, 256, 128, other, 256, None, 1 << 30, None) == _lib.EINVAL
-    assert lib.pratchya_gemm_bf16_gram(fake, 128, 0, 128, other, 256, None, 0, None) == 0
+    assert lib.pratchya_gemm_bf16_gram(fake, 128, 256, 128, 0, other, 256, None, 1 << 30, None) == _lib.EINVAL
+    assert lib.pratchya_gemm_bf16_gram(fake, 128, 0, 128, 0, other, 256, None, 0, None) == 0
+    # K-major A: the row stride must cover M
+    assert lib.pratchya_gemm_bf16_gram(fake, 128, 256, 128, 1, other, 256, other, 1 << 30, None) == _lib.EINVAL
+    assert b"K-major" in lib.pratchya_last_error()
 
 
 def test_gemm_bf16_ns_argument_codes_without_gpu():

@@ -13,7 +13,8 @@ with f32 accumulation), pratchya_gemm_bf16_gram.
   K is split before the f32 sums are added); exactly symmetric;
   identical bits on a repeated call (the partials are added in a fixed order).
 * Shapes cover one tile (a single range), tiles split between two or three
-  ranges, K of a single step (no split), and newton_schulz's [4096, 16384].
+  ranges, K of a single step (no split), and newton_schulz's [4096, 16384];
+  A given K-major (the tall iterate's own layout) gives the same bits.
 """
 import numpy as np
 import pytest
@@ -44,13 +45,16 @@ SHAPES = [(256, 512), (768, 64), (768, 192), (1024, 2048), (2048, 1024), (4096, 
           (8192, 256)]
 
 
+@pytest.mark.parametrize("k_major", [False, True], ids=["rows", "kmajor"])
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_gram_exact_integers(shape):
+def test_gram_exact_integers(shape, k_major):
+    """Also with A given K-major ([K, M], the tall iterate itself), read
+    through the LDS transposing loads."""
     M, Kd = shape
-    print(f"gram exact integers M={M} K={Kd}", flush=True)
+    print(f"gram exact integers M={M} K={Kd} k_major={k_major}", flush=True)
     g = torch.Generator(device="cuda").manual_seed(M + Kd)
     a = torch.randint(-4, 5, (M, Kd), generator=g, device="cuda").to(torch.bfloat16)
-    c = _K().gemm_bf16_gram(a)
+    c = _K().gemm_bf16_gram(a.T.contiguous(), k_major=True) if k_major else _K().gemm_bf16_gram(a)
     ad = a.double()
     ref = (ad @ ad.T).to(torch.bfloat16)        # exact integers, rounded once (RNE)
     torch.cuda.synchronize()
@@ -66,7 +70,12 @@ def test_gram_normal_against_f64_and_nt(shape):
     a = _bf16((M, Kd), 7, 1.0 / np.sqrt(Kd))
     c = K.gemm_bf16_gram(a)
     c2 = K.gemm_bf16_gram(a)
+    # the K-major read of the same matrix (its MFMAs group the K values of a
+    # step differently, so the f32 sums may differ in the last bits)
+    ck = K.gemm_bf16_gram(a.T.contiguous(), k_major=True)
     nt = K.gemm_bf16_nt(a, a, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(ck.view(torch.int16), ck.T.contiguous().view(torch.int16)), "K-major: not symmetric"
     ad = a.double()
     ref = (ad @ ad.T).cpu().numpy()
     torch.cuda.synchronize()
@@ -74,6 +83,7 @@ def test_gram_normal_against_f64_and_nt(shape):
     assert torch.equal(c.view(torch.int16), c.T.contiguous().view(torch.int16)), "not exactly symmetric"
     got = f32(c).astype(np.float64)
     assert O.rel_fro(got, ref) <= 4e-3
+    assert O.rel_fro(f32(ck).astype(np.float64), ref) <= 4e-3
     # against the NT kernel's upper triangle: one bf16 ulp of the larger
     # magnitude, plus the f32 sums' own rounding where a value cancels to
     # near zero (|sum| of the products of a row pair is about 1 here, so

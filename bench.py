@@ -626,10 +626,11 @@ def bench_optimizer(steps: int):
     u = newton_schulz(c, 5)
     ns_ms = _event_ms(lambda: newton_schulz(c, 5), 3)
     # the Gram product of one iteration alone: X^T X of the [16384, 4096]
-    # iterate (its transpose [4096, 16384] is the kernel's operand), on the
-    # symmetric kernel (upper-triangle tiles) and on the plain NT kernel
+    # iterate, on the symmetric kernel reading the iterate K-major (as
+    # newton_schulz does) and on the plain NT kernel (which needs the
+    # transposed copy [4096, 16384] as its operand)
     xt = K.transpose_b16(c)
-    gram_ms = _event_ms(lambda: K.gemm_bf16_gram(xt), 10)
+    gram_ms = _event_ms(lambda: K.gemm_bf16_gram(c, k_major=True), 10)
     gram_nt_ms = _event_ms(lambda: K.gemm_bf16_nt(xt, xt), 10)
     gram_flop = 2 * din * dout * min(din, dout)
     upd_ms = _event_ms(lambda: K.apply_update(u, False, 128.0, sl(p_t), tg, bf, 0.05, 0.005, bf), 10)
@@ -650,11 +651,13 @@ def bench_optimizer(steps: int):
             "ffn_down_newton_schulz": {"ms": round(ns_ms, 3), "TFLOP/s": round(ns_tf, 1),
                                        "frac_of_bf16_peak": round(ns_tf / BF16_PEAK_TFLOPS, 4),
                                        "flop": leaf_ns_flop,
-                                       "kernels": "pratchya_transpose_b16 + pratchya_gemm_bf16_gram (the "
-                                                  "Gram product's 136 upper-triangle tiles of 256, mirrored) + "
-                                                  "pratchya_gemm_bf16_nt_ns (the 1.5X - 0.5B combination in "
-                                                  "the second product's epilogue) per iteration; flop counts "
-                                                  "both products in full, as the reference computes them"},
+                                       "kernels": "pratchya_ns_normalize, then per iteration "
+                                                  "pratchya_gemm_bf16_gram (the Gram product's 136 upper-"
+                                                  "triangle tiles of 256, the tall iterate read K-major, no "
+                                                  "transposed copy) + pratchya_gemm_bf16_nt_ns (the 1.5X - "
+                                                  "0.5B combination in the second product's epilogue); flop "
+                                                  "counts both products in full, as the reference computes "
+                                                  "them"},
             "ffn_down_gram_product": {"us": round(gram_ms * 1e3, 1),
                                       "frac_of_bf16_peak": round(gram_flop / (gram_ms * 1e-3) / 1e12
                                                                  / BF16_PEAK_TFLOPS, 4),

@@ -329,6 +329,18 @@ int pratchya_gemm_bs_nt_fq(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, 
 int pratchya_gemm_bf16_nt(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
                           int64_t K, void* C, int64_t ldc, int c_dtype, hipStream_t stream);
 
+/* Frobenius normalization of newton_schulz's bf16 input (_optimizer.py:17:
+ * X = G / (jnp.linalg.norm(G, ord='fro') + 1e-7), replacing its four jnp
+ * element passes): each square rounded to bf16, their f32 sum rounded to
+ * bf16, the square root and the sum with 1e-7 each rounded to bf16, every
+ * quotient rounded to bf16; two passes in a fixed reduction order
+ * (deterministic).  g, x: bf16 [n], 16-byte aligned; x may be g.  workspace:
+ * device memory of pratchya_ns_normalize_workspace_bytes() bytes (the first
+ * pass's partial sums), 4-byte aligned. */
+int64_t pratchya_ns_normalize_workspace_bytes(void);
+int pratchya_ns_normalize(const void* g, void* x, int64_t n, void* workspace, int64_t workspace_bytes,
+                          hipStream_t stream);
+
 /* One Newton-Schulz step on the bf16 MFMA kernel: C = 1.5 X - 0.5 bf16(A . B^T),
  * the product of pratchya_gemm_bf16_nt (_optimizer.py:20-22, rounded once to
  * bf16) combined with X in its epilogue exactly as pratchya_ns_combine

@@ -682,6 +682,24 @@ def transpose_b16(x: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def ns_normalize(g: torch.Tensor) -> torch.Tensor:
+    """``g / (||g||_F + 1e-7)`` for a bf16 ``g`` with the roundings of the
+    bf16 jnp expression (pratchya/_nnx_impl/_optimizer.py:17): the squares, their
+    sum, the square root, the sum with 1e-7 and every quotient rounded to bf16
+    (the sum accumulated in f32 in a fixed order).  Returns a new contiguous
+    tensor of g's shape."""
+    _require_gpu(g)
+    if g.dtype != torch.bfloat16:
+        raise ValueError("ns_normalize: g must be bfloat16")
+    gc = g.contiguous()
+    out = torch.empty_like(gc)
+    lib = _lib.load()
+    ws = torch.empty(int(lib.pratchya_ns_normalize_workspace_bytes()), dtype=torch.uint8, device=gc.device)
+    _lib.check(lib.pratchya_ns_normalize(_ptr(gc), _ptr(out), gc.numel(), _ptr(ws), ws.numel(), _stream(gc)),
+               "ns_normalize")
+    return out
+
+
 _GRAM_WS = {}
 
 

@@ -215,6 +215,84 @@ __global__ __launch_bounds__(256) void k_ns_combine(const void* x, const void* _
   store_chunk<BF16, CH, true>(out, base, v);        // the difference's rounding (RNE)
 }
 
+// Frobenius normalization of a bf16 Newton-Schulz input, X = G / (||G||_F +
+// 1e-7) (_optimizer.py:17), with the roundings of that bf16 expression: each
+// square rounded to bf16, their f32 sum rounded to bf16, the square root and
+// the sum with 1e-7 each rounded to bf16, every quotient rounded to bf16.  Two
+// passes with a fixed reduction order, so the result is the same on every
+// call: per-workgroup sums of the squares, then every workgroup of the second
+// pass sums those partials in one order before it scales its elements.
+constexpr int kNormBlocks = 1024;
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return u2f(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return u2f(w & 0xFFFF0000u); }
+__device__ __forceinline__ float bf16_rne(float v) { return bf16_lo(pack_bf16x2(v, 0.0f)); }
+
+// Sum of a wave's 64 values, the same tree on every call.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__global__ __launch_bounds__(256) void k_sumsq_b16(const uint16_t* __restrict__ x, int64_t n,
+                                                   float* __restrict__ part) {
+  const int64_t n8 = n / 8;
+  float s = 0.0f;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (int64_t)gridDim.x * 256) {
+    const uint4 v = *reinterpret_cast<const uint4*>(x + i * 8);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float lo = bf16_lo(w[k]), hi = bf16_hi(w[k]);
+      const uint32_t q = pack_bf16x2(lo * lo, hi * hi);   // each square rounded to bf16
+      s += bf16_lo(q);
+      s += bf16_hi(q);
+    }
+  }
+  if (blockIdx.x == 0)
+    for (int64_t i = n8 * 8 + threadIdx.x; i < n; i += 256) {
+      const float f = bf16_lo(x[i]);
+      s += bf16_rne(f * f);
+    }
+  __shared__ float ws[4];
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) part[blockIdx.x] = (ws[0] + ws[1]) + (ws[2] + ws[3]);
+}
+
+// (x and y may be the same array: each element is read and written by one
+// thread)
+__global__ __launch_bounds__(256) void k_ns_scale_b16(const uint16_t* x, int64_t n, const float* __restrict__ part,
+                                                      uint16_t* y) {
+  __shared__ float sden;
+  if (threadIdx.x < 64) {
+    float s = 0.0f;
+    for (int i = (int)threadIdx.x; i < kNormBlocks; i += 64) s += part[i];
+    s = wave_sum(s);
+    if (threadIdx.x == 0) {
+      const float total = bf16_rne(s);                 // the sum is a bf16 value
+      const float norm = bf16_rne(sqrtf(total));
+      sden = bf16_rne(norm + 1e-7f);
+    }
+  }
+  __syncthreads();
+  const float den = sden;
+  const int64_t n8 = n / 8;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (int64_t)gridDim.x * 256) {
+    const uint4 v = *reinterpret_cast<const uint4*>(x + i * 8);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = pack_bf16x2(bf16_lo(w[k]) / den, bf16_hi(w[k]) / den);
+    *reinterpret_cast<uint4*>(y + i * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  if (blockIdx.x == 0)
+    for (int64_t i = n8 * 8 + threadIdx.x; i < n; i += 256)
+      y[i] = (uint16_t)(pack_bf16x2(bf16_lo(x[i]) / den, 0.0f) & 0xFFFFu);
+}
+
 // jnp.sign: +-1 for nonzero, the argument itself for +-0 and NaN.
 __device__ __forceinline__ float sign_of(float x) { return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : x); }
 
@@ -359,6 +437,29 @@ extern "C" int pratchya_ns_combine(const void* x, const void* b, void* out, int6
     else hipLaunchKernelGGL((k_ns_combine<false, 1>), grid, dim3(256), 0, stream, x, b, out, chunks);
   }
   return check_launch("ns_combine");
+}
+
+extern "C" int64_t pratchya_ns_normalize_workspace_bytes(void) { return (int64_t)kNormBlocks * 4; }
+
+extern "C" int pratchya_ns_normalize(const void* g, void* x, int64_t n, void* workspace, int64_t workspace_bytes,
+                                     hipStream_t stream) {
+  if (n < 0) return pratchya_set_error(PRATCHYA_EINVAL, "ns_normalize: negative size");
+  if (n == 0) return PRATCHYA_OK;
+  if (!g || !x || !workspace) return pratchya_set_error(PRATCHYA_EINVAL, "ns_normalize: null buffer");
+  if (workspace_bytes < (int64_t)kNormBlocks * 4 || reinterpret_cast<uintptr_t>(workspace) % 4)
+    return pratchya_set_error(PRATCHYA_EINVAL, "ns_normalize: workspace of %lld bytes (need %d, 4-byte aligned)",
+                              (long long)workspace_bytes, kNormBlocks * 4);
+  if ((reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(x)) % 16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "ns_normalize: g and x must be 16-byte aligned");
+  float* part = static_cast<float*>(workspace);
+  hipLaunchKernelGGL(k_sumsq_b16, dim3(kNormBlocks), dim3(256), 0, stream, static_cast<const uint16_t*>(g), n, part);
+  int rc = check_launch("ns_normalize");
+  if (rc) return rc;
+  const int64_t chunks = n / 8;
+  const int64_t blocks = chunks / 256 + 1 < 4096 ? chunks / 256 + 1 : 4096;
+  hipLaunchKernelGGL(k_ns_scale_b16, dim3((unsigned)blocks), dim3(256), 0, stream, static_cast<const uint16_t*>(g),
+                     n, part, static_cast<uint16_t*>(x));
+  return check_launch("ns_normalize");
 }
 
 extern "C" int pratchya_apply_update(const void* u, int u_dtype, int use_sign, float scale, const void* p,

@@ -54,7 +54,8 @@ def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
     tall ``G``), then ``steps`` times ``X = 1.5 X - 0.5 (X X^T) X``, in ``G``'s
     dtype.  bf16 products run on the bf16 MFMA kernel (``pratchya_gemm_bf16_nt``;
     the Gram product on ``pratchya_gemm_bf16_gram`` where its side is a
-    multiple of 256), others on the BLAS library (f32 accumulation)."""
+    multiple of 256) and the normalization on ``pratchya_ns_normalize``, others
+    on the BLAS library (f32 accumulation) and torch."""
     m, n = G.shape
     transpose = m > n
     # A tall G is iterated untransposed: with Y = X^T = G / (||G|| + eps),
@@ -63,12 +64,15 @@ def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
     # transposing copies.  Y stays row-major, and the library reads the
     # transposed operand in place (2-D TN / NT GEMMs).
     X = G.contiguous()
-    X = X / (torch.sqrt(torch.sum(X * X)) + 1e-7)
-    fused = X.dtype in (torch.bfloat16, torch.float32)
     # bf16 leaves run both products on the bf16 MFMA kernel (NT form: rows of
-    # both operands K-contiguous), with one transposing copy per iteration;
-    # other dtypes and sizes use the BLAS library (f32 accumulation either way).
+    # both operands K-contiguous); other dtypes and sizes use the BLAS library
+    # (f32 accumulation either way).
     on_kernel = X.dtype == torch.bfloat16 and m % 64 == 0 and n % 64 == 0
+    if on_kernel:
+        X = K.ns_normalize(X)                    # one fused two-pass kernel pair
+    else:
+        X = X / (torch.sqrt(torch.sum(X * X)) + 1e-7)
+    fused = X.dtype in (torch.bfloat16, torch.float32)
     # the Gram product computes only its upper-triangle tiles (exactly
     # symmetric result) where its side is a multiple of 256; a tall iterate
     # is read K-major by it, with no transposed copy

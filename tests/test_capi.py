@@ -377,6 +377,22 @@ def test_gemm_bf16_gram_argument_codes_without_gpu():
     assert b"K-major" in lib.pratchya_last_error()
 
 
+def test_ns_normalize_argument_codes_without_gpu():
+    """The fused normalization rejects a null buffer, a short workspace and a
+    misaligned operand before any launch; n = 0 is a no-op."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)
+    ws_bytes = lib.pratchya_ns_normalize_workspace_bytes()
+    assert ws_bytes == 1024 * 4
+    assert lib.pratchya_ns_normalize(fake, fake, 0, None, 0, None) == 0
+    assert lib.pratchya_ns_normalize(fake, None, 64, fake, ws_bytes, None) == _lib.EINVAL
+    assert lib.pratchya_ns_normalize(fake, fake, 64, fake, ws_bytes - 4, None) == _lib.EINVAL
+    assert b"workspace" in lib.pratchya_last_error()
+    assert lib.pratchya_ns_normalize(ctypes.c_void_p((1 << 20) + 2), fake, 64, fake, ws_bytes, None) == _lib.EINVAL
+    assert b"aligned" in lib.pratchya_last_error()
+
+
 def test_gemm_bf16_ns_argument_codes_without_gpu():
     """The fused Newton-Schulz GEMM rejects an output overlapping X, a bad X
     and K not a multiple of 64 before any launch."""

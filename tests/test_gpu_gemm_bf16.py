@@ -107,6 +107,35 @@ def test_gemm_bf16_ns_rejects_output_over_x():
         K.gemm_bf16_nt_ns(a, b, x, out=x)
 
 
+@pytest.mark.parametrize("shape", [(16384, 4096), (4096, 4096), (999, 7), (8, 8)], ids=lambda s: "x".join(map(str, s)))
+def test_ns_normalize_roundings(shape):
+    """pratchya_ns_normalize against the bf16 expression's roundings computed
+    on the host: each square rounded to bf16, the sum rounded to bf16, the
+    square root and the sum with 1e-7 rounded to bf16, each quotient rounded
+    to bf16.  The kernel sums in f32 (a fixed order) and the host in f64: both
+    candidates for the rounded sum next to the f64 sum are accepted, and the
+    quotients must then match bit for bit (with a tail of n % 8 elements for
+    [999, 7])."""
+    K = _K()
+    g = _bf16(shape, 17, 1e-3)
+    got = K.ns_normalize(g)
+    torch.cuda.synchronize()
+    G = f32(g)
+    sq = O.bf16_round((G * G).astype(np.float32))
+    s = float(sq.astype(np.float64).sum())
+    wants = []
+    for t in {float(O.bf16_round(np.array([np.float32(s * f)], np.float32))[0]) for f in (1 - 1e-6, 1.0, 1 + 1e-6)}:
+        norm = O.bf16_round(np.sqrt(np.array([t], np.float32)))
+        den = O.bf16_round((norm + np.float32(1e-7)).astype(np.float32))
+        wants.append(O.bf16_round((G / den[0]).astype(np.float32)))
+    gb = f32(got)
+    assert any(np.array_equal(gb, w) for w in wants)
+    # and the same bits on a second call (fixed reduction order)
+    again = K.ns_normalize(g)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), again.view(torch.int16))
+
+
 @pytest.mark.parametrize("shape", [(1024, 2048), (2048, 1024)])
 def test_newton_schulz_kernel_against_oracle(shape):
     from pratchya_amd.optim import newton_schulz

@@ -348,9 +348,13 @@ int pratchya_ns_normalize(const void* g, void* x, int64_t n, void* workspace, in
  * difference), so that B never goes through HBM.  A, B, M, N, K as
  * pratchya_gemm_bf16_nt with a bf16 output; X: bf16 [M, N] (row stride ldx, a
  * multiple of 8; 16-byte aligned); C: bf16 [M, N] (ldc), not overlapping X
- * (PRATCHYA_EINVAL otherwise). */
-int pratchya_gemm_bf16_nt_ns(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
-                             int64_t K, const void* X, int64_t ldx, void* C, int64_t ldc, hipStream_t stream);
+ * (PRATCHYA_EINVAL otherwise).  b_kmajor: B is given in its K-major layout,
+ * the [K, N] matrix B^T (row stride ldb >= N; N and ldb multiples of 8),
+ * read through the LDS transposing loads: with B^T = X (the iterate of a
+ * wide or square leaf) the second product needs no transposed copy. */
+int pratchya_gemm_bf16_nt_ns(const void* A, int64_t lda, const void* B, int64_t ldb, int b_kmajor, int64_t M,
+                             int64_t N, int64_t K, const void* X, int64_t ldx, void* C, int64_t ldc,
+                             hipStream_t stream);
 
 /* Symmetric bf16 product C = A . A^T:     replaces the Gram product of newton_schulz
  *   C[m, n] = sum_k A[m, k] * A[n, k]      (pratchya/_nnx_impl/_optimizer.py:20-22,

@@ -735,25 +735,31 @@ def gemm_bf16_gram(a: torch.Tensor, k_major: bool = False) -> torch.Tensor:
     return out
 
 
-def gemm_bf16_nt_ns(a: torch.Tensor, b: torch.Tensor, x: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
+def gemm_bf16_nt_ns(a: torch.Tensor, b: torch.Tensor, x: torch.Tensor, out: torch.Tensor = None,
+                    b_k_major: bool = False) -> torch.Tensor:
     """One Newton-Schulz step ``1.5 x - 0.5 (a @ b^T)`` (pratchya/_nnx_impl/
     _optimizer.py:20-27) with the combination in the bf16 GEMM's epilogue: the
     same bits as ``ns_combine(x, gemm_bf16_nt(a, b))``.  ``a`` [M, K], ``b``
-    [N, K], ``x`` [M, N], all bf16; ``out`` must not overlap ``x``."""
+    [N, K] (with ``b_k_major``: ``b`` given as its [K, N] transpose, read
+    without a transposed copy), ``x`` [M, N], all bf16; ``out`` must not
+    overlap ``x``."""
     _require_gpu(a, b, x)
     if any(t.dtype != torch.bfloat16 or t.dim() != 2 for t in (a, b, x)):
         raise ValueError("gemm_bf16_nt_ns: a, b and x must be 2-D bfloat16")
-    if a.shape[1] != b.shape[1]:
-        raise ValueError(f"contraction mismatch: {a.shape[1]} vs {b.shape[1]}")
-    M, N, Kd = int(a.shape[0]), int(b.shape[0]), int(a.shape[1])
+    bk = int(b.shape[0]) if b_k_major else int(b.shape[1])
+    if a.shape[1] != bk:
+        raise ValueError(f"contraction mismatch: {a.shape[1]} vs {bk}")
+    M, N, Kd = int(a.shape[0]), int(b.shape[1] if b_k_major else b.shape[0]), int(a.shape[1])
     if tuple(x.shape) != (M, N):
         raise ValueError(f"gemm_bf16_nt_ns: x is {tuple(x.shape)}, the product is {(M, N)}")
-    ap, bp = _tile_readable(a.contiguous()), _tile_readable(b.contiguous())
+    ap = _tile_readable(a.contiguous())
+    bp = b.contiguous() if b_k_major else _tile_readable(b.contiguous())
     xc = x.contiguous()
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=ap.device)
-    _lib.check(_lib.load().pratchya_gemm_bf16_nt_ns(_ptr(ap), Kd, _ptr(bp), Kd, M, N, Kd, _ptr(xc), N, _ptr(out),
-                                                    out.stride(0), _stream(ap)), "gemm_bf16_ns")
+    _lib.check(_lib.load().pratchya_gemm_bf16_nt_ns(_ptr(ap), Kd, _ptr(bp), int(bp.stride(0)), 1 if b_k_major else 0,
+                                                    M, N, Kd, _ptr(xc), N, _ptr(out), out.stride(0), _stream(ap)),
+               "gemm_bf16_ns")
     return out
 
 

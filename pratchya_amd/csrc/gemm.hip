@@ -132,12 +132,14 @@ __device__ __forceinline__ v4i tr_pair(const uint8_t* p0, const uint8_t* p1) {
   return v4i{x.x, x.y, y.x, y.y};
 }
 // 32-byte fragment of 32 operand rows at `base` (the lane's row and K-row
-// offsets folded in): K rows +0..7 / +8..15 (lane halves) for the first MFMA,
-// +16..23 / +24..31 for the second.
+// offsets folded in: K rows +0 for lanes 0-31, +16 for lanes 32-63): K rows
+// +0..7 for the first MFMA, +8..15 for the second -- the K values the NT
+// fragment gives each lane (read_frag2), so K-major and K-contiguous operands
+// mix in one product and give the same sums.
 template <int OFF>
 __device__ __forceinline__ v8i read_frag_tn(const uint8_t* base) {
   const v4i lo = tr_pair(base + OFF, base + OFF + 4 * 512);
-  const v4i hi = tr_pair(base + OFF + 16 * 512, base + OFF + 20 * 512);
+  const v4i hi = tr_pair(base + OFF + 8 * 512, base + OFF + 12 * 512);
   return v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 }
 
@@ -254,10 +256,9 @@ struct DmaRows {
 // Row group i (8 rows) of a stage load whose row group 0 starts at byte
 // offset soff0 of the operand (row0 * ld + kt * BK) and LDS address lds0:
 // one add per row group, so that little scalar work sits between the MFMAs.
-template <bool TN = false>
-__device__ __forceinline__ void dma_rows_at(const DmaHalf& h, uint32_t soff0, uint8_t* lds0, int i) {
+__device__ __forceinline__ void dma_rows_at(const DmaHalf& h, uint32_t soff0, uint8_t* lds0, int i, bool tn) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(h.pay, (lds_void*)(lds0 + i * 1024), 16, h.off[i & 1],
-                                           soff0 + (uint32_t)i * ((TN ? 2u : 8u) * h.ld), 0, 0);
+                                           soff0 + (uint32_t)i * ((tn ? 2u : 8u) * h.ld), 0, 0);
 }
 
 // TN: K rows 2i, 2i + 1 of this wave's 16 for K block kt (64 K rows) of the
@@ -444,7 +445,7 @@ struct FqArgs {
   uint32_t* arrive;    // per strip: workgroups that published their maxima
   uint32_t* status;    // set to 1 if a strip's partners did not arrive in time
   int xcd;             // strip partners: workgroups b, b+8, b+16, b+24 (1) or b..b+3 (0)
-  // Newton-Schulz combination in the epilogue (FQ == 3): X [M, N] bf16 (row
+  // Newton-Schulz combination in the epilogue (FQ 3, 6): X [M, N] bf16 (row
   // stride ldx elements), read where the tile's product is stored
   const uint16_t* ns_x;
   int64_t ldx;
@@ -1011,10 +1012,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   int nk = K / BK;                        // K steps of the current unit
   const int T = tiles_m * tiles_n;
   // the Gram product (upper-triangle tiles by stream-K), with K-contiguous
-  // (FQ 4) or K-major (FQ 5, "TN") operand rows
+  // (FQ 4) or K-major (FQ 5, "TN") operand rows; the Newton-Schulz product
+  // with a K-major B (FQ 6)
   constexpr bool GRAM = FQ == 4 || FQ == 5;
-  constexpr bool TN = FQ == 5;
+  constexpr bool TN_A = FQ == 5, TN_B = FQ == 5 || FQ == 6;
   static_assert(!GRAM || BF, "the Gram product is a bf16 product");
+  const bool kmaj = (wave >> 2) == 0 ? TN_A : TN_B;   // K-major layout of this wave's stage loads
   const int l32 = lane & 31, lhi = lane >> 5;
 
   // this wave's half of every stage load: A rows (group 0) or B rows (group 1)
@@ -1029,7 +1032,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     h.ld = (uint32_t)(grp == 0 ? lda : ldb);
     h.s_k = (uint32_t)so.s_k;
     h.kg = (uint32_t)so.kg;
-    if constexpr (TN) dma_offsets_tn(grp == 0 ? lda : ldb, lane, h.off);
+    if (kmaj) dma_offsets_tn(grp == 0 ? lda : ldb, lane, h.off);
     else dma_offsets(grp == 0 ? lda : ldb, lane, h.off);
     h.krow0 = (uint32_t)(16 * w4);
     h.lds_pay = (grp == 0 ? 0 : OFF_B) + w4 * 8 * 1024;
@@ -1048,7 +1051,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   auto rows_of = [&](int tm_, int tn_, int kb_) {
     DmaRows r;
     // TN: the tile's first operand row (the wave's share is 16 K rows)
-    r.row0 = (uint32_t)((grp == 0 ? tile_base(tm_, M) : tile_base(tn_, N)) + (TN ? 0 : w4 * 64));
+    r.row0 = (uint32_t)((grp == 0 ? tile_base(tm_, M) : tile_base(tn_, N)) + (kmaj ? 0 : w4 * 64));
     r.e_word = (uint32_t)blk_index(so, (int64_t)r.row0 + lane, 0);
     r.kb = kb_;
     return r;
@@ -1056,7 +1059,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   // K block of a unit's first step: 0 except for the segments of a Gram range
   auto kb_of = [&](const DmaRows& r) { return GRAM ? r.kb : 0; };
   auto stage_rows = [&](const DmaRows& r, uint8_t* st, int kt, int i) {
-    if constexpr (TN) dma_rows_tn(h, r, st, kt, i);
+    if (kmaj) dma_rows_tn(h, r, st, kt, i);
     else dma_rows(h, r, st, kt, i);
   };
   const uint32_t skA = (uint32_t)sa.s_k, skB = (uint32_t)sb.s_k;
@@ -1071,14 +1074,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
       for (int hh = 0; hh < 2; ++hh) ch[ks][hh] = ((ks * 4 + lhi * 2 + hh) ^ sw) << 4;
   }
   // TN fragment reads (read_frag_tn): in 16-lane group g, lane j reads K row
-  // 8 (g / 2) + j / 4 at operand row 16 (g % 2) + 4 (j % 4) of a 32-row block;
-  // tn_kc is that K row's byte offset plus the row's chunk (c = 2 (g % 2) +
-  // (j % 4) / 2 inside the block's 4 chunks) and byte ((j % 2) 8) offsets, tn_s
-  // the row's swizzle (k mod 4 = j / 4)
+  // 16 (g / 2) + j / 4 at operand row 16 (g % 2) + 4 (j % 4) of a 32-row
+  // block; tn_kc is that K row's byte offset plus the row's chunk (c = 2 (g %
+  // 2) + (j % 4) / 2 inside the block's 4 chunks) and byte ((j % 2) 8)
+  // offsets, tn_s the row's swizzle (k mod 4 = j / 4)
   int tn_kc = 0, tn_s = 0;
-  if constexpr (TN) {
+  if constexpr (TN_A || TN_B) {
     const int g16 = lane >> 4, j16 = lane & 15;
-    tn_kc = (8 * (g16 >> 1) + (j16 >> 2)) * 512 + (2 * (g16 & 1) + ((j16 & 3) >> 1)) * 16 + (j16 & 1) * 8;
+    tn_kc = (16 * (g16 >> 1) + (j16 >> 2)) * 512 + (2 * (g16 & 1) + ((j16 & 3) >> 1)) * 16 + (j16 & 1) * 8;
     tn_s = j16 >> 2;
   }
 
@@ -1223,20 +1226,24 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
         const uint8_t* blo = st + (wn * 128 + l32) * BK + ch[ks][0];
         const uint8_t* bhi = st + (wn * 128 + l32) * BK + ch[ks][1];
         v8i fa[2], fb[4];
-        if constexpr (TN) {
-          // the lane's 32-row block R (A: 2 wm + mi, B: 4 wn + ni): K rows
-          // tn_k (+ 32 ks), operand rows from chunk (4 R + tn_c) ^ (4 tn_s)
-          const uint8_t* kb0 = st + tn_kc + ks * 32 * 512;
-          auto rb = [&](int R) { return kb0 + ((R ^ tn_s) << 6); };
+        // K-major operands: the lane's 32-row block R (A: 2 wm + mi, B: 4 wn
+        // + ni) at K rows tn_kc (+ 32 ks), operand rows from chunk
+        // (4 R + c) ^ (4 tn_s)
+        const uint8_t* kb0 = st + tn_kc + ks * 32 * 512;
+        auto rb = [&](int R) { return kb0 + ((R ^ tn_s) << 6); };
+        if constexpr (TN_A) {
           fa[0] = read_frag_tn<0>(rb(2 * wm));
           fa[1] = read_frag_tn<0>(rb(2 * wm + 1));
+        } else {
+          fa[0] = read_frag2<0>(alo, ahi);
+          fa[1] = read_frag2<32 * BK>(alo, ahi);
+        }
+        if constexpr (TN_B) {
           fb[0] = read_frag_tn<OFF_B>(rb(4 * wn));
           fb[1] = read_frag_tn<OFF_B>(rb(4 * wn + 1));
           fb[2] = read_frag_tn<OFF_B>(rb(4 * wn + 2));
           fb[3] = read_frag_tn<OFF_B>(rb(4 * wn + 3));
         } else {
-          fa[0] = read_frag2<0>(alo, ahi);
-          fa[1] = read_frag2<32 * BK>(alo, ahi);
           fb[0] = read_frag2<OFF_B>(blo, bhi);
           fb[1] = read_frag2<OFF_B + 32 * BK>(blo, bhi);
           fb[2] = read_frag2<OFF_B + 64 * BK>(blo, bhi);
@@ -1267,18 +1274,18 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
         const DmaRows& dr = to_next ? nxt : cur;
         const int lkt = to_next ? 0 : dkt;            // K block inside the tile loaded
         uint8_t* dst = lds + ((dkt + par) & 1) * STAGE_BYTES;
-        const uint32_t soff0 = TN ? dr.row0 * 2u + ((uint32_t)(lkt + kb_of(dr)) * 64u + h.krow0) * h.ld
+        const uint32_t soff0 = kmaj ? dr.row0 * 2u + ((uint32_t)(lkt + kb_of(dr)) * 64u + h.krow0) * h.ld
                                   : dr.row0 * h.ld + (uint32_t)(lkt + kb_of(dr)) * BK;
         uint8_t* const lds0 = dst + h.lds_pay;
         pin_frags(fa, fb);
         mfma_pinned<0, 0, BF>(acc, fa, fb, eA, eB);
-        if (dma_now) { dma_rows_at<TN>(h, soff0, lds0, 0); dma_rows_at<TN>(h, soff0, lds0, 1); }
+        if (dma_now) { dma_rows_at(h, soff0, lds0, 0, kmaj); dma_rows_at(h, soff0, lds0, 1, kmaj); }
         mfma_pinned<0, 1, BF>(acc, fa, fb, eA, eB);
-        if (dma_now) { dma_rows_at<TN>(h, soff0, lds0, 2); dma_rows_at<TN>(h, soff0, lds0, 3); }
+        if (dma_now) { dma_rows_at(h, soff0, lds0, 2, kmaj); dma_rows_at(h, soff0, lds0, 3, kmaj); }
         mfma_pinned<0, 2, BF>(acc, fa, fb, eA, eB);
-        if (dma_now) { dma_rows_at<TN>(h, soff0, lds0, 4); dma_rows_at<TN>(h, soff0, lds0, 5); }
+        if (dma_now) { dma_rows_at(h, soff0, lds0, 4, kmaj); dma_rows_at(h, soff0, lds0, 5, kmaj); }
         mfma_pinned<0, 3, BF>(acc, fa, fb, eA, eB);
-        if (dma_now) { dma_rows_at<TN>(h, soff0, lds0, 6); dma_rows_at<TN>(h, soff0, lds0, 7); }
+        if (dma_now) { dma_rows_at(h, soff0, lds0, 6, kmaj); dma_rows_at(h, soff0, lds0, 7, kmaj); }
         mfma_pinned<1, 0, BF>(acc, fa, fb, eA, eB);
         if (dma_now && !BF) {
           dma_scales(h, dr, dst, lkt);
@@ -1332,7 +1339,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
         store_tile_gram(acc, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc, m0 + wm * 64,
                         n0 + wn * 128, tm != tn);
       }
-    } else if constexpr (FQ == 3) {
+    } else if constexpr (FQ == 3 || FQ == 6) {
       static_assert(BF && OUT_BF16, "the Newton-Schulz epilogue combines bf16 products");
       store_tile_ns(acc, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc, fq.ns_x, fq.ldx,
                     m0 + wm * 64, n0 + wn * 128, M, N);
@@ -1727,13 +1734,24 @@ extern "C" int pratchya_gemm_bf16_nt(const void* A, int64_t lda, const void* B, 
   return launch_status("gemm_bf16");
 }
 
-extern "C" int pratchya_gemm_bf16_nt_ns(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
-                                        int64_t N, int64_t K, const void* X, int64_t ldx, void* C, int64_t ldc,
-                                        hipStream_t stream) {
+extern "C" int pratchya_gemm_bf16_nt_ns(const void* A, int64_t lda, const void* B, int64_t ldb, int b_kmajor,
+                                        int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx, void* C,
+                                        int64_t ldc, hipStream_t stream) {
   GemmPlan P;
   bool empty;
-  int rc = bf16_plan("gemm_bf16_ns", A, lda, B, ldb, M, N, K, C, ldc, true, &P, &empty);
+  // a K-major B ([K, N], row stride ldb >= N) is validated as the plan of its
+  // [N, K] view, with the operand size of its own layout
+  int rc = bf16_plan("gemm_bf16_ns", A, lda, B, b_kmajor ? K : ldb, M, N, K, C, ldc, true, &P, &empty);
   if (rc || empty) return rc;
+  if (b_kmajor) {
+    if (ldb < N || ldb % 8 || N % 8)
+      return pratchya_set_error(PRATCHYA_EINVAL, "gemm_bf16_ns: a K-major B needs N and a row stride of at "
+                                "least N that are multiples of 8");
+    const int64_t bytes = ((K - 1) * ldb + N) * 2;
+    if (bytes > (int64_t)INT32_MAX)
+      return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_bf16_ns: operand beyond 2 GiB");
+    P.b_bytes = bytes;
+  }
   if (!X || ldx < N || ldx % 8 || reinterpret_cast<uintptr_t>(X) % 16)
     return pratchya_set_error(PRATCHYA_EINVAL, "gemm_bf16_ns: X must be a 16-byte aligned [M, N] bf16 matrix "
                               "with a row stride that is a multiple of 8");
@@ -1746,7 +1764,8 @@ extern "C" int pratchya_gemm_bf16_nt_ns(const void* A, int64_t lda, const void* 
   FqArgs fq{};
   fq.ns_x = static_cast<const uint16_t*>(X);
   fq.ldx = ldx;
-  bf16_launch<true, 3>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+  if (b_kmajor) bf16_launch<true, 6>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+  else bf16_launch<true, 3>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
   return launch_status("gemm_bf16_ns");
 }
 

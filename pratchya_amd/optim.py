@@ -91,7 +91,14 @@ def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
             continue
         elif on_kernel:
             A = K.gemm_bf16_gram(X) if gram_ok else K.gemm_bf16_nt(X, X)   # X X^T [m, m]
-            X = K.gemm_bf16_nt_ns(A, K.transpose_b16(X), X)   # 1.5 X - 0.5 A X
+            # 1.5 X - 0.5 A X: a wide X is read K-major (no transposed copy);
+            # for a square one the copy is cheaper than the K-major read
+            # (measured: [4096, 4096] 1.08 vs 1.13 ms, [4096, 16384] 3.83 vs
+            # 3.74 ms for 5 iterations)
+            if n > m:
+                X = K.gemm_bf16_nt_ns(A, X, X, b_k_major=True)
+            else:
+                X = K.gemm_bf16_nt_ns(A, K.transpose_b16(X), X)
             continue
         elif transpose:
             A = X.T @ X

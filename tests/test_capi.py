@@ -400,11 +400,15 @@ def test_gemm_bf16_ns_argument_codes_without_gpu():
     lib = _lib.load()
     fake = ctypes.c_void_p(1 << 20)
     other = ctypes.c_void_p(1 << 30)
-    assert lib.pratchya_gemm_bf16_nt_ns(fake, 128, fake, 128, 256, 256, 128, other, 256, other, 256,
+    assert lib.pratchya_gemm_bf16_nt_ns(fake, 128, fake, 128, 0, 256, 256, 128, other, 256, other, 256,
                                         None) == _lib.EINVAL
     assert b"overlaps" in lib.pratchya_last_error()
-    assert lib.pratchya_gemm_bf16_nt_ns(fake, 128, fake, 128, 256, 256, 128, None, 256, other, 256,
+    assert lib.pratchya_gemm_bf16_nt_ns(fake, 128, fake, 128, 0, 256, 256, 128, None, 256, other, 256,
                                         None) == _lib.EINVAL
-    assert lib.pratchya_gemm_bf16_nt_ns(fake, 96, fake, 96, 256, 256, 96, fake, 256, other, 256,
+    assert lib.pratchya_gemm_bf16_nt_ns(fake, 96, fake, 96, 0, 256, 256, 96, fake, 256, other, 256,
                                         None) == _lib.EUNSUPPORTED
-    assert lib.pratchya_gemm_bf16_nt_ns(fake, 128, fake, 128, 0, 256, 128, fake, 256, other, 256, None) == 0
+    assert lib.pratchya_gemm_bf16_nt_ns(fake, 128, fake, 128, 0, 0, 256, 128, fake, 256, other, 256, None) == 0
+    # a K-major B with a row stride below N
+    assert lib.pratchya_gemm_bf16_nt_ns(fake, 128, fake, 128, 1, 256, 256, 128, fake, 256, other, 256,
+                                        None) == _lib.EINVAL
+    assert b"K-major" in lib.pratchya_last_error()

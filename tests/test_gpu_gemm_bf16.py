@@ -88,7 +88,8 @@ def test_transpose_b16(shape):
 def test_gemm_bf16_ns_equals_product_then_combine(shape):
     """pratchya_gemm_bf16_nt_ns: the product's epilogue forms 1.5 X - 0.5 B
     with the same bits as pratchya_ns_combine applied to the bf16 product,
-    including edge tiles and short operands; run twice into the same output."""
+    including edge tiles and short operands; run twice into the same output;
+    and with B given K-major."""
     M, N, Kd = shape
     K = _K()
     a, b, x = _bf16((M, Kd), 31, 0.05), _bf16((N, Kd), 32, 0.05), _bf16((M, N), 33)
@@ -98,6 +99,11 @@ def test_gemm_bf16_ns_equals_product_then_combine(shape):
         got = K.gemm_bf16_nt_ns(a, b, x, out=out)
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    # B given K-major ([K, N]) and read through the LDS transposing loads: the
+    # same K values per MFMA lane, so the same bits
+    got_k = K.gemm_bf16_nt_ns(a, b.T.contiguous(), x, b_k_major=True)
+    torch.cuda.synchronize()
+    assert torch.equal(got_k.view(torch.int16), want.view(torch.int16))
 
 
 def test_gemm_bf16_ns_rejects_output_over_x():

@@ -318,6 +318,21 @@ int pratchya_gemm_bs_nt_fq(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, 
                            uint8_t* c_sc8, float* c_sc32, void* workspace, int64_t workspace_bytes,
                            hipStream_t stream);
 
+/* pratchya_gemm_bs_nt with both operands K-major:  the weight gradient
+ * (Q:621-622, matmul_impl's backward, dW = x^T . dY over the tokens) reading
+ * x and dY quantized (128, 1) in their own [T, C] layout, through the LDS
+ * transposing loads, instead of transposed payloads.  A: e4m3fn [K, M] (row
+ * stride lda >= M), B: [K, N] (ldb >= N); M, N, lda, ldb multiples of 16;
+ * scales, K and C as pratchya_gemm_bs_nt (the scale layouts address
+ * (row, K block) as for the [M, K] / [N, K] views).  Each MFMA lane sums the
+ * same K values as with the K-contiguous operands, so the output is
+ * bit-identical to pratchya_gemm_bs_nt on the transposed payloads. */
+int pratchya_gemm_bs_kmajor(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, const float* a_sc32,
+                            int64_t a_rdiv, int64_t a_sr, int64_t a_sk, int64_t a_kg, const uint8_t* B,
+                            int64_t ldb, const uint8_t* b_sc8, const float* b_sc32, int64_t b_rdiv,
+                            int64_t b_sr, int64_t b_sk, int64_t b_kg, int64_t M, int64_t N, int64_t K,
+                            void* C, int64_t ldc, int c_dtype, hipStream_t stream);
+
 /* bf16 GEMM, "NT" form:                  replaces the bf16 dots of newton_schulz
  *   C[m, n] = sum_k A[m, k] * B[n, k]     (pratchya/_nnx_impl/_optimizer.py:20-22,
  * A @ A.T and (A @ A.T) @ A in the leaf's dtype; jnp's bf16 dot accumulates in f32)

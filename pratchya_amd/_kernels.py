@@ -471,21 +471,22 @@ class Operand:
     block // kg.
     """
 
-    __slots__ = ("payload", "sc8", "sc32", "desc")
+    __slots__ = ("payload", "sc8", "sc32", "desc", "k_major")
 
-    def __init__(self, payload, sc8, sc32, desc):
+    def __init__(self, payload, sc8, sc32, desc, k_major=False):
         self.payload = payload
         self.sc8 = sc8
         self.sc32 = sc32
         self.desc = tuple(int(v) for v in desc)
+        self.k_major = bool(k_major)      # payload [K, rows] instead of [rows, K]
 
     @property
     def rows(self) -> int:
-        return int(self.payload.shape[0])
+        return int(self.payload.shape[1 if self.k_major else 0])
 
     @property
     def k(self) -> int:
-        return int(self.payload.shape[1])
+        return int(self.payload.shape[0 if self.k_major else 1])
 
 
 def operand_rows(x8: torch.Tensor, sc8: torch.Tensor, sc32: torch.Tensor, tgrid) -> Operand:
@@ -521,6 +522,16 @@ def operand_t128(xt8: torch.Tensor, sc8: torch.Tensor, sc32: torch.Tensor) -> Op
         raise ValueError("operand_t128 needs the payload of a 2-D tensor")
     C, T = xt8.shape
     return Operand(xt8, sc8, sc32, (1, 1, C, 8))
+
+
+def operand_k128(x8: torch.Tensor, sc8: torch.Tensor, sc32: torch.Tensor) -> Operand:
+    """Operand from a 2-D [T, C] tensor quantized with tgrid (128, 1) in its own
+    layout (``quantize(x, (128, 1))``): rows are the C channels, the
+    contraction runs over the T tokens, and the payload is read K-major."""
+    if x8.dim() != 2:
+        raise ValueError("operand_k128 needs the payload of a 2-D tensor")
+    T, C = x8.shape
+    return Operand(x8, sc8, sc32, (1, 1, C, 8), k_major=True)
 
 
 def transpose_u8(x8: torch.Tensor) -> torch.Tensor:
@@ -575,12 +586,23 @@ def gemm_nt(a: Operand, b: Operand, out_dtype: torch.dtype = torch.bfloat16,
     if a.k != b.k:
         raise ValueError(f"contraction mismatch: {a.k} vs {b.k}")
     M, N, K = a.rows, b.rows, a.k
-    ap, bp = _tile_readable(_u8(a.payload).contiguous()), _tile_readable(_u8(b.payload).contiguous())
+    if a.k_major or b.k_major:
+        if not (a.k_major and b.k_major):
+            raise PratchyaUnsupported("gemm_nt: K-major FP8 operands are supported as a pair")
+        ap, bp = _u8(a.payload).contiguous(), _u8(b.payload).contiguous()
+    else:
+        ap, bp = _tile_readable(_u8(a.payload).contiguous()), _tile_readable(_u8(b.payload).contiguous())
     as8, bs8 = _word_readable(_u8(a.sc8).contiguous()), _word_readable(_u8(b.sc8).contiguous())
     as32, bs32 = a.sc32.contiguous().float(), b.sc32.contiguous().float()
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=ap.device)
     lib = _lib.load()
+    if a.k_major:
+        _lib.check(lib.pratchya_gemm_bs_kmajor(_ptr(ap), M, _ptr(as8), _ptr(as32), *a.desc,
+                                               _ptr(bp), N, _ptr(bs8), _ptr(bs32), *b.desc,
+                                               M, N, K, _ptr(out), out.stride(0), _dtype_code(out.dtype),
+                                               _stream(ap)), "gemm_kmajor")
+        return out
     _lib.check(lib.pratchya_gemm_bs_nt(_ptr(ap), K, _ptr(as8), _ptr(as32), *a.desc,
                                        _ptr(bp), K, _ptr(bs8), _ptr(bs32), *b.desc,
                                        M, N, K, _ptr(out), out.stride(0), _dtype_code(out.dtype),

@@ -73,6 +73,9 @@ SIGNATURES = {
                                         _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_int, _c_int, _c_p, _c_p,
                                         _c_p, _c_i64, _c_p]),
     "pratchya_gemm_bs_nt_fq_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "pratchya_gemm_bs_kmajor": (_c_int, [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
+                                         _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
+                                         _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_int, _c_p]),
     "pratchya_gemm_bf16_nt": (_c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64,
                                        _c_int, _c_p]),
     "pratchya_gemm_bf16_nt_ns": (_c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_int, _c_i64, _c_i64, _c_i64, _c_p,

@@ -44,6 +44,7 @@
 #include <stdint.h>
 
 #include <numeric>
+#include <type_traits>
 
 #include "pratchya_fp8.h"
 #include "quant_device.h"
@@ -143,6 +144,23 @@ __device__ __forceinline__ v8i read_frag_tn(const uint8_t* base) {
   return v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 }
 
+// FP8 K-major operand: the stage holds 128 K rows of 256 operand bytes, 16-byte
+// chunks XOR-swizzled by 2 * (k mod 8).  ds_read_b64_tr_b8: in a 16-lane
+// group, lane i holds byte i mod 8 of the 8-byte reads of lanes i / 8 + 2 e
+// (e = 0..7); with lane j reading K row k0 + j / 2 at operand row m0 + 8 (j mod
+// 2), lane i receives operand row m0 + i and K rows k0 .. k0 + 7.  Four reads
+// (K rows +0, +8, +16, +24) give the 32 consecutive K values of an FP8 MFMA
+// lane, the K-contiguous fragment's (read_frag2) values.
+typedef __attribute__((address_space(3))) v2i lds_v2i;
+template <int OFF>
+__device__ __forceinline__ v8i read_frag_tn8(const uint8_t* base) {
+  const v2i a = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(base + OFF));
+  const v2i b = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(base + OFF + 8 * 256));
+  const v2i c = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(base + OFF + 16 * 256));
+  const v2i d = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(base + OFF + 24 * 256));
+  return v8i{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
+
 // One 32x32x64 MFMA of output tile (MI, NI): a-operand = B rows (e8m0 byte NI
 // of eB), b-operand = A rows (byte MI of eA); op_sel picks the byte.  BF: the
 // operands are bf16 (a 32-byte fragment is 16 K values), two 32x32x16 bf16
@@ -217,15 +235,23 @@ __device__ __forceinline__ void dma_offsets(int64_t ld, int lane, uint32_t (&off
   }
 }
 
-// K-major operand (TN): instruction i of a wave loads K rows 2i, 2i + 1 of
-// its 16 (512 bytes each): lane -> K row (lane >> 5), LDS chunk lane & 31,
-// which holds the operand's chunk (lane & 31) ^ 4 (k mod 4) of that row.
+// K-major operand: instruction i of a wave loads 1 KB of consecutive K rows
+// (bf16: K rows 2i, 2i + 1 of its 16, 512 bytes each; fp8: K rows 4i .. 4i + 3
+// of its 32, 256 bytes each): lane -> K row, LDS chunk c of that row, which
+// holds the operand's chunk c ^ 4 (k mod 4) (bf16) or c ^ 2 (k mod 8) (fp8).
+template <bool BF>
 __device__ __forceinline__ void dma_offsets_tn(int64_t ld, int lane, uint32_t (&off)[2]) {
 #pragma unroll
   for (int par = 0; par < 2; ++par) {
-    const int rp = lane >> 5, c = lane & 31;
-    const int sw = ((2 * par + rp) & 3) << 2;
-    off[par] = (uint32_t)(rp * ld + ((c ^ sw) << 4));
+    if constexpr (BF) {
+      const int rp = lane >> 5, c = lane & 31;
+      const int sw = ((2 * par + rp) & 3) << 2;
+      off[par] = (uint32_t)(rp * ld + ((c ^ sw) << 4));
+    } else {
+      const int rp = lane >> 4, c = lane & 15;
+      const int sw = ((4 * par + rp) & 7) << 1;
+      off[par] = (uint32_t)(rp * ld + ((c ^ sw) << 4));
+    }
   }
 }
 
@@ -256,16 +282,19 @@ struct DmaRows {
 // Row group i (8 rows) of a stage load whose row group 0 starts at byte
 // offset soff0 of the operand (row0 * ld + kt * BK) and LDS address lds0:
 // one add per row group, so that little scalar work sits between the MFMAs.
-__device__ __forceinline__ void dma_rows_at(const DmaHalf& h, uint32_t soff0, uint8_t* lds0, int i, bool tn) {
+// (rows: operand rows per instruction, 8, or K rows of a K-major operand)
+__device__ __forceinline__ void dma_rows_at(const DmaHalf& h, uint32_t soff0, uint8_t* lds0, int i, uint32_t rows) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(h.pay, (lds_void*)(lds0 + i * 1024), 16, h.off[i & 1],
-                                           soff0 + (uint32_t)i * ((tn ? 2u : 8u) * h.ld), 0, 0);
+                                           soff0 + (uint32_t)i * (rows * h.ld), 0, 0);
 }
 
-// TN: K rows 2i, 2i + 1 of this wave's 16 for K block kt (64 K rows) of the
-// operand rows starting at r.row0, into stage st.
+// K-major: DMA instruction i of this wave's K rows for K block kt (64 bf16 /
+// 128 fp8 K rows) of the operand rows starting at r.row0, into stage st.
+template <bool BF>
 __device__ __forceinline__ void dma_rows_tn(const DmaHalf& h, const DmaRows& r, uint8_t* st, int kt, int i) {
+  constexpr uint32_t ESZ = BF ? 2u : 1u, KROWS = BK / ESZ, RPI = 1024 / (256 * ESZ);
   __builtin_amdgcn_raw_ptr_buffer_load_lds(h.pay, (lds_void*)(st + h.lds_pay + i * 1024), 16, h.off[i & 1],
-                                           r.row0 * 2u + ((uint32_t)kt * 64u + h.krow0 + (uint32_t)(2 * i)) * h.ld,
+                                           r.row0 * ESZ + ((uint32_t)kt * KROWS + h.krow0 + RPI * (uint32_t)i) * h.ld,
                                            0, 0);
 }
 
@@ -445,7 +474,7 @@ struct FqArgs {
   uint32_t* arrive;    // per strip: workgroups that published their maxima
   uint32_t* status;    // set to 1 if a strip's partners did not arrive in time
   int xcd;             // strip partners: workgroups b, b+8, b+16, b+24 (1) or b..b+3 (0)
-  // Newton-Schulz combination in the epilogue (FQ 3, 6): X [M, N] bf16 (row
+  // Newton-Schulz combination in the epilogue (FQ 3): X [M, N] bf16 (row
   // stride ldx elements), read where the tile's product is stored
   const uint16_t* ns_x;
   int64_t ldx;
@@ -994,7 +1023,7 @@ __device__ __forceinline__ void store_tile_ns(const v16f (&acc)[2][4], uint8_t* 
   }
 }
 
-template <bool OUT_BF16, int BG, int FQ, bool BF = false>
+template <bool OUT_BF16, int BG, int FQ, bool BF = false, int KM = 0>
 __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     Scales sa, Scales sb, void* __restrict__ C, int64_t ldc, int K, int span, int tiles_m,
@@ -1011,11 +1040,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   const int wm = wave & 3, wn = grp;      // 64-row band wm, 128-column half wn
   int nk = K / BK;                        // K steps of the current unit
   const int T = tiles_m * tiles_n;
-  // the Gram product (upper-triangle tiles by stream-K), with K-contiguous
-  // (FQ 4) or K-major (FQ 5, "TN") operand rows; the Newton-Schulz product
-  // with a K-major B (FQ 6)
-  constexpr bool GRAM = FQ == 4 || FQ == 5;
-  constexpr bool TN_A = FQ == 5, TN_B = FQ == 5 || FQ == 6;
+  // the Gram product (upper-triangle tiles by stream-K, FQ 4); operands
+  // given K-major (KM bit 0: A, bit 1: B; read through the LDS transposing
+  // loads) or K-contiguous
+  constexpr bool GRAM = FQ == 4;
+  constexpr bool TN_A = (KM & 1) != 0, TN_B = (KM & 2) != 0;
   static_assert(!GRAM || BF, "the Gram product is a bf16 product");
   const bool kmaj = (wave >> 2) == 0 ? TN_A : TN_B;   // K-major layout of this wave's stage loads
   const int l32 = lane & 31, lhi = lane >> 5;
@@ -1032,9 +1061,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     h.ld = (uint32_t)(grp == 0 ? lda : ldb);
     h.s_k = (uint32_t)so.s_k;
     h.kg = (uint32_t)so.kg;
-    if (kmaj) dma_offsets_tn(grp == 0 ? lda : ldb, lane, h.off);
+    if (kmaj) dma_offsets_tn<BF>(grp == 0 ? lda : ldb, lane, h.off);
     else dma_offsets(grp == 0 ? lda : ldb, lane, h.off);
-    h.krow0 = (uint32_t)(16 * w4);
+    h.krow0 = (uint32_t)(w4 * (BF ? 16 : 32));   // the wave's K rows of a K-major stage
     h.lds_pay = (grp == 0 ? 0 : OFF_B) + w4 * 8 * 1024;
     h.lds_e = (grp == 0 ? OFF_EA : OFF_EB) + w4 * 256;
     h.lds_r = grp == 0 ? OFF_RA : OFF_RB;
@@ -1050,16 +1079,18 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   }
   auto rows_of = [&](int tm_, int tn_, int kb_) {
     DmaRows r;
-    // TN: the tile's first operand row (the wave's share is 16 K rows)
-    r.row0 = (uint32_t)((grp == 0 ? tile_base(tm_, M) : tile_base(tn_, N)) + (kmaj ? 0 : w4 * 64));
-    r.e_word = (uint32_t)blk_index(so, (int64_t)r.row0 + lane, 0);
+    // K-major: the tile's first operand row (the wave loads K rows of all
+    // 256); the e8m0 words and group maxima stay the wave's 64 operand rows
+    const int rb0 = grp == 0 ? tile_base(tm_, M) : tile_base(tn_, N);
+    r.row0 = (uint32_t)(rb0 + (kmaj ? 0 : w4 * 64));
+    r.e_word = (uint32_t)blk_index(so, (int64_t)rb0 + w4 * 64 + lane, 0);
     r.kb = kb_;
     return r;
   };
   // K block of a unit's first step: 0 except for the segments of a Gram range
   auto kb_of = [&](const DmaRows& r) { return GRAM ? r.kb : 0; };
   auto stage_rows = [&](const DmaRows& r, uint8_t* st, int kt, int i) {
-    if (kmaj) dma_rows_tn(h, r, st, kt, i);
+    if (kmaj) dma_rows_tn<BF>(h, r, st, kt, i);
     else dma_rows(h, r, st, kt, i);
   };
   const uint32_t skA = (uint32_t)sa.s_k, skB = (uint32_t)sb.s_k;
@@ -1078,11 +1109,18 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   // block; tn_kc is that K row's byte offset plus the row's chunk (c = 2 (g %
   // 2) + (j % 4) / 2 inside the block's 4 chunks) and byte ((j % 2) 8)
   // offsets, tn_s the row's swizzle (k mod 4 = j / 4)
+  // (fp8: lane j reads K row 32 (g / 2) + j / 2 at operand row 16 (g % 2) +
+  // 8 (j % 2), swizzle k mod 8 = j / 2)
   int tn_kc = 0, tn_s = 0;
   if constexpr (TN_A || TN_B) {
     const int g16 = lane >> 4, j16 = lane & 15;
-    tn_kc = (16 * (g16 >> 1) + (j16 >> 2)) * 512 + (2 * (g16 & 1) + ((j16 & 3) >> 1)) * 16 + (j16 & 1) * 8;
-    tn_s = j16 >> 2;
+    if constexpr (BF) {
+      tn_kc = (16 * (g16 >> 1) + (j16 >> 2)) * 512 + (2 * (g16 & 1) + ((j16 & 3) >> 1)) * 16 + (j16 & 1) * 8;
+      tn_s = j16 >> 2;
+    } else {
+      tn_kc = (32 * (g16 >> 1) + (j16 >> 1)) * 256 + (g16 & 1) * 16 + (j16 & 1) * 8;
+      tn_s = j16 >> 1;
+    }
   }
 
   // Persistent: workgroup b computes tiles b, b + G, b + 2G, ... (G = grid
@@ -1092,7 +1130,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   // steps into the stage buffer they no longer read, and its latency is
   // covered by the epilogue, which stages the output in the other buffer.
   //
-  // Gram (FQ 4, 5): the units are the segments of this workgroup's range of
+  // Gram (FQ 4): the units are the segments of this workgroup's range of
   // the stream-K step sequence (see FqArgs): a unit is the part of one tile's
   // K steps inside the range, at most two per range.
   int t = blockIdx.x;
@@ -1227,22 +1265,28 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
         const uint8_t* bhi = st + (wn * 128 + l32) * BK + ch[ks][1];
         v8i fa[2], fb[4];
         // K-major operands: the lane's 32-row block R (A: 2 wm + mi, B: 4 wn
-        // + ni) at K rows tn_kc (+ 32 ks), operand rows from chunk
-        // (4 R + c) ^ (4 tn_s)
-        const uint8_t* kb0 = st + tn_kc + ks * 32 * 512;
-        auto rb = [&](int R) { return kb0 + ((R ^ tn_s) << 6); };
+        // + ni) at K rows tn_kc (+ the K half ks), operand rows from chunk
+        // (4 R + c) ^ (4 tn_s) (bf16) or (2 R + c) ^ (2 tn_s) (fp8)
+        const uint8_t* kb0 = st + tn_kc + ks * (BF ? 32 * 512 : 64 * 256);
+        auto rb = [&](int R) { return kb0 + ((R ^ tn_s) << (BF ? 6 : 5)); };
+        auto frag_tn = [&](const uint8_t* base, auto off) {
+          if constexpr (BF) return read_frag_tn<decltype(off)::value>(base);
+          else return read_frag_tn8<decltype(off)::value>(base);
+        };
+        using Z = std::integral_constant<int, 0>;
+        using OB = std::integral_constant<int, OFF_B>;
         if constexpr (TN_A) {
-          fa[0] = read_frag_tn<0>(rb(2 * wm));
-          fa[1] = read_frag_tn<0>(rb(2 * wm + 1));
+          fa[0] = frag_tn(rb(2 * wm), Z{});
+          fa[1] = frag_tn(rb(2 * wm + 1), Z{});
         } else {
           fa[0] = read_frag2<0>(alo, ahi);
           fa[1] = read_frag2<32 * BK>(alo, ahi);
         }
         if constexpr (TN_B) {
-          fb[0] = read_frag_tn<OFF_B>(rb(4 * wn));
-          fb[1] = read_frag_tn<OFF_B>(rb(4 * wn + 1));
-          fb[2] = read_frag_tn<OFF_B>(rb(4 * wn + 2));
-          fb[3] = read_frag_tn<OFF_B>(rb(4 * wn + 3));
+          fb[0] = frag_tn(rb(4 * wn), OB{});
+          fb[1] = frag_tn(rb(4 * wn + 1), OB{});
+          fb[2] = frag_tn(rb(4 * wn + 2), OB{});
+          fb[3] = frag_tn(rb(4 * wn + 3), OB{});
         } else {
           fb[0] = read_frag2<OFF_B>(blo, bhi);
           fb[1] = read_frag2<OFF_B + 32 * BK>(blo, bhi);
@@ -1274,18 +1318,20 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
         const DmaRows& dr = to_next ? nxt : cur;
         const int lkt = to_next ? 0 : dkt;            // K block inside the tile loaded
         uint8_t* dst = lds + ((dkt + par) & 1) * STAGE_BYTES;
-        const uint32_t soff0 = kmaj ? dr.row0 * 2u + ((uint32_t)(lkt + kb_of(dr)) * 64u + h.krow0) * h.ld
-                                  : dr.row0 * h.ld + (uint32_t)(lkt + kb_of(dr)) * BK;
+        constexpr uint32_t KESZ = BF ? 2u : 1u, KROWS = BK / KESZ, KRPI = 1024 / (256 * KESZ);
+        const uint32_t soff0 = kmaj ? dr.row0 * KESZ + ((uint32_t)(lkt + kb_of(dr)) * KROWS + h.krow0) * h.ld
+                                    : dr.row0 * h.ld + (uint32_t)(lkt + kb_of(dr)) * BK;
+        const uint32_t drows = kmaj ? KRPI : 8u;
         uint8_t* const lds0 = dst + h.lds_pay;
         pin_frags(fa, fb);
         mfma_pinned<0, 0, BF>(acc, fa, fb, eA, eB);
-        if (dma_now) { dma_rows_at(h, soff0, lds0, 0, kmaj); dma_rows_at(h, soff0, lds0, 1, kmaj); }
+        if (dma_now) { dma_rows_at(h, soff0, lds0, 0, drows); dma_rows_at(h, soff0, lds0, 1, drows); }
         mfma_pinned<0, 1, BF>(acc, fa, fb, eA, eB);
-        if (dma_now) { dma_rows_at(h, soff0, lds0, 2, kmaj); dma_rows_at(h, soff0, lds0, 3, kmaj); }
+        if (dma_now) { dma_rows_at(h, soff0, lds0, 2, drows); dma_rows_at(h, soff0, lds0, 3, drows); }
         mfma_pinned<0, 2, BF>(acc, fa, fb, eA, eB);
-        if (dma_now) { dma_rows_at(h, soff0, lds0, 4, kmaj); dma_rows_at(h, soff0, lds0, 5, kmaj); }
+        if (dma_now) { dma_rows_at(h, soff0, lds0, 4, drows); dma_rows_at(h, soff0, lds0, 5, drows); }
         mfma_pinned<0, 3, BF>(acc, fa, fb, eA, eB);
-        if (dma_now) { dma_rows_at(h, soff0, lds0, 6, kmaj); dma_rows_at(h, soff0, lds0, 7, kmaj); }
+        if (dma_now) { dma_rows_at(h, soff0, lds0, 6, drows); dma_rows_at(h, soff0, lds0, 7, drows); }
         mfma_pinned<1, 0, BF>(acc, fa, fb, eA, eB);
         if (dma_now && !BF) {
           dma_scales(h, dr, dst, lkt);
@@ -1339,7 +1385,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
         store_tile_gram(acc, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc, m0 + wm * 64,
                         n0 + wn * 128, tm != tn);
       }
-    } else if constexpr (FQ == 3 || FQ == 6) {
+    } else if constexpr (FQ == 3) {
       static_assert(BF && OUT_BF16, "the Newton-Schulz epilogue combines bf16 products");
       store_tile_ns(acc, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc, fq.ns_x, fq.ldx,
                     m0 + wm * 64, n0 + wn * 128, M, N);
@@ -1555,10 +1601,10 @@ int gemm_plan(const char* who, const uint8_t* A, int64_t lda, const uint8_t* a_s
   return PRATCHYA_OK;
 }
 
-template <bool BF, int BG, int FQ>
+template <bool BF, int BG, int FQ, int KM = 0>
 void gemm_launch(const GemmPlan& P, const uint8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, void* C,
                  int64_t ldc, int64_t M, int64_t N, int64_t K, const FqArgs& fq, hipStream_t stream) {
-  hipLaunchKernelGGL((k_gemm_bs_nt<BF, BG, FQ>), dim3((unsigned)P.grid), dim3(NTHREADS), 0, stream, A, lda, B,
+  hipLaunchKernelGGL((k_gemm_bs_nt<BF, BG, FQ, false, KM>), dim3((unsigned)P.grid), dim3(NTHREADS), 0, stream, A, lda, B,
                      ldb, P.sa, P.sb, C, ldc, (int)K, (int)P.span, (int)P.tiles_m, (int)P.tiles_n,
                      (uint32_t)P.a_bytes, (uint32_t)P.b_bytes, (uint32_t)P.ea_bytes, (uint32_t)P.eb_bytes,
                      (uint32_t)P.ga_bytes, (uint32_t)P.gb_bytes, (int)M, (int)N, fq);
@@ -1603,6 +1649,42 @@ extern "C" int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t*
     else gemm_launch<false, 2, 0>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
   }
   return launch_status("gemm");
+}
+
+extern "C" int pratchya_gemm_bs_kmajor(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, const float* a_sc32,
+                                       int64_t a_rdiv, int64_t a_sr, int64_t a_sk, int64_t a_kg, const uint8_t* B,
+                                       int64_t ldb, const uint8_t* b_sc8, const float* b_sc32, int64_t b_rdiv,
+                                       int64_t b_sr, int64_t b_sk, int64_t b_kg, int64_t M, int64_t N, int64_t K,
+                                       void* C, int64_t ldc, int c_dtype, hipStream_t stream) {
+  if (M <= 0 || N <= 0 || K <= 0) {
+    if (M < 0 || N < 0 || K < 0) return pratchya_set_error(PRATCHYA_EINVAL, "gemm_kmajor: negative size");
+    return PRATCHYA_OK;
+  }
+  GemmPlan P;
+  // validated as the plan of the operands' [rows, K] views, then with the
+  // operand sizes of the K-major layouts ([K, M] and [K, N], row strides lda,
+  // ldb)
+  int rc = gemm_plan("gemm_kmajor", A, K, a_sc8, a_sc32, a_rdiv, a_sr, a_sk, a_kg, B, K, b_sc8, b_sc32, b_rdiv,
+                     b_sr, b_sk, b_kg, M, N, K, C, ldc, c_dtype, &P);
+  if (rc) return rc;
+  if (lda < M || ldb < N || lda % 16 || ldb % 16 || M % 16 || N % 16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "gemm_kmajor: M, N and the row strides (at least M, N) must be "
+                              "multiples of 16");
+  P.a_bytes = (K - 1) * lda + M;
+  P.b_bytes = (K - 1) * ldb + N;
+  if (P.a_bytes > (int64_t)INT32_MAX || P.b_bytes > (int64_t)INT32_MAX)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_kmajor: operands beyond 2 GiB");
+  const FqArgs none{};
+  if (c_dtype == PRATCHYA_DT_BF16) {
+    if (P.bg == 0) gemm_launch<true, 0, 0, 3>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
+    else if (P.bg == 1) gemm_launch<true, 1, 0, 3>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
+    else gemm_launch<true, 2, 0, 3>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
+  } else {
+    if (P.bg == 0) gemm_launch<false, 0, 0, 3>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
+    else if (P.bg == 1) gemm_launch<false, 1, 0, 3>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
+    else gemm_launch<false, 2, 0, 3>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
+  }
+  return launch_status("gemm_kmajor");
 }
 
 extern "C" int64_t pratchya_gemm_bs_nt_fq_workspace_bytes(int64_t M, int64_t N) {
@@ -1708,10 +1790,10 @@ int bf16_plan(const char* who, const void* A, int64_t lda, const void* B, int64_
   return PRATCHYA_OK;
 }
 
-template <bool OB, int FQ>
+template <bool OB, int FQ, int KM = 0>
 void bf16_launch(const GemmPlan& P, const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
                  int64_t M, int64_t N, int64_t K, const FqArgs& fq, hipStream_t stream) {
-  hipLaunchKernelGGL((k_gemm_bs_nt<OB, 0, FQ, true>), dim3((unsigned)P.grid), dim3(NTHREADS), 0, stream,
+  hipLaunchKernelGGL((k_gemm_bs_nt<OB, 0, FQ, true, KM>), dim3((unsigned)P.grid), dim3(NTHREADS), 0, stream,
                      static_cast<const uint8_t*>(A), lda * 2, static_cast<const uint8_t*>(B), ldb * 2, P.sa, P.sb,
                      C, ldc, (int)(K * 2), 1, (int)P.tiles_m, (int)P.tiles_n, (uint32_t)P.a_bytes,
                      (uint32_t)P.b_bytes, 0u, 0u, 0u, 0u, (int)M, (int)N, fq);
@@ -1764,7 +1846,7 @@ extern "C" int pratchya_gemm_bf16_nt_ns(const void* A, int64_t lda, const void* 
   FqArgs fq{};
   fq.ns_x = static_cast<const uint16_t*>(X);
   fq.ldx = ldx;
-  if (b_kmajor) bf16_launch<true, 6>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+  if (b_kmajor) bf16_launch<true, 3, 2>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
   else bf16_launch<true, 3>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
   return launch_status("gemm_bf16_ns");
 }
@@ -1839,7 +1921,7 @@ extern "C" int pratchya_gemm_bf16_gram(const void* A, int64_t lda, int64_t M, in
   rc = launch_status("gemm_bf16_gram");
   if (rc) return rc;
   P.grid = G;
-  if (a_kmajor) bf16_launch<true, 5>(P, A, lda, A, lda, C, ldc, M, M, K, fq, stream);
+  if (a_kmajor) bf16_launch<true, 4, 3>(P, A, lda, A, lda, C, ldc, M, M, K, fq, stream);
   else bf16_launch<true, 4>(P, A, lda, A, lda, C, ldc, M, M, K, fq, stream);
   return launch_status("gemm_bf16_gram");
 }

@@ -192,6 +192,26 @@ def test_wgrad_from_transposed_requantize():
     check(C, ref, F32_TOL, "wgrad via quantize_t128")
 
 
+@pytest.mark.parametrize("shape", [(1024, 512, 768), (2048, 256, 4096), (16384, 2048, 8192)],
+                         ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("out", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_wgrad_k_major_operands_same_bits(shape, out):
+    """The wgrad operands read K-major ([T, C], quantize_impl's own layout for
+    tgrid (128, 1)) through the LDS transposing loads: each MFMA lane sums the
+    same K values as with the transposed payloads, so the product is the same
+    bit for bit (span-1 rescales, per-row B group maxima, config 4's shape)."""
+    K = _K()
+    T, Cin, N_ = shape
+    a8 = K.quantize(to_dev_bf16(O.activation_input(T, Cin, seed=5)), (1, 128))
+    at = K.quantize_t128(*a8)
+    dt = K.quantize_t128(to_dev_bf16(O.normal_input((T, N_), 1e-3, seed=6)))
+    nt = K.gemm_nt(K.operand_t128(*at), K.operand_t128(*dt), out)
+    km = K.gemm_nt(K.operand_k128(K.transpose_u8(at[0]), at[1], at[2]),
+                   K.operand_k128(K.transpose_u8(dt[0]), dt[1], dt[2]), out)
+    torch.cuda.synchronize()
+    assert torch.equal(km.view(torch.uint8), nt.view(torch.uint8))
+
+
 def test_per_column_b_groups_exact():
     """B quantized (1, 128) as rows: every output column has its own group
     maxima, which change between the two 1024-wide K spans differently per

@@ -453,9 +453,13 @@ def bench_config4():
     N(0, 1e-3) (seed 4) requantized (1, 128) for dgrad and (128, 1) along
     tokens for wgrad; the stored activation A (config 2, (1, 128)) requantized
     (128, 1) from its fp8 payload; dgrad = q(dY) . W^T -> f32 [16384, 2048],
-    wgrad = q(A)^T . q(dY) -> f32 [2048, 8192].  Each kernel is timed on its
-    own (median of 5 timed replays of 50 launches; dY rotates through two
-    copies); requant bytes and GEMM FLOPs are the algorithmic counts."""
+    wgrad = q(A)^T . q(dY) -> f32 [2048, 8192].  The (128, 1) requantizations
+    write the payload in the tensor's own [T, C] layout and the wgrad GEMM
+    reads both operands K-major (the backward's path); the "_t" legs time the
+    transposed-payload form and the GEMM over it for comparison.  Each kernel
+    is timed on its own (median of 5 timed replays of 50 launches; dY rotates
+    through two copies); requant bytes and GEMM FLOPs are the algorithmic
+    counts."""
     import torch
     from oracle import qarr_oracle as O
     from pratchya_amd import _kernels as K
@@ -469,10 +473,13 @@ def bench_config4():
     op_w = K.operand_rows(*wq, (128, 128))               # W [2048, 8192]: rows Din, contraction Dout
     dyq = K.quantize(dy, (1, 128))
     dyt = K.quantize_t128(dy)
+    dyk = K.quantize_128x1(dy)
     # the 268 MB dY rotates through two copies (537 MB > the 256 MB MALL)
     dys = [dy, dy.clone()]
     at = K.quantize_t128(*a8)
+    ak = K.quantize_128x1(*a8)
     op_dy, op_dyt, op_at = K.operand_rows(*dyq, (1, 128)), K.operand_t128(*dyt), K.operand_t128(*at)
+    op_dyk, op_ak = K.operand_k128(*dyk), K.operand_k128(*ak)
     gx = torch.empty((T, Din), dtype=torch.float32, device="cuda")
     gw = torch.empty((Din, Dout), dtype=torch.float32, device="cuda")
     # outputs written in place; the 33 MB activation rotates through 8 copies
@@ -480,13 +487,19 @@ def bench_config4():
     n_a = 8
     a_sets = [tuple(t.clone() for t in a8) for _ in range(n_a)]
     at_outs = [tuple(torch.empty_like(t) for t in at) for _ in range(n_a)]
+    ak_outs = [tuple(torch.empty_like(t) for t in ak) for _ in range(n_a)]
     dyq_out = tuple(torch.empty_like(t) for t in dyq)
     dyt_out = tuple(torch.empty_like(t) for t in dyt)
+    dyk_out = tuple(torch.empty_like(t) for t in dyk)
     res = {}
     e_dy, e_a = T * Dout, T * Din
     cases = [
         ("requant_dy_1x128", lambda i: K.quantize(dys[i % 2], (1, 128), out=dyq_out),
          e_dy * 3 + e_dy // 128 + e_dy // 1024 * 4),
+        ("requant_dy_128x1", lambda i: K.quantize_128x1(dys[i % 2], out=dyk_out),
+         e_dy * 3 + e_dy // 128 + e_dy // 1024 * 4),
+        ("requant_a_fp8_to_128x1", lambda i: K.quantize_128x1(*a_sets[i % n_a], out=ak_outs[i % n_a]),
+         e_a * 2 + 2 * (e_a // 128 + e_a // 1024 * 4)),
         ("requant_dy_128x1_t", lambda i: K.quantize_t128(dys[i % 2], out=dyt_out),
          e_dy * 3 + e_dy // 128 + e_dy // 1024 * 4),
         ("requant_a_fp8_to_128x1_t", lambda i: K.quantize_t128(*a_sets[i % n_a], out=at_outs[i % n_a]),
@@ -500,7 +513,8 @@ def bench_config4():
                      "bytes": nbytes}
     flop = 2 * T * Din * Dout
     for name, fn in (("dgrad_gemm", lambda i: K.gemm_nt(op_dy, op_w, out=gx)),
-                     ("wgrad_gemm", lambda i: K.gemm_nt(op_at, op_dyt, out=gw))):
+                     ("wgrad_gemm", lambda i: K.gemm_nt(op_ak, op_dyk, out=gw)),
+                     ("wgrad_gemm_t", lambda i: K.gemm_nt(op_at, op_dyt, out=gw))):
         _log(f"config 4 {name}: start")
         ms, _ = timed_graph(fn, GEMM_LAUNCHES, 4, GEMM_REPLAYS)
         tf = flop / (ms * 1e-3) / 1e12

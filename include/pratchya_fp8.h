@@ -249,6 +249,17 @@ int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t* x_sc8, con
                            int64_t slices, int64_t T, int64_t C, uint8_t* xt_fp8, uint8_t* sc_fp8,
                            float* sc_fp32, hipStream_t stream);
 
+/* Requantize, tgrid (128, 1), payload in x's layout:
+ *                                      replaces quantize_impl(x, (128, 1)), Q:458-506.
+ * Arguments, inputs, scales and errors as for pratchya_quantize_t128; the
+ * payload q_fp8 is [slices, T, C] (quantize_impl's own output, 16-byte
+ * aligned; sc_fp8 8-byte aligned), which the FP8 GEMM reads K-major
+ * (pratchya_gemm_bs_kmajor) when it contracts over the tokens (fp8_matmul's
+ * weight gradient, Q:784-789). */
+int pratchya_quantize_128x1(const void* x, int x_dtype, const uint8_t* x_sc8, const float* x_sc32,
+                            int64_t slices, int64_t T, int64_t C, uint8_t* q_fp8, uint8_t* sc_fp8,
+                            float* sc_fp32, hipStream_t stream);
+
 /* Transposed quantize, tgrid (1, 128) of the transposed tensor:
  *                                         replaces quantize_impl(x^T, (1, 128)),
  * Q:458-506, as fp8_matmul's backward quantizes its transposed raw inputs

@@ -245,6 +245,16 @@ def quantize_t1x128(x: torch.Tensor, x_sc8: torch.Tensor = None, x_sc32: torch.T
     return xt8.view(E4M3), sc8.view(E8M0), sc32
 
 
+def quantize_128x1(x: torch.Tensor, x_sc8: torch.Tensor = None, x_sc32: torch.Tensor = None, out=None):
+    """``quantize_impl(x, (128, 1))`` (pratchya/_qualia/_qarr.py:458-506) with
+    the payload in ``x``'s own [..., T, C] layout, from the same inputs as
+    ``quantize_t128`` (bf16 / f32, an fp8 payload with its (1, 128) scales, or
+    a bf16 cotangent with them).  Returns ``(q_fp8 [..., T, C] e4m3fn, sc_fp8
+    [..., M, 8] e8m0, sc_fp32 [..., M, 1, 1] f32)``, exactly quantize_impl's.
+    """
+    return _quantize_128x1(x, x_sc8, x_sc32, out, rows=True)
+
+
 def quantize_t128(x: torch.Tensor, x_sc8: torch.Tensor = None, x_sc32: torch.Tensor = None, out=None):
     """``quantize_impl(x, (128, 1))`` (pratchya/_qualia/_qarr.py:458-506) with
     the payload transposed per slice.
@@ -258,9 +268,14 @@ def quantize_t128(x: torch.Tensor, x_sc8: torch.Tensor = None, x_sc32: torch.Ten
     exactly ``quantize_impl(x, (128, 1))``'s, the payload is its payload with
     the last two axes swapped.  ``out`` may hold preallocated buffers.
     """
+    return _quantize_128x1(x, x_sc8, x_sc32, out, rows=False)
+
+
+def _quantize_128x1(x, x_sc8, x_sc32, out, rows):
+    name = "quantize_128x1" if rows else "quantize_t128"
     _require_gpu(x)
     if x.dim() < 2:
-        raise ValueError("quantize_t128 needs a [..., T, C] tensor")
+        raise ValueError(f"{name} needs a [..., T, C] tensor")
     lead = tuple(x.shape[:-2])
     T, C = int(x.shape[-2]), int(x.shape[-1])
     S = 1
@@ -285,19 +300,19 @@ def quantize_t128(x: torch.Tensor, x_sc8: torch.Tensor = None, x_sc32: torch.Ten
     if not xin.is_contiguous() or not _aligned(xin, 16):
         xin = xin.contiguous() if not xin.is_contiguous() else xin.clone()
     _, K, M = group_layout(T, C, (128, 1))
+    qshape = lead + ((T, C) if rows else (C, T))
     if out is None:
-        xt = torch.empty(lead + (C, T), dtype=torch.uint8, device=x.device)
+        xt = torch.empty(qshape, dtype=torch.uint8, device=x.device)
         sc8 = torch.empty(lead + (M, K), dtype=torch.uint8, device=x.device)
         sc32 = torch.empty(lead + (M, 1, 1), dtype=torch.float32, device=x.device)
     else:
-        _check_out(out, [(lead + (C, T), 1), (lead + (M, K), 1), (lead + (M, 1, 1), 4)], "quantize_t128")
+        _check_out(out, [(qshape, 1), (lead + (M, K), 1), (lead + (M, 1, 1), 4)], name)
         xt, sc8, sc32 = _u8(out[0]), _u8(out[1]), out[2]
     lib = _lib.load()
-    _lib.check(lib.pratchya_quantize_t128(_ptr(xin), code,
-                                          _ptr(xs8) if xs8 is not None else None,
-                                          _ptr(xs32) if xs32 is not None else None,
-                                          S, T, C, _ptr(xt), _ptr(sc8), _ptr(sc32), _stream(xin)),
-               "quantize_t128")
+    fn = lib.pratchya_quantize_128x1 if rows else lib.pratchya_quantize_t128
+    _lib.check(fn(_ptr(xin), code, _ptr(xs8) if xs8 is not None else None,
+                  _ptr(xs32) if xs32 is not None else None,
+                  S, T, C, _ptr(xt), _ptr(sc8), _ptr(sc32), _stream(xin)), name)
     return xt.view(E4M3), sc8.view(E8M0), sc32
 
 

@@ -48,6 +48,8 @@ SIGNATURES = {
                                          _c_i64, _c_p, _c_p]),
     "pratchya_quantize_t128": (_c_int, [_c_p, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64,
                                         _c_p, _c_p, _c_p, _c_p]),
+    "pratchya_quantize_128x1": (_c_int, [_c_p, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64,
+                                         _c_p, _c_p, _c_p, _c_p]),
     "pratchya_gather_quantize": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_i64,
                                           _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, ctypes.c_size_t, _c_p]),
     "pratchya_elementwise_workspace_bytes": (ctypes.c_size_t, [_c_i64] * 9),

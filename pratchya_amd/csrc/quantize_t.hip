@@ -575,6 +575,177 @@ __global__ __launch_bounds__(256) void k_quant_t1x128_fp8(const uint8_t* __restr
   }
 }
 
+// quantize_impl(x, (128, 1)) with the payload in x's own layout [slices, T,
+// C] (the K-major operand of the weight-gradient GEMM): no transposition, so
+// each thread owns one group (8 channels) of 8 token rows of a 128-token x
+// 128-channel tile, and 16 threads cover a row's 128 channels with
+// consecutive pieces (whole 128-byte lines for fp8 payloads and bf16 rows).
+// Thread t of the 256: group t % 16, token rows t / 16 + 16 i (i < 8).
+// Channel maxima: an in-thread max over the 8 rows, the 4 lanes of a wave
+// sharing the group (row swaps), then the 4 waves through LDS.  The cast is
+// k_quant_t128's (the same e8m0 bytes, y and midpoint check), row by row.  A
+// workgroup walks nblk consecutive token blocks of its column, the next
+// block's loads issued after the current block's stores (prefetching the next
+// block into registers measured slower: 83 vs 76 us on config 4's dY, the
+// extra registers cost a wave per SIMD).
+#ifndef PRATCHYA_ROWS_WGS
+#define PRATCHYA_ROWS_WGS 2048   // workgroups the token blocks are spread over
+#endif
+template <int IN>
+__global__ __launch_bounds__(256) void k_quant_128x1_rows(const uint8_t* __restrict__ x,
+                                                          const uint8_t* __restrict__ x_sc8,
+                                                          const float* __restrict__ x_sc32, int kg_shift,
+                                                          int64_t T, int64_t C, int nblk, uint8_t* __restrict__ q,
+                                                          uint8_t* __restrict__ sc8, float* __restrict__ sc32) {
+  constexpr int ESZ = InTraits<IN>::ESZ, NW = InTraits<IN>::NW;
+  constexpr bool SCALED = IN == IN_FP8 || IN == IN_BF16S;
+  constexpr int INC = IN == IN_BF16S ? IN_BF16 : IN;
+  constexpr int R = 8;                        // token rows per thread and block
+  const int lane = (int)threadIdx.x & 63, wv = (int)(threadIdx.x >> 6);
+  const int grp = lane & 15, rr = wv * 4 + (lane >> 4);
+  const int64_t s = blockIdx.z;
+  const int64_t c0 = (int64_t)blockIdx.x * 128 + grp * 8;
+  const bool live = c0 < C;                   // C is a multiple of 8: whole groups
+  const int64_t nbr = T / 128, nb = nbr * C;
+  const int64_t tb0 = (int64_t)blockIdx.y * nblk;
+  const int64_t tb1 = tb0 + nblk < nbr ? tb0 + nblk : nbr;
+  // input scale blocks of a token row: C / 128 (scaled inputs); this
+  // workgroup's column is block blockIdx.x of each row.  32-bit indices: the
+  // host checks slices * T * C / 128 < 2^32.
+  const uint32_t nsr = (uint32_t)(C >> 7);
+  __shared__ __attribute__((aligned(16))) uint32_t smx[2][4][128];
+
+  uint32_t w[R][NW];
+  uint32_t se[R];
+  float sg[R];
+  auto load_block = [&](int64_t tb, uint32_t (&wd)[R][NW], uint32_t (&sed)[R], float (&sgd)[R]) {
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int64_t t = tb * 128 + rr + 16 * i;
+      if (live) {
+        load_row<IN>(x + ((s * T + t) * C + c0) * ESZ, wd[i]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < NW; ++k) wd[i][k] = 0u;
+      }
+      if constexpr (SCALED) {
+        const uint32_t blk = (uint32_t)(s * T + t) * nsr + blockIdx.x;
+        sed[i] = x_sc8[blk];
+        sgd[i] = x_sc32[blk >> kg_shift];
+      }
+    }
+  };
+  load_block(tb0, w, se, sg);
+  int par = 0;
+  for (int64_t tb = tb0; tb < tb1; ++tb, par ^= 1) {
+    float dq[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) dq[i] = SCALED ? e8m0_decode(se[i]) * sg[i] : 1.0f;
+    if constexpr (IN == IN_BF16S) {
+      // the cotangent's dequantize_impl_bwd, in place (as in k_quant_t128)
+#pragma unroll
+      for (int i = 0; i < R; ++i)
+#pragma unroll
+        for (int k = 0; k < NW; ++k) {
+          const float lo = (u2f(w[i][k] << 16) * dq[i]) * 0.0078125f;
+          const float hi = (u2f(w[i][k] & 0xFFFF0000u) * dq[i]) * 0.0078125f;
+          w[i][k] = pack_bf16x2(lo, hi);
+        }
+    }
+    constexpr bool ONCE = INC == IN_FP8;
+    float vv[ONCE ? R : 1][ONCE ? 8 : 1];
+    if constexpr (ONCE) {
+      static_for<8>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+#pragma unroll
+        for (int i = 0; i < R; ++i) vv[i][j] = row_elem<INC, j>(w[i], dq[i]);
+      });
+    }
+    auto val = [&](auto jc, int i) -> float {
+      constexpr int j = decltype(jc)::value;
+      if constexpr (ONCE) return vv[i][j];
+      else return row_elem<INC, j>(w[i], dq[i]);
+    };
+    // channel maxima (|x| bits): 8 rows in-thread, 4 lanes, then 4 waves
+    uint32_t mx[8];
+    static_for<8>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      uint32_t m = 0;
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        if constexpr (ONCE) m = umax(m, f2u(vv[i][j]) & 0x7FFFFFFFu);
+        else m = umax(m, row_abs_bits<INC, j>(w[i], dq[i]));
+      }
+      mx[j] = xor_max_u32<32>(xor_max_u32<16>(m));
+    });
+    if (lane < 16) {
+      uint4* d = reinterpret_cast<uint4*>(&smx[par][wv][grp * 8]);
+      d[0] = make_uint4(mx[0], mx[1], mx[2], mx[3]);
+      d[1] = make_uint4(mx[4], mx[5], mx[6], mx[7]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const uint4 a = *reinterpret_cast<const uint4*>(&smx[par][v][grp * 8]);
+      const uint4 b = *reinterpret_cast<const uint4*>(&smx[par][v][grp * 8 + 4]);
+      mx[0] = umax(mx[0], a.x); mx[1] = umax(mx[1], a.y); mx[2] = umax(mx[2], a.z); mx[3] = umax(mx[3], a.w);
+      mx[4] = umax(mx[4], b.x); mx[5] = umax(mx[5], b.y); mx[6] = umax(mx[6], b.z); mx[7] = umax(mx[7], b.w);
+    }
+    // the group max, e8m0 bytes and y per channel (k_quant_t128's scheme)
+    uint32_t Gb = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) Gb = umax(Gb, mx[j]);
+    const float G = u2f(Gb);
+    const bool fin = (Gb >> 23) < 255u;
+    const float rG = __builtin_amdgcn_rcpf(G * 0.0078125f);
+    uint32_t e[8];
+    float y[8];
+    uint32_t clamped = fin ? 0u : 1u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (fin) {
+        const BlockScale bs = block_scale(mx[j], Gb, rG);
+        e[j] = bs.e;
+        y[j] = bs.y;
+        clamped |= bs.clamped ? 1u : 0u;
+      } else {
+        e[j] = e8m0_of(u2f(mx[j]), G);
+        y[j] = PRATCHYA_Y_CLAMP;
+      }
+    }
+    const bool check = INC != IN_BF16 || __any(clamped);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      float t[8];
+      static_for<8>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        t[j] = val(jc, i) * y[j];
+      });
+      uint32_t lo = cvt4<true>(t[0], t[1], t[2], t[3]), hi = cvt4<true>(t[4], t[5], t[6], t[7]);
+      const uint32_t key = check ? umin(mid_key4(t[0], t[1], t[2], t[3]), mid_key4(t[4], t[5], t[6], t[7]))
+                                 : 0xFFFFFFFFu;
+      if (key <= kMidKey || !fin) {
+        uint32_t b[8];
+        static_for<8>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          b[j] = quant_elem_exact(val(jc, i), quant_scale(e[j], G));
+        });
+        lo = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+        hi = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+      }
+      if (live) store_stream8(q + (s * T + tb * 128 + rr + 16 * i) * C + c0, u32x2_t{lo, hi});
+    }
+    if (wv == 0 && lane < 16 && live) {
+      // blocks (tb, c0 .. c0 + 7) are consecutive bytes; they form group (tb*C + c0) / 8
+      const int64_t blk = tb * C + c0;
+      store_stream8(sc8 + s * nb + blk, u32x2_t{e[0] | (e[1] << 8) | (e[2] << 16) | (e[3] << 24),
+                                                e[4] | (e[5] << 8) | (e[6] << 16) | (e[7] << 24)});
+      sc32[s * (nb / 8) + blk / 8] = G;
+    }
+    if (tb + 1 < tb1) load_block(tb + 1, w, se, sg);
+  }
+}
+
 int64_t gcd64(int64_t a, int64_t b) {
   while (b) {
     const int64_t t = a % b;
@@ -586,35 +757,40 @@ int64_t gcd64(int64_t a, int64_t b) {
 
 }  // namespace
 
-extern "C" int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t* x_sc8,
-                                      const float* x_sc32, int64_t slices, int64_t T, int64_t C,
-                                      uint8_t* xt_fp8, uint8_t* sc_fp8, float* sc_fp32,
-                                      hipStream_t stream) {
-  if (slices < 0 || T < 0 || C < 0) return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t128: negative size");
+namespace {
+
+// pratchya_quantize_t128 (rows = false: payload [C, T] per slice) and
+// pratchya_quantize_128x1 (rows = true: payload [T, C], x's own layout):
+// the same checks and outputs but for the payload's layout.
+int quantize_128x1_impl(bool rows, const void* x, int x_dtype, const uint8_t* x_sc8, const float* x_sc32,
+                        int64_t slices, int64_t T, int64_t C, uint8_t* xt_fp8, uint8_t* sc_fp8, float* sc_fp32,
+                        hipStream_t stream) {
+  const char* name = rows ? "quantize_128x1" : "quantize_t128";
+  if (slices < 0 || T < 0 || C < 0) return pratchya_set_error(PRATCHYA_EINVAL, "%s: negative size", name);
   if (x_dtype != PRATCHYA_DT_F32 && x_dtype != PRATCHYA_DT_BF16 && x_dtype != PRATCHYA_DT_E4M3)
-    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t128: unsupported input dtype %d", x_dtype);
+    return pratchya_set_error(PRATCHYA_EINVAL, "%s: unsupported input dtype %d", name, x_dtype);
   if (T % 128)
-    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t128: tgrid (128, 1) does not divide %lld tokens",
+    return pratchya_set_error(PRATCHYA_EINVAL, "%s: tgrid (128, 1) does not divide %lld tokens", name,
                               (long long)T);
   // an fp8 payload, or a bf16 cotangent given with scales: (1, 128) input scales
   const bool scaled = x_dtype == PRATCHYA_DT_E4M3 || (x_dtype == PRATCHYA_DT_BF16 && x_sc8 && x_sc32);
   if (scaled && C % 128)
-    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t128: tgrid (1, 128) of the input scales does not divide "
-                              "%lld channels", (long long)C);
+    return pratchya_set_error(PRATCHYA_EINVAL, "%s: tgrid (1, 128) of the input scales does not divide "
+                              "%lld channels", name, (long long)C);
   if (slices == 0 || T == 0 || C == 0) return PRATCHYA_OK;
   if (C % 8)
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t128: channels must be a multiple of 8 (got %lld)",
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: channels must be a multiple of 8 (got %lld)", name,
                               (long long)C);
   if (!x || !xt_fp8 || !sc_fp8 || !sc_fp32 || (x_dtype == PRATCHYA_DT_E4M3 && (!x_sc8 || !x_sc32)))
-    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_t128: null buffer");
+    return pratchya_set_error(PRATCHYA_EINVAL, "%s: null buffer", name);
   const uintptr_t xa = reinterpret_cast<uintptr_t>(x);
   if (xa % 16 || reinterpret_cast<uintptr_t>(xt_fp8) % 16 ||
-      reinterpret_cast<uintptr_t>(sc_fp8) % 4 || reinterpret_cast<uintptr_t>(sc_fp32) % 4)
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t128: buffers are not aligned");
+      reinterpret_cast<uintptr_t>(sc_fp8) % (rows ? 8 : 4) || reinterpret_cast<uintptr_t>(sc_fp32) % 4)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: buffers are not aligned", name);
   if (T / 128 > 65535 || slices > 65535)
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t128: too many token blocks or slices");
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: too many token blocks or slices", name);
   if (scaled && (slices * T) * (C / 128) >= ((int64_t)1 << 32))
-    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_t128: input scales beyond 2^32 blocks");
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: input scales beyond 2^32 blocks", name);
   // 16 tokens per lane (64 channels per wave, 128-byte row segments) for bf16
   // inputs; 8 (32 channels per wave, half the registers) for the VALU-heavier
   // f32 and fp8 inputs, where occupancy matters more than segment length
@@ -633,7 +809,28 @@ extern "C" int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t*
   // blocks per group of a (1, 128) input: gcd(8, n_blk), a power of two
   const int64_t kg = scaled ? gcd64(8, T * (C / 128)) : 1;
   const int kg_shift = kg == 8 ? 3 : (kg == 4 ? 2 : (kg == 2 ? 1 : 0));
-  if (x_dtype == PRATCHYA_DT_BF16 && scaled) {
+  if (rows) {
+    // a workgroup per 128-channel column and nblk token blocks: about 2048
+    // workgroups (measured on config 4's dY: 76 us, one block per workgroup
+    // 78 us)
+    const int64_t ncol = (C + 127) / 128, nbr = T / 128;
+    int64_t nblk = (ncol * nbr * slices) / PRATCHYA_ROWS_WGS;
+    nblk = nblk < 1 ? 1 : (nblk > 8 ? 8 : nblk);
+    const dim3 grid((unsigned)ncol, (unsigned)((nbr + nblk - 1) / nblk), (unsigned)slices);
+    const int nb_i = (int)nblk;
+    if (x_dtype == PRATCHYA_DT_BF16 && scaled)
+      hipLaunchKernelGGL((k_quant_128x1_rows<IN_BF16S>), grid, dim3(256), 0, stream, xb, x_sc8, x_sc32, kg_shift, T,
+                         C, nb_i, xt_fp8, sc_fp8, sc_fp32);
+    else if (x_dtype == PRATCHYA_DT_BF16)
+      hipLaunchKernelGGL((k_quant_128x1_rows<IN_BF16>), grid, dim3(256), 0, stream, xb, nullptr, nullptr, 0, T, C,
+                         nb_i, xt_fp8, sc_fp8, sc_fp32);
+    else if (x_dtype == PRATCHYA_DT_F32)
+      hipLaunchKernelGGL((k_quant_128x1_rows<IN_F32>), grid, dim3(256), 0, stream, xb, nullptr, nullptr, 0, T, C,
+                         nb_i, xt_fp8, sc_fp8, sc_fp32);
+    else
+      hipLaunchKernelGGL((k_quant_128x1_rows<IN_FP8>), grid, dim3(256), 0, stream, xb, x_sc8, x_sc32, kg_shift, T,
+                         C, nb_i, xt_fp8, sc_fp8, sc_fp32);
+  } else if (x_dtype == PRATCHYA_DT_BF16 && scaled) {
     hipLaunchKernelGGL((k_quant_t128<IN_BF16S, true, 16>), grid_for_tok(16), dim3(256), 0, stream, xb, x_sc8, x_sc32, kg_shift,
                        T, C, xt_fp8, sc_fp8, sc_fp32, tok_major);
   } else if (x_dtype == PRATCHYA_DT_BF16) {
@@ -648,8 +845,23 @@ extern "C" int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t*
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess)
-    return pratchya_set_error(PRATCHYA_EHIP, "quantize_t128: launch failed: %s", hipGetErrorString(err));
+    return pratchya_set_error(PRATCHYA_EHIP, "%s: launch failed: %s", name, hipGetErrorString(err));
   return PRATCHYA_OK;
+}
+
+}  // namespace
+
+extern "C" int pratchya_quantize_t128(const void* x, int x_dtype, const uint8_t* x_sc8,
+                                      const float* x_sc32, int64_t slices, int64_t T, int64_t C,
+                                      uint8_t* xt_fp8, uint8_t* sc_fp8, float* sc_fp32,
+                                      hipStream_t stream) {
+  return quantize_128x1_impl(false, x, x_dtype, x_sc8, x_sc32, slices, T, C, xt_fp8, sc_fp8, sc_fp32, stream);
+}
+
+extern "C" int pratchya_quantize_128x1(const void* x, int x_dtype, const uint8_t* x_sc8, const float* x_sc32,
+                                       int64_t slices, int64_t T, int64_t C, uint8_t* q_fp8, uint8_t* sc_fp8,
+                                       float* sc_fp32, hipStream_t stream) {
+  return quantize_128x1_impl(true, x, x_dtype, x_sc8, x_sc32, slices, T, C, q_fp8, sc_fp8, sc_fp32, stream);
 }
 
 extern "C" int pratchya_quantize_t1x128(const void* x, int x_dtype, const uint8_t* x_sc8, const float* x_sc32,

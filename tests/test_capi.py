@@ -190,11 +190,13 @@ def test_gemm_span_matches_brute_force():
         assert P == (want or nk), (rows, nk, rdiv, sr, sk, kg, P, want)
 
 
-def test_quantize_t128_argument_codes_without_gpu():
-    """Shape errors are reported before anything touches a buffer."""
+@pytest.mark.parametrize("entry", ["pratchya_quantize_t128", "pratchya_quantize_128x1"])
+def test_quantize_t128_argument_codes_without_gpu(entry):
+    """Shape errors are reported before anything touches a buffer (both
+    payload layouts share the checks)."""
     from pratchya_amd import _lib
     lib = _lib.load()
-    f = lib.pratchya_quantize_t128
+    f = getattr(lib, entry)
     # 100 tokens: tgrid (128, 1) does not divide -> the reference's reshape error
     assert f(None, _lib.DT_BF16, None, None, 1, 100, 64, None, None, None, None) == _lib.EINVAL
     # fp8 input whose (1, 128) grid does not divide the channels
@@ -412,3 +414,20 @@ def test_gemm_bf16_ns_argument_codes_without_gpu():
     assert lib.pratchya_gemm_bf16_nt_ns(fake, 128, fake, 128, 1, 256, 256, 128, fake, 256, other, 256,
                                         None) == _lib.EINVAL
     assert b"K-major" in lib.pratchya_last_error()
+
+
+def test_gemm_kmajor_argument_codes_without_gpu():
+    """pratchya_gemm_bs_kmajor: M, N and the row strides must be multiples of
+    16 with strides of at least M and N; checked before any launch."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)          # aligned, never dereferenced
+    op = (1, 1, 256, 8)                      # (128, 1) groups of a [T, C] operand (K = T = 256)
+    args = lambda M, N, lda, ldb: (fake, lda, fake, fake, *op, fake, ldb, fake, fake, *op, M, N, 256, fake, N,
+                                   _lib.DT_F32, None)
+    assert lib.pratchya_gemm_bs_kmajor(*args(264, 256, 264, 256)) == _lib.EINVAL
+    assert b"multiples of 16" in lib.pratchya_last_error()
+    assert lib.pratchya_gemm_bs_kmajor(*args(256, 256, 128, 256)) == _lib.EINVAL
+    assert lib.pratchya_gemm_bs_kmajor(*args(256, 256, 256, 264)) == _lib.EINVAL
+    assert lib.pratchya_gemm_bs_kmajor(*args(0, 256, 256, 256)) == _lib.OK
+    assert lib.pratchya_gemm_bs_kmajor(*args(-1, 256, 256, 256)) == _lib.EINVAL

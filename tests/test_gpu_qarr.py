@@ -198,6 +198,31 @@ def test_linear_forward_uses_the_fp8_kernel(Q, monkeypatch):
     assert len(calls) == 2
 
 
+@pytest.mark.parametrize("M,Kd,N", [(512, 1024, 768), (1024, 256, 384)])
+def test_fp8_wgrad_layouts_same_bits(Q, M, Kd, N):
+    """The fp8 weight gradient from (128, 1) payloads in the [tokens, channels]
+    layout read K-major, and from transposed payloads read K-contiguous: the
+    same MFMA K order per lane, so W's cotangent has the same bits (x's does
+    not depend on the layout)."""
+    assert Kd <= Q._WGRAD_K_MAJOR_ROWS          # the K-major path is taken
+    Q.set_matmul_backward("fp8")
+    xb, wb, gb = _linear_case(seed=21, M=M, Kd=Kd, N=N)
+    grads = []
+    try:
+        for k_major in (True, False):
+            Q._wgrad_k_major = k_major
+            x = to_dev_bf16(xb).requires_grad_(True)
+            w = to_dev_bf16(wb).requires_grad_(True)
+            y = (Q.QArrayImpl(x, (1, 128)) @ Q.QArrayImpl(w, (128, 128))).astype(torch.bfloat16)
+            y.backward(to_dev_bf16(gb))
+            grads.append((w.grad.clone(), x.grad.clone()))
+    finally:
+        Q._wgrad_k_major = True
+    torch.cuda.synchronize()
+    assert torch.equal(grads[0][0].view(torch.int16), grads[1][0].view(torch.int16)), "W cotangents differ"
+    assert torch.equal(grads[0][1].view(torch.int16), grads[1][1].view(torch.int16))
+
+
 @pytest.mark.parametrize("mode", ["f32", "fp8"])
 @pytest.mark.parametrize("xdtype", ["bf16", "f32"])
 def test_fused_linear_matches_materialised_composition(Q, mode, xdtype):

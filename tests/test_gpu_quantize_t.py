@@ -1,9 +1,12 @@
-"""GPU parity of the transposed requantize (tgrid (128, 1), payload [C, T]).
+"""GPU parity of the tgrid (128, 1) requantize, with the payload transposed
+([C, T], quantize_t128) and in the input's own layout ([T, C],
+quantize_128x1, which the K-major FP8 GEMM reads).
 
-Expected values: the oracle's quantize_impl(x, (128, 1)) with the payload's
-last two axes swapped; for an fp8 input, quantize_impl(dequantize_impl(x8,
-sc8, sc32, f32, (1, 128)), (128, 1)).  Bit-exact payload, e8m0 and f32 bytes
-(a NaN payload byte's sign is compared as NaN-ness only).
+Expected values: the oracle's quantize_impl(x, (128, 1)) (its payload's last
+two axes swapped for quantize_t128); for an fp8 input,
+quantize_impl(dequantize_impl(x8, sc8, sc32, f32, (1, 128)), (128, 1)).
+Bit-exact payload, e8m0 and f32 bytes (a NaN payload byte's sign is compared
+as NaN-ness only).  Every case runs both entry points.
 """
 import numpy as np
 import pytest
@@ -21,6 +24,10 @@ def _K():
     return _kernels
 
 
+def u8_dev(t):
+    return t.view(torch.uint8)
+
+
 def oracle_t128(x_f32):
     r8, rs8, rs32 = O.quantize_impl(x_f32, (128, 1))
     return np.ascontiguousarray(np.swapaxes(r8, -1, -2)), rs8, rs32
@@ -28,13 +35,17 @@ def oracle_t128(x_f32):
 
 def check(dev, x_f32, what, x_sc8=None, x_sc32=None):
     xt, s8, s32 = _K().quantize_t128(dev, x_sc8, x_sc32)
+    xr, q8, q32 = _K().quantize_128x1(dev, x_sc8, x_sc32)
     torch.cuda.synchronize()
-    r8, rs8, rs32 = oracle_t128(x_f32)
-    assert tuple(xt.shape) == r8.shape, (tuple(xt.shape), r8.shape)
-    assert tuple(s8.shape) == rs8.shape and tuple(s32.shape) == rs32.shape
-    assert_payload_equal(u8(xt), r8, f"{what} payload")
-    assert_bytes_equal(u8(s8), rs8, f"{what} e8m0")
-    assert_f32_bits_equal(f32(s32), rs32, f"{what} group max")
+    r8, rs8, rs32 = O.quantize_impl(x_f32, (128, 1))
+    rt8 = np.ascontiguousarray(np.swapaxes(r8, -1, -2))
+    assert tuple(xt.shape) == rt8.shape and tuple(xr.shape) == r8.shape, (tuple(xt.shape), r8.shape)
+    for tag, (a8, a32) in (("transposed", (s8, s32)), ("rows", (q8, q32))):
+        assert tuple(a8.shape) == rs8.shape and tuple(a32.shape) == rs32.shape
+        assert_bytes_equal(u8(a8), rs8, f"{what} {tag} e8m0")
+        assert_f32_bits_equal(f32(a32), rs32, f"{what} {tag} group max")
+    assert_payload_equal(u8(xt), rt8, f"{what} transposed payload")
+    assert_payload_equal(u8(xr), r8, f"{what} rows payload")
     return xt, s8, s32
 
 
@@ -111,9 +122,12 @@ def test_fp8_input_many_tiles_sampled_token_blocks():
     x[:, :, 5] *= 50.0
     x8, s8, s32 = _K().quantize(x.to(torch.bfloat16), (1, 128))
     xt, t8, t32 = _K().quantize_t128(x8, s8, s32)
+    xr, q8, q32 = _K().quantize_128x1(x8, s8, s32)
     torch.cuda.synchronize()
     x8_h, s8_h, s32_h = u8(x8), u8(s8).reshape(S, -1), f32(s32).reshape(S, -1)
     xt_h, t8_h, t32_h = u8(xt), u8(t8).reshape(S, -1), f32(t32).reshape(S, -1)
+    assert torch.equal(u8_dev(q8), u8_dev(t8)) and torch.equal(q32.view(torch.int32), t32.view(torch.int32))
+    assert torch.equal(u8_dev(xr).transpose(-1, -2), u8_dev(xt))
     gpr = C // 1024                             # input groups per token row
     for s in range(S):
         for tb in (0, 1, 31, 63):
@@ -156,7 +170,10 @@ def test_config4_dy_full_size_sampled_token_blocks():
     g = torch.Generator(device="cuda").manual_seed(4)
     dy = (torch.randn((T, C), generator=g, device="cuda") * 1e-3).to(torch.bfloat16)
     xt, s8, s32 = _K().quantize_t128(dy)
+    xr, q8, q32 = _K().quantize_128x1(dy)
     torch.cuda.synchronize()
+    assert torch.equal(u8_dev(q8), u8_dev(s8)) and torch.equal(q32.view(torch.int32), s32.view(torch.int32))
+    assert torch.equal(u8_dev(xr).T, u8_dev(xt))
     xt_h = u8(xt)
     s8_h = u8(s8).reshape(-1)
     s32_h = f32(s32).reshape(-1)
@@ -168,13 +185,14 @@ def test_config4_dy_full_size_sampled_token_blocks():
         assert_f32_bits_equal(s32_h[tb * C // 8:(tb + 1) * C // 8], rs32.reshape(-1), f"slab {tb} G")
 
 
-def test_argument_errors():
-    K = _K()
+@pytest.mark.parametrize("fn", ["quantize_t128", "quantize_128x1"])
+def test_argument_errors(fn):
+    f = getattr(_K(), fn)
     with pytest.raises(ValueError, match="does not divide"):
-        K.quantize_t128(torch.zeros((100, 64), dtype=torch.bfloat16, device="cuda"))
+        f(torch.zeros((100, 64), dtype=torch.bfloat16, device="cuda"))
     from pratchya_amd._lib import PratchyaError
     with pytest.raises(PratchyaError, match="multiple of 8"):
-        K.quantize_t128(torch.zeros((128, 12), dtype=torch.bfloat16, device="cuda"))
+        f(torch.zeros((128, 12), dtype=torch.bfloat16, device="cuda"))
 
 
 @pytest.mark.parametrize("T,C", [(256, 256), (384, 1024)])

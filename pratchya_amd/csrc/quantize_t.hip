@@ -591,8 +591,11 @@ __global__ __launch_bounds__(256) void k_quant_t1x128_fp8(const uint8_t* __restr
 #ifndef PRATCHYA_ROWS_WGS
 #define PRATCHYA_ROWS_WGS 2048   // workgroups the token blocks are spread over
 #endif
-template <int IN>
-__global__ __launch_bounds__(256) void k_quant_128x1_rows(const uint8_t* __restrict__ x,
+// threads of k_quant_128x1_rows<IN, R>'s workgroup: 32 / R waves
+constexpr int rows_threads(int R) { return 2048 / R; }
+
+template <int IN, int R>
+__global__ __launch_bounds__(rows_threads(R)) void k_quant_128x1_rows(const uint8_t* __restrict__ x,
                                                           const uint8_t* __restrict__ x_sc8,
                                                           const float* __restrict__ x_sc32, int kg_shift,
                                                           int64_t T, int64_t C, int nblk, uint8_t* __restrict__ q,
@@ -600,7 +603,11 @@ __global__ __launch_bounds__(256) void k_quant_128x1_rows(const uint8_t* __restr
   constexpr int ESZ = InTraits<IN>::ESZ, NW = InTraits<IN>::NW;
   constexpr bool SCALED = IN == IN_FP8 || IN == IN_BF16S;
   constexpr int INC = IN == IN_BF16S ? IN_BF16 : IN;
-  constexpr int R = 8;                        // token rows per thread and block
+  // R token rows per thread and block: NWV = 32 / R waves, token rows
+  // rr + SR * i with rr < SR = 128 / R
+  static_assert(R == 4 || R == 8, "4 or 8 token rows per thread");
+  constexpr int NWV = 32 / R, SR = 128 / R;
+  static_assert(NWV * 64 == rows_threads(R), "the workgroup is NWV waves");
   const int lane = (int)threadIdx.x & 63, wv = (int)(threadIdx.x >> 6);
   const int grp = lane & 15, rr = wv * 4 + (lane >> 4);
   const int64_t s = blockIdx.z;
@@ -613,7 +620,7 @@ __global__ __launch_bounds__(256) void k_quant_128x1_rows(const uint8_t* __restr
   // workgroup's column is block blockIdx.x of each row.  32-bit indices: the
   // host checks slices * T * C / 128 < 2^32.
   const uint32_t nsr = (uint32_t)(C >> 7);
-  __shared__ __attribute__((aligned(16))) uint32_t smx[2][4][128];
+  __shared__ __attribute__((aligned(16))) uint32_t smx[2][NWV][128];
 
   uint32_t w[R][NW];
   uint32_t se[R];
@@ -621,7 +628,7 @@ __global__ __launch_bounds__(256) void k_quant_128x1_rows(const uint8_t* __restr
   auto load_block = [&](int64_t tb, uint32_t (&wd)[R][NW], uint32_t (&sed)[R], float (&sgd)[R]) {
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      const int64_t t = tb * 128 + rr + 16 * i;
+      const int64_t t = tb * 128 + rr + SR * i;
       if (live) {
         load_row<IN>(x + ((s * T + t) * C + c0) * ESZ, wd[i]);
       } else {
@@ -685,7 +692,7 @@ __global__ __launch_bounds__(256) void k_quant_128x1_rows(const uint8_t* __restr
     }
     __syncthreads();
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
+    for (int v = 0; v < NWV; ++v) {
       const uint4 a = *reinterpret_cast<const uint4*>(&smx[par][v][grp * 8]);
       const uint4 b = *reinterpret_cast<const uint4*>(&smx[par][v][grp * 8 + 4]);
       mx[0] = umax(mx[0], a.x); mx[1] = umax(mx[1], a.y); mx[2] = umax(mx[2], a.z); mx[3] = umax(mx[3], a.w);
@@ -733,7 +740,7 @@ __global__ __launch_bounds__(256) void k_quant_128x1_rows(const uint8_t* __restr
         lo = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
         hi = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
       }
-      if (live) store_stream8(q + (s * T + tb * 128 + rr + 16 * i) * C + c0, u32x2_t{lo, hi});
+      if (live) store_stream8(q + (s * T + tb * 128 + rr + SR * i) * C + c0, u32x2_t{lo, hi});
     }
     if (wv == 0 && lane < 16 && live) {
       // blocks (tb, c0 .. c0 + 7) are consecutive bytes; they form group (tb*C + c0) / 8
@@ -818,17 +825,21 @@ int quantize_128x1_impl(bool rows, const void* x, int x_dtype, const uint8_t* x_
     nblk = nblk < 1 ? 1 : (nblk > 8 ? 8 : nblk);
     const dim3 grid((unsigned)ncol, (unsigned)((nbr + nblk - 1) / nblk), (unsigned)slices);
     const int nb_i = (int)nblk;
+    // 8 token rows per thread (4 measured slower at 8 waves per workgroup and
+    // 4-5 waves per SIMD: config 4's dY 81 vs 76 us, its fp8 activation 35 vs
+    // 32 us)
+    constexpr int RF = 8, RB = 8;
     if (x_dtype == PRATCHYA_DT_BF16 && scaled)
-      hipLaunchKernelGGL((k_quant_128x1_rows<IN_BF16S>), grid, dim3(256), 0, stream, xb, x_sc8, x_sc32, kg_shift, T,
+      hipLaunchKernelGGL((k_quant_128x1_rows<IN_BF16S, RB>), grid, dim3(rows_threads(RB)), 0, stream, xb, x_sc8, x_sc32, kg_shift, T,
                          C, nb_i, xt_fp8, sc_fp8, sc_fp32);
     else if (x_dtype == PRATCHYA_DT_BF16)
-      hipLaunchKernelGGL((k_quant_128x1_rows<IN_BF16>), grid, dim3(256), 0, stream, xb, nullptr, nullptr, 0, T, C,
+      hipLaunchKernelGGL((k_quant_128x1_rows<IN_BF16, RB>), grid, dim3(rows_threads(RB)), 0, stream, xb, nullptr, nullptr, 0, T, C,
                          nb_i, xt_fp8, sc_fp8, sc_fp32);
     else if (x_dtype == PRATCHYA_DT_F32)
-      hipLaunchKernelGGL((k_quant_128x1_rows<IN_F32>), grid, dim3(256), 0, stream, xb, nullptr, nullptr, 0, T, C,
+      hipLaunchKernelGGL((k_quant_128x1_rows<IN_F32, RB>), grid, dim3(rows_threads(RB)), 0, stream, xb, nullptr, nullptr, 0, T, C,
                          nb_i, xt_fp8, sc_fp8, sc_fp32);
     else
-      hipLaunchKernelGGL((k_quant_128x1_rows<IN_FP8>), grid, dim3(256), 0, stream, xb, x_sc8, x_sc32, kg_shift, T,
+      hipLaunchKernelGGL((k_quant_128x1_rows<IN_FP8, RF>), grid, dim3(rows_threads(RF)), 0, stream, xb, x_sc8, x_sc32, kg_shift, T,
                          C, nb_i, xt_fp8, sc_fp8, sc_fp32);
   } else if (x_dtype == PRATCHYA_DT_BF16 && scaled) {
     hipLaunchKernelGGL((k_quant_t128<IN_BF16S, true, 16>), grid_for_tok(16), dim3(256), 0, stream, xb, x_sc8, x_sc32, kg_shift,

@@ -217,3 +217,32 @@ def test_scales_rejected_for_f32_input():
     x = torch.zeros((128, 128), device="cuda")
     with pytest.raises(ValueError, match="input scales"):
         _K().quantize_t128(x, torch.zeros(16, dtype=torch.uint8, device="cuda"), torch.ones(2, device="cuda"))
+
+
+@pytest.mark.parametrize("kind,T,C", [("bf16", 32768, 2048), ("f32", 32768, 2048), ("fp8", 32768, 2048),
+                                      ("bf16_scaled", 16384, 4096), ("bf16", 65536, 1032)])
+def test_rows_layout_equals_transposed_at_size(kind, T, C):
+    """Sizes where a workgroup of the row-layout kernel walks 2 or more token
+    blocks (and, with 1032 channels, a partial last column): every byte of
+    quantize_128x1 against quantize_t128's (oracle-checked above) transposed
+    back, and the same scales."""
+    print(f"rows vs transposed {kind} [{T},{C}]", flush=True)
+    K = _K()
+    g = torch.Generator(device="cuda").manual_seed(T + C)
+    x = torch.randn((T, C), generator=g, device="cuda")
+    x[:, 3] *= 40.0
+    if kind == "f32":
+        args = (x,)
+    elif kind == "bf16":
+        args = (x.to(torch.bfloat16),)
+    elif kind == "fp8":
+        args = K.quantize(x.to(torch.bfloat16), (1, 128))
+    else:
+        y8 = K.quantize((x * 3).to(torch.bfloat16), (1, 128))
+        args = ((x * 1e-3).to(torch.bfloat16), y8[1], y8[2])
+    xt, s8, s32 = K.quantize_t128(*args)
+    xr, q8, q32 = K.quantize_128x1(*args)
+    torch.cuda.synchronize()
+    assert torch.equal(u8_dev(q8), u8_dev(s8)), "e8m0 bytes differ"
+    assert torch.equal(q32.view(torch.int32), s32.view(torch.int32)), "group maxima differ"
+    assert torch.equal(u8_dev(xr), u8_dev(xt).T), "payloads differ"

@@ -183,19 +183,24 @@ __global__ __launch_bounds__(GT ? 512 : 256) void k_quant_t128(const uint8_t* __
       const uint32_t blk = (uint32_t)(s * T + (int64_t)by * 1024 + i) * nbr + cb;
       sdq[0][i] = e8m0_decode(x_sc8[blk]) * x_sc32[blk >> kg_shift];
     }
-  } else if constexpr (SCALED) {
-    const uint32_t nbr = (uint32_t)(C >> 7);
-    const uint32_t cb0 = bx * NB;
-    for (int i = (int)threadIdx.x; i < NB * 128; i += 256) {
-      const uint32_t b = (uint32_t)i >> 7, row = (uint32_t)i & 127u;
-      float v = 0.0f;
-      if (cb0 + b < nbr) {
-        const uint32_t blk = (uint32_t)(s * T + tb * 128 + row) * nbr + cb0 + b;
-        v = e8m0_decode(x_sc8[blk]) * x_sc32[blk >> kg_shift];
-      }
-      sdq[b][row] = v;
-    }
   }
+  // (not GT) staged after the payload loads are issued, so that the two
+  // round trips to memory overlap
+  auto stage_scales = [&]() {
+    if constexpr (SCALED && !GT) {
+      const uint32_t nbr = (uint32_t)(C >> 7);
+      const uint32_t cb0 = bx * NB;
+      for (int i = (int)threadIdx.x; i < NB * 128; i += 256) {
+        const uint32_t b = (uint32_t)i >> 7, row = (uint32_t)i & 127u;
+        float v = 0.0f;
+        if (cb0 + b < nbr) {
+          const uint32_t blk = (uint32_t)(s * T + tb * 128 + row) * nbr + cb0 + b;
+          v = e8m0_decode(x_sc8[blk]) * x_sc32[blk >> kg_shift];
+        }
+        sdq[b][row] = v;
+      }
+    }
+  };
 
   uint32_t w[TOK][NW];
   if constexpr (GT) {
@@ -222,13 +227,19 @@ __global__ __launch_bounds__(GT ? 512 : 256) void k_quant_t128(const uint8_t* __
     __shared__ __attribute__((aligned(16))) uint8_t tile[128 * kPitch];
     const int64_t cw = (int64_t)bx * 128;
     const uint8_t* xt = x + (s * T + tb * 128) * C + cw;
+    uint4 v[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int q = i * 256 + (int)threadIdx.x, row = q >> 3, cc = (q & 7) * 16;
-      const uint4 v = load_stream16(reinterpret_cast<const char*>(xt + (int64_t)row * C + cc));
+      v[i] = load_stream16(reinterpret_cast<const char*>(xt + (int64_t)row * C + cc));
+    }
+    stage_scales();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = i * 256 + (int)threadIdx.x, row = q >> 3, cc = (q & 7) * 16;
       uint2* d = reinterpret_cast<uint2*>(tile + row * kPitch + cc);
-      d[0] = make_uint2(v.x, v.y);
-      d[1] = make_uint2(v.z, v.w);
+      d[0] = make_uint2(v[i].x, v[i].y);
+      d[1] = make_uint2(v[i].z, v[i].w);
     }
     __syncthreads();
     const int lc = (int)(threadIdx.x >> 6) * 32 + cg * 8;   // the lane's first channel in the tile
@@ -245,6 +256,7 @@ __global__ __launch_bounds__(GT ? 512 : 256) void k_quant_t128(const uint8_t* __
       for (int r = 0; r < TOK; ++r) load_row<IN>(xr + (int64_t)r * C * ESZ, w[r]);
     }
     if constexpr (SCALED) {
+      stage_scales();
       __syncthreads();                       // the staged scales are visible
       if (c0 >= C) return;
     }

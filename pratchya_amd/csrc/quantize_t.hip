@@ -185,7 +185,9 @@ __global__ __launch_bounds__(GT ? 512 : 256) void k_quant_t128(const uint8_t* __
     }
   }
   // (not GT) staged after the payload loads are issued, so that the two
-  // round trips to memory overlap
+  // round trips to memory overlap (for GT, staging the 1024 rows' scales
+  // after the loads measured slower: 132 vs 123 us on a scaled [32768, 4096]
+  // cotangent)
   auto stage_scales = [&]() {
     if constexpr (SCALED && !GT) {
       const uint32_t nbr = (uint32_t)(C >> 7);

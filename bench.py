@@ -25,6 +25,7 @@ METRIC = "block-scaled FP8 GEMM TFLOP/s + quantize GB/s, as % of MI355X peak (1 
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
 BF16_PEAK_TFLOPS = 2500.0
+F32_PEAK_TFLOPS = 157.3
 
 # Algorithmic bytes of config 2 (bf16 in, e4m3fn out, e8m0 per block, f32 per group)
 CFG2_ROWS, CFG2_COLS = 16384, 2048
@@ -648,6 +649,11 @@ def bench_optimizer(steps: int):
     gram_nt_ms = _event_ms(lambda: K.gemm_bf16_nt(xt, xt), 10)
     gram_flop = 2 * din * dout * min(din, dout)
     upd_ms = _event_ms(lambda: K.apply_update(u, False, 128.0, sl(p_t), tg, bf, 0.05, 0.005, bf), 10)
+    # a 2-D quantized leaf runs in f32 (_optimizer.py:155-199): Newton-Schulz
+    # of an f32 [4096, 4096] slice on the f32 products over exact bf16 pieces
+    c32 = torch.randn((CFG5_D, CFG5_D), generator=gen, device="cuda") * 1e-3
+    ns32_ms = _event_ms(lambda: newton_schulz(c32, 5), 3)
+    ns32_flop = 5 * 4 * CFG5_D ** 3
     mom_bytes = n * (1 + 1 + 2 + 2)          # fp8 momentum + fp8 gradient in, bf16 c + bf16 new momentum out
     upd_bytes = n * (2 + 1 + 2)              # bf16 u + fp8 parameter in, bf16 update out
     leaf_ns_flop = 5 * 4 * min(din, dout) ** 2 * max(din, dout)
@@ -672,6 +678,15 @@ def bench_optimizer(steps: int):
                                                   "0.5B combination in the second product's epilogue); flop "
                                                   "counts both products in full, as the reference computes "
                                                   "them"},
+            "f32_leaf_newton_schulz": {"ms": round(ns32_ms, 3), "shape": f"f32 [{CFG5_D},{CFG5_D}]",
+                                       "f32_TFLOP/s": round(ns32_flop / (ns32_ms * 1e-3) / 1e12, 1),
+                                       "frac_of_f32_peak": round(ns32_flop / (ns32_ms * 1e-3) / 1e12
+                                                                 / F32_PEAK_TFLOPS, 4),
+                                       "flop": ns32_flop,
+                                       "kernels": "pratchya_ns_normalize_f32, then per iteration two f32 "
+                                                  "products on the bf16 MFMA kernel over exact bf16 pieces "
+                                                  "(pratchya_split_pack_bf16 + pratchya_gemm_bf16_nt, six bf16 "
+                                                  "MACs per f32 MAC) and pratchya_ns_combine; flop as f32"},
             "ffn_down_gram_product": {"us": round(gram_ms * 1e3, 1),
                                       "frac_of_bf16_peak": round(gram_flop / (gram_ms * 1e-3) / 1e12
                                                                  / BF16_PEAK_TFLOPS, 4),

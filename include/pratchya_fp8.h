@@ -367,6 +367,14 @@ int64_t pratchya_ns_normalize_workspace_bytes(void);
 int pratchya_ns_normalize(const void* g, void* x, int64_t n, void* workspace, int64_t workspace_bytes,
                           hipStream_t stream);
 
+/* The same normalization of an f32 input (_optimizer.py:17 on the f32 leaves
+ * of 2-D quantized parameters, _optimizer.py:157-163): each square rounded to
+ * f32, their f32 sum (the fixed order of pratchya_ns_normalize), sqrt and the
+ * sum with 1e-7 in f32, IEEE f32 quotients.  g, x: f32 [n], 16-byte aligned;
+ * x may be g; workspace as pratchya_ns_normalize. */
+int pratchya_ns_normalize_f32(const float* g, float* x, int64_t n, void* workspace, int64_t workspace_bytes,
+                              hipStream_t stream);
+
 /* One Newton-Schulz step on the bf16 MFMA kernel: C = 1.5 X - 0.5 bf16(A . B^T),
  * the product of pratchya_gemm_bf16_nt (_optimizer.py:20-22, rounded once to
  * bf16) combined with X in its epilogue exactly as pratchya_ns_combine

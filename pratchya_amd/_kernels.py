@@ -720,20 +720,21 @@ def transpose_b16(x: torch.Tensor) -> torch.Tensor:
 
 
 def ns_normalize(g: torch.Tensor) -> torch.Tensor:
-    """``g / (||g||_F + 1e-7)`` for a bf16 ``g`` with the roundings of the
-    bf16 jnp expression (pratchya/_nnx_impl/_optimizer.py:17): the squares, their
-    sum, the square root, the sum with 1e-7 and every quotient rounded to bf16
-    (the sum accumulated in f32 in a fixed order).  Returns a new contiguous
-    tensor of g's shape."""
+    """``g / (||g||_F + 1e-7)`` (pratchya/_nnx_impl/_optimizer.py:17) in g's
+    dtype.  bf16: the roundings of the bf16 jnp expression -- the squares,
+    their sum, the square root, the sum with 1e-7 and every quotient rounded
+    to bf16; f32: f32 squares, sum, square root and quotients.  The sum is
+    accumulated in f32 in a fixed order.  Returns a new contiguous tensor of
+    g's shape."""
     _require_gpu(g)
-    if g.dtype != torch.bfloat16:
-        raise ValueError("ns_normalize: g must be bfloat16")
+    if g.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("ns_normalize: g must be bfloat16 or float32")
     gc = g.contiguous()
     out = torch.empty_like(gc)
     lib = _lib.load()
     ws = torch.empty(int(lib.pratchya_ns_normalize_workspace_bytes()), dtype=torch.uint8, device=gc.device)
-    _lib.check(lib.pratchya_ns_normalize(_ptr(gc), _ptr(out), gc.numel(), _ptr(ws), ws.numel(), _stream(gc)),
-               "ns_normalize")
+    fn = lib.pratchya_ns_normalize if g.dtype == torch.bfloat16 else lib.pratchya_ns_normalize_f32
+    _lib.check(fn(_ptr(gc), _ptr(out), gc.numel(), _ptr(ws), ws.numel(), _stream(gc)), "ns_normalize")
     return out
 
 

@@ -62,6 +62,7 @@ SIGNATURES = {
     "pratchya_ns_combine": (_c_int, [_c_p, _c_p, _c_p, _c_i64, _c_int, _c_p]),
     "pratchya_ns_normalize_workspace_bytes": (_c_i64, []),
     "pratchya_ns_normalize": (_c_int, [_c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p]),
+    "pratchya_ns_normalize_f32": (_c_int, [_c_p, _c_p, _c_i64, _c_p, _c_i64, _c_p]),
     "pratchya_apply_update": (_c_int, [_c_p, _c_int, _c_int, ctypes.c_float, _c_p, _c_int, _c_p, _c_p,
                                        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, ctypes.c_float,
                                        ctypes.c_float, _c_p, _c_int, _c_p]),

@@ -293,6 +293,50 @@ __global__ __launch_bounds__(256) void k_ns_scale_b16(const uint16_t* x, int64_t
       y[i] = (uint16_t)(pack_bf16x2(bf16_lo(x[i]) / den, 0.0f) & 0xFFFFu);
 }
 
+// The f32 normalization (pratchya/_nnx_impl/_optimizer.py:17 on an f32
+// leaf): each square rounded to f32 (no contraction into the sum), the sum
+// in f32 in the same fixed order as the bf16 pass, sqrt and the sum with
+// 1e-7 in f32, IEEE quotients.
+__global__ __launch_bounds__(256) void k_sumsq_f32(const float* __restrict__ x, int64_t n,
+                                                   float* __restrict__ part) {
+  const int64_t n4 = n / 4;
+  float s = 0.0f;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+    const float4 v = *reinterpret_cast<const float4*>(x + i * 4);
+    s += __fmul_rn(v.x, v.x);
+    s += __fmul_rn(v.y, v.y);
+    s += __fmul_rn(v.z, v.z);
+    s += __fmul_rn(v.w, v.w);
+  }
+  if (blockIdx.x == 0)
+    for (int64_t i = n4 * 4 + threadIdx.x; i < n; i += 256) s += __fmul_rn(x[i], x[i]);
+  __shared__ float ws[4];
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) part[blockIdx.x] = (ws[0] + ws[1]) + (ws[2] + ws[3]);
+}
+
+__global__ __launch_bounds__(256) void k_ns_scale_f32(const float* x, int64_t n, const float* __restrict__ part,
+                                                      float* y) {
+  __shared__ float sden;
+  if (threadIdx.x < 64) {
+    float s = 0.0f;
+    for (int i = (int)threadIdx.x; i < kNormBlocks; i += 64) s += part[i];
+    s = wave_sum(s);
+    if (threadIdx.x == 0) sden = sqrtf(s) + 1e-7f;
+  }
+  __syncthreads();
+  const float den = sden;
+  const int64_t n4 = n / 4;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+    const float4 v = *reinterpret_cast<const float4*>(x + i * 4);
+    *reinterpret_cast<float4*>(y + i * 4) = make_float4(v.x / den, v.y / den, v.z / den, v.w / den);
+  }
+  if (blockIdx.x == 0)
+    for (int64_t i = n4 * 4 + threadIdx.x; i < n; i += 256) y[i] = x[i] / den;
+}
+
 // jnp.sign: +-1 for nonzero, the argument itself for +-0 and NaN.
 __device__ __forceinline__ float sign_of(float x) { return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : x); }
 
@@ -460,6 +504,26 @@ extern "C" int pratchya_ns_normalize(const void* g, void* x, int64_t n, void* wo
   hipLaunchKernelGGL(k_ns_scale_b16, dim3((unsigned)blocks), dim3(256), 0, stream, static_cast<const uint16_t*>(g),
                      n, part, static_cast<uint16_t*>(x));
   return check_launch("ns_normalize");
+}
+
+extern "C" int pratchya_ns_normalize_f32(const float* g, float* x, int64_t n, void* workspace,
+                                         int64_t workspace_bytes, hipStream_t stream) {
+  if (n < 0) return pratchya_set_error(PRATCHYA_EINVAL, "ns_normalize_f32: negative size");
+  if (n == 0) return PRATCHYA_OK;
+  if (!g || !x || !workspace) return pratchya_set_error(PRATCHYA_EINVAL, "ns_normalize_f32: null buffer");
+  if (workspace_bytes < (int64_t)kNormBlocks * 4 || reinterpret_cast<uintptr_t>(workspace) % 4)
+    return pratchya_set_error(PRATCHYA_EINVAL, "ns_normalize_f32: workspace of %lld bytes (need %d, 4-byte aligned)",
+                              (long long)workspace_bytes, kNormBlocks * 4);
+  if ((reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(x)) % 16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "ns_normalize_f32: g and x must be 16-byte aligned");
+  float* part = static_cast<float*>(workspace);
+  hipLaunchKernelGGL(k_sumsq_f32, dim3(kNormBlocks), dim3(256), 0, stream, g, n, part);
+  int rc = check_launch("ns_normalize_f32");
+  if (rc) return rc;
+  const int64_t chunks = n / 4;
+  const int64_t blocks = chunks / 256 + 1 < 4096 ? chunks / 256 + 1 : 4096;
+  hipLaunchKernelGGL(k_ns_scale_f32, dim3((unsigned)blocks), dim3(256), 0, stream, g, n, part, x);
+  return check_launch("ns_normalize_f32");
 }
 
 extern "C" int pratchya_apply_update(const void* u, int u_dtype, int use_sign, float scale, const void* p,

@@ -13,8 +13,9 @@ Per quantized leaf the step is
     momentum from the quantized momentum and gradient in one kernel, the new
     momentum requantized with the parameter's block grid;
   * Muon for 2-D slices not named ``embed_tokens`` / ``lm_head``:
-    ``newton_schulz(c)`` (5 iterations of two GEMMs: bf16 on the bf16 MFMA
-    kernel, f32 on the BLAS library), scaled by ``sqrt(max(N, M))``; Lion
+    ``newton_schulz(c)`` (5 iterations of two GEMMs on the hand-written MFMA
+    kernel: bf16 directly, f32 over exact bf16 pieces), scaled by
+    ``sqrt(max(N, M))``; Lion
     otherwise: ``sign(c)``;
   * the update pass on the GPU (``pratchya_apply_update``):
     ``-(lr * u + lr * wd * p)`` with the quantized parameter dequantized in
@@ -52,62 +53,73 @@ def newton_schulz(G: torch.Tensor, steps: int = 5) -> torch.Tensor:
     """Orthogonalization by the cubic Newton-Schulz iteration
     (``_optimizer.py:11-29``): ``X = G / (||G||_F + 1e-7)`` (the transpose of a
     tall ``G``), then ``steps`` times ``X = 1.5 X - 0.5 (X X^T) X``, in ``G``'s
-    dtype.  bf16 products run on the bf16 MFMA kernel (``pratchya_gemm_bf16_nt``;
-    the Gram product on ``pratchya_gemm_bf16_gram`` where its side is a
-    multiple of 256) and the normalization on ``pratchya_ns_normalize``, others
-    on the BLAS library (f32 accumulation) and torch."""
-    m, n = G.shape
+    dtype (bf16 for layer-stacked leaves, f32 for 2-D leaves, the two dtypes
+    the optimizer passes; others are a ``TypeError``).  Everything runs on the
+    hand-written kernels: the normalization on ``pratchya_ns_normalize``;
+    bf16 products on the bf16 MFMA kernel (``pratchya_gemm_bf16_gram`` for
+    the symmetric product where its side is a multiple of 256,
+    ``pratchya_gemm_bf16_nt`` otherwise, ``pratchya_gemm_bf16_nt_ns`` for the
+    second product with the combination in its epilogue); f32 products on the
+    same kernel over exact bf16 pieces (``_kernels.matmul_f32``, f32
+    accuracy) with ``pratchya_ns_combine``."""
+    if G.dim() != 2:
+        raise ValueError(f"newton_schulz: a 2-D array is required, got shape {tuple(G.shape)}")
+    if G.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"newton_schulz: bfloat16 or float32 expected, got {G.dtype}")
+    m, n = (int(d) for d in G.shape)
     transpose = m > n
-    # A tall G is iterated untransposed: with Y = X^T = G / (||G|| + eps),
-    # X X^T = Y^T Y and ((X X^T) X)^T = Y (Y^T Y) (X X^T is symmetric), so
-    # Y <- 1.5 Y - 0.5 Y (Y^T Y) is the transposed iteration without the two
-    # transposing copies.  Y stays row-major, and the library reads the
-    # transposed operand in place (2-D TN / NT GEMMs).
-    X = G.contiguous()
-    # bf16 leaves run both products on the bf16 MFMA kernel (NT form: rows of
-    # both operands K-contiguous); other dtypes and sizes use the BLAS library
-    # (f32 accumulation either way).
-    on_kernel = X.dtype == torch.bfloat16 and m % 64 == 0 and n % 64 == 0
-    if on_kernel:
-        X = K.ns_normalize(X)                    # one fused two-pass kernel pair
-    else:
-        X = X / (torch.sqrt(torch.sum(X * X)) + 1e-7)
-    fused = X.dtype in (torch.bfloat16, torch.float32)
+    X = K.ns_normalize(G)                        # one fused two-pass kernel pair
+    if m == 0 or n == 0:
+        return X
+    if X.dtype == torch.float32:
+        # A tall G is iterated untransposed: with Y = X^T, X X^T = Y^T Y and
+        # ((X X^T) X)^T = Y (Y^T Y), so Y <- 1.5 Y - 0.5 Y (Y^T Y) is the
+        # transposed iteration without the transposes.
+        for _ in range(steps):
+            if transpose:
+                A = K.matmul_f32(X, X, a_t=True)      # X^T X   [n, n]
+                B = K.matmul_f32(X, A)                # X A     [m, n]
+            else:
+                A = K.matmul_f32(X, X, b_t=True)      # X X^T   [m, m]
+                B = K.matmul_f32(A, X)                # A X     [m, n]
+            X = K.ns_combine(X, B, out=X)
+        return X
+    # bf16: the kernel takes sides that are multiples of 64, so the iterate
+    # is zero-padded to them; the pad rows and columns stay exactly zero
+    # through every product and combination, and the products over the
+    # original block are sums of the same bf16 products (plus exact zeros)
+    mp, npad = -(-m // 64) * 64, -(-n // 64) * 64
+    padded = (mp, npad) != (m, n)
+    if padded:
+        Xp = torch.zeros((mp, npad), dtype=X.dtype, device=X.device)
+        Xp[:m, :n] = X
+        X = Xp
     # the Gram product computes only its upper-triangle tiles (exactly
     # symmetric result) where its side is a multiple of 256; a tall iterate
     # is read K-major by it, with no transposed copy
-    gram_side = n if transpose else m
+    gram_side = npad if transpose else mp
     gram_ok = gram_side % 256 == 0
     for _ in range(steps):
-        # on the kernel, the second product's epilogue also forms
-        # 1.5 X - 0.5 B (the bits of ns_combine), into a new buffer
-        if on_kernel and transpose:
+        # the second product's epilogue also forms 1.5 X - 0.5 B (the bits
+        # of ns_combine), into a new buffer
+        if transpose:
             if gram_ok:
                 A = K.gemm_bf16_gram(X, k_major=True)    # X^T X     [n, n]
             else:
                 Xt = K.transpose_b16(X)                  # [n, m]
                 A = K.gemm_bf16_nt(Xt, Xt)
             X = K.gemm_bf16_nt_ns(X, A, X)           # 1.5 X - 0.5 X A (A = A^T)
-            continue
-        elif on_kernel:
+        else:
             A = K.gemm_bf16_gram(X) if gram_ok else K.gemm_bf16_nt(X, X)   # X X^T [m, m]
             # 1.5 X - 0.5 A X: a wide X is read K-major (no transposed copy);
             # for a square one the copy is cheaper than the K-major read
             # (measured: [4096, 4096] 1.08 vs 1.13 ms, [4096, 16384] 3.83 vs
             # 3.74 ms for 5 iterations)
-            if n > m:
+            if npad > mp:
                 X = K.gemm_bf16_nt_ns(A, X, X, b_k_major=True)
             else:
                 X = K.gemm_bf16_nt_ns(A, K.transpose_b16(X), X)
-            continue
-        elif transpose:
-            A = X.T @ X
-            B = X @ A
-        else:
-            A = X @ X.T
-            B = A @ X
-        X = K.ns_combine(X, B, out=X) if fused else 1.5 * X - 0.5 * B
-    return X
+    return X[:m, :n].contiguous() if padded else X
 
 
 class MiulionState(NamedTuple):

@@ -21,7 +21,8 @@ quantize backward would produce -- straight to that tensor.
 
 GEMM backward.  ``matmul_impl``'s reference backward contracts the f32
 cotangent with the dequantized operands in f32 (Q:621-622) and is the default
-here ("f32": dequantize kernels plus an f32 library GEMM).  The "fp8" mode
+here ("f32": dequantize kernels plus the f32 product on the bf16 MFMA
+kernel over exact bf16 pieces).  The "fp8" mode
 (``set_matmul_backward("fp8")``) runs dgrad and wgrad on the FP8 MFMA kernel
 instead, with the cotangent quantized (1, 128) for dgrad and both wgrad
 operands requantized along the token axis (128, 1) -- the scheme of

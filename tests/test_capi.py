@@ -393,6 +393,13 @@ def test_ns_normalize_argument_codes_without_gpu():
     assert b"workspace" in lib.pratchya_last_error()
     assert lib.pratchya_ns_normalize(ctypes.c_void_p((1 << 20) + 2), fake, 64, fake, ws_bytes, None) == _lib.EINVAL
     assert b"aligned" in lib.pratchya_last_error()
+    # the f32 form: the same argument checks
+    assert lib.pratchya_ns_normalize_f32(fake, fake, 0, None, 0, None) == 0
+    assert lib.pratchya_ns_normalize_f32(fake, None, 64, fake, ws_bytes, None) == _lib.EINVAL
+    assert lib.pratchya_ns_normalize_f32(fake, fake, 64, fake, ws_bytes - 4, None) == _lib.EINVAL
+    assert b"workspace" in lib.pratchya_last_error()
+    assert lib.pratchya_ns_normalize_f32(ctypes.c_void_p((1 << 20) + 8), fake, 64, fake, ws_bytes, None) == _lib.EINVAL
+    assert b"aligned" in lib.pratchya_last_error()
 
 
 def test_gemm_bf16_ns_argument_codes_without_gpu():

@@ -8,6 +8,8 @@ newton_schulz (pratchya/_nnx_impl/_optimizer.py:11-29: ``A = X @ X.T``,
   relative per element, plus the f32 error); exact sums bit for bit (small
   integers); edge tiles (M, N not multiples of 256, operands below 256 rows).
 * pratchya_transpose_b16: bit for bit against torch's transpose copy.
+* pratchya_ns_normalize_f32: quotients bit for bit against the host's f32
+  expression for a denominator within 64 ulps of the host's.
 * newton_schulz on the kernel: against the oracle at (1024, 2048) and
   (2048, 1024) within the bf16 tolerance of the optimizer tests (3e-2), and at
   the [16384, 4096] leaf against the BLAS-library iteration (same tolerance).
@@ -140,6 +142,30 @@ def test_ns_normalize_roundings(shape):
     again = K.ns_normalize(g)
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), again.view(torch.int16))
+
+
+@pytest.mark.parametrize("shape", [(1024, 1024), (999, 7), (3, 5)], ids=lambda s: "x".join(map(str, s)))
+def test_ns_normalize_f32(shape):
+    """pratchya_ns_normalize_f32 against the f32 expression on the host: the
+    denominator is sqrt(sum of f32 squares) + 1e-7 in f32, where the kernel's
+    f32 sum (a fixed order) may differ from the host's f64 sum in its last
+    bits, so every f32 denominator within 64 ulps of the host's is tried; the
+    quotients must then match bit for bit for one of them.  Deterministic."""
+    K = _K()
+    rng = np.random.default_rng(31)
+    G = (rng.standard_normal(shape) * 1e-3).astype(np.float32)
+    g = torch.from_numpy(G).cuda()
+    got = K.ns_normalize(g)
+    torch.cuda.synchronize()
+    out = got.cpu().numpy()
+    sq = (G * G).astype(np.float32)
+    den64 = np.float32(np.sqrt(np.float32(sq.astype(np.float64).sum())) + np.float32(1e-7))
+    bits = np.array([den64], np.float32).view(np.int32)[0]
+    cands = np.arange(bits - 64, bits + 65, dtype=np.int32).view(np.float32)
+    assert any(np.array_equal((G / d).astype(np.float32).view(np.uint32), out.view(np.uint32)) for d in cands)
+    again = K.ns_normalize(g)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int32), again.view(torch.int32))
 
 
 @pytest.mark.parametrize("shape", [(1024, 2048), (2048, 1024)])

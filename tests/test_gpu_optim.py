@@ -6,8 +6,11 @@
   momentum's payload and scales bit-exact.
 * pratchya_apply_update: bit-exact (Lion and Muon forms, fp8 / bf16 / f32
   parameters).
-* newton_schulz on the BLAS library: relative Frobenius error <= 1e-4 (f32)
-  and <= 3e-2 (bf16) against the oracle (summation order differs).
+* newton_schulz on the hand-written kernels (bf16 MFMA products; f32 products
+  over exact bf16 pieces): relative Frobenius error <= 1e-4 (f32) and
+  <= 3e-2 (bf16) against the oracle (summation order differs), for aligned,
+  unaligned, tall and wide slices and at config 5's [16384, 4096] leaf; with
+  torch's products disabled, so that no library GEMM takes part.
 * A two-step miulion_optimizer update over a tree with a layer-stacked (3-D,
   bf16) leaf, a 2-D (f32) Muon leaf, an embed_tokens (Lion) leaf and a plain
   1-D leaf: momentum triples bit-exact; Lion updates bit-exact; Muon updates
@@ -141,9 +144,25 @@ def test_ns_combine_kernel(n, dtype):
     assert_f32_bits_equal(_host(got), OO.ns_combine(X, B, dtype), f"ns_combine {dtype} n={n}")
 
 
-@pytest.mark.parametrize("shape", [(256, 384), (384, 256)])
+@pytest.fixture
+def no_library_products(monkeypatch):
+    """torch's matrix products raise: a product that is not on the
+    hand-written kernels fails the test."""
+    def refuse(*a, **k):
+        raise AssertionError("a torch matrix product was called")
+    for name in ("matmul", "mm", "bmm", "einsum", "addmm", "baddbmm", "tensordot", "inner", "dot"):
+        monkeypatch.setattr(torch, name, refuse)
+    for name in ("__matmul__", "__rmatmul__", "matmul", "mm", "bmm", "addmm"):
+        monkeypatch.setattr(torch.Tensor, name, refuse)
+    monkeypatch.setattr(torch.nn.functional, "linear", refuse)
+
+
+NS_SHAPES = [(256, 384), (384, 256), (100, 37), (37, 100), (70, 65), (1, 130), (512, 512), (300, 1024)]
+
+
+@pytest.mark.parametrize("shape", NS_SHAPES, ids=lambda s: "x".join(map(str, s)))
 @pytest.mark.parametrize("dtype,tol", [("float32", 1e-4), ("bfloat16", 3e-2)])
-def test_newton_schulz(shape, dtype, tol):
+def test_newton_schulz(shape, dtype, tol, no_library_products):
     from pratchya_amd.optim import newton_schulz
     rng = np.random.default_rng(21)
     G = (rng.standard_normal(shape) * 1e-3).astype(np.float32)
@@ -151,9 +170,33 @@ def test_newton_schulz(shape, dtype, tol):
         G = O.bf16_round(G)
     got = newton_schulz(torch.from_numpy(G).cuda().to(TDT[dtype]), 5)
     torch.cuda.synchronize()
-    assert got.dtype == TDT[dtype] and tuple(got.shape) == shape
+    assert got.dtype == TDT[dtype] and tuple(got.shape) == shape and got.is_contiguous()
     want = OO.newton_schulz(G, 5, dtype)
     assert O.rel_fro(_host(got), want) <= tol
+
+
+@pytest.mark.parametrize("dtype,tol", [("float32", 1e-4), ("bfloat16", 3e-2)])
+def test_newton_schulz_config5_leaf_against_oracle(dtype, tol, no_library_products):
+    """Config 5's FFN weight shape [16384, 4096] (the tall iteration, K-major
+    Gram product for bf16): against the oracle's f64-accumulated iteration
+    with the same roundings (about 5.5 TFLOP of host f64 BLAS)."""
+    from pratchya_amd.optim import newton_schulz
+    rng = np.random.default_rng(24)
+    G = (rng.standard_normal((16384, 4096)) * 1e-3).astype(np.float32)
+    if dtype == "bfloat16":
+        G = O.bf16_round(G)
+    got = newton_schulz(torch.from_numpy(G).cuda().to(TDT[dtype]), 5)
+    torch.cuda.synchronize()
+    want = OO.newton_schulz(G, 5, dtype)
+    assert O.rel_fro(_host(got), want) <= tol
+
+
+def test_newton_schulz_rejects_other_dtypes():
+    from pratchya_amd.optim import newton_schulz
+    with pytest.raises(TypeError):
+        newton_schulz(torch.zeros((64, 64), dtype=torch.float16, device="cuda"))
+    with pytest.raises(ValueError):
+        newton_schulz(torch.zeros((2, 64, 64), dtype=torch.float32, device="cuda"))
 
 
 def _np_triple(q):
@@ -178,7 +221,7 @@ def _oracle_leaf(path, g, m, p, tgrid, dtype, lion_lr, muon_lr, wd):
     return upd, nm
 
 
-def test_miulion_two_steps():
+def test_miulion_two_steps(no_library_products):
     from pratchya_amd.optim import MiulionHyperParams, MiulionScheduler, miulion_optimizer
     from pratchya_amd.qarr import QArrayImpl
     torch.manual_seed(0)

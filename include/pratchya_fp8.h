@@ -318,9 +318,12 @@ int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, con
  * pratchya_gemm_bs_nt to f32 followed by pratchya_quantize_dequantize bit for
  * bit.  workspace: pratchya_gemm_bs_nt_fq_workspace_bytes(M, N) bytes, 4-byte
  * aligned, cleared by a kernel of this call (calls sharing one workspace must
- * not overlap); its last word is set to 1 if the kernel's bounded wait for a
- * group's four tiles ran out (never expected: results are then invalid). */
+ * not overlap); the 32-bit word at byte pratchya_gemm_bs_nt_fq_status_offset(M,
+ * N) of it is set to 1 if the kernel's bounded wait for a group's four tiles
+ * ran out (never expected: that group's outputs are then NaN), else left 0;
+ * the caller reads it after the call has completed (-1: unsupported shape). */
 int64_t pratchya_gemm_bs_nt_fq_workspace_bytes(int64_t M, int64_t N);
+int64_t pratchya_gemm_bs_nt_fq_status_offset(int64_t M, int64_t N);
 int pratchya_gemm_bs_nt_fq(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, const float* a_sc32,
                            int64_t a_rdiv, int64_t a_sr, int64_t a_sk, int64_t a_kg,
                            const uint8_t* B, int64_t ldb, const uint8_t* b_sc8, const float* b_sc32,
@@ -404,10 +407,13 @@ int pratchya_gemm_bf16_nt_ns(const void* A, int64_t lda, const void* B, int64_t 
  * multiple of 8, 16-byte aligned; M a multiple of 256 and K of 64
  * (PRATCHYA_EUNSUPPORTED otherwise).  C: bf16 [M, M] (ldc), not overlapping A.  workspace: device memory of
  * pratchya_gemm_bf16_gram_workspace_bytes(M, K) bytes (f32 partial tiles and
- * flags, ~64 MB on a 256-CU device), 16-byte aligned; its last word is set to
- * 1 if a partial tile did not arrive in time (that tile is then NaN).  Calls
- * that share a workspace must not overlap. */
+ * flags, ~64 MB on a 256-CU device), 16-byte aligned; the 32-bit word at byte
+ * pratchya_gemm_bf16_gram_status_offset(M, K) of it is set to 1 if a partial
+ * tile did not arrive in time (that tile is then NaN), else left 0; the
+ * caller reads it after the call has completed (-1: unsupported shape).
+ * Calls that share a workspace must not overlap. */
 int64_t pratchya_gemm_bf16_gram_workspace_bytes(int64_t M, int64_t K);
+int64_t pratchya_gemm_bf16_gram_status_offset(int64_t M, int64_t K);
 int pratchya_gemm_bf16_gram(const void* A, int64_t lda, int64_t M, int64_t K, int a_kmajor, void* C, int64_t ldc,
                             void* workspace, int64_t workspace_bytes, hipStream_t stream);
 

@@ -6,12 +6,13 @@ the current stream of the tensor's device; there is no CPU path.
 from __future__ import annotations
 
 import ctypes
+import os
 from typing import Tuple
 
 import torch
 
 from . import _lib
-from ._lib import PratchyaError, PratchyaUnsupported  # noqa: F401  (re-exported)
+from ._lib import PratchyaError, PratchyaUnsupported, PratchyaWaitTimeout  # noqa: F401  (re-exported)
 
 E4M3 = torch.float8_e4m3fn
 E8M0 = torch.float8_e8m0fnu
@@ -738,10 +739,53 @@ def ns_normalize(g: torch.Tensor) -> torch.Tensor:
     return out
 
 
+# The Gram product and the requantizing GEMM exchange data between
+# workgroups with bounded waits; a wait that runs out sets a status word in
+# the call's workspace (and NaN in the outputs concerned) instead of hanging.
+# With checks on (check_waits(True), or PRATCHYA_CHECK_WAITS=1 in the
+# environment) each such call synchronizes its stream and raises
+# PratchyaWaitTimeout when the word is set (not while the stream is being
+# captured into a graph); either call also copies the word into a caller's
+# ``status`` tensor (int32, on the device, no sync).
+_CHECK_WAITS = os.environ.get("PRATCHYA_CHECK_WAITS", "0") not in ("", "0")
+
+
+def check_waits(enable: bool = True) -> bool:
+    """Turn the synchronous status check of the bounded waits on or off;
+    returns the previous setting."""
+    global _CHECK_WAITS
+    prev, _CHECK_WAITS = _CHECK_WAITS, bool(enable)
+    return prev
+
+
+def _wait_status(ws: torch.Tensor, offset: int, status, what: str) -> None:
+    word = ws[offset:offset + 4].view(torch.int32)
+    if status is not None:
+        if status.dtype != torch.int32 or status.device != ws.device or status.numel() < 1:
+            raise ValueError(f"{what}: status must be an int32 tensor on {ws.device}")
+        status.view(-1)[:1].copy_(word)
+    if _CHECK_WAITS and not torch.cuda.is_current_stream_capturing() and int(word.item()) != 0:
+        raise PratchyaWaitTimeout(f"{what}: a bounded wait between workgroups ran out (outputs hold NaN)")
+
+
 _GRAM_WS = {}
 
 
-def gemm_bf16_gram(a: torch.Tensor, k_major: bool = False) -> torch.Tensor:
+def _gram_workspace(device: torch.device, stream) -> torch.Tensor:
+    """The Gram product's workspace for ``stream``: sized once for the largest
+    grid (one range per CU) and never replaced, so that a graph that captured
+    a Gram call keeps a valid workspace whatever later calls need."""
+    key = (device.index, stream.cuda_stream)
+    ws = _GRAM_WS.get(key)
+    if ws is None:
+        # a shape whose grid is one range per CU: the largest workspace
+        big = int(_lib.load().pratchya_gemm_bf16_gram_workspace_bytes(256 * 64, 64 * 4096))
+        ws = torch.empty(big, dtype=torch.uint8, device=device)
+        _GRAM_WS[key] = ws
+    return ws
+
+
+def gemm_bf16_gram(a: torch.Tensor, k_major: bool = False, status: torch.Tensor = None) -> torch.Tensor:
     """The symmetric bf16 product ``a @ a^T`` (f32 accumulation, rounded once
     to bf16) of a bf16 ``a`` [M, K], the Gram product of newton_schulz
     (pratchya/_nnx_impl/_optimizer.py:20-22): only the tiles on and above the
@@ -751,7 +795,8 @@ def gemm_bf16_gram(a: torch.Tensor, k_major: bool = False) -> torch.Tensor:
     a tall iterate, read without a transposed copy).  M must be a multiple of
     256 and K of 64 (``PratchyaUnsupported`` otherwise).  The partial-tile
     workspace is kept per device and stream; calls on one stream run in
-    order."""
+    order.  ``status``: an int32 device tensor that receives the bounded
+    wait's status word (0: every partial tile arrived)."""
     _require_gpu(a)
     if a.dtype != torch.bfloat16 or a.dim() != 2:
         raise ValueError("gemm_bf16_gram: a must be 2-D bfloat16")
@@ -761,15 +806,13 @@ def gemm_bf16_gram(a: torch.Tensor, k_major: bool = False) -> torch.Tensor:
     if ws_bytes <= 0:
         raise PratchyaUnsupported(f"gemm_bf16_gram: M must be a multiple of 256 and K of 64 (got {M}, {Kd})")
     ap = a.contiguous()
-    stream = torch.cuda.current_stream(ap.device)
-    key = (ap.device.index, stream.cuda_stream)
-    ws = _GRAM_WS.get(key)
-    if ws is None or ws.numel() < ws_bytes:
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=ap.device)
-        _GRAM_WS[key] = ws
+    ws = _gram_workspace(ap.device, torch.cuda.current_stream(ap.device))
+    if ws.numel() < ws_bytes:
+        raise PratchyaError(f"gemm_bf16_gram: workspace of {ws.numel()} bytes, {ws_bytes} needed")
     out = torch.empty((M, M), dtype=torch.bfloat16, device=ap.device)
     _lib.check(lib.pratchya_gemm_bf16_gram(_ptr(ap), int(ap.stride(0)), M, Kd, 1 if k_major else 0, _ptr(out), M,
                                            _ptr(ws), int(ws.numel()), _stream(ap)), "gemm_bf16_gram")
+    _wait_status(ws, int(lib.pratchya_gemm_bf16_gram_status_offset(M, Kd)), status, "gemm_bf16_gram")
     return out
 
 
@@ -819,7 +862,8 @@ def mfma_ceiling(a: torch.Tensor, b: torch.Tensor, bf16: bool, iters: int) -> in
     return int(flop.value)
 
 
-def gemm_nt_fq(a: Operand, b: Operand, out_dtype: torch.dtype, fix_nan: bool = False, lead=None):
+def gemm_nt_fq(a: Operand, b: Operand, out_dtype: torch.dtype, fix_nan: bool = False, lead=None,
+               status: torch.Tensor = None):
     """``QArrayImpl(dequant(a) @ dequant(b)^T, (1, 128)).astype(out_dtype)``
     with the requantization in the GEMM's epilogue: returns ``(y [M, N],
     sc_fp8, sc_fp32)`` bit-identical to ``quantize_dequantize(gemm_nt(a, b,
@@ -827,7 +871,8 @@ def gemm_nt_fq(a: Operand, b: Operand, out_dtype: torch.dtype, fix_nan: bool = F
     of the product (its rows are ``prod(lead) * H`` flattened; the scales are
     shaped per slice as quantize_impl returns them).  Raises
     ``PratchyaUnsupported`` unless N is a multiple of 1024 and B's scale
-    groups span at least 32 rows."""
+    groups span at least 32 rows.  ``status``: an int32 device tensor that
+    receives the strip exchange's status word (0: every wait completed)."""
     _require_gpu(a.payload, b.payload)
     if a.k != b.k:
         raise ValueError(f"contraction mismatch: {a.k} vs {b.k}")
@@ -854,6 +899,7 @@ def gemm_nt_fq(a: Operand, b: Operand, out_dtype: torch.dtype, fix_nan: bool = F
                                           _ptr(bp), K, _ptr(bs8), _ptr(bs32), *b.desc,
                                           M, N, K, _ptr(y), N, _dtype_code(out_dtype), 1 if fix_nan else 0,
                                           _ptr(sc8), _ptr(sc32), _ptr(ws), int(ws_bytes), _stream(ap)), "gemm_fq")
+    _wait_status(ws, int(lib.pratchya_gemm_bs_nt_fq_status_offset(M, N)), status, "gemm_fq")
     return y, sc8.view(E8M0), sc32
 
 

@@ -76,6 +76,7 @@ SIGNATURES = {
                                         _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_int, _c_int, _c_p, _c_p,
                                         _c_p, _c_i64, _c_p]),
     "pratchya_gemm_bs_nt_fq_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "pratchya_gemm_bs_nt_fq_status_offset": (_c_i64, [_c_i64, _c_i64]),
     "pratchya_gemm_bs_kmajor": (_c_int, [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
                                          _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
                                          _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_int, _c_p]),
@@ -84,6 +85,7 @@ SIGNATURES = {
     "pratchya_gemm_bf16_nt_ns": (_c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_int, _c_i64, _c_i64, _c_i64, _c_p,
                                           _c_i64, _c_p, _c_i64, _c_p]),
     "pratchya_gemm_bf16_gram_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "pratchya_gemm_bf16_gram_status_offset": (_c_i64, [_c_i64, _c_i64]),
     "pratchya_gemm_bf16_gram": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_p, _c_i64, _c_p]),
     "pratchya_transpose_b16": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "pratchya_split_pack_bf16": (_c_int, [_c_p, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
@@ -106,6 +108,13 @@ class PratchyaError(RuntimeError):
 class PratchyaUnsupported(PratchyaError):
     """A valid request outside what the kernels cover (PRATCHYA_EUNSUPPORTED),
     e.g. a GEMM shape that is not a multiple of its tile."""
+
+
+class PratchyaWaitTimeout(PratchyaError):
+    """A kernel's bounded wait for other workgroups ran out (the status word
+    of pratchya_gemm_bs_nt_fq or pratchya_gemm_bf16_gram): the outputs that
+    depended on it hold NaN.  Never expected while the kernel has the device
+    to itself; reported when wait checks are on (``_kernels.check_waits``)."""
 
 
 def load() -> ctypes.CDLL:

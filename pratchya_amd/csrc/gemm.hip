@@ -1692,6 +1692,12 @@ extern "C" int64_t pratchya_gemm_bs_nt_fq_workspace_bytes(int64_t M, int64_t N) 
   return ((fq_workspace_words(M, N) * 4 + 255) / 256) * 256;
 }
 
+extern "C" int64_t pratchya_gemm_bs_nt_fq_status_offset(int64_t M, int64_t N) {
+  if (M <= 0 || N <= 0 || N % 1024) return -1;
+  const int64_t strips = fq_strips(M, N);
+  return (strips * 256 + strips) * 4;
+}
+
 extern "C" int pratchya_gemm_bs_nt_fq(const uint8_t* A, int64_t lda, const uint8_t* a_sc8,
                                       const float* a_sc32, int64_t a_rdiv, int64_t a_sr, int64_t a_sk,
                                       int64_t a_kg, const uint8_t* B, int64_t ldb, const uint8_t* b_sc8,
@@ -1876,6 +1882,12 @@ extern "C" int64_t pratchya_gemm_bf16_gram_workspace_bytes(int64_t M, int64_t K)
   if (M <= 0 || K <= 0 || M % BM || K % 64) return 0;
   const int64_t G = gram_grid(M, K);
   return G * 8 * (32 * 256) * 4 + (G * 8 + 1) * 4;
+}
+
+extern "C" int64_t pratchya_gemm_bf16_gram_status_offset(int64_t M, int64_t K) {
+  if (M <= 0 || K <= 0 || M % BM || K % 64) return -1;
+  const int64_t G = gram_grid(M, K);
+  return (G * 8 * (32 * 256) + G * 8) * 4;
 }
 
 extern "C" int pratchya_gemm_bf16_gram(const void* A, int64_t lda, int64_t M, int64_t K, int a_kmajor, void* C,

@@ -322,9 +322,15 @@ def _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y, pre=N
             op_g = K.operand_rows(*gq, (1, 128))
             op_w = K.operand_rows(y8, ys8, ys32, gy)          # W [K, N]: rows K, contraction N
             if x_dtype is not None and Kd % 1024 == 0:
-                gxf = K.gemm_nt_fq(op_g, op_w, x_dtype, fix_nan=True)[0]
-                gx_final = True
-            else:
+                try:
+                    gxf = K.gemm_nt_fq(op_g, op_w, x_dtype, fix_nan=True)[0]
+                    gx_final = True
+                except K.PratchyaUnsupported:
+                    # the epilogue requantization takes B scale groups of 32
+                    # rows or more; other weight grids keep the FP8 dgrad with
+                    # the requantization as a separate pass
+                    gxf = None
+            if gxf is None:
                 gxf = K.gemm_nt(op_g, op_w, torch.float32)
             gxf = gxf.reshape(tuple(g.shape[:-1]) + (Kd,))
         if need_y and _wgrad_k_major and Kd <= _WGRAD_K_MAJOR_ROWS:

@@ -27,3 +27,17 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture(autouse=True, scope="session")
+def _check_bounded_waits():
+    """Every requantizing GEMM and Gram product of a GPU test checks its
+    bounded-wait status word: a wait that ran out fails the test
+    (PratchyaWaitTimeout) instead of leaving NaN outputs."""
+    if not _gpu_available():
+        yield
+        return
+    from pratchya_amd import _kernels
+    prev = _kernels.check_waits(True)
+    yield
+    _kernels.check_waits(prev)

@@ -438,3 +438,21 @@ def test_gemm_kmajor_argument_codes_without_gpu():
     assert lib.pratchya_gemm_bs_kmajor(*args(256, 256, 256, 264)) == _lib.EINVAL
     assert lib.pratchya_gemm_bs_kmajor(*args(0, 256, 256, 256)) == _lib.OK
     assert lib.pratchya_gemm_bs_kmajor(*args(-1, 256, 256, 256)) == _lib.EINVAL
+
+
+def test_status_offsets_without_gpu():
+    """The bounded waits' status words: the last word of the requantizing
+    GEMM's workspace layout (maxima, arrival counts, status) and the word
+    after the Gram product's partial tiles and flags; -1 for shapes the
+    calls reject."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    for M, N in ((2048, 2048), (32768, 16384), (300, 1024)):
+        strips = -(-M // 256) * (N // 1024)
+        assert lib.pratchya_gemm_bs_nt_fq_status_offset(M, N) == strips * 257 * 4
+        assert lib.pratchya_gemm_bs_nt_fq_status_offset(M, N) + 4 <= lib.pratchya_gemm_bs_nt_fq_workspace_bytes(M, N)
+    assert lib.pratchya_gemm_bs_nt_fq_status_offset(2048, 1000) == -1
+    for M, Kd in ((4096, 16384), (256, 64), (1024, 2048)):
+        off = lib.pratchya_gemm_bf16_gram_status_offset(M, Kd)
+        assert off > 0 and off + 4 == lib.pratchya_gemm_bf16_gram_workspace_bytes(M, Kd)
+    assert lib.pratchya_gemm_bf16_gram_status_offset(300, 64) == -1

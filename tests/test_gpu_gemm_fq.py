@@ -150,6 +150,7 @@ def test_workspace_status_and_reuse():
         torch.cuda.synchronize()
         outs.append((f32(y), u8(s8), f32(s32)))
         n_words = (M // 256) * (N // 1024) * 257 + 1   # maxima, arrival counts, status
+        assert lib.pratchya_gemm_bs_nt_fq_status_offset(M, N) == (n_words - 1) * 4
         assert int(ws.view(torch.int32)[n_words - 1].item()) == 0, "strip wait ran out"
     assert_f32_bits_equal(outs[0][0], outs[1][0], "repeat values")
     assert_bytes_equal(outs[0][1], outs[1][1], "repeat e8m0")
@@ -194,3 +195,23 @@ def test_fused_linear_forward_and_dgrad(monkeypatch):
         Q.set_matmul_backward(prev)
     for a, b, what in zip(results[0], results[1], ("y", "x.grad", "w.grad")):
         assert_f32_bits_equal(a, b, f"fused vs unfused Linear {what}")
+
+
+def test_status_word_at_ffn_size():
+    """Config 5's FFN up-projection with the requantization in the epilogue
+    ([32768, 4096] x [4096, 16384], 512 strips of four tiles exchanged over
+    32 persistent rounds): the status tensor receives 0 (no bounded wait ran
+    out) and no output is NaN."""
+    K = _K()
+    M, Kd, N = 32768, 4096, 16384
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn((M, Kd), generator=g, device="cuda").to(torch.bfloat16)
+    w = (torch.randn((Kd, N), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    a = K.operand_rows(*K.quantize(x, (1, 128)), (1, 128))
+    b = K.operand_transposed(*K.quantize(w, (128, 128)), (128, 128))
+    del x, w
+    st = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    y, s8, s32 = K.gemm_nt_fq(a, b, torch.bfloat16, status=st)
+    torch.cuda.synchronize()
+    assert int(st.item()) == 0, "strip wait ran out"
+    assert not torch.isnan(y).any()

@@ -118,3 +118,34 @@ def test_gram_two_streams_keep_their_workspaces():
     torch.cuda.synchronize()
     assert torch.equal(ca.view(torch.int16), ref_a.view(torch.int16))
     assert torch.equal(cb.view(torch.int16), ref_b.view(torch.int16))
+
+
+def test_gram_status_word_at_config5_leaf():
+    """The tall [16384, 4096] iterate's Gram product (newton_schulz on config
+    5's FFN weight, K-major): the status word of the bounded partial-tile
+    waits is 0 after the call, on a stream the call shares with no other,
+    and the result equals the NT kernel's within the bf16 tolerance."""
+    K = _K()
+    y = _bf16((16384, 4096), 41, 1.0 / 64)
+    st = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    c = K.gemm_bf16_gram(y, k_major=True, status=st)
+    torch.cuda.synchronize()
+    assert int(st.item()) == 0, "a partial tile of the Gram product did not arrive in time"
+    assert not torch.isnan(c.float()).any()
+    ref = K.gemm_bf16_nt(K.transpose_b16(y), K.transpose_b16(y))
+    torch.cuda.synchronize()
+    err = (c.float() - ref.float()).norm() / ref.float().norm()
+    assert err.item() <= 4e-3
+
+
+def test_gram_workspace_is_fixed_per_stream():
+    """A smaller call after a larger one keeps the same workspace (a graph
+    that captured the larger call would keep writing into it)."""
+    K = _K()
+    K.gemm_bf16_gram(_bf16((4096, 4096), 42))
+    key = (torch.cuda.current_device(), torch.cuda.current_stream().cuda_stream)
+    ws = K._GRAM_WS[key]
+    K.gemm_bf16_gram(_bf16((512, 256), 43))
+    K.gemm_bf16_gram(_bf16((8192, 256), 44))
+    torch.cuda.synchronize()
+    assert K._GRAM_WS[key] is ws

@@ -3,7 +3,8 @@ pratchya_quantize with a caller workspace, through the C ABI: identical
 payload, e8m0 and group-max bytes on two calls in a row (the second with a
 smaller input, so stale scratch contents from the first would show), on
 layouts that take the general path (block maxima in the library's scratch
-array) and one that takes the single-pass kernel (no scratch)."""
+array) and one that takes the single-pass kernel (no scratch); and captured
+in a HIP graph, replayed with new inputs."""
 import ctypes
 
 import pytest
@@ -46,6 +47,43 @@ def _run(x, S, H, W, a, b, noalloc):
 def _same(got, want, what):
     for g, w, name in zip(got, want, ("payload", "e8m0", "group max")):
         assert torch.equal(g.view(torch.uint8), w.view(torch.uint8)), f"{what}: {name} differs"
+
+
+def test_noalloc_inside_graph_replays():
+    """pratchya_quantize_noalloc captured in a HIP graph (the callers it is
+    for), on the general path (block maxima in the shared scratch array,
+    cleared by a fill kernel, no memset node).  Defined first in this file, so
+    that run alone the capture is the process's first call (the scratch
+    address is then resolved during the capture).  Three replays, each after
+    copying a new input in and an eager call on another, smaller input (which
+    leaves other contents in the scratch array), each compared with
+    pratchya_quantize run eagerly on the same input, byte for byte."""
+    L = _lib()
+    lib = L.load()
+    S, H, W, a, b = 1, 2048, 8192, 128, 128
+    n_blk, K, M = _layout(H, W, a, b)
+    g = torch.Generator(device="cuda").manual_seed(43)
+    xs = [(torch.randn((S, H, W), generator=g, device="cuda") * std).to(torch.bfloat16) for std in (1.0, 0.02, 40.0)]
+    x = torch.empty_like(xs[0])
+    q = torch.empty((S * H * W,), dtype=torch.uint8, device="cuda")
+    s8 = torch.empty((S * n_blk,), dtype=torch.uint8, device="cuda")
+    s32 = torch.empty((S * M,), dtype=torch.float32, device="cuda")
+    P = lambda t: ctypes.c_void_p(t.data_ptr())     # noqa: E731
+    x.copy_(xs[0])
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        rc = lib.pratchya_quantize_noalloc(P(x), L.DT_BF16, S, H, W, a, b, P(q), P(s8), P(s32), st)
+    assert rc == 0, lib.pratchya_last_error().decode()
+    small = torch.randn((1, 512, 1024), generator=g, device="cuda").to(torch.bfloat16)
+    for r, xr in enumerate(xs):
+        x.copy_(xr)
+        _run(small, 1, 512, 1024, 128, 128, noalloc=True)        # eager work on the shared scratch
+        graph.replay()
+        torch.cuda.synchronize()
+        want = _run(xr, S, H, W, a, b, noalloc=False)
+        _same((q, s8, s32), want, f"replay {r}")
 
 
 @pytest.mark.parametrize("cases", [

@@ -142,6 +142,86 @@ def test_linear_forward_backward(Q, mode):
     assert rel(f32(w.grad), gw_ref) <= TOL, rel(f32(w.grad), gw_ref)
 
 
+def _linear_reference_grid(xb, wb, gb, blk, out_scales):
+    """The reference Linear (M:46-50) with the preset grids of block size
+    ``blk``: x quantized (1, blk), W (blk, blk), the product requantized
+    (1, blk) (Q:104-105); the backward's f32 dots (Q:618-622), x's cotangent
+    requantized (1, blk) and W's (blk, blk) (Q:637-638), each dequantized to
+    bf16 (Q:525).  The output cotangent is taken through dequantize_impl_bwd
+    with the output scales of the forward under test (see _linear_reference)."""
+    gx_, gw_ = (1, blk), (blk, blk)
+    xq = oq(O.bf16_bits_to_f32(xb), gx_)
+    wq = oq(O.bf16_bits_to_f32(wb), gw_)
+    xd, wd = odq(xq, gx_).astype(np.float64), odq(wq, gw_).astype(np.float64)
+    y = odq(oq((xd @ wd).astype(np.float32), (1, blk)), (1, blk), "bfloat16")
+    o8, o32 = out_scales
+    g1 = O.bf16_bits_to_f32(O.dequantize_bwd(O.bf16_bits_to_f32(gb), o8, o32, (1, blk), "bfloat16"))
+    gx = odq(oq((g1.astype(np.float64) @ wd.T).astype(np.float32), gx_), gx_)
+    gw = odq(oq((xd.T @ g1.astype(np.float64)).astype(np.float32), gw_), gw_)
+    return y, O.bf16_round(gx), O.bf16_round(gw)
+
+
+@pytest.mark.parametrize("mode", ["f32", "fp8"])
+@pytest.mark.parametrize("blk", [16, 32])
+def test_linear_preset_block_sizes(Q, mode, blk, monkeypatch):
+    """The reference's presets (pratchya/preset.py:21, :30, :39, :48: blksize 16
+    and 32): Linear's x (1, blk) @ W (blk, blk), forward and both backward
+    modes against the oracle.  These grids' f32 group maxima change along K
+    every 16 (x (1, 16): one block per group), 64 (x (1, 32): two blocks) or
+    32 K values (W (32, 32) read transposed), below the 128-wide K block
+    whose scale the FP8 kernel applies, so their products run on the exact
+    f32 product over bf16 pieces in either mode (asserted: no FP8 GEMM)."""
+    Q.set_matmul_backward(mode)
+    calls = []
+    for name in ("gemm_nt", "gemm_nt_fq"):
+        real = getattr(Q.K, name)
+        monkeypatch.setattr(Q.K, name, (lambda r: (lambda *a, **k: calls.append(1) or r(*a, **k)))(real))
+    xb, wb, gb = _linear_case(seed=11, M=256, Kd=512, N=384)
+    x = to_dev_bf16(xb).requires_grad_(True)
+    w = to_dev_bf16(wb).requires_grad_(True)
+    out = Q.QArrayImpl(x, (1, blk)) @ Q.QArrayImpl(w, (blk, blk))
+    y = out.astype(torch.bfloat16)
+    y.backward(to_dev_bf16(gb))
+    assert not calls, "a non-128 grid reached the FP8 GEMM"
+    _, o8, o32 = triple(out)
+    assert out.tgrid == (1, blk)
+    y_ref, gx_ref, gw_ref = _linear_reference_grid(xb, wb, gb, blk, (o8, o32))
+    assert rel(f32(y), O.bf16_bits_to_f32(y_ref)) <= TOL
+    assert rel(f32(x.grad), gx_ref) <= TOL, rel(f32(x.grad), gx_ref)
+    assert rel(f32(w.grad), gw_ref) <= TOL, rel(f32(w.grad), gw_ref)
+
+
+def test_fp8_dgrad_with_narrow_weight_row_groups(Q, monkeypatch):
+    """x (1, 128) @ W (16, 128) in the "fp8" backward: W's scale groups span
+    16 rows, which the requantizing epilogue does not take; the dgrad still
+    runs on the FP8 kernel (gemm_nt) with the requantization as its own
+    pass, and the results match the oracle's FP8 backward chain."""
+    Q.set_matmul_backward("fp8")
+    calls = []
+    real = Q.K.gemm_nt
+    monkeypatch.setattr(Q.K, "gemm_nt", lambda *a, **k: calls.append(1) or real(*a, **k))
+    xb, wb, gb = _linear_case(seed=13, M=256, Kd=1024, N=512)
+    x = to_dev_bf16(xb).requires_grad_(True)
+    w = to_dev_bf16(wb).requires_grad_(True)
+    out = Q.QArrayImpl(x, (1, 128)) @ Q.QArrayImpl(w, (16, 128))
+    y = out.astype(torch.bfloat16)
+    n_fwd = len(calls)
+    y.backward(to_dev_bf16(gb))
+    assert len(calls) - n_fwd == 2, "dgrad and wgrad on the FP8 kernel"
+    _, o8, o32 = triple(out)
+    wq = oq(O.bf16_bits_to_f32(wb), (16, 128))
+    wd = odq(wq, (16, 128)).astype(np.float64)
+    xd = odq(oq(O.bf16_bits_to_f32(xb), (1, 128)), (1, 128)).astype(np.float64)
+    g1 = O.bf16_bits_to_f32(O.dequantize_bwd(O.bf16_bits_to_f32(gb), o8, o32, (1, 128), "bfloat16"))
+    gd = odq(oq(g1, (1, 128)), (1, 128)).astype(np.float64)
+    gx = O.bf16_round(odq(oq((gd @ wd.T).astype(np.float32), (1, 128)), (1, 128)))
+    xt = odq(oq(xd.astype(np.float32), (128, 1)), (128, 1)).astype(np.float64)
+    gt = odq(oq(g1, (128, 1)), (128, 1)).astype(np.float64)
+    gw = O.bf16_round(odq(oq((xt.T @ gt).astype(np.float32), (16, 128)), (16, 128)))
+    assert rel(f32(x.grad), gx) <= TOL
+    assert rel(f32(w.grad), gw) <= TOL
+
+
 # lm_head: Linear(hidden, vocab, (blksize, 1)) (_model.py:77); LoRA:
 # Linear(hidden, rank, (a, 1)) then Linear(rank, hidden, (b, 1)) (M:75-88).
 # The product's grid is (1, 1): every element is its own group.
@@ -321,6 +401,29 @@ def test_fp8_matmul(Q):
     def fwd(a, b):
         p = odq(oq(a, (1, 128)), (1, 128)).astype(np.float64) @ odq(oq(b, (1, 128)), (1, 128)).astype(np.float64)
         return odq(oq(p.astype(np.float32), (1, 128)), (1, 128))
+
+    assert rel(f32(out), fwd(x, y)) <= TOL
+    out.backward(to_dev_f32(g))
+    assert rel(f32(xd.grad), fwd(g, y.T.copy())) <= TOL
+    assert rel(f32(yd.grad), fwd(x.T.copy(), g)) <= TOL
+
+
+@pytest.mark.parametrize("tgrid", [(1, 16), (1, 32)])
+def test_fp8_matmul_default_and_preset_grids(Q, tgrid):
+    """fp8_matmul at its default tgrid (1, 16) (Q:766) and at (1, 32): forward
+    and the backward's products of the transposed raw inputs, each quantized
+    with the same grid (Q:784-789), against the oracle's chain."""
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((256, 384)).astype(np.float32)
+    y = rng.standard_normal((384, 128)).astype(np.float32)
+    g = rng.standard_normal((256, 128)).astype(np.float32)
+    xd = to_dev_f32(x).requires_grad_(True)
+    yd = to_dev_f32(y).requires_grad_(True)
+    out = Q.fp8_matmul(xd, yd) if tgrid == (1, 16) else Q.fp8_matmul(xd, yd, tgrid)
+
+    def fwd(a, b):
+        p = odq(oq(a, tgrid), tgrid).astype(np.float64) @ odq(oq(b, tgrid), tgrid).astype(np.float64)
+        return odq(oq(p.astype(np.float32), tgrid), tgrid)
 
     assert rel(f32(out), fwd(x, y)) <= TOL
     out.backward(to_dev_f32(g))

@@ -260,6 +260,25 @@ int pratchya_quantize_128x1(const void* x, int x_dtype, const uint8_t* x_sc8, co
                             int64_t slices, int64_t T, int64_t C, uint8_t* q_fp8, uint8_t* sc_fp8,
                             float* sc_fp32, hipStream_t stream);
 
+/* Quantize (1, 128) and requantize (128, 1) in one pass:
+ *       replaces quantize_impl(x, (1, 128)) (Q:458-506, the quantized Linear's
+ *       input, pratchya/_nnx_impl/_module.py:46-50) together with
+ *       quantize_impl(dequantize_impl(<that>), (128, 1)) (Q:541-569, Q:458-506:
+ *       the stored activation requantized along the tokens for the FP8 weight
+ *       gradient, fp8_matmul's scheme Q:784-789).
+ * x: bf16 or f32 [slices, T, C] (PRATCHYA_DT_*), 16-byte aligned; T a multiple
+ * of 128 and C of 128 (PRATCHYA_EINVAL), C of 1024 (PRATCHYA_EUNSUPPORTED).
+ * Outputs, per slice exactly quantize_impl's: q_fp8 [slices, T, C], sc_fp8
+ * [slices * T * C / 128] (8-byte aligned), sc_fp32 [slices * T * C / 1024]
+ * for (1, 128); t_fp8 [slices, T, C] (the (128, 1) payload in x's layout, as
+ * pratchya_quantize_128x1 writes it), t_sc8 [slices * T * C / 128] (16-byte
+ * aligned), t_sc32 [slices * T * C / 1024] (8-byte aligned) for (128, 1).
+ * Bit-identical to pratchya_quantize followed by pratchya_quantize_128x1 of
+ * its payload; the input is read once. */
+int pratchya_quantize_dual(const void* x, int x_dtype, int64_t slices, int64_t T, int64_t C, uint8_t* q_fp8,
+                           uint8_t* sc_fp8, float* sc_fp32, uint8_t* t_fp8, uint8_t* t_sc8, float* t_sc32,
+                           hipStream_t stream);
+
 /* Transposed quantize, tgrid (1, 128) of the transposed tensor:
  *                                         replaces quantize_impl(x^T, (1, 128)),
  * Q:458-506, as fp8_matmul's backward quantizes its transposed raw inputs

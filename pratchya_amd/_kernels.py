@@ -256,6 +256,43 @@ def quantize_128x1(x: torch.Tensor, x_sc8: torch.Tensor = None, x_sc32: torch.Te
     return _quantize_128x1(x, x_sc8, x_sc32, out, rows=True)
 
 
+def quantize_dual(x: torch.Tensor):
+    """``quantize_impl(x, (1, 128))`` and, from the same pass,
+    ``quantize_impl(dequantize_impl(that), (128, 1))`` with the second payload
+    in ``x``'s own [..., T, C] layout (pratchya/_qualia/_qarr.py:458-506,
+    :541-569): a quantized Linear's input and the FP8 weight gradient's
+    token-axis requantization of it (Q:784-789).  ``x``: bf16 or f32
+    [..., T, C] with T a multiple of 128 and C of 1024
+    (``PratchyaUnsupported`` for other C).  Returns ``((q, sc8, sc32), (q2,
+    sc8b, sc32b))``, bit-identical to ``quantize(x, (1, 128))`` and
+    ``quantize_128x1`` of its payload."""
+    _require_gpu(x)
+    if x.dim() < 2:
+        raise ValueError("quantize_dual needs a [..., T, C] tensor")
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        x = x.float()
+    if not x.is_contiguous() or not _aligned(x, 16):
+        x = x.contiguous() if not x.is_contiguous() else x.clone()
+    lead = tuple(x.shape[:-2])
+    T, C = int(x.shape[-2]), int(x.shape[-1])
+    S = 1
+    for d in lead:
+        S *= int(d)
+    _, K1, M1 = group_layout(T, C, (1, 128))
+    _, K2, M2 = group_layout(T, C, (128, 1))
+    dev = x.device
+    q = torch.empty(x.shape, dtype=torch.uint8, device=dev)
+    sc8 = torch.empty(lead + (M1, K1), dtype=torch.uint8, device=dev)
+    sc32 = torch.empty(lead + (M1, 1, 1), dtype=torch.float32, device=dev)
+    q2 = torch.empty(x.shape, dtype=torch.uint8, device=dev)
+    sc8b = torch.empty(lead + (M2, K2), dtype=torch.uint8, device=dev)
+    sc32b = torch.empty(lead + (M2, 1, 1), dtype=torch.float32, device=dev)
+    _lib.check(_lib.load().pratchya_quantize_dual(_ptr(x), _dtype_code(x.dtype), S, T, C, _ptr(q), _ptr(sc8),
+                                                  _ptr(sc32), _ptr(q2), _ptr(sc8b), _ptr(sc32b), _stream(x)),
+               "quantize_dual")
+    return (q.view(E4M3), sc8.view(E8M0), sc32), (q2.view(E4M3), sc8b.view(E8M0), sc32b)
+
+
 def quantize_t128(x: torch.Tensor, x_sc8: torch.Tensor = None, x_sc32: torch.Tensor = None, out=None):
     """``quantize_impl(x, (128, 1))`` (pratchya/_qualia/_qarr.py:458-506) with
     the payload transposed per slice.

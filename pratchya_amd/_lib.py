@@ -68,6 +68,8 @@ SIGNATURES = {
                                        ctypes.c_float, _c_p, _c_int, _c_p]),
     "pratchya_quantize_t1x128": (_c_int, [_c_p, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p,
                                           _c_p]),
+    "pratchya_quantize_dual": (_c_int, [_c_p, _c_int, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
+                                        _c_p]),
     "pratchya_gemm_bs_nt": (_c_int, [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
                                      _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
                                      _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_int, _c_p]),

@@ -138,6 +138,13 @@ __device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int lane) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, lane);
 }
 
+// Raw buffer resources for stores issued by every lane of a wave with the
+// lanes that should not store given an offset past the end (the range check
+// drops them): a store count that does not depend on a branch lets a wait for
+// later loads leave the stores in flight.
+constexpr int kRawBuffer = 0x00020000;            // raw buffer resource, 32-bit data format
+constexpr int kOutOfRange = (int)0xFFFFFFF0u;     // buffer offset past any scale array
+
 // 16-byte streaming load: the input is read exactly once, so it is loaded
 // non-temporally (measured ~12% more HBM throughput than a plain load here).
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));

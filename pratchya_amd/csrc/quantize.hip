@@ -222,8 +222,6 @@ __global__ __launch_bounds__(256) void k_quant_rowgroup(
 // dequantize_impl_bwd first ((x * 2^(e-127) * G) / 128 in x's dtype,
 // _qarr.py:575-601), in registers.
 // --------------------------------------------------------------------------
-constexpr int kRawBuffer = 0x00020000;            // raw buffer resource, 32-bit data format
-constexpr int kOutOfRange = (int)0xFFFFFFF0u;     // buffer offset past any scale array
 
 template <bool IS_BF16, bool HW, int OUT, bool FIXNAN, bool PRE>
 __global__ __launch_bounds__(256) void k_quant_g8(const void* __restrict__ xv,

@@ -767,6 +767,251 @@ __global__ __launch_bounds__(rows_threads(R)) void k_quant_128x1_rows(const uint
   }
 }
 
+// The activation quantize and the weight gradient's requantization of it in
+// one pass: (q, sc8, sc32) = quantize_impl(x, (1, 128)) (Q:458-506, the
+// quantized Linear's input, M:46-50) and (q2, sc8b, sc32b) =
+// quantize_impl(dequantize_impl(q, sc8, sc32), (128, 1)) (Q:541-569 then
+// Q:458-506: the stored activation requantized along the tokens for the FP8
+// weight gradient, fp8_matmul's scheme Q:784-789), q2 in x's own [T, C]
+// layout.  Bit-identical to pratchya_quantize followed by
+// pratchya_quantize_128x1 of its payload.
+//
+// A workgroup of 8 waves owns 128 tokens x 1024 channels (one (1, 128) group
+// of each of its tokens, 128 (128, 1) groups).  Wave w takes tokens 16w ..
+// 16w + 15 and lane l the channels 16l .. 16l + 15 (one 128-channel block per
+// 8 lanes) in both phases, so each lane reads back only bytes it wrote.
+// Phase 1, token by token (the next two tokens' loads in flight): block
+// maxima over 8 lanes, the group max from the 8 block leaders
+// (wave-uniform), the cast, the payload row stored (1 KB per wave), the
+// block's dequantization factor 2^(e-127) * G to LDS, and a running maximum
+// of each channel's dequantized values (dequantize_impl's (f32(q) * dq) /
+// 128).  The channel maxima over the 128 tokens meet in LDS by atomic max;
+// each lane then forms its two 8-channel groups' maxima, e8m0 bytes and y.
+// Phase 2, token by token: the lane reloads its 16 payload bytes (just
+// written, from the cache), dequantizes, casts with the division-free scheme
+// (every element checked against the bf16 rounding midpoint, a close one
+// recast exactly), and stores the second payload.  Nothing but running maxima
+// is held between the phases, so several workgroups share a CU and one's
+// arithmetic overlaps another's memory traffic.  C must be a multiple of 1024
+// and the token count of 128 (slices flatten into tokens).
+template <bool IS_BF16>
+__global__ __launch_bounds__(512) void k_quant_dual(const void* __restrict__ xv, int64_t C,
+                                                    uint8_t* __restrict__ q, uint8_t* __restrict__ sc8,
+                                                    float* __restrict__ sc32, uint8_t* __restrict__ q2,
+                                                    uint8_t* __restrict__ sc8b, float* __restrict__ sc32b) {
+  constexpr int ESZ = IS_BF16 ? 2 : 4;
+  constexpr int NV = ESZ;                       // 16-byte loads per token and lane (16 channels)
+  constexpr int TK = 16;                        // tokens per wave
+  const int lane = (int)threadIdx.x & 63, wv = (int)(threadIdx.x >> 6);
+  const int64_t cg = blockIdx.x, tb = blockIdx.y;
+  const int64_t c0 = cg * 1024 + lane * 16;     // the lane's first channel
+  const int tw = wv * TK;                       // the wave's first token in the tile
+  const int64_t t0 = tb * 128 + tw;
+  const int64_t ngc = C >> 10;                  // (1, 128) groups per token row
+  const char* xb = static_cast<const char*>(xv);
+  __shared__ float dqt[128][8];                 // per token and block: 2^(e-127) * G
+  __shared__ __attribute__((aligned(16))) uint32_t cmx[1024];       // channel maxima (|x| bits)
+  // the (1, 128) scale arrays as raw buffers (byte counts below 2^31, checked
+  // on the host): every lane issues the scale stores, lanes other than 0 past
+  // the end, so that the loop's wait for the next tokens' loads does not
+  // also wait for them
+  const int64_t n_groups = (int64_t)gridDim.y * 128 * ngc;
+  const __amdgpu_buffer_rsrc_t r8 = __builtin_amdgcn_make_buffer_rsrc(sc8, 0, (int)(n_groups * 8), kRawBuffer);
+  const __amdgpu_buffer_rsrc_t r32 = __builtin_amdgcn_make_buffer_rsrc(sc32, 0, (int)(n_groups * 4), kRawBuffer);
+
+  cmx[threadIdx.x] = 0u;
+  cmx[threadIdx.x + 512] = 0u;
+
+  // ---- phase 1: quantize_impl(x, (1, 128)) token by token ----
+  auto load_tok = [&](int i, uint4 (&v)[NV]) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) v[k] = load_stream16(xb + ((t0 + i) * C + c0) * ESZ + 16 * k);
+  };
+  uint32_t mx[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) mx[j] = 0u;
+  // two token buffers used alternately (no register copy waits for a load in
+  // flight); the loads are unconditional, so the count in flight is fixed
+  uint4 va[NV], vb[NV];
+  load_tok(0, va);
+  load_tok(1, vb);
+  auto quant_tok = [&](int i, const uint4 (&v)[NV]) {
+    uint32_t lm = 0;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) lm = umax(lm, IS_BF16 ? absmax8_bf16(v[k]) : vec_absmax_bits<false>(v[k]));
+    const uint32_t mb = lane_group_max<8>(lm);            // this lane's block max
+    uint32_t Gb = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) Gb = umax(Gb, readlane_u32(mb, 8 * k));
+    const float G = u2f(Gb);
+    float x[16];
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+#pragma unroll
+      for (int j = 0; j < 16 / NV; ++j) x[k * (16 / NV) + j] = elem_f32<IS_BF16>(v[k], j);
+    uint32_t e, w4[4];
+    if ((Gb >> 23) < 255u) {
+      const BlockScale bs = block_scale(mb, Gb, __builtin_amdgcn_rcpf(G * 0.0078125f));
+      e = bs.e;
+      const bool check = !IS_BF16 || __any(bs.clamped ? 1 : 0);
+      uint32_t key = 0xFFFFFFFFu;
+      float tt[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) tt[k] = x[k] * bs.y;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) w4[w] = cvt4_hw(tt[4 * w], tt[4 * w + 1], tt[4 * w + 2], tt[4 * w + 3]);
+      if (check) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) key = umin(key, mid_key4(tt[4 * w], tt[4 * w + 1], tt[4 * w + 2], tt[4 * w + 3]));
+      }
+      // a product near a bf16 rounding midpoint: the token's cast redone
+      // exactly by the whole wave (a wave-uniform branch, skipped as a whole
+      // otherwise; the exact cast equals the fast one wherever that is valid)
+      if (check && __any(key <= kMidKey ? 1 : 0)) {
+        const float S = quant_scale(e, G);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) w4[w] = cvt4_exact(x[4 * w], x[4 * w + 1], x[4 * w + 2], x[4 * w + 3], S);
+      }
+    } else {
+      e = e8m0_of(u2f(mb), G);
+      const float S = quant_scale(e, G);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) w4[w] = cvt4_exact(x[4 * w], x[4 * w + 1], x[4 * w + 2], x[4 * w + 3], S);
+    }
+    const int64_t t = t0 + i;
+    // an ordinary store: phase 2 reads these bytes back from the cache
+    *reinterpret_cast<u32x4_t*>(q + t * C + c0) = u32x4_t{w4[0], w4[1], w4[2], w4[3]};
+    const float dqi = e8m0_decode(e) * G;
+    if ((lane & 7) == 0) dqt[tw + i][lane >> 3] = dqi;
+    // running channel maxima of f32(|q|) * dq (= |f32(q) * dq|, dq >= 0); the
+    // dequantized value divides that by 128, which keeps the order (rounding
+    // is monotonic), so the maxima are scaled once after the exchange
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      float d[4];
+      fp8_word(w4[w] & 0x7F7F7F7Fu, d[0], d[1], d[2], d[3]);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) mx[4 * w + b] = umax(mx[4 * w + b], f2u(d[b] * dqi));
+    }
+    // the group's 8 e8m0 bytes (block k: leader lane 8k) and G
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t ek = readlane_u32(e, 8 * k);
+      if (k < 4) lo |= ek << (8 * k);
+      else hi |= ek << (8 * (k - 4));
+    }
+    const int gi = (int)(t * ngc + cg);
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{lo, hi}, r8, lane == 0 ? gi * 8 : kOutOfRange, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(f2u(G), r32, lane == 0 ? gi * 4 : kOutOfRange, 0, 0);
+  };
+#pragma unroll 1
+  for (int i = 0; i < TK; i += 2) {
+    quant_tok(i, va);
+    load_tok(i + 2 < TK ? i + 2 : TK - 1, va);
+    quant_tok(i + 1, vb);
+    load_tok(i + 3 < TK ? i + 3 : TK - 1, vb);
+  }
+  __syncthreads();                              // cmx cleared by every thread
+#pragma unroll
+  for (int j = 0; j < 16; ++j) atomicMax(&cmx[lane * 16 + j], mx[j]);
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint4 a = *reinterpret_cast<const uint4*>(&cmx[lane * 16 + 4 * w]);
+    const uint32_t m4[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int b = 0; b < 4; ++b) mx[4 * w + b] = f2u(u2f(m4[b]) * 0.0078125f) & 0x7FFFFFFFu;
+  }
+
+  // ---- phase 2: quantize_impl(dequantize_impl(q), (128, 1)) ----
+  // the two 8-channel groups of the lane: group max, e8m0 bytes (packed, 4
+  // per word) and y per channel
+  uint32_t ew[4] = {0u, 0u, 0u, 0u};
+  float y2[16], Gh[2];
+  bool finh[2];
+#pragma unroll
+  for (int gh = 0; gh < 2; ++gh) {
+    uint32_t Gb = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) Gb = umax(Gb, mx[8 * gh + j]);
+    const float G = u2f(Gb);
+    Gh[gh] = G;
+    finh[gh] = (Gb >> 23) < 255u;
+    const float rG = __builtin_amdgcn_rcpf(G * 0.0078125f);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      uint32_t ej;
+      if (finh[gh]) {
+        const BlockScale bs = block_scale(mx[8 * gh + j], Gb, rG);
+        ej = bs.e;
+        y2[8 * gh + j] = bs.y;
+      } else {
+        ej = e8m0_of(u2f(mx[8 * gh + j]), G);
+        y2[8 * gh + j] = PRATCHYA_Y_CLAMP;
+      }
+      ew[(8 * gh + j) >> 2] |= ej << (8 * (j & 3));
+    }
+  }
+  // the lane's payload bytes of the next two tokens in flight (alternating
+  // buffers, unconditional loads, as in phase 1)
+  auto load_q = [&](int i) { return *reinterpret_cast<const u32x4_t*>(q + (t0 + i) * C + c0); };
+  u32x4_t pa = load_q(0), pb = load_q(1);
+  // ONE: (f32(q) * dq) / 128 as f32(q) * (dq / 128), exact for every q when
+  // dequant_one_mul(dq) holds (taken when it does on the whole wave)
+  auto requant_body = [&](auto one_c, int i, const u32x4_t wq, float dqi) {
+    constexpr bool ONE = decltype(one_c)::value;
+    const int64_t t = t0 + i;
+    const float dqx = ONE ? dqi * 0.0078125f : dqi;
+    const uint32_t qw[4] = {wq.x, wq.y, wq.z, wq.w};
+    uint32_t out[4];
+#pragma unroll
+    for (int gh = 0; gh < 2; ++gh) {
+      float d[8], tv[8];
+      fp8_word(qw[2 * gh], d[0], d[1], d[2], d[3]);
+      fp8_word(qw[2 * gh + 1], d[4], d[5], d[6], d[7]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        d[j] = ONE ? d[j] * dqx : (d[j] * dqx) * 0.0078125f;
+        tv[j] = d[j] * y2[8 * gh + j];
+      }
+      out[2 * gh] = cvt4<true>(tv[0], tv[1], tv[2], tv[3]);
+      out[2 * gh + 1] = cvt4<true>(tv[4], tv[5], tv[6], tv[7]);
+      const uint32_t key = umin(mid_key4(tv[0], tv[1], tv[2], tv[3]), mid_key4(tv[4], tv[5], tv[6], tv[7]));
+      // the exact cast by the whole wave when a lane needs it (a wave-uniform
+      // branch; the exact cast equals the fast one wherever that is valid)
+      if (__any((key <= kMidKey || !finh[gh]) ? 1 : 0)) {
+        const uint32_t elo = ew[2 * gh], ehi = ew[2 * gh + 1];
+        uint32_t b[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          b[j] = quant_elem_exact(d[j], quant_scale(((j < 4 ? elo : ehi) >> (8 * (j & 3))) & 0xFFu, Gh[gh]));
+        out[2 * gh] = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+        out[2 * gh + 1] = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+      }
+    }
+    store_stream16(q2 + t * C + c0, u32x4_t{out[0], out[1], out[2], out[3]});
+  };
+  auto requant_tok = [&](int i, const u32x4_t wq) {
+    const float dqi = dqt[tw + i][lane >> 3];
+    if (__all(dequant_one_mul(dqi) ? 1 : 0)) requant_body(std::true_type{}, i, wq, dqi);
+    else requant_body(std::false_type{}, i, wq, dqi);
+  };
+#pragma unroll 1
+  for (int i = 0; i < TK; i += 2) {
+    requant_tok(i, pa);
+    pa = load_q(i + 2 < TK ? i + 2 : TK - 1);
+    requant_tok(i + 1, pb);
+    pb = load_q(i + 3 < TK ? i + 3 : TK - 1);
+  }
+  if (wv == 0) {
+    // blocks (tb, c0 .. c0 + 15) are consecutive bytes: groups (tb * C + c0) / 8 and the next
+    const int64_t blk = tb * C + c0;
+    store_stream16(sc8b + blk, u32x4_t{ew[0], ew[1], ew[2], ew[3]});
+    store_stream8(reinterpret_cast<uint8_t*>(sc32b + blk / 8), u32x2_t{f2u(Gh[0]), f2u(Gh[1])});
+  }
+}
+
 int64_t gcd64(int64_t a, int64_t b) {
   while (b) {
     const int64_t t = a % b;
@@ -944,5 +1189,48 @@ extern "C" int pratchya_quantize_t1x128(const void* x, int x_dtype, const uint8_
   hipError_t err = hipGetLastError();
   if (err != hipSuccess)
     return pratchya_set_error(PRATCHYA_EHIP, "quantize_t1x128: launch failed: %s", hipGetErrorString(err));
+  return PRATCHYA_OK;
+}
+
+extern "C" int pratchya_quantize_dual(const void* x, int x_dtype, int64_t slices, int64_t T, int64_t C,
+                                      uint8_t* q_fp8, uint8_t* sc_fp8, float* sc_fp32, uint8_t* t_fp8,
+                                      uint8_t* t_sc8, float* t_sc32, hipStream_t stream) {
+  if (slices < 0 || T < 0 || C < 0) return pratchya_set_error(PRATCHYA_EINVAL, "quantize_dual: negative size");
+  if (x_dtype != PRATCHYA_DT_F32 && x_dtype != PRATCHYA_DT_BF16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_dual: unsupported input dtype %d", x_dtype);
+  if (T % 128)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_dual: tgrid (128, 1) does not divide %lld tokens",
+                              (long long)T);
+  if (C % 128)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_dual: tgrid (1, 128) does not divide %lld channels",
+                              (long long)C);
+  if (slices == 0 || T == 0 || C == 0) return PRATCHYA_OK;
+  if (C % 1024)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_dual: channels must be a multiple of 1024 (one "
+                              "(1, 128) group per 1024-channel row segment; got %lld)", (long long)C);
+  if (!x || !q_fp8 || !sc_fp8 || !sc_fp32 || !t_fp8 || !t_sc8 || !t_sc32)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_dual: null buffer");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(q_fp8) | reinterpret_cast<uintptr_t>(t_fp8) |
+       reinterpret_cast<uintptr_t>(t_sc8)) % 16 ||
+      reinterpret_cast<uintptr_t>(sc_fp8) % 8 || reinterpret_cast<uintptr_t>(t_sc32) % 8 ||
+      reinterpret_cast<uintptr_t>(sc_fp32) % 4)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_dual: buffers are not aligned");
+  const int64_t rows = slices * T;
+  if (rows / 128 > 65535 || C / 1024 > 65535 || rows * (C / 128) >= ((int64_t)1 << 31))
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "quantize_dual: too many token blocks, channel groups or "
+                              "scale bytes (2^31 or more)");
+  // slices flatten into tokens: with T a multiple of 128 and C of 1024 neither
+  // grid's blocks or groups cross a slice, and the per-slice scale arrays
+  // concatenate in token order
+  const dim3 grid((unsigned)(C / 1024), (unsigned)(rows / 128));
+  if (x_dtype == PRATCHYA_DT_BF16)
+    hipLaunchKernelGGL(k_quant_dual<true>, grid, dim3(512), 0, stream, x, C, q_fp8, sc_fp8, sc_fp32, t_fp8, t_sc8,
+                       t_sc32);
+  else
+    hipLaunchKernelGGL(k_quant_dual<false>, grid, dim3(512), 0, stream, x, C, q_fp8, sc_fp8, sc_fp32, t_fp8, t_sc8,
+                       t_sc32);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess)
+    return pratchya_set_error(PRATCHYA_EHIP, "quantize_dual: launch failed: %s", hipGetErrorString(err));
   return PRATCHYA_OK;
 }

@@ -456,3 +456,24 @@ def test_status_offsets_without_gpu():
         off = lib.pratchya_gemm_bf16_gram_status_offset(M, Kd)
         assert off > 0 and off + 4 == lib.pratchya_gemm_bf16_gram_workspace_bytes(M, Kd)
     assert lib.pratchya_gemm_bf16_gram_status_offset(300, 64) == -1
+
+
+def test_quantize_dual_argument_codes_without_gpu():
+    """pratchya_quantize_dual rejects other dtypes, token counts and channel
+    counts (EINVAL for grids that do not divide, EUNSUPPORTED for a width that
+    is not a multiple of 1024), null and misaligned buffers, before any
+    launch; an empty tensor is a no-op."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    f = ctypes.c_void_p(1 << 20)
+    args = lambda q: (q, f, f, f, f, f, None)    # noqa: E731  (q: the payload, 16-byte aligned)
+    assert lib.pratchya_quantize_dual(f, _lib.DT_BF16, 1, 0, 1024, *args(f)) == 0
+    assert lib.pratchya_quantize_dual(f, _lib.DT_E4M3, 1, 128, 1024, *args(f)) == _lib.EINVAL
+    assert lib.pratchya_quantize_dual(f, _lib.DT_BF16, 1, 100, 1024, *args(f)) == _lib.EINVAL
+    assert lib.pratchya_quantize_dual(f, _lib.DT_BF16, 1, 128, 1000, *args(f)) == _lib.EINVAL
+    assert lib.pratchya_quantize_dual(f, _lib.DT_BF16, 1, 128, 2560, *args(f)) == _lib.EUNSUPPORTED
+    assert b"1024" in lib.pratchya_last_error()
+    assert lib.pratchya_quantize_dual(f, _lib.DT_BF16, 1, 128, 1024, *args(None)) == _lib.EINVAL
+    assert lib.pratchya_quantize_dual(f, _lib.DT_F32, 1, 128, 1024, *args(ctypes.c_void_p((1 << 20) + 8))) \
+        == _lib.EUNSUPPORTED
+    assert b"aligned" in lib.pratchya_last_error()

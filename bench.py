@@ -82,103 +82,122 @@ def cpu_baseline_config1(reps: int = 5):
 
 def _gemm_host_sample(xq, wq, out, rows, n_blk_row):
     """Host copies for a GEMM's CPU baseline and parity check: the quantized
-    activation's payload and scales on the sampled ``rows`` ((1,128) grid:
-    ``n_blk_row`` e8m0 bytes and n_blk_row/8 group maxima per row), the whole
-    quantized weight (payload [K, N], e8m0, group maxima), and the GPU
-    output's sampled rows as f32."""
+    activation's payload and scales on ``rows`` ((1,128) grid: ``n_blk_row``
+    e8m0 bytes and n_blk_row/8 group maxima per row; all rows for the
+    full-shape baseline), the whole quantized weight (payload [K, N], e8m0,
+    group maxima), and the GPU output's rows as f32."""
     import torch
-    ridx = torch.from_numpy(rows).cuda()
-    x8 = xq[0].view(torch.uint8)[ridx].cpu().numpy()
-    s8 = xq[1].view(torch.uint8).reshape(-1, n_blk_row)[ridx].cpu().numpy().reshape(-1, 8)
-    s32 = xq[2].reshape(-1, n_blk_row // 8)[ridx].cpu().numpy().reshape(-1, 1, 1)
+    full = len(rows) == int(out.shape[0])
+    ridx = None if full else torch.from_numpy(rows).cuda()
+    pick = (lambda t: t) if full else (lambda t: t[ridx])
+    x8 = pick(xq[0].view(torch.uint8)).cpu().numpy()
+    s8 = pick(xq[1].view(torch.uint8).reshape(-1, n_blk_row)).cpu().numpy().reshape(-1, 8)
+    s32 = pick(xq[2].reshape(-1, n_blk_row // 8)).cpu().numpy().reshape(-1, 1, 1)
     w = tuple(t.view(torch.uint8).cpu().numpy() if t.dtype != torch.float32 else t.cpu().numpy() for t in wq)
-    c = out[ridx].float().cpu().numpy()
+    c = pick(out).float().cpu().numpy()
     return {"rows": rows, "x": (x8, s8, s32), "w": w, "c": c}
 
 
 def cpu_baseline_gemm(sample, total_rows: int):
     """The oracle's matmul_impl forward (Q:605-608) -- both operands
     dequantized to f32 and multiplied -- on the GPU run's own quantized bytes
-    for a row sample of the activation, timed on this host's BLAS threads;
-    the GPU output's rows are checked against it (relative Frobenius error,
-    bf16 output tolerance 1e-2)."""
+    at full shape, timed once on this host's BLAS threads (after a small
+    matmul that starts the thread pool; NumPy compiles nothing); the GPU
+    output is checked against it in full (relative Frobenius error, bf16
+    output tolerance 1e-2)."""
+    from oracle import c_oracle as C
     from oracle import qarr_oracle as O
     rows = sample["rows"]
-    xd = O.dequantize_impl(*sample["x"], "float32", (1, 128))
-    wd = O.dequantize_impl(*sample["w"], "float32", (128, 128))
-    ref = xd @ wd                                      # warm
+    np.ones((256, 256), np.float32) @ np.ones((256, 256), np.float32)
     t0 = time.perf_counter()
-    reps = 3
-    for _ in range(reps):
-        ref = xd @ wd
-    per = (time.perf_counter() - t0) / reps
+    xd = C.dequantize(*sample["x"], (1, 128))
+    wd = C.dequantize(*sample["w"], (128, 128))
+    ref = xd @ wd
+    per = time.perf_counter() - t0
     Kd, N = wd.shape
     tf = 2 * len(rows) * Kd * N / per / 1e12
-    err = O.rel_fro(sample["c"], ref.astype(np.float64))
+    err = O.rel_fro(sample["c"], ref)
+    shape = "full shape" if len(rows) == total_rows else f"{len(rows)} of {total_rows} rows"
     return {"value": round(tf, 4), "unit": "TFLOP/s", "cores": _blas_threads(), "kind": "port",
-            "sample": f"f32 matmul of the oracle-dequantized operands of this run, {len(rows)} of {total_rows} "
-                      f"rows, {reps} reps (NumPy / OpenBLAS)",
+            "sample": f"{shape}: the oracle dequantizes this run's quantized operands to f32 (C restatement, "
+                      f"OpenMP) and multiplies them ({len(rows)} x {Kd} x {N}, NumPy / OpenBLAS), {per:.1f} s, "
+                      f"one timed run",
             "parity_rel_fro_vs_oracle": float(f"{err:.3e}"), "parity_ok": bool(err <= 1e-2)}
 
 
-def cpu_baseline_config4(rows: int = 256):
-    """The oracle's config-4 backward on a token sample: dY (rows tokens)
-    requantized (1,128) and contracted with W^T (dgrad), and A^T dY with both
-    operands requantized (128,1) along the sampled tokens (wgrad), f32 dots on
-    the host's BLAS threads.  Reported per token, scaled to the full 16384."""
-    from oracle import qarr_oracle as O
-    T, Cin, N = rows, 2048, 8192
-    dy = O.bf16_bits_to_f32(O.normal_input((T, N), 1e-3, seed=4))
-    a = O.bf16_bits_to_f32(O.activation_input(T, Cin, seed=2))
-    wd = O.dequantize_impl(*O.quantize_impl(O.bf16_bits_to_f32(O.normal_input((Cin, N), 0.02, seed=3)),
-                                            (128, 128)), "float32", (128, 128))
+def cpu_baseline_config4(inputs):
+    """The oracle's config-4 backward at full shape (16384 tokens) on the GPU
+    run's own inputs: dY requantized (1,128) and contracted with W^T (dgrad),
+    and A^T dY with both operands requantized (128,1) along the tokens
+    (wgrad); quantize / dequantize on the oracle's C restatement (OpenMP
+    threads), the f32 dots on the host's BLAS threads; one timed run.
+    ``inputs``: host f32 copies of dY [16384, 8192], the activation A
+    [16384, 2048] and W [2048, 8192] (bf16 values)."""
+    from oracle import c_oracle as C
+    dy, a, w = inputs
+    np.ones((256, 256), np.float32) @ np.ones((256, 256), np.float32)
     t0 = time.perf_counter()
-    dyd = O.dequantize_impl(*O.quantize_impl(dy, (1, 128)), "float32", (1, 128))
+    wd = C.dequantize(*C.quantize(w, (128, 128)), (128, 128))
+    dyd = C.dequantize(*C.quantize(dy, (1, 128)), (1, 128))
     dyd @ wd.T                                                       # dgrad
-    ad = O.dequantize_impl(*O.quantize_impl(a, (1, 128)), "float32", (1, 128))
-    at = O.dequantize_impl(*O.quantize_impl(ad, (128, 1)), "float32", (128, 1))
-    gt = O.dequantize_impl(*O.quantize_impl(dy, (128, 1)), "float32", (128, 1))
+    ad = C.dequantize(*C.quantize(a, (1, 128)), (1, 128))
+    at = C.dequantize(*C.quantize(ad, (128, 1)), (128, 1))
+    gt = C.dequantize(*C.quantize(dy, (128, 1)), (128, 1))
     at.T @ gt                                                        # wgrad
     el = time.perf_counter() - t0
-    full_s = el * 16384 / rows
-    return {"value": round(2 * 549755813888 / full_s / 1e12, 4), "unit": "TFLOP/s (dgrad + wgrad)",
+    return {"value": round(2 * 549755813888 / el / 1e12, 4), "unit": "TFLOP/s (dgrad + wgrad)",
             "cores": _blas_threads(), "kind": "port",
-            "sample": f"{rows} of 16384 tokens: requantizes + f32 dots of dgrad and wgrad, {el:.1f} s, "
-                      f"scaled to the full token count (NumPy / OpenBLAS)"}
+            "sample": f"full shape (16384 tokens) on this run's dY, A and W: the oracle's requantizes (C "
+                      f"restatement, OpenMP) and f32 dots of dgrad and wgrad (NumPy / OpenBLAS), {el:.1f} s, one "
+                      f"timed run"}
 
 
-def cpu_baseline_config5(tokens: int = 256):
-    """The oracle's config-5 layer, estimated from one [4096, 4096] linear:
-    the per-token part (x quantized (1,128), the f32 forward dot, the output
-    requantized, the f32 dgrad and wgrad dots of the reference's matmul
-    backward, Q:616-640, the dgrad requantize) timed on ``tokens`` tokens, and
-    the per-step part (the weight gradient's (128,128) requantize) timed once;
-    both scale with din x dout, so the six linears cost 12x the [4096, 4096]
-    one.  Reported as tokens/s of the full 32768-token step."""
-    from oracle import qarr_oracle as O
-    rng = np.random.default_rng(5)
-    d = CFG5_D
-    x = O.bf16_round(rng.standard_normal((tokens, d)).astype(np.float32))
-    w = O.bf16_round((rng.standard_normal((d, d)) * 0.02).astype(np.float32))
-    g = O.bf16_round((rng.standard_normal((tokens, d)) * 1e-3).astype(np.float32))
-    wd = O.dequantize_impl(*O.quantize_impl(w, (128, 128)), "float32", (128, 128))
-    t0 = time.perf_counter()
-    xd = O.dequantize_impl(*O.quantize_impl(x, (1, 128)), "float32", (1, 128))
-    y = xd @ wd
-    O.dequantize_impl(*O.quantize_impl(y, (1, 128)), "bfloat16", (1, 128))
-    gx = g @ wd.T
-    O.quantize_impl(gx, (1, 128))
-    gw = xd.T @ g
-    per_token = (time.perf_counter() - t0) / tokens
-    t0 = time.perf_counter()
-    O.quantize_impl(gw, (128, 128))
-    per_step = time.perf_counter() - t0
-    scale = sum(a * b for a, b in CFG5_LINEARS) / (d * d)
-    step_s = scale * (per_token * CFG5_TOKENS + per_step)
+def cpu_baseline_config5(tokens: int = None):
+    """The oracle's config-5 layer step on a token sample: the six linears
+    (r, k, v, o [4096, 4096], FFN up [4096, 16384], down [16384, 4096]), each
+    as the reference computes it -- the weight quantized (128,128), x
+    quantized (1,128), the f32 forward dot, the output requantized (1,128),
+    the f32 dgrad and wgrad dots of matmul_impl's backward (Q:616-640) and
+    their requantizations ((1,128), (128,128)) -- with quantize / dequantize
+    on the oracle's C restatement (OpenMP threads) and the dots on the host's
+    BLAS threads; one timed run at full shape (32768 tokens) by default.  With
+    fewer ``tokens`` the per-token work (activation quantizes and the three
+    dots) is scaled to 32768 and the per-step work (the weight's quantize and
+    its gradient's requantize) counted once.  Synthetic bf16 values N(0,1)
+    activations, N(0,0.02) weights, N(0,1e-3) cotangents (torch CPU
+    generator, seed 5; not timed)."""
+    import torch
+    from oracle import c_oracle as C
+    tokens = CFG5_TOKENS if tokens is None else tokens
+    gen = torch.Generator().manual_seed(5)
+    bf = lambda t: t.to(torch.bfloat16).float().numpy()   # noqa: E731  (bf16 values as f32)
+    np.ones((256, 256), np.float32) @ np.ones((256, 256), np.float32)
+    per_token = per_step = 0.0
+    for din, dout in CFG5_LINEARS:
+        x = bf(torch.randn((tokens, din), generator=gen))
+        w = bf(torch.randn((din, dout), generator=gen) * 0.02)
+        g = bf(torch.randn((tokens, dout), generator=gen) * 1e-3)
+        t0 = time.perf_counter()
+        wd = C.dequantize(*C.quantize(w, (128, 128)), (128, 128))
+        t1 = time.perf_counter()
+        xd = C.dequantize(*C.quantize(x, (1, 128)), (1, 128))
+        y = xd @ wd
+        C.dequantize(*C.quantize(y, (1, 128)), (1, 128))
+        gx = g @ wd.T
+        C.dequantize(*C.quantize(gx, (1, 128)), (1, 128))
+        gw = xd.T @ g
+        t2 = time.perf_counter()
+        C.dequantize(*C.quantize(gw, (128, 128)), (128, 128))
+        t3 = time.perf_counter()
+        per_step += (t1 - t0) + (t3 - t2)
+        per_token += (t2 - t1) / tokens
+    step_s = per_token * CFG5_TOKENS + per_step
+    shape = ("full shape: the six linears on all 32768 tokens" if tokens == CFG5_TOKENS else
+             f"the six linears on {tokens} of {CFG5_TOKENS} tokens, the per-token part scaled")
     return {"value": round(CFG5_TOKENS / step_s, 2), "unit": "tokens/s", "cores": _blas_threads(), "kind": "port",
-            "sample": f"one [4096,4096] linear on {tokens} tokens ({per_token * 1e3:.2f} ms/token) + its weight-"
-                      f"gradient requantize ({per_step:.2f} s), scaled x{scale:.0f} to the six linears and to "
-                      f"{CFG5_TOKENS} tokens: {step_s:.0f} s per layer step (NumPy / OpenBLAS)"}
+            "sample": f"{shape} ({per_token * 1e3:.3f} ms per token) + the weights' quantize and gradient "
+                      f"requantize ({per_step:.2f} s per step): {step_s:.1f} s per layer step, one timed run "
+                      f"(oracle C restatement for the quantizers, NumPy / OpenBLAS dots)"}
 
 
 def cpu_baseline_optimizer():
@@ -198,6 +217,7 @@ def cpu_baseline_optimizer():
 
 
 MAX_GRAPH_STEPS = 256
+SUSTAINED_STEPS = 200
 
 
 def timed_graph(step, steps: int, warmup: int, replays: int = 1):
@@ -270,12 +290,15 @@ def bench_quantize(steps: int, warmup: int):
             raise RuntimeError(lib.pratchya_last_error().decode())
 
     ms, wall = timed_graph(step, steps, warmup)
+    # the same launches sustained over SUSTAINED_STEPS (reported beside the
+    # headline's --steps figure; not the headline)
+    ms_long, _ = timed_graph(step, SUSTAINED_STEPS, 0)
     # parity spot check of the last output against the oracle on a slice
     q8, s8, s32 = outs[(steps - 1) % n_sets]
     xb = O.activation_input(CFG2_ROWS, CFG2_COLS, seed=2)[:64]
     r8, rs8, _ = O.quantize_impl(O.bf16_bits_to_f32(xb), (1, 128))
     ok = np.array_equal(q8[:64].cpu().numpy(), r8) and np.array_equal(s8[:64 * 2].cpu().numpy(), rs8)
-    return ms, wall, ok
+    return ms, wall, ok, ms_long
 
 
 CFG1_N = 1024
@@ -352,8 +375,7 @@ def bench_gemm_fwd():
         K.gemm_nt(a, b, out=outs[i % 2])
 
     ms, _ = timed_graph(step, GEMM_LAUNCHES, 4, GEMM_REPLAYS)
-    rows = np.sort(np.random.default_rng(3).choice(M, 256, replace=False))
-    sample = _gemm_host_sample(xq, wq, outs[(GEMM_LAUNCHES - 1) % 2], rows, Kd // 128)
+    sample = _gemm_host_sample(xq, wq, outs[(GEMM_LAUNCHES - 1) % 2], np.arange(M), Kd // 128)
     return ms, 2.0 * M * N * Kd / (ms * 1e-3) / 1e12, sample
 
 
@@ -378,8 +400,7 @@ def bench_gemm_ffn():
     del x, w
     out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     ms, _ = timed_graph(lambda i: K.gemm_nt(a, b, out=out), 20, 2, GEMM_REPLAYS)
-    rows = np.sort(np.random.default_rng(5).choice(M, 128, replace=False))
-    sample = _gemm_host_sample(xq, wq, out, rows, Kd // 128)
+    sample = _gemm_host_sample(xq, wq, out, np.arange(M), Kd // 128)
     flop = 2 * M * N * Kd
     tf = flop / (ms * 1e-3) / 1e12
     return {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1), "frac_of_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4),
@@ -458,9 +479,9 @@ def bench_config4():
     write the payload in the tensor's own [T, C] layout and the wgrad GEMM
     reads both operands K-major (the backward's path); the "_t" legs time the
     transposed-payload form and the GEMM over it for comparison.  Each kernel
-    is timed on its own (median of 5 timed replays of 50 launches; dY rotates
-    through two copies); requant bytes and GEMM FLOPs are the algorithmic
-    counts."""
+    is timed on its own (median of 5 timed replays of 50 launches; dY and the
+    dY legs' outputs rotate through two copies); requant bytes and GEMM FLOPs
+    are the algorithmic counts."""
     import torch
     from oracle import qarr_oracle as O
     from pratchya_amd import _kernels as K
@@ -489,19 +510,21 @@ def bench_config4():
     a_sets = [tuple(t.clone() for t in a8) for _ in range(n_a)]
     at_outs = [tuple(torch.empty_like(t) for t in at) for _ in range(n_a)]
     ak_outs = [tuple(torch.empty_like(t) for t in ak) for _ in range(n_a)]
-    dyq_out = tuple(torch.empty_like(t) for t in dyq)
-    dyt_out = tuple(torch.empty_like(t) for t in dyt)
-    dyk_out = tuple(torch.empty_like(t) for t in dyk)
+    # the dY legs' outputs rotate with their inputs (2 x (268 MB in + 134 MB
+    # out) > the 256 MB MALL), so no output rewrite is absorbed by the cache
+    dyq_outs = [tuple(torch.empty_like(t) for t in dyq) for _ in range(2)]
+    dyt_outs = [tuple(torch.empty_like(t) for t in dyt) for _ in range(2)]
+    dyk_outs = [tuple(torch.empty_like(t) for t in dyk) for _ in range(2)]
     res = {}
     e_dy, e_a = T * Dout, T * Din
     cases = [
-        ("requant_dy_1x128", lambda i: K.quantize(dys[i % 2], (1, 128), out=dyq_out),
+        ("requant_dy_1x128", lambda i: K.quantize(dys[i % 2], (1, 128), out=dyq_outs[i % 2]),
          e_dy * 3 + e_dy // 128 + e_dy // 1024 * 4),
-        ("requant_dy_128x1", lambda i: K.quantize_128x1(dys[i % 2], out=dyk_out),
+        ("requant_dy_128x1", lambda i: K.quantize_128x1(dys[i % 2], out=dyk_outs[i % 2]),
          e_dy * 3 + e_dy // 128 + e_dy // 1024 * 4),
         ("requant_a_fp8_to_128x1", lambda i: K.quantize_128x1(*a_sets[i % n_a], out=ak_outs[i % n_a]),
          e_a * 2 + 2 * (e_a // 128 + e_a // 1024 * 4)),
-        ("requant_dy_128x1_t", lambda i: K.quantize_t128(dys[i % 2], out=dyt_out),
+        ("requant_dy_128x1_t", lambda i: K.quantize_t128(dys[i % 2], out=dyt_outs[i % 2]),
          e_dy * 3 + e_dy // 128 + e_dy // 1024 * 4),
         ("requant_a_fp8_to_128x1_t", lambda i: K.quantize_t128(*a_sets[i % n_a], out=at_outs[i % n_a]),
          e_a * 2 + 2 * (e_a // 128 + e_a // 1024 * 4)),
@@ -513,6 +536,7 @@ def bench_config4():
         res[name] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                      "bytes": nbytes}
     flop = 2 * T * Din * Dout
+    host_inputs = tuple(t.float().cpu().numpy() for t in (dy, x, w))   # for the CPU baseline
     for name, fn in (("dgrad_gemm", lambda i: K.gemm_nt(op_dy, op_w, out=gx)),
                      ("wgrad_gemm", lambda i: K.gemm_nt(op_ak, op_dyk, out=gw)),
                      ("wgrad_gemm_t", lambda i: K.gemm_nt(op_at, op_dyt, out=gw))):
@@ -521,7 +545,7 @@ def bench_config4():
         tf = flop / (ms * 1e-3) / 1e12
         res[name] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1), "frac_of_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4),
                      "flop": flop}
-    return res
+    return res, host_inputs
 
 
 CFG5_TOKENS, CFG5_D, CFG5_F = 32768, 4096, 16384
@@ -878,7 +902,8 @@ COPY_BYTES = 256 << 20   # bytes read (and written) by the reference copy of the
 
 def counter_workload(reps: int = 10) -> None:
     """Direct launches (no graph) for rocprofv3 counter runs: ``reps`` x the
-    config-2 quantize, ``reps`` x the config-3 GEMM, ``reps`` x the d=4096 FFN
+    config-2 quantize, ``reps`` x config 4's dY quantize, ``reps`` x the
+    config-3 GEMM, ``reps`` x the d=4096 FFN
     GEMM (after its operands are quantized), and ``reps`` x a plain
     device-to-device copy of COPY_BYTES (``dst.copy_(src)``, which the HIP
     runtime runs as its copyBuffer kernel), whose FETCH_SIZE / WRITE_SIZE
@@ -898,6 +923,16 @@ def counter_workload(reps: int = 10) -> None:
         q = K.quantize(x, (1, 128))
     torch.cuda.synchronize()
     _log(f"counter workload: {reps} x quantize done")
+    # config 4's cotangent dY [16384, 8192] ~ N(0, 1e-3) quantized (1, 128)
+    # (the requant_dy_1x128 leg; its grid, 4x the config-2 one, tells it apart)
+    g4 = torch.Generator(device="cuda").manual_seed(4)
+    dy = (torch.randn((CFG2_ROWS, 8192), generator=g4, device="cuda") * 1e-3).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        K.quantize(dy, (1, 128))
+    torch.cuda.synchronize()
+    del dy
+    _log(f"counter workload: {reps} x config-4 dY quantize done")
     a = K.operand_rows(*q, (1, 128))
     out = torch.empty((CFG2_ROWS, 8192), dtype=torch.bfloat16, device="cuda")
     for _ in range(reps):
@@ -969,7 +1004,7 @@ def main():
             ms_, tf_, _ = bench_gemm_fwd()
             res = {"ms": ms_, "TFLOP/s": tf_}
         elif args.only == "cfg4":
-            res = bench_config4()
+            res = bench_config4()[0]
         elif args.only == "ffn":
             res = bench_gemm_ffn()[0]
         elif args.only == "optim":
@@ -999,9 +1034,16 @@ def main():
     extra["elementwise_add"] = bench_elementwise(max(20, args.steps // 2), max(4, args.warmup // 4))
     _log(f"elementwise add: {extra['elementwise_add']['us']} us")
     _log("config 2 quantize: start")
-    ms, wall, ok = bench_quantize(args.steps, args.warmup)
-    _log(f"config 2 quantize: {ms * 1e3:.2f} us/step, parity spot check {'ok' if ok else 'FAILED'}")
+    ms, wall, ok, ms_long = bench_quantize(args.steps, args.warmup)
+    _log(f"config 2 quantize: {ms * 1e3:.2f} us/step, parity spot check {'ok' if ok else 'FAILED'}; "
+         f"{SUSTAINED_STEPS} launches: {ms_long * 1e3:.2f} us/step")
     gbs = CFG2_BYTES / (ms * 1e-3) / 1e9
+    gbs_long = CFG2_BYTES / (ms_long * 1e-3) / 1e9
+    extra["config2_quantize_sustained"] = {
+        "steps": SUSTAINED_STEPS, "us": round(ms_long * 1e3, 2), "GB/s": round(gbs_long, 1),
+        "frac_of_hbm_peak": round(gbs_long / HBM_PEAK_GBS, 4),
+        "note": f"the headline's kernel and inputs over {SUSTAINED_STEPS} launches in one timed region "
+                f"(the headline times --steps launches)"}
     if not args.no_gemm:
         _log("mfma ceiling: start")
         extra["mfma_ceiling"] = bench_mfma_ceiling()
@@ -1020,7 +1062,7 @@ def main():
         extra["ffn_d4096_gemm_fwd"], ffn_sample = bench_gemm_ffn()
         _log(f"d=4096 FFN gemm fwd: {extra['ffn_d4096_gemm_fwd']['TFLOP/s']} TFLOP/s")
         _log("config 4: start")
-        extra["config4_backward"] = bench_config4()
+        extra["config4_backward"], cfg4_inputs = bench_config4()
         _log("config 5: start")
         extra["config5_layer"] = bench_config5()
         _log(f"config 5: {extra['config5_layer']['tokens_per_s']} tokens/s")
@@ -1038,7 +1080,7 @@ def main():
         if "config3_gemm_fwd" in extra:
             extra["config3_gemm_fwd"]["cpu_baseline"] = cpu_baseline_gemm(cfg3_sample, 16384)
             extra["ffn_d4096_gemm_fwd"]["cpu_baseline"] = cpu_baseline_gemm(ffn_sample, CFG5_TOKENS)
-            extra["config4_backward"]["cpu_baseline"] = cpu_baseline_config4()
+            extra["config4_backward"]["cpu_baseline"] = cpu_baseline_config4(cfg4_inputs)
             extra["config5_layer"]["cpu_baseline"] = cpu_baseline_config5()
             extra["optimizer_step"]["cpu_baseline"] = cpu_baseline_optimizer()
         _log("cpu baselines of configs 1, 3, 4, 5, the FFN GEMM, the embedding lookup, the elementwise add and "

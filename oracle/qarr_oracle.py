@@ -28,7 +28,9 @@ vectors for this path, so no reference KAT exists):
                             edge patterns; NaN sign/payload unpinned (XLA).
 ``bf16_to_e4m3fn``          pinned: exhaustive vs torch ``.to(float8_e4m3fn)``.
 ``quantize_impl``           pinned: KATs + brute force + C restatement.
-``dequantize_impl``         pinned: KATs + exact-rational brute force.
+``dequantize_impl``         pinned: closed forms (exact values where the scale
+                            is a power of two, (1,1) grids, e8m0 0 blocks),
+                            the 2^-4 block error bound, bf16 = RNE(f32).
 ``dequantize_bwd``          pinned: closed form on power-of-two scales.
 ``matmul_*`` (f32 GEMM)     pinned: float64 matmul of the dequantized operands;
                             tolerance-based, as the reference GEMM is f32.

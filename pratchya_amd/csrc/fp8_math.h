@@ -1,5 +1,5 @@
 // Scalar arithmetic of pratchya's FP8 block format, shared by the gfx950
-// kernels and by a host build used to test it exhaustively on the CPU.
+// kernels (host-callable as well, so the same definitions compile on both sides).
 //
 // Format (pratchya/_qualia/_qarr.py:484-499, quantize_impl):
 //   m  = max|x| of an a x b block;  G = max m over K consecutive blocks

@@ -351,6 +351,35 @@ int pratchya_gemm_bs_nt_fq(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, 
                            uint8_t* c_sc8, float* c_sc32, void* workspace, int64_t workspace_bytes,
                            hipStream_t stream);
 
+/* The quantize prologue: replaces the quantized Linear's
+ *   QArrayImpl(x, (1, 128)) @ kernel            (pratchya/_nnx_impl/_module.py:46-50)
+ * i.e. quantize_impl(X, (1, 128)) (Q:458-506) followed by matmul_impl
+ * (Q:605-608), in one launch: before their first output tiles, the GEMM's
+ * workgroups quantize each 1024-value group of the bf16 activation X [M, K]
+ * once (row stride ldx elements, a multiple of 8, 16-byte aligned) and write
+ * the payload A [M, K] (row stride K), e8m0 bytes a_sc8 [M * K / 1024, 8] and
+ * group maxima a_sc32 [M * K / 1024] (the arrays quantize_impl returns, bit
+ * for bit; 256-byte aligned), wait for one another, and read them back as
+ * their A operand.  B and its scales, C, ldc, c_dtype as pratchya_gemm_bs_nt
+ * (B's scale groups at least 32 rows); fq = 1: the output requantization of
+ * pratchya_gemm_bs_nt_fq as well (N a multiple of 1024, c_sc8 / c_sc32 as
+ * there; fq = 0: they are unused).  M at least 256, K a multiple of 1024
+ * (PRATCHYA_EUNSUPPORTED otherwise).  workspace:
+ * pratchya_gemm_bs_nt_qa_workspace_bytes(M, N, fq) bytes, 4-byte aligned,
+ * cleared by a kernel of this call (calls sharing one workspace must not
+ * overlap); its 32-bit word at byte pratchya_gemm_bs_nt_qa_status_offset(M, N,
+ * fq) has bit 1 set if a wait for a group of four output tiles ran out (those
+ * outputs are then NaN) and bit 2 if the wait for the prologue's end ran out
+ * (the outputs are then not defined); never expected while the call has the
+ * device to itself. */
+int64_t pratchya_gemm_bs_nt_qa_workspace_bytes(int64_t M, int64_t N, int fq);
+int64_t pratchya_gemm_bs_nt_qa_status_offset(int64_t M, int64_t N, int fq);
+int pratchya_gemm_bs_nt_qa(const void* X, int64_t ldx, uint8_t* A, uint8_t* a_sc8, float* a_sc32,
+                           const uint8_t* B, int64_t ldb, const uint8_t* b_sc8, const float* b_sc32,
+                           int64_t b_rdiv, int64_t b_sr, int64_t b_sk, int64_t b_kg, int64_t M, int64_t N,
+                           int64_t K, void* C, int64_t ldc, int c_dtype, int fq, uint8_t* c_sc8, float* c_sc32,
+                           void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
 /* pratchya_gemm_bs_nt with both operands K-major:  the weight gradient
  * (Q:621-622, matmul_impl's backward, dW = x^T . dY over the tokens) reading
  * x and dY quantized (128, 1) in their own [T, C] layout, through the LDS

@@ -940,6 +940,66 @@ def gemm_nt_fq(a: Operand, b: Operand, out_dtype: torch.dtype, fix_nan: bool = F
     return y, sc8.view(E8M0), sc32
 
 
+def gemm_nt_qa(x: torch.Tensor, b: Operand, out_dtype: torch.dtype, fq: bool = False, lead=None,
+               status: torch.Tensor = None):
+    """``quantize_impl(x, (1, 128))`` of a bf16 activation ``x`` [..., K] and
+    the GEMM ``dequant(x_q) @ dequant(b)^T`` in one launch (the quantize
+    prologue, pratchya_gemm_bs_nt_qa): each row of ``x`` is quantized once,
+    by the GEMM's workgroups before their first tiles.  Returns ``(y [M, N], (x8, sc8,
+    sc32), out_scales)``: ``(x8, sc8, sc32)`` bit-identical to
+    ``quantize(x, (1, 128))`` (what the backward keeps), ``y`` bit-identical to
+    ``gemm_nt(operand_rows(*that), b, out_dtype)``, or with ``fq`` to
+    ``gemm_nt_fq(..., out_dtype)``, whose output scales are ``out_scales``
+    (else None).  ``lead`` shapes the output scales as in gemm_nt_fq.  Raises ``PratchyaUnsupported`` where the fused path does not
+    apply (x not bf16, fewer than 256 rows, K not a multiple of 1024, B's scale
+    groups narrower than 32 rows, N not a multiple of 1024 with ``fq``)."""
+    _require_gpu(x, b.payload)
+    if x.dtype != torch.bfloat16:
+        raise PratchyaUnsupported(f"gemm_qa: the quantize prologue takes bf16 activations (got {x.dtype})")
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"gemm_qa: output dtype {out_dtype} is not float32 or bfloat16")
+    K = int(x.shape[-1])
+    if b.k != K:
+        raise ValueError(f"contraction mismatch: {K} vs {b.k}")
+    if b.k_major:
+        raise PratchyaUnsupported("gemm_qa: B must be K-contiguous")
+    M, N = x.numel() // K, b.rows
+    if not x.is_contiguous() or not _aligned(x, 16):
+        x = x.contiguous() if not x.is_contiguous() else x.clone()
+    S, H, W = slices_hw(x.shape)
+    _, Kg, Mg = group_layout(H, W, (1, 128))
+    xlead = tuple(x.shape[:-2]) if x.dim() >= 2 else ()
+    x8 = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    xs8 = torch.empty(xlead + (Mg, Kg), dtype=torch.uint8, device=x.device)
+    xs32 = torch.empty(xlead + (Mg, 1, 1), dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    ws_bytes = lib.pratchya_gemm_bs_nt_qa_workspace_bytes(M, N, 1 if fq else 0)
+    if ws_bytes <= 0:
+        raise PratchyaUnsupported(f"gemm_qa: unsupported shape M={M} N={N} fq={fq}")
+    bp = _tile_readable(_u8(b.payload).contiguous())
+    bs8, bs32 = _word_readable(_u8(b.sc8).contiguous()), b.sc32.contiguous().float()
+    y = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    if fq:
+        lead = tuple(lead) if lead else (1,)
+        Sl = 1
+        for d in lead[:-1]:
+            Sl *= int(d)
+        Hl = M // Sl
+        osc8 = torch.empty(tuple(lead[:-1]) + (Hl * N // 1024, 8), dtype=torch.uint8, device=x.device)
+        osc32 = torch.empty(tuple(lead[:-1]) + (Hl * N // 1024, 1, 1), dtype=torch.float32, device=x.device)
+    else:
+        osc8 = osc32 = None
+    ws = torch.empty(int(ws_bytes), dtype=torch.uint8, device=x.device)
+    _lib.check(lib.pratchya_gemm_bs_nt_qa(_ptr(x), K, _ptr(x8), _ptr(xs8), _ptr(xs32),
+                                          _ptr(bp), K, _ptr(bs8), _ptr(bs32), *b.desc,
+                                          M, N, K, _ptr(y), N, _dtype_code(out_dtype), 1 if fq else 0,
+                                          _ptr(osc8) if fq else None, _ptr(osc32) if fq else None,
+                                          _ptr(ws), int(ws_bytes), _stream(x)), "gemm_qa")
+    _wait_status(ws, int(lib.pratchya_gemm_bs_nt_qa_status_offset(M, N, 1 if fq else 0)), status, "gemm_qa")
+    xq = (x8.view(E4M3), xs8.view(E8M0), xs32)
+    return y, xq, ((osc8.view(E8M0), osc32) if fq else None)
+
+
 def _as_operand(x, what):
     """(tensor, dtype code, sc8, sc32) of an optimizer operand: an fp8 payload
     given as a (payload, sc8, sc32) triple, or a bf16 / f32 tensor."""

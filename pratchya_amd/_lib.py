@@ -78,6 +78,12 @@ SIGNATURES = {
                                         _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_int, _c_int, _c_p, _c_p,
                                         _c_p, _c_i64, _c_p]),
     "pratchya_gemm_bs_nt_fq_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "pratchya_gemm_bs_nt_qa": (_c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p,
+                                        _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
+                                        _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_int, _c_int, _c_p, _c_p,
+                                        _c_p, _c_i64, _c_p]),
+    "pratchya_gemm_bs_nt_qa_workspace_bytes": (_c_i64, [_c_i64, _c_i64, _c_int]),
+    "pratchya_gemm_bs_nt_qa_status_offset": (_c_i64, [_c_i64, _c_i64, _c_int]),
     "pratchya_gemm_bs_nt_fq_status_offset": (_c_i64, [_c_i64, _c_i64]),
     "pratchya_gemm_bs_kmajor": (_c_int, [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
                                          _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,

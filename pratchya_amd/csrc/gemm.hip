@@ -449,7 +449,7 @@ __device__ __forceinline__ void scale_by_units(v16f (&acc)[2][4], const uint8_t*
 }
 
 // Output tile of workgroup `bid`: XCD-aware numbering (see the file header).
-__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int* tm, int* tn) {
+__host__ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int* tm, int* tn) {
   const int T = tiles_m * tiles_n;
   int L = bid;
   if (T % 8 == 0) L = (bid % 8) * (T / 8) + bid / 8;
@@ -549,6 +549,7 @@ __device__ __forceinline__ void tri_of(int q, int tri, bool order16, int* ti, in
 // device-scope release and acquire fences, which write back and invalidate
 // the whole L2 (measured: 18% of the kernel's time).
 constexpr int kSc1 = 16;           // cache policy bit sc1 of buffer loads and stores
+constexpr int kNt = 2;             // cache policy bit nt (non-temporal: data read once)
 
 __device__ __forceinline__ float* gram_slot(const FqArgs& fq, int r, int wave) {
   return fq.part + ((int64_t)r * 8 + wave) * (32 * 256);
@@ -643,7 +644,7 @@ __device__ __forceinline__ void gram_add_partials(v16f (&acc)[2][4], const FqArg
 // and L is XCD-aware as in tile_of when `xcd` (the counters b, b+8, b+16, b+24
 // of the workgroups on one XCD then hold one strip); bands of up to 4 tile rows
 // are walked strip by strip.
-__device__ __forceinline__ void tile_of_fq(int bid, int tiles_m, int tiles_n, bool xcd, int* tm, int* tn) {
+__host__ __device__ __forceinline__ void tile_of_fq(int bid, int tiles_m, int tiles_n, bool xcd, int* tm, int* tn) {
   const int T = tiles_m * tiles_n;
   int L = xcd ? (bid % 8) * (T / 8) + bid / 8 : bid;
   const int q = L & 3;
@@ -665,9 +666,230 @@ __device__ __forceinline__ void tile_of_fq(int bid, int tiles_m, int tiles_n, bo
 // multiple of them, and the host requires N % 4 == 0 for finer groups.)  A
 // dimension below 256 rows has one tile at 0: its operand buffer holds 256
 // readable rows, and outputs beyond n are not stored.
-__device__ __forceinline__ int tile_base(int t, int n) {
+__host__ __device__ __forceinline__ int tile_base(int t, int n) {
   const int b = t * 256;
   return (n >= 256 && b > n - 256) ? n - 256 : b;
+}
+
+// Quantize prologue (QA, pratchya_gemm_bs_nt_qa): the A operand is
+// quantize_impl(X, (1, 128)) of a bf16 activation X [M, K] (Q:458-506; the
+// quantized Linear's QArrayImpl(x, (1, a)) @ kernel, pratchya/_nnx_impl/
+// _module.py:46-50), computed inside the GEMM's launch, once per row, and
+// written to the caller's payload and scale arrays, which the GEMM then reads
+// as its A operand.
+//
+// Work: the 1024-element groups of X (K / 1024 per row, in row order), cut
+// into runs of 32 consecutive groups (one line of group maxima, two lines of
+// e8m0 bytes).  Workgroup b quantizes runs b, b + G, b + 2G, ... before its
+// first tile, 4 groups per wave and run, three runs' loads (24 KB) in flight
+// per wave while one run is quantized; then every workgroup waits
+// until all have finished (a grid-wide count: the persistent grid is
+// resident as a whole), and the tile loop runs exactly as without the
+// prologue.  The prologue is a function of its own, called once, so that its
+// registers (all free before the first tile) do not shape the allocation of
+// the tile loop, whose scalar registers are all in use.  (Measured and not
+// kept: spreading the runs over the tile boundaries, so that the quantization
+// overlaps other workgroups' MFMA work, and per-tile waits for the rows a
+// tile reads: either made the K loop reload spilled scalar registers.)
+//
+// Visibility across XCDs: every line of the payload and scale arrays is
+// written by the waves of one workgroup (one XCD's L2), with stores issued at
+// device scope (sc1: written through to the device's coherence point, counted
+// complete by vmcnt only once performed there), and no XCD reads A before
+// every store has been performed, so no L2 holds a line of it from before its
+// writes (lines cached by earlier launches are not valid across a launch
+// boundary).  Each workgroup adds 1 to the count (device-scope atomic) once
+// all its waves have passed a vmcnt(0), and waits for G (bounded: a wait that
+// runs out sets bit 2 of the status word; the outputs are then not defined).
+
+// Buffer resources of the quantized outputs (range-checked, 32-bit offsets).
+struct QaRsrc {
+  __amdgpu_buffer_rsrc_t q, e8, g32;
+};
+
+struct QaArgs {
+  const uint8_t* x;        // X, bf16 [M, K] (row stride ldx bytes)
+  uint8_t* q;              // payload [M, K] (the GEMM's A, row stride K)
+  uint8_t* sc8;            // e8m0 bytes [M, K / 128]
+  float* sc32;             // group maxima [M, K / 1024]
+  uint32_t* done;          // workgroups done with the prologue; then the status word
+  int64_t ldx;
+};
+struct QaNone {};
+
+template <typename T>
+__device__ __forceinline__ T* qa_rfl(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
+
+// One group of 1024 bf16 values quantized by one wave, the arithmetic of
+// k_quant_g8's bf16 payload path: v[r] holds the lane's 8 values at elements
+// r * 512 + 8 lane.  Block max by DPP within 16-lane rows, group max G by
+// readlane, e8m0 and 128 / S by block_scale, the division-free cast where no
+// block is clamped (exact for bf16 inputs), else each 4-value word checked
+// against the bf16 rounding midpoints and redone exactly near one; a group
+// whose G is not finite takes the exact per-element path.  g: the group's
+// index (row * K / 1024 + group in the row).
+__device__ __forceinline__ void qa_quant_group(const QaRsrc& rs, const uint4 (&v)[2], int lane, int g) {
+  uint32_t m[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) m[r] = lane_group_max<16>(absmax8_bf16(v[r]));
+  uint32_t Gb = 0;
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) Gb = umax(Gb, readlane_u32(m[r], k * 16));
+  const float G = u2f(Gb);
+  uint32_t e[2], out[2][2];
+  if ((Gb >> 23) < 255u) {
+    const float rcpG128 = __builtin_amdgcn_rcpf(G * 0.0078125f);
+    float y[2];
+    uint32_t clamped = 0;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const BlockScale b = block_scale(m[r], Gb, rcpG128);
+      e[r] = b.e;
+      y[r] = b.y;
+      clamped |= b.clamped ? 1u : 0u;
+    }
+    if (!__any(clamped)) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          out[r][j] = cvt4_hw(elem_f32<true>(v[r], 4 * j) * y[r], elem_f32<true>(v[r], 4 * j + 1) * y[r],
+                              elem_f32<true>(v[r], 4 * j + 2) * y[r], elem_f32<true>(v[r], 4 * j + 3) * y[r]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const float x0 = elem_f32<true>(v[r], 4 * j), x1 = elem_f32<true>(v[r], 4 * j + 1);
+          const float x2 = elem_f32<true>(v[r], 4 * j + 2), x3 = elem_f32<true>(v[r], 4 * j + 3);
+          const float t0 = x0 * y[r], t1 = x1 * y[r], t2 = x2 * y[r], t3 = x3 * y[r];
+          out[r][j] = cvt4_hw(t0, t1, t2, t3);
+          if (mid_key4(t0, t1, t2, t3) <= kMidKey) out[r][j] = cvt4_exact(x0, x1, x2, x3, quant_scale(e[r], G));
+        }
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      e[r] = e8m0_of(u2f(m[r]), G);
+      const float S = quant_scale(e[r], G);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        out[r][j] = cvt4_exact(elem_f32<true>(v[r], 4 * j), elem_f32<true>(v[r], 4 * j + 1),
+                               elem_f32<true>(v[r], 4 * j + 2), elem_f32<true>(v[r], 4 * j + 3), S);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{out[r][0], out[r][1]}, rs.q, g * 1024 + r * 512 + lane * 8, 0,
+                                          kSc1);
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t ek = readlane_u32(e[k / 4], (k % 4) * 16);
+    if (k < 4) lo |= ek << (8 * k);
+    else hi |= ek << (8 * (k - 4));
+  }
+  const bool lead = lane == 0;
+  __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{lo, hi}, rs.e8, lead ? g * 8 : kOutOfRange, 0, kSc1);
+  __builtin_amdgcn_raw_buffer_store_b32(f2u(G), rs.g32, lead ? g * 4 : kOutOfRange, 0, kSc1);
+}
+
+// Groups 4 wave .. 4 wave + 3 of run R: their indices (ngroups marks none:
+// past the last group) and their loads, issued for every group (past the
+// last, at an offset the range check turns into zeros), so that the number of
+// memory operations in flight never depends on a branch and the waits count
+// exactly.
+__device__ __forceinline__ void qa_load_run(const __amdgpu_buffer_rsrc_t& rx, int64_t ldx, int gpr, int ngroups,
+                                            int R, int wave, int lane, int (&g)[4], uint4 (&v)[4][2]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int gg = R * 32 + wave * 4 + j;
+    const bool ok = gg < ngroups;
+    g[j] = ok ? gg : ngroups;
+    const int row = gg / gpr, gi = gg - row * gpr;
+    const int off = (int)(row * ldx) + gi * 2048 + lane * 16;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      v[j][h] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? off + h * 1024 : kOutOfRange,
+                                                                                 0, kNt));
+  }
+}
+
+__device__ __forceinline__ void qa_quant_run(const QaRsrc& rs, const uint4 (&v)[4][2], int lane, const int (&g)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) qa_quant_group(rs, v[j], lane, g[j]);
+}
+
+// The quantize prologue of one wave (see above), then the grid-wide wait.
+__device__ __attribute__((noinline)) void qa_prologue(const uint8_t* x, uint8_t* q, uint8_t* sc8, float* sc32,
+                                                      uint32_t* done, int64_t ldx, int M, int K, int wave,
+                                                      int lane) {
+  x = qa_rfl(x);
+  q = qa_rfl(q);
+  sc8 = qa_rfl(sc8);
+  sc32 = qa_rfl(sc32);
+  done = qa_rfl(done);
+  ldx = ((int64_t)__builtin_amdgcn_readfirstlane((int)(ldx >> 32)) << 32) |
+        (uint32_t)__builtin_amdgcn_readfirstlane((int)ldx);
+  M = __builtin_amdgcn_readfirstlane(M);
+  K = __builtin_amdgcn_readfirstlane(K);
+  wave = __builtin_amdgcn_readfirstlane(wave);
+  const int gpr = K >> 10, ngroups = M * gpr, runs = (ngroups + 31) >> 5, G = (int)gridDim.x, b = (int)blockIdx.x;
+  // (the host keeps X within 2^31 bytes)
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(x), 0, (int)((M - 1) * ldx + 2 * (int64_t)K), kRawBuffer);
+  QaRsrc rs;
+  rs.q = __builtin_amdgcn_make_buffer_rsrc(q, 0, (int)((int64_t)M * K), kRawBuffer);
+  rs.e8 = __builtin_amdgcn_make_buffer_rsrc(sc8, 0, ngroups * 8, kRawBuffer);
+  rs.g32 = __builtin_amdgcn_make_buffer_rsrc(sc32, 0, ngroups * 4, kRawBuffer);
+  // four buffers of one run each in rotation: three runs' loads in flight
+  // while one is quantized; every load and store is issued on every pass
+  uint4 v0[4][2], v1[4][2], v2[4][2], v3[4][2];
+  int g0[4], g1[4], g2[4], g3[4];
+  qa_load_run(rx, ldx, gpr, ngroups, b, wave, lane, g0, v0);
+  qa_load_run(rx, ldx, gpr, ngroups, b + G, wave, lane, g1, v1);
+  qa_load_run(rx, ldx, gpr, ngroups, b + 2 * G, wave, lane, g2, v2);
+  for (int R = b; R < runs; R += 4 * G) {
+    qa_load_run(rx, ldx, gpr, ngroups, R + 3 * G, wave, lane, g3, v3);
+    qa_quant_run(rs, v0, lane, g0);
+    if (R + G >= runs) break;
+    qa_load_run(rx, ldx, gpr, ngroups, R + 4 * G, wave, lane, g0, v0);
+    qa_quant_run(rs, v1, lane, g1);
+    if (R + 2 * G >= runs) break;
+    qa_load_run(rx, ldx, gpr, ngroups, R + 5 * G, wave, lane, g1, v1);
+    qa_quant_run(rs, v2, lane, g2);
+    if (R + 3 * G >= runs) break;
+    qa_load_run(rx, ldx, gpr, ngroups, R + 6 * G, wave, lane, g2, v2);
+    qa_quant_run(rs, v3, lane, g3);
+  }
+  // every wave's stores performed (device scope) before the workgroup is
+  // counted: one atomic per workgroup on the shared count, and one poller
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  asm volatile("" ::: "memory");
+  __syncthreads();
+  if (wave == 0 && lane == 0) {
+    __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the grid is resident as a whole (one workgroup per CU, grid <= CUs);
+    // the bound only keeps a broken launch from spinning forever
+    for (int it = 0; __hip_atomic_fetch_add(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (uint32_t)G;
+         ++it) {
+      if (it >= (1 << 20)) {
+        __hip_atomic_fetch_or(done + 1, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(16);
+    }
+  }
+  asm volatile("" ::: "memory");       // the operand loads stay after the count was seen
+  __syncthreads();
 }
 
 // Epilogue: C[m][n] = acc * gA * gB / 2^14 (the two /128 of the dequant) for
@@ -1023,12 +1245,14 @@ __device__ __forceinline__ void store_tile_ns(const v16f (&acc)[2][4], uint8_t* 
   }
 }
 
-template <bool OUT_BF16, int BG, int FQ, bool BF = false, int KM = 0>
+template <bool OUT_BF16, int BG, int FQ, bool BF = false, int KM = 0, bool QA = false>
 __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B, int64_t ldb,
     Scales sa, Scales sb, void* __restrict__ C, int64_t ldc, int K, int span, int tiles_m,
     int tiles_n, uint32_t a_bytes, uint32_t b_bytes, uint32_t ea_bytes, uint32_t eb_bytes,
-    uint32_t ga_bytes, uint32_t gb_bytes, int M, int N, FqArgs fq) {
+    uint32_t ga_bytes, uint32_t gb_bytes, int M, int N, FqArgs fq,
+    std::conditional_t<QA, QaArgs, QaNone> qa) {
+  static_assert(!QA || (!BF && KM == 0 && FQ <= 2), "the quantize prologue feeds an FP8 A operand");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + ((FQ == 1 || FQ == 2) ? FQ_TABLE_BYTES : 0)];
   const OperandRsrc ra = make_rsrc(A, a_bytes, sa, ea_bytes, ga_bytes);
   const OperandRsrc rb = make_rsrc(B, b_bytes, sb, eb_bytes, gb_bytes);
@@ -1157,6 +1381,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
   } else {
     next_tile(t, &tm, &tn);
   }
+
+  // quantize prologue: A is written and complete on every XCD before any
+  // tile loads it
+  if constexpr (QA) qa_prologue(qa.x, qa.q, qa.sc8, qa.sc32, qa.done, qa.ldx, M, K, wave, lane);
   DmaRows cur = rows_of(tm, tn, kb);
   int par = 0;                            // stage buffer of the unit's first K block
 
@@ -1607,7 +1835,7 @@ void gemm_launch(const GemmPlan& P, const uint8_t* A, int64_t lda, const uint8_t
   hipLaunchKernelGGL((k_gemm_bs_nt<BF, BG, FQ, false, KM>), dim3((unsigned)P.grid), dim3(NTHREADS), 0, stream, A, lda, B,
                      ldb, P.sa, P.sb, C, ldc, (int)K, (int)P.span, (int)P.tiles_m, (int)P.tiles_n,
                      (uint32_t)P.a_bytes, (uint32_t)P.b_bytes, (uint32_t)P.ea_bytes, (uint32_t)P.eb_bytes,
-                     (uint32_t)P.ga_bytes, (uint32_t)P.gb_bytes, (int)M, (int)N, fq);
+                     (uint32_t)P.ga_bytes, (uint32_t)P.gb_bytes, (int)M, (int)N, fq, QaNone{});
 }
 
 int launch_status(const char* who) {
@@ -1756,6 +1984,111 @@ extern "C" int pratchya_gemm_bs_nt_fq(const uint8_t* A, int64_t lda, const uint8
 
 namespace {
 
+
+template <bool OB, int FQ>
+void gemm_launch_qa(const GemmPlan& P, const uint8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, void* C,
+                    int64_t ldc, int64_t M, int64_t N, int64_t K, const FqArgs& fq, const QaArgs& qa,
+                    hipStream_t stream) {
+  hipLaunchKernelGGL((k_gemm_bs_nt<OB, 0, FQ, false, 0, true>), dim3((unsigned)P.grid), dim3(NTHREADS), 0, stream,
+                     A, lda, B, ldb, P.sa, P.sb, C, ldc, (int)K, (int)P.span, (int)P.tiles_m, (int)P.tiles_n,
+                     (uint32_t)P.a_bytes, (uint32_t)P.b_bytes, (uint32_t)P.ea_bytes, (uint32_t)P.eb_bytes,
+                     (uint32_t)P.ga_bytes, (uint32_t)P.gb_bytes, (int)M, (int)N, fq, qa);
+}
+
+}  // namespace
+
+// Workspace of the quantize prologue: the count of waves done with it, the
+// status word, then the output requantization's maxima and counts (fq).
+extern "C" int64_t pratchya_gemm_bs_nt_qa_workspace_bytes(int64_t M, int64_t N, int fq) {
+  if (M < BM || N <= 0 || (fq && N % 1024)) return 0;
+  const int64_t words = 2 + (fq ? fq_workspace_words(M, N) : 0);
+  return ((words * 4 + 255) / 256) * 256;
+}
+
+extern "C" int64_t pratchya_gemm_bs_nt_qa_status_offset(int64_t M, int64_t N, int fq) {
+  if (M < BM || N <= 0 || (fq && N % 1024)) return -1;
+  return 4;
+}
+
+extern "C" int pratchya_gemm_bs_nt_qa(const void* X, int64_t ldx, uint8_t* A, uint8_t* a_sc8, float* a_sc32,
+                                      const uint8_t* B, int64_t ldb, const uint8_t* b_sc8, const float* b_sc32,
+                                      int64_t b_rdiv, int64_t b_sr, int64_t b_sk, int64_t b_kg, int64_t M,
+                                      int64_t N, int64_t K, void* C, int64_t ldc, int c_dtype, int fq,
+                                      uint8_t* c_sc8, float* c_sc32, void* workspace, int64_t workspace_bytes,
+                                      hipStream_t stream) {
+  const char* who = "gemm_qa";
+  if (M < 0 || N < 0 || K < 0) return pratchya_set_error(PRATCHYA_EINVAL, "%s: negative size", who);
+  if (M == 0 || N == 0 || K == 0) return PRATCHYA_OK;
+  if (M < BM)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: M must be at least 256 (got %lld)", who, (long long)M);
+  if (K % 1024)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: K must be a multiple of 1024 (got %lld)", who,
+                              (long long)K);
+  if (fq != 0 && fq != 1) return pratchya_set_error(PRATCHYA_EINVAL, "%s: fq must be 0 or 1", who);
+  if (fq && N % 1024)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: N must be a multiple of 1024 with the output "
+                              "requantization (got %lld)", who, (long long)N);
+  if (!X || !A || !a_sc8 || !a_sc32 || !workspace) return pratchya_set_error(PRATCHYA_EINVAL, "%s: null buffer", who);
+  if (ldx < K || ldx % 8 || reinterpret_cast<uintptr_t>(X) % 16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "%s: X must be 16-byte aligned with a row stride of at least K, a "
+                              "multiple of 8", who);
+  if ((M - 1) * ldx * 2 + 2 * K > (int64_t)INT32_MAX)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: X beyond 2 GiB", who);
+  if ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(a_sc8) | reinterpret_cast<uintptr_t>(a_sc32)) %
+      256)
+    return pratchya_set_error(PRATCHYA_EINVAL, "%s: the quantized outputs must be 256-byte aligned", who);
+  GemmPlan P;
+  int rc = gemm_plan(who, A, K, a_sc8, a_sc32, 1, K / 128, 1, 8, B, ldb, b_sc8, b_sc32, b_rdiv, b_sr, b_sk, b_kg,
+                     M, N, K, C, ldc, c_dtype, &P);
+  if (rc) return rc;
+  if (P.bg != 0) return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: B scale groups narrower than 32 rows", who);
+  if (workspace_bytes < pratchya_gemm_bs_nt_qa_workspace_bytes(M, N, fq) ||
+      reinterpret_cast<uintptr_t>(workspace) % 4)
+    return pratchya_set_error(PRATCHYA_EINVAL, "%s: workspace of %lld bytes (need %lld, 4-byte aligned)", who,
+                              (long long)workspace_bytes, (long long)pratchya_gemm_bs_nt_qa_workspace_bytes(M, N, fq));
+  uint32_t* ws = static_cast<uint32_t*>(workspace);
+  FqArgs fqa{};
+  if (fq) {
+    if (ldc >= (int64_t)1 << 23)
+      return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: output row stride of 2^23 elements or more", who);
+    if (!c_sc8 || !c_sc32) return pratchya_set_error(PRATCHYA_EINVAL, "%s: null buffer", who);
+    const int64_t tiles = P.tiles_m * P.tiles_n;
+    fqa.xcd = tiles % 32 == 0 && P.grid >= 32 ? 1 : 0;
+    P.grid -= P.grid % (fqa.xcd ? 32 : 4);
+    const int64_t strips = fq_strips(M, N);
+    fqa.sc8 = c_sc8;
+    fqa.sc32 = c_sc32;
+    fqa.gmax = ws + 2;
+    fqa.arrive = fqa.gmax + strips * 256;
+    fqa.status = ws + 1;
+  }
+  QaArgs qa;
+  qa.x = static_cast<const uint8_t*>(X);
+  qa.q = A;
+  qa.sc8 = a_sc8;
+  qa.sc32 = a_sc32;
+  qa.done = ws;                        // the status word follows
+  qa.ldx = ldx * 2;
+  // count, status (and the output requantization's maxima and counts) start
+  // at zero: a kernel, not a memset, so the call can be captured
+  const int64_t words = 2 + (fq ? fq_workspace_words(M, N) : 0);
+  const int64_t fill_blocks = (words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024;
+  hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)fill_blocks), dim3(256), 0, stream, ws, words, 0u);
+  rc = launch_status(who);
+  if (rc) return rc;
+  const bool bf = c_dtype == PRATCHYA_DT_BF16;
+  if (fq) {
+    if (bf) gemm_launch_qa<true, 1>(P, A, K, B, ldb, C, ldc, M, N, K, fqa, qa, stream);
+    else gemm_launch_qa<false, 1>(P, A, K, B, ldb, C, ldc, M, N, K, fqa, qa, stream);
+  } else {
+    if (bf) gemm_launch_qa<true, 0>(P, A, K, B, ldb, C, ldc, M, N, K, fqa, qa, stream);
+    else gemm_launch_qa<false, 0>(P, A, K, B, ldb, C, ldc, M, N, K, fqa, qa, stream);
+  }
+  return launch_status(who);
+}
+
+namespace {
+
 // Validated plan of a bf16 product C [M, N] = A [M, K] . B [N, K]^T (returns
 // a status; *empty when there is nothing to compute).
 int bf16_plan(const char* who, const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M, int64_t N,
@@ -1802,7 +2135,7 @@ void bf16_launch(const GemmPlan& P, const void* A, int64_t lda, const void* B, i
   hipLaunchKernelGGL((k_gemm_bs_nt<OB, 0, FQ, true, KM>), dim3((unsigned)P.grid), dim3(NTHREADS), 0, stream,
                      static_cast<const uint8_t*>(A), lda * 2, static_cast<const uint8_t*>(B), ldb * 2, P.sa, P.sb,
                      C, ldc, (int)(K * 2), 1, (int)P.tiles_m, (int)P.tiles_n, (uint32_t)P.a_bytes,
-                     (uint32_t)P.b_bytes, 0u, 0u, 0u, 0u, (int)M, (int)N, fq);
+                     (uint32_t)P.b_bytes, 0u, 0u, 0u, 0u, (int)M, (int)N, fq, QaNone{});
 }
 
 }  // namespace

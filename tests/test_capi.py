@@ -477,3 +477,43 @@ def test_quantize_dual_argument_codes_without_gpu():
     assert lib.pratchya_quantize_dual(f, _lib.DT_F32, 1, 128, 1024, *args(ctypes.c_void_p((1 << 20) + 8))) \
         == _lib.EUNSUPPORTED
     assert b"aligned" in lib.pratchya_last_error()
+
+
+def test_gemm_qa_arguments_without_gpu():
+    """pratchya_gemm_bs_nt_qa: workspace and status-word queries (the
+    prologue's count, the status word, then the output requantization's
+    layout with fq), and the argument checks that return before any launch:
+    too few rows, K not a multiple of 1024, N not a multiple of 1024 with fq,
+    narrow B groups, misaligned X or outputs, null or short workspace."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    for M, N, fq in ((512, 2048, 0), (32768, 16384, 1), (300, 1024, 1)):
+        units = -(-M // 256)
+        words = 2 + ((units * (N // 1024)) * 257 + 1 if fq else 0)
+        assert lib.pratchya_gemm_bs_nt_qa_workspace_bytes(M, N, fq) == (words * 4 + 255) // 256 * 256
+        assert lib.pratchya_gemm_bs_nt_qa_status_offset(M, N, fq) == 4
+    assert lib.pratchya_gemm_bs_nt_qa_workspace_bytes(255, 1024, 0) == 0
+    assert lib.pratchya_gemm_bs_nt_qa_workspace_bytes(512, 768, 1) == 0
+    assert lib.pratchya_gemm_bs_nt_qa_status_offset(512, 768, 1) == -1
+    fake = ctypes.c_void_p(1 << 20)          # aligned, never dereferenced
+    wgt = (128, 1, 8, 1024)                  # (128,128) weight used transposed
+    need = lib.pratchya_gemm_bs_nt_qa_workspace_bytes(512, 1024, 1)
+
+    def args(M=512, N=1024, K=1024, bdesc=wgt, x=fake, A=fake, fq=1, ws=fake, ws_bytes=need):
+        return (x, K, A, fake, fake, fake, K, fake, fake, *bdesc, M, N, K, fake, N, _lib.DT_BF16, fq,
+                fake, fake, ws, ws_bytes, None)
+
+    assert lib.pratchya_gemm_bs_nt_qa(*args(M=0)) == 0
+    assert lib.pratchya_gemm_bs_nt_qa(*args(M=-1)) == _lib.EINVAL
+    assert lib.pratchya_gemm_bs_nt_qa(*args(M=255)) == _lib.EUNSUPPORTED
+    assert lib.pratchya_gemm_bs_nt_qa(*args(K=512)) == _lib.EUNSUPPORTED
+    assert b"1024" in lib.pratchya_last_error()
+    assert lib.pratchya_gemm_bs_nt_qa(*args(N=768)) == _lib.EUNSUPPORTED
+    assert lib.pratchya_gemm_bs_nt_qa(*args(bdesc=(1, 1, 1024, 8))) == _lib.EUNSUPPORTED
+    assert lib.pratchya_gemm_bs_nt_qa(*args(x=ctypes.c_void_p((1 << 20) + 8))) == _lib.EINVAL
+    assert lib.pratchya_gemm_bs_nt_qa(*args(A=ctypes.c_void_p((1 << 20) + 128))) == _lib.EINVAL
+    assert b"256-byte" in lib.pratchya_last_error()
+    assert lib.pratchya_gemm_bs_nt_qa(*args(ws=None)) == _lib.EINVAL
+    assert lib.pratchya_gemm_bs_nt_qa(*args(ws_bytes=need - 4)) == _lib.EINVAL
+    assert b"workspace" in lib.pratchya_last_error()
+    assert lib.pratchya_gemm_bs_nt_qa(*args(fq=2)) == _lib.EINVAL

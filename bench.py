@@ -553,7 +553,7 @@ CFG5_LINEARS = [(CFG5_D, CFG5_D)] * 4 + [(CFG5_D, CFG5_F), (CFG5_F, CFG5_D)]   #
 CFG5_FLOP = 3 * 2 * CFG5_TOKENS * sum(a * b for a, b in CFG5_LINEARS)
 
 
-def bench_config5(steps: int = 10, warmup: int = 2):
+def bench_config5(steps: int = 10, warmup: int = 2, prologue: bool = False):
     """Config 5: the six quantized linears of one RWKV-7 block at d_model 4096
     (r/k/v/o [4096, 4096], FFN [4096, 16384] and [16384, 4096]) over 32768
     tokens (batch 8 x seq 4096): forward, dgrad and wgrad of each through the
@@ -562,11 +562,15 @@ def bench_config5(steps: int = 10, warmup: int = 2):
     bf16, cotangents requantized), with the FP8 MFMA backward.  Synthetic bf16
     activations N(0, 1), weights N(0, 0.02), output cotangents N(0, 1e-3),
     seed 5.  A step is one layer's fwd + bwd; the median of ``steps`` (10)
-    event-timed steps is reported as tokens/s."""
+    event-timed steps is reported as tokens/s.  ``prologue``: each activation's
+    (1, 128) quantization runs inside its forward GEMM's launch
+    (qarr.set_quantize_prologue) instead of as its own kernel."""
     import torch
     from pratchya_amd import qarr as Q
     prev = Q.get_matmul_backward()
+    prev_qa = Q.get_quantize_prologue()
     Q.set_matmul_backward("fp8")
+    Q.set_quantize_prologue(prologue)
     try:
         gen = torch.Generator(device="cuda").manual_seed(5)
         xs = {n: torch.randn((CFG5_TOKENS, n), generator=gen, device="cuda").to(torch.bfloat16)
@@ -599,11 +603,14 @@ def bench_config5(steps: int = 10, warmup: int = 2):
         ms = float(np.median([ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]))
     finally:
         Q.set_matmul_backward(prev)
+        Q.set_quantize_prologue(prev_qa)
     tf = CFG5_FLOP / (ms * 1e-3) / 1e12
     return {"tokens_per_s": round(CFG5_TOKENS / (ms * 1e-3), 1), "ms_per_layer_step": round(ms, 3),
             "effective_TFLOP/s": round(tf, 1), "frac_of_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4),
             "gemm_flop_per_step": CFG5_FLOP, "steps": f"median of {steps}",
-            "path": "pratchya_amd.qarr Linear composition, fp8 backward, eager (no graph)"}
+            "path": "pratchya_amd.qarr Linear composition, fp8 backward, eager (no graph)"
+                    + (", activation quantize fused into the forward GEMM (pratchya_gemm_bs_nt_qa)" if prologue
+                       else ", activation quantized by its own kernel")}
 
 
 def _event_ms(fn, reps: int) -> float:
@@ -981,8 +988,8 @@ def main():
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--counter-workload", action="store_true",
                     help="only run the direct-launch workload used for rocprofv3 --pmc runs")
-    ap.add_argument("--only", choices=["cfg3", "ffn", "cfg4", "cfg5", "optim", "elementwise", "embedding",
-                                       "ceiling"],
+    ap.add_argument("--only", choices=["cfg3", "ffn", "cfg4", "cfg5", "cfg5qa", "optim", "elementwise",
+                                       "embedding", "ceiling"],
                     default=None,
                     help="run one secondary configuration alone (for profiling) and print its result")
     args = ap.parse_args()
@@ -1015,6 +1022,8 @@ def main():
             res = bench_embedding(max(20, args.steps // 4), max(4, args.warmup // 4))
         elif args.only == "ceiling":
             res = bench_mfma_ceiling()
+        elif args.only == "cfg5qa":
+            res = bench_config5(prologue=True)
         else:
             res = bench_config5()
         print(json.dumps({args.only: res}), flush=True)
@@ -1066,6 +1075,10 @@ def main():
         _log("config 5: start")
         extra["config5_layer"] = bench_config5()
         _log(f"config 5: {extra['config5_layer']['tokens_per_s']} tokens/s")
+        qa = bench_config5(prologue=True)
+        extra["config5_layer_fused_prologue"] = {k: qa[k] for k in ("tokens_per_s", "ms_per_layer_step",
+                                                                    "frac_of_fp8_peak", "path")}
+        _log(f"config 5 with the fused quantize prologue: {qa['tokens_per_s']} tokens/s")
         _log("optimizer step: start")
         extra["optimizer_step"] = bench_optimizer(3)
         _log(f"optimizer step: {extra['optimizer_step']['ms_per_step']} ms")

@@ -73,6 +73,42 @@ def get_matmul_backward() -> str:
     return _backward_mode
 
 
+# The quantized Linear's QArrayImpl(x, (1, 128)) @ kernel (pratchya/_nnx_impl/
+# _module.py:46-50): the activation quantized by its own kernel before the
+# GEMM (default), or inside the GEMM's launch as a prologue
+# (pratchya_gemm_bs_nt_qa; same bytes).  Measured at d_model 4096 the
+# prologue is 1-3% slower than the separate pass: it runs at the GEMM's two
+# waves per SIMD, where the quantizer alone runs at full occupancy.
+_quantize_prologue = False
+
+
+def set_quantize_prologue(fused: bool) -> None:
+    """Fuse the (1, 128) activation quantization of ``QArrayImpl(x, (1, 128))
+    @ kernel`` into the GEMM's launch (True) or run it as its own pass
+    (False, default).  With True, such an array of a bf16 activation is held
+    unquantized until first use; a product with a quantized weight dequantized
+    by ``astype`` / ``dequantize`` (the Linear's output) then runs the fused
+    kernel, any other use quantizes it as before.  Results are bit-identical
+    either way."""
+    global _quantize_prologue
+    _quantize_prologue = bool(fused)
+
+
+def get_quantize_prologue() -> bool:
+    return _quantize_prologue
+
+
+def _prologue_eligible(value, tgrid, quant) -> bool:
+    """A bf16 CUDA activation [..., K] with tgrid (1, 128), K a multiple of
+    1024 and at least 256 rows: what pratchya_gemm_bs_nt_qa takes."""
+    if not (_quantize_prologue and quant and torch.is_tensor(value) and tgrid is not None):
+        return False
+    if tuple(tgrid) != (1, 128) or value.dtype != torch.bfloat16 or not value.is_cuda or value.dim() < 2:
+        return False
+    K = int(value.shape[-1])
+    return K % 1024 == 0 and value.numel() // K >= 256
+
+
 def _grid_hw(shape) -> Tuple[int, int]:
     """(H, W) of the last two axes as the reference sees them (Q:461-464)."""
     if len(shape) == 0:
@@ -440,30 +476,66 @@ class _QLinear(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, g):
-        x8, y8 = ctx.saved[0], ctx.saved[3]
-        gx, gy, go = ctx.grids
-        os8, os32 = ctx.out_scales
-        need_x, need_y = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        g = g.contiguous()
-        res = None
-        if (_backward_mode == "fp8" and tuple(go) == (1, 128) and g.dtype == torch.bfloat16
-                and int(os8.shape[-1]) == 8):
-            # the FP8 dgrad / wgrad quantizers take the cotangent through the
-            # output's dequantize_impl_bwd themselves (8-block groups: the
-            # output's scales index the same way for the flattened rows)
-            res = _fp8_backward(g, *ctx.saved, gx, gy, need_x, need_y, pre=(os8, os32), x_dtype=ctx.dtypes[0])
-        gx_final = False
-        if res is not None:
-            gxf, gyf, gx_final = res
-        else:
-            g1 = K.dequantize_bwd(g, os8, os32, go)
-            gxf, gyf = _matmul_cotangents(g1, ctx.saved, (gx, gy), need_x, need_y)
-        grad_x = grad_y = None
-        if need_x:
-            grad_x = gxf if gx_final else _requant_cotangent(_reduce_broadcast(gxf, x8.shape), gx, ctx.dtypes[0])
-        if need_y:
-            grad_y = _requant_cotangent(_reduce_broadcast(gyf, y8.shape), gy, ctx.dtypes[1])
-        return (grad_x, grad_y) + (None,) * 10
+        return _qlinear_grads(ctx, g) + (None,) * 10
+
+
+def _qlinear_grads(ctx, g):
+    """(grad_x, grad_y) of a quantized Linear's node (_QLinear, _QLinearQA):
+    inputs 0 and 1 are the sources of x and y."""
+    x8, y8 = ctx.saved[0], ctx.saved[3]
+    gx, gy, go = ctx.grids
+    os8, os32 = ctx.out_scales
+    need_x, need_y = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+    g = g.contiguous()
+    res = None
+    if (_backward_mode == "fp8" and tuple(go) == (1, 128) and g.dtype == torch.bfloat16
+            and int(os8.shape[-1]) == 8):
+        # the FP8 dgrad / wgrad quantizers take the cotangent through the
+        # output's dequantize_impl_bwd themselves (8-block groups: the
+        # output's scales index the same way for the flattened rows)
+        res = _fp8_backward(g, *ctx.saved, gx, gy, need_x, need_y, pre=(os8, os32), x_dtype=ctx.dtypes[0])
+    gx_final = False
+    if res is not None:
+        gxf, gyf, gx_final = res
+    else:
+        g1 = K.dequantize_bwd(g, os8, os32, go)
+        gxf, gyf = _matmul_cotangents(g1, ctx.saved, (gx, gy), need_x, need_y)
+    grad_x = grad_y = None
+    if need_x:
+        grad_x = gxf if gx_final else _requant_cotangent(_reduce_broadcast(gxf, x8.shape), gx, ctx.dtypes[0])
+    if need_y:
+        grad_y = _requant_cotangent(_reduce_broadcast(gyf, y8.shape), gy, ctx.dtypes[1])
+    return grad_x, grad_y
+
+
+class _QLinearQA(torch.autograd.Function):
+    """_QLinear with x given unquantized (a bf16 activation, grid (1, 128)):
+    the activation's quantization runs inside the GEMM's launch
+    (pratchya_gemm_bs_nt_qa, with the output's requantization in its
+    epilogue), and the quantized activation it writes -- the bytes
+    quantize_impl returns -- becomes x's fields (``xo``) and what the backward
+    contracts.  Same values and gradients as quantize_impl followed by
+    _QLinear."""
+
+    @staticmethod
+    def forward(ctx, src_x, src_y, x, xo, y8, ys8, ys32, gy, go, dtype):
+        op_b = _rhs_operand(y8, ys8, ys32, gy)
+        if op_b is None:
+            raise K.PratchyaUnsupported("gemm_qa: the weight's layout does not fit the FP8 GEMM")
+        lead, N = tuple(x.shape[:-1]), int(y8.shape[1])
+        res, xq, (os8, os32) = K.gemm_nt_qa(x.detach(), op_b, dtype, fq=True, lead=lead)
+        if src_x is not None:
+            setattr(xq[0], _SRC, src_x)
+        xo._materialize(xq)
+        ctx.saved = xq + (y8, ys8, ys32)
+        ctx.out_scales = (os8, os32)
+        ctx.grids = ((1, 128), tuple(gy), tuple(go))
+        ctx.dtypes = (_grad_dtype(src_x), _grad_dtype(src_y))
+        return res.reshape(lead + (N,))
+
+    @staticmethod
+    def backward(ctx, g):
+        return _qlinear_grads(ctx, g) + (None,) * 8
 
 
 def matmul_impl(x_fp8, x_sc8, x_sc32, y_fp8, y_sc8, y_sc32, block_grid_x: Tuple, block_grid_y: Tuple):
@@ -672,6 +744,14 @@ class QArrayImpl:
     """An FP8 block-quantized array: e4m3fn payload, per-block e8m0 scales and
     per-group f32 maxima (Q:15-425).  ``quant=False`` wraps a plain tensor."""
 
+    def __new__(cls, value=None, tgrid=None, quant=True, **kwargs):
+        # with the quantize prologue on, an activation the fused GEMM takes is
+        # held unquantized (_PendingQuant) until its first use (subclasses
+        # pass their own constructor arguments through)
+        if cls is QArrayImpl and _prologue_eligible(value, tgrid, quant):
+            return super().__new__(_PendingQuant)
+        return super().__new__(cls)
+
     def __init__(self, value: Union["QArrayImpl", torch.Tensor], tgrid: Optional[Tuple[int, int]] = None,
                  quant: bool = True):
         if not quant:
@@ -751,6 +831,9 @@ class QArrayImpl:
 
     def __matmul__(self, other):
         other = _value_of(other)
+        if "_pending" in self.__dict__ and isinstance(other, QArrayImpl):
+            # x not quantized yet: the product keeps it so, for the fused GEMM
+            return _LazyProduct(None, self.__tgrid, other.__tgrid, pending=(self, other))
         if isinstance(other, QArrayImpl):
             other = self._promote(other, 1)
             # QArrayImpl(matmul_impl(self, other), (self.tgrid[0], other.tgrid[1])) (Q:100-105)
@@ -965,13 +1048,50 @@ class _LazyProduct(QArrayImpl):
 
     _FIELDS = ("_QArrayImpl__value", "_QArrayImpl__sc_fp8", "_QArrayImpl__sc_fp32")
 
-    def __init__(self, operands, gx, gy):
+    def __init__(self, operands, gx, gy, pending=None):
         self._QArrayImpl__tgrid = (int(gx[0]), int(gy[1]))
         self._operands = operands
         self._grids = (tuple(gx), tuple(gy))
         self._grad_enabled = torch.is_grad_enabled()
-        self._srcs = (_src(operands[0]), _src(operands[3]))
         self._dequantized = {}
+        if pending is not None:
+            # (x, y) with x a _PendingQuant not quantized yet: the Linear's
+            # output (dequantize) takes x into the fused GEMM, anything else
+            # quantizes it first (_resolve)
+            self._pending_xy = pending
+        else:
+            self._srcs = (_src(operands[0]), _src(operands[3]))
+
+    def _resolve(self):
+        """The operands of a product whose x was pending, x quantized now."""
+        if "_pending_xy" in self.__dict__:
+            xo, yo = self.__dict__.pop("_pending_xy")
+            with torch.set_grad_enabled(self._grad_enabled):
+                self._operands = (xo._QArrayImpl__value, xo._QArrayImpl__sc_fp8, xo._QArrayImpl__sc_fp32,
+                                  yo._QArrayImpl__value, yo._QArrayImpl__sc_fp8, yo._QArrayImpl__sc_fp32)
+                self._srcs = (_src(self._operands[0]), _src(self._operands[3]))
+
+    def _fused_dequantize(self, dtype):
+        """The Linear's output with x's quantization in the GEMM's launch, or
+        None where the fused kernel does not apply (x is then still pending)."""
+        xo, yo = self._pending_xy
+        go = self._QArrayImpl__tgrid
+        gy = self._grids[1]
+        if "_pending" not in xo.__dict__ or tuple(go) != (1, 128):
+            return None
+        y8, ys8, ys32 = yo._QArrayImpl__value, yo._QArrayImpl__sc_fp8, yo._QArrayImpl__sc_fp32
+        if y8.dim() != 2 or int(y8.shape[1]) % 1024 or _rhs_operand(y8, ys8, ys32, gy) is None:
+            return None
+        x = xo._pending
+        with torch.set_grad_enabled(self._grad_enabled):
+            sx = x if (x.requires_grad and torch.is_grad_enabled()) else None
+            sy = _src(y8)
+            try:
+                res = _QLinearQA.apply(sx, sy, x, xo, y8, ys8, ys32, gy, go, dtype)
+            except K.PratchyaUnsupported:
+                return None
+        self._resolve()
+        return res
 
     def __getattr__(self, name):
         # reached only for attributes not set yet: the quantized fields
@@ -981,6 +1101,7 @@ class _LazyProduct(QArrayImpl):
         raise AttributeError(name)
 
     def _materialize(self):
+        self._resolve()
         x8, xs8, xs32, y8, ys8, ys32 = self._operands
         gx, gy = self._grids
         sx, sy = self._srcs
@@ -999,6 +1120,12 @@ class _LazyProduct(QArrayImpl):
         hit = self._dequantized.get(dtype)
         if hit is not None and hit[0]._version == hit[1]:
             return hit[0].clone()
+        if "_pending_xy" in self.__dict__:
+            res = self._fused_dequantize(dtype)
+            if res is not None:
+                self._dequantized[dtype] = (res, res._version)
+                return res
+            self._resolve()
         x8, xs8, xs32, y8, ys8, ys32 = self._operands
         gx, gy = self._grids
         go = self._QArrayImpl__tgrid
@@ -1014,6 +1141,9 @@ class _LazyProduct(QArrayImpl):
 
     @property
     def shape(self):
+        if "_pending_xy" in self.__dict__:
+            xs, ys = self._pending_xy[0].shape, self._pending_xy[1].shape
+            return tuple(torch.empty(xs, device="meta").matmul(torch.empty(ys, device="meta")).shape)
         if "_operands" in self.__dict__:
             x8, y8 = self._operands[0], self._operands[3]
             return tuple(torch.empty(x8.shape, device="meta").matmul(torch.empty(y8.shape, device="meta")).shape)
@@ -1028,7 +1158,54 @@ class _LazyProduct(QArrayImpl):
         return E4M3
 
 
-for _cls in (QArrayImpl, _LazyProduct):      # a lazy product flattens to its materialised fields
+class _PendingQuant(QArrayImpl):
+    """``QArrayImpl(x, (1, 128))`` of a bf16 activation with the quantize
+    prologue on (set_quantize_prologue): x held unquantized until first use.
+    A product with a quantized weight that the Linear dequantizes quantizes x
+    inside the GEMM's launch (_QLinearQA) and fills the fields with its bytes;
+    any other use (payload, scales, arithmetic, slicing, pytree flattening)
+    quantizes x first with quantize_impl.  Either way the fields hold
+    quantize_impl(x, (1, 128)) bit for bit."""
+
+    _FIELDS = ("_QArrayImpl__value", "_QArrayImpl__sc_fp8", "_QArrayImpl__sc_fp32")
+
+    def __init__(self, value, tgrid=None, quant: bool = True):
+        self._QArrayImpl__tgrid = (1, 128)
+        self._pending = value
+        self._grad_enabled = torch.is_grad_enabled()
+
+    def __getattr__(self, name):
+        # reached only for attributes not set yet: the quantized fields
+        if name in _PendingQuant._FIELDS and "_pending" in self.__dict__:
+            self._materialize()
+            return self.__dict__[name]
+        raise AttributeError(name)
+
+    def _materialize(self, q=None):
+        """Fill the fields: with ``q`` (the fused GEMM's quantized x) or by
+        quantize_impl."""
+        value = self.__dict__.pop("_pending")
+        if q is None:
+            with torch.set_grad_enabled(self._grad_enabled):
+                q = quantize_impl(value, (1, 128))
+        self._QArrayImpl__value, self._QArrayImpl__sc_fp8, self._QArrayImpl__sc_fp32 = q
+
+    @property
+    def shape(self):
+        if "_pending" in self.__dict__:
+            return tuple(self._pending.shape)
+        return super().shape
+
+    @property
+    def size(self):
+        return math.prod(self.shape)
+
+    @property
+    def dtype(self):
+        return E4M3
+
+
+for _cls in (QArrayImpl, _LazyProduct, _PendingQuant):   # lazy forms flatten to their materialised fields
     pytree.register_pytree_node(
         _cls,
         lambda q: q._tree_flatten(),

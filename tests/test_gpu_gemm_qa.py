@@ -152,3 +152,80 @@ def test_rejects_what_it_does_not_fuse():
         K.gemm_nt_qa(_act((128, 1024), seed=72), wop, torch.bfloat16)          # fewer than 256 rows
     with pytest.raises(K.PratchyaUnsupported):
         K.gemm_nt_qa(_act((512, 1024), seed=73).float(), wop, torch.bfloat16)  # not bf16
+
+
+# --------------------------------------------------------------------------
+# The quantized-array API with the prologue on (qarr.set_quantize_prologue)
+# --------------------------------------------------------------------------
+def _linear(x0, w0, g, prologue, mode):
+    """``(QArrayImpl(x, (1, 128)) @ QArrayImpl(w, (128, 128))).astype(bf16)``
+    and its backward (pratchya/_nnx_impl/_module.py:46-50): output, x.grad,
+    w.grad, and x's quantized fields read after the step."""
+    from pratchya_amd import qarr as Q
+    prev = (Q.get_quantize_prologue(), Q.get_matmul_backward())
+    Q.set_quantize_prologue(prologue)
+    Q.set_matmul_backward(mode)
+    try:
+        x = x0.detach().clone().requires_grad_(True)
+        w = w0.detach().clone().requires_grad_(True)
+        xq = Q.QArrayImpl(x, (1, 128))
+        assert isinstance(xq, Q._PendingQuant) == prologue
+        y = (xq @ Q.QArrayImpl(w, (128, 128))).astype(torch.bfloat16)
+        y.backward(g)
+        fields = (xq._QArrayImpl__value, xq._QArrayImpl__sc_fp8, xq._QArrayImpl__sc_fp32)
+        torch.cuda.synchronize()
+        return y.detach(), x.grad, w.grad, fields
+    finally:
+        Q.set_quantize_prologue(prev[0])
+        Q.set_matmul_backward(prev[1])
+
+
+@pytest.mark.parametrize("mode", ["fp8", "f32"])
+@pytest.mark.parametrize("shape", [(4096, 4096, 4096), (2, 1024, 2048, 1024)], ids=lambda s: "x".join(map(str, s)))
+def test_linear_with_prologue_matches_separate_pass(shape, mode):
+    """The Linear through the API with the quantize prologue on: output, both
+    gradients and x's quantized fields bit-identical to the default path
+    (the activation quantized by its own kernel)."""
+    *xs, N = shape
+    x0 = _act(tuple(xs), seed=81)
+    g_ = torch.Generator(device="cuda").manual_seed(82)
+    w0 = (torch.randn((xs[-1], N), generator=g_, device="cuda") * 0.02).to(torch.bfloat16)
+    g = (torch.randn(tuple(xs[:-1]) + (N,), generator=g_, device="cuda") * 1e-3).to(torch.bfloat16)
+    got = _linear(x0, w0, g, True, mode)
+    want = _linear(x0, w0, g, False, mode)
+    for a, b, what in zip(got[:3], want[:3], ("output", "x.grad", "w.grad")):
+        assert a.dtype == b.dtype and a.shape == b.shape, what
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), f"{what} differs with the prologue ({mode})"
+    _same_q(got[3], want[3], f"x fields ({mode})")
+
+
+def test_pending_activation_other_uses():
+    """A pending activation used other than through the Linear quantizes as
+    before: fields, dequantize, arithmetic, a product materialized by its
+    payload, and shapes the fused kernel does not take (stay eager)."""
+    from pratchya_amd import qarr as Q
+    prev = Q.get_quantize_prologue()
+    Q.set_quantize_prologue(True)
+    try:
+        x = _act((512, 2048), seed=91)
+        want = _K().quantize(x, (1, 128))
+        q = Q.QArrayImpl(x, (1, 128))
+        assert isinstance(q, Q._PendingQuant) and q.shape == (512, 2048)
+        _same_q((q._QArrayImpl__value, q._QArrayImpl__sc_fp8, q._QArrayImpl__sc_fp32), want, "fields")
+        d = Q.QArrayImpl(x, (1, 128)).astype(torch.float32)
+        assert torch.equal(d, _K().dequantize(*want, torch.float32, (1, 128)))
+        wq = Q.QArrayImpl((torch.randn((2048, 1024), device="cuda") * 0.02).to(torch.bfloat16), (128, 128))
+        p = Q.QArrayImpl(x, (1, 128)) @ wq
+        assert p.shape == (512, 1024)
+        v = p._QArrayImpl__value                          # materialized as the reference builds it
+        Q.set_quantize_prologue(False)
+        p2 = Q.QArrayImpl(x, (1, 128)) @ wq
+        assert torch.equal(v.view(torch.uint8), p2._QArrayImpl__value.view(torch.uint8))
+        Q.set_quantize_prologue(True)
+        assert not isinstance(Q.QArrayImpl(_act((512, 1536), seed=92), (1, 128)), Q._PendingQuant)
+        assert not isinstance(Q.QArrayImpl(_act((128, 2048), seed=93), (1, 128)), Q._PendingQuant)
+        assert not isinstance(Q.QArrayImpl(x.float(), (1, 128)), Q._PendingQuant)
+        assert not isinstance(Q.QArrayImpl(x, (128, 128)), Q._PendingQuant)
+        torch.cuda.synchronize()
+    finally:
+        Q.set_quantize_prologue(prev)

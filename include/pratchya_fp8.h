@@ -107,6 +107,16 @@ int pratchya_quantize_dequantize(const void* x, int x_dtype, int64_t slices, int
                                  uint8_t* sc_fp8, float* sc_fp32, void* workspace,
                                  size_t workspace_bytes, hipStream_t stream);
 
+/* pratchya_quantize_dequantize of an f32 x whose block maxima are given:
+ * block_max holds, per block of the (a, b) grid (row-major over the block
+ * grid, slices stacked), max |x| as f32 bits (what
+ * pratchya_gemm_bs_blockmax writes for a = b = 128), so only the group scales
+ * and the cast run.  Same outputs and arguments as
+ * pratchya_quantize_dequantize otherwise (x_dtype f32, no workspace). */
+int pratchya_quantize_dequantize_premax(const float* x, int64_t slices, int64_t H, int64_t W, int64_t a,
+                                        int64_t b, const uint32_t* block_max, void* out, int out_dtype,
+                                        int fix_nan, uint8_t* sc_fp8, float* sc_fp32, hipStream_t stream);
+
 /* Requantization of a Linear output's cotangent for the FP8 dgrad, tgrid (1, 128):
  *   quantize_impl(dequantize_impl_bwd(g, g_sc8, g_sc32, (1, 128)), (1, 128))
  * i.e. the output quantization's backward (Q:575-601: (g * 2^(e-127) * G) / 128
@@ -394,6 +404,21 @@ int pratchya_gemm_bs_kmajor(const uint8_t* A, int64_t lda, const uint8_t* a_sc8,
                             int64_t ldb, const uint8_t* b_sc8, const float* b_sc32, int64_t b_rdiv,
                             int64_t b_sr, int64_t b_sk, int64_t b_kg, int64_t M, int64_t N, int64_t K,
                             void* C, int64_t ldc, int c_dtype, hipStream_t stream);
+
+/* The weight gradient's GEMM with its requantization's first pass in the
+ * epilogue: pratchya_gemm_bs_nt (kmajor = 0) or pratchya_gemm_bs_kmajor
+ * (kmajor = 1; lda / ldb as there) to an f32 C [M, N], which also writes, for
+ * each 128 x 128 block of C, max |c| as f32 bits into block_max [M / 128, N /
+ * 128] -- the block maxima quantize_impl(C, (128, 128)) starts from (Q:484-487),
+ * so that the requantization of matmul_impl's weight cotangent (Q:621-622,
+ * :637-638) skips its own pass over C (pratchya_quantize_dequantize_premax).
+ * M and N multiples of 128 (PRATCHYA_EUNSUPPORTED otherwise); the other
+ * arguments and limits as the two GEMMs. */
+int pratchya_gemm_bs_blockmax(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, const float* a_sc32,
+                              int64_t a_rdiv, int64_t a_sr, int64_t a_sk, int64_t a_kg, const uint8_t* B,
+                              int64_t ldb, const uint8_t* b_sc8, const float* b_sc32, int64_t b_rdiv,
+                              int64_t b_sr, int64_t b_sk, int64_t b_kg, int64_t M, int64_t N, int64_t K,
+                              int kmajor, float* C, int64_t ldc, uint32_t* block_max, hipStream_t stream);
 
 /* bf16 GEMM, "NT" form:                  replaces the bf16 dots of newton_schulz
  *   C[m, n] = sum_k A[m, k] * B[n, k]     (pratchya/_nnx_impl/_optimizer.py:20-22,

@@ -663,6 +663,62 @@ def gemm_nt(a: Operand, b: Operand, out_dtype: torch.dtype = torch.bfloat16,
     return out
 
 
+def gemm_nt_blockmax(a: Operand, b: Operand) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``gemm_nt(a, b, float32)`` plus the 128 x 128 block maxima of the
+    product (max |c| as f32 bits, [M / 128, N / 128] int32) from the GEMM's
+    epilogue: the first pass of the product's (128, 128) requantization.
+    Operands K-contiguous or both K-major; M and N multiples of 128
+    (``PratchyaUnsupported`` otherwise)."""
+    _require_gpu(a.payload, b.payload)
+    if a.k != b.k:
+        raise ValueError(f"contraction mismatch: {a.k} vs {b.k}")
+    M, N, K = a.rows, b.rows, a.k
+    if a.k_major != b.k_major:
+        raise PratchyaUnsupported("gemm_blockmax: K-major FP8 operands are supported as a pair")
+    if a.k_major:
+        ap, bp = _u8(a.payload).contiguous(), _u8(b.payload).contiguous()
+    else:
+        ap, bp = _tile_readable(_u8(a.payload).contiguous()), _tile_readable(_u8(b.payload).contiguous())
+    as8, bs8 = _word_readable(_u8(a.sc8).contiguous()), _word_readable(_u8(b.sc8).contiguous())
+    as32, bs32 = a.sc32.contiguous().float(), b.sc32.contiguous().float()
+    out = torch.empty((M, N), dtype=torch.float32, device=ap.device)
+    bmax = torch.empty((max(M // 128, 1), max(N // 128, 1)), dtype=torch.int32, device=ap.device)
+    lda, ldb = (M, N) if a.k_major else (K, K)
+    _lib.check(_lib.load().pratchya_gemm_bs_blockmax(_ptr(ap), lda, _ptr(as8), _ptr(as32), *a.desc,
+                                                     _ptr(bp), ldb, _ptr(bs8), _ptr(bs32), *b.desc,
+                                                     M, N, K, 1 if a.k_major else 0, _ptr(out), N, _ptr(bmax),
+                                                     _stream(ap)), "gemm_blockmax")
+    return out, bmax
+
+
+def quantize_dequantize_premax(x: torch.Tensor, block_max: torch.Tensor, tgrid, dtype: torch.dtype,
+                               fix_nan: bool = False):
+    """``quantize_dequantize(x, tgrid, dtype, fix_nan)`` of an f32 ``x`` whose
+    block maxima ``block_max`` (f32 bits of max |x| per block, as
+    ``gemm_nt_blockmax`` returns them) are already known: only the group
+    scales and the cast run.  Returns ``(y, sc_fp8, sc_fp32)``."""
+    _require_gpu(x, block_max)
+    if x.dtype != torch.float32:
+        raise ValueError("quantize_dequantize_premax: x must be float32")
+    if dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"quantize_dequantize_premax: output dtype {dtype} is not float32 or bfloat16")
+    a, b = int(tgrid[0]), int(tgrid[1])
+    S, H, W = slices_hw(x.shape)
+    n_blk, K, M = group_layout(H, W, (a, b))
+    if block_max.numel() != S * n_blk or block_max.dtype not in (torch.int32, torch.uint32):
+        raise ValueError(f"quantize_dequantize_premax: block_max must hold {S * n_blk} 32-bit maxima")
+    lead = tuple(x.shape[:-2]) if x.dim() >= 2 else ()
+    x = x.contiguous()
+    bm = block_max.contiguous()
+    y = torch.empty(x.shape, dtype=dtype, device=x.device)
+    sc8 = torch.empty(lead + (M, K), dtype=torch.uint8, device=x.device)
+    sc32 = torch.empty(lead + (M, 1, 1), dtype=torch.float32, device=x.device)
+    _lib.check(_lib.load().pratchya_quantize_dequantize_premax(
+        _ptr(x), S, H, W, a, b, _ptr(bm), _ptr(y), _dtype_code(dtype), 1 if fix_nan else 0, _ptr(sc8), _ptr(sc32),
+        _stream(x)), "quantize_dequantize_premax")
+    return y, sc8.view(E8M0), sc32
+
+
 def gemm_bf16_nt(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
     """C[M, N] = a @ b^T for bf16 ``a`` [M, K] and ``b`` [N, K] with f32
     accumulation, rounded once to ``out_dtype``: the bf16 dots of

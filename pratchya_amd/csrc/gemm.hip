@@ -492,6 +492,12 @@ struct FqArgs {
   // tile's sums NaN.
   float* part;
   uint32_t* flags;
+  // Block maxima of the f32 output (FQ 5, pratchya_gemm_bs_blockmax): for
+  // each 128 x 128 block of C, max |c| as f32 bits (the block maxima of
+  // quantize_impl with tgrid (128, 128), Q:484-487), block (r, c) at
+  // r * bmax_ld + c
+  uint32_t* bmax;
+  int bmax_ld;
   int64_t iters;
   int steps;
   int tri;
@@ -900,12 +906,14 @@ __device__ __attribute__((noinline)) void qa_prologue(const uint8_t* x, uint8_t*
 // passed the barrier below) and write them back as full 16-byte lane chunks
 // covering whole rows, with non-temporal stores (the output is not read again
 // by this kernel; streaming it keeps the operand panels in L2).
-template <bool OUT_BF16, int BG>
-__device__ __forceinline__ void store_tile(const v16f (&acc)[2][4], const float (&gA)[2],
-                                           const float (&gB)[4][BG == 1 ? 4 : 1], const uint8_t* ub,
-                                           uint8_t* stage, int wave, int lane, void* C, int64_t ldc, int row0,
-                                           int col0, int M, int N) {
+// BMAX: also returns the lane's max |c| (f32 bits) over the values it wrote.
+template <bool OUT_BF16, int BG, bool BMAX = false>
+__device__ __forceinline__ uint32_t store_tile(const v16f (&acc)[2][4], const float (&gA)[2],
+                                               const float (&gB)[4][BG == 1 ? 4 : 1], const uint8_t* ub,
+                                               uint8_t* stage, int wave, int lane, void* C, int64_t ldc, int row0,
+                                               int col0, int M, int N) {
   const int l32 = lane & 31, lhi = lane >> 5;
+  uint32_t lmax = 0;
   constexpr int ESZ = OUT_BF16 ? 2 : 4;
   constexpr int ROWB = 128 * ESZ;           // bytes of one staged row
   constexpr int PITCH = ROWB + 16;          // padded LDS row pitch
@@ -946,6 +954,8 @@ __device__ __forceinline__ void store_tile(const v16f (&acc)[2][4], const float 
                   make_uint2(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1));
             } else {
               *reinterpret_cast<float4*>(dst) = make_float4(c0, c1, c2, c3);
+              if constexpr (BMAX)
+                lmax = umax(umax(lmax, umax(abs_bits(c0), abs_bits(c1))), umax(abs_bits(c2), abs_bits(c3)));
             }
           }
         }
@@ -964,6 +974,27 @@ __device__ __forceinline__ void store_tile(const v16f (&acc)[2][4], const float 
       }
       __builtin_amdgcn_s_waitcnt(0xC07F);   // staging reads done before the next pass overwrites
     }
+  }
+  return lmax;
+}
+
+// The 128 x 128 block maxima of a tile (FQ 5): each wave's max over its 64 x
+// 128 values (lanes by xor shuffles), the two waves of a block row (wm = 2 br,
+// 2 br + 1, same wn) combined through LDS, one plain store per block (the
+// tiles partition C, so every block is written by one workgroup; an edge tile
+// moved back by 128 rows or columns writes its overlap's maxima again, the
+// same values; blocks past M or N, of a dimension below one tile, are not
+// written).  The barrier waits for LDS only: the output stores stay in flight.
+__device__ __forceinline__ void store_block_max(uint32_t lmax, uint32_t* slot, const FqArgs& fq, int wave, int lane,
+                                                int row0, int col0, int M, int N) {
+#pragma unroll
+  for (int s = 1; s < 64; s <<= 1) lmax = umax(lmax, shfl_xor_u32(lmax, s));
+  if (lane == 0) slot[wave] = lmax;
+  PINNED_WAITCNT(0xC07F);
+  wg_barrier();
+  if ((wave & 1) == 0 && lane == 0 && row0 < M && col0 < N) {
+    const uint32_t m = umax(slot[wave], slot[wave + 1]);
+    fq.bmax[(int64_t)(row0 >> 7) * fq.bmax_ld + (col0 >> 7)] = m;
   }
 }
 
@@ -1253,7 +1284,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
     uint32_t ga_bytes, uint32_t gb_bytes, int M, int N, FqArgs fq,
     std::conditional_t<QA, QaArgs, QaNone> qa) {
   static_assert(!QA || (!BF && KM == 0 && FQ <= 2), "the quantize prologue feeds an FP8 A operand");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + ((FQ == 1 || FQ == 2) ? FQ_TABLE_BYTES : 0)];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES + ((FQ == 1 || FQ == 2) ? FQ_TABLE_BYTES : 0) +
+                                                         (FQ == 5 ? 64 : 0)];
   const OperandRsrc ra = make_rsrc(A, a_bytes, sa, ea_bytes, ga_bytes);
   const OperandRsrc rb = make_rsrc(B, b_bytes, sb, eb_bytes, gb_bytes);
 
@@ -1624,6 +1656,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
                              m0 + wm * 64, n0 + wn * 128, M, N);
       store_tile_fq<OUT_BF16>(acc, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, table, wave, lane, C, ldc,
                               m0 + wm * 64, n0 + wn * 128, M);
+    } else if constexpr (FQ == 5) {
+      static_assert(!OUT_BF16 && !BF, "block maxima of an f32 FP8 product");
+      const uint32_t lm = store_tile<false, BG, true>(acc, gA, gB, lds + OFF_UB + (wn * 128 + lhi * 16) * 4,
+                                                      lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc,
+                                                      m0 + wm * 64, n0 + wn * 128, M, N);
+      store_block_max(lm, reinterpret_cast<uint32_t*>(lds + LDS_BYTES), fq, wave, lane, m0 + wm * 64, n0 + wn * 128,
+                      M, N);
     } else {
       store_tile<OUT_BF16, BG>(acc, gA, gB, lds + OFF_UB + (wn * 128 + lhi * 16) * 4, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc,
                                    m0 + wm * 64, n0 + wn * 128, M, N);
@@ -1913,6 +1952,48 @@ extern "C" int pratchya_gemm_bs_kmajor(const uint8_t* A, int64_t lda, const uint
     else gemm_launch<false, 2, 0, 3>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
   }
   return launch_status("gemm_kmajor");
+}
+
+extern "C" int pratchya_gemm_bs_blockmax(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, const float* a_sc32,
+                                         int64_t a_rdiv, int64_t a_sr, int64_t a_sk, int64_t a_kg, const uint8_t* B,
+                                         int64_t ldb, const uint8_t* b_sc8, const float* b_sc32, int64_t b_rdiv,
+                                         int64_t b_sr, int64_t b_sk, int64_t b_kg, int64_t M, int64_t N, int64_t K,
+                                         int kmajor, float* C, int64_t ldc, uint32_t* bmax, hipStream_t stream) {
+  const char* who = "gemm_blockmax";
+  if (M <= 0 || N <= 0 || K <= 0) {
+    if (M < 0 || N < 0 || K < 0) return pratchya_set_error(PRATCHYA_EINVAL, "%s: negative size", who);
+    return PRATCHYA_OK;
+  }
+  if (M % 128 || N % 128)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: M and N must be multiples of 128 (got %lld, %lld)", who,
+                              (long long)M, (long long)N);
+  if (!bmax) return pratchya_set_error(PRATCHYA_EINVAL, "%s: null buffer", who);
+  GemmPlan P;
+  int rc = gemm_plan(who, A, kmajor ? K : lda, a_sc8, a_sc32, a_rdiv, a_sr, a_sk, a_kg, B, kmajor ? K : ldb, b_sc8,
+                     b_sc32, b_rdiv, b_sr, b_sk, b_kg, M, N, K, C, ldc, PRATCHYA_DT_F32, &P);
+  if (rc) return rc;
+  if (kmajor) {
+    if (lda < M || ldb < N || lda % 16 || ldb % 16 || M % 16 || N % 16)
+      return pratchya_set_error(PRATCHYA_EINVAL, "%s: M, N and the row strides (at least M, N) must be multiples of 16",
+                                who);
+    P.a_bytes = (K - 1) * lda + M;
+    P.b_bytes = (K - 1) * ldb + N;
+    if (P.a_bytes > (int64_t)INT32_MAX || P.b_bytes > (int64_t)INT32_MAX)
+      return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "%s: operands beyond 2 GiB", who);
+  }
+  FqArgs fq{};
+  fq.bmax = bmax;
+  fq.bmax_ld = (int)(N / 128);
+  if (kmajor) {
+    if (P.bg == 0) gemm_launch<false, 0, 5, 3>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+    else if (P.bg == 1) gemm_launch<false, 1, 5, 3>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+    else gemm_launch<false, 2, 5, 3>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+  } else {
+    if (P.bg == 0) gemm_launch<false, 0, 5>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+    else if (P.bg == 1) gemm_launch<false, 1, 5>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+    else gemm_launch<false, 2, 5>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+  }
+  return launch_status(who);
 }
 
 extern "C" int64_t pratchya_gemm_bs_nt_fq_workspace_bytes(int64_t M, int64_t N) {

@@ -858,13 +858,16 @@ unsigned grid_for(int64_t n, int per_block) {
   return (unsigned)(g < 1 ? 1 : g);
 }
 
+// premax: ws already holds the block maxima (f32 bits of max |x| per block,
+// the layout k_blockmax writes), e.g. from the GEMM that produced x.
 template <bool IS_BF16, int OUT = 0>
 int launch_general(const void* x, void* q, uint8_t* sc8, float* sc32, uint32_t* ws,
-                   const Layout& L, hipStream_t st, int fix_nan = 0) {
+                   const Layout& L, hipStream_t st, int fix_nan = 0, bool premax = false) {
   const int64_t n_blocks_total = L.S * L.n_blk;
   const int64_t n_groups = L.S * L.M;
-  hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(n_blocks_total, 256) > 4096 ? 4096 : grid_for(n_blocks_total, 256)),
-                     dim3(256), 0, st, ws, n_blocks_total, 0u);
+  if (!premax)
+    hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(n_blocks_total, 256) > 4096 ? 4096 : grid_for(n_blocks_total, 256)),
+                       dim3(256), 0, st, ws, n_blocks_total, 0u);
   const int ch = chunk_elems(L.b, IS_BF16);
   const int64_t n_chunks = L.n() / ch;
   const int64_t seg = L.b / ch;
@@ -878,7 +881,8 @@ int launch_general(const void* x, void* q, uint8_t* sc8, float* sc32, uint32_t* 
 #define PRATCHYA_BM(C, V)                                                                        \
   hipLaunchKernelGGL((k_blockmax<IS_BF16, C, V>), dim3(grid_for(n_bm, 256)), dim3(256), 0, st, x, ws, \
                      n_bm, L.W, L.a, L.b, seg_log2, rows)
-  if (vin) {
+  if (premax) {
+  } else if (vin) {
     PRATCHYA_BM((IS_BF16 ? 8 : 4), true);
   } else {
     switch (ch) {
@@ -1045,6 +1049,26 @@ extern "C" size_t pratchya_quantize_dequantize_workspace_bytes(int x_dtype, int6
   // aligned x and out) needs none; every other layout runs the general path
   if (g8_layout(L)) return 0;
   return (size_t)(L.S * L.n_blk) * sizeof(uint32_t);
+}
+
+extern "C" int pratchya_quantize_dequantize_premax(const float* x, int64_t slices, int64_t H, int64_t W, int64_t a,
+                                                   int64_t b, const uint32_t* block_max, void* out, int out_dtype,
+                                                   int fix_nan, uint8_t* sc_fp8, float* sc_fp32, hipStream_t stream) {
+  Layout L;
+  int rc = make_layout(slices, H, W, a, b, &L);
+  if (rc) return rc;
+  if (out_dtype != PRATCHYA_DT_F32 && out_dtype != PRATCHYA_DT_BF16)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_dequantize_premax: unsupported output dtype %d", out_dtype);
+  if (L.n() == 0) {
+    g_err[0] = 0;
+    return PRATCHYA_OK;
+  }
+  if (!x || !out || !sc_fp8 || !sc_fp32 || !block_max)
+    return pratchya_set_error(PRATCHYA_EINVAL, "quantize_dequantize_premax: null buffer");
+  uint32_t* ws = const_cast<uint32_t*>(block_max);      // read only: the fill and block-max kernels are skipped
+  const int f = fix_nan ? 1 : 0;
+  return out_dtype == PRATCHYA_DT_BF16 ? launch_general<false, 1>(x, out, sc_fp8, sc_fp32, ws, L, stream, f, true)
+                                       : launch_general<false, 2>(x, out, sc_fp8, sc_fp32, ws, L, stream, f, true);
 }
 
 extern "C" int pratchya_quantize_dequantize(const void* x, int x_dtype, int64_t slices, int64_t H,

@@ -331,15 +331,21 @@ def _matmul_forward(x8, xs8, xs32, y8, ys8, ys32, gx, gy) -> torch.Tensor:
     return _mm_f32(_deq32(x8, xs8, xs32, gx), _deq32(y8, ys8, ys32, gy))
 
 
-def _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y, pre=None, x_dtype=None):
+def _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y, pre=None, x_dtype=None,
+                  y_dtype=None):
     """dgrad / wgrad on the FP8 MFMA kernel (the "fp8" backward), or None
     when the layouts do not fit it.  ``pre``: the (1, 128) scales of the
     product's output quantization when ``g`` is the cotangent of that output
     before dequantize_impl_bwd (the quantizers apply it in registers).
-    Returns ``(gxf, gyf, gx_final)``: with ``x_dtype`` given and x's rows a
-    multiple of 1024 wide, the dgrad GEMM's epilogue also requantizes x's
-    cotangent with x's grid and dequantizes it to ``x_dtype`` as
-    ``_requant_cotangent`` would (``gx_final`` True), bit for bit."""
+    Returns ``(gxf, gyf, gx_final, gy_final)``: with ``x_dtype`` given and
+    x's rows a multiple of 1024 wide, the dgrad GEMM's epilogue also
+    requantizes x's cotangent with x's grid and dequantizes it to ``x_dtype``
+    as ``_requant_cotangent`` would (``gx_final`` True), bit for bit; with
+    ``y_dtype`` given, a (128, 128) weight grid and both weight dimensions
+    multiples of 128, the wgrad GEMM's epilogue writes the gradient's block
+    maxima and ``gyf`` is the weight's cotangent requantized and dequantized
+    to ``y_dtype`` as ``_requant_cotangent`` would (``gy_final`` True), from
+    the group scales and the cast alone."""
     if y8.dim() != 2 or tuple(gx) != (1, 128) or tuple(gy)[1] != 128:
         return None
     if _lhs_operand(x8, xs8, xs32, gx) is None:
@@ -351,7 +357,8 @@ def _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y, pre=N
         return None
     g2 = g.reshape(rows, N)
     gxf = gyf = None
-    gx_final = False
+    gx_final = gy_final = False
+    premax = y_dtype is not None and tuple(gy) == (128, 128) and Kd % 128 == 0 and N % 128 == 0
     try:
         if need_x:
             gq = K.requantize_cotangent(g2, *pre) if pre is not None else K.quantize(g2.contiguous(), (1, 128))
@@ -374,14 +381,26 @@ def _fp8_backward(g, x8, xs8, xs32, y8, ys8, ys32, gx, gy, need_x, need_y, pre=N
             # layout and read K-major by the GEMM (no transposed payloads)
             xq = K.quantize_128x1(x8.reshape(rows, Kd), xs8, xs32)   # stored activation, requantized
             gq = K.quantize_128x1(g2.contiguous(), *(pre if pre is not None else ()))
-            gyf = K.gemm_nt(K.operand_k128(*xq), K.operand_k128(*gq), torch.float32)
+            op_x, op_g = K.operand_k128(*xq), K.operand_k128(*gq)
         elif need_y:
             xt = K.quantize_t128(x8.reshape(rows, Kd), xs8, xs32)
             gt = K.quantize_t128(g2.contiguous(), *(pre if pre is not None else ()))
-            gyf = K.gemm_nt(K.operand_t128(*xt), K.operand_t128(*gt), torch.float32)
+            op_x, op_g = K.operand_t128(*xt), K.operand_t128(*gt)
+        if need_y and premax:
+            # the (128, 128) requantization's block maxima come from the GEMM;
+            # where that variant does not apply, the plain GEMM and the full
+            # requantization below
+            try:
+                gw, bmax = K.gemm_nt_blockmax(op_x, op_g)
+                gyf = K.quantize_dequantize_premax(gw, bmax, gy, y_dtype, fix_nan=True)[0]
+                gy_final = True
+            except K.PratchyaUnsupported:
+                gyf = None
+        if need_y and gyf is None:
+            gyf = K.gemm_nt(op_x, op_g, torch.float32)
     except K.PratchyaUnsupported:
         return None
-    return gxf, gyf, gx_final
+    return gxf, gyf, gx_final, gy_final
 
 
 def _matmul_cotangents(g, saved, grids, need_x, need_y):
@@ -493,10 +512,11 @@ def _qlinear_grads(ctx, g):
         # the FP8 dgrad / wgrad quantizers take the cotangent through the
         # output's dequantize_impl_bwd themselves (8-block groups: the
         # output's scales index the same way for the flattened rows)
-        res = _fp8_backward(g, *ctx.saved, gx, gy, need_x, need_y, pre=(os8, os32), x_dtype=ctx.dtypes[0])
-    gx_final = False
+        res = _fp8_backward(g, *ctx.saved, gx, gy, need_x, need_y, pre=(os8, os32), x_dtype=ctx.dtypes[0],
+                            y_dtype=ctx.dtypes[1] if y8.dim() == 2 else None)
+    gx_final = gy_final = False
     if res is not None:
-        gxf, gyf, gx_final = res
+        gxf, gyf, gx_final, gy_final = res
     else:
         g1 = K.dequantize_bwd(g, os8, os32, go)
         gxf, gyf = _matmul_cotangents(g1, ctx.saved, (gx, gy), need_x, need_y)
@@ -504,7 +524,7 @@ def _qlinear_grads(ctx, g):
     if need_x:
         grad_x = gxf if gx_final else _requant_cotangent(_reduce_broadcast(gxf, x8.shape), gx, ctx.dtypes[0])
     if need_y:
-        grad_y = _requant_cotangent(_reduce_broadcast(gyf, y8.shape), gy, ctx.dtypes[1])
+        grad_y = gyf if gy_final else _requant_cotangent(_reduce_broadcast(gyf, y8.shape), gy, ctx.dtypes[1])
     return grad_x, grad_y
 
 

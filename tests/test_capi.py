@@ -517,3 +517,26 @@ def test_gemm_qa_arguments_without_gpu():
     assert lib.pratchya_gemm_bs_nt_qa(*args(ws_bytes=need - 4)) == _lib.EINVAL
     assert b"workspace" in lib.pratchya_last_error()
     assert lib.pratchya_gemm_bs_nt_qa(*args(fq=2)) == _lib.EINVAL
+
+
+def test_gemm_blockmax_and_premax_arguments_without_gpu():
+    """pratchya_gemm_bs_blockmax rejects M or N not multiples of 128 and a
+    null maxima buffer, pratchya_quantize_dequantize_premax a null buffer, an
+    other output dtype and a non-dividing grid, before any launch; empty
+    shapes are no-ops."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    f = ctypes.c_void_p(1 << 20)
+    act = (1, 1, 2048, 8)                    # (128,1)-requantized operand read transposed
+    args = lambda M, N, bm: (f, 256, f, f, *act, f, 256, f, f, *act, M, N, 256, 0, f, N, bm, None)  # noqa: E731
+    assert lib.pratchya_gemm_bs_blockmax(*args(0, 256, f)) == 0
+    assert lib.pratchya_gemm_bs_blockmax(*args(-1, 256, f)) == _lib.EINVAL
+    assert lib.pratchya_gemm_bs_blockmax(*args(200, 256, f)) == _lib.EUNSUPPORTED
+    assert b"128" in lib.pratchya_last_error()
+    assert lib.pratchya_gemm_bs_blockmax(*args(256, 320, f)) == _lib.EUNSUPPORTED
+    assert lib.pratchya_gemm_bs_blockmax(*args(256, 256, None)) == _lib.EINVAL
+    q = lambda H, W, a, b, bm, dt: (f, 1, H, W, a, b, bm, f, dt, 1, f, f, None)  # noqa: E731
+    assert lib.pratchya_quantize_dequantize_premax(*q(0, 256, 128, 128, f, _lib.DT_BF16)) == 0
+    assert lib.pratchya_quantize_dequantize_premax(*q(256, 256, 128, 128, None, _lib.DT_BF16)) == _lib.EINVAL
+    assert lib.pratchya_quantize_dequantize_premax(*q(256, 256, 128, 128, f, _lib.DT_E4M3)) == _lib.EINVAL
+    assert lib.pratchya_quantize_dequantize_premax(*q(200, 256, 128, 128, f, _lib.DT_F32)) == _lib.EINVAL

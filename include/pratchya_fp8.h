@@ -361,6 +361,27 @@ int pratchya_gemm_bs_nt_fq(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, 
                            uint8_t* c_sc8, float* c_sc32, void* workspace, int64_t workspace_bytes,
                            hipStream_t stream);
 
+/* The GEMM with the product's (1, 1) requantization in its epilogue: replaces
+ *   QArrayImpl(matmul_impl(x, y), (1, 1)).astype(dtype)
+ * (Q:605-608, then quantize_impl Q:458-506 and dequantize_impl Q:541-569), the
+ * output of a Linear whose weight grid is (a, 1): lm_head
+ * (pratchya/_nnx_impl/_model.py:77) and the LoRA projections
+ * (pratchya/_nnx_impl/_module.py:82-84), whose output grid is (x.tgrid[0],
+ * W.tgrid[1]) (Q:104-105).  With tgrid (1, 1) each element is its own block
+ * and group, so the epilogue needs no exchange between tiles.  Operands, M, K,
+ * C, ldc and c_dtype as pratchya_gemm_bs_nt; N a multiple of 16
+ * (PRATCHYA_EUNSUPPORTED otherwise).  C [M, N] receives the dequantized values
+ * in c_dtype, c_sc8 [M * N] the e8m0 bytes and c_sc32 [M * N] the group maxima
+ * (both in row order, 16-byte aligned), the arrays quantize_impl(C_f32, (1, 1))
+ * returns.  The results equal pratchya_gemm_bs_nt to f32 followed by
+ * pratchya_quantize_dequantize with tgrid (1, 1) bit for bit. */
+int pratchya_gemm_bs_nt_q11(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, const float* a_sc32,
+                            int64_t a_rdiv, int64_t a_sr, int64_t a_sk, int64_t a_kg,
+                            const uint8_t* B, int64_t ldb, const uint8_t* b_sc8, const float* b_sc32,
+                            int64_t b_rdiv, int64_t b_sr, int64_t b_sk, int64_t b_kg,
+                            int64_t M, int64_t N, int64_t K, void* C, int64_t ldc, int c_dtype,
+                            uint8_t* c_sc8, float* c_sc32, hipStream_t stream);
+
 /* The quantize prologue: replaces the quantized Linear's
  *   QArrayImpl(x, (1, 128)) @ kernel            (pratchya/_nnx_impl/_module.py:46-50)
  * i.e. quantize_impl(X, (1, 128)) (Q:458-506) followed by matmul_impl

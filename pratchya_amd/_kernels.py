@@ -996,6 +996,40 @@ def gemm_nt_fq(a: Operand, b: Operand, out_dtype: torch.dtype, fix_nan: bool = F
     return y, sc8.view(E8M0), sc32
 
 
+def gemm_nt_q11(a: Operand, b: Operand, out_dtype: torch.dtype, lead=None):
+    """``QArrayImpl(dequant(a) @ dequant(b)^T, (1, 1)).astype(out_dtype)``
+    with the requantization in the GEMM's epilogue (the output grid of a
+    weight quantized (a, 1): lm_head, LoRA): returns ``(y [M, N], sc_fp8,
+    sc_fp32)`` bit-identical to ``quantize_dequantize(gemm_nt(a, b, float32),
+    (1, 1), out_dtype)``, the scales shaped per slice of ``lead`` as there.
+    Raises ``PratchyaUnsupported`` unless N is a multiple of 16."""
+    _require_gpu(a.payload, b.payload)
+    if a.k != b.k:
+        raise ValueError(f"contraction mismatch: {a.k} vs {b.k}")
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"gemm_nt_q11: output dtype {out_dtype} is not float32 or bfloat16")
+    M, N, K = a.rows, b.rows, a.k
+    if N % 16:
+        raise PratchyaUnsupported(f"gemm_q11: N must be a multiple of 16 (got {N})")
+    lib = _lib.load()
+    ap, bp = _tile_readable(_u8(a.payload).contiguous()), _tile_readable(_u8(b.payload).contiguous())
+    as8, bs8 = _word_readable(_u8(a.sc8).contiguous()), _word_readable(_u8(b.sc8).contiguous())
+    as32, bs32 = a.sc32.contiguous().float(), b.sc32.contiguous().float()
+    lead = tuple(lead) if lead else (1,)
+    S = 1
+    for d in lead[:-1]:
+        S *= int(d)
+    H = M // S
+    y = torch.empty((M, N), dtype=out_dtype, device=ap.device)
+    sc8 = torch.empty(tuple(lead[:-1]) + (H * N, 1), dtype=torch.uint8, device=ap.device)
+    sc32 = torch.empty(tuple(lead[:-1]) + (H * N, 1, 1), dtype=torch.float32, device=ap.device)
+    _lib.check(lib.pratchya_gemm_bs_nt_q11(_ptr(ap), K, _ptr(as8), _ptr(as32), *a.desc,
+                                           _ptr(bp), K, _ptr(bs8), _ptr(bs32), *b.desc,
+                                           M, N, K, _ptr(y), N, _dtype_code(out_dtype),
+                                           _ptr(sc8), _ptr(sc32), _stream(ap)), "gemm_q11")
+    return y, sc8.view(E8M0), sc32
+
+
 def gemm_nt_qa(x: torch.Tensor, b: Operand, out_dtype: torch.dtype, fq: bool = False, lead=None,
                status: torch.Tensor = None):
     """``quantize_impl(x, (1, 128))`` of a bf16 activation ``x`` [..., K] and

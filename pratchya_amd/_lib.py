@@ -78,6 +78,9 @@ SIGNATURES = {
                                         _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_int, _c_int, _c_p, _c_p,
                                         _c_p, _c_i64, _c_p]),
     "pratchya_gemm_bs_nt_fq_workspace_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "pratchya_gemm_bs_nt_q11": (_c_int, [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
+                                         _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
+                                         _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_int, _c_p, _c_p, _c_p]),
     "pratchya_gemm_bs_blockmax": (_c_int, [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
                                            _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
                                            _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_i64, _c_p, _c_p]),

@@ -998,6 +998,116 @@ __device__ __forceinline__ void store_block_max(uint32_t lmax, uint32_t* slot, c
   }
 }
 
+// Output requantization with tgrid (1, 1) in the epilogue (FQ 6,
+// pratchya_gemm_bs_nt_q11): every element is its own block and group, so no
+// workgroup needs another's maxima.  Per element c (the value store_tile
+// would write): fake_quant11's dequantized value in the output dtype, its
+// e8m0 byte and its group max |c| (the arrays quantize_impl(C, (1, 1))
+// returns, both [M, N] in row order, row stride N).  The f32 tile is staged
+// through the wave's LDS slice 16 rows at a time, as store_tile stages an f32
+// output; then every lane takes 16 consecutive values of a staged row and
+// writes their 16 e8m0 bytes, 64 bytes of maxima and the values as whole
+// 16-byte chunks (non-temporal).  N is a multiple of 16, so such a segment
+// is inside or outside the output as a whole.
+template <bool OUT_BF16, int BG>
+__device__ __forceinline__ void store_tile_q11(const v16f (&acc)[2][4], const float (&gA)[2],
+                                               const float (&gB)[4][BG == 1 ? 4 : 1], const uint8_t* ub,
+                                               uint8_t* stage, int wave, int lane, void* C, int64_t ldc,
+                                               uint8_t* sc8, float* sc32, int row0, int col0, int M, int N) {
+  const int l32 = lane & 31, lhi = lane >> 5;
+  constexpr int RP = 16;                    // rows staged per pass
+  constexpr int PITCH = 512 + 16;           // padded LDS pitch of a row of 128 f32
+  static_assert(8 * RP * PITCH <= STAGE_BYTES, "staging must fit one stage buffer");
+  constexpr int ESZ = OUT_BF16 ? 2 : 4;
+  uint8_t* stg = stage + wave * (RP * PITCH);
+  __syncthreads();                          // every wave is done with the stage buffer
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      if ((l32 >> 4) == p) {                // lanes whose row is staged in this pass
+        uint8_t* srow = stg + (l32 % RP) * PITCH;
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            float f0, f1, f2, f3;
+            if constexpr (BG == 2) {
+              const v4f u = *reinterpret_cast<const v4f*>(ub + (ni * 32 + j * 4) * 4);
+              const float fa = gA[mi] * 6.103515625e-05f;
+              f0 = fa * u.x;
+              f1 = fa * u.y;
+              f2 = fa * u.z;
+              f3 = fa * u.w;
+            } else {
+              f0 = f1 = f2 = f3 = gA[mi] * gB[ni][BG == 1 ? j : 0] * 6.103515625e-05f;
+            }
+            *reinterpret_cast<float4*>(srow + (ni * 32 + 8 * j + 4 * lhi) * 4) =
+                make_float4(acc[mi][ni][4 * j] * f0, acc[mi][ni][4 * j + 1] * f1, acc[mi][ni][4 * j + 2] * f2,
+                            acc[mi][ni][4 * j + 3] * f3);
+          }
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's staging writes are done
+      const int rbase = row0 + mi * 32 + p * RP;
+#pragma unroll 1
+      for (int it = 0; it < 2; ++it) {
+        const int q = it * 64 + lane;       // 16 rows x 8 segments of 16 values
+        const int r = q >> 3, s = q & 7;
+        const uint8_t* src = stg + r * PITCH + s * 64;
+        float v[16];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const v4f x = *reinterpret_cast<const v4f*>(src + k * 16);
+          v[4 * k] = x.x;
+          v[4 * k + 1] = x.y;
+          v[4 * k + 2] = x.z;
+          v[4 * k + 3] = x.w;
+        }
+        v4i g[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          g[k] = v4i{(int)abs_bits(v[4 * k]), (int)abs_bits(v[4 * k + 1]), (int)abs_bits(v[4 * k + 2]),
+                     (int)abs_bits(v[4 * k + 3])};
+        uint32_t ew[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          uint32_t e0, e1, e2, e3;
+          v[4 * k] = fake_quant11(v[4 * k], e0);
+          v[4 * k + 1] = fake_quant11(v[4 * k + 1], e1);
+          v[4 * k + 2] = fake_quant11(v[4 * k + 2], e2);
+          v[4 * k + 3] = fake_quant11(v[4 * k + 3], e3);
+          ew[k] = e0 | (e1 << 8) | (e2 << 16) | (e3 << 24);
+        }
+        const int row = rbase + r, col = col0 + s * 16;
+        if (row < M && col < N) {
+          const int64_t o = (int64_t)row * N + col;
+          v4i* gd = reinterpret_cast<v4i*>(sc32 + o);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) __builtin_nontemporal_store(g[k], gd + k);
+          __builtin_nontemporal_store(v4i{(int)ew[0], (int)ew[1], (int)ew[2], (int)ew[3]},
+                                      reinterpret_cast<v4i*>(sc8 + o));
+          uint8_t* cd = static_cast<uint8_t*>(C) + ((int64_t)row * ldc + col) * ESZ;
+          if constexpr (OUT_BF16) {
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+              __builtin_nontemporal_store(
+                  v4i{(int)pack_bf16x2(v[8 * k], v[8 * k + 1]), (int)pack_bf16x2(v[8 * k + 2], v[8 * k + 3]),
+                      (int)pack_bf16x2(v[8 * k + 4], v[8 * k + 5]), (int)pack_bf16x2(v[8 * k + 6], v[8 * k + 7])},
+                  reinterpret_cast<v4i*>(cd) + k);
+          } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+              __builtin_nontemporal_store(v4i{(int)f2u(v[4 * k]), (int)f2u(v[4 * k + 1]), (int)f2u(v[4 * k + 2]),
+                                              (int)f2u(v[4 * k + 3])},
+                                          reinterpret_cast<v4i*>(cd) + k);
+          }
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);   // staging reads done before the next pass overwrites
+    }
+  }
+}
+
 // Epilogue of the Gram product (bf16 output): the tile as store_tile writes
 // it and, for a tile off the diagonal (mirror), its transpose at the mirrored
 // position: from each pass's 32 staged rows, a lane takes a column pair and
@@ -1192,7 +1302,21 @@ __device__ __forceinline__ void store_tile_fq(const v16f (&acc)[2][4], uint8_t* 
         const v4f sc = *reinterpret_cast<const v4f*>(table + rw * 16);
         const uint32_t flags = f2u(sc.w);
         float x0 = x.x, x1 = x.y, x2 = x.z, x3 = x.w;
-        fake_quant4(x0, x1, x2, x3, sc.x, sc.y, (flags & 1u) != 0u, sc.z, (flags & 2u) != 0u);
+        if (__all((flags & 3u) == 3u)) {
+          // every row of the wave finite and dequantized with one multiply
+          // (the common case): fake_quant4's arithmetic without its per-lane
+          // selections of those two paths
+          const float t0 = x0 * sc.x, t1 = x1 * sc.x, t2 = x2 * sc.x, t3 = x3 * sc.x;
+          uint32_t w = cvt4_hw(t0, t1, t2, t3);
+          if (mid_key4(t0, t1, t2, t3) <= kMidKey) w = cvt4_exact(x0, x1, x2, x3, sc.y);
+          fp8_word(w, x0, x1, x2, x3);
+          x0 *= sc.z;
+          x1 *= sc.z;
+          x2 *= sc.z;
+          x3 *= sc.z;
+        } else {
+          fake_quant4(x0, x1, x2, x3, sc.x, sc.y, (flags & 1u) != 0u, sc.z, (flags & 2u) != 0u);
+        }
         if (row0 + rw < M) {
           uint8_t* dst = Cw + (uint32_t)((rw * (int)ldc + l32 * 4) * OSZ);
           if constexpr (OUT_BF16) {
@@ -1663,6 +1787,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_bs_nt(
                                                       m0 + wm * 64, n0 + wn * 128, M, N);
       store_block_max(lm, reinterpret_cast<uint32_t*>(lds + LDS_BYTES), fq, wave, lane, m0 + wm * 64, n0 + wn * 128,
                       M, N);
+    } else if constexpr (FQ == 6) {
+      static_assert(!BF, "the (1, 1) requantization of an FP8 product");
+      store_tile_q11<OUT_BF16, BG>(acc, gA, gB, lds + OFF_UB + (wn * 128 + lhi * 16) * 4,
+                                   lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc, fq.sc8, fq.sc32,
+                                   m0 + wm * 64, n0 + wn * 128, M, N);
     } else {
       store_tile<OUT_BF16, BG>(acc, gA, gB, lds + OFF_UB + (wn * 128 + lhi * 16) * 4, lds + ((nk - 1 + par) & 1) * STAGE_BYTES, wave, lane, C, ldc,
                                    m0 + wm * 64, n0 + wn * 128, M, N);
@@ -1916,6 +2045,40 @@ extern "C" int pratchya_gemm_bs_nt(const uint8_t* A, int64_t lda, const uint8_t*
     else gemm_launch<false, 2, 0>(P, A, lda, B, ldb, C, ldc, M, N, K, none, stream);
   }
   return launch_status("gemm");
+}
+
+extern "C" int pratchya_gemm_bs_nt_q11(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, const float* a_sc32,
+                                       int64_t a_rdiv, int64_t a_sr, int64_t a_sk, int64_t a_kg, const uint8_t* B,
+                                       int64_t ldb, const uint8_t* b_sc8, const float* b_sc32, int64_t b_rdiv,
+                                       int64_t b_sr, int64_t b_sk, int64_t b_kg, int64_t M, int64_t N, int64_t K,
+                                       void* C, int64_t ldc, int c_dtype, uint8_t* c_sc8, float* c_sc32,
+                                       hipStream_t stream) {
+  if (M <= 0 || N <= 0 || K <= 0) {
+    if (M < 0 || N < 0 || K < 0) return pratchya_set_error(PRATCHYA_EINVAL, "gemm_q11: negative size");
+    return PRATCHYA_OK;
+  }
+  if (N % 16)
+    return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "gemm_q11: N must be a multiple of 16 (got %lld)",
+                              (long long)N);
+  if (!c_sc8 || !c_sc32 || (reinterpret_cast<uintptr_t>(c_sc8) & 15) || (reinterpret_cast<uintptr_t>(c_sc32) & 15))
+    return pratchya_set_error(PRATCHYA_EINVAL, "gemm_q11: the scale arrays must be 16-byte aligned device memory");
+  GemmPlan P;
+  int rc = gemm_plan("gemm_q11", A, lda, a_sc8, a_sc32, a_rdiv, a_sr, a_sk, a_kg, B, ldb, b_sc8, b_sc32, b_rdiv,
+                     b_sr, b_sk, b_kg, M, N, K, C, ldc, c_dtype, &P);
+  if (rc) return rc;
+  FqArgs fq{};
+  fq.sc8 = c_sc8;
+  fq.sc32 = c_sc32;
+  if (c_dtype == PRATCHYA_DT_BF16) {
+    if (P.bg == 0) gemm_launch<true, 0, 6>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+    else if (P.bg == 1) gemm_launch<true, 1, 6>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+    else gemm_launch<true, 2, 6>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+  } else {
+    if (P.bg == 0) gemm_launch<false, 0, 6>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+    else if (P.bg == 1) gemm_launch<false, 1, 6>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+    else gemm_launch<false, 2, 6>(P, A, lda, B, ldb, C, ldc, M, N, K, fq, stream);
+  }
+  return launch_status("gemm_q11");
 }
 
 extern "C" int pratchya_gemm_bs_kmajor(const uint8_t* A, int64_t lda, const uint8_t* a_sc8, const float* a_sc32,

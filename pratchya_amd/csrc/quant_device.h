@@ -280,6 +280,32 @@ __device__ __forceinline__ void fake_quant4(float& x0, float& x1, float& x2, flo
   }
 }
 
+// Fake quantization of one value with tgrid (1, 1), quantize_impl then
+// dequantize_impl (Q:484-499, Q:562-564): the value is its own block and
+// group, so G = |c|, r = |c| / G = 1 and e = 127 for a finite nonzero c (0
+// for a zero, 255 for NaN / inf: r is NaN).  Where 1e-7 <= |c| < 2^121, S =
+// |c|, c / S * 128 = +-128 exactly (payload +-128) and (128 |c|) / 128 = c;
+// a zero stays itself (payload +-0, dequant scale 0).  Elsewhere the
+// composition's closed forms: NaN / inf (r NaN, so e = 255 and S is NaN or
+// inf): the payload and the value are NaN; 2^121 <= |c| < inf: the payload is
+// +-128 and 128 |c| overflows, so +-inf; 0 < |c| < 1e-7: S = 1e-7, the payload
+// e4m3fn(bf16(c / S * 128)) (IEEE division; the hardware conversions are exact
+// for these finite values), dequantized as (f32(q) * |c|) / 128.  Returns the
+// dequantized f32 value; e: the e8m0 byte.
+__device__ __forceinline__ float fake_quant11(float c, uint32_t& e) {
+  constexpr uint32_t kClampBits = __builtin_bit_cast(uint32_t, kClamp);
+  const uint32_t a = abs_bits(c);
+  e = a == 0u ? 0u : 127u;
+  if (a - kClampBits < 0x7C000000u - kClampBits || a == 0u) return c;
+  if (a >= 0x7F800000u) {
+    e = 255u;
+    return __builtin_nanf("");
+  }
+  if (a >= 0x7C000000u) return u2f((f2u(c) & 0x80000000u) | 0x7F800000u);
+  const uint32_t w = cvt4_hw((c / kClamp) * 128.0f, 0.0f, 0.0f, 0.0f);
+  return (fp8_elem<0>(w) * u2f(a)) * 0.0078125f;
+}
+
 // (f32(q) * dq) / 128 equals f32(q) * (dq / 128) for every e4m3fn q when
 // 2^-110 <= dq < 2^118: dq / 128 is exact, no product of a nonzero q
 // (2^-9 <= |q| <= 448) is subnormal or overflows in either order, and scaling

@@ -444,25 +444,31 @@ class _Matmul(torch.autograd.Function):
 
 
 def _linear_forward_fused(x8, xs8, xs32, y8, ys8, ys32, gx, gy, go, dtype):
-    """``QArrayImpl(matmul_impl(x, y), (1, 128)).astype(dtype)`` with the
+    """``QArrayImpl(matmul_impl(x, y), go).astype(dtype)`` with the
     requantization in the GEMM's epilogue: ``(y, sc_fp8, sc_fp32)`` bit-identical
     to the f32 product followed by ``quantize_dequantize``, or None when the
-    layouts do not fit (grid other than (1, 128), N not a multiple of 1024,
-    operands the GEMM does not tile)."""
-    if tuple(go) != (1, 128) or dtype not in (torch.float32, torch.bfloat16) or y8.dim() != 2:
+    layouts do not fit.  ``go`` (1, 128), a quantized Linear's output, takes
+    N a multiple of 1024 (its groups span four output tiles); (1, 1), the
+    output of a weight quantized (a, 1) (lm_head, LoRA), N a multiple of 16."""
+    go = tuple(go)
+    if go not in ((1, 128), (1, 1)) or dtype not in (torch.float32, torch.bfloat16) or y8.dim() != 2:
         return None
     N = int(y8.shape[1])
-    if N % 1024:
+    if N % (1024 if go == (1, 128) else 16):
         return None
     op_a = _lhs_operand(x8, xs8, xs32, gx)
     op_b = _rhs_operand(y8, ys8, ys32, gy) if op_a is not None else None
     if op_a is None or op_b is None:
         return None
+    lead = tuple(x8.shape[:-1])
     try:
-        res, s8, s32 = K.gemm_nt_fq(op_a, op_b, dtype, lead=tuple(x8.shape[:-1]))
+        if go == (1, 1):
+            res, s8, s32 = K.gemm_nt_q11(op_a, op_b, dtype, lead=lead)
+        else:
+            res, s8, s32 = K.gemm_nt_fq(op_a, op_b, dtype, lead=lead)
     except K.PratchyaUnsupported:
         return None
-    return res.reshape(tuple(x8.shape[:-1]) + (N,)), s8, s32
+    return res.reshape(lead + (N,)), s8, s32
 
 
 class _QLinear(torch.autograd.Function):
@@ -1154,8 +1160,12 @@ class _LazyProduct(QArrayImpl):
             if sx is not None or sy is not None:
                 res = _QLinear.apply(sx, sy, x8, xs8, xs32, y8, ys8, ys32, gx, gy, go, dtype)
             else:
-                out = _matmul_forward(x8, xs8, xs32, y8, ys8, ys32, gx, gy)
-                res = K.quantize_dequantize(out, go, dtype)[0]
+                fused = _linear_forward_fused(x8, xs8, xs32, y8, ys8, ys32, gx, gy, go, dtype)
+                if fused is not None:
+                    res = fused[0]
+                else:
+                    out = _matmul_forward(x8, xs8, xs32, y8, ys8, ys32, gx, gy)
+                    res = K.quantize_dequantize(out, go, dtype)[0]
         self._dequantized[dtype] = (res, res._version)   # recomputed if changed in place
         return res
 

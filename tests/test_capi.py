@@ -519,6 +519,29 @@ def test_gemm_qa_arguments_without_gpu():
     assert lib.pratchya_gemm_bs_nt_qa(*args(fq=2)) == _lib.EINVAL
 
 
+def test_gemm_q11_arguments_without_gpu():
+    """pratchya_gemm_bs_nt_q11: the checks that return before any launch --
+    empty and negative sizes, N not a multiple of 16, null or misaligned
+    scale arrays."""
+    from pratchya_amd import _lib
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)          # aligned, never dereferenced
+    wgt = (1, 1, 1024, 8)                    # (128,1) weight used transposed
+
+    def args(M=512, N=1024, K=1024, sc8=fake, sc32=fake):
+        return (fake, K, fake, fake, 1, 8, 1, 8, fake, K, fake, fake, *wgt, M, N, K, fake, N, _lib.DT_BF16,
+                sc8, sc32, None)
+
+    assert lib.pratchya_gemm_bs_nt_q11(*args(M=0)) == 0
+    assert lib.pratchya_gemm_bs_nt_q11(*args(N=0)) == 0
+    assert lib.pratchya_gemm_bs_nt_q11(*args(M=-1)) == _lib.EINVAL
+    assert lib.pratchya_gemm_bs_nt_q11(*args(N=1000)) == _lib.EUNSUPPORTED
+    assert b"multiple of 16" in lib.pratchya_last_error()
+    assert lib.pratchya_gemm_bs_nt_q11(*args(sc8=None)) == _lib.EINVAL
+    assert lib.pratchya_gemm_bs_nt_q11(*args(sc32=ctypes.c_void_p((1 << 20) + 4))) == _lib.EINVAL
+    assert b"16-byte" in lib.pratchya_last_error()
+
+
 def test_gemm_blockmax_and_premax_arguments_without_gpu():
     """pratchya_gemm_bs_blockmax rejects M or N not multiples of 128 and a
     null maxima buffer, pratchya_quantize_dequantize_premax a null buffer, an

@@ -173,7 +173,7 @@ def test_linear_preset_block_sizes(Q, mode, blk, monkeypatch):
     f32 product over bf16 pieces in either mode (asserted: no FP8 GEMM)."""
     Q.set_matmul_backward(mode)
     calls = []
-    for name in ("gemm_nt", "gemm_nt_fq"):
+    for name in ("gemm_nt", "gemm_nt_fq", "gemm_nt_q11"):
         real = getattr(Q.K, name)
         monkeypatch.setattr(Q.K, name, (lambda r: (lambda *a, **k: calls.append(1) or r(*a, **k)))(real))
     xb, wb, gb = _linear_case(seed=11, M=256, Kd=512, N=384)
@@ -238,15 +238,18 @@ def test_odd_grid_linears(Q, mode, case, monkeypatch):
     Q.set_matmul_backward(mode)
     Kd, N, M = ODD_LINEARS[case]
     calls = []
-    real = Q.K.gemm_nt
-    monkeypatch.setattr(Q.K, "gemm_nt", lambda *a, **k: calls.append(1) or real(*a, **k))
+    real, real11 = Q.K.gemm_nt, Q.K.gemm_nt_q11
+    monkeypatch.setattr(Q.K, "gemm_nt", lambda *a, **k: calls.append("nt") or real(*a, **k))
+    monkeypatch.setattr(Q.K, "gemm_nt_q11", lambda *a, **k: calls.append("q11") or real11(*a, **k))
     xb, wb, gb = _linear_case(seed=31, M=M, Kd=Kd, N=N)
     x = to_dev_bf16(xb).requires_grad_(True)
     w = to_dev_bf16(wb).requires_grad_(True)
     out = Q.QArrayImpl(x, (1, 128)) @ Q.QArrayImpl(w, (128, 1))
     assert out.tgrid == (1, 1)
     y = out.astype(torch.bfloat16)
-    assert len(calls) == 1                   # the forward ran on the FP8 kernel
+    # the forward ran on the FP8 kernel, with the (1, 1) requantization in its
+    # epilogue (every width here is a multiple of 16)
+    assert calls == ["q11"], calls
     y.backward(to_dev_bf16(gb))
     _, o8, o32 = triple(out)
     xq, wq = oq(O.bf16_bits_to_f32(xb), (1, 128)), oq(O.bf16_bits_to_f32(wb), (128, 1))

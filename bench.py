@@ -413,6 +413,39 @@ def bench_gemm_ffn():
             "hipblaslt_fp8_no_block_scales": bench_library_fp8(10, (M, Kd, N))}, sample
 
 
+def bench_lm_head():
+    """The (1, 1) output requantization of an lm_head-shaped product
+    (pratchya/_nnx_impl/_model.py:77: Linear(hidden, vocab, (blksize, 1)),
+    output grid (1, 1)): A = quantize(x, (1,128)) [16384, 2048] x W =
+    quantize(N(0, 0.02) [2048, 32768], (128, 1)), output bf16 plus its e8m0
+    bytes and group maxima (7 bytes per element).  Fused: the requantization
+    in the GEMM's epilogue (pratchya_gemm_bs_nt_q11); separate: the f32
+    product, then the one-pass fake quantization at (1, 1).  Median of
+    GEMM_REPLAYS replays of 10 launches each."""
+    import torch
+    from pratchya_amd import _kernels as K
+    M, Kd, N = 16384, 2048, 32768
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    x = torch.randn((M, Kd), generator=gen, device="cuda").to(torch.bfloat16)
+    w = (torch.randn((Kd, N), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+    a = K.operand_rows(*K.quantize(x, (1, 128)), (1, 128))
+    b = K.operand_transposed(*K.quantize(w, (128, 1)), (128, 1))
+    del x, w
+    fused_ms, _ = timed_graph(lambda i: K.gemm_nt_q11(a, b, torch.bfloat16), 10, 2, GEMM_REPLAYS)
+    c32 = torch.empty((M, N), dtype=torch.float32, device="cuda")
+
+    def separate(i):
+        K.gemm_nt(a, b, torch.float32, out=c32)
+        K.quantize_dequantize(c32, (1, 1), torch.bfloat16)
+
+    sep_ms, _ = timed_graph(separate, 10, 2, GEMM_REPLAYS)
+    flop = 2 * M * N * Kd
+    return {"fused_us": round(fused_ms * 1e3, 1), "separate_us": round(sep_ms * 1e3, 1),
+            "fused_TFLOP/s": round(flop / (fused_ms * 1e-3) / 1e12, 1),
+            "output_bytes": 7 * M * N, "shape": f"[{M},{Kd}] x [{Kd},{N}] (128,1) -> (1,1) bf16",
+            "launches": f"median of {GEMM_REPLAYS} x 10"}
+
+
 def bench_mfma_ceiling():
     """The MFMA pipes' sustained rate on the GEMMs' own operand bytes with no
     memory traffic (``pratchya_mfma_ceiling``: the GEMM kernel's MFMA sequence
@@ -994,7 +1027,7 @@ def main():
     ap.add_argument("--counter-workload", action="store_true",
                     help="only run the direct-launch workload used for rocprofv3 --pmc runs")
     ap.add_argument("--only", choices=["cfg3", "ffn", "cfg4", "cfg5", "cfg5qa", "optim", "elementwise",
-                                       "embedding", "ceiling"],
+                                       "embedding", "ceiling", "lmhead"],
                     default=None,
                     help="run one secondary configuration alone (for profiling) and print its result")
     args = ap.parse_args()
@@ -1027,6 +1060,8 @@ def main():
             res = bench_embedding(max(20, args.steps // 4), max(4, args.warmup // 4))
         elif args.only == "ceiling":
             res = bench_mfma_ceiling()
+        elif args.only == "lmhead":
+            res = bench_lm_head()
         elif args.only == "cfg5qa":
             res = bench_config5(prologue=True)
         else:
@@ -1075,6 +1110,10 @@ def main():
         _log("d=4096 FFN gemm fwd: start")
         extra["ffn_d4096_gemm_fwd"], ffn_sample = bench_gemm_ffn()
         _log(f"d=4096 FFN gemm fwd: {extra['ffn_d4096_gemm_fwd']['TFLOP/s']} TFLOP/s")
+        _log("lm_head (1,1) output: start")
+        extra["lm_head_out_requant"] = bench_lm_head()
+        _log(f"lm_head (1,1) output: fused {extra['lm_head_out_requant']['fused_us']} us, "
+             f"separate {extra['lm_head_out_requant']['separate_us']} us")
         _log("config 4: start")
         extra["config4_backward"], cfg4_inputs = bench_config4()
         _log("config 5: start")

@@ -1005,10 +1005,13 @@ __device__ __forceinline__ void store_block_max(uint32_t lmax, uint32_t* slot, c
 // e8m0 byte and its group max |c| (the arrays quantize_impl(C, (1, 1))
 // returns, both [M, N] in row order, row stride N).  The f32 tile is staged
 // through the wave's LDS slice 16 rows at a time, as store_tile stages an f32
-// output; then every lane takes 16 consecutive values of a staged row and
-// writes their 16 e8m0 bytes, 64 bytes of maxima and the values as whole
-// 16-byte chunks (non-temporal).  N is a multiple of 16, so such a segment
-// is inside or outside the output as a whole.
+// output; the maxima are written from there; each lane then reads 2 x 16
+// consecutive values of the staged rows, casts them, and writes the values
+// and e8m0 bytes back into the slice in row layout (the f32 values in place,
+// the bytes in a pass of their own); every array leaves the slice as whole
+// 16-byte chunks, consecutive lanes on consecutive chunks of a row, so that
+// each store instruction writes whole lines (non-temporal).  N is a multiple
+// of 16, so no chunk straddles the edge of a partial tile.
 template <bool OUT_BF16, int BG>
 __device__ __forceinline__ void store_tile_q11(const v16f (&acc)[2][4], const float (&gA)[2],
                                                const float (&gB)[4][BG == 1 ? 4 : 1], const uint8_t* ub,
@@ -1019,7 +1022,22 @@ __device__ __forceinline__ void store_tile_q11(const v16f (&acc)[2][4], const fl
   constexpr int PITCH = 512 + 16;           // padded LDS pitch of a row of 128 f32
   static_assert(8 * RP * PITCH <= STAGE_BYTES, "staging must fit one stage buffer");
   constexpr int ESZ = OUT_BF16 ? 2 : 4;
+  constexpr int E8_AT = OUT_BF16 ? 256 : 0; // byte of a staged row where its e8m0 bytes go
   uint8_t* stg = stage + wave * (RP * PITCH);
+  // the staged rows to dst + row * ld (rowb bytes of a row at byte `at`,
+  // colw output columns per chunk), output rows rbase + [0, 16)
+  auto copy_out = [&](uint8_t* dst, int64_t ld, int at, int rowb, int colw, int rbase, bool absval) {
+    const int chunks = rowb / 16;
+#pragma unroll 1
+    for (int q = lane; q < RP * chunks; q += 64) {
+      const int r = q / chunks, c = q % chunks;
+      v4i v = *reinterpret_cast<const v4i*>(stg + r * PITCH + at + c * 16);
+      if (absval) v &= 0x7FFFFFFF;
+      if (rbase + r < M && col0 + c * colw < N)
+        __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(dst + (int64_t)(rbase + r) * ld + c * 16));
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);     // staging reads done before the slice is written again
+  };
   __syncthreads();                          // every wave is done with the stage buffer
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi) {
@@ -1049,26 +1067,28 @@ __device__ __forceinline__ void store_tile_q11(const v16f (&acc)[2][4], const fl
       }
       __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's staging writes are done
       const int rbase = row0 + mi * 32 + p * RP;
+      // group maxima |c|
+      copy_out(reinterpret_cast<uint8_t*>(sc32 + col0), (int64_t)N * 4, 0, 512, 4, rbase, true);
+      // the lane's segments: values 16 s + [0, 16) of staged row r, for
+      // q = lane + 64 h (r = q / 8, s = q % 8): half h reads rows 8 h + [0, 8)
+      // and writes its results back into the same rows once every lane's
+      // reads of them are done
+      uint32_t ew[2][4];
 #pragma unroll 1
-      for (int it = 0; it < 2; ++it) {
-        const int q = it * 64 + lane;       // 16 rows x 8 segments of 16 values
-        const int r = q >> 3, s = q & 7;
-        const uint8_t* src = stg + r * PITCH + s * 64;
+      for (int h = 0; h < 2; ++h) {
+        uint8_t* row = stg + ((h * 64 + lane) >> 3) * PITCH;
+        const int s = lane & 7;
         float v[16];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          const v4f x = *reinterpret_cast<const v4f*>(src + k * 16);
-          v[4 * k] = x.x;
-          v[4 * k + 1] = x.y;
-          v[4 * k + 2] = x.z;
-          v[4 * k + 3] = x.w;
+          const v4f xx = *reinterpret_cast<const v4f*>(row + s * 64 + k * 16);
+          v[4 * k] = xx.x;
+          v[4 * k + 1] = xx.y;
+          v[4 * k + 2] = xx.z;
+          v[4 * k + 3] = xx.w;
         }
-        v4i g[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          g[k] = v4i{(int)abs_bits(v[4 * k]), (int)abs_bits(v[4 * k + 1]), (int)abs_bits(v[4 * k + 2]),
-                     (int)abs_bits(v[4 * k + 3])};
-        uint32_t ew[4];
+        __builtin_amdgcn_s_waitcnt(0xC07F); // every lane's reads of these rows are done
+        uint32_t e[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           uint32_t e0, e1, e2, e3;
@@ -1076,34 +1096,38 @@ __device__ __forceinline__ void store_tile_q11(const v16f (&acc)[2][4], const fl
           v[4 * k + 1] = fake_quant11(v[4 * k + 1], e1);
           v[4 * k + 2] = fake_quant11(v[4 * k + 2], e2);
           v[4 * k + 3] = fake_quant11(v[4 * k + 3], e3);
-          ew[k] = e0 | (e1 << 8) | (e2 << 16) | (e3 << 24);
+          e[k] = e0 | (e1 << 8) | (e2 << 16) | (e3 << 24);
         }
-        const int row = rbase + r, col = col0 + s * 16;
-        if (row < M && col < N) {
-          const int64_t o = (int64_t)row * N + col;
-          v4i* gd = reinterpret_cast<v4i*>(sc32 + o);
+        if constexpr (OUT_BF16) {
 #pragma unroll
-          for (int k = 0; k < 4; ++k) __builtin_nontemporal_store(g[k], gd + k);
-          __builtin_nontemporal_store(v4i{(int)ew[0], (int)ew[1], (int)ew[2], (int)ew[3]},
-                                      reinterpret_cast<v4i*>(sc8 + o));
-          uint8_t* cd = static_cast<uint8_t*>(C) + ((int64_t)row * ldc + col) * ESZ;
-          if constexpr (OUT_BF16) {
+          for (int k = 0; k < 2; ++k)
+            *reinterpret_cast<v4i*>(row + s * 32 + k * 16) =
+                v4i{(int)pack_bf16x2(v[8 * k], v[8 * k + 1]), (int)pack_bf16x2(v[8 * k + 2], v[8 * k + 3]),
+                    (int)pack_bf16x2(v[8 * k + 4], v[8 * k + 5]), (int)pack_bf16x2(v[8 * k + 6], v[8 * k + 7])};
+          *reinterpret_cast<v4i*>(row + E8_AT + s * 16) = v4i{(int)e[0], (int)e[1], (int)e[2], (int)e[3]};
+        } else {
 #pragma unroll
-            for (int k = 0; k < 2; ++k)
-              __builtin_nontemporal_store(
-                  v4i{(int)pack_bf16x2(v[8 * k], v[8 * k + 1]), (int)pack_bf16x2(v[8 * k + 2], v[8 * k + 3]),
-                      (int)pack_bf16x2(v[8 * k + 4], v[8 * k + 5]), (int)pack_bf16x2(v[8 * k + 6], v[8 * k + 7])},
-                  reinterpret_cast<v4i*>(cd) + k);
-          } else {
+          for (int k = 0; k < 4; ++k)
+            *reinterpret_cast<v4f*>(row + s * 64 + k * 16) = v4f{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-              __builtin_nontemporal_store(v4i{(int)f2u(v[4 * k]), (int)f2u(v[4 * k + 1]), (int)f2u(v[4 * k + 2]),
-                                              (int)f2u(v[4 * k + 3])},
-                                          reinterpret_cast<v4i*>(cd) + k);
+          for (int k = 0; k < 4; ++k) {
+            ew[0][k] = h == 0 ? e[k] : ew[0][k];
+            ew[1][k] = h == 1 ? e[k] : ew[1][k];
           }
         }
       }
-      __builtin_amdgcn_s_waitcnt(0xC07F);   // staging reads done before the next pass overwrites
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      uint8_t* Cb = static_cast<uint8_t*>(C) + (int64_t)col0 * ESZ;
+      copy_out(Cb, ldc * ESZ, 0, 128 * ESZ, 16 / ESZ, rbase, false);
+      if constexpr (!OUT_BF16) {
+        // the f32 values filled the rows: the e8m0 bytes in a pass of their own
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          *reinterpret_cast<v4i*>(stg + ((h * 64 + lane) >> 3) * PITCH + E8_AT + (lane & 7) * 16) =
+              v4i{(int)ew[h][0], (int)ew[h][1], (int)ew[h][2], (int)ew[h][3]};
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+      }
+      copy_out(sc8 + col0, N, E8_AT, 128, 16, rbase, false);
     }
   }
 }

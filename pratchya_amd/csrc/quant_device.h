@@ -292,8 +292,8 @@ __device__ __forceinline__ void fake_quant4(float& x0, float& x1, float& x2, flo
 // e4m3fn(bf16(c / S * 128)) (IEEE division; the hardware conversions are exact
 // for these finite values), dequantized as (f32(q) * |c|) / 128.  Returns the
 // dequantized f32 value; e: the e8m0 byte.
+constexpr uint32_t kClampBits = __builtin_bit_cast(uint32_t, kClamp);
 __device__ __forceinline__ float fake_quant11(float c, uint32_t& e) {
-  constexpr uint32_t kClampBits = __builtin_bit_cast(uint32_t, kClamp);
   const uint32_t a = abs_bits(c);
   e = a == 0u ? 0u : 127u;
   if (a - kClampBits < 0x7C000000u - kClampBits || a == 0u) return c;
@@ -304,6 +304,20 @@ __device__ __forceinline__ float fake_quant11(float c, uint32_t& e) {
   if (a >= 0x7C000000u) return u2f((f2u(c) & 0x80000000u) | 0x7F800000u);
   const uint32_t w = cvt4_hw((c / kClamp) * 128.0f, 0.0f, 0.0f, 0.0f);
   return (fp8_elem<0>(w) * u2f(a)) * 0.0078125f;
+}
+
+// quantize_impl with tgrid (1, 1) for one value (its own block and group, G
+// = |c|): the payload byte and the e8m0 byte.  A finite c with |c| >= 1e-7
+// quantizes to +-128 (0x70 | sign), a zero to +-0; the 1e-7 clamp, NaN and
+// inf take the exact composition.
+__device__ __forceinline__ uint32_t quant11(float c, uint32_t& e) {
+  const uint32_t a = abs_bits(c);
+  const uint32_t sign = (f2u(c) >> 24) & 0x80u;
+  e = a == 0u ? 0u : 127u;
+  if (a - kClampBits < 0x7F800000u - kClampBits) return 0x70u | sign;
+  if (a == 0u) return sign;
+  if (a >= 0x7F800000u) e = 255u;
+  return quant_elem_exact(c, quant_scale(e, u2f(a)));
 }
 
 // (f32(q) * dq) / 128 equals f32(q) * (dq / 128) for every e4m3fn q when

@@ -612,6 +612,73 @@ __device__ __forceinline__ void dq_load(const void* __restrict__ x, int64_t off,
   }
 }
 
+// tgrid (1, 1) (K = 1): every element is its own block and group, so the
+// quantization is elementwise (quant11 / fake_quant11): G = |x| into sc32,
+// the e8m0 byte into sc8 and the payload (OUT 0) or the dequantized value
+// (OUT 1: bf16, 2: f32) into out, all in element order.  A lane takes 4
+// consecutive elements per step, so each load and store instruction of a
+// wave covers one contiguous span; four steps per iteration are issued
+// unconditionally (their loads in flight together), the tail one at a time.
+// (quantize_impl_bwd's repair of NaN e8m0 bytes cannot change a (1, 1)
+// value: the byte is 255 only where the payload is NaN.)
+template <bool IS_BF16, int OUT>
+__device__ __forceinline__ void q11_load(const void* x, int64_t t, float (&v)[4]) {
+  if constexpr (IS_BF16) {
+    const u32x2_t w = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(x) + t);
+    v[0] = u2f(w.x << 16);
+    v[1] = u2f(w.x & 0xFFFF0000u);
+    v[2] = u2f(w.y << 16);
+    v[3] = u2f(w.y & 0xFFFF0000u);
+  } else {
+    const u32x4_t w = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(x) + t);
+    v[0] = u2f(w.x);
+    v[1] = u2f(w.y);
+    v[2] = u2f(w.z);
+    v[3] = u2f(w.w);
+  }
+}
+
+template <int OUT>
+__device__ __forceinline__ void q11_store(const float (&v)[4], void* out, uint8_t* sc8, float* sc32, int64_t t) {
+  store_stream16(sc32 + 4 * t, u32x4_t{abs_bits(v[0]), abs_bits(v[1]), abs_bits(v[2]), abs_bits(v[3])});
+  uint32_t e[4];
+  if constexpr (OUT == 0) {
+    uint32_t q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = quant11(v[i], e[i]);
+    store_stream4(static_cast<uint8_t*>(out) + 4 * t, q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24));
+  } else {
+    float y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i] = fake_quant11(v[i], e[i]);
+    if constexpr (OUT == 1)
+      store_stream8(static_cast<uint8_t*>(out) + 8 * t, u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])});
+    else
+      store_stream16(static_cast<float*>(out) + 4 * t, u32x4_t{f2u(y[0]), f2u(y[1]), f2u(y[2]), f2u(y[3])});
+  }
+  store_stream4(sc8 + 4 * t, e[0] | (e[1] << 8) | (e[2] << 16) | (e[3] << 24));
+}
+
+template <bool IS_BF16, int OUT>
+__global__ __launch_bounds__(256) void k_quant_11(const void* __restrict__ x, void* __restrict__ out,
+                                                  uint8_t* __restrict__ sc8, float* __restrict__ sc32,
+                                                  int64_t n4) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  for (; t + 3 * stride < n4; t += 4 * stride) {
+    float v[4][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) q11_load<IS_BF16, OUT>(x, t + u * stride, v[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) q11_store<OUT>(v[u], out, sc8, sc32, t + u * stride);
+  }
+  for (; t < n4; t += stride) {
+    float v[4];
+    q11_load<IS_BF16, OUT>(x, t, v);
+    q11_store<OUT>(v, out, sc8, sc32, t);
+  }
+}
+
 template <int IN, bool OUT_BF16, int CH, bool VEC, typename I = int64_t, bool FLAT = false>
 __global__ __launch_bounds__(256) void k_dequant(const void* __restrict__ x,
                                                  const uint8_t* __restrict__ sc8,
@@ -853,6 +920,24 @@ int launch_rowgroup(const void* x, uint8_t* q, uint8_t* sc8, float* sc32, int64_
   return check_launch("quantize(row-group)");
 }
 
+// The elementwise (1, 1) kernel where its vector accesses fit: n a multiple
+// of 4, x, out and sc32 aligned to their 4-element vectors, sc8 to 4 bytes.
+bool q11_fits(const Layout& L, bool bf16, const void* x, const void* out, int out_esz, const void* sc8,
+              const void* sc32) {
+  return L.a == 1 && L.b == 1 && L.n() % 4 == 0 && aligned(x, bf16 ? 8 : 16) && aligned(out, 4 * out_esz) &&
+         aligned(sc8, 4) && aligned(sc32, 16);
+}
+
+template <bool IS_BF16, int OUT>
+int launch_q11(const void* x, void* out, uint8_t* sc8, float* sc32, int64_t n, hipStream_t st) {
+  const int64_t n4 = n / 4;
+  int64_t blocks = (n4 + 1023) / 1024;     // four 4-element steps per lane
+  if (blocks > 4096) blocks = 4096;        // grid-stride beyond 16 workgroups per CU
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL((k_quant_11<IS_BF16, OUT>), dim3((unsigned)blocks), dim3(256), 0, st, x, out, sc8, sc32, n4);
+  return check_launch("quantize(1, 1)");
+}
+
 unsigned grid_for(int64_t n, int per_block) {
   int64_t g = (n + per_block - 1) / per_block;
   return (unsigned)(g < 1 ? 1 : g);
@@ -1022,6 +1107,9 @@ extern "C" int pratchya_quantize(const void* x, int x_dtype, int64_t slices, int
   const bool bf16 = x_dtype == PRATCHYA_DT_BF16;
   if (use_g8(L, bf16, x, x_fp8, sc_fp8))
     return launch_g8(bf16, x, x_fp8, sc_fp8, sc_fp32, n / 1024, stream);
+  if (q11_fits(L, bf16, x, x_fp8, 1, sc_fp8, sc_fp32))
+    return bf16 ? launch_q11<true, 0>(x, x_fp8, sc_fp8, sc_fp32, n, stream)
+                : launch_q11<false, 0>(x, x_fp8, sc_fp8, sc_fp32, n, stream);
   RowGroupPlan p;
   if (plan_rowgroup(L, bf16, x, x_fp8, &p))
     return bf16 ? launch_rowgroup<true>(x, x_fp8, sc_fp8, sc_fp32, n, p, stream)
@@ -1097,6 +1185,13 @@ extern "C" int pratchya_quantize_dequantize(const void* x, int x_dtype, int64_t 
   if (g8_layout(L) && aligned(x, 16) && aligned(out, 16) && aligned(sc_fp8, 8))
     return bf16 ? launch_g8_qdq<true>(x, out, obf16, fix, sc_fp8, sc_fp32, n / 1024, stream)
                 : launch_g8_qdq<false>(x, out, obf16, fix, sc_fp8, sc_fp32, n / 1024, stream);
+  if (q11_fits(L, bf16, x, out, obf16 ? 2 : 4, sc_fp8, sc_fp32)) {
+    if (bf16)
+      return obf16 ? launch_q11<true, 1>(x, out, sc_fp8, sc_fp32, n, stream)
+                   : launch_q11<true, 2>(x, out, sc_fp8, sc_fp32, n, stream);
+    return obf16 ? launch_q11<false, 1>(x, out, sc_fp8, sc_fp32, n, stream)
+                 : launch_q11<false, 2>(x, out, sc_fp8, sc_fp32, n, stream);
+  }
   const size_t need = (size_t)(L.S * L.n_blk) * sizeof(uint32_t);
   if (!workspace || workspace_bytes < need)
     return pratchya_set_error(PRATCHYA_EINVAL,

@@ -17,7 +17,7 @@ import torch
 from oracle import qarr_oracle as O
 from tests.helpers import (assert_bytes_equal, assert_f32_bits_equal, assert_payload_equal, f32,
                            to_dev_bf16, to_dev_f32, u8)
-from tests.test_gpu_quantize import edge_tensor
+from tests.test_gpu_quantize import edge_tensor, tensor_1x1
 
 pytestmark = pytest.mark.gpu
 
@@ -88,6 +88,26 @@ def test_edge_values(xdt, tgrid, out, fix_nan):
     x = edge_tensor(xdt)
     dev = to_dev_bf16(O.f32_to_bf16_bits(x)) if xdt == "bf16" else to_dev_f32(x)
     check(dev, x, tgrid, out, fix_nan, f"edge {xdt} {tgrid}->{out} fix {fix_nan}")
+
+
+@pytest.mark.parametrize("xdt", ["bf16", "f32"])
+@pytest.mark.parametrize("out", ["bfloat16", "float32"])
+@pytest.mark.parametrize("fix_nan", [False, True])
+def test_grid_1x1(xdt, out, fix_nan):
+    """tgrid (1, 1) (the output grid of lm_head and LoRA products) on its
+    elementwise kernel, and at an element count that is not a multiple of 4
+    (the general kernel), against the oracle."""
+    x = tensor_1x1()
+    if xdt == "bf16":
+        bits = O.f32_to_bf16_bits(x)
+        x = O.bf16_bits_to_f32(bits)
+        check(to_dev_bf16(bits), x, (1, 1), out, fix_nan, f"(1,1) {xdt}->{out} fix {fix_nan}")
+        odd = np.ascontiguousarray(bits[:7, :13])
+        check(to_dev_bf16(odd), O.bf16_bits_to_f32(odd), (1, 1), out, fix_nan, "(1,1) odd count")
+    else:
+        check(to_dev_f32(x), x, (1, 1), out, fix_nan, f"(1,1) {xdt}->{out} fix {fix_nan}")
+        odd = np.ascontiguousarray(x[:7, :13])
+        check(to_dev_f32(odd), odd, (1, 1), out, fix_nan, "(1,1) odd count")
 
 
 def test_matches_quantize_then_dequantize_on_device():

@@ -124,6 +124,41 @@ def test_quantize_degenerate_shapes(shape):
     run_and_compare(x, to_dev_f32(x), tgrid, f"degenerate{shape}")
 
 
+def tensor_1x1():
+    """Every case of tgrid (1, 1)'s closed forms (each element its own block
+    and group): zeros and -0, values around the 1e-7 clamp and below it,
+    subnormals, ordinary values over a wide exponent range, values around
+    2^121 (where 128 |x| overflows and the dequantized value is +-inf), the
+    largest finite values, +-inf and NaN."""
+    rng = np.random.default_rng(111)
+    x = (rng.standard_normal((64, 96)) * np.exp2(rng.integers(-40, 40, size=(64, 1)))).astype(np.float32)
+    sign = np.where(rng.random(96) < 0.5, -1.0, 1.0)
+    x[0] = 0.0
+    x[1] = -0.0
+    x[2] = rng.uniform(-2e-7, 2e-7, 96)
+    x[3] = rng.standard_normal(96) * 1e-38
+    x[4] = sign * 2.0 ** 121 * rng.uniform(0.5, 2.0, 96)
+    x[5, :5] = [3.4028235e38, -3.4028235e38, np.inf, -np.inf, np.nan]
+    c = np.float32(1e-7)
+    x[6, :4] = [c, -c, np.nextafter(c, np.float32(0)), np.nextafter(c, np.float32(1))]
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_quantize_grid_1x1_edges(dtype):
+    """tgrid (1, 1) payloads and scales on the elementwise kernel (zeros, the
+    clamp, subnormals, values near 2^121 and the largest finite, inf, NaN),
+    and at an element count that is not a multiple of 4 (the general
+    kernel)."""
+    x = tensor_1x1()
+    for arr, what in ((x, "(1,1) edges"), (np.ascontiguousarray(x[:7, :13]), "(1,1) odd count")):
+        if dtype == "bf16":
+            bits = O.f32_to_bf16_bits(arr)
+            run_and_compare(O.bf16_bits_to_f32(bits), to_dev_bf16(bits), (1, 1), f"{what} bf16")
+        else:
+            run_and_compare(arr, to_dev_f32(arr), (1, 1), f"{what} f32")
+
+
 def edge_tensor(dtype):
     """Rows exercising zeros, -0, clamps, overflow via clamp, NaN, inf and
     near-midpoint f32 quotients; (1,128) groups of 8 blocks."""

@@ -1073,7 +1073,7 @@ __device__ __forceinline__ void store_tile_q11(const v16f (&acc)[2][4], const fl
       // q = lane + 64 h (r = q / 8, s = q % 8): half h reads rows 8 h + [0, 8)
       // and writes its results back into the same rows once every lane's
       // reads of them are done
-      uint32_t ew[2][4];
+      uint32_t ew[2][4] = {};                // f32 output: the bytes kept for their own pass
 #pragma unroll 1
       for (int h = 0; h < 2; ++h) {
         uint8_t* row = stg + ((h * 64 + lane) >> 3) * PITCH;

@@ -504,20 +504,30 @@ __global__ __launch_bounds__(256) void k_blockmax(const void* __restrict__ x,
 // VEC: CH is 16 output bytes (16 payload bytes, 8 bf16 or 4 f32 values), the
 // input read with 16-byte loads and the output with one 16-byte store
 // (host-checked alignment).  I: index type (32-bit below 2^31 elements).
-template <bool IS_BF16, int CH, int OUT, bool VEC, typename I = int64_t>
+// POW2: W, a, b and K powers of two, their log2 in lg (x, y, z, w): block and
+// group indices by shifts instead of four divisions per thread.
+template <bool IS_BF16, int CH, int OUT, bool VEC, typename I = int64_t, bool POW2 = false>
 __global__ __launch_bounds__(256) void k_cast_general(const void* __restrict__ x,
                                                       void* __restrict__ outv,
                                                       const uint8_t* __restrict__ sc8,
                                                       const float* __restrict__ sc32,
                                                       int64_t n_chunks, int64_t W, int64_t a,
-                                                      int64_t b, int64_t K, int fix_nan) {
+                                                      int64_t b, int64_t K, int fix_nan, int4 lg) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n_chunks) return;
   const I off = (I)t * CH;
-  const I i = off / (I)W, c = off - i * (I)W;
-  const I blk = (i / (I)a) * ((I)W / (I)b) + c / (I)b;
+  I blk, grp;
+  if constexpr (POW2) {
+    const I i = off >> lg.x, c = off & (((I)1 << lg.x) - 1);
+    blk = ((i >> lg.y) << (lg.x - lg.z)) + (c >> lg.z);
+    grp = blk >> lg.w;
+  } else {
+    const I i = off / (I)W, c = off - i * (I)W;
+    blk = (i / (I)a) * ((I)W / (I)b) + c / (I)b;
+    grp = blk / (I)K;
+  }
   const uint32_t e = sc8[blk];
-  const float G = sc32[blk / (I)K];
+  const float G = sc32[grp];
   const float sG = e8m0_decode(e) * G;
   const float S = quant_scale(e, G);
   const bool ok = sG >= kClamp && sG <= 3.0e38f;
@@ -526,19 +536,58 @@ __global__ __launch_bounds__(256) void k_cast_general(const void* __restrict__ x
   float xv[CH];
   load_chunk<IS_BF16, CH, VEC && (CH * (IS_BF16 ? 2 : 4) >= 16)>(x, (int64_t)off, xv);
   uint32_t ov[CH];                              // output element bits
+  if constexpr (CH % 4 == 0) {
+    // 4 values at a time on the hardware conversions: the division-free cast
+    // where the block's scale is neither clamped nor huge, each 4-value word
+    // with a value near a bf16 rounding midpoint redone exactly (the
+    // arithmetic of k_quant_g8 and fake_quant4)
+    const bool one = dequant_one_mul(dq);
+    const float dqx = one ? dq * 0.0078125f : dq;
 #pragma unroll
-  for (int k = 0; k < CH; ++k) {
-    uint32_t code;
-    const float tv = xv[k] * yv;
-    if (ok && (IS_BF16 || !near_bf16_midpoint(tv)))
-      code = bf16_to_e4m3fn(f32_to_bf16_rne_nonan(tv));
-    else
-      code = quant_elem_exact(xv[k], S);
-    if constexpr (OUT == 0) {
-      ov[k] = code;
-    } else {
-      const float d = (e4m3fn_to_f32(code) * dq) * 0.0078125f;
-      ov[k] = OUT == 1 ? f32_to_bf16_rne(d) : f2u(d);
+    for (int q = 0; q < CH / 4; ++q) {
+      float x0 = xv[4 * q], x1 = xv[4 * q + 1], x2 = xv[4 * q + 2], x3 = xv[4 * q + 3];
+      if constexpr (OUT == 0) {
+        uint32_t w;
+        if (ok) {
+          const float t0 = x0 * yv, t1 = x1 * yv, t2 = x2 * yv, t3 = x3 * yv;
+          w = cvt4_hw(t0, t1, t2, t3);
+          if (mid_key4(t0, t1, t2, t3) <= kMidKey) w = cvt4_exact(x0, x1, x2, x3, S);
+        } else {
+          w = cvt4_exact(x0, x1, x2, x3, S);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ov[4 * q + i] = (w >> (8 * i)) & 0xFFu;
+      } else {
+        fake_quant4(x0, x1, x2, x3, yv, S, ok, dqx, one);
+        if constexpr (OUT == 1) {
+          const uint32_t p0 = pack_bf16x2(x0, x1), p1 = pack_bf16x2(x2, x3);
+          ov[4 * q] = p0 & 0xFFFFu;
+          ov[4 * q + 1] = p0 >> 16;
+          ov[4 * q + 2] = p1 & 0xFFFFu;
+          ov[4 * q + 3] = p1 >> 16;
+        } else {
+          ov[4 * q] = f2u(x0);
+          ov[4 * q + 1] = f2u(x1);
+          ov[4 * q + 2] = f2u(x2);
+          ov[4 * q + 3] = f2u(x3);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      uint32_t code;
+      const float tv = xv[k] * yv;
+      if (ok && (IS_BF16 || !near_bf16_midpoint(tv)))
+        code = bf16_to_e4m3fn(f32_to_bf16_rne_nonan(tv));
+      else
+        code = quant_elem_exact(xv[k], S);
+      if constexpr (OUT == 0) {
+        ov[k] = code;
+      } else {
+        const float d = (e4m3fn_to_f32(code) * dq) * 0.0078125f;
+        ov[k] = OUT == 1 ? f32_to_bf16_rne(d) : f2u(d);
+      }
     }
   }
   if constexpr (VEC) {
@@ -994,10 +1043,14 @@ int launch_general(const void* x, void* q, uint8_t* sc8, float* sc32, uint32_t* 
   const bool cvec = cch == want && aligned(x, (size_t)(cch * in_esz < 16 ? cch * in_esz : 16)) && aligned(q, 16);
   const int64_t n_cast = L.n() / cch;
   const unsigned gc = grid_for(n_cast, 256);
+  const bool pow2 = is_pow2(L.W) && is_pow2(L.a) && is_pow2(L.b) && is_pow2(L.K);
+  const int4 lg = pow2 ? make_int4(ilog2(L.W), ilog2(L.a), ilog2(L.b), ilog2(L.K)) : make_int4(0, 0, 0, 0);
 #define PRATCHYA_CAST(C, V, ...)                                                                  \
   hipLaunchKernelGGL((k_cast_general<IS_BF16, C, OUT, V, ##__VA_ARGS__>), dim3(gc), dim3(256), 0, st, x, q, sc8, \
-                     sc32, n_cast, L.W, L.a, L.b, L.K, fix_nan)
-  if (cvec && L.n() <= 0x7FFFFFFF) {
+                     sc32, n_cast, L.W, L.a, L.b, L.K, fix_nan, lg)
+  if (cvec && L.n() <= 0x7FFFFFFF && pow2) {
+    PRATCHYA_CAST((16 / (OUT == 0 ? 1 : (OUT == 1 ? 2 : 4))), true, uint32_t, true);
+  } else if (cvec && L.n() <= 0x7FFFFFFF) {
     PRATCHYA_CAST((16 / (OUT == 0 ? 1 : (OUT == 1 ? 2 : 4))), true, uint32_t);
   } else if (cvec) {
     PRATCHYA_CAST((16 / (OUT == 0 ? 1 : (OUT == 1 ? 2 : 4))), true);

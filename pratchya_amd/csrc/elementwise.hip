@@ -236,16 +236,17 @@ __global__ __launch_bounds__(256) void k_ew_rowgroup(QOperand X, QOperand Y, uin
   const bool ok = !live || (sG >= kClamp && sG <= 3.0e38f);
 
   // t = z * RN(128 / S) is within 2 ulp of RN(z / S) * 128; four elements
-  // whose t lies within 4 ulp of a bf16 rounding midpoint are recomputed with
-  // the exact division (a few per thousand waves), and a wave with a clamped
-  // or non-finite block takes the exact path throughout.
+  // whose t lies within 8 ulp of a bf16 rounding midpoint (the mid_key test,
+  // one compare of the smallest key) are recomputed with the exact division
+  // (a few per thousand waves), and a wave with a clamped or non-finite block
+  // takes the exact path throughout.
   uint32_t out[4];
   if (__all(ok)) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float t0 = z[4 * j] * yv, t1 = z[4 * j + 1] * yv, t2 = z[4 * j + 2] * yv, t3 = z[4 * j + 3] * yv;
       out[j] = cvt4<true>(t0, t1, t2, t3);
-      if (near_bf16_midpoint(t0) || near_bf16_midpoint(t1) || near_bf16_midpoint(t2) || near_bf16_midpoint(t3))
+      if (mid_key4(t0, t1, t2, t3) <= kMidKey)
         out[j] = cvt4_exact(z[4 * j], z[4 * j + 1], z[4 * j + 2], z[4 * j + 3], S);
     }
   } else {
@@ -313,11 +314,28 @@ __global__ __launch_bounds__(256) void k_ew_cast(QOperand X, QOperand Y, uint8_t
   float z[CH];
   ew_chunk<OP, CH, VEC, I>(X, Y, i, c, (I)W, z);
   uint32_t code[CH];
+  if constexpr (CH % 4 == 0) {
+    // 4 values at a time on the hardware conversions, as k_ew_rowgroup casts
 #pragma unroll
-  for (int k = 0; k < CH; ++k) {
-    const float tv = z[k] * yv;
-    code[k] = (ok && !near_bf16_midpoint(tv)) ? bf16_to_e4m3fn(f32_to_bf16_rne_nonan(tv))
-                                              : quant_elem_exact(z[k], S);
+    for (int j = 0; j < CH / 4; ++j) {
+      uint32_t w;
+      if (ok) {
+        const float t0 = z[4 * j] * yv, t1 = z[4 * j + 1] * yv, t2 = z[4 * j + 2] * yv, t3 = z[4 * j + 3] * yv;
+        w = cvt4_hw(t0, t1, t2, t3);
+        if (mid_key4(t0, t1, t2, t3) <= kMidKey) w = cvt4_exact(z[4 * j], z[4 * j + 1], z[4 * j + 2], z[4 * j + 3], S);
+      } else {
+        w = cvt4_exact(z[4 * j], z[4 * j + 1], z[4 * j + 2], z[4 * j + 3], S);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) code[4 * j + i] = (w >> (8 * i)) & 0xFFu;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const float tv = z[k] * yv;
+      code[k] = (ok && !near_bf16_midpoint(tv)) ? bf16_to_e4m3fn(f32_to_bf16_rne_nonan(tv))
+                                                : quant_elem_exact(z[k], S);
+    }
   }
   uint8_t* o = q + off;
   if constexpr (VEC) {

@@ -4,7 +4,9 @@ bytes of the same calls made eagerly.  This covers the contract that the
 entry points only enqueue work (no allocation, no host synchronisation, no
 memset nodes): the general quantizer clears its block-max workspace with a
 kernel on every replay, and the fused elementwise general path and the Gram
-product's partial-tile flags likewise."""
+product's partial-tile flags likewise; the (1, 1) requantization epilogue,
+the elementwise (1, 1) quantizer, and the weight gradient's block maxima with
+the requantization that starts from them are captured too."""
 import numpy as np
 import pytest
 import torch
@@ -51,7 +53,12 @@ def test_graph_replays_match_eager():
         q = K.dequantize(*xq, torch.float32, (1, 128))
         gr = K.gemm_bf16_gram(x)                                        # stream-K, flags cleared by a kernel
         ns = K.gemm_bf16_nt_ns(x, x, gr)                                # Newton-Schulz epilogue
-        return [*xq, *wq, c, *s, *d, *t, q, gr, ns]
+        b11 = K.operand_transposed(*K.quantize(w, (128, 1)), (128, 1))
+        o11 = K.gemm_nt_q11(a, b11, torch.bfloat16)                     # (1, 1) requantization epilogue
+        x11 = K.quantize(x, (1, 1))                                     # elementwise (1, 1) kernel
+        c32, bm = K.gemm_nt_blockmax(a, b)                              # block maxima from the epilogue
+        wg = K.quantize_dequantize_premax(c32, bm, (128, 128), torch.bfloat16)
+        return [*xq, *wq, c, *s, *d, *t, q, gr, ns, *o11, *x11, c32, bm, *wg]
 
     fill()
     torch.cuda.synchronize()

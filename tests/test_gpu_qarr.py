@@ -578,6 +578,27 @@ def test_embedding_lookup_matches_full_dequantize(Q):
     assert torch.equal(bf.view(torch.int16), want.to(torch.bfloat16).view(torch.int16))
 
 
+@pytest.mark.parametrize("V,D,grid", [(384, 4096, (128, 128)), (64, 24, (4, 4))], ids=["wide", "narrow"])
+def test_gather_dequantize_paths(V, D, grid):
+    """gather_dequantize against the whole-table dequantization indexed, f32
+    and bf16 output, for a wide table (the split kernel: whole-line loads and
+    non-temporal stores) and a table whose 4-wide blocks send the bf16 output
+    down the per-thread-chunk kernel; 1000 ids with repeats, negatives and
+    out-of-range values (clamped as jnp does)."""
+    from pratchya_amd import _kernels as K
+    tb = O.normal_input((V, D), 1.0, seed=53)
+    x8, s8, s32 = K.quantize(to_dev_bf16(tb), grid)
+    gen = torch.Generator(device="cuda").manual_seed(54)
+    ids = torch.randint(-V - 50, V + 50, (1000,), generator=gen, device="cuda")
+    full = K.dequantize(x8, s8, s32, torch.float32, grid)
+    idx = torch.where(ids < 0, ids + V, ids).clamp(0, V - 1)
+    want = full[idx]
+    got = K.gather_dequantize(x8, s8, s32, grid, ids, torch.float32)
+    assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+    gotb = K.gather_dequantize(x8, s8, s32, grid, ids, torch.bfloat16)
+    assert torch.equal(gotb.view(torch.int16), want.to(torch.bfloat16).view(torch.int16))
+
+
 def test_embedding_lookup_gradient(Q):
     """The table's gradient through the fast path equals the dequantize-then-
     index path (distinct ids: no summation-order freedom)."""

@@ -605,7 +605,7 @@ __global__ __launch_bounds__(256) void k_cast_general(const void* __restrict__ x
         w[j] = ov[j];
     }
     char* o = static_cast<char*>(outv) + (int64_t)off * (OUT == 0 ? 1 : (OUT == 1 ? 2 : 4));
-    *reinterpret_cast<uint4*>(o) = make_uint4(w[0], w[1], w[2], w[3]);
+    store_stream16(o, u32x4_t{w[0], w[1], w[2], w[3]});   // a wave's stores: one contiguous span
   } else {
 #pragma unroll
     for (int k = 0; k < CH; ++k) {

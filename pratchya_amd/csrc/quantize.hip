@@ -807,7 +807,9 @@ __global__ __launch_bounds__(256) void k_dequant(const void* __restrict__ x,
       return;
     }
   }
-  dq_chunk<IN, OUT_BF16, CH, VEC, I, FLAT, false>(x, sc8, sc32, out, t * CH, W, a, b, K, lb, lk);
+  // a cotangent input: 16 output bytes per lane, one contiguous span per
+  // wave, stored non-temporally
+  dq_chunk<IN, OUT_BF16, CH, VEC, I, FLAT, IN != 0 && VEC>(x, sc8, sc32, out, t * CH, W, a, b, K, lb, lk);
 }
 
 // --------------------------------------------------------------------------

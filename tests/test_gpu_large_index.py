@@ -1,0 +1,90 @@
+"""Arrays of 2^31 elements: the quantize / dequantize kernels' 64-bit index
+paths (quantize_impl, pratchya/_qualia/_qarr.py:458-506; dequantize_impl,
+:541-569; QArrayImpl(x).astype, :339-342).
+
+No configuration of the reference reaches 2^31 elements and the CPU oracle
+cannot run at that size, so these tests use a property that does not depend
+on the size: a [524288, 4096] array made of 128 copies of a [4096, 4096]
+slice, with grids whose blocks and groups tile each copy exactly (tgrid
+(128, 128): groups of 1024 blocks = 4096 rows; (1, 128): groups of 8 blocks
+inside a row), must quantize to 128 copies of the slice's own result, and
+dequantize to 128 copies of the slice's dequantization.  The slice runs on
+the 32-bit index paths, which the oracle tests pin; the copy runs on the
+64-bit ones (more than 0x7FFFFFFF elements).  Bitwise comparisons (NaN and
+inf included).
+"""
+import pytest
+import torch
+
+from pratchya_amd import _kernels as K
+
+pytestmark = pytest.mark.gpu
+
+REPS = 128
+ROWS = COLS = 4096
+
+
+def _slice():
+    g = torch.Generator(device="cuda").manual_seed(31)
+    x = torch.randn((ROWS, COLS), generator=g, device="cuda")
+    # per 128-row band magnitudes from 2^-20 to 2^20 (different e8m0 bytes and
+    # group maxima), an all-zero block, a NaN and an inf in groups of their own
+    band = torch.arange(ROWS, device="cuda") // 128
+    x = x * torch.exp2((band % 41).float() - 20.0)[:, None]
+    x[:128, :128] = 0.0
+    x[1024 + 5, 300] = float("nan")
+    x[2048 + 7, 4000] = float("inf")
+    return x.to(torch.bfloat16)
+
+
+def _bits(t: torch.Tensor) -> torch.Tensor:
+    return t.view(torch.uint8) if t.element_size() == 1 else t.view(torch.int16 if t.element_size() == 2 else torch.int32)
+
+
+def _assert_copies(big: torch.Tensor, small: torch.Tensor, what: str) -> None:
+    b = _bits(big.contiguous()).reshape(REPS, -1)
+    s = _bits(small.contiguous()).reshape(1, -1)
+    assert b.shape[1] == s.shape[1], what
+    for r in range(0, REPS, 16):
+        assert torch.equal(b[r:r + 16], s.expand(16, -1)), f"{what}: copies {r}..{r + 15} differ"
+
+
+@pytest.fixture(scope="module")
+def arrays():
+    xs = _slice()
+    xb = xs.repeat(REPS, 1)
+    assert xb.numel() > 0x7FFFFFFF
+    yield xs, xb
+    del xb
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("tgrid", [(128, 128), (1, 128)])
+def test_quantize_dequantize_past_2_31(arrays, tgrid):
+    xs, xb = arrays
+    qs = K.quantize(xs, tgrid)
+    # the slice's result is not degenerate: many scale exponents, a NaN group
+    assert bool(qs[0].view(torch.uint8).any())
+    assert torch.unique(qs[1].view(torch.uint8)).numel() > 20
+    assert bool(torch.isnan(qs[2]).any())
+    qb = K.quantize(xb, tgrid)
+    for name, big, small in zip(("payload", "e8m0", "group max"), qb, qs):
+        _assert_copies(big, small, f"quantize {tgrid} {name}")
+    ds = K.dequantize(*qs, torch.bfloat16, tgrid)
+    db = K.dequantize(*qb, torch.bfloat16, tgrid)
+    del qb
+    _assert_copies(db, ds, f"dequantize {tgrid}")
+    del db
+    torch.cuda.empty_cache()
+
+
+def test_fake_quantize_past_2_31(arrays):
+    """One-pass QArrayImpl(x, (128, 128)).astype(bf16) on the general cast's
+    64-bit path."""
+    xs, xb = arrays
+    ys = K.quantize_dequantize(xs, (128, 128), torch.bfloat16)
+    yb = K.quantize_dequantize(xb, (128, 128), torch.bfloat16)
+    for name, big, small in zip(("values", "e8m0", "group max"), yb, ys):
+        _assert_copies(big, small, f"quantize_dequantize {name}")
+    del yb
+    torch.cuda.empty_cache()

@@ -4,11 +4,11 @@ paths (quantize_impl, pratchya/_qualia/_qarr.py:458-506; dequantize_impl,
 
 No configuration of the reference reaches 2^31 elements and the CPU oracle
 cannot run at that size, so these tests use a property that does not depend
-on the size: a [524288, 4096] array made of 128 copies of a [4096, 4096]
+on the size: a [524288, 4096] array made of 64 copies of an [8192, 4096]
 slice, with grids whose blocks and groups tile each copy exactly (tgrid
-(128, 128): groups of 1024 blocks = 4096 rows; (1, 128): groups of 8 blocks
-inside a row), must quantize to 128 copies of the slice's own result, and
-dequantize to 128 copies of the slice's dequantization.  The slice runs on
+(128, 128): groups of 1024 blocks = 4096 rows, two per slice; (1, 128):
+groups of 8 blocks inside a row), must quantize to 64 copies of the slice's
+own result, and dequantize to 64 copies of the slice's dequantization.  The slice runs on
 the 32-bit index paths, which the oracle tests pin; the copy runs on the
 64-bit ones (more than 0x7FFFFFFF elements).  Bitwise comparisons (NaN and
 inf included).
@@ -20,20 +20,21 @@ from pratchya_amd import _kernels as K
 
 pytestmark = pytest.mark.gpu
 
-REPS = 128
-ROWS = COLS = 4096
+REPS = 64
+ROWS, COLS = 8192, 4096
 
 
 def _slice():
     g = torch.Generator(device="cuda").manual_seed(31)
     x = torch.randn((ROWS, COLS), generator=g, device="cuda")
     # per 128-row band magnitudes from 2^-20 to 2^20 (different e8m0 bytes and
-    # group maxima), an all-zero block, a NaN and an inf in groups of their own
+    # group maxima), an all-zero block; a NaN and an inf in the second 4096
+    # rows only (a (128, 128) group of their own)
     band = torch.arange(ROWS, device="cuda") // 128
     x = x * torch.exp2((band % 41).float() - 20.0)[:, None]
     x[:128, :128] = 0.0
-    x[1024 + 5, 300] = float("nan")
-    x[2048 + 7, 4000] = float("inf")
+    x[4096 + 1024 + 5, 300] = float("nan")
+    x[4096 + 2048 + 7, 4000] = float("inf")
     return x.to(torch.bfloat16)
 
 
@@ -63,10 +64,14 @@ def arrays():
 def test_quantize_dequantize_past_2_31(arrays, tgrid):
     xs, xb = arrays
     qs = K.quantize(xs, tgrid)
-    # the slice's result is not degenerate: many scale exponents, a NaN group
+    # the slice's result is not degenerate: block scales 2^(e - 127) G over
+    # many exponents, finite and NaN groups
     assert bool(qs[0].view(torch.uint8).any())
-    assert torch.unique(qs[1].view(torch.uint8)).numel() > 20
-    assert bool(torch.isnan(qs[2]).any())
+    e = qs[1].view(torch.uint8).float()
+    scale = torch.exp2(e - 127.0) * qs[2].reshape(e.shape[0], 1)
+    live = torch.isfinite(scale) & (scale > 0)
+    assert torch.unique(torch.floor(torch.log2(scale[live]))).numel() > 20
+    assert bool(torch.isnan(qs[2]).any()) and bool(torch.isfinite(qs[2]).any())
     qb = K.quantize(xb, tgrid)
     for name, big, small in zip(("payload", "e8m0", "group max"), qb, qs):
         _assert_copies(big, small, f"quantize {tgrid} {name}")

@@ -1,6 +1,7 @@
-"""Arrays of 2^31 elements: the quantize / dequantize kernels' 64-bit index
-paths (quantize_impl, pratchya/_qualia/_qarr.py:458-506; dequantize_impl,
-:541-569; QArrayImpl(x).astype, :339-342).
+"""Arrays of 2^31 elements: the kernels' 64-bit index paths (quantize_impl,
+pratchya/_qualia/_qarr.py:458-506; dequantize_impl, :541-569;
+QArrayImpl(x).astype, :339-342; indexing, :263-284; the binary operators,
+:121-261).
 
 No configuration of the reference reaches 2^31 elements and the CPU oracle
 cannot run at that size, so these tests use a property that does not depend
@@ -42,12 +43,13 @@ def _bits(t: torch.Tensor) -> torch.Tensor:
     return t.view(torch.uint8) if t.element_size() == 1 else t.view(torch.int16 if t.element_size() == 2 else torch.int32)
 
 
-def _assert_copies(big: torch.Tensor, small: torch.Tensor, what: str) -> None:
-    b = _bits(big.contiguous()).reshape(REPS, -1)
+def _assert_copies(big: torch.Tensor, small: torch.Tensor, what: str, reps: int = REPS) -> None:
+    b = _bits(big.contiguous()).reshape(reps, -1)
     s = _bits(small.contiguous()).reshape(1, -1)
     assert b.shape[1] == s.shape[1], what
-    for r in range(0, REPS, 16):
-        assert torch.equal(b[r:r + 16], s.expand(16, -1)), f"{what}: copies {r}..{r + 15} differ"
+    step = min(16, reps)
+    for r in range(0, reps, step):
+        assert torch.equal(b[r:r + step], s.expand(step, -1)), f"{what}: copies {r}..{r + step - 1} differ"
 
 
 @pytest.fixture(scope="module")
@@ -92,4 +94,50 @@ def test_fake_quantize_past_2_31(arrays):
     for name, big, small in zip(("values", "e8m0", "group max"), yb, ys):
         _assert_copies(big, small, f"quantize_dequantize {name}")
     del yb
+    torch.cuda.empty_cache()
+
+
+def _repeat_q(q):
+    """A quantized triple of one slice, as the triple of REPS stacked copies
+    (blocks and groups tile each copy, so the scale arrays stack too)."""
+    return (q[0].view(torch.uint8).repeat(REPS, 1), q[1].view(torch.uint8).repeat(REPS, 1), q[2].repeat(REPS, 1, 1))
+
+
+@pytest.mark.parametrize("op,tgrid", [("add", (1, 128)), ("mul", (128, 128))])
+def test_elementwise_past_2_31(arrays, op, tgrid):
+    """The fused binary operators on operands of 2^31 elements: the one-pass
+    kernel (result grid (1, 128)) and the general path (block maxima, group
+    scales, cast; result grid (128, 128)) on 64-bit indices."""
+    xs, _ = arrays
+    ys = (xs.float() * -0.75 + 0.5).to(torch.bfloat16)
+    gx = (1, 128)
+    qx, qy = K.quantize(xs, gx), K.quantize(ys, gx)
+    rs = K.elementwise(op, qx, gx, qy, gx, tgrid)
+    bx, by = _repeat_q(qx), _repeat_q(qy)
+    assert bx[0].numel() > 0x7FFFFFFF
+    rb = K.elementwise(op, bx, gx, by, gx, tgrid)
+    del bx, by
+    for name, big, small in zip(("payload", "e8m0", "group max"), rb, rs):
+        _assert_copies(big, small, f"{op} {tgrid} {name}")
+    del rb
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("tgrid,dtype", [((128, 128), torch.bfloat16), ((128, 128), torch.float32),
+                                         ((1, 4), torch.bfloat16)])
+def test_gather_dequantize_past_2_31(tgrid, dtype):
+    """Embedding lookups whose output passes 2^31 elements: 524288 indices
+    into a [65536, 4096] table, every row eight times (odd passes as negative
+    indices), equal eight copies of the dequantized table (the split kernel for
+    (128, 128), the per-chunk kernel for (1, 4))."""
+    g = torch.Generator(device="cuda").manual_seed(7)
+    table = (torch.randn((65536, 4096), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    q = K.quantize(table, tgrid)
+    ref = K.dequantize(*q, dtype, tgrid)
+    rows = torch.arange(65536, device="cuda")
+    idx = torch.cat([rows - 65536 if k % 2 else rows for k in range(8)])
+    out = K.gather_dequantize(*q, tgrid, idx, dtype)
+    assert out.numel() > 0x7FFFFFFF
+    _assert_copies(out, ref, f"gather {tgrid} {dtype}", reps=8)
+    del out
     torch.cuda.empty_cache()

@@ -15,6 +15,7 @@ import json
 import os
 import sys
 import time
+import traceback
 
 import numpy as np
 
@@ -1073,15 +1074,42 @@ def main():
     # same graph replay timed first and third), so the headline is timed after
     # them, with its own W warmup steps and exactly K timed steps.
     extra = {}
-    _log("config 1 round trip: start")
-    extra["config1_round_trip"] = bench_config1(max(20, args.steps // 4), max(4, args.warmup // 4))
-    _log(f"config 1 round trip: {extra['config1_round_trip']['us_per_round_trip']} us")
-    _log("embedding lookup: start")
-    extra["embedding_lookup"] = bench_embedding(max(20, args.steps // 4), max(4, args.warmup // 4))
-    _log(f"embedding lookup: {extra['embedding_lookup']['us']} us")
-    _log("elementwise add: start")
-    extra["elementwise_add"] = bench_elementwise(max(20, args.steps // 2), max(4, args.warmup // 4))
-    _log(f"elementwise add: {extra['elementwise_add']['us']} us")
+    samples = {}
+
+    def leg(key, fn, summary=None):
+        """One secondary leg, its result under extra[key].  A Python error in
+        it is printed to stderr and recorded in its place, so that the
+        headline line is still printed (a GPU fault ends the process
+        regardless)."""
+        _log(f"{key}: start")
+        try:
+            res = fn()
+        except Exception as e:  # recorded in the JSON line and on stderr
+            traceback.print_exc(file=sys.stderr)
+            extra[key] = {"error": f"{type(e).__name__}: {e}"}
+            _log(f"{key}: FAILED ({type(e).__name__})")
+            return None
+        extra[key] = res
+        if summary is not None:
+            _log(f"{key}: {summary(res)}")
+        return res
+
+    def attach(key, name, fn):
+        """A CPU baseline beside a secondary leg that ran (errors recorded as in leg)."""
+        if "error" in extra.get(key, {"error": None}):
+            return
+        try:
+            extra[key][name] = fn()
+        except Exception as e:
+            traceback.print_exc(file=sys.stderr)
+            extra[key][name] = {"error": f"{type(e).__name__}: {e}"}
+
+    leg("config1_round_trip", lambda: bench_config1(max(20, args.steps // 4), max(4, args.warmup // 4)),
+        lambda r: f"{r['us_per_round_trip']} us")
+    leg("embedding_lookup", lambda: bench_embedding(max(20, args.steps // 4), max(4, args.warmup // 4)),
+        lambda r: f"{r['us']} us")
+    leg("elementwise_add", lambda: bench_elementwise(max(20, args.steps // 2), max(4, args.warmup // 4)),
+        lambda r: f"{r['us']} us")
     _log("config 2 quantize: start")
     ms, wall, ok, ms_long = bench_quantize(args.steps, args.warmup)
     _log(f"config 2 quantize: {ms * 1e3:.2f} us/step, parity spot check {'ok' if ok else 'FAILED'}; "
@@ -1094,52 +1122,53 @@ def main():
         "note": f"the headline's kernel and inputs over {SUSTAINED_STEPS} launches in one timed region "
                 f"(the headline times --steps launches)"}
     if not args.no_gemm:
-        _log("mfma ceiling: start")
-        extra["mfma_ceiling"] = bench_mfma_ceiling()
-        _log(f"mfma ceiling: fp8 {extra['mfma_ceiling']['fp8']['TFLOP/s']} TFLOP/s, "
-             f"bf16 {extra['mfma_ceiling']['bf16']['TFLOP/s']} TFLOP/s")
-        _log("config 3 gemm fwd: start")
-        gms, tflops, cfg3_sample = bench_gemm_fwd()
-        _log(f"config 3 gemm fwd: {gms * 1e3:.1f} us, {tflops:.1f} TFLOP/s")
-        extra["config3_gemm_fwd"] = {"value": round(tflops, 1), "unit": "TFLOP/s", "ms": round(gms, 4),
-                                     "frac_of_fp8_peak": round(tflops / FP8_PEAK_TFLOPS, 4),
-                                     "shape": "[16384,2048] x [2048,8192] -> bf16",
-                                     "flop": 2 * 16384 * 2048 * 8192,
-                                     "launches": f"median of {GEMM_REPLAYS} x {GEMM_LAUNCHES}",
-                                     "hipblaslt_fp8_no_block_scales": bench_library_fp8(20)}
-        _log("d=4096 FFN gemm fwd: start")
-        extra["ffn_d4096_gemm_fwd"], ffn_sample = bench_gemm_ffn()
-        _log(f"d=4096 FFN gemm fwd: {extra['ffn_d4096_gemm_fwd']['TFLOP/s']} TFLOP/s")
-        _log("lm_head (1,1) output: start")
-        extra["lm_head_out_requant"] = bench_lm_head()
-        _log(f"lm_head (1,1) output: fused {extra['lm_head_out_requant']['fused_us']} us, "
-             f"separate {extra['lm_head_out_requant']['separate_us']} us")
-        _log("config 4: start")
-        extra["config4_backward"], cfg4_inputs = bench_config4()
-        _log("config 5: start")
-        extra["config5_layer"] = bench_config5()
-        _log(f"config 5: {extra['config5_layer']['tokens_per_s']} tokens/s")
-        qa = bench_config5(prologue=True)
-        extra["config5_layer_fused_prologue"] = {k: qa[k] for k in ("tokens_per_s", "ms_per_layer_step",
-                                                                    "frac_of_fp8_peak", "path")}
-        _log(f"config 5 with the fused quantize prologue: {qa['tokens_per_s']} tokens/s")
-        _log("optimizer step: start")
-        extra["optimizer_step"] = bench_optimizer(3)
-        _log(f"optimizer step: {extra['optimizer_step']['ms_per_step']} ms")
+        leg("mfma_ceiling", bench_mfma_ceiling,
+            lambda r: f"fp8 {r['fp8']['TFLOP/s']} TFLOP/s, bf16 {r['bf16']['TFLOP/s']} TFLOP/s")
+
+        def cfg3():
+            gms, tflops, samples["cfg3"] = bench_gemm_fwd()
+            return {"value": round(tflops, 1), "unit": "TFLOP/s", "ms": round(gms, 4),
+                    "frac_of_fp8_peak": round(tflops / FP8_PEAK_TFLOPS, 4),
+                    "shape": "[16384,2048] x [2048,8192] -> bf16",
+                    "flop": 2 * 16384 * 2048 * 8192,
+                    "launches": f"median of {GEMM_REPLAYS} x {GEMM_LAUNCHES}",
+                    "hipblaslt_fp8_no_block_scales": bench_library_fp8(20)}
+
+        leg("config3_gemm_fwd", cfg3, lambda r: f"{r['ms'] * 1e3:.1f} us, {r['value']} TFLOP/s")
+
+        def ffn():
+            res, samples["ffn"] = bench_gemm_ffn()
+            return res
+
+        leg("ffn_d4096_gemm_fwd", ffn, lambda r: f"{r['TFLOP/s']} TFLOP/s")
+        leg("lm_head_out_requant", bench_lm_head,
+            lambda r: f"fused {r['fused_us']} us, separate {r['separate_us']} us")
+
+        def cfg4():
+            res, samples["cfg4"] = bench_config4()
+            return res
+
+        leg("config4_backward", cfg4)
+        leg("config5_layer", bench_config5, lambda r: f"{r['tokens_per_s']} tokens/s")
+        leg("config5_layer_fused_prologue",
+            lambda: {k: v for k, v in bench_config5(prologue=True).items()
+                     if k in ("tokens_per_s", "ms_per_layer_step", "frac_of_fp8_peak", "path")},
+            lambda r: f"{r['tokens_per_s']} tokens/s")
+        leg("optimizer_step", lambda: bench_optimizer(3), lambda r: f"{r['ms_per_step']} ms")
     cpu = None
     if not args.no_cpu_baseline:
         _log("cpu baseline: start")
         cpu = cpu_baseline_quantize()
         _log(f"cpu baseline: {cpu['value']} GB/s")
-        extra["config1_round_trip"]["cpu_baseline"] = cpu_baseline_config1()
-        extra["elementwise_add"]["cpu_baseline"] = cpu_baseline_elementwise()
-        extra["embedding_lookup"]["cpu_baseline"] = cpu_baseline_embedding()
-        if "config3_gemm_fwd" in extra:
-            extra["config3_gemm_fwd"]["cpu_baseline"] = cpu_baseline_gemm(cfg3_sample, 16384)
-            extra["ffn_d4096_gemm_fwd"]["cpu_baseline"] = cpu_baseline_gemm(ffn_sample, CFG5_TOKENS)
-            extra["config4_backward"]["cpu_baseline"] = cpu_baseline_config4(cfg4_inputs)
-            extra["config5_layer"]["cpu_baseline"] = cpu_baseline_config5()
-            extra["optimizer_step"]["cpu_baseline"] = cpu_baseline_optimizer()
+        attach("config1_round_trip", "cpu_baseline", cpu_baseline_config1)
+        attach("elementwise_add", "cpu_baseline", cpu_baseline_elementwise)
+        attach("embedding_lookup", "cpu_baseline", cpu_baseline_embedding)
+        if not args.no_gemm:
+            attach("config3_gemm_fwd", "cpu_baseline", lambda: cpu_baseline_gemm(samples["cfg3"], 16384))
+            attach("ffn_d4096_gemm_fwd", "cpu_baseline", lambda: cpu_baseline_gemm(samples["ffn"], CFG5_TOKENS))
+            attach("config4_backward", "cpu_baseline", lambda: cpu_baseline_config4(samples["cfg4"]))
+            attach("config5_layer", "cpu_baseline", cpu_baseline_config5)
+            attach("optimizer_step", "cpu_baseline", cpu_baseline_optimizer)
         _log("cpu baselines of configs 1, 3, 4, 5, the FFN GEMM, the embedding lookup, the elementwise add and "
              "the optimizer: done")
     line = {

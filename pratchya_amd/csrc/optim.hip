@@ -127,19 +127,30 @@ __device__ __forceinline__ void load_operand(const void* __restrict__ x, float s
 
 // HW: round pairs with v_cvt_pk_bf16_f32 (k_update keeps the integer
 // rounding: the compiler's selection of the packed conversion fails on its
-// negated sums with packed f32 operations disabled).
+// negated sums with packed f32 operations disabled).  A 16-byte chunk (8 bf16
+// or 4 f32 values, consecutive lanes on consecutive chunks) is stored
+// non-temporally: measured on the FFN down-projection's [16384,4096] leaf,
+// the momentum kernel 90-97 -> 71-72 us, the update 62 -> 61 us, the
+// optimizer step unchanged.
 template <bool BF16, int CH, bool HW = false>
 __device__ __forceinline__ void store_chunk(void* out, int64_t off, const float (&v)[CH]) {
   if constexpr (BF16 && HW && CH % 2 == 0) {
     Vec<uint32_t, CH / 2> w;
 #pragma unroll
     for (int k = 0; k < CH; k += 2) w.v[k / 2] = pack_bf16x2(v[k], v[k + 1]);
-    *reinterpret_cast<Vec<uint32_t, CH / 2>*>(static_cast<uint16_t*>(out) + off) = w;
+    if constexpr (CH == 8) store_stream16(static_cast<uint16_t*>(out) + off, u32x4_t{w.v[0], w.v[1], w.v[2], w.v[3]});
+    else *reinterpret_cast<Vec<uint32_t, CH / 2>*>(static_cast<uint16_t*>(out) + off) = w;
   } else if constexpr (BF16) {
     Vec<uint16_t, CH> w;
 #pragma unroll
     for (int k = 0; k < CH; ++k) w.v[k] = (uint16_t)f32_to_bf16_rne(v[k]);
-    *reinterpret_cast<Vec<uint16_t, CH>*>(static_cast<uint16_t*>(out) + off) = w;
+    if constexpr (CH == 8)
+      store_stream16(static_cast<uint16_t*>(out) + off,
+                     u32x4_t{(uint32_t)w.v[0] | ((uint32_t)w.v[1] << 16), (uint32_t)w.v[2] | ((uint32_t)w.v[3] << 16),
+                             (uint32_t)w.v[4] | ((uint32_t)w.v[5] << 16), (uint32_t)w.v[6] | ((uint32_t)w.v[7] << 16)});
+    else *reinterpret_cast<Vec<uint16_t, CH>*>(static_cast<uint16_t*>(out) + off) = w;
+  } else if constexpr (CH == 4) {
+    store_stream16(static_cast<float*>(out) + off, u32x4_t{f2u(v[0]), f2u(v[1]), f2u(v[2]), f2u(v[3])});
   } else {
     Vec<float, CH> w;
 #pragma unroll

@@ -2699,21 +2699,27 @@ __global__ __launch_bounds__(256) void k_split_pack(const void* __restrict__ src
   }
   __syncthreads();
   (void)seg_len;
-  // write: thread t -> output row i = t >> 2, 16 columns (t & 3) * 16 .. +16 of each segment
-  const int i = t >> 2, j0 = (t & 3) * 16;
-  if (r0 + i >= out_rows) return;
-  for (int s = 0; s < nseg; ++s) {
-    const int p = (planes >> (2 * s)) & 3;
-    uint32_t w[8];
+  // write: in pass h, thread t -> output row i = 32 h + t / 8, the 8 columns
+  // (t % 8) * 8 .. +8 of each segment, one 16-byte store, so that every store
+  // instruction of a wave writes 8 whole 128-byte row pieces (16 values per
+  // thread as two 16-byte halves of a 32-byte piece wrote half of each line
+  // per instruction)
+  const int j0 = (t & 7) * 8;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const float a = bf16_piece(tile[i][j0 + 2 * q], p), b = bf16_piece(tile[i][j0 + 2 * q + 1], p);
-      w[q] = (pfp8::f2u(a) >> 16) | (pfp8::f2u(b) & 0xFFFF0000u);   // pieces are bf16 values
+  for (int h = 0; h < 2; ++h) {
+    const int i = 32 * h + (t >> 3);
+    if (r0 + i >= out_rows) break;
+    for (int s = 0; s < nseg; ++s) {
+      const int p = (planes >> (2 * s)) & 3;
+      uint32_t w[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float a = bf16_piece(tile[i][j0 + 2 * q], p), b = bf16_piece(tile[i][j0 + 2 * q + 1], p);
+        w[q] = (pfp8::f2u(a) >> 16) | (pfp8::f2u(b) & 0xFFFF0000u);   // pieces are bf16 values
+      }
+      const int64_t col = (int64_t)s * kp + k0 + j0;   // kp is a multiple of 64: whole 8-value pieces
+      *reinterpret_cast<uint4*>(dst + (r0 + i) * ldd + col) = make_uint4(w[0], w[1], w[2], w[3]);
     }
-    const int64_t col = (int64_t)s * kp + k0 + j0;     // kp is a multiple of 64: whole 16-value pieces
-    uint4* d = reinterpret_cast<uint4*>(dst + (r0 + i) * ldd + col);
-    d[0] = make_uint4(w[0], w[1], w[2], w[3]);
-    d[1] = make_uint4(w[4], w[5], w[6], w[7]);
   }
 }
 }  // namespace

@@ -180,10 +180,13 @@ __global__ __launch_bounds__(256) void k_quant_rowgroup(
   for (int r = 0; r < R; ++r) {
     if (!live[r]) continue;
     const int64_t off = base + (int64_t)(r * 64 + lane) * VEC;
+    // non-temporal payload stores (consecutive lanes on consecutive pieces):
+    // (1, 16) / (1, 32) / (1, 64) on config 2's shape 22.6 -> 21.7 / 22.5 ->
+    // 21.0-22.1 / 22.4-23.1 -> 21.7-22.2 us
     if constexpr (IS_BF16) {
-      *reinterpret_cast<uint2*>(q + off) = make_uint2(out[r][0], out[r][1]);
+      store_stream8(q + off, u32x2_t{out[r][0], out[r][1]});
     } else {
-      *reinterpret_cast<uint32_t*>(q + off) = out[r][0];
+      store_stream4(q + off, out[r][0]);
     }
   }
 }

@@ -126,8 +126,16 @@ __device__ __forceinline__ void ew_words(const uint4& xw, const uint4& yw, float
     fp8_word(xa[j], xv[4 * j], xv[4 * j + 1], xv[4 * j + 2], xv[4 * j + 3]);
     fp8_word(ya[j], yv[4 * j], yv[4 * j + 1], yv[4 * j + 2], yv[4 * j + 3]);
   }
+  // (f32(q) * s) / 128 as one multiply by s / 128 where that is exact for
+  // every payload byte (dequant_one_mul), the two-step form otherwise
+  if (dequant_one_mul(sx) && dequant_one_mul(sy)) {
+    const float sx7 = sx * 0.0078125f, sy7 = sy * 0.0078125f;
 #pragma unroll
-  for (int k = 0; k < 16; ++k) z[k] = ew_apply<OP>((xv[k] * sx) * 0.0078125f, (yv[k] * sy) * 0.0078125f);
+    for (int k = 0; k < 16; ++k) z[k] = ew_apply<OP>(xv[k] * sx7, yv[k] * sy7);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) z[k] = ew_apply<OP>((xv[k] * sx) * 0.0078125f, (yv[k] * sy) * 0.0078125f);
+  }
 }
 
 template <int OP, int CH, bool VEC>

@@ -307,6 +307,41 @@ def bench_quantize(steps: int, warmup: int):
     return ms, wall, ok, ms_long
 
 
+def bench_quantize_presets(steps: int, warmup: int):
+    """The config 2 activation quantized with the reference presets' activation
+    grids (blksize 16 and 32: tgrid (1, 16) and (1, 32), pratchya/preset.py:21,
+    :30, :39, :48; the row-group kernel), timed like the headline over 6
+    rotating input and output sets, with a parity spot check of a slice
+    against the oracle."""
+    import torch
+    from oracle import qarr_oracle as O
+    from pratchya_amd import _kernels as K
+
+    n_sets = 6
+    base = torch.from_numpy(O.activation_input(CFG2_ROWS, CFG2_COLS, seed=2).view(np.int16)).view(
+        torch.bfloat16).cuda()
+    xs = [base.clone() for _ in range(n_sets)]
+    xb = O.activation_input(CFG2_ROWS, CFG2_COLS, seed=2)[:64]
+    res = {}
+    for b in (16, 32):
+        g = (1, b)
+        outs = [tuple(torch.empty_like(t) for t in K.quantize(xs[0], g)) for _ in range(n_sets)]
+        ms, _ = timed_graph(lambda i: K.quantize(xs[i % n_sets], g, out=outs[i % n_sets]), steps, warmup,
+                            replays=HEADLINE_REPEATS)
+        nbytes = CFG2_ROWS * CFG2_COLS * 3 + sum(t.numel() * t.element_size() for t in outs[0][1:])
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        q8, s8, s32 = outs[(steps - 1) % n_sets]
+        r8, rs8, rs32 = O.quantize_impl(O.bf16_bits_to_f32(xb), g)
+        ok = (np.array_equal(q8[:64].view(torch.uint8).cpu().numpy(), r8.view(np.uint8))
+              and np.array_equal(s8.view(torch.uint8).cpu().numpy().reshape(-1)[:rs8.size], rs8.view(np.uint8).reshape(-1))
+              and np.array_equal(s32.cpu().numpy().reshape(-1)[:rs32.size].view(np.uint32),
+                                 rs32.reshape(-1).view(np.uint32)))
+        res[f"(1,{b})"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                           "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes,
+                           "bit_exact_vs_oracle_slice": bool(ok)}
+    return res
+
+
 CFG1_N = 1024
 # quantize: 2 B in + 1 B payload; dequantize: 1 B payload + 2 B out; the 68 scale bytes
 # (64 e8m0 + 1 group max) written once and read once
@@ -1028,7 +1063,7 @@ def main():
     ap.add_argument("--counter-workload", action="store_true",
                     help="only run the direct-launch workload used for rocprofv3 --pmc runs")
     ap.add_argument("--only", choices=["cfg3", "ffn", "cfg4", "cfg5", "cfg5qa", "optim", "elementwise",
-                                       "embedding", "ceiling", "lmhead"],
+                                       "embedding", "ceiling", "lmhead", "presets"],
                     default=None,
                     help="run one secondary configuration alone (for profiling) and print its result")
     args = ap.parse_args()
@@ -1057,6 +1092,8 @@ def main():
             res = bench_optimizer(3)
         elif args.only == "elementwise":
             res = bench_elementwise(max(20, args.steps // 2), max(4, args.warmup // 4))
+        elif args.only == "presets":
+            res = bench_quantize_presets(max(20, args.steps // 4), max(4, args.warmup // 4))
         elif args.only == "embedding":
             res = bench_embedding(max(20, args.steps // 4), max(4, args.warmup // 4))
         elif args.only == "ceiling":
@@ -1110,6 +1147,9 @@ def main():
         lambda r: f"{r['us']} us")
     leg("elementwise_add", lambda: bench_elementwise(max(20, args.steps // 2), max(4, args.warmup // 4)),
         lambda r: f"{r['us']} us")
+    leg("config2_quantize_preset_grids", lambda: bench_quantize_presets(max(20, args.steps // 4),
+                                                                        max(4, args.warmup // 4)),
+        lambda r: ", ".join(f"{k} {v['us']} us" for k, v in r.items()))
     _log("config 2 quantize: start")
     ms, wall, ok, ms_long = bench_quantize(args.steps, args.warmup)
     _log(f"config 2 quantize: {ms * 1e3:.2f} us/step, parity spot check {'ok' if ok else 'FAILED'}; "

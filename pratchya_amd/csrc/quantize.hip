@@ -1037,13 +1037,14 @@ int chunk_elems(int64_t b, bool bf16) {
 
 template <bool IS_BF16, int R, bool SPAN>
 void launch_rowgroup_t(const void* x, uint8_t* q, uint8_t* sc8, float* sc32, int64_t n,
-                       const RowGroupPlan& p, hipStream_t st) {
+                       const RowGroupPlan& p, hipStream_t st, int wg = 256) {
   constexpr int VEC = IS_BF16 ? 8 : 4;
   const int64_t tile = (int64_t)R * 64 * VEC;
   const int64_t waves = (n + tile - 1) / tile;
-  const int64_t blocks = (waves + 3) / 4;
+  const int64_t wpb = wg / 64;
+  const int64_t blocks = (waves + wpb - 1) / wpb;
   hipLaunchKernelGGL((k_quant_rowgroup<IS_BF16, R, SPAN, PRATCHYA_HW_CVT != 0>), dim3((unsigned)blocks),
-                     dim3(256), 0, st, x, q, sc8, sc32, n, p.bl_log2, p.gl_log2);
+                     dim3((unsigned)wg), 0, st, x, q, sc8, sc32, n, p.bl_log2, p.gl_log2);
 }
 
 template <bool IS_BF16>
@@ -1056,7 +1057,10 @@ int launch_rowgroup(const void* x, uint8_t* q, uint8_t* sc8, float* sc32, int64_
       default: return pratchya_set_error(PRATCHYA_EUNSUPPORTED, "row-group plan R=%d", p.R);
     }
   } else {
-    launch_rowgroup_t<IS_BF16, 2, false>(x, q, sc8, sc32, n, p, st);
+    // one wave per workgroup (config 2's shape at (1, 16) / (1, 32): 21.5-21.8 ->
+    // 20.9-21.0 / 21.3-21.5 -> 20.9 us against four waves; 4 rows per wave
+    // slower either way)
+    launch_rowgroup_t<IS_BF16, 2, false>(x, q, sc8, sc32, n, p, st, 64);
   }
   return check_launch("quantize(row-group)");
 }

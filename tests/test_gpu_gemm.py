@@ -104,6 +104,19 @@ def test_transpose_u8_tall():
     assert torch.equal(t, x.t().contiguous())
 
 
+@pytest.mark.parametrize("shape", [(4096 + 16, 16384 - 48), (1040, 4048), (2032, 2064)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_transpose_u8_ragged_large(shape):
+    """128x128 tiles (from 2^22 bytes) with partial tiles on both edges, and
+    sizes just around the switch from 64x64 tiles."""
+    K = _K()
+    g = torch.Generator(device="cuda").manual_seed(sum(shape))
+    x = torch.randint(0, 256, shape, dtype=torch.uint8, device="cuda", generator=g)
+    t = K.transpose_u8(x)
+    torch.cuda.synchronize()
+    assert torch.equal(t, x.t().contiguous())
+
+
 def test_dgrad_shape():
     """g (1,128) @ W^T: W [K_out, N] read as B rows without a transpose."""
     K = _K()

@@ -69,7 +69,11 @@ def test_transpose_arguments_without_gpu():
     assert lib.pratchya_transpose_u8(fake, 0, 64, fake, None) == 0
     assert lib.pratchya_transpose_u8(fake, 100, 64, fake, None) == _lib.EUNSUPPORTED
     assert lib.pratchya_transpose_u8(None, 64, 64, None, None) == _lib.EINVAL
-    assert lib.pratchya_transpose_u8(fake, 64 << 31, 128, fake, None) == _lib.EUNSUPPORTED
+    # 128x128 tiles from 2^22 bytes: 2^31 tile rows of one tile each, and a
+    # product of sides that would overflow 64 bits
+    assert lib.pratchya_transpose_u8(fake, 128 << 31, 128, fake, None) == _lib.EUNSUPPORTED
+    assert b"2^31" in lib.pratchya_last_error()
+    assert lib.pratchya_transpose_u8(fake, 1 << 40, 1 << 40, fake, None) == _lib.EUNSUPPORTED
     assert b"2^31" in lib.pratchya_last_error()
 
 
